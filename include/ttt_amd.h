@@ -1,0 +1,91 @@
+/* C ABI of libttt_amd.so: the TTT-Linear / TTT-MLP mini-batch inner loop on
+ * MI355X (gfx950), forward, backward and the MLP fixed-weight readout.
+ *
+ * Conventions shared by every entry point
+ *   - Every pointer is device memory, contiguous, row-major, with the layouts
+ *     given per argument.  B batch, H heads, NC mini-batches, K tokens per
+ *     mini-batch (16), F head dim (32 or 64), FF MLP hidden width (F, 2F or
+ *     4F, multiple of 64 up to 256), G checkpoint group size (1..NC),
+ *     NK = ceil(NC / G).
+ *   - Activations (XQ, XK, XV, eta, out and their gradients) share one dtype,
+ *     `dtype` (TTT_DTYPE_F32 or TTT_DTYPE_BF16).  Fast-weight state, LayerNorm
+ *     parameters, checkpoints, memo snapshots and weight gradients are fp32.
+ *   - The caller allocates every buffer; nothing is allocated or kept between
+ *     calls.  `stream` is a hipStream_t (NULL = the null stream); launches are
+ *     asynchronous on it.
+ *   - Arguments are validated on the host before any launch.  Return value:
+ *     TTT_OK or a negative TTT_ERR_* code (see ttt_error_string).
+ *   - Semantics are those of the reference's PyTorch ops path: dual form with
+ *     a general KxK eta (no implicit tril), LayerNorm eps given by `eps`
+ *     (the ops path uses 1e-8), dense KxK eta gradient.
+ */
+#ifndef TTT_AMD_H_
+#define TTT_AMD_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTT_AMD_ABI_VERSION 1
+
+enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
+
+enum ttt_status {
+  TTT_OK = 0,
+  TTT_ERR_SHAPE = -1,     /* unsupported or inconsistent shape */
+  TTT_ERR_DTYPE = -2,     /* unsupported dtype */
+  TTT_ERR_NULL = -3,      /* required pointer is NULL */
+  TTT_ERR_ALIGN = -4,     /* pointer not 16-byte aligned */
+  TTT_ERR_HIP = -5,       /* launch failed (hipGetLastError) */
+  TTT_ERR_WORKSPACE = -6, /* workspace missing or too small */
+  TTT_ERR_ARG = -7        /* other invalid argument (eps, G, M) */
+};
+
+/* ABI version of the loaded library (TTT_AMD_ABI_VERSION). */
+int ttt_abi_version(void);
+
+/* Static description of a status code. */
+const char* ttt_error_string(int status);
+
+/* TTT-Linear forward over all NC mini-batches of B*H chains.
+ * Replaces ttt_linear_scan_forward (kernels/linear_forward.py:5-148) as
+ * launched by TritonLinear._forward_core (linear_triton.py:62-144), and is
+ * the forward of ops.ttt_linear (ops/ttt_linear.py:57-84).
+ *   XQ, XK, XV  [B,H,NC,K,F] dtype      eta [B,H,NC,K,K] dtype
+ *   ln_w, ln_b  [H,F] fp32              W1_init [B,H,F,F], b1_init [B,H,1,F] fp32
+ *   out         [B,H,NC,K,F] dtype      (XQ + LN(Z1_bar) per mini-batch)
+ *   W1_last, b1_last  [B,H,F,F], [B,H,1,F] fp32, final state (both or neither)
+ *   W1_ckpt, b1_ckpt  [B,H,NK,F,F], [B,H,NK,1,F] fp32, state entering
+ *                     mini-batch k*G (both or neither; needed by the backward) */
+int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
+                   const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
+                   int B, int H, int NC, int K, int F, int G, int dtype, float eps,
+                   void* out, float* W1_last, float* b1_last, float* W1_ckpt, float* b1_ckpt,
+                   void* stream);
+
+/* Bytes of device workspace ttt_linear_bwd needs for these sizes. */
+size_t ttt_linear_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int G);
+
+/* TTT-Linear backward: gradients of sum(out * dout) wrt every input, the
+ * final state's gradient taken as zero (the ops path discards W_last).
+ * Replaces ttt_linear_scan_backward (kernels/linear_backward.py:207-520) as
+ * launched by TritonLinear._backward_core (linear_triton.py:146-265).
+ *   W1_ckpt, b1_ckpt   checkpoints written by ttt_linear_fwd with the same G
+ *   dout               [B,H,NC,K,F] dtype
+ *   dXQ, dXK, dXV      [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
+ *   dW1, db1           [B,H,F,F], [B,H,1,F] fp32 (gradient wrt W1_init, b1_init)
+ *   dln_w, dln_b       [B,H,F] fp32 per-chain partials; sum over B for [H,F]
+ *   workspace          >= ttt_linear_bwd_workspace_bytes(...) bytes */
+int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
+                   const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
+                   const void* dout, int B, int H, int NC, int K, int F, int G, int dtype, float eps,
+                   void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1,
+                   float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTT_AMD_H_ */

@@ -1,0 +1,150 @@
+"""CPU check of the hand-derived backward the HIP kernels implement.
+
+The kernels do not use autograd: they run the reverse sweep written out in
+`_linear_reverse` / `_mlp_reverse` below (per mini-batch, with the fast
+weights rebuilt backwards from checkpoints as W_s = W_{s+1} + XK_s^T diag(e) G_s).
+These fp64 restatements of that algorithm are checked against autograd of the
+oracle, so a wrong term in the derivation fails here on the CPU before any
+GPU run."""
+
+import torch
+import torch.nn.functional as F
+
+from oracle import ttt_oracle as O
+
+DT = torch.float64
+
+
+def _lnl2_parts(z, tgt, lw, lb, eps):
+    Fd = z.shape[-1]
+    mu = z.mean(-1, keepdim=True)
+    rstd = 1.0 / torch.sqrt(((z - mu) ** 2).mean(-1, keepdim=True) + eps)
+    xh = (z - mu) * rstd
+    go = lw * xh + lb - tgt
+    gx = go * lw
+    s1 = gx.mean(-1, keepdim=True)
+    s2 = (gx * xh).mean(-1, keepdim=True)
+    G = (gx - s1 - xh * s2) * rstd
+    return dict(xh=xh, go=go, gx=gx, rstd=rstd, s2=s2, G=G, F=Fd)
+
+
+def _lnl2_backward(dG, P, lw):
+    """Backward of ln_fused_l2_bwd: returns dZ, dtgt, dlw, dlb."""
+    xh, go, gx, rstd, c_, G, Fd = P["xh"], P["go"], P["gx"], P["rstd"], P["s2"], P["G"], P["F"]
+    u = dG * rstd
+    mu_u = u.mean(-1, keepdim=True)
+    mu_ux = (u * xh).mean(-1, keepdim=True)
+    d_gx = u - mu_u - xh * mu_ux
+    d_xh = -c_ * u - mu_ux * gx
+    dsig = -(u * G).sum(-1, keepdim=True)
+    d_go = d_gx * lw
+    dlw = (d_gx * go + d_go * xh).sum(-2)
+    dlb = d_go.sum(-2)
+    d_xh = d_xh + d_go * lw
+    dZ = rstd * (d_xh - d_xh.mean(-1, keepdim=True) - xh * (d_xh * xh).mean(-1, keepdim=True)) + dsig * xh / Fd
+    return dZ, -d_go, dlw, dlb
+
+
+def _ln_backward(dy, xh, rstd, lw):
+    gy = dy * lw
+    return rstd * (gy - gy.mean(-1, keepdim=True) - xh * (gy * xh).mean(-1, keepdim=True))
+
+
+def _linear_reverse(d, dout, G_ckpt, eps=1e-8):
+    """Reverse sweep of one TTT-Linear chain set (all B,H at once)."""
+    XQ, XK, XV, eta, lw, lb = d["XQ"], d["XK"], d["XV"], d["eta"], d["ln_w"], d["ln_b"]
+    B, H, NC, K, Fd = XQ.shape
+    lw_, lb_ = lw[:, None], lb[:, None]  # [H,1,F]
+    full = O.linear_forward_full(lw, lb, d["W1"], d["b1"], XQ, XV, XK, eta, G_ckpt, eps)
+    dW = torch.zeros_like(d["W1"])
+    db = torch.zeros_like(d["b1"])
+    dXQ, dXK, dXV, deta = (torch.zeros_like(XQ), torch.zeros_like(XK), torch.zeros_like(XV), torch.zeros_like(eta))
+    dlw = torch.zeros(B, H, Fd, dtype=DT)
+    dlb = torch.zeros(B, H, Fd, dtype=DT)
+    NK = O.ceil_div(NC, G_ckpt)
+    for k in reversed(range(NK)):
+        s0, s1 = k * G_ckpt, min(k * G_ckpt + G_ckpt, NC)
+        W, b = full["W1_ckpt"][:, :, k], full["b1_ckpt"][:, :, k]
+        Gs = []
+        for s in range(s0, s1):  # phase 1: recompute the inner-loss gradients
+            xk, xv, e = XK[:, :, s], XV[:, :, s], eta[:, :, s, -1]
+            P = _lnl2_parts(xk @ W + b, xv - xk, lw_, lb_, eps)
+            Gs.append(P["G"])
+            W = W - xk.transpose(-1, -2) @ (e[..., None] * P["G"])
+            b = b - (e[..., None] * P["G"]).sum(-2, keepdim=True)
+        for s in reversed(range(s0, s1)):  # phase 2
+            xq, xk, xv, et, e, do = XQ[:, :, s], XK[:, :, s], XV[:, :, s], eta[:, :, s], eta[:, :, s, -1], dout[:, :, s]
+            Gm = Gs[s - s0]
+            W = W + xk.transpose(-1, -2) @ (e[..., None] * Gm)  # state entering s
+            b = b + (e[..., None] * Gm).sum(-2, keepdim=True)
+            P = _lnl2_parts(xk @ W + b, xv - xk, lw_, lb_, eps)
+            A = xq @ xk.transpose(-1, -2)
+            M = et * A + et
+            Zb = xq @ W - M @ Gm + b
+            mb = Zb.mean(-1, keepdim=True)
+            rsb = 1.0 / torch.sqrt(((Zb - mb) ** 2).mean(-1, keepdim=True) + eps)
+            xhb = (Zb - mb) * rsb
+            # readout
+            dlw += (do * xhb).sum(-2)
+            dlb += do.sum(-2)
+            dZb = _ln_backward(do, xhb, rsb, lw_)
+            dxq = do + dZb @ W.transpose(-1, -2)
+            dM = -dZb @ Gm.transpose(-1, -2)
+            det = dM * (1 + A)
+            dA = dM * et
+            dxq = dxq + dA @ xk
+            dxk = dA.transpose(-1, -2) @ xq
+            dG = -M.transpose(-1, -2) @ dZb
+            # state update (uses dW, db = gradient wrt the state after step s)
+            Qm = xk @ dW
+            dG = dG - e[..., None] * Qm - e[..., None] * db
+            de = -(Gm * (Qm + db)).sum(-1)
+            dxk = dxk - (e[..., None] * Gm) @ dW.transpose(-1, -2)
+            det[:, :, -1, :] += de
+            dZ1, dtgt, dlw_i, dlb_i = _lnl2_backward(dG, P, lw_)
+            dlw += dlw_i
+            dlb += dlb_i
+            dxv = dtgt
+            dxk = dxk - dtgt + dZ1 @ W.transpose(-1, -2)
+            dW = dW + xq.transpose(-1, -2) @ dZb + xk.transpose(-1, -2) @ dZ1
+            db = db + dZb.sum(-2, keepdim=True) + dZ1.sum(-2, keepdim=True)
+            dXQ[:, :, s], dXK[:, :, s], dXV[:, :, s], deta[:, :, s] = dxq, dxk, dxv, det
+    return dict(dXQ=dXQ, dXK=dXK, dXV=dXV, deta=deta, dW1=dW, db1=db, dln_w=dlw.sum(0), dln_b=dlb.sum(0))
+
+
+def _autograd_linear(d, dout):
+    names = ["XK", "XQ", "XV", "eta", "ln_w", "ln_b", "W1", "b1"]
+    args = {n: d[n].clone().requires_grad_(True) for n in names}
+    out = O.ttt_linear(*[args[n] for n in names], 0)  # [B,NC,K,H,F]
+    out.backward(dout.permute(0, 2, 3, 1, 4))
+    g = {n: args[n].grad for n in names}
+    return dict(dXQ=g["XQ"], dXK=g["XK"], dXV=g["XV"], deta=g["eta"], dW1=g["W1"], db1=g["b1"],
+                dln_w=g["ln_w"], dln_b=g["ln_b"])
+
+
+def _inputs(B, H, NC, FF=0, seed=0, kind="causal"):
+    d = O.make_inputs(B, H, NC, 16, 64, FF=FF, seed=seed, dtype=DT, eta_kind=kind, with_grad=True)
+    d = {k: v.to(DT) for k, v in d.items()}
+    g = torch.Generator().manual_seed(seed + 100)
+    d["ln_w"] = 1 + 0.1 * torch.randn(H, 64, generator=g, dtype=DT)
+    d["ln_b"] = 0.1 * torch.randn(H, 64, generator=g, dtype=DT)
+    d["b1"] = 0.05 * torch.randn(*d["b1"].shape, generator=g, dtype=DT)
+    if FF:
+        d["b2"] = 0.05 * torch.randn(*d["b2"].shape, generator=g, dtype=DT)
+    return d
+
+
+def test_linear_reverse_sweep_matches_autograd():
+    d = _inputs(2, 2, 5, seed=1)
+    mine = _linear_reverse(d, d["dOut"], G_ckpt=2)
+    ref = _autograd_linear(d, d["dOut"])
+    for k in ref:
+        torch.testing.assert_close(mine[k], ref[k], rtol=1e-9, atol=1e-10, msg=k)
+
+
+def test_linear_reverse_sweep_layer_eta():
+    d = _inputs(1, 2, 4, seed=2, kind="layer")
+    mine = _linear_reverse(d, d["dOut"], G_ckpt=4)
+    ref = _autograd_linear(d, d["dOut"])
+    for k in ref:
+        torch.testing.assert_close(mine[k], ref[k], rtol=1e-9, atol=1e-10, msg=k)

@@ -1,0 +1,137 @@
+"""TTT-Linear HIP kernels vs the CPU oracle (forward, side outputs, backward).
+
+Tolerances (north star): fp32 activations max-abs <= 1e-4 against the ops
+path; bf16 activations with fp32 state rel-L2 <= 2e-2.  The oracle runs in
+fp64 on the same (bf16-rounded) inputs."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import ttt_oracle as O
+from tests._util import max_abs, oracle_linear_grads, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_RTOL = 2e-2
+
+
+def fp32_bound(ref: torch.Tensor) -> float:
+    """max-abs bound for fp32 parity: 1e-4 on O(1) tensors, scaled by the
+    tensor's magnitude when it exceeds 1 (fp32 itself resolves ~6e-8 of it;
+    the eta gradient reaches 1e4-1e5 on unnormalised N(0,1) inputs)."""
+    return FP32_ATOL * max(1.0, float(ref.abs().max()))
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _fwd(d, G, want_last=True):
+    from ttt_amd.linear import linear_forward
+    g = to_dev(d)
+    return linear_forward(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["XQ"], g["XV"], g["XK"], g["eta"], G,
+                          want_ckpt=True, want_last=want_last)
+
+
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_linear_fwd_fp32_config0(kind):
+    """B2 H4 T256 (NC16 K16) F64, fp32."""
+    _say("linear fwd fp32 config0", kind)
+    d = O.make_inputs(2, 4, 16, 16, 64, seed=0, dtype=torch.float32, eta_kind=kind)
+    out, (Wc, bc), (Wl, bl) = _fwd(d, G=4)
+    torch.cuda.synchronize()
+    ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=4)
+    assert max_abs(out, ref["out"]) <= FP32_ATOL
+    assert max_abs(Wl, ref["W1_last"]) <= FP32_ATOL
+    assert max_abs(bl, ref["b1_last"]) <= FP32_ATOL
+    assert max_abs(Wc, ref["W1_ckpt"]) <= FP32_ATOL
+    assert max_abs(bc, ref["b1_ckpt"]) <= FP32_ATOL
+
+
+def test_linear_fwd_fp32_nonzero_ln_and_bias():
+    _say("linear fwd fp32 ln/bias")
+    d = O.make_inputs(1, 3, 8, 16, 64, seed=5, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(9)
+    d["ln_w"] = 1 + 0.2 * torch.randn(3, 64, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(3, 64, generator=gen)
+    d["b1"] = 0.1 * torch.randn(1, 3, 1, 64, generator=gen)
+    out, _, (Wl, bl) = _fwd(d, G=3)
+    ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=3)
+    assert max_abs(out, ref["out"]) <= FP32_ATOL
+    assert max_abs(Wl, ref["W1_last"]) <= FP32_ATOL
+    assert max_abs(bl, ref["b1_last"]) <= FP32_ATOL
+
+
+def test_linear_fwd_f32_headdim32():
+    _say("linear fwd fp32 F=32")
+    d = O.make_inputs(2, 2, 6, 16, 32, seed=3, dtype=torch.float32)
+    out, _, (Wl, _) = _fwd(d, G=2)
+    ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=2)
+    assert max_abs(out, ref["out"]) <= FP32_ATOL
+    assert max_abs(Wl, ref["W1_last"]) <= FP32_ATOL
+
+
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_linear_fwd_bf16(kind):
+    _say("linear fwd bf16", kind)
+    d = O.make_inputs(2, 3, 32, 16, 64, seed=1, dtype=torch.bfloat16, eta_kind=kind)
+    out, (Wc, _), (Wl, bl) = _fwd(d, G=8)
+    ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=8)
+    assert out.dtype == torch.bfloat16
+    assert rel_l2(out, ref["out"]) <= BF16_RTOL
+    assert rel_l2(Wl, ref["W1_last"]) <= BF16_RTOL
+    assert rel_l2(Wc, ref["W1_ckpt"]) <= BF16_RTOL
+
+
+def test_linear_fwd_deterministic():
+    _say("linear fwd determinism")
+    d = O.make_inputs(2, 2, 8, 16, 64, seed=2, dtype=torch.bfloat16)
+    a, _, _ = _fwd(d, G=4)
+    b, _, _ = _fwd(d, G=4)
+    assert torch.equal(a, b)
+
+
+def _bwd(d, dout, G):
+    from ttt_amd.linear import linear_backward
+    g = to_dev(d)
+    _, (Wc, bc), _ = _fwd(d, G, want_last=False)
+    (dlw, dlb, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, bc, dout.cuda(), G)
+    return dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW, db1=db, dln_w=dlw, dln_b=dlb)
+
+
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_linear_bwd_fp32(kind):
+    _say("linear bwd fp32", kind)
+    d = O.make_inputs(2, 2, 6, 16, 64, seed=4, dtype=torch.float32, eta_kind=kind, with_grad=True)
+    gen = torch.Generator().manual_seed(10)
+    d["ln_w"] = 1 + 0.2 * torch.randn(2, 64, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(2, 64, generator=gen)
+    mine = _bwd(d, d["dOut"], G=4)
+    ref = oracle_linear_grads(d, d["dOut"], G=0)
+    ref32 = oracle_linear_grads(d, d["dOut"], G=0, dtype=torch.float32)
+    bad = []
+    for k in mine:
+        err = max_abs(mine[k], ref[k])
+        _say(f"  {k}: max-abs {err:.3e} (fp32 oracle {max_abs(ref32[k], ref[k]):.3e}, bound {fp32_bound(ref[k]):.3e})"
+             f"  rel-L2 {rel_l2(mine[k], ref[k]):.3e}")
+        if err > fp32_bound(ref[k]):
+            bad.append(k)
+    assert not bad
+
+
+def test_linear_bwd_bf16():
+    _say("linear bwd bf16")
+    d = O.make_inputs(2, 3, 24, 16, 64, seed=6, dtype=torch.bfloat16, with_grad=True)
+    mine = _bwd(d, d["dOut"], G=8)
+    ref = oracle_linear_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        err = rel_l2(mine[k], ref[k])
+        _say(f"  {k}: rel-L2 {err:.3e}")
+        if err > BF16_RTOL:
+            bad.append(k)
+    assert not bad

@@ -1,0 +1,165 @@
+// extern "C" entry points of libttt_amd.so: host-side validation, then one
+// launch per call on the caller's stream.  Declarations and argument
+// contracts are in include/ttt_amd.h.
+#include <stdint.h>
+
+#include "ttt_kernels.h"
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(int B, int H, int NC, int K, int F, int G, int dtype, float eps) {
+  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
+  if (B <= 0 || H <= 0 || NC <= 0) return TTT_ERR_SHAPE;
+  if (K != 16) return TTT_ERR_SHAPE;
+  if (F != 32 && F != 64) return TTT_ERR_SHAPE;
+  if (G < 1 || G > NC) return TTT_ERR_ARG;
+  if (!(eps > 0.0f) || eps > 1.0f) return TTT_ERR_ARG;
+  if ((long long)B * H > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return TTT_OK;
+}
+
+#define REQUIRE_PTR(p)                 \
+  do {                                 \
+    if ((p) == nullptr) return TTT_ERR_NULL; \
+    if (!aligned16(p)) return TTT_ERR_ALIGN; \
+  } while (0)
+
+#define OPTIONAL_PTR(p)                            \
+  do {                                             \
+    if ((p) != nullptr && !aligned16(p)) return TTT_ERR_ALIGN; \
+  } while (0)
+
+int hip_status(hipError_t e) { return e == hipSuccess ? TTT_OK : TTT_ERR_HIP; }
+
+}  // namespace
+
+extern "C" {
+
+int ttt_abi_version(void) { return TTT_AMD_ABI_VERSION; }
+
+const char* ttt_error_string(int status) {
+  switch (status) {
+    case TTT_OK: return "ok";
+    case TTT_ERR_SHAPE: return "unsupported or inconsistent shape";
+    case TTT_ERR_DTYPE: return "unsupported dtype";
+    case TTT_ERR_NULL: return "required pointer is NULL";
+    case TTT_ERR_ALIGN: return "pointer is not 16-byte aligned";
+    case TTT_ERR_HIP: return "HIP launch failed";
+    case TTT_ERR_WORKSPACE: return "workspace missing or too small";
+    case TTT_ERR_ARG: return "invalid argument";
+    default: return "unknown status";
+  }
+}
+
+int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                   const float* ln_b, const float* W1_init, const float* b1_init, int B, int H, int NC, int K,
+                   int F, int G, int dtype, float eps, void* out, float* W1_last, float* b1_last, float* W1_ckpt,
+                   float* b1_ckpt, void* stream) {
+  int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  REQUIRE_PTR(XQ);
+  REQUIRE_PTR(XK);
+  REQUIRE_PTR(XV);
+  REQUIRE_PTR(eta);
+  REQUIRE_PTR(ln_w);
+  REQUIRE_PTR(ln_b);
+  REQUIRE_PTR(W1_init);
+  REQUIRE_PTR(b1_init);
+  REQUIRE_PTR(out);
+  OPTIONAL_PTR(W1_last);
+  OPTIONAL_PTR(b1_last);
+  OPTIONAL_PTR(W1_ckpt);
+  OPTIONAL_PTR(b1_ckpt);
+  if ((W1_last == nullptr) != (b1_last == nullptr)) return TTT_ERR_NULL;
+  if ((W1_ckpt == nullptr) != (b1_ckpt == nullptr)) return TTT_ERR_NULL;
+
+  ttt::LinearFwdParams p;
+  p.XQ = XQ;
+  p.XK = XK;
+  p.XV = XV;
+  p.eta = eta;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.W_init = W1_init;
+  p.b_init = b1_init;
+  p.out = out;
+  p.W_last = W1_last;
+  p.b_last = b1_last;
+  p.W_ckpt = W1_ckpt;
+  p.b_ckpt = b1_ckpt;
+  p.B = B;
+  p.H = H;
+  p.NC = NC;
+  p.F = F;
+  p.G = G;
+  p.NK = (NC + G - 1) / G;
+  p.eps = eps;
+  return hip_status(ttt::launch_linear_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+size_t ttt_linear_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int G) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || G <= 0) return 0;
+  const int g = G < NC ? G : NC;
+  return (size_t)B * H * g * K * F * sizeof(float);
+}
+
+int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                   const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const void* dout, int B, int H,
+                   int NC, int K, int F, int G, int dtype, float eps, void* dXQ, void* dXK, void* dXV, void* deta,
+                   float* dW1, float* db1, float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  REQUIRE_PTR(XQ);
+  REQUIRE_PTR(XK);
+  REQUIRE_PTR(XV);
+  REQUIRE_PTR(eta);
+  REQUIRE_PTR(ln_w);
+  REQUIRE_PTR(ln_b);
+  REQUIRE_PTR(W1_ckpt);
+  REQUIRE_PTR(b1_ckpt);
+  REQUIRE_PTR(dout);
+  REQUIRE_PTR(dXQ);
+  REQUIRE_PTR(dXK);
+  REQUIRE_PTR(dXV);
+  REQUIRE_PTR(deta);
+  REQUIRE_PTR(dW1);
+  REQUIRE_PTR(db1);
+  REQUIRE_PTR(dln_w);
+  REQUIRE_PTR(dln_b);
+  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return TTT_ERR_ALIGN;
+  if (workspace_bytes < ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, G)) return TTT_ERR_WORKSPACE;
+
+  ttt::LinearBwdParams p;
+  p.XQ = XQ;
+  p.XK = XK;
+  p.XV = XV;
+  p.eta = eta;
+  p.dout = dout;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.W_ckpt = W1_ckpt;
+  p.b_ckpt = b1_ckpt;
+  p.dXQ = dXQ;
+  p.dXK = dXK;
+  p.dXV = dXV;
+  p.deta = deta;
+  p.dW = dW1;
+  p.db = db1;
+  p.dln_w = dln_w;
+  p.dln_b = dln_b;
+  p.ws = static_cast<float*>(workspace);
+  p.B = B;
+  p.H = H;
+  p.NC = NC;
+  p.F = F;
+  p.G = G;
+  p.NK = (NC + G - 1) / G;
+  p.eps = eps;
+  return hip_status(ttt::launch_linear_bwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

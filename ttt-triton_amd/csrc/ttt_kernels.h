@@ -1,0 +1,33 @@
+// Kernel-side parameter blocks and launchers (internal to libttt_amd.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/ttt_amd.h"
+#include "ttt_tile.h"
+
+namespace ttt {
+
+struct LinearFwdParams {
+  const void *XQ, *XK, *XV, *eta;
+  const float *ln_w, *ln_b, *W_init, *b_init;
+  void* out;
+  float *W_last, *b_last, *W_ckpt, *b_ckpt;
+  int B, H, NC, F, G, NK;
+  float eps;
+};
+
+struct LinearBwdParams {
+  const void *XQ, *XK, *XV, *eta, *dout;
+  const float *ln_w, *ln_b, *W_ckpt, *b_ckpt;
+  void *dXQ, *dXK, *dXV, *deta;
+  float *dW, *db, *dln_w, *dln_b;
+  float* ws;  // per-chain scratch: G mini-batches of the inner-loss gradient
+  int B, H, NC, F, G, NK;
+  float eps;
+};
+
+hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t stream);
+
+}  // namespace ttt

@@ -1,0 +1,297 @@
+// Tile algebra for one wavefront on gfx950 (CDNA4) MFMA.
+//
+// Every matrix the TTT kernels touch has a 16-row token dimension (one
+// mini-batch of K = 16 tokens) or is a fast weight made of 16x16 blocks, so
+// all products are built from 16x16 output tiles:
+//
+//   Tile (fp32 accumulator, "C layout" of v_mfma_f32_16x16x*):
+//       lane l = 16*g + n (g = l>>4 in 0..3, n = l&15) holds X[4g + j][n], j = 0..3.
+//   Frag<T> (one K16 operand fragment):
+//       lane l = 16*g + r holds four values P[r][4g + j], j = 0..3: the lane
+//       index r runs over the operand's free index (a row of A, a column of B)
+//       and the register index over 4 consecutive contraction indices.
+//
+// A product Y[m][n] = sum_k P[m][k] Q[k][n] takes P as frags (free = m,
+// contraction = k) and Q as frags (free = n, contraction = k).  A C-layout
+// tile of X [rows x cols] *is* a frag set with free = cols, contraction = rows
+// (the register index runs over rows), so an accumulator can be fed straight
+// back into a product that contracts over its rows -- as the right factor X or
+// as the left factor X^T.  Contracting over its columns needs a transpose,
+// which `transpose16` does exactly with one MFMA against the identity.
+//
+// A 32-deep contraction step (v_mfma_f32_16x16x32_bf16) packs two K16 frags:
+// elements 0-3 carry k-block 2c and elements 4-7 k-block 2c+1.  Any fixed
+// permutation of k that is the same for both operands gives the same sum, so
+// this packing lets a pair of C-layout tiles (rows 0-15 and 16-31) serve as a
+// K32 operand with no data movement.
+//
+// fp32 activations use v_mfma_f32_16x16x4_f32 (four per K16 frag, register j
+// of every lane group in the j-th instruction), which keeps the same frag
+// layout and gives fp32-exact products.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ttt {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+struct Tile {
+  f4 v;
+};
+
+template <typename T> struct FragT;
+template <> struct FragT<float> { typedef f4 type; };
+template <> struct FragT<__bf16> { typedef bf4 type; };
+
+template <typename T> struct Frag {
+  typename FragT<T>::type v;
+};
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ __bf16 to_bf16(float x) { return (__bf16)x; }
+
+template <typename T> __device__ __forceinline__ Frag<T> to_frag(f4 x);
+template <> __device__ __forceinline__ Frag<float> to_frag<float>(f4 x) { return Frag<float>{x}; }
+template <> __device__ __forceinline__ Frag<__bf16> to_frag<__bf16>(f4 x) {
+  Frag<__bf16> f;
+  f.v[0] = (__bf16)x[0];
+  f.v[1] = (__bf16)x[1];
+  f.v[2] = (__bf16)x[2];
+  f.v[3] = (__bf16)x[3];
+  return f;
+}
+
+template <typename T> __device__ __forceinline__ f4 frag_to_f4(Frag<T> f) {
+  return f4{(float)f.v[0], (float)f.v[1], (float)f.v[2], (float)f.v[3]};
+}
+
+// ---------------------------------------------------------------- MFMA
+// acc += P * Q over one 16-deep k-block
+__device__ __forceinline__ void mma16(f4& acc, Frag<__bf16> p, Frag<__bf16> q) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p.v, q.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma16(f4& acc, Frag<float> p, Frag<float> q) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[0], q.v[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[1], q.v[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[2], q.v[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[3], q.v[3], acc, 0, 0, 0);
+}
+// acc += P * Q over two 16-deep k-blocks (p0/q0 = block 2c, p1/q1 = block 2c+1)
+__device__ __forceinline__ void mma32(f4& acc, Frag<__bf16> p0, Frag<__bf16> p1, Frag<__bf16> q0,
+                                      Frag<__bf16> q1) {
+  bf8 a = __builtin_shufflevector(p0.v, p1.v, 0, 1, 2, 3, 4, 5, 6, 7);
+  bf8 b = __builtin_shufflevector(q0.v, q1.v, 0, 1, 2, 3, 4, 5, 6, 7);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma32(f4& acc, Frag<float> p0, Frag<float> p1, Frag<float> q0, Frag<float> q1) {
+  mma16(acc, p0, q0);
+  mma16(acc, p1, q1);
+}
+
+// Y[MT x NT tiles] += P (MT free tiles x KB k-blocks) * Q (NT free tiles x KB k-blocks)
+template <int MT, int NT, int KB, typename T>
+__device__ __forceinline__ void gemm(Tile (&y)[MT][NT], const Frag<T> (&p)[MT][KB], const Frag<T> (&q)[NT][KB]) {
+#pragma unroll
+  for (int c = 0; c + 1 < KB; c += 2)
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) mma32(y[m][n].v, p[m][c], p[m][c + 1], q[n][c], q[n][c + 1]);
+  if (KB & 1) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) mma16(y[m][n].v, p[m][KB - 1], q[n][KB - 1]);
+  }
+}
+
+// Y[MT x NT] += P (frags [MT][KB]) * X where X is held as C-layout tiles
+// w[KB][NT] of the matrix [16*KB x 16*NT] (contraction over its rows);
+// operand frags are converted just before each MFMA.
+template <int MT, int NT, int KB, typename T>
+__device__ __forceinline__ void gemm_pt(Tile (&y)[MT][NT], const Frag<T> (&p)[MT][KB], const Tile (&w)[KB][NT]) {
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+#pragma unroll
+    for (int c = 0; c + 1 < KB; c += 2) {
+      const Frag<T> q0 = to_frag<T>(w[c][n].v), q1 = to_frag<T>(w[c + 1][n].v);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) mma32(y[m][n].v, p[m][c], p[m][c + 1], q0, q1);
+    }
+    if (KB & 1) {
+      const Frag<T> q = to_frag<T>(w[KB - 1][n].v);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) mma16(y[m][n].v, p[m][KB - 1], q);
+    }
+  }
+}
+// Y[MT x NT] += X^T * Q with X held as C-layout tiles w[KB][MT] of [16*KB x 16*MT]
+template <int MT, int NT, int KB, typename T>
+__device__ __forceinline__ void gemm_tp(Tile (&y)[MT][NT], const Tile (&w)[KB][MT], const Frag<T> (&q)[NT][KB]) {
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+#pragma unroll
+    for (int c = 0; c + 1 < KB; c += 2) {
+      const Frag<T> p0 = to_frag<T>(w[c][m].v), p1 = to_frag<T>(w[c + 1][m].v);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) mma32(y[m][n].v, p0, p1, q[n][c], q[n][c + 1]);
+    }
+    if (KB & 1) {
+      const Frag<T> p0 = to_frag<T>(w[KB - 1][m].v);
+#pragma unroll
+      for (int n = 0; n < NT; ++n) mma16(y[m][n].v, p0, q[n][KB - 1]);
+    }
+  }
+}
+
+// The identity as a K16 frag: lane (g, r) holds I[r][4g + j] (symmetric).
+template <typename T> __device__ __forceinline__ Frag<T> identity_frag() {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  f4 x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = (4 * g + j == r) ? 1.0f : 0.0f;
+  return to_frag<T>(x);
+}
+
+// Frag P (free = a, contraction = b) -> C-layout tile of the matrix [a x b],
+// i.e. a frag with free = b, contraction = a.  Exact: P*I.
+template <typename T> __device__ __forceinline__ Tile transpose16(Frag<T> p, Frag<T> ident) {
+  Tile t;
+  t.v = f4{0.f, 0.f, 0.f, 0.f};
+  mma16(t.v, p, ident);
+  return t;
+}
+
+// Square block of operand frags of X (a[p][q]: free = block p, contraction =
+// block q) -> frags of X^T (b[q][p]: free = block q, contraction = block p).
+// Exact for values representable in T.
+template <int N, typename T>
+__device__ __forceinline__ void transpose_frags(const Frag<T> (&a)[N][N], Frag<T> (&b)[N][N], Frag<T> ident) {
+#pragma unroll
+  for (int p = 0; p < N; ++p)
+#pragma unroll
+    for (int q = 0; q < N; ++q) b[q][p] = to_frag<T>(transpose16(a[p][q], ident).v);
+}
+
+// ---------------------------------------------------------------- lane reductions
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// sum over the 16 lanes that share g (one DPP row)
+__device__ __forceinline__ float sum_row16(float x) {
+  x += dpp<0x128>(x);  // row_ror:8
+  x += dpp<0x124>(x);  // row_ror:4
+  x += dpp<0x122>(x);  // row_ror:2
+  x += dpp<0x121>(x);  // row_ror:1
+  return x;
+}
+// sum over the 4 lanes that share n (lanes n, n+16, n+32, n+48)
+__device__ __forceinline__ float sum_col4(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+// ---------------------------------------------------------------- loads / stores
+// Load a K16 frag from a row-major matrix: lane (g, r) reads
+// X[r][c0 + 4g .. c0 + 4g + 3] (row stride ld elements).
+__device__ __forceinline__ Frag<__bf16> load_frag(const __bf16* __restrict__ x, int ld, int c0) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  Frag<__bf16> f;
+  f.v = *reinterpret_cast<const bf4*>(x + r * ld + c0 + 4 * g);
+  return f;
+}
+__device__ __forceinline__ Frag<float> load_frag(const float* __restrict__ x, int ld, int c0) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  Frag<float> f;
+  f.v = *reinterpret_cast<const f4*>(x + r * ld + c0 + 4 * g);
+  return f;
+}
+// four values X[r][c0 + 4g + j] as fp32 (same pattern, any element type)
+template <typename T> __device__ __forceinline__ f4 load_f4(const T* __restrict__ x, int ld, int c0) {
+  return frag_to_f4(load_frag(x, ld, c0));
+}
+
+// four consecutive values at p as fp32
+__device__ __forceinline__ f4 load4(const __bf16* __restrict__ p) {
+  const bf4 v = *reinterpret_cast<const bf4*>(p);
+  return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ f4 load4(const float* __restrict__ p) { return *reinterpret_cast<const f4*>(p); }
+
+// Store four values to X[r][c0 + 4g + j]
+__device__ __forceinline__ void store_f4(__bf16* __restrict__ x, int ld, int c0, f4 v) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  *reinterpret_cast<bf4*>(x + r * ld + c0 + 4 * g) = to_frag<__bf16>(v).v;
+}
+__device__ __forceinline__ void store_f4(float* __restrict__ x, int ld, int c0, f4 v) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  *reinterpret_cast<f4*>(x + r * ld + c0 + 4 * g) = v;
+}
+
+// C-layout tile <-> row-major fp32 matrix block at (r0, c0)
+__device__ __forceinline__ Tile load_tile(const float* __restrict__ x, int ld, int r0, int c0) {
+  const int l = lane_id();
+  const int g = l >> 4, n = l & 15;
+  Tile t;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) t.v[j] = x[(r0 + 4 * g + j) * ld + c0 + n];
+  return t;
+}
+__device__ __forceinline__ void store_tile(float* __restrict__ x, int ld, int r0, int c0, Tile t) {
+  const int l = lane_id();
+  const int g = l >> 4, n = l & 15;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[(r0 + 4 * g + j) * ld + c0 + n] = t.v[j];
+}
+
+// Tile registers <-> scratch in register order (fully coalesced float4 per lane)
+__device__ __forceinline__ void spill_tile(float* __restrict__ x, Tile t) {
+  reinterpret_cast<f4*>(x)[lane_id()] = t.v;
+}
+__device__ __forceinline__ Tile fill_tile(const float* __restrict__ x) {
+  Tile t;
+  t.v = reinterpret_cast<const f4*>(x)[lane_id()];
+  return t;
+}
+
+// ---------------------------------------------------------------- GELU (tanh form)
+// tanh via exp: t = 1 - 2/(exp(2x)+1); saturates correctly for large |x|.
+__device__ __forceinline__ float tanh_f(float x) {
+  const float e = __expf(2.0f * x);
+  return 1.0f - 2.0f / (e + 1.0f);
+}
+// F.gelu(x, approximate="tanh"): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;
+  return 0.5f * x * (1.0f + tanh_f(k0 * (x + 0.044715f * x * x * x)));
+}
+// derivative with the ops path's constants (ops/ttt_utils.py:51-54)
+__device__ __forceinline__ float gelu_bwd(float x) {
+  const float t = tanh_f(0.79788456f * x * (1.0f + 0.044715f * x * x));
+  return 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
+}
+// d/dx of gelu_bwd above, differentiating the same expression:
+//   gelu_bwd = 0.5 x s D + 0.5 (1 + t),  t = tanh(u), u = k x (1 + c x^2),
+//   s = 1 - t^2, D = k + c3 x^2, du/dx = k (1 + 3 c x^2)
+__device__ __forceinline__ float gelu_bwd2(float x) {
+  const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
+  const float t = tanh_f(k * x * (1.0f + c * x * x));
+  const float s = 1.0f - t * t;
+  const float D = k + c3 * x * x;
+  const float du = k * (1.0f + 3.0f * c * x * x);
+  return 0.5f * s * D + 0.5f * s * du - x * t * s * du * D + c3 * x * x * s;
+}
+
+}  // namespace ttt

@@ -1,0 +1,130 @@
+"""TTT-Linear on the HIP path: forward/backward launchers and the autograd
+Function behind `linear_triton.TritonLinear` and `ops.ttt_linear`.
+
+Semantics are the reference ops path's (ops/ttt_linear.py:8-84): dual form
+with a general KxK eta, LayerNorm eps 1e-8, gradient of every input including
+a dense eta gradient.  Layouts follow TritonLinear (linear_triton.py:62-265):
+activations [B,H,NC,K,F], eta [B,H,NC,K,K], fast weights [B,H,F,F] and
+[B,H,1,F], LN parameters [H,F]."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._common import as_act, check_device, dtype_code, ptr, stream_of
+
+LN_EPS = 1e-8  # ops/ttt_utils.py:4,21
+
+
+def _check_shapes(ln_w, ln_b, W1, b1, XQ, XV, XK, eta):
+    if XQ.dim() != 5:
+        raise ValueError(f"XQ must be [B,H,NC,K,F], got {tuple(XQ.shape)}")
+    B, H, NC, K, F = XQ.shape
+    for name, t in (("XK", XK), ("XV", XV)):
+        if tuple(t.shape) != (B, H, NC, K, F):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != XQ shape {tuple(XQ.shape)}")
+    if tuple(eta.shape) != (B, H, NC, K, K):
+        raise ValueError(f"eta must be [B,H,NC,K,K]={(B, H, NC, K, K)}, got {tuple(eta.shape)}")
+    if tuple(W1.shape) != (B, H, F, F):
+        raise ValueError(f"W1 must be [B,H,F,F]={(B, H, F, F)}, got {tuple(W1.shape)}")
+    if tuple(b1.shape) != (B, H, 1, F):
+        raise ValueError(f"b1 must be [B,H,1,F]={(B, H, 1, F)}, got {tuple(b1.shape)}")
+    if tuple(ln_w.shape) != (H, F) or tuple(ln_b.shape) != (H, F):
+        raise ValueError(f"LN weight/bias must be [H,F]={(H, F)}")
+    return B, H, NC, K, F
+
+
+def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_EPS,
+                   want_ckpt: bool = True, want_last: bool = False):
+    """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
+    (W1_ckpt, b1_ckpt) or None, (W1_last, b1_last) or None)."""
+    B, H, NC, K, F = _check_shapes(ln_w, ln_b, W1, b1, XQ, XV, XK, eta)
+    dev = check_device(XQ, XK, XV, eta, W1, b1, ln_w, ln_b)
+    mp = XQ.dtype
+    code = dtype_code(mp)
+    G = int(G)
+    NK = math.ceil(NC / G)
+    xq, xk, xv, et = (as_act(t, mp) for t in (XQ, XK, XV, eta))
+    w1 = W1.detach().to(torch.float32).contiguous()
+    bb = b1.detach().to(torch.float32).contiguous()
+    lw = ln_w.detach().to(torch.float32).contiguous()
+    lb = ln_b.detach().to(torch.float32).contiguous()
+    out = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
+    ck = last = None
+    if want_ckpt:
+        ck = (torch.empty((B, H, NK, F, F), device=dev, dtype=torch.float32),
+              torch.empty((B, H, NK, 1, F), device=dev, dtype=torch.float32))
+    if want_last:
+        last = (torch.empty((B, H, F, F), device=dev, dtype=torch.float32),
+                torch.empty((B, H, 1, F), device=dev, dtype=torch.float32))
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.ttt_linear_fwd(
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb),
+            B, H, NC, K, F, G, code, float(eps), ptr(out),
+            ptr(last[0]) if last else None, ptr(last[1]) if last else None,
+            ptr(ck[0]) if ck else None, ptr(ck[1]) if ck else None, stream_of(dev))
+    _lib.check(st, "ttt_linear_fwd")
+    return out, ck, last
+
+
+def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, b1_ckpt, dout, G: int, eps: float = LN_EPS):
+    """Run the backward kernel.  Returns fp32 (dln_w [H,F], dln_b [H,F],
+    dW1 [B,H,F,F], db1 [B,H,1,F]) and (dXQ, dXV, dXK, deta) in XQ.dtype."""
+    B, H, NC, K, F = XQ.shape
+    dev = check_device(XQ, XK, XV, eta, W1_ckpt, b1_ckpt, dout)
+    mp = XQ.dtype
+    code = dtype_code(mp)
+    xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
+    lw = ln_w.detach().to(torch.float32).contiguous()
+    lb = ln_b.detach().to(torch.float32).contiguous()
+    dxq = torch.empty_like(xq)
+    dxk = torch.empty_like(xq)
+    dxv = torch.empty_like(xq)
+    deta = torch.empty_like(et)
+    dW = torch.empty((B, H, F, F), device=dev, dtype=torch.float32)
+    db = torch.empty((B, H, 1, F), device=dev, dtype=torch.float32)
+    dlw = torch.empty((B, H, F), device=dev, dtype=torch.float32)
+    dlb = torch.empty((B, H, F), device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    nbytes = lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, int(G))
+    ws = torch.empty((max(nbytes, 16) + 3) // 4, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        st = lib.ttt_linear_bwd(
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(W1_ckpt), ptr(b1_ckpt), ptr(do),
+            B, H, NC, K, F, int(G), code, float(eps),
+            ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW), ptr(db), ptr(dlw), ptr(dlb),
+            ptr(ws), ws.numel() * 4, stream_of(dev))
+    _lib.check(st, "ttt_linear_bwd")
+    return (dlw.sum(0), dlb.sum(0), dW, db), (dxq, dxv, dxk, deta)
+
+
+class TTTLinearFunction(torch.autograd.Function):
+    """autograd Function with TritonLinear's signature (linear_triton.py:15-60):
+    apply(ln_w, ln_b, W1_init, b1_init, XQ, XV, XK, eta, checkpoint_group_size[, eps])
+    -> XQW [B,H,NC,K,F] in XQ.dtype."""
+
+    @staticmethod
+    def forward(ctx, ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, XQ_batch, XV_batch, XK_batch, eta_batch,
+                checkpoint_group_size, eps=LN_EPS):
+        NC = XQ_batch.shape[2]
+        G = min(max(int(checkpoint_group_size), 1), NC)
+        out, ck, _ = linear_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, XQ_batch, XV_batch,
+                                    XK_batch, eta_batch, G, eps, want_ckpt=True)
+        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck)
+        ctx.G, ctx.eps = G, eps
+        ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype,
+                      XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        XQ, XV, XK, eta, lw, lb, Wc, bc = ctx.saved_tensors
+        (dlw, dlb, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
+            lw, lb, XQ, XV, XK, eta, Wc, bc, grad_out, ctx.G, ctx.eps)
+        grads = (dlw, dlb, dW, db, dxq, dxv, dxk, deta)
+        grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
+        return grads + (None, None)
