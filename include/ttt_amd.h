@@ -84,6 +84,24 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
                    void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1,
                    float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
 
+/* TTT-MLP forward (2-layer GELU(tanh) fast-weight MLP) over all NC
+ * mini-batches.  Replaces ttt_mlp_scan_forward (kernels/mlp_forward.py:6-237)
+ * as launched by TritonMLP._forward_core (mlp_triton.py:71-197), and is the
+ * forward of ops.ttt_mlp (ops/ttt_mlp.py:70-99).  FF in {64, 128, 256}.
+ *   W1_init [B,H,F,FF], b1_init [B,H,1,FF], W2_init [B,H,FF,F], b2_init [B,H,1,F] fp32
+ *   out               [B,H,NC,K,F] dtype
+ *   *_last            final state, shapes of *_init (all four or none)
+ *   *_ckpt            [B,H,NK,...] state entering mini-batch k*G (all four or none)
+ *   *_memo            [B,H,NS,...], NS = ceil(NC/M): state after mini-batch
+ *                     s*M has been applied (all four or none; M >= 1 then) */
+int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
+                const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
+                const float* W2_init, const float* b2_init,
+                int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
+                void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last,
+                float* W1_ckpt, float* b1_ckpt, float* W2_ckpt, float* b2_ckpt,
+                float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,84 @@
+"""TTT-MLP HIP kernels vs the CPU oracle (forward, side outputs, backward,
+cached readout).  Tolerances as for TTT-Linear: fp32 max-abs <= 1e-4 (scaled
+by the tensor's magnitude above 1), bf16 rel-L2 <= 2e-2."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import ttt_oracle as O
+from tests._util import max_abs, oracle_mlp_grads, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_RTOL = 2e-2
+
+
+def fp32_bound(ref):
+    return FP32_ATOL * max(1.0, float(ref.abs().max()))
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+KEYS = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
+
+
+def _fwd(d, G, M=0):
+    from ttt_amd.mlp import mlp_forward
+    g = to_dev(d)
+    return mlp_forward(*(g[k] for k in KEYS), G, M=M, want_ckpt=True, want_last=True)
+
+
+def _perturb(d, H, F_, FF, seed):
+    gen = torch.Generator().manual_seed(seed)
+    d["ln_w"] = 1 + 0.2 * torch.randn(H, F_, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(H, F_, generator=gen)
+    d["b1"] = 0.1 * torch.randn(*d["b1"].shape, generator=gen)
+    d["b2"] = 0.1 * torch.randn(*d["b2"].shape, generator=gen)
+    return d
+
+
+@pytest.mark.parametrize("FF", [64, 128, 256])
+def test_mlp_fwd_fp32(FF):
+    _say("mlp fwd fp32 FF", FF)
+    d = _perturb(O.make_inputs(2, 2, 6, 16, 64, FF=FF, seed=1, dtype=torch.float32), 2, 64, FF, 3)
+    out, ck, memo, last = _fwd(d, G=4, M=2)
+    ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=4, M=2)
+    bad = []
+    for name, mine in (("out", out), ("W1_last", last[0]), ("b1_last", last[1]), ("W2_last", last[2]),
+                       ("b2_last", last[3]), ("W1_ckpt", ck[0]), ("W2_ckpt", ck[2]), ("b2_ckpt", ck[3]),
+                       ("W1_memo", memo[0]), ("b1_memo", memo[1]), ("W2_memo", memo[2]), ("b2_memo", memo[3])):
+        err = max_abs(mine, ref[name])
+        _say(f"  {name}: max-abs {err:.3e}")
+        if err > fp32_bound(ref[name]):
+            bad.append(name)
+    assert not bad
+
+
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_mlp_fwd_bf16_ff256(kind):
+    _say("mlp fwd bf16 FF256", kind)
+    d = O.make_inputs(2, 3, 24, 16, 64, FF=256, seed=2, dtype=torch.bfloat16, eta_kind=kind)
+    out, ck, memo, last = _fwd(d, G=8, M=2)
+    ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=8, M=2)
+    bad = []
+    for name, mine in (("out", out), ("W1_last", last[0]), ("W2_last", last[2]), ("W1_ckpt", ck[0]),
+                       ("W2_memo", memo[2])):
+        err = rel_l2(mine, ref[name])
+        _say(f"  {name}: rel-L2 {err:.3e}")
+        if err > BF16_RTOL:
+            bad.append(name)
+    assert not bad
+
+
+def test_mlp_fwd_headdim32():
+    _say("mlp fwd fp32 F32 FF64")
+    d = O.make_inputs(1, 2, 5, 16, 32, FF=64, seed=4, dtype=torch.float32)
+    out, _, _, last = _fwd(d, G=2)
+    ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=2)
+    assert max_abs(out, ref["out"]) <= FP32_ATOL
+    assert max_abs(last[2], ref["W2_last"]) <= FP32_ATOL

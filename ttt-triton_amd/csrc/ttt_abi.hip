@@ -162,4 +162,72 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   return hip_status(ttt::launch_linear_bwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                const float* ln_b, const float* W1_init, const float* b1_init, const float* W2_init,
+                const float* b2_init, int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
+                void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last, float* W1_ckpt,
+                float* b1_ckpt, float* W2_ckpt, float* b2_ckpt, float* W1_memo, float* b1_memo, float* W2_memo,
+                float* b2_memo, void* stream) {
+  int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  REQUIRE_PTR(XQ);
+  REQUIRE_PTR(XK);
+  REQUIRE_PTR(XV);
+  REQUIRE_PTR(eta);
+  REQUIRE_PTR(ln_w);
+  REQUIRE_PTR(ln_b);
+  REQUIRE_PTR(W1_init);
+  REQUIRE_PTR(b1_init);
+  REQUIRE_PTR(W2_init);
+  REQUIRE_PTR(b2_init);
+  REQUIRE_PTR(out);
+  const float* groups[3][4] = {{W1_last, b1_last, W2_last, b2_last},
+                               {W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt},
+                               {W1_memo, b1_memo, W2_memo, b2_memo}};
+  for (auto& grp : groups) {
+    const bool any = grp[0] || grp[1] || grp[2] || grp[3];
+    const bool all = grp[0] && grp[1] && grp[2] && grp[3];
+    if (any && !all) return TTT_ERR_NULL;
+    for (const float* q : grp) OPTIONAL_PTR(q);
+  }
+  if (W1_memo != nullptr && (M < 1 || M > NC)) return TTT_ERR_ARG;
+
+  ttt::MlpFwdParams p;
+  p.XQ = XQ;
+  p.XK = XK;
+  p.XV = XV;
+  p.eta = eta;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.W1_init = W1_init;
+  p.b1_init = b1_init;
+  p.W2_init = W2_init;
+  p.b2_init = b2_init;
+  p.out = out;
+  p.W1_last = W1_last;
+  p.b1_last = b1_last;
+  p.W2_last = W2_last;
+  p.b2_last = b2_last;
+  p.W1_ckpt = W1_ckpt;
+  p.b1_ckpt = b1_ckpt;
+  p.W2_ckpt = W2_ckpt;
+  p.b2_ckpt = b2_ckpt;
+  p.W1_memo = W1_memo;
+  p.b1_memo = b1_memo;
+  p.W2_memo = W2_memo;
+  p.b2_memo = b2_memo;
+  p.B = B;
+  p.H = H;
+  p.NC = NC;
+  p.F = F;
+  p.FF = FF;
+  p.G = G;
+  p.NK = (NC + G - 1) / G;
+  p.M = W1_memo != nullptr ? M : 1;
+  p.NS = (NC + p.M - 1) / p.M;
+  p.eps = eps;
+  return hip_status(ttt::launch_mlp_fwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

@@ -27,6 +27,19 @@ struct LinearBwdParams {
   float eps;
 };
 
+struct MlpFwdParams {
+  const void *XQ, *XK, *XV, *eta;
+  const float *ln_w, *ln_b, *W1_init, *b1_init, *W2_init, *b2_init;
+  void* out;
+  float *W1_last, *b1_last, *W2_last, *b2_last;
+  float *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
+  float *W1_memo, *b1_memo, *W2_memo, *b2_memo;
+  int B, H, NC, F, FF, G, NK, M, NS;
+  float eps;
+};
+
+hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream);
+
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t stream);
 

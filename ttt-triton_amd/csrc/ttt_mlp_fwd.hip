@@ -1,0 +1,352 @@
+// TTT-MLP mini-batch forward on gfx950.
+//
+// One workgroup per (batch, head) chain with NW = FF/64 wavefronts.  Wave w
+// owns hidden units [64w, 64w+64): its slice of W1 (F x 64) and W2 (64 x F)
+// stays in registers (fp32, MFMA accumulator layout) for all NC mini-batches;
+// b2 is replicated in every wave.  Per mini-batch of K = 16 tokens
+// (ops/ttt_mlp.py:9-67, dual form with a full KxK eta):
+//
+//   Z1 = XK W1 + b1, X2 = gelu(Z1)               per wave, its 64 hidden units
+//   Z2 = sum_w X2_w W2_w + b2                     partial sums reduced through LDS
+//   G2 = ln_fused_l2_bwd(Z2, XV - XK)             every wave, token-major rows
+//   G1 = (G2 W2^T) (.) gelu'(Z1)                  per wave
+//   Z1b = XQ W1 - (eta o XQ XK^T + eta) G1 + b1, X2b = gelu(Z1b)
+//   Z2b = sum_w X2b_w W2_w - (eta o X2b X2^T + eta) G2 + b2
+//   out = XQ + LN(Z2b)                            wave w writes feature tiles w, w+NW, ...
+//   W1 -= XK^T diag(e) G1, W2 -= X2^T diag(e) G2, b -= G^T e   (e = eta[K-1])
+//
+// Checkpoints hold the state entering mini-batch k*G
+// (kernels/mlp_forward.py:84-117); memo snapshot s holds the state after
+// mini-batch s*M is applied (kernels/mlp_forward.py:193-226).
+#include "ttt_kernels.h"
+#include "ttt_ln.h"
+
+namespace ttt {
+
+template <int FT, int NW> struct MlpFwdShared {
+  f4 z2p[NW][FT][64];   // per-wave partial Z2 (token-major tiles, register order)
+  f4 z2bp[NW][FT][64];  // per-wave partial X2b W2
+  f4 a2p[NW][64];       // per-wave partial (X2b X2^T)^T
+};
+
+template <typename T, int FT, int NW>
+__global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
+  constexpr int F = 16 * FT;
+  constexpr int K = 16;
+  constexpr int HT = 4;  // hidden tiles per wave
+  constexpr int FF = 64 * NW;
+  __shared__ MlpFwdShared<FT, NW> sh;
+
+  const int chain = blockIdx.x;
+  const int h = chain % p.H;
+  const int NC = p.NC;
+  const int wave = threadIdx.x >> 6;
+  const int l = lane_id(), g = l >> 4, n = l & 15;
+  const int hs = 64 * wave;  // first hidden unit of this wave
+
+  const size_t xoff = (size_t)chain * NC * K * F;
+  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
+  const T* __restrict__ XK = static_cast<const T*>(p.XK) + xoff;
+  const T* __restrict__ XV = static_cast<const T*>(p.XV) + xoff;
+  const T* __restrict__ ETA = static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
+  T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
+
+  // state slice: W1[:, hs:hs+64] as tiles [f block][hidden block], W2[hs:hs+64, :]
+  Tile W1[FT][HT], W2[HT][FT];
+  float b1_tm[HT], b2_tm[FT];
+  {
+    const float* w1 = p.W1_init + (size_t)chain * F * FF;
+    const float* w2 = p.W2_init + (size_t)chain * FF * F;
+#pragma unroll
+    for (int i = 0; i < FT; ++i)
+#pragma unroll
+      for (int o = 0; o < HT; ++o) W1[i][o] = load_tile(w1, FF, 16 * i, hs + 16 * o);
+#pragma unroll
+    for (int i = 0; i < HT; ++i)
+#pragma unroll
+      for (int o = 0; o < FT; ++o) W2[i][o] = load_tile(w2, F, hs + 16 * i, 16 * o);
+#pragma unroll
+    for (int o = 0; o < HT; ++o) b1_tm[o] = p.b1_init[(size_t)chain * FF + hs + 16 * o + n];
+#pragma unroll
+    for (int o = 0; o < FT; ++o) b2_tm[o] = p.b2_init[(size_t)chain * F + 16 * o + n];
+  }
+  float lnw_tm[FT], lnb_tm[FT];
+#pragma unroll
+  for (int o = 0; o < FT; ++o) {
+    lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
+    lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
+  }
+  const float eps = p.eps;
+  const Frag<T> I = identity_frag<T>();
+
+  auto store_state = [&](float* w1d, float* b1d, float* w2d, float* b2d) {
+#pragma unroll
+    for (int i = 0; i < FT; ++i)
+#pragma unroll
+      for (int o = 0; o < HT; ++o) store_tile(w1d, FF, 16 * i, hs + 16 * o, W1[i][o]);
+#pragma unroll
+    for (int i = 0; i < HT; ++i)
+#pragma unroll
+      for (int o = 0; o < FT; ++o) store_tile(w2d, F, hs + 16 * i, 16 * o, W2[i][o]);
+    if (g == 0) {
+#pragma unroll
+      for (int o = 0; o < HT; ++o) b1d[hs + 16 * o + n] = b1_tm[o];
+      if (wave == 0) {
+#pragma unroll
+        for (int o = 0; o < FT; ++o) b2d[16 * o + n] = b2_tm[o];
+      }
+    }
+  };
+
+  for (int s = 0; s < NC; ++s) {
+    if (p.W1_ckpt != nullptr && (s % p.G) == 0) {
+      const size_t k = (size_t)chain * p.NK + s / p.G;
+      store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt + k * FF, p.W2_ckpt + k * FF * F, p.b2_ckpt + k * F);
+    }
+    const size_t xo = (size_t)s * K * F;
+    const T* etas = ETA + (size_t)s * K * K;
+    Frag<T> xq[1][FT], xk[1][FT];
+#pragma unroll
+    for (int q = 0; q < FT; ++q) {
+      xq[0][q] = load_frag(XQ + xo, F, 16 * q);
+      xk[0][q] = load_frag(XK + xo, F, 16 * q);
+    }
+
+    // ---- layer 1 on this wave's hidden units (token-major)
+    Frag<T> x2f[HT];     // token-major frags of X2 (free = hidden, k = t)
+    Frag<T> x2F[1][HT];  // feature-major frags of X2 (free = t, k = hidden)
+    f4 gp[HT];           // gelu'(Z1)
+    {
+      Tile z1[1][HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) z1[0][o].v = f4{b1_tm[o], b1_tm[o], b1_tm[o], b1_tm[o]};
+      gemm_pt<1, HT, FT>(z1, xk, W1);
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        f4 x2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x2[j] = gelu_tanh(z1[0][o].v[j]);
+          gp[o][j] = gelu_bwd(z1[0][o].v[j]);
+        }
+        x2f[o] = to_frag<T>(x2);
+        x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
+      }
+    }
+    {
+      Tile z2p[1][FT];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) z2p[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
+      gemm_pt<1, FT, HT>(z2p, x2F, W2);
+#pragma unroll
+      for (int o = 0; o < FT; ++o) sh.z2p[wave][o][l] = z2p[0][o].v;
+    }
+    __syncthreads();
+
+    // ---- Z2 and its inner-loss gradient (every wave, identical)
+    Frag<T> xkTf[FT];
+    Tile G2[FT];
+    {
+      f4 tgt[FT];
+#pragma unroll
+      for (int q = 0; q < FT; ++q) {
+        const Tile xkT = transpose16(xk[0][q], I);
+        xkTf[q] = to_frag<T>(xkT.v);
+        tgt[q] = transpose16(load_frag(XV + xo, F, 16 * q), I).v - xkT.v;
+      }
+      Tile z2[FT];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        z2[o].v = f4{b2_tm[o], b2_tm[o], b2_tm[o], b2_tm[o]};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) z2[o].v += sh.z2p[w][o][l];
+      }
+      LnL2TM<FT> ln;
+      ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
+    }
+
+    // ---- G1 = (G2 W2^T) (.) gelu'(Z1); W2^T blocks by exact transposes
+    Tile G1[HT];
+    {
+      Frag<T> g2F[1][FT];  // feature-major frags of G2 (free = t, k = f)
+#pragma unroll
+      for (int o = 0; o < FT; ++o) g2F[0][o] = to_frag<T>(transpose16(to_frag<T>(G2[o].v), I).v);
+#pragma unroll
+      for (int i = 0; i < HT; ++i) {
+        G1[i].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q + 1 < FT; q += 2) {
+          const Frag<T> t0 = to_frag<T>(transpose16(to_frag<T>(W2[i][q].v), I).v);
+          const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
+          mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
+        }
+        G1[i].v *= gp[i];
+      }
+    }
+
+    // ---- readout layer 1: Z1b = XQ W1 - (eta o A1 + eta) G1 + b1, X2b = gelu(Z1b)
+    const f4 etaT = load_f4(etas, K, 0);  // [t_k x t_q]: eta[n][4g+j]
+    Frag<T> x2bF[1][HT];
+    {
+      Tile at[1][1];
+      at[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
+      gemm<1, 1, FT>(at, xk, xq);  // (XQ XK^T)^T
+      f4 m1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m1[j] = -(etaT[j] * at[0][0].v[j] + etaT[j]);
+      const Frag<T> m1f = to_frag<T>(m1);
+      Tile zb[1][HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) zb[0][o].v = f4{b1_tm[o], b1_tm[o], b1_tm[o], b1_tm[o]};
+      gemm_pt<1, HT, FT>(zb, xq, W1);
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        mma16(zb[0][o].v, m1f, to_frag<T>(G1[o].v));
+        f4 x2b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x2b[j] = gelu_tanh(zb[0][o].v[j]);
+        x2bF[0][o] = to_frag<T>(transpose16(to_frag<T>(x2b), I).v);
+      }
+    }
+    {
+      Tile z2bp[1][FT], a2p[1][1];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) z2bp[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
+      a2p[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
+      gemm_pt<1, FT, HT>(z2bp, x2bF, W2);   // uses W2 before the update
+      gemm<1, 1, HT>(a2p, x2F, x2bF);       // (X2b X2^T)^T over this wave's units
+#pragma unroll
+      for (int o = 0; o < FT; ++o) sh.z2bp[wave][o][l] = z2bp[0][o].v;
+      sh.a2p[wave][l] = a2p[0][0].v;
+    }
+    const f4 e = load4(etas + (K - 1) * K + 4 * g);
+
+    // ---- state update (the readout above used the state entering s)
+    float b2_old[FT];
+#pragma unroll
+    for (int o = 0; o < FT; ++o) b2_old[o] = b2_tm[o];
+    {
+      Frag<T> g1e[HT], g2e[FT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        f4 v;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = -e[j] * G1[o].v[j];
+          acc += e[j] * G1[o].v[j];
+        }
+        g1e[o] = to_frag<T>(v);
+        b1_tm[o] -= sum_col4(acc);
+      }
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        f4 v;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = -e[j] * G2[o].v[j];
+          acc += e[j] * G2[o].v[j];
+        }
+        g2e[o] = to_frag<T>(v);
+        b2_tm[o] -= sum_col4(acc);
+      }
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int o = 0; o < HT; ++o) mma16(W1[i][o].v, xkTf[i], g1e[o]);
+#pragma unroll
+      for (int i = 0; i < HT; ++i)
+#pragma unroll
+        for (int o = 0; o < FT; ++o) mma16(W2[i][o].v, x2f[i], g2e[o]);
+    }
+    __syncthreads();
+
+    // ---- readout layer 2, LayerNorm, residual
+    {
+      Tile a2[1];
+      a2[0].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NW; ++w) a2[0].v += sh.a2p[w][l];
+      f4 m2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m2[j] = -(etaT[j] * a2[0].v[j] + etaT[j]);
+      const Frag<T> m2f = to_frag<T>(m2);
+      Tile z2b[FT];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        z2b[o].v = f4{b2_old[o], b2_old[o], b2_old[o], b2_old[o]};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) z2b[o].v += sh.z2bp[w][o][l];
+        mma16(z2b[o].v, m2f, to_frag<T>(G2[o].v));
+      }
+      // LayerNorm over features of each token row (token-major)
+      constexpr float invF = 1.0f / F;
+      f4 mu, rs;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int o = 0; o < FT; ++o) acc += z2b[o].v[j];
+        mu[j] = sum_row16(acc) * invF;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          const float d = z2b[o].v[j] - mu[j];
+          acc += d * d;
+        }
+        rs[j] = 1.0f / sqrtf(sum_row16(acc) * invF + eps);
+      }
+      T* o_s = OUT + xo;
+      for (int o = wave; o < FT; o += NW) {
+        const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
+        f4 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = q[j] + lnw_tm[o] * ((z2b[o].v[j] - mu[j]) * rs[j]) + lnb_tm[o];
+        store_f4(o_s, F, 16 * o, transpose16(to_frag<T>(y), I).v);
+      }
+    }
+
+    if (p.W1_memo != nullptr && (s % p.M) == 0) {
+      const size_t k = (size_t)chain * p.NS + s / p.M;
+      store_state(p.W1_memo + k * F * FF, p.b1_memo + k * FF, p.W2_memo + k * FF * F, p.b2_memo + k * F);
+    }
+  }
+
+  if (p.W1_last != nullptr) {
+    store_state(p.W1_last + (size_t)chain * F * FF, p.b1_last + (size_t)chain * FF, p.W2_last + (size_t)chain * FF * F,
+                p.b2_last + (size_t)chain * F);
+  }
+}
+
+template <typename T, int FT, int NW>
+static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T, int FT>
+static hipError_t launch_mlp_fwd_f(const MlpFwdParams& p, hipStream_t stream) {
+  switch (p.FF) {
+    case 64: return launch_mlp_fwd_t<T, FT, 1>(p, stream);
+    case 128: return launch_mlp_fwd_t<T, FT, 2>(p, stream);
+    case 256: return launch_mlp_fwd_t<T, FT, 4>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream) {
+  if (dtype == TTT_DTYPE_BF16) {
+    if (p.F == 64) return launch_mlp_fwd_f<__bf16, 4>(p, stream);
+    if (p.F == 32) return launch_mlp_fwd_f<__bf16, 2>(p, stream);
+  } else {
+    if (p.F == 64) return launch_mlp_fwd_f<float, 4>(p, stream);
+    if (p.F == 32) return launch_mlp_fwd_f<float, 2>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ttt

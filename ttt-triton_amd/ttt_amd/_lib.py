@@ -30,6 +30,7 @@ SIGNATURES = {
     "ttt_linear_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
     "ttt_linear_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),
+    "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 14),
 }
 
 _lock = threading.Lock()

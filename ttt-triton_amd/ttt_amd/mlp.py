@@ -1,0 +1,86 @@
+"""TTT-MLP on the HIP path: forward/backward launchers, the autograd Function
+behind `mlp_triton.TritonMLP` and `ops.ttt_mlp`, and the fixed-weight readout
+behind `kernels.mlp_cached_readout.mlp_cached_readout_triton`.
+
+Semantics are the reference ops path's (ops/ttt_mlp.py:9-99): two-layer
+GELU(tanh) fast-weight MLP, dual form for both layers with a general KxK eta,
+LayerNorm eps 1e-8, gradients of every input including a dense eta gradient.
+Layouts follow TritonMLP (mlp_triton.py:71-351): W1 [B,H,F,FF], b1 [B,H,1,FF],
+W2 [B,H,FF,F], b2 [B,H,1,F]; memo snapshots [B,H,NS,...] fp32."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._common import as_act, check_device, dtype_code, ptr, stream_of
+
+LN_EPS = 1e-8  # ops/ttt_utils.py:4,21
+
+
+def _f32(t):
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
+    if XQ.dim() != 5:
+        raise ValueError(f"XQ must be [B,H,NC,K,F], got {tuple(XQ.shape)}")
+    B, H, NC, K, F = XQ.shape
+    FF = W1.shape[-1]
+    for name, t in (("XK", XK), ("XV", XV)):
+        if tuple(t.shape) != (B, H, NC, K, F):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != XQ shape {tuple(XQ.shape)}")
+    if tuple(eta.shape) != (B, H, NC, K, K):
+        raise ValueError(f"eta must be [B,H,NC,K,K]={(B, H, NC, K, K)}, got {tuple(eta.shape)}")
+    # mlp_triton.py:91-94
+    if tuple(W1.shape) != (B, H, F, FF):
+        raise ValueError(f"W1 must be [B,H,F,FF]={(B, H, F, FF)}, got {tuple(W1.shape)}")
+    if tuple(b1.shape) != (B, H, 1, FF):
+        raise ValueError(f"b1 must be [B,H,1,FF]={(B, H, 1, FF)}, got {tuple(b1.shape)}")
+    if tuple(W2.shape) != (B, H, FF, F):
+        raise ValueError(f"W2 must be [B,H,FF,F]={(B, H, FF, F)}, got {tuple(W2.shape)}")
+    if tuple(b2.shape) != (B, H, 1, F):
+        raise ValueError(f"b2 must be [B,H,1,F]={(B, H, 1, F)}, got {tuple(b2.shape)}")
+    if tuple(ln_w.shape) != (H, F) or tuple(ln_b.shape) != (H, F):
+        raise ValueError(f"LN weight/bias must be [H,F]={(H, F)}")
+    return B, H, NC, K, F, FF
+
+
+def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0, eps: float = LN_EPS,
+                want_ckpt: bool = True, want_last: bool = False):
+    """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
+    ckpt (W1,b1,W2,b2) or None, memo (W1,b1,W2,b2) or None, last or None)."""
+    B, H, NC, K, F, FF = _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta)
+    dev = check_device(XQ, XK, XV, eta, W1, b1, W2, b2, ln_w, ln_b)
+    mp = XQ.dtype
+    code = dtype_code(mp)
+    G = int(G)
+    NK = math.ceil(NC / G)
+    xq, xk, xv, et = (as_act(t, mp) for t in (XQ, XK, XV, eta))
+    w1, bb1, w2, bb2, lw, lb = (_f32(t) for t in (W1, b1, W2, b2, ln_w, ln_b))
+    out = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
+
+    def state(n):
+        lead = (B, H) if n is None else (B, H, n)
+        return (torch.empty(lead + (F, FF), device=dev, dtype=torch.float32),
+                torch.empty(lead + (1, FF), device=dev, dtype=torch.float32),
+                torch.empty(lead + (FF, F), device=dev, dtype=torch.float32),
+                torch.empty(lead + (1, F), device=dev, dtype=torch.float32))
+
+    ck = state(NK) if want_ckpt else None
+    memo = state(math.ceil(NC / M)) if M and M > 0 else None
+    last = state(None) if want_last else None
+    none4 = (None, None, None, None)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.ttt_mlp_fwd(
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb1), ptr(w2), ptr(bb2),
+            B, H, NC, K, F, FF, G, int(M) if M else 0, code, float(eps), ptr(out),
+            *(tuple(ptr(t) for t in last) if last else none4),
+            *(tuple(ptr(t) for t in ck) if ck else none4),
+            *(tuple(ptr(t) for t in memo) if memo else none4),
+            stream_of(dev))
+    _lib.check(st, "ttt_mlp_fwd")
+    return out, ck, memo, last
