@@ -102,6 +102,26 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 float* W1_ckpt, float* b1_ckpt, float* W2_ckpt, float* b2_ckpt,
                 float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo, void* stream);
 
+/* Bytes of device workspace ttt_mlp_bwd needs for these sizes. */
+size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int G, int dtype);
+
+/* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
+ * state's gradient zero, as in the ops path).  Replaces ttt_mlp_scan_backward
+ * (kernels/mlp_backward.py:247-651) as launched by TritonMLP._backward_core
+ * (mlp_triton.py:200-351).
+ *   *_ckpt           checkpoints written by ttt_mlp_fwd with the same G
+ *   dout             [B,H,NC,K,F] dtype
+ *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
+ *   dW1, db1, dW2, db2  fp32, shapes of W1_init ... (gradient wrt the initial state)
+ *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
+ *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes */
+int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
+                const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
+                const float* W2_ckpt, const float* b2_ckpt, const void* dout,
+                int B, int H, int NC, int K, int F, int FF, int G, int dtype, float eps,
+                void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
+                float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

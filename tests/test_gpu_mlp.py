@@ -82,3 +82,41 @@ def test_mlp_fwd_headdim32():
     ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=2)
     assert max_abs(out, ref["out"]) <= FP32_ATOL
     assert max_abs(last[2], ref["W2_last"]) <= FP32_ATOL
+
+
+def _bwd(d, G):
+    from ttt_amd.mlp import mlp_backward
+    g = to_dev(d)
+    out, ck, _, _ = _fwd(d, G)
+    (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, g["dOut"], G)
+    return dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2, dln_w=dlw, dln_b=dlb)
+
+
+@pytest.mark.parametrize("FF", [64, 256])
+def test_mlp_bwd_fp32(FF):
+    _say("mlp bwd fp32 FF", FF)
+    d = _perturb(O.make_inputs(1, 2, 5, 16, 64, FF=FF, seed=5, dtype=torch.float32, with_grad=True), 2, 64, FF, 6)
+    mine = _bwd(d, G=2)
+    ref = oracle_mlp_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        err = max_abs(mine[k], ref[k])
+        _say(f"  {k}: max-abs {err:.3e} bound {fp32_bound(ref[k]):.3e} rel-L2 {rel_l2(mine[k], ref[k]):.3e}")
+        if err > fp32_bound(ref[k]):
+            bad.append(k)
+    assert not bad
+
+
+def test_mlp_bwd_bf16_ff256():
+    _say("mlp bwd bf16 FF256")
+    d = O.make_inputs(2, 2, 16, 16, 64, FF=256, seed=7, dtype=torch.bfloat16, with_grad=True)
+    mine = _bwd(d, G=8)
+    ref = oracle_mlp_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        err = rel_l2(mine[k], ref[k])
+        _say(f"  {k}: rel-L2 {err:.3e}")
+        if err > BF16_RTOL:
+            bad.append(k)
+    assert not bad

@@ -230,4 +230,60 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   return hip_status(ttt::launch_mlp_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int G, int dtype) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0 || G <= 0) return 0;
+  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
+  const int g = G < NC ? G : NC;
+  return (size_t)B * H * g * ttt::mlp_bwd_slot_bytes(F, FF, dtype);
+}
+
+int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
+                const float* b2_ckpt, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
+                float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
+                float* db2, float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  const void* req[] = {XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt, dout,
+                       dXQ, dXK, dXV, deta, dW1, db1, dW2, db2, dln_w, dln_b};
+  for (const void* q : req) REQUIRE_PTR(q);
+  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return TTT_ERR_ALIGN;
+  if (workspace_bytes < ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, dtype)) return TTT_ERR_WORKSPACE;
+
+  ttt::MlpBwdParams p;
+  p.XQ = XQ;
+  p.XK = XK;
+  p.XV = XV;
+  p.eta = eta;
+  p.dout = dout;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.W1_ckpt = W1_ckpt;
+  p.b1_ckpt = b1_ckpt;
+  p.W2_ckpt = W2_ckpt;
+  p.b2_ckpt = b2_ckpt;
+  p.dXQ = dXQ;
+  p.dXK = dXK;
+  p.dXV = dXV;
+  p.deta = deta;
+  p.dW1 = dW1;
+  p.db1 = db1;
+  p.dW2 = dW2;
+  p.db2 = db2;
+  p.dln_w = dln_w;
+  p.dln_b = dln_b;
+  p.ws = workspace;
+  p.B = B;
+  p.H = H;
+  p.NC = NC;
+  p.F = F;
+  p.FF = FF;
+  p.G = G;
+  p.NK = (NC + G - 1) / G;
+  p.eps = eps;
+  return hip_status(ttt::launch_mlp_bwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

@@ -38,6 +38,19 @@ struct MlpFwdParams {
   float eps;
 };
 
+struct MlpBwdParams {
+  const void *XQ, *XK, *XV, *eta, *dout;
+  const float *ln_w, *ln_b, *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
+  void *dXQ, *dXK, *dXV, *deta;
+  float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
+  void* ws;  // per-chain: G slots of the state's operand values
+  int B, H, NC, F, FF, G, NK;
+  float eps;
+};
+
+hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
+size_t mlp_bwd_slot_bytes(int F, int FF, int dtype);
+
 hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream);
 
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);

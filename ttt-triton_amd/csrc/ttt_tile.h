@@ -72,9 +72,19 @@ template <typename T> __device__ __forceinline__ f4 frag_to_f4(Frag<T> f) {
 }
 
 // ---------------------------------------------------------------- MFMA
-// acc += P * Q over one 16-deep k-block
+// acc += P * Q over one 16-deep k-block.
+//
+// bf16 uses only v_mfma_f32_16x16x32_bf16 (upper k-half zero for a 16-deep
+// block).  On gfx950, a 16x16x16 bf16 MFMA issued back to back with a
+// 16x16x32 bf16 MFMA that reads its result as the accumulator produces wrong
+// values unless the pair is padded, and the compiler inserts no padding for
+// that mixed-opcode pair; same-opcode accumulation chains are forwarded
+// correctly.  Both opcodes issue at the same rate, so the zero half is free.
 __device__ __forceinline__ void mma16(f4& acc, Frag<__bf16> p, Frag<__bf16> q) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p.v, q.v, acc, 0, 0, 0);
+  const bf4 z = {(__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f, (__bf16)0.0f};
+  const bf8 a = __builtin_shufflevector(p.v, z, 0, 1, 2, 3, 4, 5, 6, 7);
+  const bf8 b = __builtin_shufflevector(q.v, z, 0, 1, 2, 3, 4, 5, 6, 7);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 __device__ __forceinline__ void mma16(f4& acc, Frag<float> p, Frag<float> q) {
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[0], q.v[0], acc, 0, 0, 0);

@@ -31,6 +31,8 @@ SIGNATURES = {
     "ttt_linear_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),
     "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 14),
+    "ttt_mlp_bwd_workspace_bytes": (_S, [_I] * 8),
+    "ttt_mlp_bwd": (_I, [_P] * 11 + [_I] * 8 + [_F] + [_P] * 11 + [_S, _P]),
 }
 
 _lock = threading.Lock()

@@ -84,3 +84,66 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
             stream_of(dev))
     _lib.check(st, "ttt_mlp_fwd")
     return out, ck, memo, last
+
+
+def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, dout, G: int, eps: float = LN_EPS):
+    """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints from
+    mlp_forward with the same G.  Returns fp32 (dln_w [H,F], dln_b [H,F], dW1,
+    db1, dW2, db2) and (dXQ, dXV, dXK, deta) in XQ.dtype."""
+    B, H, NC, K, F = XQ.shape
+    FF = ckpt[0].shape[-1]
+    dev = check_device(XQ, XK, XV, eta, dout, *ckpt)
+    mp = XQ.dtype
+    code = dtype_code(mp)
+    xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
+    lw, lb = _f32(ln_w), _f32(ln_b)
+    dxq, dxk, dxv = torch.empty_like(xq), torch.empty_like(xq), torch.empty_like(xq)
+    deta = torch.empty_like(et)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dW1, db1 = torch.empty((B, H, F, FF), **f32), torch.empty((B, H, 1, FF), **f32)
+    dW2, db2 = torch.empty((B, H, FF, F), **f32), torch.empty((B, H, 1, F), **f32)
+    dlw, dlb = torch.empty((B, H, F), **f32), torch.empty((B, H, F), **f32)
+    lib = _lib.load()
+    nbytes = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, int(G), code)
+    ws = torch.empty(((max(nbytes, 16) + 15) // 16) * 4, **f32)
+    with torch.cuda.device(dev):
+        st = lib.ttt_mlp_bwd(
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), *(ptr(t) for t in ckpt), ptr(do),
+            B, H, NC, K, F, FF, int(G), code, float(eps),
+            ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
+            ptr(ws), ws.numel() * 4, stream_of(dev))
+    _lib.check(st, "ttt_mlp_bwd")
+    return (dlw.sum(0), dlb.sum(0), dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
+
+
+class TTTMLPFunction(torch.autograd.Function):
+    """autograd Function with TritonMLP's signature (mlp_triton.py:15-69):
+    apply(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, checkpoint_group_size,
+    memo_segment_size[, eps]) -> (XQW [B,H,NC,K,F] in XQ.dtype, W1_memo, b1_memo,
+    W2_memo, b2_memo); the memo snapshots are fp32 and non-differentiable."""
+
+    @staticmethod
+    def forward(ctx, ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init, XQ_batch, XV_batch,
+                XK_batch, eta_batch, checkpoint_group_size, memo_segment_size, eps=LN_EPS):
+        NC = XQ_batch.shape[2]
+        G = min(max(int(checkpoint_group_size), 1), NC)
+        M = int(memo_segment_size)
+        out, ck, memo, _ = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
+                                       XQ_batch, XV_batch, XK_batch, eta_batch, G, M=M, eps=eps, want_ckpt=True)
+        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck)
+        ctx.G, ctx.eps = G, eps
+        ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype, W2_init.dtype,
+                      b2_init.dtype, XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
+        if memo is None:
+            memo = tuple(torch.empty(0, device=XQ_batch.device) for _ in range(4))
+        ctx.mark_non_differentiable(*memo)
+        return (out,) + tuple(memo)
+
+    @staticmethod
+    def backward(ctx, grad_out, *unused):
+        XQ, XV, XK, eta, lw, lb, W1c, b1c, W2c, b2c = ctx.saved_tensors
+        (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
+            lw, lb, XQ, XV, XK, eta, (W1c, b1c, W2c, b2c), grad_out, ctx.G, ctx.eps)
+        grads = (dlw, dlb, dW1, db1, dW2, db2, dxq, dxv, dxk, deta)
+        grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
+        return grads + (None, None, None)
