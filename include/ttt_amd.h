@@ -122,6 +122,24 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
                 float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Fixed-weight TTT-MLP readout over a segment of NS mini-batches:
+ *   out = XQ + LN_eps(gelu(XQ W1 + b1) W2 + b2)   (no state update)
+ * with the weights of each (b,h) chain.  Replaces mlp_cached_readout_triton
+ * (kernels/mlp_cached_readout.py:112-143) and its kernel (:7-109), as called
+ * per cached memo slice from ttt_layer.py:542-552; the residual the
+ * reference adds on the host (:143) is fused.  The reference uses eps 1e-6.
+ *   XQ               [B,H,NS,K,F] dtype
+ *   W1, b1, W2, b2   fp32; chain c = b*H + h reads W1 + c*S*F*FF,
+ *                    b1 + c*S*FF, W2 + c*S*FF*F, b2 + c*S*F.  S = 1 for
+ *                    [B,H,...] tensors; S = number of stacked states when the
+ *                    pointers address slice j of [B,H,S,...] memo tensors,
+ *                    so a memo slice is read in place.
+ *   out              [B,H,NS,K,F] fp32 */
+int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, const float* W2,
+                           const float* b2, const float* ln_w, const float* ln_b,
+                           int B, int H, int NS, int K, int F, int FF, int S, int dtype, float eps,
+                           float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

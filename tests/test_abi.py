@@ -1,0 +1,158 @@
+"""The C ABI without a GPU: libttt_amd.so loads, exports every function that
+include/ttt_amd.h declares (with the argument count the ctypes table uses),
+and host-side validation returns the documented status codes.  Every call
+below is rejected before any launch, so no device is touched."""
+
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ttt_amd.h")
+
+OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG = 0, -1, -2, -3, -4, -5, -6, -7
+F32, BF16 = 0, 1
+P = 0x10000  # an aligned, never-dereferenced address
+Q = 0x10008  # misaligned
+
+
+def _declarations():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(ttt_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.M | re.S):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip()]
+        if args == ["void"]:
+            args = []
+        decls[m.group(1)] = len(args)
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from ttt_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_the_abi():
+    decls = _declarations()
+    for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
+                 "ttt_linear_bwd_workspace_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_bwd_workspace_bytes",
+                 "ttt_mlp_cached_readout"):
+        assert name in decls, name
+
+
+def test_every_declared_symbol_is_exported(lib):
+    from ttt_amd import _lib
+    decls = _declarations()
+    assert set(decls) == set(_lib.SIGNATURES), set(decls) ^ set(_lib.SIGNATURES)
+    for name, nargs in decls.items():
+        assert hasattr(lib, name), name
+        assert len(_lib.SIGNATURES[name][1]) == nargs, (name, nargs, len(_lib.SIGNATURES[name][1]))
+
+
+def test_version_and_error_strings(lib):
+    from ttt_amd import _lib
+    assert lib.ttt_abi_version() == _lib.ABI_VERSION
+    for code in (OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG):
+        assert lib.ttt_error_string(code)
+    assert lib.ttt_error_string(-99) == b"unknown status"
+
+
+def _lin_fwd(lib, **kw):
+    a = dict(XQ=P, XK=P, XV=P, eta=P, lw=P, lb=P, W=P, b=P, B=2, H=4, NC=16, K=16, F=64, G=4, dtype=F32,
+             eps=1e-8, out=P, Wl=None, bl=None, Wc=None, bc=None, stream=None)
+    a.update(kw)
+    return lib.ttt_linear_fwd(*a.values())
+
+
+def test_linear_fwd_validation(lib):
+    assert _lin_fwd(lib, K=8) == E_SHAPE
+    assert _lin_fwd(lib, F=48) == E_SHAPE
+    assert _lin_fwd(lib, B=0) == E_SHAPE
+    assert _lin_fwd(lib, dtype=7) == E_DTYPE
+    assert _lin_fwd(lib, XQ=None) == E_NULL
+    assert _lin_fwd(lib, out=None) == E_NULL
+    assert _lin_fwd(lib, XK=Q) == E_ALIGN
+    assert _lin_fwd(lib, G=0) == E_ARG
+    assert _lin_fwd(lib, G=17) == E_ARG
+    assert _lin_fwd(lib, eps=0.0) == E_ARG
+    assert _lin_fwd(lib, Wl=P, XQ=None) == E_NULL
+    assert _lin_fwd(lib, Wl=P, bl=None, Wc=Q, bc=P, XQ=P, K=16) in (E_NULL, E_ALIGN)
+
+
+def test_linear_bwd_workspace(lib):
+    B, H, NC, K, F, G = 2, 4, 16, 16, 64, 4
+    need = lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, G)
+    assert need == B * H * G * K * F * 4
+    assert lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, 99) == B * H * NC * K * F * 4
+    assert lib.ttt_linear_bwd_workspace_bytes(0, H, NC, K, F, G) == 0
+    args = [P] * 9 + [B, H, NC, K, F, G, F32, 1e-8] + [P] * 8
+    assert lib.ttt_linear_bwd(*args, P, need - 4, None) == E_WS
+    assert lib.ttt_linear_bwd(*args, None, need, None) == E_WS
+    assert lib.ttt_linear_bwd(*args, Q, need, None) == E_ALIGN
+    bad = list(args)
+    bad[8] = None  # dout
+    assert lib.ttt_linear_bwd(*bad, P, need, None) == E_NULL
+
+
+def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, **kw):
+    a = [P] * 10 + [2, 4, 16, 16, 64, FF, 4, M, kw.get("dtype", BF16), 1e-8, P] + [None] * 8 + list(memo) + [None]
+    return lib.ttt_mlp_fwd(*a)
+
+
+def test_mlp_fwd_validation(lib):
+    assert _mlp_fwd(lib, FF=96) == E_SHAPE
+    assert _mlp_fwd(lib, FF=512) == E_SHAPE
+    assert _mlp_fwd(lib, dtype=3) == E_DTYPE
+    assert _mlp_fwd(lib, memo=(P, P, P, None), M=2) == E_NULL
+    assert _mlp_fwd(lib, memo=(P, P, P, P), M=0) == E_ARG
+    assert _mlp_fwd(lib, memo=(P, P, P, P), M=17) == E_ARG
+    assert _mlp_fwd(lib, memo=(P, P, Q, P), M=2) == E_ALIGN
+
+
+def test_mlp_bwd_workspace(lib):
+    B, H, NC, K, F, FF, G = 2, 4, 16, 16, 64, 256, 8
+    n16 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, BF16)
+    n32 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, F32)
+    # per step: W1^T, W2^T, W1, W2 operand copies in the activation type + fp32 biases
+    assert n16 == B * H * G * (4 * F * FF * 2 + (FF + F) * 4)
+    assert n32 == B * H * G * (4 * F * FF * 4 + (FF + F) * 4)
+    assert lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, 9) == 0
+    args = [P] * 11 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
+    assert lib.ttt_mlp_bwd(*args, P, n16 - 1, None) == E_WS
+
+
+def _readout(lib, **kw):
+    a = dict(XQ=P, W1=P, b1=P, W2=P, b2=P, lw=P, lb=P, B=2, H=4, NS=3, K=16, F=64, FF=256, S=1, dtype=BF16,
+             eps=1e-6, out=P, stream=None)
+    a.update(kw)
+    return lib.ttt_mlp_cached_readout(*a.values())
+
+
+def test_readout_validation(lib):
+    assert _readout(lib, K=32) == E_SHAPE
+    assert _readout(lib, FF=32) == E_SHAPE
+    assert _readout(lib, NS=0) == E_SHAPE
+    assert _readout(lib, S=0) == E_ARG
+    assert _readout(lib, eps=-1.0) == E_ARG
+    assert _readout(lib, dtype=2) == E_DTYPE
+    assert _readout(lib, W2=None) == E_NULL
+    assert _readout(lib, out=Q) == E_ALIGN
+
+
+def test_product_fails_loudly_without_a_gpu():
+    """On a host without a GPU the launchers refuse instead of computing on the CPU."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from oracle import ttt_oracle as O
+    from ttt_amd.linear import linear_forward
+    from ttt_amd.mlp import mlp_cached_readout
+    d = O.make_inputs(1, 1, 2, 16, 64, seed=0)
+    with pytest.raises(ValueError, match="GPU"):
+        linear_forward(d["ln_w"], d["ln_b"], d["W1"], d["b1"], d["XQ"], d["XV"], d["XK"], d["eta"], 1)
+    with pytest.raises(ValueError, match="GPU"):
+        W = torch.zeros(1, 1, 64, 64)
+        mlp_cached_readout(d["XQ"], W, torch.zeros(1, 1, 1, 64), W, torch.zeros(1, 1, 1, 64), d["ln_w"], d["ln_b"])

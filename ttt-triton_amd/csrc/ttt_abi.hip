@@ -286,4 +286,37 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   return hip_status(ttt::launch_mlp_bwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, const float* W2, const float* b2,
+                           const float* ln_w, const float* ln_b, int B, int H, int NS, int K, int F, int FF, int S,
+                           int dtype, float eps, float* out, void* stream) {
+  int st = check_common(B, H, NS, K, F, 1, dtype, eps);
+  if (st != TTT_OK) return st;
+  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  if (S < 1) return TTT_ERR_ARG;
+  if ((long long)NS * K > 0x7fffffffLL / 64) return TTT_ERR_SHAPE;
+  const void* req[] = {XQ, W1, b1, W2, b2, ln_w, ln_b, out};
+  for (const void* q : req) REQUIRE_PTR(q);
+
+  ttt::MlpReadoutParams p;
+  p.XQ = XQ;
+  p.W1 = W1;
+  p.b1 = b1;
+  p.W2 = W2;
+  p.b2 = b2;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.out = out;
+  p.B = B;
+  p.H = H;
+  p.ntok = NS * K;
+  p.F = F;
+  p.FF = FF;
+  p.S = S;
+  const int chunk = ttt::mlp_readout_chunk_tokens();
+  p.nchunk = (p.ntok + chunk - 1) / chunk;
+  if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  p.eps = eps;
+  return hip_status(ttt::launch_mlp_readout(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

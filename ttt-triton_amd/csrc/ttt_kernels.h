@@ -48,6 +48,17 @@ struct MlpBwdParams {
   float eps;
 };
 
+struct MlpReadoutParams {
+  const void* XQ;
+  const float *W1, *b1, *W2, *b2, *ln_w, *ln_b;
+  float* out;
+  int B, H, ntok, F, FF, S, nchunk;
+  float eps;
+};
+
+hipError_t launch_mlp_readout(const MlpReadoutParams& p, int dtype, hipStream_t stream);
+int mlp_readout_chunk_tokens();
+
 hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
 size_t mlp_bwd_slot_bytes(int F, int FF, int dtype);
 

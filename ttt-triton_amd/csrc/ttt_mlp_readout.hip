@@ -1,0 +1,212 @@
+// Fixed-weight TTT-MLP readout on gfx950:
+//   out = XQ + LN_eps(gelu(XQ W1 + b1) W2 + b2)      (no state update)
+// for every token of a segment, with one (W1, b1, W2, b2) per (batch, head)
+// chain (kernels/mlp_cached_readout.py:88-109,143, indexed per chain).
+//
+// The weights are fixed, so tokens are independent: a workgroup of four waves
+// takes one chain and a chunk of up to 256 tokens.  It stages the chain's W1
+// and W2 once into LDS, already in MFMA operand order (one 4-element vector
+// per lane per 16x16 block, so every operand read is one conflict-free
+// ds_read), then each wave runs up to four 16-token tiles through
+//
+//   Z1^T = W1^T XQ^T           (hidden x token: its C layout is the A operand
+//   X2^T = gelu(Z1^T + b1)      of the next product with no transpose)
+//   Z2   = X2 W2 + b2           accumulated over hidden tiles two at a time
+//   out  = XQ + ln_w * (Z2 - mean) / sqrt(var + eps) + ln_b
+//
+// W is read from HBM once per workgroup; blocks are mapped so that the chunks
+// of one chain run on one XCD and share its L2.
+#include "ttt_kernels.h"
+
+namespace ttt {
+
+template <typename T, int FT, int HTT> struct ReadoutShared {
+  typename FragT<T>::type w1[FT * HTT][64];  // block (kb, ht): W1[16kb + 4g + j][16ht + n]
+  typename FragT<T>::type w2[HTT * FT][64];  // block (ht, ct): W2[16ht + 4g + j][16ct + n]
+  float b1[16 * HTT];
+  float b2[16 * FT];
+  float lnw[16 * FT];
+  float lnb[16 * FT];
+};
+
+constexpr int kReadoutWaves = 4;
+constexpr int kReadoutTilesPerWave = 4;
+constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave;  // tokens per workgroup
+
+template <typename T, int FT, int HTT>
+__global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpReadoutParams p) {
+  constexpr int F = 16 * FT;
+  constexpr int FF = 16 * HTT;
+  constexpr int NT = kReadoutTilesPerWave;
+  __shared__ ReadoutShared<T, FT, HTT> sh;
+
+  // blockIdx -> (chain, chunk): consecutive block ids go to different XCDs, so
+  // renumber such that the chunks of a chain sit on the same XCD.
+  const int total = gridDim.x;
+  int lin = blockIdx.x;
+  if ((total & 7) == 0) lin = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+  const int chain = lin / p.nchunk;
+  const int chunk = lin - chain * p.nchunk;
+  const int h = chain % p.H;
+
+  const int wave = threadIdx.x >> 6;
+  const int l = lane_id(), g = l >> 4, n = l & 15;
+
+  // ---- stage W1, W2, biases and LN parameters of this chain
+  {
+    const size_t S = (size_t)p.S;
+    const float* __restrict__ w1 = p.W1 + (size_t)chain * S * F * FF;
+    const float* __restrict__ w2 = p.W2 + (size_t)chain * S * FF * F;
+    for (int blk = wave; blk < FT * HTT; blk += kReadoutWaves) {
+      const int kb = blk / HTT, ht = blk - kb * HTT;
+      f4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
+      sh.w1[blk][l] = to_frag<T>(x).v;
+    }
+    for (int blk = wave; blk < HTT * FT; blk += kReadoutWaves) {
+      const int ht = blk / FT, ct = blk - ht * FT;
+      f4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
+      sh.w2[blk][l] = to_frag<T>(x).v;
+    }
+    const float* __restrict__ b1 = p.b1 + (size_t)chain * S * FF;
+    const float* __restrict__ b2 = p.b2 + (size_t)chain * S * F;
+    for (int i = threadIdx.x; i < FF; i += 64 * kReadoutWaves) sh.b1[i] = b1[i];
+    for (int i = threadIdx.x; i < F; i += 64 * kReadoutWaves) {
+      sh.b2[i] = b2[i];
+      sh.lnw[i] = p.ln_w[h * F + i];
+      sh.lnb[i] = p.ln_b[h * F + i];
+    }
+  }
+  __syncthreads();
+
+  const int ntiles = p.ntok >> 4;
+  const int t0 = chunk * (kReadoutChunk / 16) + wave * NT;  // first token tile of this wave
+  const int nv = min(NT, ntiles - t0);                      // valid tiles (may be <= 0)
+  if (nv <= 0) return;                                      // no barrier follows
+
+  const size_t xoff = (size_t)chain * p.ntok * F;
+  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
+  float* __restrict__ OUT = p.out + xoff;
+
+  // XQ^T operand frags (free = token, contraction = feature); tiles past the
+  // valid range repeat the last valid one and are not stored.
+  Frag<T> xq[NT][FT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const T* x = XQ + (size_t)(t0 + min(t, nv - 1)) * 16 * F;
+#pragma unroll
+    for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(x, F, 16 * kb);
+  }
+
+  Tile acc[NT][FT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+  for (int ht = 0; ht < HTT; ht += 2) {
+    Frag<T> x2[2][NT];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      Frag<T> w1f[FT];
+#pragma unroll
+      for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
+      const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        Tile z;
+        z.v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
+        f4 a;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
+        x2[hh][t] = to_frag<T>(a);
+      }
+    }
+    Frag<T> q0[FT], q1[FT];
+#pragma unroll
+    for (int c = 0; c < FT; ++c) {
+      q0[c].v = sh.w2[ht * FT + c][l];
+      q1[c].v = sh.w2[(ht + 1) * FT + c][l];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
+  }
+
+  // ---- b2, LayerNorm over the F features of each token row, residual, store
+  float b2v[FT], lwv[FT], lbv[FT];
+#pragma unroll
+  for (int c = 0; c < FT; ++c) {
+    b2v[c] = sh.b2[16 * c + n];
+    lwv[c] = sh.lnw[16 * c + n];
+    lbv[c] = sh.lnb[16 * c + n];
+  }
+  const float invF = 1.0f / (float)F;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t >= nv) break;
+    const size_t row0 = (size_t)(t0 + t) * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v[FT], s = 0.f;
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        v[c] = acc[t][c].v[j] + b2v[c];
+        s += v[c];
+      }
+      const float mean = sum_row16(s) * invF;
+      float q = 0.f;
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        v[c] -= mean;
+        q += v[c] * v[c];
+      }
+      const float rstd = 1.0f / sqrtf(sum_row16(q) * invF + p.eps);
+      const size_t r = (row0 + 4 * g + j) * F;
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        const float x = (float)XQ[r + 16 * c + n];
+        OUT[r + 16 * c + n] = x + lwv[c] * (v[c] * rstd) + lbv[c];
+      }
+    }
+  }
+}
+
+template <typename T, int FT, int HTT>
+static hipError_t launch_readout_t(const MlpReadoutParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((mlp_readout_kernel<T, FT, HTT>), dim3(p.B * p.H * p.nchunk), dim3(64 * kReadoutWaves), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+template <typename T, int FT>
+static hipError_t launch_readout_f(const MlpReadoutParams& p, hipStream_t stream) {
+  switch (p.FF) {
+    case 64: return launch_readout_t<T, FT, 4>(p, stream);
+    case 128: return launch_readout_t<T, FT, 8>(p, stream);
+    case 256: return launch_readout_t<T, FT, 16>(p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int mlp_readout_chunk_tokens() { return kReadoutChunk; }
+
+hipError_t launch_mlp_readout(const MlpReadoutParams& p, int dtype, hipStream_t stream) {
+  if (dtype == TTT_DTYPE_BF16) {
+    if (p.F == 64) return launch_readout_f<__bf16, 4>(p, stream);
+    if (p.F == 32) return launch_readout_f<__bf16, 2>(p, stream);
+  } else {
+    if (p.F == 64) return launch_readout_f<float, 4>(p, stream);
+    if (p.F == 32) return launch_readout_f<float, 2>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ttt

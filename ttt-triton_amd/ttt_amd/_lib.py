@@ -33,6 +33,7 @@ SIGNATURES = {
     "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 14),
     "ttt_mlp_bwd_workspace_bytes": (_S, [_I] * 8),
     "ttt_mlp_bwd": (_I, [_P] * 11 + [_I] * 8 + [_F] + [_P] * 11 + [_S, _P]),
+    "ttt_mlp_cached_readout": (_I, [_P] * 7 + [_I] * 8 + [_F] + [_P, _P]),
 }
 
 _lock = threading.Lock()

@@ -147,3 +147,57 @@ class TTTMLPFunction(torch.autograd.Function):
         grads = (dlw, dlb, dW1, db1, dW2, db2, dxq, dxv, dxk, deta)
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
         return grads + (None, None, None)
+
+
+READOUT_EPS = 1e-6  # kernels/mlp_cached_readout.py:98
+
+
+def _states_per_chain(t: torch.Tensor, B: int, H: int, inner: int):
+    """S such that `t` ([B,H,*,*]) is slice j of a contiguous [B,H,S,*,*] tensor,
+    i.e. its chain stride is S*inner with contiguous inner dims; None otherwise."""
+    st = t.stride()
+    if st[3] != 1 or st[2] != t.shape[3] or st[1] % inner != 0:
+        return None
+    S = st[1] // inner
+    if S < 1 or (B > 1 and st[0] != H * st[1]):
+        return None
+    return S
+
+
+def mlp_cached_readout(XQ_seg, W1, b1, W2, b2, ln_w, ln_b, eps: float = READOUT_EPS):
+    """XQ_seg + LN_eps(gelu(XQ_seg W1 + b1) W2 + b2) per (b,h) chain, fp32.
+
+    XQ_seg [B,H,NS,K,F] (fp32 or bf16); W1 [B,H,F,FF], b1 [B,H,1,FF],
+    W2 [B,H,FF,F], b2 [B,H,1,F] fp32, either contiguous or the same slice j of
+    [B,H,S,...] memo tensors (read in place); ln_w, ln_b [H,F]."""
+    if XQ_seg.dim() != 5:
+        raise ValueError(f"XQ_seg must be [B,H,NS,K,F], got {tuple(XQ_seg.shape)}")
+    B, H, NS, K, F = XQ_seg.shape
+    FF = W1.shape[-1]
+    want = {"W1": (W1, (B, H, F, FF)), "b1": (b1, (B, H, 1, FF)), "W2": (W2, (B, H, FF, F)),
+            "b2": (b2, (B, H, 1, F))}
+    for name, (t, shp) in want.items():
+        if tuple(t.shape) != shp:
+            raise ValueError(f"{name} must be {shp}, got {tuple(t.shape)}")
+    if tuple(ln_w.shape) != (H, F) or tuple(ln_b.shape) != (H, F):
+        raise ValueError(f"LN weight/bias must be [H,F]={(H, F)}")
+    dev = check_device(XQ_seg, W1, b1, W2, b2, ln_w, ln_b)
+    mp = XQ_seg.dtype
+    code = dtype_code(mp)
+    xq = as_act(XQ_seg, mp)
+    ws = [W1, b1, W2, b2]
+    S = None
+    if all(t.dtype == torch.float32 for t in ws):
+        Ss = {_states_per_chain(t, B, H, t.shape[2] * t.shape[3]) for t in ws}
+        if len(Ss) == 1:
+            S = Ss.pop()
+    if S is None:
+        ws, S = [_f32(t) for t in ws], 1
+    lw, lb = _f32(ln_w), _f32(ln_b)
+    out = torch.empty((B, H, NS, K, F), device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        st = lib.ttt_mlp_cached_readout(ptr(xq), *(ptr(t) for t in ws), ptr(lw), ptr(lb),
+                                        B, H, NS, K, F, FF, int(S), code, float(eps), ptr(out), stream_of(dev))
+    _lib.check(st, "ttt_mlp_cached_readout")
+    return out
