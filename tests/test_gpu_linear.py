@@ -135,3 +135,19 @@ def test_linear_bwd_bf16():
         if err > BF16_RTOL:
             bad.append(k)
     assert not bad
+
+
+@pytest.mark.parametrize("NC,G,F_", [(1, 1, 64), (7, 3, 64), (5, 5, 32), (9, 4, 32)])
+def test_linear_bwd_edges_fp32(NC, G, F_):
+    """single mini-batch, a group size that does not divide NC, F = 32"""
+    _say(f"linear bwd fp32 NC{NC} G{G} F{F_}")
+    d = O.make_inputs(1, 2, NC, 16, F_, seed=20 + NC, dtype=torch.float32, with_grad=True)
+    mine = _bwd(d, d["dOut"], G=G)
+    ref = oracle_linear_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        err = max_abs(mine[k], ref[k])
+        _say(f"  {k}: max-abs {err:.3e} bound {fp32_bound(ref[k]):.3e}")
+        if err > fp32_bound(ref[k]):
+            bad.append(k)
+    assert not bad

@@ -120,3 +120,28 @@ def test_mlp_bwd_bf16_ff256():
         if err > BF16_RTOL:
             bad.append(k)
     assert not bad
+
+
+@pytest.mark.parametrize("NC,G,F_,FF,dt", [
+    (1, 1, 64, 256, torch.float32),
+    (7, 3, 64, 128, torch.float32),
+    (6, 4, 32, 64, torch.float32),
+    (1, 1, 64, 256, torch.bfloat16),
+    (9, 4, 32, 128, torch.bfloat16),
+])
+def test_mlp_bwd_edges(NC, G, F_, FF, dt):
+    """single mini-batch, group sizes that do not divide NC, F = 32, FF = 64/128"""
+    _say(f"mlp bwd NC{NC} G{G} F{F_} FF{FF} {dt}")
+    d = _perturb(O.make_inputs(1, 2, NC, 16, F_, FF=FF, seed=30 + NC, dtype=dt, with_grad=True), 2, F_, FF, 31)
+    mine = _bwd(d, G=G)
+    ref = oracle_mlp_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        if dt == torch.float32:
+            err, bound = max_abs(mine[k], ref[k]), fp32_bound(ref[k])
+        else:
+            err, bound = rel_l2(mine[k], ref[k]), BF16_RTOL
+        _say(f"  {k}: err {err:.3e} bound {bound:.3e}")
+        if err > bound:
+            bad.append(k)
+    assert not bad
