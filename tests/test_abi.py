@@ -116,9 +116,11 @@ def test_mlp_bwd_workspace(lib):
     B, H, NC, K, F, FF, G = 2, 4, 16, 16, 64, 256, 8
     n16 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, BF16)
     n32 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, F32)
-    # per step: W1^T, W2^T, W1, W2 operand copies in the activation type + fp32 biases
-    assert n16 == B * H * G * (4 * F * FF * 2 + (FF + F) * 4)
-    assert n32 == B * H * G * (4 * F * FF * 4 + (FF + F) * 4)
+    # per step: the update operands -e*G1 [K x FF] and one copy of -e*G2 [K x F]
+    # per wave (FF/64 waves) in the activation type, and their fp32 bias decrements
+    nw = FF // 64
+    assert n16 == B * H * G * ((FF + nw * F) * K * 2 + (FF + nw * F) * 4)
+    assert n32 == B * H * G * ((FF + nw * F) * K * 4 + (FF + nw * F) * 4)
     assert lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, 9) == 0
     args = [P] * 11 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
     assert lib.ttt_mlp_bwd(*args, P, n16 - 1, None) == E_WS

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
         const float d = z1[0][o].v[j] - mu[j];
         sacc += d * d;
       }
-      rstd[j] = 1.0f / sqrtf(sum_row16(sacc) * invF + eps);
+      rstd[j] = rsqrt_f(sum_row16(sacc) * invF + eps);
     }
     f4 xh[FT], gx[FT];
     f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
           const float d = zb[o][0].v[j] - m;
           vacc += d * d;
         }
-      const float rs = 1.0f / sqrtf(sum_col4(vacc) * invF + eps);
+      const float rs = rsqrt_f(sum_col4(vacc) * invF + eps);
       T* o_s = OUT + (size_t)s * K * F;
 #pragma unroll
       for (int o = 0; o < FT; ++o) {

@@ -42,7 +42,7 @@ template <int FT> struct LnL2TM {
         const float d = z[o].v[j] - mu[j];
         s += d * d;
       }
-      rstd[j] = 1.0f / sqrtf(sum_row16(s) * invF + eps);
+      rstd[j] = rsqrt_f(sum_row16(s) * invF + eps);
     }
     f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -121,6 +121,112 @@ template <int FT> struct LnL2TM {
   }
 };
 
+// The same function as LnL2TM keeping only rstd, c and xh between forward and
+// backward (16 + 8 registers per lane at F = 64 instead of 56); the backward
+// recomputes gamma*xh + beta - tgt from xh and the target.
+template <int FT> struct LnL2Lite {
+  f4 rstd;    // 1/sqrt(var + eps) per row j
+  f4 c;       // mean(gx * xh) per row j
+  f4 xh[FT];  // normalised z
+
+  __device__ __forceinline__ void forward(const Tile (&z)[FT], const f4 (&tgt)[FT], const float (&lnw)[FT],
+                                          const float (&lnb)[FT], float eps, Tile (&G)[FT]) {
+    constexpr float invF = 1.0f / (16 * FT);
+    f4 mu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int o = 0; o < FT; ++o) s += z[o].v[j];
+      mu[j] = sum_row16(s) * invF;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        const float d = z[o].v[j] - mu[j];
+        s += d * d;
+      }
+      rstd[j] = rsqrt_f(sum_row16(s) * invF + eps);
+    }
+    f4 gx[FT];
+    f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int o = 0; o < FT; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xh[o][j] = (z[o].v[j] - mu[j]) * rstd[j];
+        gx[o][j] = (lnw[o] * xh[o][j] + lnb[o] - tgt[o][j]) * lnw[o];
+        s1[j] += gx[o][j];
+        s2[j] += gx[o][j] * xh[o][j];
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s1[j] = sum_row16(s1[j]) * invF;
+      c[j] = sum_row16(s2[j]) * invF;
+    }
+#pragma unroll
+    for (int o = 0; o < FT; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) G[o].v[j] = (gx[o][j] - s1[j] - xh[o][j] * c[j]) * rstd[j];
+  }
+
+  __device__ __forceinline__ void backward(const Tile (&dG)[FT], const Tile (&G)[FT], const f4 (&tgt)[FT],
+                                           const float (&lnw)[FT], const float (&lnb)[FT], f4 (&dz)[FT],
+                                           f4 (&dtgt)[FT], float (&dlnw)[FT], float (&dlnb)[FT]) const {
+    constexpr float invF = 1.0f / (16 * FT);
+    f4 u[FT];
+    f4 mu_u = f4{0.f, 0.f, 0.f, 0.f}, mu_ux = f4{0.f, 0.f, 0.f, 0.f}, dsig = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int o = 0; o < FT; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u[o][j] = dG[o].v[j] * rstd[j];
+        mu_u[j] += u[o][j];
+        mu_ux[j] += u[o][j] * xh[o][j];
+        dsig[j] += u[o][j] * G[o].v[j];
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mu_u[j] = sum_row16(mu_u[j]) * invF;
+      mu_ux[j] = sum_row16(mu_ux[j]) * invF;
+      dsig[j] = -sum_row16(dsig[j]);
+    }
+    f4 dxh[FT];
+    f4 m1 = f4{0.f, 0.f, 0.f, 0.f}, m2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      float aw = 0.f, ab = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float go = lnw[o] * xh[o][j] + lnb[o] - tgt[o][j];
+        const float gx = go * lnw[o];
+        const float d_gx = u[o][j] - mu_u[j] - xh[o][j] * mu_ux[j];
+        const float d_go = d_gx * lnw[o];
+        aw += d_gx * go + d_go * xh[o][j];
+        ab += d_go;
+        dtgt[o][j] = -d_go;
+        dxh[o][j] = -c[j] * u[o][j] - mu_ux[j] * gx + d_go * lnw[o];
+        m1[j] += dxh[o][j];
+        m2[j] += dxh[o][j] * xh[o][j];
+      }
+      dlnw[o] += aw;
+      dlnb[o] += ab;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m1[j] = sum_row16(m1[j]) * invF;
+      m2[j] = sum_row16(m2[j]) * invF;
+    }
+#pragma unroll
+    for (int o = 0; o < FT; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dz[o][j] = rstd[j] * (dxh[o][j] - m1[j] - xh[o][j] * m2[j]) + dsig[j] * xh[o][j] * invF;
+  }
+};
+
 // LayerNorm statistics of FM tiles (one token per lane column).
 template <int FT> __device__ __forceinline__ void ln_stats_fm(const Tile (&z)[FT][1], float eps, float& mean,
                                                               float& rstd) {
@@ -139,7 +245,7 @@ template <int FT> __device__ __forceinline__ void ln_stats_fm(const Tile (&z)[FT
       const float d = z[o][0].v[j] - mean;
       v += d * d;
     }
-  rstd = 1.0f / sqrtf(sum_col4(v) * invF + eps);
+  rstd = rsqrt_f(sum_col4(v) * invF + eps);
 }
 
 }  // namespace ttt

@@ -1,51 +1,65 @@
 // TTT-MLP backward on gfx950: one workgroup of NW = FF/64 wavefronts per
 // (batch, head) chain; wave w owns hidden units S = [64w, 64w+64).
 //
+// Where the state lives.  The fast weights are kept in LDS in fp32, W1 as
+// [F][FF] and W2 transposed, W2^T [F][FF] (columns XOR-swizzled so both access
+// shapes are bank-conflict free), so every operand orientation the backward
+// needs is a direct read: a C-layout tile (4 x ds_read_b32) or a row vector
+// (ds_read_b128), no transposes.  Each
+// wave only ever touches its own hidden columns S of both, so no barrier
+// guards the state.  Registers hold the gradient accumulators dW1[:, S],
+// dW2[S, :], db1[S], db2 -- the gradient wrt the state after the mini-batch
+// being processed -- and the biases b1[S], b2.
+//
 // Reverse sweep over checkpoint groups (kernels/mlp_backward.py:340 walks the
 // same groups; the algorithm and data flow here are our own):
 //   pass 1  reload the state entering the group from its checkpoint and run
-//           the group's mini-batches forward (state path only).  Before each
-//           mini-batch the state's MFMA operand values (W1 and W2 in both
-//           orientations, in the activation dtype, plus b1, b2 in fp32) are
-//           written to the per-chain workspace, so pass 2 can load any operand
-//           frag with contiguous 4-element reads.  While pass 1 holds the
-//           state in registers, the gradient accumulators dW1, dW2 are parked
-//           in LDS.
-//   pass 2  walk the group backwards: recompute the mini-batch forward from
-//           the stored operands and apply its gradient (ops/ttt_mlp.py:9-67
-//           differentiated by hand), with dW1 = dL/dW1', dW2, db1, db2 (the
-//           gradient wrt the state after the mini-batch) in registers.
+//           the group's mini-batches forward (state path only,
+//           ops/ttt_mlp.py:28-52).  For each mini-batch the update operands
+//           -e*G1 and -e*G2 (exactly the values the update MFMAs consume) and
+//           the fp32 bias decrements are written to the per-chain workspace.
+//   pass 2  walk the group backwards.  Mini-batch s first rebuilds the state
+//           entering it from the state after it, W1_s = W1_{s+1} + XK_s^T (e G1_s)
+//           and W2_s = W2_{s+1} + X2_s^T (e G2_s), with the same operands, then
+//           recomputes the mini-batch forward and applies its gradient
+//           (ops/ttt_mlp.py:9-67 differentiated by hand).
 // Row-wise work on [16 x F] tiles (LayerNorms and their backward) is done
-// redundantly by every wave; contractions over the hidden units are split by
-// slice and reduced through LDS (five barriers per mini-batch).
+// redundantly by every wave.  Contractions over the hidden units are split by
+// slice; their [16 x F] partials meet in one 32 KB LDS exchange area, so each
+// reduction is fenced by a barrier after the writes (the partials are in) and
+// one after the reads (the area is free): eight barriers per mini-batch.  The
+// gradient accumulators are pinned to the MFMA accumulator registers.
+#include "ttt_buf.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
 namespace ttt {
 
-template <typename T, int FT, int NW> struct MlpBwdShared {
-  static constexpr int HT = 4;
-  f4 partZ[NW][FT][64];                       // Z2 partials (both passes)
-  union {
-    f4 park[NW][2 * FT * HT][64];             // pass 1: parked dW1, dW2 tiles
-    struct {
-      f4 partA[NW][FT][64];                   // dXQ partials
-      f4 partB[NW][FT][64];                   // Z2b partials, then dG2 partials
-      f4 partC[NW][FT][64];                   // Q2 partials, then dXK partials
-      f4 partD[NW][FT][64];                   // -(e G1) dW1'^T partials
-      f4 a2T[NW][64], a2[NW][64];             // (X2b X2^T) partials, both layouts
-      f4 dn1[NW][64], dn1T[NW][64];           // dN1 partials, both layouts
-      f4 de[NW][64];                          // eta-row gradient partials
-    } s;
-  } u;
+template <int FT, int NW> union MlpBwdExchange {
+  struct {
+    f4 part[NW][FT][64];  // [16 x F] partials, one per wave
+    f4 sm[3][NW][64];     // [16 x 16] partials
+  } a;
+  struct {
+    f4 dxq[NW][FT][64];  // dXQ partials
+    f4 dxk[NW][FT][64];  // dXK partials
+  } b;
 };
 
-template <typename T> __device__ __forceinline__ void store4(T* __restrict__ p, f4 v);
-template <> __device__ __forceinline__ void store4<__bf16>(__bf16* __restrict__ p, f4 v) {
-  *reinterpret_cast<bf4*>(p) = to_frag<__bf16>(v).v;
-}
-template <> __device__ __forceinline__ void store4<float>(float* __restrict__ p, f4 v) {
-  *reinterpret_cast<f4*>(p) = v;
+template <int FT, int NW> struct MlpBwdShared {
+  float w1[16 * FT * 64 * NW];   // W1   [F][FF], swizzled
+  float w2t[16 * FT * 64 * NW];  // W2^T [F][FF], swizzled
+  MlpBwdExchange<FT, NW> x;
+};
+
+// Per-chain workspace slot for one mini-batch (element type T for operands):
+//   g1e [NW][4][64] x 4 T     -e * G1 as the update MFMA's operand frags
+//   g2e [NW][FT][64] x 4 T    -e * G2 (one copy per wave)
+//   b1d [FF] fp32, b2d [NW][F] fp32   bias decrements
+size_t mlp_bwd_slot_bytes(int F, int FF, int dtype) {
+  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
+  const size_t nw = (size_t)FF / 64;
+  return (FF + nw * F) * 16 * t + (FF + nw * F) * sizeof(float);
 }
 
 template <typename T, int FT, int NW>
@@ -55,39 +69,54 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   constexpr int HT = 4;
   constexpr int FF = 64 * NW;
   constexpr float invF = 1.0f / F;
-  __shared__ MlpBwdShared<T, FT, NW> sh;
+  constexpr int ST = (int)sizeof(T);
+  __shared__ MlpBwdShared<FT, NW> sh;
 
   const int chain = blockIdx.x;
   const int h = chain % p.H;
   const int NC = p.NC, G = p.G, NK = p.NK;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int l = lane_id(), g = l >> 4, n = l & 15;
   const int hs = 64 * wave;
 
+  // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
   const size_t eoff = (size_t)chain * NC * K * K;
-  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
-  const T* __restrict__ XK = static_cast<const T*>(p.XK) + xoff;
-  const T* __restrict__ XV = static_cast<const T*>(p.XV) + xoff;
-  const T* __restrict__ DO = static_cast<const T*>(p.dout) + xoff;
-  const T* __restrict__ ETA = static_cast<const T*>(p.eta) + eoff;
-  T* __restrict__ DXQ = static_cast<T*>(p.dXQ) + xoff;
-  T* __restrict__ DXK = static_cast<T*>(p.dXK) + xoff;
-  T* __restrict__ DXV = static_cast<T*>(p.dXV) + xoff;
-  T* __restrict__ DETA = static_cast<T*>(p.deta) + eoff;
-  // workspace slot: W1t [FF][F], W2t [F][FF], W1 [F][FF], W2 [FF][F] (T), b1 [FF], b2 [F] (fp32)
-  const size_t mat = (size_t)F * FF;
-  const size_t slot_bytes = 4 * mat * sizeof(T) + (FF + F) * sizeof(float);
-  char* WSB = reinterpret_cast<char*>(p.ws) + (size_t)chain * G * slot_bytes;
+  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * ST);
+  const rsrc_t rXQ = make_rsrc(static_cast<const T*>(p.XQ) + xoff, xbytes);
+  const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
+  const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
+  const rsrc_t rDO = make_rsrc(static_cast<const T*>(p.dout) + xoff, xbytes);
+  const rsrc_t rET = make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+  const rsrc_t rDXQ = make_rsrc(static_cast<T*>(p.dXQ) + xoff, xbytes);
+  const rsrc_t rDXK = make_rsrc(static_cast<T*>(p.dXK) + xoff, xbytes);
+  const rsrc_t rDXV = make_rsrc(static_cast<T*>(p.dXV) + xoff, xbytes);
+  const rsrc_t rDET = make_rsrc(static_cast<T*>(p.deta) + eoff, ebytes);
+  const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
+  const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
+  const int en = (4 * g * K + n) * ST;        // eta[4g + j][n]: + j * K * ST
+  const int e4 = ((K - 1) * K + 4 * g) * ST;  // eta[K-1][4g .. 4g+3]
+  auto xs = [&](int s) { return s * K * F * ST; };
+  auto es = [&](int s) { return s * K * K * ST; };
 
-  float lnw_tm[FT], lnb_tm[FT];
-#pragma unroll
-  for (int o = 0; o < FT; ++o) {
-    lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
-    lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
-  }
-  const float eps = p.eps;
-  const Frag<T> I = identity_frag<T>();
+  // workspace slot layout (bytes): g1e [NW][HT][64] x 4T | g2e [NW][FT][64] x 4T | b1d [FF] f32 | b2d [NW][F] f32
+  constexpr int SLOT = (FF + NW * F) * 16 * ST + (FF + NW * F) * 4;
+  constexpr int G2E_OFF = FF * 16 * ST;
+  constexpr int B1D_OFF = (FF + NW * F) * 16 * ST;
+  constexpr int B2D_OFF = B1D_OFF + FF * 4;
+  const rsrc_t rWS = make_rsrc(reinterpret_cast<char*>(p.ws) + (size_t)chain * G * SLOT, (unsigned)(G * SLOT));
+  const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST
+  const int g2l = ((wave * FT) * 64 + l) * 4 * ST;  // + c * 256 * ST (+ G2E_OFF)
+  const int b1l = (hs + n) * 4;                     // + 64 * o (+ B1D_OFF)
+  const int b2l = (wave * F + n) * 4;               // + 64 * c (+ B2D_OFF)
+
+  // checkpoints [NK][...] of this chain; lane offsets include the wave's slice
+  const rsrc_t rW1c = make_rsrc(p.W1_ckpt + (size_t)chain * NK * F * FF, (unsigned)((size_t)NK * F * FF * 4));
+  const rsrc_t rW2c = make_rsrc(p.W2_ckpt + (size_t)chain * NK * FF * F, (unsigned)((size_t)NK * FF * F * 4));
+  const rsrc_t rB1c = make_rsrc(p.b1_ckpt + (size_t)chain * NK * FF, (unsigned)((size_t)NK * FF * 4));
+  const rsrc_t rB2c = make_rsrc(p.b2_ckpt + (size_t)chain * NK * F, (unsigned)((size_t)NK * F * 4));
+  const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
+  const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
 
   // gradient wrt the state after the current mini-batch (this wave's slice)
   Tile dW1[FT][HT], dW2[HT][FT];
@@ -103,741 +132,676 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   for (int o = 0; o < HT; ++o) db1[o] = 0.f;
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
+  // LDS state accessors (this wave's hidden columns only)
+  const LdsMat<FF> W1s{sh.w1}, W2t{sh.w2t};
+  // W1 tile [F block kb x hidden block o]: frag (free = hidden, k = feature)
+  auto w1_tile = [&](int kb, int o) { return W1s.tile(16 * kb, hs + 16 * o); };
+  auto w1_put = [&](int kb, int o, Tile t) { W1s.put_tile(16 * kb, hs + 16 * o, t); };
+  // W1^T frag (free = feature block f, k = hidden block c)
+  auto w1T_frag = [&](int f, int c) { return to_frag<T>(W1s.row4(16 * f, hs + 16 * c)); };
+  // W2 tile [hidden block o x F block c] (C layout): frag (free = feature, k = hidden)
+  auto w2_tile = [&](int o, int c) {
+    Tile t;
+    t.v = W2t.row4(16 * c, hs + 16 * o);
+    return t;
+  };
+  auto w2_put = [&](int o, int c, Tile t) { W2t.put_row4(16 * c, hs + 16 * o, t.v); };
+  // W2^T frag (free = hidden block o, k = feature block c)
+  auto w2T_frag = [&](int o, int c) { return to_frag<T>(W2t.tile(16 * c, hs + 16 * o).v); };
+  // keep the gradient accumulators in the MFMA accumulator registers
+  auto pin_dW = [&]() {
+#pragma unroll
+    for (int q_ = 0; q_ < FT; ++q_)
+#pragma unroll
+      for (int o_ = 0; o_ < HT; ++o_) {
+        asm volatile("" : "+a"(dW1[q_][o_].v));
+        asm volatile("" : "+a"(dW2[o_][q_].v));
+      }
+  };
+
+  float lnw_tm[FT], lnb_tm[FT];
+#pragma unroll
+  for (int o = 0; o < FT; ++o) {
+    lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
+    lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
+  }
+  const float eps = p.eps;
+  const Frag<T> I = identity_frag<T>();
+
   float dlnw[FT], dlnb[FT];  // LN-parameter gradient partials (wave 0)
 #pragma unroll
   for (int o = 0; o < FT; ++o) {
     dlnw[o] = 0.f;
     dlnb[o] = 0.f;
   }
+  float b1[HT], b2[FT];
 
   for (int kk = NK - 1; kk >= 0; --kk) {
     const int s0 = kk * G, s1 = min(s0 + G, NC);
 
-    // ===================== pass 1: advance the state, store operands
-    __syncthreads();  // LDS partials of the previous group are consumed
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        sh.u.park[wave][i * HT + o][l] = dW1[i][o].v;
-        sh.u.park[wave][FT * HT + o * FT + i][l] = dW2[o][i].v;
-      }
+    // ===================== pass 1: forward over the group, store update operands
     {
-      Tile W1[FT][HT], W2[HT][FT];
-      float b1[HT], b2[FT];
-      {
-        const size_t k = (size_t)chain * NK + kk;
-        const float* w1 = p.W1_ckpt + k * F * FF;
-        const float* w2 = p.W2_ckpt + k * FF * F;
+      const int ko = kk * F * FF * 4;  // byte offset of checkpoint kk in this chain's slab
 #pragma unroll
-        for (int i = 0; i < FT; ++i)
+      for (int i = 0; i < FT; ++i)
 #pragma unroll
-          for (int o = 0; o < HT; ++o) W1[i][o] = load_tile(w1, FF, 16 * i, hs + 16 * o);
-#pragma unroll
-        for (int i = 0; i < HT; ++i)
-#pragma unroll
-          for (int o = 0; o < FT; ++o) W2[i][o] = load_tile(w2, F, hs + 16 * i, 16 * o);
-#pragma unroll
-        for (int o = 0; o < HT; ++o) b1[o] = p.b1_ckpt[k * FF + hs + 16 * o + n];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) b2[o] = p.b2_ckpt[k * F + 16 * o + n];
-      }
-      for (int s = s0; s < s1; ++s) {
-        char* slot = WSB + (size_t)(s - s0) * slot_bytes;
-        T* W1t_ = reinterpret_cast<T*>(slot);
-        T* W2t_ = W1t_ + mat;
-        T* W1_ = W2t_ + mat;
-        T* W2_ = W1_ + mat;
-        float* b1_ = reinterpret_cast<float*>(W2_ + mat);
-        float* b2_ = b1_ + FF;
-#pragma unroll
-        for (int i = 0; i < FT; ++i)
-#pragma unroll
-          for (int o = 0; o < HT; ++o) {
-            // W1 tile rows f = 16i+4g+j, cols hs+16o+n
-            store4<T>(W1t_ + (size_t)(hs + 16 * o + n) * F + 16 * i + 4 * g, W1[i][o].v);
-            store4<T>(W1_ + (size_t)(16 * i + n) * FF + hs + 16 * o + 4 * g,
-                      transpose16(to_frag<T>(W1[i][o].v), I).v);
-          }
-#pragma unroll
-        for (int i = 0; i < HT; ++i)
-#pragma unroll
-          for (int o = 0; o < FT; ++o) {
-            // W2 tile rows hs+16i+4g+j, cols f = 16o+n
-            store4<T>(W2t_ + (size_t)(16 * o + n) * FF + hs + 16 * i + 4 * g, W2[i][o].v);
-            store4<T>(W2_ + (size_t)(hs + 16 * i + n) * F + 16 * o + 4 * g,
-                      transpose16(to_frag<T>(W2[i][o].v), I).v);
-          }
-        if (g == 0) {
-#pragma unroll
-          for (int o = 0; o < HT; ++o) b1_[hs + 16 * o + n] = b1[o];
-          if (wave == 0) {
-#pragma unroll
-            for (int o = 0; o < FT; ++o) b2_[16 * o + n] = b2[o];
-          }
-        }
-        if (s == s1 - 1) break;  // the state after the group is not needed
-
-        // state path of the forward (mlp_fwd_kernel without the readout)
-        const size_t xo = (size_t)s * K * F;
-        Frag<T> xk[1][FT], xkTf[FT];
-        f4 tgt[FT];
-#pragma unroll
-        for (int q = 0; q < FT; ++q) {
-          xk[0][q] = load_frag(XK + xo, F, 16 * q);
-          const Tile xkT = transpose16(xk[0][q], I);
-          xkTf[q] = to_frag<T>(xkT.v);
-          tgt[q] = transpose16(load_frag(XV + xo, F, 16 * q), I).v - xkT.v;
-        }
-        Frag<T> x2f[HT], x2F[1][HT];
-        f4 gp[HT];
-        {
-          Tile z1[1][HT];
-#pragma unroll
-          for (int o = 0; o < HT; ++o) z1[0][o].v = f4{b1[o], b1[o], b1[o], b1[o]};
-          gemm_pt<1, HT, FT>(z1, xk, W1);
-#pragma unroll
-          for (int o = 0; o < HT; ++o) {
-            f4 x2;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              x2[j] = gelu_tanh(z1[0][o].v[j]);
-              gp[o][j] = gelu_bwd(z1[0][o].v[j]);
-            }
-            x2f[o] = to_frag<T>(x2);
-            x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
-          }
-        }
-        {
-          Tile z2p[1][FT];
-#pragma unroll
-          for (int o = 0; o < FT; ++o) z2p[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-          gemm_pt<1, FT, HT>(z2p, x2F, W2);
-#pragma unroll
-          for (int o = 0; o < FT; ++o) sh.partZ[wave][o][l] = z2p[0][o].v;
-        }
-        __syncthreads();
-        Tile G2[FT];
-        {
-          Tile z2[FT];
-#pragma unroll
-          for (int o = 0; o < FT; ++o) {
-            z2[o].v = f4{b2[o], b2[o], b2[o], b2[o]};
-#pragma unroll
-            for (int w = 0; w < NW; ++w) z2[o].v += sh.partZ[w][o][l];
-          }
-          LnL2TM<FT> ln;
-          ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
-        }
-        __syncthreads();  // partZ is rewritten by the next mini-batch
-        Tile G1[HT];
-        {
-          Frag<T> g2F[1][FT];
-#pragma unroll
-          for (int o = 0; o < FT; ++o) g2F[0][o] = to_frag<T>(transpose16(to_frag<T>(G2[o].v), I).v);
-#pragma unroll
-          for (int i = 0; i < HT; ++i) {
-            G1[i].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int q = 0; q + 1 < FT; q += 2) {
-              const Frag<T> t0 = to_frag<T>(transpose16(to_frag<T>(W2[i][q].v), I).v);
-              const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
-              mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
-            }
-            G1[i].v *= gp[i];
-          }
-        }
-        const f4 e = load4(ETA + (size_t)s * K * K + (K - 1) * K + 4 * g);
-        Frag<T> g1e[HT], g2e[FT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          f4 v;
-          float acc = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[j] = -e[j] * G1[o].v[j];
-            acc += e[j] * G1[o].v[j];
-          }
-          g1e[o] = to_frag<T>(v);
-          b1[o] -= sum_col4(acc);
-        }
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          f4 v;
-          float acc = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[j] = -e[j] * G2[o].v[j];
-            acc += e[j] * G2[o].v[j];
-          }
-          g2e[o] = to_frag<T>(v);
-          b2[o] -= sum_col4(acc);
-        }
-#pragma unroll
-        for (int i = 0; i < FT; ++i)
-#pragma unroll
-          for (int o = 0; o < HT; ++o) mma16(W1[i][o].v, xkTf[i], g1e[o]);
-#pragma unroll
-        for (int i = 0; i < HT; ++i)
-#pragma unroll
-          for (int o = 0; o < FT; ++o) mma16(W2[i][o].v, x2f[i], g2e[o]);
-      }
-    }
-    __syncthreads();  // workspace written; parked dW visible
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        dW1[i][o].v = sh.u.park[wave][i * HT + o][l];
-        dW2[o][i].v = sh.u.park[wave][FT * HT + o * FT + i][l];
-      }
-    __syncthreads();  // park area is reused for pass-2 partials
-
-    // ===================== pass 2: reverse through the group
-    for (int s = s1 - 1; s >= s0; --s) {
-      const char* slot = WSB + (size_t)(s - s0) * slot_bytes;
-      const T* W1t_ = reinterpret_cast<const T*>(slot);
-      const T* W2t_ = W1t_ + mat;
-      const T* W1_ = W2t_ + mat;
-      const T* W2_ = W1_ + mat;
-      const float* b1_ = reinterpret_cast<const float*>(W2_ + mat);
-      const float* b2_ = b1_ + FF;
-      const size_t xo = (size_t)s * K * F;
-      const T* etas = ETA + (size_t)s * K * K;
-
-      Frag<T> xq[1][FT], xk[1][FT];
-#pragma unroll
-      for (int q = 0; q < FT; ++q) {
-        xq[0][q] = load_frag(XQ + xo, F, 16 * q);
-        xk[0][q] = load_frag(XK + xo, F, 16 * q);
-      }
-      float b1s[HT], b2s[FT];
-#pragma unroll
-      for (int o = 0; o < HT; ++o) b1s[o] = b1_[hs + 16 * o + n];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) b2s[o] = b2_[16 * o + n];
-
-      // ---- R1: layer 1 (Z1 for this slice) and XQ W1
-      Frag<T> x2f[HT], x2F[1][HT];
-      f4 sp1[HT], spp1[HT];
-      Tile zq[1][HT];
-      {
-        Frag<T> w1t[HT][FT];  // (free = hidden, k = f)
-#pragma unroll
-        for (int o = 0; o < HT; ++o)
-#pragma unroll
-          for (int q = 0; q < FT; ++q) w1t[o][q] = load_frag(W1t_ + (size_t)(hs + 16 * o) * F, F, 16 * q);
-        Tile z1[1][HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          z1[0][o].v = f4{b1s[o], b1s[o], b1s[o], b1s[o]};
-          zq[0][o].v = f4{b1s[o], b1s[o], b1s[o], b1s[o]};
-        }
-        gemm<1, HT, FT>(z1, xk, w1t);
-        gemm<1, HT, FT>(zq, xq, w1t);
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          f4 x2;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float z = z1[0][o].v[j];
-            x2[j] = gelu_tanh(z);
-            sp1[o][j] = gelu_bwd(z);
-            spp1[o][j] = gelu_bwd2(z);
-          }
-          x2f[o] = to_frag<T>(x2);
-          x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
-        }
-      }
-      // ---- R2: Z2 partial over this slice
-      {
-        Frag<T> w2t[FT][HT];  // (free = f, k = hidden)
-#pragma unroll
-        for (int o = 0; o < FT; ++o)
-#pragma unroll
-          for (int c = 0; c < HT; ++c) w2t[o][c] = load_frag(W2t_ + (size_t)(16 * o) * FF, FF, hs + 16 * c);
-        Tile z2p[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) z2p[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, FT, HT>(z2p, x2F, w2t);
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.partZ[wave][o][l] = z2p[0][o].v;
-      }
-      __syncthreads();  // (1)
-
-      // ---- R3: G2 (every wave), G1 and the readout of layer 1 (per slice)
-      Frag<T> xkTf[FT], xqTf[FT];
-      LnL2TM<FT> ln2;
-      Tile G2[FT];
-      {
-        f4 tgt[FT];
-#pragma unroll
-        for (int q = 0; q < FT; ++q) {
-          const Tile xkT = transpose16(xk[0][q], I);
-          xkTf[q] = to_frag<T>(xkT.v);
-          xqTf[q] = to_frag<T>(transpose16(xq[0][q], I).v);
-          tgt[q] = transpose16(load_frag(XV + xo, F, 16 * q), I).v - xkT.v;
-        }
-        Tile z2[FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          z2[o].v = f4{b2s[o], b2s[o], b2s[o], b2s[o]};
-#pragma unroll
-          for (int w = 0; w < NW; ++w) z2[o].v += sh.partZ[w][o][l];
-        }
-        ln2.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
-      }
-      Frag<T> g2F[1][FT], g2f[FT];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        g2f[o] = to_frag<T>(G2[o].v);
-        g2F[0][o] = to_frag<T>(transpose16(g2f[o], I).v);
-      }
-      Frag<T> w2[HT][FT];  // (free = hidden, k = f)
+        for (int o = 0; o < HT; ++o) w1_put(i, o, bload_tile(rW1c, w1l, ko, FF, 16 * i, 16 * o));
 #pragma unroll
       for (int i = 0; i < HT; ++i)
 #pragma unroll
-        for (int q = 0; q < FT; ++q) w2[i][q] = load_frag(W2_ + (size_t)(hs + 16 * i) * F, F, 16 * q);
-      Tile Pm[1][HT];
+        for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(rW2c, w2l, ko, F, 16 * i, 16 * o));
 #pragma unroll
-      for (int i = 0; i < HT; ++i) Pm[0][i].v = f4{0.f, 0.f, 0.f, 0.f};
-      gemm<1, HT, FT>(Pm, g2F, w2);
-      Tile G1[HT];
+      for (int o = 0; o < HT; ++o) b1[o] = bload_f32(rB1c, (hs + n) * 4, (kk * FF + 16 * o) * 4);
 #pragma unroll
-      for (int i = 0; i < HT; ++i) G1[i].v = Pm[0][i].v * sp1[i];
-
-      const f4 etaT = load_f4(etas, K, 0);  // [t_k x t_q]: eta[n][4g+j]
-      f4 eta_n;                             // [t_q x t_k]: eta[4g+j][n]
+      for (int o = 0; o < FT; ++o) b2[o] = bload_f32(rB2c, n * 4, (kk * F + 16 * o) * 4);
+    }
+    for (int s = s0; s < s1; ++s) {
+      const int i = s - s0;
+      Frag<T> xk[FT], xkTf[FT];
+      f4 tgt[FT];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) eta_n[j] = (float)etas[(4 * g + j) * K + n];
-      const f4 e = load4(etas + (K - 1) * K + 4 * g);
-      Tile at[1][1], a[1][1];
-      at[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-      a[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-      gemm<1, 1, FT>(at, xk, xq);  // A1^T [t_k x t_q]
-      gemm<1, 1, FT>(a, xq, xk);   // A1   [t_q x t_k]
-      f4 m1T, m1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        m1T[j] = etaT[j] * at[0][0].v[j] + etaT[j];
-        m1[j] = eta_n[j] * a[0][0].v[j] + eta_n[j];
+      for (int q = 0; q < FT; ++q) {
+        xk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
+        const Tile xkT = transpose16(xk[q], I);
+        xkTf[q] = to_frag<T>(xkT.v);
+        tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - xkT.v;
       }
-      Frag<T> x2bf[HT], x2bF[1][HT];
-      f4 sp1b[HT];
+      // Z1 = XK W1 + b1 (token-major, this slice), X2 = gelu(Z1)
+      Frag<T> x2f[HT], x2F[HT];
+      f4 gp[HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        Tile z1;
+        z1.v = f4{b1[o], b1[o], b1[o], b1[o]};
+#pragma unroll
+        for (int q = 0; q < FT; q += 2)
+          mma32(z1.v, xk[q], xk[q + 1], to_frag<T>(w1_tile(q, o).v), to_frag<T>(w1_tile(q + 1, o).v));
+        f4 x2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x2[j] = gelu_tanh(z1.v[j]);
+          gp[o][j] = gelu_bwd(z1.v[j]);
+        }
+        x2f[o] = to_frag<T>(x2);
+        x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
+      }
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        f4 z = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; o += 2)
+          mma32(z, x2F[o], x2F[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
+        sh.x.a.part[wave][c][l] = z;
+      }
+      __syncthreads();  // Z2 partials in
+      Tile G2[FT];
       {
-        const Frag<T> mnf = to_frag<T>(-m1T);
+        Tile z2[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          z2[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
+#pragma unroll
+          for (int w = 0; w < NW; ++w) z2[c].v += sh.x.a.part[w][c][l];
+        }
+        __syncthreads();  // partial buffer free
+        LnL2Lite<FT> ln;
+        ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
+      }
+      // G1 = (G2 W2^T) (.) gelu'(Z1)
+      Tile G1[HT];
+      {
+        Frag<T> g2F[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) g2F[c] = to_frag<T>(transpose16(to_frag<T>(G2[c].v), I).v);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          mma16(zq[0][o].v, mnf, to_frag<T>(G1[o].v));  // Z1b = XQ W1 + b1 - M1 G1
+          G1[o].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < FT; c += 2) mma32(G1[o].v, g2F[c], g2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+          G1[o].v *= gp[o];
+        }
+      }
+      // update operands and bias decrements: store them, then apply the update
+      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        f4 v;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = -e[j] * G1[o].v[j];
+          acc += e[j] * G1[o].v[j];
+        }
+        const Frag<T> g1e = to_frag<T>(v);
+        const float d = sum_col4(acc);
+        b1[o] -= d;
+        bstore_frag<T>(rWS, g1l + o * 256 * ST, i * SLOT, g1e);
+        if (g == 0) bstore_f32(rWS, b1l + 64 * o, i * SLOT + B1D_OFF, d);
+#pragma unroll
+        for (int q = 0; q < FT; ++q) {
+          Tile w = w1_tile(q, o);
+          mma16(w.v, xkTf[q], g1e);
+          w1_put(q, o, w);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        f4 v;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = -e[j] * G2[c].v[j];
+          acc += e[j] * G2[c].v[j];
+        }
+        const Frag<T> g2e = to_frag<T>(v);
+        const float d = sum_col4(acc);
+        b2[c] -= d;
+        bstore_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF, g2e);
+        if (g == 0) bstore_f32(rWS, b2l + 64 * c, i * SLOT + B2D_OFF, d);
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          Tile w = w2_tile(o, c);
+          mma16(w.v, x2f[o], g2e);
+          w2_put(o, c, w);
+        }
+      }
+    }
+
+    // ===================== pass 2: reverse through the group
+    // Regions between barriers:   R1-R2 | R3 | R4-B1 | B2 | B3
+    // exchange area:              Z2 partials; Z2b, A2 partials; dG2, dN1, de
+    //                             partials; dXQ, dXK partials
+    for (int s = s1 - 1; s >= s0; --s) {
+      const int i = s - s0;
+      pin_dW();
+
+      Frag<T> g1e[HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) g1e[o] = bload_frag<T>(rWS, g1l + o * 256 * ST, i * SLOT);
+      Frag<T> xk[FT], xkTf[FT], xqTf[FT];
+      f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
+      Tile z1[HT], zq[HT];
+      {
+        Frag<T> xq[FT];
+#pragma unroll
+        for (int q = 0; q < FT; ++q) {
+          xq[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
+          xk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
+          xkTf[q] = to_frag<T>(transpose16(xk[q], I).v);
+          xqTf[q] = to_frag<T>(transpose16(xq[q], I).v);
+        }
+#pragma unroll
+        for (int q = 0; q < FT; q += 2) {
+          mma32(at, xk[q], xk[q + 1], xq[q], xq[q + 1]);  // A1^T [t_k x t_q]
+          mma32(a, xq[q], xq[q + 1], xk[q], xk[q + 1]);   // A1   [t_q x t_k]
+        }
+        // ---- R1: rebuild W1_s (this slice) and use it at once for
+        //      Z1 = XK W1 + b1 and Zq = XQ W1 + b1
+#pragma unroll
+        for (int o = 0; o < HT; ++o) b1[o] += bload_f32(rWS, b1l + 64 * o, i * SLOT + B1D_OFF);
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          z1[o].v = f4{b1[o], b1[o], b1[o], b1[o]};
+          zq[o].v = z1[o].v;
+          const Frag<T> ng = negate(g1e[o]);
+#pragma unroll
+          for (int q = 0; q < FT; q += 2) {
+            Tile w0 = w1_tile(q, o), w1 = w1_tile(q + 1, o);
+            mma16(w0.v, xkTf[q], ng);
+            mma16(w1.v, xkTf[q + 1], ng);
+            w1_put(q, o, w0);
+            w1_put(q + 1, o, w1);
+            const Frag<T> f0 = to_frag<T>(w0.v), f1 = to_frag<T>(w1.v);
+            mma32(z1[o].v, xk[q], xk[q + 1], f0, f1);
+            mma32(zq[o].v, xq[q], xq[q + 1], f0, f1);
+          }
+        }
+      }
+      Frag<T> x2f[HT], x2F[HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        f4 x2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x2[j] = gelu_tanh(z1[o].v[j]);
+        x2f[o] = to_frag<T>(x2);
+        x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
+      }
+      // ---- R2: rebuild W2_s and b2_s, and the Z2 partial over this slice with it
+#pragma unroll
+      for (int c = 0; c < FT; ++c) b2[c] += bload_f32(rWS, b2l + 64 * c, i * SLOT + B2D_OFF);
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        const Frag<T> ng = negate(bload_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF));
+        f4 z = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; o += 2) {
+          Tile w0 = w2_tile(o, c), w1 = w2_tile(o + 1, c);
+          mma16(w0.v, x2f[o], ng);
+          mma16(w1.v, x2f[o + 1], ng);
+          w2_put(o, c, w0);
+          w2_put(o + 1, c, w1);
+          mma32(z, x2F[o], x2F[o + 1], to_frag<T>(w0.v), to_frag<T>(w1.v));
+        }
+        sh.x.a.part[wave][c][l] = z;
+      }
+      __syncthreads();  // (1) Z2 partials in
+
+      // ---- R3: G2 (every wave), G1 and the readout of layer 1 (per slice)
+      LnL2Lite<FT> ln2;
+      Tile G2[FT];
+      {
+        Tile z2[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          z2[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
+#pragma unroll
+          for (int w = 0; w < NW; ++w) z2[c].v += sh.x.a.part[w][c][l];
+        }
+        f4 tgt[FT];
+#pragma unroll
+        for (int q = 0; q < FT; ++q)
+          tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - frag_to_f4(xkTf[q]);
+        ln2.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
+      }
+      __syncthreads();  // (1x) exchange area free
+      pin_dW();
+      Frag<T> g2f[FT], g2F[FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        g2f[c] = to_frag<T>(G2[c].v);
+        g2F[c] = to_frag<T>(transpose16(g2f[c], I).v);
+      }
+      Tile Pm[HT];  // G2 W2^T; G1 = Pm (.) gelu'(Z1)
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        Pm[o].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < FT; c += 2) mma32(Pm[o].v, g2F[c], g2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+      }
+      auto G1_of = [&](int o) {
+        f4 sp;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sp[j] = gelu_bwd(z1[o].v[j]);
+        return Pm[o].v * sp;
+      };
+
+      const f4 etaT = frag_to_f4(bload_frag<T>(rET, el, es(s)));  // [t_k x t_q]: eta[n][4g+j]
+      f4 eta_n;                                                   // [t_q x t_k]: eta[4g+j][n]
+#pragma unroll
+      for (int j = 0; j < 4; ++j) eta_n[j] = bload1<T>(rET, en + j * K * ST, es(s));
+      Frag<T> x2bf[HT];
+      f4 sp1b[HT];
+      {
+        f4 m1T;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m1T[j] = etaT[j] * at[j] + etaT[j];
+        const Frag<T> mnf = to_frag<T>(-m1T);
+        Frag<T> x2bF[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          mma16(zq[o].v, mnf, to_frag<T>(G1_of(o)));  // Z1b = XQ W1 + b1 - M1 G1
           f4 x2b;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            x2b[j] = gelu_tanh(zq[0][o].v[j]);
-            sp1b[o][j] = gelu_bwd(zq[0][o].v[j]);
+            x2b[j] = gelu_tanh(zq[o].v[j]);
+            sp1b[o][j] = gelu_bwd(zq[o].v[j]);
           }
           x2bf[o] = to_frag<T>(x2b);
-          x2bF[0][o] = to_frag<T>(transpose16(x2bf[o], I).v);
+          x2bF[o] = to_frag<T>(transpose16(x2bf[o], I).v);
         }
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          f4 z = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int o = 0; o < HT; o += 2)
+            mma32(z, x2bF[o], x2bF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
+          sh.x.a.part[wave][c][l] = z;
+        }
+        f4 a2Tp = f4{0.f, 0.f, 0.f, 0.f}, a2p = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; o += 2) {
+          mma32(a2Tp, x2F[o], x2F[o + 1], x2bF[o], x2bF[o + 1]);  // A2^T [t_k x t_q]
+          mma32(a2p, x2bF[o], x2bF[o + 1], x2F[o], x2F[o + 1]);   // A2   [t_q x t_k]
+        }
+        sh.x.a.sm[0][wave][l] = a2Tp;
+        sh.x.a.sm[1][wave][l] = a2p;
       }
-      {
-        Frag<T> w2t[FT][HT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o)
-#pragma unroll
-          for (int c = 0; c < HT; ++c) w2t[o][c] = load_frag(W2t_ + (size_t)(16 * o) * FF, FF, hs + 16 * c);
-        Tile z2bp[1][FT], a2Tp[1][1], a2p[1][1];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) z2bp[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        a2Tp[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        a2p[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, FT, HT>(z2bp, x2bF, w2t);
-        gemm<1, 1, HT>(a2Tp, x2F, x2bF);  // A2^T [t_k x t_q]
-        gemm<1, 1, HT>(a2p, x2bF, x2F);   // A2   [t_q x t_k]
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.u.s.partB[wave][o][l] = z2bp[0][o].v;
-        sh.u.s.a2T[wave][l] = a2Tp[0][0].v;
-        sh.u.s.a2[wave][l] = a2p[0][0].v;
-      }
-      __syncthreads();  // (2)
+      __syncthreads();  // (2) Z2b, A2 partials in
 
       // ---- R4: readout layer 2 and its LayerNorm backward (every wave)
       f4 a2T = f4{0.f, 0.f, 0.f, 0.f}, a2 = f4{0.f, 0.f, 0.f, 0.f};
+      Tile z2b[FT];
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        a2T += sh.u.s.a2T[w][l];
-        a2 += sh.u.s.a2[w][l];
+        a2T += sh.x.a.sm[0][w][l];
+        a2 += sh.x.a.sm[1][w][l];
       }
-      f4 m2T, m2;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        m2T[j] = etaT[j] * a2T[j] + etaT[j];
-        m2[j] = eta_n[j] * a2[j] + eta_n[j];
+      for (int c = 0; c < FT; ++c) {
+        z2b[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) z2b[c].v += sh.x.a.part[w][c][l];
       }
-      Frag<T> dz2bf[FT], dz2bF[1][FT];
-      float dz2b_cs[FT];  // column sums of dZ2b (fp32)
+      __syncthreads();  // (2x) exchange area free
+      pin_dW();
+      Frag<T> dz1bf[HT], dz1bF[HT];
+      float dz1b_cs[HT], dz2b_cs[FT];  // column sums of dZ1b, dZ2b (fp32)
+      f4 detT;
+      Tile dX2[HT], dZ1[HT];
       {
-        Tile z2b[FT];
-        const Frag<T> mnf = to_frag<T>(-m2T);
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          z2b[o].v = f4{b2s[o], b2s[o], b2s[o], b2s[o]};
-#pragma unroll
-          for (int w = 0; w < NW; ++w) z2b[o].v += sh.u.s.partB[w][o][l];
-          mma16(z2b[o].v, mnf, g2f[o]);
-        }
-        f4 mb, rsb;
+        Frag<T> dz2bf[FT], dz2bF[FT];
+        f4 m2T, m2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int o = 0; o < FT; ++o) acc += z2b[o].v[j];
-          mb[j] = sum_row16(acc) * invF;
+          m2T[j] = etaT[j] * a2T[j] + etaT[j];
+          m2[j] = eta_n[j] * a2[j] + eta_n[j];
         }
+        {
+          const Frag<T> mnf = to_frag<T>(-m2T);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int o = 0; o < FT; ++o) {
-            const float d = z2b[o].v[j] - mb[j];
-            acc += d * d;
-          }
-          rsb[j] = 1.0f / sqrtf(sum_row16(acc) * invF + eps);
-        }
-        f4 dT[FT], xhb[FT], gy[FT];
-        f4 a1 = f4{0.f, 0.f, 0.f, 0.f}, a2s = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          dT[o] = transpose16(load_frag(DO + xo, F, 16 * o), I).v;  // dout, token-major
+          for (int c = 0; c < FT; ++c) mma16(z2b[c].v, mnf, g2f[c]);
+          f4 mb, rsb;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            xhb[o][j] = (z2b[o].v[j] - mb[j]) * rsb[j];
-            gy[o][j] = dT[o][j] * lnw_tm[o];
-            a1[j] += gy[o][j];
-            a2s[j] += gy[o][j] * xhb[o][j];
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < FT; ++c) acc += z2b[c].v[j];
+            mb[j] = sum_row16(acc) * invF;
           }
-          if (wave == 0) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < FT; ++c) {
+              const float d = z2b[c].v[j] - mb[j];
+              acc += d * d;
+            }
+            rsb[j] = rsqrt_f(sum_row16(acc) * invF + eps);
+          }
+          f4 xhb[FT], gy[FT];
+          f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            const f4 dT = transpose16(bload_frag<T>(rDO, xl + 16 * c * ST, xs(s)), I).v;  // dout, token-major
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              dlnw[o] += dT[o][j] * xhb[o][j];
-              dlnb[o] += dT[o][j];
+              xhb[c][j] = (z2b[c].v[j] - mb[j]) * rsb[j];
+              gy[c][j] = dT[j] * lnw_tm[c];
+              s1[j] += gy[c][j];
+              s2[j] += gy[c][j] * xhb[c][j];
+            }
+            if (wave == 0) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                dlnw[c] += dT[j] * xhb[c][j];
+                dlnb[c] += dT[j];
+              }
             }
           }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          a1[j] = sum_row16(a1[j]) * invF;
-          a2s[j] = sum_row16(a2s[j]) * invF;
-        }
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          f4 dz;
-          float cs = 0.f;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            dz[j] = rsb[j] * (gy[o][j] - a1[j] - xhb[o][j] * a2s[j]);
-            cs += dz[j];
+            s1[j] = sum_row16(s1[j]) * invF;
+            s2[j] = sum_row16(s2[j]) * invF;
           }
-          dz2b_cs[o] = sum_col4(cs);
-          dz2bf[o] = to_frag<T>(dz);
-          dz2bF[0][o] = to_frag<T>(transpose16(dz2bf[o], I).v);
-        }
-      }
-      // dN2 = -dZ2b G2^T (both layouts), deta part, dA2; dG2 = -M2^T dZ2b
-      f4 detT, dA2T, dA2;
-      {
-        Tile dn[1][1], dnT[1][1];
-        dn[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        dnT[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, 1, FT>(dn, dz2bF, g2F);   // dZ2b G2^T [t_q x t_k]
-        gemm<1, 1, FT>(dnT, g2F, dz2bF);  // G2 dZ2b^T [t_k x t_q]
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          detT[j] = -dnT[0][0].v[j] * (1.0f + a2T[j]);
-          dA2T[j] = -dnT[0][0].v[j] * etaT[j];
-          dA2[j] = -dn[0][0].v[j] * eta_n[j];
+          for (int c = 0; c < FT; ++c) {
+            f4 dz;
+            float cs = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dz[j] = rsb[j] * (gy[c][j] - s1[j] - xhb[c][j] * s2[j]);
+              cs += dz[j];
+            }
+            dz2b_cs[c] = sum_col4(cs);
+            dz2bf[c] = to_frag<T>(dz);
+            dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
+          }
         }
+        // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
+        f4 dA2T, dA2;
+        {
+          f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < FT; c += 2) {
+            mma32(dn, dz2bF[c], dz2bF[c + 1], g2F[c], g2F[c + 1]);   // dZ2b G2^T [t_q x t_k]
+            mma32(dnT, g2F[c], g2F[c + 1], dz2bF[c], dz2bF[c + 1]);  // G2 dZ2b^T [t_k x t_q]
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            detT[j] = -dnT[j] * (1.0f + a2T[j]);
+            dA2T[j] = -dnT[j] * etaT[j];
+            dA2[j] = -dn[j] * eta_n[j];
+          }
+        }
+
+        // ---- B1: readout layer 1 backward (per slice)
+        {
+          const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
+#pragma unroll
+          for (int o = 0; o < HT; ++o) {
+            f4 dx2b = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < FT; c += 2) mma32(dx2b, dz2bF[c], dz2bF[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+            mma16(dx2b, dA2Tf, x2f[o]);  // + dA2 X2
+            const f4 dz = dx2b * sp1b[o];
+            dz1b_cs[o] = sum_col4(dz[0] + dz[1] + dz[2] + dz[3]);
+            dz1bf[o] = to_frag<T>(dz);
+            dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
+            dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
+            mma16(dX2[o].v, dA2f, x2bf[o]);  // dA2^T X2b
+          }
+        }
+        // dN1 = dZ1b G1^T (both layouts)
+        {
+          Frag<T> g1F[HT];
+#pragma unroll
+          for (int o = 0; o < HT; ++o) g1F[o] = to_frag<T>(transpose16(to_frag<T>(G1_of(o)), I).v);
+          f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int o = 0; o < HT; o += 2) {
+            mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
+            mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
+          }
+          sh.x.a.sm[0][wave][l] = dn;
+          sh.x.a.sm[1][wave][l] = dnT;
+        }
+        // dG1 = -M1^T dZ1b - e (XK dW1' + db1'); eta-row gradient partial (G1 . Q1 + G2 . Q2)
+        const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+        Tile dG1[HT];
+        f4 eq2[FT];  // this slice's share of -e Q2, Q2 = X2 dW2' + db2'
+        {
+          f4 m1;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
+          const Frag<T> mf = to_frag<T>(-m1);
+          f4 dep = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int o = 0; o < HT; ++o) {
+            f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
+#pragma unroll
+            for (int q = 0; q < FT; q += 2)
+              mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
+            dG1[o].v = f4{0.f, 0.f, 0.f, 0.f};
+            mma16(dG1[o].v, mf, dz1bf[o]);
+            const f4 g1 = G1_of(o);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dG1[o].v[j] -= e[j] * q1[j];
+              dep[j] += g1[j] * q1[j];
+            }
+          }
+          // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2; both are
+          // linear in Q2, so this slice's share goes into the partials as it is
+          // (wave 0's share carries db2')
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int o = 0; o < HT; o += 2)
+              mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
+            if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dep[j] += G2[c].v[j] * q2[j];
+              eq2[c][j] = -e[j] * q2[j];
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
+          sh.x.a.sm[2][wave][l] = dep;
+        }
+        // dX2 += (-e G2) dW2'^T  (contraction over features; dW2'^T frags by transposes)
+        {
+          Frag<T> eg2F[FT];
+#pragma unroll
+          for (int c = 0; c < FT; ++c)
+            eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF), I).v);
+#pragma unroll
+          for (int o = 0; o < HT; ++o)
+#pragma unroll
+            for (int c = 0; c < FT; c += 2) {
+              const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c].v), I).v);
+              const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c + 1].v), I).v);
+              mma32(dX2[o].v, eg2F[c], eg2F[c + 1], u0, u1);
+            }
+        }
+        // dP = dG1 (.) gelu'(Z1), dZ1 <- dG1 (.) Pm (.) gelu''(Z1); dG2 partial over this
+        // slice: dP W2 - e Q2 (- M2^T dZ2b, which every wave holds, added once by wave 0)
+        Frag<T> dPf[HT], dPF[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          f4 sp, spp;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sp[j] = gelu_bwd(z1[o].v[j]);
+            spp[j] = gelu_bwd2(z1[o].v[j]);
+          }
+          dZ1[o].v = dG1[o].v * Pm[o].v * spp;
+          dPf[o] = to_frag<T>(dG1[o].v * sp);
+          dPF[o] = to_frag<T>(transpose16(dPf[o], I).v);
+        }
+        {
+          const Frag<T> mf = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            f4 z = eq2[c];
+            mma16(z, mf, dz2bf[c]);
+#pragma unroll
+            for (int o = 0; o < HT; o += 2)
+              mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
+            sh.x.a.part[wave][c][l] = z;
+          }
+        }
+        // two terms of the layer-2 state gradient (dW2' has been used)
+#pragma unroll
+        for (int o = 0; o < HT; ++o)
+#pragma unroll
+          for (int c = 0; c < FT; ++c) mma32(dW2[o][c].v, x2bf[o], dPf[o], dz2bf[c], g2f[c]);
       }
+      __syncthreads();  // (3) dG2, dN1, eta-row partials in
+
+      // ---- B2: assemble dN1, de; deta (wave 0); G2 backward (every wave); dX2, dZ1;
+      //      dXQ and dXK partials; the rest of the state gradient
+      f4 dA1T, dA1;
       Tile dG2[FT];
       {
-        const Frag<T> mf = to_frag<T>(-m2);
+        f4 dn1 = f4{0.f, 0.f, 0.f, 0.f}, dn1T = f4{0.f, 0.f, 0.f, 0.f}, de = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          dG2[o].v = f4{0.f, 0.f, 0.f, 0.f};
-          mma16(dG2[o].v, mf, dz2bf[o]);
+        for (int w = 0; w < NW; ++w) {
+          dn1 += sh.x.a.sm[0][w][l];
+          dn1T += sh.x.a.sm[1][w][l];
+          de += sh.x.a.sm[2][w][l];
         }
-      }
-
-      // ---- B1: readout layer 1 backward and the state-update terms (per slice)
-      Frag<T> dz1bf[HT], dz1bF[1][HT];
-      float dz1b_cs[HT];  // column sums of dZ1b (fp32)
-      Tile dX2[HT], dG1[HT];
-      {
-        Tile dx2b[1][HT];
 #pragma unroll
-        for (int i = 0; i < HT; ++i) dx2b[0][i].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, HT, FT>(dx2b, dz2bF, w2);  // dZ2b W2^T
-        const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
+        for (int c = 0; c < FT; ++c) {
+          dG2[c].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          mma16(dx2b[0][o].v, dA2Tf, x2f[o]);  // + dA2 X2
-          const f4 dz = dx2b[0][o].v * sp1b[o];
-          dz1b_cs[o] = sum_col4(dz[0] + dz[1] + dz[2] + dz[3]);
-          dz1bf[o] = to_frag<T>(dz);
-          dz1bF[0][o] = to_frag<T>(transpose16(dz1bf[o], I).v);
-          dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
-          mma16(dX2[o].v, dA2f, x2bf[o]);      // dA2^T X2b
+          for (int w = 0; w < NW; ++w) dG2[c].v += sh.x.a.part[w][c][l];
         }
-      }
-      {
-        Frag<T> g1F[1][HT];
 #pragma unroll
-        for (int o = 0; o < HT; ++o) g1F[0][o] = to_frag<T>(transpose16(to_frag<T>(G1[o].v), I).v);
-        Tile dn[1][1], dnT[1][1];
-        dn[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        dnT[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, 1, HT>(dn, dz1bF, g1F);
-        gemm<1, 1, HT>(dnT, g1F, dz1bF);
-        sh.u.s.dn1[wave][l] = dn[0][0].v;
-        sh.u.s.dn1T[wave][l] = dnT[0][0].v;
-        // -(e G1) dW1'^T over this slice -> dXK partial
-        Frag<T> eg1F[1][HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          f4 v;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = -e[j] * G1[o].v[j];
-          eg1F[0][o] = to_frag<T>(transpose16(to_frag<T>(v), I).v);
+        for (int j = 0; j < 4; ++j) {
+          dn1[j] = -dn1[j];
+          dn1T[j] = -dn1T[j];
+          detT[j] += dn1T[j] * (1.0f + at[j]);
+          dA1T[j] = dn1T[j] * etaT[j];
+          dA1[j] = dn1[j] * eta_n[j];
         }
-        Tile t1[1][FT];
+        if (wave == 0) {
+          if (n == K - 1) {
 #pragma unroll
-        for (int q = 0; q < FT; ++q) {
-          t1[0][q].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < HT; c += 2) {
-            const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW1[q][c].v), I).v);
-            const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW1[q][c + 1].v), I).v);
-            mma32(t1[0][q].v, eg1F[0][c], eg1F[0][c + 1], u0, u1);
+            for (int j = 0; j < 4; ++j) detT[j] -= de[j];
           }
-          sh.u.s.partD[wave][q][l] = t1[0][q].v;
+          bstore_frag<T>(rDET, el, es(s), to_frag<T>(detT));
         }
       }
-      {
-        Frag<T> w1[FT][HT];  // (free = f, k = hidden)
-#pragma unroll
-        for (int o = 0; o < FT; ++o)
-#pragma unroll
-          for (int c = 0; c < HT; ++c) w1[o][c] = load_frag(W1_ + (size_t)(16 * o) * FF, FF, hs + 16 * c);
-        Tile dxqp[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) dxqp[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, FT, HT>(dxqp, dz1bF, w1);  // dZ1b W1^T
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.u.s.partA[wave][o][l] = dxqp[0][o].v;
-      }
-      {
-        // dG1 = -M1^T dZ1b - e (XK dW1' + db1')
-        Tile q1[1][HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) q1[0][o].v = f4{db1[o], db1[o], db1[o], db1[o]};
-        gemm_pt<1, HT, FT>(q1, xk, dW1);
-        const Frag<T> mf = to_frag<T>(-m1);
-        f4 dep = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          dG1[o].v = f4{0.f, 0.f, 0.f, 0.f};
-          mma16(dG1[o].v, mf, dz1bf[o]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dG1[o].v[j] -= e[j] * q1[0][o].v[j];
-            dep[j] += G1[o].v[j] * q1[0][o].v[j];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
-        sh.u.s.de[wave][l] = dep;
-        // X2 dW2' over this slice -> Q2 partial
-        Tile q2p[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) q2p[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm_pt<1, FT, HT>(q2p, x2F, dW2);
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.u.s.partC[wave][o][l] = q2p[0][o].v;
-        // dX2 -= (e G2) dW2'^T  (contraction over f, dW2'^T frags by transposes)
-        Frag<T> eg2F[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          f4 v;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = -e[j] * G2[o].v[j];
-          eg2F[0][o] = to_frag<T>(transpose16(to_frag<T>(v), I).v);
-        }
-#pragma unroll
-        for (int c = 0; c < HT; ++c)
-#pragma unroll
-          for (int q = 0; q + 1 < FT; q += 2) {
-            const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW2[c][q].v), I).v);
-            const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW2[c][q + 1].v), I).v);
-            mma32(dX2[c].v, eg2F[0][q], eg2F[0][q + 1], u0, u1);
-          }
-      }
-      __syncthreads();  // (3)
-
-      // ---- B2: assemble dN1, Q2, de; dXQ and deta (wave 0); dP, dZ1
-      f4 dn1 = f4{0.f, 0.f, 0.f, 0.f}, dn1T = f4{0.f, 0.f, 0.f, 0.f}, de = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        dn1 += sh.u.s.dn1[w][l];
-        dn1T += sh.u.s.dn1T[w][l];
-        de += sh.u.s.de[w][l];
-      }
-      f4 dA1T, dA1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        dn1[j] = -dn1[j];
-        dn1T[j] = -dn1T[j];
-        detT[j] += dn1T[j] * (1.0f + at[0][0].v[j]);
-        dA1T[j] = dn1T[j] * etaT[j];
-        dA1[j] = dn1[j] * eta_n[j];
-      }
-      {
-        f4 dep = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          f4 q2 = f4{db2[o], db2[o], db2[o], db2[o]};
-#pragma unroll
-          for (int w = 0; w < NW; ++w) q2 += sh.u.s.partC[w][o][l];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dG2[o].v[j] -= e[j] * q2[j];
-            dep[j] += G2[o].v[j] * q2[j];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) de[j] = -(de[j] + sum_row16(dep[j]));
-      }
-      if (wave == 0) {
-        const Frag<T> dA1Tf = to_frag<T>(dA1T);
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          Tile dxq;
-          dxq.v = transpose16(load_frag(DO + xo, F, 16 * o), I).v;
-#pragma unroll
-          for (int w = 0; w < NW; ++w) dxq.v += sh.u.s.partA[w][o][l];
-          mma16(dxq.v, dA1Tf, xkTf[o]);  // + dA1 XK
-          store_f4(DXQ + xo, F, 16 * o, transpose16(to_frag<T>(dxq.v), I).v);
-        }
-        if (n == K - 1) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) detT[j] += de[j];
-        }
-        store_f4(DETA + (size_t)s * K * K, K, 0, detT);
-      }
-      Frag<T> dPf[HT];
-      Tile dZ1[HT];
-      {
-        Frag<T> dPF[1][HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          const f4 dp = dG1[o].v * sp1[o];
-          dZ1[o].v = dG1[o].v * Pm[0][o].v * spp1[o];
-          dPf[o] = to_frag<T>(dp);
-          dPF[0][o] = to_frag<T>(transpose16(dPf[o], I).v);
-        }
-        Frag<T> w2t[FT][HT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o)
-#pragma unroll
-          for (int c = 0; c < HT; ++c) w2t[o][c] = load_frag(W2t_ + (size_t)(16 * o) * FF, FF, hs + 16 * c);
-        Tile dg2p[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) dg2p[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, FT, HT>(dg2p, dPF, w2t);  // dP W2
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.u.s.partB[wave][o][l] = dg2p[0][o].v;
-      }
-      __syncthreads();  // (4)
-
-      // ---- B3: G2 backward (every wave), dX2, dZ1, dXK partials
-#pragma unroll
-      for (int o = 0; o < FT; ++o)
-#pragma unroll
-        for (int w = 0; w < NW; ++w) dG2[o].v += sh.u.s.partB[w][o][l];
+      __syncthreads();  // (3x) exchange area free
+      pin_dW();
       f4 dz2[FT], dtgt[FT];
       {
         float lw_i[FT], lb_i[FT];
 #pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          lw_i[o] = 0.f;
-          lb_i[o] = 0.f;
+        for (int c = 0; c < FT; ++c) {
+          lw_i[c] = 0.f;
+          lb_i[c] = 0.f;
         }
-        ln2.backward(dG2, G2, lnw_tm, dz2, dtgt, lw_i, lb_i);
+        f4 tgt[FT];
+#pragma unroll
+        for (int q = 0; q < FT; ++q)
+          tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - frag_to_f4(xkTf[q]);
+        ln2.backward(dG2, G2, tgt, lnw_tm, lnb_tm, dz2, dtgt, lw_i, lb_i);
         if (wave == 0) {
 #pragma unroll
-          for (int o = 0; o < FT; ++o) {
-            dlnw[o] += lw_i[o];
-            dlnb[o] += lb_i[o];
+          for (int c = 0; c < FT; ++c) {
+            dlnw[c] += lw_i[c];
+            dlnb[c] += lb_i[c];
           }
         }
       }
-      Frag<T> dz2f[FT], dz2F[1][FT];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        dz2f[o] = to_frag<T>(dz2[o]);
-        dz2F[0][o] = to_frag<T>(transpose16(dz2f[o], I).v);
-      }
       Frag<T> dz1f[HT];
       {
-        Tile dx2[1][HT];
+        Frag<T> dz2F[FT];
 #pragma unroll
-        for (int o = 0; o < HT; ++o) dx2[0][o] = dX2[o];
-        gemm<1, HT, FT>(dx2, dz2F, w2);  // + dZ2 W2^T
-        Frag<T> dz1F[1][HT];
+        for (int c = 0; c < FT; ++c) {
+          const Frag<T> dz2f = to_frag<T>(dz2[c]);
+          dz2F[c] = to_frag<T>(transpose16(dz2f, I).v);
+#pragma unroll
+          for (int o = 0; o < HT; ++o) mma16(dW2[o][c].v, x2f[o], dz2f);  // + X2^T dZ2
+        }
+        Frag<T> dz1F[HT], eg1F[HT];
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          dZ1[o].v += dx2[0][o].v * sp1[o];
+#pragma unroll
+          for (int c = 0; c < FT; c += 2) mma32(dX2[o].v, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+          f4 sp;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sp[j] = gelu_bwd(z1[o].v[j]);
+          dZ1[o].v += dX2[o].v * sp;
           dz1f[o] = to_frag<T>(dZ1[o].v);
-          dz1F[0][o] = to_frag<T>(transpose16(dz1f[o], I).v);
+          dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
+          eg1F[o] = to_frag<T>(transpose16(g1e[o], I).v);
         }
-        Frag<T> w1[FT][HT];
+        // dXQ partial = dZ1b W1^T, dXK partial = dZ1 W1^T + (-e G1) dW1'^T (this slice)
 #pragma unroll
-        for (int o = 0; o < FT; ++o)
+        for (int f = 0; f < FT; ++f) {
+          f4 zq_ = f4{0.f, 0.f, 0.f, 0.f}, zk_ = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < HT; ++c) w1[o][c] = load_frag(W1_ + (size_t)(16 * o) * FF, FF, hs + 16 * c);
-        Tile dxkp[1][FT];
-#pragma unroll
-        for (int o = 0; o < FT; ++o) dxkp[0][o].v = f4{0.f, 0.f, 0.f, 0.f};
-        gemm<1, FT, HT>(dxkp, dz1F, w1);  // dZ1 W1^T
-#pragma unroll
-        for (int o = 0; o < FT; ++o) sh.u.s.partC[wave][o][l] = dxkp[0][o].v;
-      }
-      __syncthreads();  // (5)
-
-      // ---- B4: dXK, dXV (wave 0); accumulate the state gradient
-      if (wave == 0) {
-        const Frag<T> dA1f = to_frag<T>(dA1);
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          Tile dxk;
-          dxk.v = -dtgt[o];
-#pragma unroll
-          for (int w = 0; w < NW; ++w) dxk.v += sh.u.s.partC[w][o][l] + sh.u.s.partD[w][o][l];
-          mma16(dxk.v, dA1f, xqTf[o]);  // + dA1^T XQ
-          store_f4(DXK + xo, F, 16 * o, transpose16(to_frag<T>(dxk.v), I).v);
-          store_f4(DXV + xo, F, 16 * o, transpose16(to_frag<T>(dtgt[o]), I).v);
+          for (int c = 0; c < HT; c += 2) {
+            const Frag<T> v0 = w1T_frag(f, c), v1 = w1T_frag(f, c + 1);
+            mma32(zq_, dz1bF[c], dz1bF[c + 1], v0, v1);
+            mma32(zk_, dz1F[c], dz1F[c + 1], v0, v1);
+            const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW1[f][c].v), I).v);
+            const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW1[f][c + 1].v), I).v);
+            mma32(zk_, eg1F[c], eg1F[c + 1], u0, u1);
+          }
+          sh.x.b.dxq[wave][f][l] = zq_;
+          sh.x.b.dxk[wave][f][l] = zk_;
         }
       }
+      // the layer-1 state gradient: dW1 += XQ^T dZ1b + XK^T dZ1; biases
 #pragma unroll
       for (int q = 0; q < FT; ++q)
 #pragma unroll
-        for (int c = 0; c < HT; ++c) mma32(dW1[q][c].v, xqTf[q], xkTf[q], dz1bf[c], dz1f[c]);
-#pragma unroll
-      for (int c = 0; c < HT; ++c)
-#pragma unroll
-        for (int o = 0; o < FT; ++o) {
-          mma32(dW2[c][o].v, x2bf[c], dPf[c], dz2bf[o], g2f[o]);
-          mma16(dW2[c][o].v, x2f[c], dz2f[o]);
-        }
-      // column sums in fp32: db1 += colsum(dZ1b + dZ1), db2 += colsum(dZ2b + dZ2)
+        for (int o = 0; o < HT; ++o) mma32(dW1[q][o].v, xqTf[q], xkTf[q], dz1bf[o], dz1f[o]);
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
         float acc = 0.f;
@@ -846,27 +810,50 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         db1[o] += sum_col4(acc) + dz1b_cs[o];
       }
 #pragma unroll
-      for (int o = 0; o < FT; ++o) {
+      for (int c = 0; c < FT; ++c) {
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc += dz2[o][j];
-        db2[o] += sum_col4(acc) + dz2b_cs[o];
+        for (int j = 0; j < 4; ++j) acc += dz2[c][j];
+        db2[c] += sum_col4(acc) + dz2b_cs[c];
       }
+      __syncthreads();  // (4) dXQ, dXK partials in
+
+      // ---- B3: dXQ, dXK, dXV (tile owners)
+      {
+        const Frag<T> dA1Tf = to_frag<T>(dA1T), dA1f = to_frag<T>(dA1);
+#pragma unroll
+        for (int f = 0; f < FT; ++f) {
+          if (f % NW != wave) continue;
+          f4 dxq = transpose16(bload_frag<T>(rDO, xl + 16 * f * ST, xs(s)), I).v;
+          f4 dxk = -dtgt[f];
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            dxq += sh.x.b.dxq[w][f][l];
+            dxk += sh.x.b.dxk[w][f][l];
+          }
+          mma16(dxq, dA1Tf, xkTf[f]);  // + dA1 XK
+          mma16(dxk, dA1f, xqTf[f]);   // + dA1^T XQ
+          bstore_frag<T>(rDXQ, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dxq), I).v));
+          bstore_frag<T>(rDXK, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dxk), I).v));
+          bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dtgt[f]), I).v));
+        }
+      }
+      __syncthreads();  // (4x) exchange area free for the next mini-batch
     }
   }
 
   // ---- outputs: gradient wrt the initial state, LN parameters
   {
-    float* w1 = p.dW1 + (size_t)chain * F * FF;
-    float* w2 = p.dW2 + (size_t)chain * FF * F;
+    const rsrc_t rdW1 = make_rsrc(p.dW1 + (size_t)chain * F * FF, (unsigned)(F * FF * 4));
+    const rsrc_t rdW2 = make_rsrc(p.dW2 + (size_t)chain * FF * F, (unsigned)(FF * F * 4));
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < HT; ++o) store_tile(w1, FF, 16 * i, hs + 16 * o, dW1[i][o]);
+      for (int o = 0; o < HT; ++o) bstore_tile(rdW1, w1l, 0, FF, 16 * i, 16 * o, dW1[i][o]);
 #pragma unroll
     for (int i = 0; i < HT; ++i)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) store_tile(w2, F, hs + 16 * i, 16 * o, dW2[i][o]);
+      for (int o = 0; o < FT; ++o) bstore_tile(rdW2, w2l, 0, F, 16 * i, 16 * o, dW2[i][o]);
     if (g == 0) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) p.db1[(size_t)chain * FF + hs + 16 * o + n] = db1[o];
@@ -911,11 +898,6 @@ hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream) 
     if (p.F == 32) return launch_mlp_bwd_f<float, 2>(p, stream);
   }
   return hipErrorInvalidValue;
-}
-
-size_t mlp_bwd_slot_bytes(int F, int FF, int dtype) {
-  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
-  return 4 * (size_t)F * FF * t + (size_t)(FF + F) * sizeof(float);
 }
 
 }  // namespace ttt

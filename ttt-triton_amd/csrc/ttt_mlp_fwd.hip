@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           const float d = z2b[o].v[j] - mu[j];
           acc += d * d;
         }
-        rs[j] = 1.0f / sqrtf(sum_row16(acc) * invF + eps);
+        rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
       T* o_s = OUT + xo;
       for (int o = wave; o < FT; o += NW) {

@@ -168,7 +168,7 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
         v[c] -= mean;
         q += v[c] * v[c];
       }
-      const float rstd = 1.0f / sqrtf(sum_row16(q) * invF + p.eps);
+      const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
       const size_t r = (row0 + 4 * g + j) * F;
 #pragma unroll
       for (int c = 0; c < FT; ++c) {

@@ -71,6 +71,16 @@ template <typename T> __device__ __forceinline__ f4 frag_to_f4(Frag<T> f) {
   return f4{(float)f.v[0], (float)f.v[1], (float)f.v[2], (float)f.v[3]};
 }
 
+// exact sign flip of every element
+__device__ __forceinline__ Frag<__bf16> negate(Frag<__bf16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 m = {0x8000, 0x8000, 0x8000, 0x8000};
+  Frag<__bf16> r;
+  r.v = __builtin_bit_cast(bf4, __builtin_bit_cast(us4, f.v) ^ m);
+  return r;
+}
+__device__ __forceinline__ Frag<float> negate(Frag<float> f) { return Frag<float>{-f.v}; }
+
 // ---------------------------------------------------------------- MFMA
 // acc += P * Q over one 16-deep k-block.
 //
@@ -266,6 +276,37 @@ __device__ __forceinline__ void store_tile(float* __restrict__ x, int ld, int r0
   for (int j = 0; j < 4; ++j) x[(r0 + 4 * g + j) * ld + c0 + n] = t.v[j];
 }
 
+// fp32 matrix [rows][COLS] in LDS with columns XOR-swizzled by 4 * (row & 7):
+// a C-layout tile (lanes of group g read rows 4g + j, 16 consecutive columns)
+// and a row-vector frag (lanes of group g read 4 consecutive columns of 16
+// rows) are both bank-conflict free with no padding.  COLS % 32 == 0.
+template <int COLS> struct LdsMat {
+  float* p;
+  __device__ __forceinline__ static int idx(int row, int col) { return row * COLS + (col ^ ((row & 7) << 2)); }
+  // C-layout tile at (r0, c0): lane (g, n) holds M[r0 + 4g + j][c0 + n]
+  __device__ __forceinline__ Tile tile(int r0, int c0) const {
+    const int l = lane_id(), g = l >> 4, n = l & 15;
+    Tile t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t.v[j] = p[idx(r0 + 4 * g + j, c0 + n)];
+    return t;
+  }
+  __device__ __forceinline__ void put_tile(int r0, int c0, Tile t) const {
+    const int l = lane_id(), g = l >> 4, n = l & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[idx(r0 + 4 * g + j, c0 + n)] = t.v[j];
+  }
+  // row-vector frag at (r0, c0): lane (g, r) holds M[r0 + r][c0 + 4g + j]
+  __device__ __forceinline__ f4 row4(int r0, int c0) const {
+    const int l = lane_id(), g = l >> 4, r = l & 15;
+    return *reinterpret_cast<const f4*>(p + idx(r0 + r, c0 + 4 * g));
+  }
+  __device__ __forceinline__ void put_row4(int r0, int c0, f4 v) const {
+    const int l = lane_id(), g = l >> 4, r = l & 15;
+    *reinterpret_cast<f4*>(p + idx(r0 + r, c0 + 4 * g)) = v;
+  }
+};
+
 // Tile registers <-> scratch in register order (fully coalesced float4 per lane)
 __device__ __forceinline__ void spill_tile(float* __restrict__ x, Tile t) {
   reinterpret_cast<f4*>(x)[lane_id()] = t.v;
@@ -276,11 +317,18 @@ __device__ __forceinline__ Tile fill_tile(const float* __restrict__ x) {
   return t;
 }
 
+// ---------------------------------------------------------------- fast reciprocals
+// v_rcp_f32 / v_rsq_f32 (about 1 ulp) instead of the IEEE divide and square
+// root sequences; every argument here is a normal positive number.
+__device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float rsqrt_f(float x) { return __builtin_amdgcn_rsqf(x); }
+
 // ---------------------------------------------------------------- GELU (tanh form)
-// tanh via exp: t = 1 - 2/(exp(2x)+1); saturates correctly for large |x|.
+// tanh via exp: t = 1 - 2/(exp(2x)+1); saturates correctly for large |x|
+// (exp -> inf gives t = 1, exp -> 0 gives t = -1).
 __device__ __forceinline__ float tanh_f(float x) {
   const float e = __expf(2.0f * x);
-  return 1.0f - 2.0f / (e + 1.0f);
+  return 1.0f - 2.0f * rcp_f(e + 1.0f);
 }
 // F.gelu(x, approximate="tanh"): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
 __device__ __forceinline__ float gelu_tanh(float x) {
