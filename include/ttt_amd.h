@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 1
+#define TTT_AMD_ABI_VERSION 2
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -93,34 +93,45 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
  *   *_last            final state, shapes of *_init (all four or none)
  *   *_ckpt            [B,H,NK,...] state entering mini-batch k*G (all four or none)
  *   *_memo            [B,H,NS,...], NS = ceil(NC/M): state after mini-batch
- *                     s*M has been applied (all four or none; M >= 1 then) */
+ *                     s*M has been applied (all four or none; M >= 1 then)
+ *   upd               NULL, or >= ttt_mlp_upd_bytes(...) bytes: receives every
+ *                     mini-batch's state-update operands for ttt_mlp_bwd.  It
+ *                     has no counterpart in the reference, whose backward
+ *                     re-runs each checkpoint group forward to recover them.
+ * Per-chain slabs are addressed with 32-bit offsets: NC * F * FF * 4 and NC
+ * times the per-mini-batch update size must stay below 2^31 bytes. */
 int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
                 const float* W2_init, const float* b2_init,
                 int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
                 void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last,
                 float* W1_ckpt, float* b1_ckpt, float* W2_ckpt, float* b2_ckpt,
-                float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo, void* stream);
+                float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo,
+                void* upd, size_t upd_bytes, void* stream);
 
-/* Bytes of device workspace ttt_mlp_bwd needs for these sizes. */
-size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int G, int dtype);
+/* Bytes of the update-operand buffer of ttt_mlp_fwd / ttt_mlp_bwd:
+ * B*H*NC mini-batches x ((FF + F) * K * sizeof(dtype) + (FF + F) * 4). */
+size_t ttt_mlp_upd_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
  * state's gradient zero, as in the ops path).  Replaces ttt_mlp_scan_backward
  * (kernels/mlp_backward.py:247-651) as launched by TritonMLP._backward_core
  * (mlp_triton.py:200-351).
  *   *_ckpt           checkpoints written by ttt_mlp_fwd with the same G
+ *   *_last           the final state written by that ttt_mlp_fwd call
  *   dout             [B,H,NC,K,F] dtype
  *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
  *   dW1, db1, dW2, db2  fp32, shapes of W1_init ... (gradient wrt the initial state)
  *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
- *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes */
+ *   upd              the update operands written by that ttt_mlp_fwd call
+ *                    (upd_bytes >= ttt_mlp_upd_bytes(...)) */
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
-                const float* W2_ckpt, const float* b2_ckpt, const void* dout,
+                const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,
+                const float* W2_last, const float* b2_last, const void* dout,
                 int B, int H, int NC, int K, int F, int FF, int G, int dtype, float eps,
                 void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
-                float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
+                float* dln_w, float* dln_b, const void* upd, size_t upd_bytes, void* stream);
 
 /* Fixed-weight TTT-MLP readout over a segment of NS mini-batches:
  *   out = XQ + LN_eps(gelu(XQ W1 + b1) W2 + b2)   (no state update)

@@ -27,10 +27,11 @@ def _say(*a):
 KEYS = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
 
 
-def _fwd(d, G, M=0):
+def _fwd(d, G, M=0, want_upd=True):
+    """(out, ckpt, memo, last, upd) of the HIP forward"""
     from ttt_amd.mlp import mlp_forward
     g = to_dev(d)
-    return mlp_forward(*(g[k] for k in KEYS), G, M=M, want_ckpt=True, want_last=True)
+    return mlp_forward(*(g[k] for k in KEYS), G, M=M, want_ckpt=True, want_last=True, want_upd=want_upd)
 
 
 def _perturb(d, H, F_, FF, seed):
@@ -46,7 +47,7 @@ def _perturb(d, H, F_, FF, seed):
 def test_mlp_fwd_fp32(FF):
     _say("mlp fwd fp32 FF", FF)
     d = _perturb(O.make_inputs(2, 2, 6, 16, 64, FF=FF, seed=1, dtype=torch.float32), 2, 64, FF, 3)
-    out, ck, memo, last = _fwd(d, G=4, M=2)
+    out, ck, memo, last, _ = _fwd(d, G=4, M=2)
     ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=4, M=2)
     bad = []
     for name, mine in (("out", out), ("W1_last", last[0]), ("b1_last", last[1]), ("W2_last", last[2]),
@@ -63,7 +64,7 @@ def test_mlp_fwd_fp32(FF):
 def test_mlp_fwd_bf16_ff256(kind):
     _say("mlp fwd bf16 FF256", kind)
     d = O.make_inputs(2, 3, 24, 16, 64, FF=256, seed=2, dtype=torch.bfloat16, eta_kind=kind)
-    out, ck, memo, last = _fwd(d, G=8, M=2)
+    out, ck, memo, last, _ = _fwd(d, G=8, M=2)
     ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=8, M=2)
     bad = []
     for name, mine in (("out", out), ("W1_last", last[0]), ("W2_last", last[2]), ("W1_ckpt", ck[0]),
@@ -78,18 +79,45 @@ def test_mlp_fwd_bf16_ff256(kind):
 def test_mlp_fwd_headdim32():
     _say("mlp fwd fp32 F32 FF64")
     d = O.make_inputs(1, 2, 5, 16, 32, FF=64, seed=4, dtype=torch.float32)
-    out, _, _, last = _fwd(d, G=2)
+    out, _, _, last, _ = _fwd(d, G=2)
     ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=2)
     assert max_abs(out, ref["out"]) <= FP32_ATOL
     assert max_abs(last[2], ref["W2_last"]) <= FP32_ATOL
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_mlp_fwd_update_operands(dt):
+    """The update-operand buffer leaves every forward output unchanged, and its
+    bias decrements add up to the bias change over the sequence:
+    b_init - sum_s b_dec[s] = b_last."""
+    _say("mlp fwd update operands", dt)
+    B, H, NC, F_, FF = 2, 2, 7, 64, 128
+    d = _perturb(O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=11, dtype=dt), H, F_, FF, 12)
+    out0, ck0, _, last0, none = _fwd(d, G=3, want_upd=False)
+    out1, ck1, _, last1, upd = _fwd(d, G=3)
+    assert none is None
+    assert torch.equal(out0, out1)
+    for a, b in zip(ck0 + last0, ck1 + last1):
+        assert torch.equal(a, b)
+    st = 2 if dt == torch.bfloat16 else 4
+    slot = (FF + F_) * 16 * st + (FF + F_) * 4
+    assert upd.numel() == B * H * NC * slot
+    u = upd.view(B * H, NC, slot)
+    b1d = u[:, :, (FF + F_) * 16 * st:(FF + F_) * 16 * st + FF * 4].contiguous().view(torch.float32)
+    b2d = u[:, :, (FF + F_) * 16 * st + FF * 4:].contiguous().view(torch.float32)
+    g = to_dev(d)
+    b1 = g["b1"].reshape(B * H, FF) - b1d.sum(1)
+    b2 = g["b2"].reshape(B * H, F_) - b2d.sum(1)
+    assert max_abs(b1, last1[1].reshape(B * H, FF)) <= 1e-5 * max(1.0, float(b1.abs().max()))
+    assert max_abs(b2, last1[3].reshape(B * H, F_)) <= 1e-5 * max(1.0, float(b2.abs().max()))
+
+
 def _bwd(d, G):
     from ttt_amd.mlp import mlp_backward
     g = to_dev(d)
-    out, ck, _, _ = _fwd(d, G)
+    out, ck, _, last, upd = _fwd(d, G)
     (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
-        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, g["dOut"], G)
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, upd, g["dOut"], G)
     return dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2, dln_w=dlw, dln_b=dlb)
 
 

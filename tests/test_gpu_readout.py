@@ -79,7 +79,7 @@ def test_readout_memo_slices_in_place():
     d = O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=5, dtype=torch.float32)
     keys = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
     g = {k: v.cuda() for k, v in d.items()}
-    _, _, memo, _ = mlp_forward(*(g[k] for k in keys), 3, M=M, want_ckpt=False)
+    _, _, memo, _, _ = mlp_forward(*(g[k] for k in keys), 3, M=M, want_ckpt=False)
     ref_full = O.mlp_forward_full(*(d[k].double() for k in keys), G=3, M=M)
     NS = memo[0].shape[2]
     for j in range(NS):

@@ -33,6 +33,15 @@ int check_common(int B, int H, int NC, int K, int F, int G, int dtype, float eps
 
 int hip_status(hipError_t e) { return e == hipSuccess ? TTT_OK : TTT_ERR_HIP; }
 
+// TTT-MLP shapes: hidden width, and per-chain slabs addressable with 32-bit
+// byte offsets (the state checkpoints are the largest, NC * F * FF * 4 bytes)
+int check_mlp(int NC, int F, int FF, int dtype) {
+  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  if ((long long)NC * F * FF * 4 > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  if ((long long)NC * ttt::mlp_upd_slot_bytes(F, FF, dtype) > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return TTT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -167,10 +176,11 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* b2_init, int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
                 void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last, float* W1_ckpt,
                 float* b1_ckpt, float* W2_ckpt, float* b2_ckpt, float* W1_memo, float* b1_memo, float* W2_memo,
-                float* b2_memo, void* stream) {
+                float* b2_memo, void* upd, size_t upd_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
-  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  st = check_mlp(NC, F, FF, dtype);
+  if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
   REQUIRE_PTR(XV);
@@ -192,6 +202,10 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
     for (const float* q : grp) OPTIONAL_PTR(q);
   }
   if (W1_memo != nullptr && (M < 1 || M > NC)) return TTT_ERR_ARG;
+  if (upd != nullptr) {
+    if (!aligned16(upd)) return TTT_ERR_ALIGN;
+    if (upd_bytes < ttt_mlp_upd_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  }
 
   ttt::MlpFwdParams p;
   p.XQ = XQ;
@@ -217,6 +231,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.b1_memo = b1_memo;
   p.W2_memo = W2_memo;
   p.b2_memo = b2_memo;
+  p.upd = upd;
   p.B = B;
   p.H = H;
   p.NC = NC;
@@ -230,27 +245,29 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   return hip_status(ttt::launch_mlp_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
-size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int G, int dtype) {
-  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0 || G <= 0) return 0;
+size_t ttt_mlp_upd_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
-  const int g = G < NC ? G : NC;
-  return (size_t)B * H * g * ttt::mlp_bwd_slot_bytes(F, FF, dtype);
+  return (size_t)B * H * NC * ttt::mlp_upd_slot_bytes(F, FF, dtype);
 }
 
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                 const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
-                const float* b2_ckpt, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
+                const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
+                const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
                 float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
-                float* db2, float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream) {
+                float* db2, float* dln_w, float* dln_b, const void* upd, size_t upd_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
-  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
-  const void* req[] = {XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt, dout,
+  st = check_mlp(NC, F, FF, dtype);
+  if (st != TTT_OK) return st;
+  const void* req[] = {XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt,
+                       W1_last, b1_last, W2_last, b2_last, dout,
                        dXQ, dXK, dXV, deta, dW1, db1, dW2, db2, dln_w, dln_b};
   for (const void* q : req) REQUIRE_PTR(q);
-  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return TTT_ERR_ALIGN;
-  if (workspace_bytes < ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, G, dtype)) return TTT_ERR_WORKSPACE;
+  if (upd == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(upd)) return TTT_ERR_ALIGN;
+  if (upd_bytes < ttt_mlp_upd_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
 
   ttt::MlpBwdParams p;
   p.XQ = XQ;
@@ -264,6 +281,11 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.b1_ckpt = b1_ckpt;
   p.W2_ckpt = W2_ckpt;
   p.b2_ckpt = b2_ckpt;
+  p.W1_last = W1_last;
+  p.b1_last = b1_last;
+  p.W2_last = W2_last;
+  p.b2_last = b2_last;
+  p.upd = upd;
   p.dXQ = dXQ;
   p.dXK = dXK;
   p.dXV = dXV;
@@ -274,7 +296,6 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.db2 = db2;
   p.dln_w = dln_w;
   p.dln_b = dln_b;
-  p.ws = workspace;
   p.B = B;
   p.H = H;
   p.NC = NC;

@@ -12,17 +12,15 @@
 // being processed -- and the biases b1[S], b2.
 //
 // Reverse sweep over checkpoint groups (kernels/mlp_backward.py:340 walks the
-// same groups; the algorithm and data flow here are our own):
-//   pass 1  reload the state entering the group from its checkpoint and run
-//           the group's mini-batches forward (state path only,
-//           ops/ttt_mlp.py:28-52).  For each mini-batch the update operands
-//           -e*G1 and -e*G2 (exactly the values the update MFMAs consume) and
-//           the fp32 bias decrements are written to the per-chain workspace.
-//   pass 2  walk the group backwards.  Mini-batch s first rebuilds the state
-//           entering it from the state after it, W1_s = W1_{s+1} + XK_s^T (e G1_s)
-//           and W2_s = W2_{s+1} + X2_s^T (e G2_s), with the same operands, then
-//           recomputes the mini-batch forward and applies its gradient
-//           (ops/ttt_mlp.py:9-67 differentiated by hand).
+// same groups; the algorithm and data flow here are our own).  A group starts
+// from the state after its last mini-batch: the next group's checkpoint, or
+// the forward's final state for the last group.  Mini-batches are then taken
+// in reverse; mini-batch s first rebuilds the state entering it from the
+// state after it, W1_s = W1_{s+1} + XK_s^T (e G1_s), W2_s = W2_{s+1} +
+// X2_s^T (e G2_s), b_s = b_{s+1} + G_s^T e, with the update operands the
+// forward wrote (exactly the values its update MFMAs consumed), then
+// recomputes the mini-batch forward and applies its gradient
+// (ops/ttt_mlp.py:9-67 differentiated by hand).
 // Row-wise work on [16 x F] tiles (LayerNorms and their backward) is done
 // redundantly by every wave.  Contractions over the hidden units are split by
 // slice; their [16 x F] partials meet in one 32 KB LDS exchange area, so each
@@ -51,16 +49,6 @@ template <int FT, int NW> struct MlpBwdShared {
   float w2t[16 * FT * 64 * NW];  // W2^T [F][FF], swizzled
   MlpBwdExchange<FT, NW> x;
 };
-
-// Per-chain workspace slot for one mini-batch (element type T for operands):
-//   g1e [NW][4][64] x 4 T     -e * G1 as the update MFMA's operand frags
-//   g2e [NW][FT][64] x 4 T    -e * G2 (one copy per wave)
-//   b1d [FF] fp32, b2d [NW][F] fp32   bias decrements
-size_t mlp_bwd_slot_bytes(int F, int FF, int dtype) {
-  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
-  const size_t nw = (size_t)FF / 64;
-  return (FF + nw * F) * 16 * t + (FF + nw * F) * sizeof(float);
-}
 
 template <typename T, int FT, int NW>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
@@ -99,22 +87,25 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   auto xs = [&](int s) { return s * K * F * ST; };
   auto es = [&](int s) { return s * K * K * ST; };
 
-  // workspace slot layout (bytes): g1e [NW][HT][64] x 4T | g2e [NW][FT][64] x 4T | b1d [FF] f32 | b2d [NW][F] f32
-  constexpr int SLOT = (FF + NW * F) * 16 * ST + (FF + NW * F) * 4;
-  constexpr int G2E_OFF = FF * 16 * ST;
-  constexpr int B1D_OFF = (FF + NW * F) * 16 * ST;
-  constexpr int B2D_OFF = B1D_OFF + FF * 4;
-  const rsrc_t rWS = make_rsrc(reinterpret_cast<char*>(p.ws) + (size_t)chain * G * SLOT, (unsigned)(G * SLOT));
+  // update operands of this chain, [NC] slots (MlpUpdSlot layout)
+  using Slot = MlpUpdSlot<F, FF, ST>;
+  const rsrc_t rUP = make_rsrc(static_cast<const char*>(p.upd) + (size_t)chain * NC * Slot::BYTES,
+                               (unsigned)(NC * Slot::BYTES));
   const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST
-  const int g2l = ((wave * FT) * 64 + l) * 4 * ST;  // + c * 256 * ST (+ G2E_OFF)
-  const int b1l = (hs + n) * 4;                     // + 64 * o (+ B1D_OFF)
-  const int b2l = (wave * F + n) * 4;               // + 64 * c (+ B2D_OFF)
+  const int g2l = l * 4 * ST;                       // + c * 256 * ST (+ Slot::G2E)
+  const int b1l = (hs + n) * 4;                     // + 64 * o (+ Slot::B1D)
+  const int b2l = n * 4;                            // + 64 * c (+ Slot::B2D)
 
   // checkpoints [NK][...] of this chain; lane offsets include the wave's slice
   const rsrc_t rW1c = make_rsrc(p.W1_ckpt + (size_t)chain * NK * F * FF, (unsigned)((size_t)NK * F * FF * 4));
   const rsrc_t rW2c = make_rsrc(p.W2_ckpt + (size_t)chain * NK * FF * F, (unsigned)((size_t)NK * FF * F * 4));
   const rsrc_t rB1c = make_rsrc(p.b1_ckpt + (size_t)chain * NK * FF, (unsigned)((size_t)NK * FF * 4));
   const rsrc_t rB2c = make_rsrc(p.b2_ckpt + (size_t)chain * NK * F, (unsigned)((size_t)NK * F * 4));
+  // the forward's final state
+  const rsrc_t rW1l = make_rsrc(p.W1_last + (size_t)chain * F * FF, (unsigned)(F * FF * 4));
+  const rsrc_t rW2l = make_rsrc(p.W2_last + (size_t)chain * FF * F, (unsigned)(FF * F * 4));
+  const rsrc_t rB1l = make_rsrc(p.b1_last + (size_t)chain * FF, (unsigned)(FF * 4));
+  const rsrc_t rB2l = make_rsrc(p.b2_last + (size_t)chain * F, (unsigned)(F * 4));
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
 
@@ -179,145 +170,37 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   for (int kk = NK - 1; kk >= 0; --kk) {
     const int s0 = kk * G, s1 = min(s0 + G, NC);
 
-    // ===================== pass 1: forward over the group, store update operands
+    // ===================== the state after the group's last mini-batch
     {
-      const int ko = kk * F * FF * 4;  // byte offset of checkpoint kk in this chain's slab
+      const bool last = kk + 1 == NK;
+      const rsrc_t r1 = last ? rW1l : rW1c, r2 = last ? rW2l : rW2c;
+      const rsrc_t q1 = last ? rB1l : rB1c, q2 = last ? rB2l : rB2c;
+      const int k1 = last ? 0 : kk + 1;
 #pragma unroll
       for (int i = 0; i < FT; ++i)
 #pragma unroll
-        for (int o = 0; o < HT; ++o) w1_put(i, o, bload_tile(rW1c, w1l, ko, FF, 16 * i, 16 * o));
+        for (int o = 0; o < HT; ++o) w1_put(i, o, bload_tile(r1, w1l, k1 * F * FF * 4, FF, 16 * i, 16 * o));
 #pragma unroll
       for (int i = 0; i < HT; ++i)
 #pragma unroll
-        for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(rW2c, w2l, ko, F, 16 * i, 16 * o));
+        for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(r2, w2l, k1 * F * FF * 4, F, 16 * i, 16 * o));
 #pragma unroll
-      for (int o = 0; o < HT; ++o) b1[o] = bload_f32(rB1c, (hs + n) * 4, (kk * FF + 16 * o) * 4);
+      for (int o = 0; o < HT; ++o) b1[o] = bload_f32(q1, (hs + n) * 4, (k1 * FF + 16 * o) * 4);
 #pragma unroll
-      for (int o = 0; o < FT; ++o) b2[o] = bload_f32(rB2c, n * 4, (kk * F + 16 * o) * 4);
-    }
-    for (int s = s0; s < s1; ++s) {
-      const int i = s - s0;
-      Frag<T> xk[FT], xkTf[FT];
-      f4 tgt[FT];
-#pragma unroll
-      for (int q = 0; q < FT; ++q) {
-        xk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
-        const Tile xkT = transpose16(xk[q], I);
-        xkTf[q] = to_frag<T>(xkT.v);
-        tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - xkT.v;
-      }
-      // Z1 = XK W1 + b1 (token-major, this slice), X2 = gelu(Z1)
-      Frag<T> x2f[HT], x2F[HT];
-      f4 gp[HT];
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        Tile z1;
-        z1.v = f4{b1[o], b1[o], b1[o], b1[o]};
-#pragma unroll
-        for (int q = 0; q < FT; q += 2)
-          mma32(z1.v, xk[q], xk[q + 1], to_frag<T>(w1_tile(q, o).v), to_frag<T>(w1_tile(q + 1, o).v));
-        f4 x2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          x2[j] = gelu_tanh(z1.v[j]);
-          gp[o][j] = gelu_bwd(z1.v[j]);
-        }
-        x2f[o] = to_frag<T>(x2);
-        x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
-      }
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        f4 z = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; o += 2)
-          mma32(z, x2F[o], x2F[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
-        sh.x.a.part[wave][c][l] = z;
-      }
-      __syncthreads();  // Z2 partials in
-      Tile G2[FT];
-      {
-        Tile z2[FT];
-#pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          z2[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
-#pragma unroll
-          for (int w = 0; w < NW; ++w) z2[c].v += sh.x.a.part[w][c][l];
-        }
-        __syncthreads();  // partial buffer free
-        LnL2Lite<FT> ln;
-        ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
-      }
-      // G1 = (G2 W2^T) (.) gelu'(Z1)
-      Tile G1[HT];
-      {
-        Frag<T> g2F[FT];
-#pragma unroll
-        for (int c = 0; c < FT; ++c) g2F[c] = to_frag<T>(transpose16(to_frag<T>(G2[c].v), I).v);
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          G1[o].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < FT; c += 2) mma32(G1[o].v, g2F[c], g2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-          G1[o].v *= gp[o];
-        }
-      }
-      // update operands and bias decrements: store them, then apply the update
-      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        f4 v;
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = -e[j] * G1[o].v[j];
-          acc += e[j] * G1[o].v[j];
-        }
-        const Frag<T> g1e = to_frag<T>(v);
-        const float d = sum_col4(acc);
-        b1[o] -= d;
-        bstore_frag<T>(rWS, g1l + o * 256 * ST, i * SLOT, g1e);
-        if (g == 0) bstore_f32(rWS, b1l + 64 * o, i * SLOT + B1D_OFF, d);
-#pragma unroll
-        for (int q = 0; q < FT; ++q) {
-          Tile w = w1_tile(q, o);
-          mma16(w.v, xkTf[q], g1e);
-          w1_put(q, o, w);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        f4 v;
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = -e[j] * G2[c].v[j];
-          acc += e[j] * G2[c].v[j];
-        }
-        const Frag<T> g2e = to_frag<T>(v);
-        const float d = sum_col4(acc);
-        b2[c] -= d;
-        bstore_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF, g2e);
-        if (g == 0) bstore_f32(rWS, b2l + 64 * c, i * SLOT + B2D_OFF, d);
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          Tile w = w2_tile(o, c);
-          mma16(w.v, x2f[o], g2e);
-          w2_put(o, c, w);
-        }
-      }
+      for (int o = 0; o < FT; ++o) b2[o] = bload_f32(q2, n * 4, (k1 * F + 16 * o) * 4);
     }
 
-    // ===================== pass 2: reverse through the group
+    // ===================== reverse through the group
     // Regions between barriers:   R1-R2 | R3 | R4-B1 | B2 | B3
     // exchange area:              Z2 partials; Z2b, A2 partials; dG2, dN1, de
     //                             partials; dXQ, dXK partials
     for (int s = s1 - 1; s >= s0; --s) {
-      const int i = s - s0;
+      const int us = s * Slot::BYTES;
       pin_dW();
 
       Frag<T> g1e[HT];
 #pragma unroll
-      for (int o = 0; o < HT; ++o) g1e[o] = bload_frag<T>(rWS, g1l + o * 256 * ST, i * SLOT);
+      for (int o = 0; o < HT; ++o) g1e[o] = bload_frag<T>(rUP, g1l + o * 256 * ST, us + Slot::G1E);
       Frag<T> xk[FT], xkTf[FT], xqTf[FT];
       f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
       Tile z1[HT], zq[HT];
@@ -338,7 +221,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         // ---- R1: rebuild W1_s (this slice) and use it at once for
         //      Z1 = XK W1 + b1 and Zq = XQ W1 + b1
 #pragma unroll
-        for (int o = 0; o < HT; ++o) b1[o] += bload_f32(rWS, b1l + 64 * o, i * SLOT + B1D_OFF);
+        for (int o = 0; o < HT; ++o) b1[o] += bload_f32(rUP, b1l + 64 * o, us + Slot::B1D);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
           z1[o].v = f4{b1[o], b1[o], b1[o], b1[o]};
@@ -368,10 +251,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       // ---- R2: rebuild W2_s and b2_s, and the Z2 partial over this slice with it
 #pragma unroll
-      for (int c = 0; c < FT; ++c) b2[c] += bload_f32(rWS, b2l + 64 * c, i * SLOT + B2D_OFF);
+      for (int c = 0; c < FT; ++c) b2[c] += bload_f32(rUP, b2l + 64 * c, us + Slot::B2D);
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        const Frag<T> ng = negate(bload_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF));
+        const Frag<T> ng = negate(bload_frag<T>(rUP, g2l + c * 256 * ST, us + Slot::G2E));
         f4 z = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int o = 0; o < HT; o += 2) {
@@ -655,7 +538,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           Frag<T> eg2F[FT];
 #pragma unroll
           for (int c = 0; c < FT; ++c)
-            eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rWS, g2l + c * 256 * ST, i * SLOT + G2E_OFF), I).v);
+            eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rUP, g2l + c * 256 * ST, us + Slot::G2E), I).v);
 #pragma unroll
           for (int o = 0; o < HT; ++o)
 #pragma unroll

@@ -17,11 +17,26 @@
 //
 // Checkpoints hold the state entering mini-batch k*G
 // (kernels/mlp_forward.py:84-117); memo snapshot s holds the state after
-// mini-batch s*M is applied (kernels/mlp_forward.py:193-226).
+// mini-batch s*M is applied (kernels/mlp_forward.py:193-226).  When `upd` is
+// given, the update operands -e*G1, -e*G2 and the bias decrements of every
+// mini-batch are written there (MlpUpdSlot layout): the backward rebuilds the
+// state of each mini-batch in reverse from them instead of re-running the
+// forward from a checkpoint.
+//
+// Slabs are read through buffer resources; the next mini-batch's XQ and XK
+// are requested right after the first barrier of the current one, before its
+// stores (gfx9 retires loads and stores in issue order), so they arrive while
+// the rest of the mini-batch computes.
+#include "ttt_buf.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
 namespace ttt {
+
+size_t mlp_upd_slot_bytes(int F, int FF, int dtype) {
+  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
+  return (size_t)(FF + F) * 16 * t + (size_t)(FF + F) * sizeof(float);
+}
 
 template <int FT, int NW> struct MlpFwdShared {
   f4 z2p[NW][FT][64];   // per-wave partial Z2 (token-major tiles, register order)
@@ -35,36 +50,51 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   constexpr int K = 16;
   constexpr int HT = 4;  // hidden tiles per wave
   constexpr int FF = 64 * NW;
+  constexpr int ST = (int)sizeof(T);
+  using Slot = MlpUpdSlot<F, FF, ST>;
   __shared__ MlpFwdShared<FT, NW> sh;
 
   const int chain = blockIdx.x;
   const int h = chain % p.H;
   const int NC = p.NC;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int l = lane_id(), g = l >> 4, n = l & 15;
   const int hs = 64 * wave;  // first hidden unit of this wave
 
+  // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
-  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
-  const T* __restrict__ XK = static_cast<const T*>(p.XK) + xoff;
-  const T* __restrict__ XV = static_cast<const T*>(p.XV) + xoff;
-  const T* __restrict__ ETA = static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
-  T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
+  const size_t eoff = (size_t)chain * NC * K * K;
+  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * ST);
+  const rsrc_t rXQ = make_rsrc(static_cast<const T*>(p.XQ) + xoff, xbytes);
+  const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
+  const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
+  const rsrc_t rET = make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+  const rsrc_t rOUT = make_rsrc(static_cast<T*>(p.out) + xoff, xbytes);
+  const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
+  const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
+  const int e4 = ((K - 1) * K + 4 * g) * ST;  // eta[K-1][4g .. 4g+3]
+  const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
+  const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
+  const bool want_upd = p.upd != nullptr;
+  const rsrc_t rUP = make_rsrc(want_upd ? static_cast<char*>(p.upd) + (size_t)chain * NC * Slot::BYTES : nullptr,
+                               want_upd ? (unsigned)(NC * Slot::BYTES) : 0u);
+  const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST
+  const int g2l = l * 4 * ST;                       // + c * 256 * ST + Slot::G2E
 
   // state slice: W1[:, hs:hs+64] as tiles [f block][hidden block], W2[hs:hs+64, :]
   Tile W1[FT][HT], W2[HT][FT];
   float b1_tm[HT], b2_tm[FT];
   {
-    const float* w1 = p.W1_init + (size_t)chain * F * FF;
-    const float* w2 = p.W2_init + (size_t)chain * FF * F;
+    const rsrc_t r1 = make_rsrc(p.W1_init + (size_t)chain * F * FF, F * FF * 4);
+    const rsrc_t r2 = make_rsrc(p.W2_init + (size_t)chain * FF * F, FF * F * 4);
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < HT; ++o) W1[i][o] = load_tile(w1, FF, 16 * i, hs + 16 * o);
+      for (int o = 0; o < HT; ++o) W1[i][o] = bload_tile(r1, w1l, 0, FF, 16 * i, 16 * o);
 #pragma unroll
     for (int i = 0; i < HT; ++i)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) W2[i][o] = load_tile(w2, F, hs + 16 * i, 16 * o);
+      for (int o = 0; o < FT; ++o) W2[i][o] = bload_tile(r2, w2l, 0, F, 16 * i, 16 * o);
 #pragma unroll
     for (int o = 0; o < HT; ++o) b1_tm[o] = p.b1_init[(size_t)chain * FF + hs + 16 * o + n];
 #pragma unroll
@@ -80,14 +110,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const Frag<T> I = identity_frag<T>();
 
   auto store_state = [&](float* w1d, float* b1d, float* w2d, float* b2d) {
+    const rsrc_t r1 = make_rsrc(w1d, F * FF * 4), r2 = make_rsrc(w2d, FF * F * 4);
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < HT; ++o) store_tile(w1d, FF, 16 * i, hs + 16 * o, W1[i][o]);
+      for (int o = 0; o < HT; ++o) bstore_tile(r1, w1l, 0, FF, 16 * i, 16 * o, W1[i][o]);
 #pragma unroll
     for (int i = 0; i < HT; ++i)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) store_tile(w2d, F, hs + 16 * i, 16 * o, W2[i][o]);
+      for (int o = 0; o < FT; ++o) bstore_tile(r2, w2l, 0, F, 16 * i, 16 * o, W2[i][o]);
     if (g == 0) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) b1d[hs + 16 * o + n] = b1_tm[o];
@@ -98,19 +129,25 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     }
   };
 
+  // XQ, XK of the current mini-batch (frags: free = token, k = feature)
+  Frag<T> xq[1][FT], xk[1][FT];
+#pragma unroll
+  for (int q = 0; q < FT; ++q) {
+    xq[0][q] = bload_frag<T>(rXQ, xl + 16 * q * ST, 0);
+    xk[0][q] = bload_frag<T>(rXK, xl + 16 * q * ST, 0);
+  }
+
   for (int s = 0; s < NC; ++s) {
     if (p.W1_ckpt != nullptr && (s % p.G) == 0) {
       const size_t k = (size_t)chain * p.NK + s / p.G;
       store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt + k * FF, p.W2_ckpt + k * FF * F, p.b2_ckpt + k * F);
     }
-    const size_t xo = (size_t)s * K * F;
-    const T* etas = ETA + (size_t)s * K * K;
-    Frag<T> xq[1][FT], xk[1][FT];
+    const int xo = s * K * F * ST, eo = s * K * K * ST;
+    Frag<T> xv[FT];
 #pragma unroll
-    for (int q = 0; q < FT; ++q) {
-      xq[0][q] = load_frag(XQ + xo, F, 16 * q);
-      xk[0][q] = load_frag(XK + xo, F, 16 * q);
-    }
+    for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
+    const Frag<T> etaTf = bload_frag<T>(rET, el, eo);  // [t_k x t_q]: eta[n][4g+j]
+    const Frag<T> ef = bload_frag<T>(rET, e4, eo);     // last eta row
 
     // ---- layer 1 on this wave's hidden units (token-major)
     Frag<T> x2f[HT];     // token-major frags of X2 (free = hidden, k = t)
@@ -126,8 +163,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         f4 x2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          x2[j] = gelu_tanh(z1[0][o].v[j]);
-          gp[o][j] = gelu_bwd(z1[0][o].v[j]);
+          float y, dy;
+          gelu_fwd_bwd(z1[0][o].v[j], y, dy);
+          x2[j] = y;
+          gp[o][j] = dy;
         }
         x2f[o] = to_frag<T>(x2);
         x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
@@ -143,6 +182,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     }
     __syncthreads();
 
+    // next mini-batch's XQ, XK (the last mini-batch re-reads its own)
+    Frag<T> xqn[FT], xkn[FT];
+    {
+      const int xn = min(s + 1, NC - 1) * K * F * ST;
+#pragma unroll
+      for (int q = 0; q < FT; ++q) {
+        xqn[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xn);
+        xkn[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xn);
+      }
+    }
+
     // ---- Z2 and its inner-loss gradient (every wave, identical)
     Frag<T> xkTf[FT];
     Tile G2[FT];
@@ -152,7 +202,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       for (int q = 0; q < FT; ++q) {
         const Tile xkT = transpose16(xk[0][q], I);
         xkTf[q] = to_frag<T>(xkT.v);
-        tgt[q] = transpose16(load_frag(XV + xo, F, 16 * q), I).v - xkT.v;
+        tgt[q] = transpose16(xv[q], I).v - xkT.v;
       }
       Tile z2[FT];
 #pragma unroll
@@ -161,7 +211,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) z2[o].v += sh.z2p[w][o][l];
       }
-      LnL2TM<FT> ln;
+      LnL2Lite<FT> ln;
       ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
     }
 
@@ -185,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     }
 
     // ---- readout layer 1: Z1b = XQ W1 - (eta o A1 + eta) G1 + b1, X2b = gelu(Z1b)
-    const f4 etaT = load_f4(etas, K, 0);  // [t_k x t_q]: eta[n][4g+j]
+    const f4 etaT = frag_to_f4(etaTf);
     Frag<T> x2bF[1][HT];
     {
       Tile at[1][1];
@@ -219,13 +269,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       for (int o = 0; o < FT; ++o) sh.z2bp[wave][o][l] = z2bp[0][o].v;
       sh.a2p[wave][l] = a2p[0][0].v;
     }
-    const f4 e = load4(etas + (K - 1) * K + 4 * g);
+    const f4 e = frag_to_f4(ef);
 
     // ---- state update (the readout above used the state entering s)
     float b2_old[FT];
 #pragma unroll
     for (int o = 0; o < FT; ++o) b2_old[o] = b2_tm[o];
     {
+      const int us = s * Slot::BYTES;
       Frag<T> g1e[HT], g2e[FT];
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
@@ -237,7 +288,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           acc += e[j] * G1[o].v[j];
         }
         g1e[o] = to_frag<T>(v);
-        b1_tm[o] -= sum_col4(acc);
+        const float d = sum_col4(acc);
+        b1_tm[o] -= d;
+        if (want_upd) {
+          bstore_frag<T>(rUP, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
+          if (g == 0) bstore_f32(rUP, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);
+        }
       }
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
@@ -249,7 +305,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           acc += e[j] * G2[o].v[j];
         }
         g2e[o] = to_frag<T>(v);
-        b2_tm[o] -= sum_col4(acc);
+        const float d = sum_col4(acc);
+        b2_tm[o] -= d;
+        if (want_upd && wave == 0) {
+          bstore_frag<T>(rUP, g2l + o * 256 * ST, us + Slot::G2E, g2e[o]);
+          if (g == 0) bstore_f32(rUP, n * 4 + 64 * o, us + Slot::B2D, d);
+        }
       }
 #pragma unroll
       for (int i = 0; i < FT; ++i)
@@ -300,19 +361,25 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         }
         rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
-      T* o_s = OUT + xo;
-      for (int o = wave; o < FT; o += NW) {
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        if (o % NW != wave) continue;  // static indices keep these arrays in registers
         const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
         f4 y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) y[j] = q[j] + lnw_tm[o] * ((z2b[o].v[j] - mu[j]) * rs[j]) + lnb_tm[o];
-        store_f4(o_s, F, 16 * o, transpose16(to_frag<T>(y), I).v);
+        bstore_frag<T>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
       }
     }
 
     if (p.W1_memo != nullptr && (s % p.M) == 0) {
       const size_t k = (size_t)chain * p.NS + s / p.M;
       store_state(p.W1_memo + k * F * FF, p.b1_memo + k * FF, p.W2_memo + k * FF * F, p.b2_memo + k * F);
+    }
+#pragma unroll
+    for (int q = 0; q < FT; ++q) {
+      xq[0][q] = xqn[q];
+      xk[0][q] = xkn[q];
     }
   }
 
@@ -324,6 +391,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 
 template <typename T, int FT, int NW>
 static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
+  static_assert(MlpUpdSlot<16 * FT, 64 * NW, (int)sizeof(T)>::BYTES ==
+                    (64 * NW + 16 * FT) * 16 * (int)sizeof(T) + (64 * NW + 16 * FT) * 4,
+                "update slot layout");
   hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }

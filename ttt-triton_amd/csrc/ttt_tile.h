@@ -340,6 +340,12 @@ __device__ __forceinline__ float gelu_bwd(float x) {
   const float t = tanh_f(0.79788456f * x * (1.0f + 0.044715f * x * x));
   return 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
 }
+// gelu_tanh(x) and gelu_bwd(x) from one tanh evaluation
+__device__ __forceinline__ void gelu_fwd_bwd(float x, float& y, float& dy) {
+  const float t = tanh_f(0.79788456f * x * (1.0f + 0.044715f * x * x));
+  y = 0.5f * x * (1.0f + t);
+  dy = 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
+}
 // d/dx of gelu_bwd above, differentiating the same expression:
 //   gelu_bwd = 0.5 x s D + 0.5 (1 + t),  t = tanh(u), u = k x (1 + c x^2),
 //   s = 1 - t^2, D = k + c3 x^2, du/dx = k (1 + 3 c x^2)
