@@ -124,21 +124,21 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
   // LDS state accessors (this wave's hidden columns only)
-  const LdsMat<FF> W1s{sh.w1}, W2t{sh.w2t};
+  LdsMat<FF> W1s(sh.w1, hs), W2t(sh.w2t, hs);
   // W1 tile [F block kb x hidden block o]: frag (free = hidden, k = feature)
-  auto w1_tile = [&](int kb, int o) { return W1s.tile(16 * kb, hs + 16 * o); };
-  auto w1_put = [&](int kb, int o, Tile t) { W1s.put_tile(16 * kb, hs + 16 * o, t); };
+  auto w1_tile = [&](int kb, int o) { return W1s.tile(16 * kb, 16 * o); };
+  auto w1_put = [&](int kb, int o, Tile t) { W1s.put_tile(16 * kb, 16 * o, t); };
   // W1^T frag (free = feature block f, k = hidden block c)
-  auto w1T_frag = [&](int f, int c) { return to_frag<T>(W1s.row4(16 * f, hs + 16 * c)); };
+  auto w1T_frag = [&](int f, int c) { return to_frag<T>(W1s.row4(16 * f, 16 * c)); };
   // W2 tile [hidden block o x F block c] (C layout): frag (free = feature, k = hidden)
   auto w2_tile = [&](int o, int c) {
     Tile t;
-    t.v = W2t.row4(16 * c, hs + 16 * o);
+    t.v = W2t.row4(16 * c, 16 * o);
     return t;
   };
-  auto w2_put = [&](int o, int c, Tile t) { W2t.put_row4(16 * c, hs + 16 * o, t.v); };
+  auto w2_put = [&](int o, int c, Tile t) { W2t.put_row4(16 * c, 16 * o, t.v); };
   // W2^T frag (free = hidden block o, k = feature block c)
-  auto w2T_frag = [&](int o, int c) { return to_frag<T>(W2t.tile(16 * c, hs + 16 * o).v); };
+  auto w2T_frag = [&](int o, int c) { return to_frag<T>(W2t.tile(16 * c, 16 * o).v); };
   // keep the gradient accumulators in the MFMA accumulator registers
   auto pin_dW = [&]() {
 #pragma unroll
@@ -197,6 +197,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     for (int s = s1 - 1; s >= s0; --s) {
       const int us = s * Slot::BYTES;
       pin_dW();
+      W1s.pin();
+      W2t.pin();
 
       Frag<T> g1e[HT];
 #pragma unroll

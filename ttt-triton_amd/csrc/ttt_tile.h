@@ -277,33 +277,66 @@ __device__ __forceinline__ void store_tile(float* __restrict__ x, int ld, int r0
 }
 
 // fp32 matrix [rows][COLS] in LDS with columns XOR-swizzled by 4 * (row & 7):
-// a C-layout tile (lanes of group g read rows 4g + j, 16 consecutive columns)
+// element (row, col) lives at row * COLS + (col ^ ((row & 7) << 2)).  A
+// C-layout tile (lanes of group g read rows 4g + j, 16 consecutive columns)
 // and a row-vector frag (lanes of group g read 4 consecutive columns of 16
 // rows) are both bank-conflict free with no padding.  COLS % 32 == 0.
+//
+// A view fixes a uniform column offset cw (a multiple of 32) and computes each
+// lane's share of every address once.  For row offsets r0 % 8 == 0 (% 16 for
+// row vectors) and column offsets c0 % 16 == 0 relative to cw, the swizzled
+// address splits into one of ten lane base addresses plus the constant
+// (r0 * COLS + (c0 & ~16)) * 4, which the LDS instruction's 16-bit immediate
+// offset absorbs (rows * COLS * 4 <= 64 KB).  `pin()` makes the bases opaque
+// to the optimiser; called once per loop iteration it keeps the compiler from
+// hoisting every base + constant sum out of the loop into its own register.
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) f4 lds_f4;
+
 template <int COLS> struct LdsMat {
-  float* p;
-  __device__ __forceinline__ static int idx(int row, int col) { return row * COLS + (col ^ ((row & 7) << 2)); }
-  // C-layout tile at (r0, c0): lane (g, n) holds M[r0 + 4g + j][c0 + n]
-  __device__ __forceinline__ Tile tile(int r0, int c0) const {
+  unsigned tb[2][4];  // tile lane base addresses by bit 4 of c0 and row j
+  unsigned rb[2];     // row-vector lane base addresses by bit 4 of c0
+  __device__ __forceinline__ LdsMat(float* base, int cw) {
+    const unsigned p = (unsigned)(uintptr_t)(lds_f32*)base;
     const int l = lane_id(), g = l >> 4, n = l & 15;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        tb[b][j] = p + 4u * ((4 * g + j) * COLS + cw + 16 * (b ^ (g & 1)) + (n ^ (4 * j)));
+      rb[b] = p + 4u * (n * COLS + cw + 16 * (b ^ ((n >> 2) & 1)) + ((4 * g) ^ ((n & 3) << 2)));
+    }
+  }
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(tb[b][j]));
+      asm volatile("" : "+v"(rb[b]));
+    }
+  }
+  __device__ __forceinline__ static lds_f32* at(unsigned a) { return (lds_f32*)(uintptr_t)a; }
+  // C-layout tile at (r0, cw + c0): lane (g, n) holds M[r0 + 4g + j][cw + c0 + n]
+  __device__ __forceinline__ Tile tile(int r0, int c0) const {
+    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
     Tile t;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) t.v[j] = p[idx(r0 + 4 * g + j, c0 + n)];
+    for (int j = 0; j < 4; ++j) t.v[j] = at(tb[b][j])[k];
     return t;
   }
   __device__ __forceinline__ void put_tile(int r0, int c0, Tile t) const {
-    const int l = lane_id(), g = l >> 4, n = l & 15;
+    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[idx(r0 + 4 * g + j, c0 + n)] = t.v[j];
+    for (int j = 0; j < 4; ++j) at(tb[b][j])[k] = t.v[j];
   }
-  // row-vector frag at (r0, c0): lane (g, r) holds M[r0 + r][c0 + 4g + j]
+  // row-vector frag at (r0, cw + c0): lane (g, r) holds M[r0 + r][cw + c0 + 4g + j]
   __device__ __forceinline__ f4 row4(int r0, int c0) const {
-    const int l = lane_id(), g = l >> 4, r = l & 15;
-    return *reinterpret_cast<const f4*>(p + idx(r0 + r, c0 + 4 * g));
+    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
+    return *reinterpret_cast<lds_f4*>(at(rb[b]) + k);
   }
   __device__ __forceinline__ void put_row4(int r0, int c0, f4 v) const {
-    const int l = lane_id(), g = l >> 4, r = l & 15;
-    *reinterpret_cast<f4*>(p + idx(r0 + r, c0 + 4 * g)) = v;
+    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
+    *reinterpret_cast<lds_f4*>(at(rb[b]) + k) = v;
   }
 };
 
