@@ -182,9 +182,9 @@ def run_mlp(torch, O, steps, warmup, only=None):
     keys = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
 
     def fwd():
-        out, ck, _, last, upd = mlp_forward(*(g[k] for k in keys), G_MLP, want_ckpt=True, want_last=True,
-                                            want_upd=True)
-        return out, (ck, last, upd)
+        out, ck, _, last, saved = mlp_forward(*(g[k] for k in keys), G_MLP, want_ckpt=True, want_last=True,
+                                              want_saved=True)
+        return out, (ck, last, saved)
 
     def bwd(saved):
         return mlp_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], *saved, g["dOut"], G_MLP)

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 2
+#define TTT_AMD_ABI_VERSION 3
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -94,12 +94,13 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
  *   *_ckpt            [B,H,NK,...] state entering mini-batch k*G (all four or none)
  *   *_memo            [B,H,NS,...], NS = ceil(NC/M): state after mini-batch
  *                     s*M has been applied (all four or none; M >= 1 then)
- *   upd               NULL, or >= ttt_mlp_upd_bytes(...) bytes: receives every
- *                     mini-batch's state-update operands for ttt_mlp_bwd.  It
- *                     has no counterpart in the reference, whose backward
- *                     re-runs each checkpoint group forward to recover them.
+ *   saved             NULL, or >= ttt_mlp_saved_bytes(...) bytes: receives, for
+ *                     every mini-batch, the state-update operands and the
+ *                     activations ttt_mlp_bwd needs.  It has no counterpart in
+ *                     the reference, whose backward re-runs each checkpoint
+ *                     group forward to recover them.
  * Per-chain slabs are addressed with 32-bit offsets: NC * F * FF * 4 and NC
- * times the per-mini-batch update size must stay below 2^31 bytes. */
+ * times the per-mini-batch saved size must stay below 2^31 bytes. */
 int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
                 const float* W2_init, const float* b2_init,
@@ -107,11 +108,11 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last,
                 float* W1_ckpt, float* b1_ckpt, float* W2_ckpt, float* b2_ckpt,
                 float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo,
-                void* upd, size_t upd_bytes, void* stream);
+                void* saved, size_t saved_bytes, void* stream);
 
-/* Bytes of the update-operand buffer of ttt_mlp_fwd / ttt_mlp_bwd:
- * B*H*NC mini-batches x ((FF + F) * K * sizeof(dtype) + (FF + F) * 4). */
-size_t ttt_mlp_upd_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
+/* Bytes of the saved buffer of ttt_mlp_fwd / ttt_mlp_bwd: B*H*NC mini-batches
+ * x ((5 FF + F) * K * sizeof(dtype) + (FF + F) * 4 + 3 * F * 64 + 4096). */
+size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
  * state's gradient zero, as in the ops path).  Replaces ttt_mlp_scan_backward
@@ -123,15 +124,15 @@ size_t ttt_mlp_upd_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
  *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
  *   dW1, db1, dW2, db2  fp32, shapes of W1_init ... (gradient wrt the initial state)
  *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
- *   upd              the update operands written by that ttt_mlp_fwd call
- *                    (upd_bytes >= ttt_mlp_upd_bytes(...)) */
+ *   saved            the saved buffer written by that ttt_mlp_fwd call
+ *                    (saved_bytes >= ttt_mlp_saved_bytes(...)) */
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
                 const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,
                 const float* W2_last, const float* b2_last, const void* dout,
                 int B, int H, int NC, int K, int F, int FF, int G, int dtype, float eps,
                 void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
-                float* dln_w, float* dln_b, const void* upd, size_t upd_bytes, void* stream);
+                float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream);
 
 /* Fixed-weight TTT-MLP readout over a segment of NS mini-batches:
  *   out = XQ + LN_eps(gelu(XQ W1 + b1) W2 + b2)   (no state update)

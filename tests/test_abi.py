@@ -38,7 +38,7 @@ def lib():
 def test_header_declares_the_abi():
     decls = _declarations()
     for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
-                 "ttt_linear_bwd_workspace_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_upd_bytes",
+                 "ttt_linear_bwd_workspace_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
                  "ttt_mlp_cached_readout"):
         assert name in decls, name
 
@@ -97,9 +97,9 @@ def test_linear_bwd_workspace(lib):
     assert lib.ttt_linear_bwd(*bad, P, need, None) == E_NULL
 
 
-def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, upd=None, upd_bytes=0, NC=16, **kw):
+def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, saved=None, saved_bytes=0, NC=16, **kw):
     a = ([P] * 10 + [2, 4, NC, 16, 64, FF, 4, M, kw.get("dtype", BF16), 1e-8, P] + [None] * 8 + list(memo)
-         + [upd, upd_bytes, None])
+         + [saved, saved_bytes, None])
     return lib.ttt_mlp_fwd(*a)
 
 
@@ -111,23 +111,25 @@ def test_mlp_fwd_validation(lib):
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=0) == E_ARG
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=17) == E_ARG
     assert _mlp_fwd(lib, memo=(P, P, Q, P), M=2) == E_ALIGN
-    need = lib.ttt_mlp_upd_bytes(2, 4, 16, 16, 64, 256, BF16)
-    assert _mlp_fwd(lib, upd=P, upd_bytes=need - 1) == E_WS
-    assert _mlp_fwd(lib, upd=Q, upd_bytes=need) == E_ALIGN
+    need = lib.ttt_mlp_saved_bytes(2, 4, 16, 16, 64, 256, BF16)
+    assert _mlp_fwd(lib, saved=P, saved_bytes=need - 1) == E_WS
+    assert _mlp_fwd(lib, saved=Q, saved_bytes=need) == E_ALIGN
     # per-chain slabs must stay addressable with 31-bit byte offsets
     assert _mlp_fwd(lib, NC=40000) == E_SHAPE
 
 
-def test_mlp_update_operand_buffer(lib):
+def test_mlp_saved_buffer(lib):
     B, H, NC, K, F, FF, G = 2, 4, 16, 16, 64, 256, 8
-    n16 = lib.ttt_mlp_upd_bytes(B, H, NC, K, F, FF, BF16)
-    n32 = lib.ttt_mlp_upd_bytes(B, H, NC, K, F, FF, F32)
-    # per mini-batch: the update operands -e*G1 [K x FF] and -e*G2 [K x F] in
-    # the activation type, and their fp32 bias decrements
-    assert n16 == B * H * NC * ((FF + F) * K * 2 + (FF + F) * 4)
-    assert n32 == B * H * NC * ((FF + F) * K * 4 + (FF + F) * 4)
-    assert lib.ttt_mlp_upd_bytes(B, H, NC, K, F, FF, 9) == 0
-    assert lib.ttt_mlp_upd_bytes(0, H, NC, K, F, FF, BF16) == 0
+    n16 = lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, BF16)
+    n32 = lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, F32)
+    # per mini-batch: the update operands -e*G1 [K x FF] and -e*G2 [K x F] and
+    # the activations Z1, X2, Z1b, G2 W2^T [K x FF] in the activation type; the
+    # fp32 bias decrements, G2 and the two normalised [K x F] rows; four
+    # [K x K]-sized fp32 blocks (row statistics, X2b X2^T)
+    for n, st in ((n16, 2), (n32, 4)):
+        assert n == B * H * NC * ((5 * FF + F) * K * st + (FF + F) * 4 + 3 * K * F * 4 + 4 * 1024)
+    assert lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, 9) == 0
+    assert lib.ttt_mlp_saved_bytes(0, H, NC, K, F, FF, BF16) == 0
     args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
     assert lib.ttt_mlp_bwd(*args, P, n16 - 1, None) == E_WS
     assert lib.ttt_mlp_bwd(*args, None, n16, None) == E_WS

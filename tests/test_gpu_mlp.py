@@ -27,11 +27,11 @@ def _say(*a):
 KEYS = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
 
 
-def _fwd(d, G, M=0, want_upd=True):
-    """(out, ckpt, memo, last, upd) of the HIP forward"""
+def _fwd(d, G, M=0, want_saved=True):
+    """(out, ckpt, memo, last, saved) of the HIP forward"""
     from ttt_amd.mlp import mlp_forward
     g = to_dev(d)
-    return mlp_forward(*(g[k] for k in KEYS), G, M=M, want_ckpt=True, want_last=True, want_upd=want_upd)
+    return mlp_forward(*(g[k] for k in KEYS), G, M=M, want_ckpt=True, want_last=True, want_saved=want_saved)
 
 
 def _perturb(d, H, F_, FF, seed):
@@ -86,38 +86,48 @@ def test_mlp_fwd_headdim32():
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_mlp_fwd_update_operands(dt):
-    """The update-operand buffer leaves every forward output unchanged, and its
-    bias decrements add up to the bias change over the sequence:
-    b_init - sum_s b_dec[s] = b_last."""
-    _say("mlp fwd update operands", dt)
+def test_mlp_fwd_saved_buffer(dt):
+    """Saving for the backward leaves every forward output unchanged; the saved
+    bias decrements add up to the bias change over the sequence,
+    b_init - sum_s b_dec[s] = b_last; the saved X2 is gelu of the saved Z1."""
+    _say("mlp fwd saved buffer", dt)
     B, H, NC, F_, FF = 2, 2, 7, 64, 128
     d = _perturb(O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=11, dtype=dt), H, F_, FF, 12)
-    out0, ck0, _, last0, none = _fwd(d, G=3, want_upd=False)
-    out1, ck1, _, last1, upd = _fwd(d, G=3)
+    out0, ck0, _, last0, none = _fwd(d, G=3, want_saved=False)
+    out1, ck1, _, last1, saved = _fwd(d, G=3)
     assert none is None
     assert torch.equal(out0, out1)
     for a, b in zip(ck0 + last0, ck1 + last1):
         assert torch.equal(a, b)
     st = 2 if dt == torch.bfloat16 else 4
-    slot = (FF + F_) * 16 * st + (FF + F_) * 4
-    assert upd.numel() == B * H * NC * slot
-    u = upd.view(B * H, NC, slot)
+    slot = (5 * FF + F_) * 16 * st + (FF + F_) * 4 + 3 * F_ * 64 + 4096
+    assert saved.numel() == B * H * NC * slot
+    u = saved.view(B * H, NC, slot)
     b1d = u[:, :, (FF + F_) * 16 * st:(FF + F_) * 16 * st + FF * 4].contiguous().view(torch.float32)
-    b2d = u[:, :, (FF + F_) * 16 * st + FF * 4:].contiguous().view(torch.float32)
+    b2d = u[:, :, (FF + F_) * 16 * st + FF * 4:(FF + F_) * 16 * st + (FF + F_) * 4].contiguous().view(torch.float32)
     g = to_dev(d)
     b1 = g["b1"].reshape(B * H, FF) - b1d.sum(1)
     b2 = g["b2"].reshape(B * H, F_) - b2d.sum(1)
     assert max_abs(b1, last1[1].reshape(B * H, FF)) <= 1e-5 * max(1.0, float(b1.abs().max()))
     assert max_abs(b2, last1[3].reshape(B * H, F_)) <= 1e-5 * max(1.0, float(b2.abs().max()))
+    # Z1 and X2 of the slice of wave w, tile o, lane l sit at the same place in
+    # their two regions (lane order, 4 values per lane): X2 = gelu_tanh(Z1)
+    z1o = (FF + F_) * 16 * st + (FF + F_) * 4
+    x2o = z1o + 3 * FF * 16 * st
+    dt_ = torch.bfloat16 if st == 2 else torch.float32
+    z1 = u[:, :, z1o:z1o + FF * 16 * st].contiguous().view(dt_).float()
+    x2 = u[:, :, x2o:x2o + FF * 16 * st].contiguous().view(dt_).float()
+    ref = torch.nn.functional.gelu(z1, approximate="tanh")
+    tol = 2e-2 if st == 2 else 1e-5
+    assert float((x2 - ref).abs().max()) <= tol * max(1.0, float(ref.abs().max()))
 
 
 def _bwd(d, G):
     from ttt_amd.mlp import mlp_backward
     g = to_dev(d)
-    out, ck, _, last, upd = _fwd(d, G)
+    out, ck, _, last, saved = _fwd(d, G)
     (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
-        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, upd, g["dOut"], G)
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
     return dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2, dln_w=dlw, dln_b=dlb)
 
 

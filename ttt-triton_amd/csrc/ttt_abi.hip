@@ -38,7 +38,7 @@ int hip_status(hipError_t e) { return e == hipSuccess ? TTT_OK : TTT_ERR_HIP; }
 int check_mlp(int NC, int F, int FF, int dtype) {
   if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
   if ((long long)NC * F * FF * 4 > 0x7fffffffLL) return TTT_ERR_SHAPE;
-  if ((long long)NC * ttt::mlp_upd_slot_bytes(F, FF, dtype) > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  if ((long long)NC * ttt::mlp_saved_slot_bytes(F, FF, dtype) > 0x7fffffffLL) return TTT_ERR_SHAPE;
   return TTT_OK;
 }
 
@@ -176,7 +176,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* b2_init, int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
                 void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last, float* W1_ckpt,
                 float* b1_ckpt, float* W2_ckpt, float* b2_ckpt, float* W1_memo, float* b1_memo, float* W2_memo,
-                float* b2_memo, void* upd, size_t upd_bytes, void* stream) {
+                float* b2_memo, void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
@@ -202,9 +202,9 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
     for (const float* q : grp) OPTIONAL_PTR(q);
   }
   if (W1_memo != nullptr && (M < 1 || M > NC)) return TTT_ERR_ARG;
-  if (upd != nullptr) {
-    if (!aligned16(upd)) return TTT_ERR_ALIGN;
-    if (upd_bytes < ttt_mlp_upd_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  if (saved != nullptr) {
+    if (!aligned16(saved)) return TTT_ERR_ALIGN;
+    if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
   }
 
   ttt::MlpFwdParams p;
@@ -231,7 +231,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.b1_memo = b1_memo;
   p.W2_memo = W2_memo;
   p.b2_memo = b2_memo;
-  p.upd = upd;
+  p.saved = saved;
   p.B = B;
   p.H = H;
   p.NC = NC;
@@ -245,10 +245,10 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   return hip_status(ttt::launch_mlp_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
-size_t ttt_mlp_upd_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
+size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
-  return (size_t)B * H * NC * ttt::mlp_upd_slot_bytes(F, FF, dtype);
+  return (size_t)B * H * NC * ttt::mlp_saved_slot_bytes(F, FF, dtype);
 }
 
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
@@ -256,7 +256,7 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
                 const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
                 float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
-                float* db2, float* dln_w, float* dln_b, const void* upd, size_t upd_bytes, void* stream) {
+                float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
@@ -265,9 +265,9 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                        W1_last, b1_last, W2_last, b2_last, dout,
                        dXQ, dXK, dXV, deta, dW1, db1, dW2, db2, dln_w, dln_b};
   for (const void* q : req) REQUIRE_PTR(q);
-  if (upd == nullptr) return TTT_ERR_WORKSPACE;
-  if (!aligned16(upd)) return TTT_ERR_ALIGN;
-  if (upd_bytes < ttt_mlp_upd_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  if (saved == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(saved)) return TTT_ERR_ALIGN;
+  if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
 
   ttt::MlpBwdParams p;
   p.XQ = XQ;
@@ -285,7 +285,7 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.b1_last = b1_last;
   p.W2_last = W2_last;
   p.b2_last = b2_last;
-  p.upd = upd;
+  p.saved = saved;
   p.dXQ = dXQ;
   p.dXK = dXK;
   p.dXV = dXV;

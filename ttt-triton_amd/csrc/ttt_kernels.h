@@ -34,7 +34,7 @@ struct MlpFwdParams {
   float *W1_last, *b1_last, *W2_last, *b2_last;
   float *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
   float *W1_memo, *b1_memo, *W2_memo, *b2_memo;
-  void* upd;  // per mini-batch update operands for the backward (may be null)
+  void* saved;  // per mini-batch values for the backward, MlpSavedSlot layout (may be null)
   int B, H, NC, F, FF, G, NK, M, NS;
   float eps;
 };
@@ -43,7 +43,7 @@ struct MlpBwdParams {
   const void *XQ, *XK, *XV, *eta, *dout;
   const float *ln_w, *ln_b, *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
   const float *W1_last, *b1_last, *W2_last, *b2_last;
-  const void* upd;  // update operands written by the forward
+  const void* saved;  // per mini-batch values written by the forward
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   int B, H, NC, F, FF, G, NK;
@@ -61,22 +61,45 @@ struct MlpReadoutParams {
 hipError_t launch_mlp_readout(const MlpReadoutParams& p, int dtype, hipStream_t stream);
 int mlp_readout_chunk_tokens();
 
-// One mini-batch's TTT-MLP update operands in the upd buffer [B*H][NC][slot]
-// (byte offsets; ST = bytes of the activation type):
-//   g1e [FF/64][4][64] x 4 ST   -e*G1, the W1-update MFMA operand frags per 64-unit slice
-//   g2e [F/16][64] x 4 ST       -e*G2, the W2-update MFMA operand frags
-//   b1d [FF] fp32, b2d [F] fp32  bias decrements (b -= G^T e)
-template <int F, int FF, int ST> struct MlpUpdSlot {
+// What the TTT-MLP forward saves per mini-batch for the backward, one slot
+// per (chain, mini-batch) in the saved buffer [B*H][NC][slot].  Byte offsets;
+// ST = bytes of the activation type; "lane order" = each lane's registers
+// stored contiguously, so a wave reads a tile back with one access per lane.
+//   state update:
+//     G1E [FF/64][4][64] x 4 ST   -e*G1 as W1-update operand frags, per 64-unit slice
+//     G2E [F/16][64] x 4 ST       -e*G2 as W2-update operand frags
+//     B1D [FF], B2D [F] fp32      bias decrements (b -= G^T e)
+//   forward activations (token-major C-layout tiles, lane order):
+//     Z1, Z1B, PM  [FF/64][4][64] x 4 ST   XK W1 + b1, the readout's Z1b, G2 W2^T
+//     X2           [FF/64][4][64] x 4 ST   gelu(Z1) as the W2-update operand frags
+//     G2, XH, XHB  [F/16][64] x 4 fp32     G2, normalised Z2, normalised Z2b
+//     RSTD, CC, RSB [64] x 4 fp32          per-row 1/sigma(Z2), mean(gx * xh), 1/sigma(Z2b)
+//     A2T [16][16] fp32 row-major          (X2b X2^T)^T
+template <int F, int FF, int ST> struct MlpSavedSlot {
   static constexpr int G1E = 0;
-  static constexpr int G2E = FF * 16 * ST;
-  static constexpr int B1D = (FF + F) * 16 * ST;
+  static constexpr int G2E = G1E + FF * 16 * ST;
+  static constexpr int B1D = G2E + F * 16 * ST;
   static constexpr int B2D = B1D + FF * 4;
-  static constexpr int BYTES = B2D + F * 4;
+  static constexpr int Z1 = B2D + F * 4;
+  static constexpr int Z1B = Z1 + FF * 16 * ST;
+  static constexpr int PM = Z1B + FF * 16 * ST;
+  static constexpr int X2 = PM + FF * 16 * ST;
+  static constexpr int G2 = X2 + FF * 16 * ST;
+  static constexpr int XH = G2 + F * 64;
+  static constexpr int XHB = XH + F * 64;
+  static constexpr int RSTD = XHB + F * 64;
+  static constexpr int CC = RSTD + 1024;
+  static constexpr int RSB = CC + 1024;
+  static constexpr int A2T = RSB + 1024;
+  static constexpr int BYTES = A2T + 1024;
 };
+constexpr size_t mlp_saved_slot_bytes_of(int F, int FF, int ST) {
+  return (size_t)(5 * FF + F) * 16 * ST + (size_t)(FF + F) * 4 + (size_t)3 * F * 64 + 4 * 1024;
+}
 
 hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
-// bytes of one mini-batch's update operands (per chain) in the forward's upd buffer
-size_t mlp_upd_slot_bytes(int F, int FF, int dtype);
+// bytes of one (chain, mini-batch) slot of the forward's saved buffer
+size_t mlp_saved_slot_bytes(int F, int FF, int dtype);
 
 hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream);
 

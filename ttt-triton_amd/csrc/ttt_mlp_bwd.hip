@@ -1,32 +1,32 @@
 // TTT-MLP backward on gfx950: one workgroup of NW = FF/64 wavefronts per
 // (batch, head) chain; wave w owns hidden units S = [64w, 64w+64).
 //
-// Where the state lives.  The fast weights are kept in LDS in fp32, W1 as
-// [F][FF] and W2 transposed, W2^T [F][FF] (columns XOR-swizzled so both access
-// shapes are bank-conflict free), so every operand orientation the backward
-// needs is a direct read: a C-layout tile (4 x ds_read_b32) or a row vector
-// (ds_read_b128), no transposes.  Each
-// wave only ever touches its own hidden columns S of both, so no barrier
-// guards the state.  Registers hold the gradient accumulators dW1[:, S],
-// dW2[S, :], db1[S], db2 -- the gradient wrt the state after the mini-batch
-// being processed -- and the biases b1[S], b2.
+// Inputs besides the sequence: the forward's checkpoints, its final state and
+// its saved buffer, which holds for every mini-batch the state-update
+// operands and the activations the gradient needs (MlpSavedSlot).  Nothing of
+// the forward is recomputed here: each mini-batch loads its activations and
+// runs only the backward (ops/ttt_mlp.py:9-67 differentiated by hand).
+//
+// The fast weights are still needed (the gradient flows through products
+// with W1 and W2), so they are kept in LDS in fp32, W1 as [F][FF] and W2
+// transposed, W2^T [F][FF] (columns XOR-swizzled so both access shapes are
+// bank-conflict free): every operand orientation is a direct read, a C-layout
+// tile or a row vector.  Each wave only touches its own hidden columns of
+// both, so no barrier guards them.  Registers hold the gradient accumulators
+// dW1[:, S], dW2[S, :], db1[S], db2 -- the gradient wrt the state after the
+// mini-batch being processed -- pinned to the MFMA accumulator registers.
 //
 // Reverse sweep over checkpoint groups (kernels/mlp_backward.py:340 walks the
 // same groups; the algorithm and data flow here are our own).  A group starts
 // from the state after its last mini-batch: the next group's checkpoint, or
-// the forward's final state for the last group.  Mini-batches are then taken
-// in reverse; mini-batch s first rebuilds the state entering it from the
-// state after it, W1_s = W1_{s+1} + XK_s^T (e G1_s), W2_s = W2_{s+1} +
-// X2_s^T (e G2_s), b_s = b_{s+1} + G_s^T e, with the update operands the
-// forward wrote (exactly the values its update MFMAs consumed), then
-// recomputes the mini-batch forward and applies its gradient
-// (ops/ttt_mlp.py:9-67 differentiated by hand).
-// Row-wise work on [16 x F] tiles (LayerNorms and their backward) is done
-// redundantly by every wave.  Contractions over the hidden units are split by
-// slice; their [16 x F] partials meet in one 32 KB LDS exchange area, so each
-// reduction is fenced by a barrier after the writes (the partials are in) and
-// one after the reads (the area is free): eight barriers per mini-batch.  The
-// gradient accumulators are pinned to the MFMA accumulator registers.
+// the forward's final state for the last group.  Mini-batch s first rebuilds
+// the state entering it, W1_s = W1_{s+1} + XK_s^T (e G1_s) and W2_s = W2_{s+1}
+// + X2_s^T (e G2_s), with the exact operands the forward's update used.
+//
+// Row-wise work on [16 x F] tiles (LayerNorm backwards) is done redundantly by
+// every wave.  Contractions over the hidden units are split by slice; their
+// [16 x F] partials meet in one 32 KB LDS exchange area, fenced by a barrier
+// after the writes and one after the reads: four barriers per mini-batch.
 #include "ttt_buf.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
@@ -58,6 +58,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   constexpr int FF = 64 * NW;
   constexpr float invF = 1.0f / F;
   constexpr int ST = (int)sizeof(T);
+  using Slot = MlpSavedSlot<F, FF, ST>;
   __shared__ MlpBwdShared<FT, NW> sh;
 
   const int chain = blockIdx.x;
@@ -87,25 +88,20 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   auto xs = [&](int s) { return s * K * F * ST; };
   auto es = [&](int s) { return s * K * K * ST; };
 
-  // update operands of this chain, [NC] slots (MlpUpdSlot layout)
-  using Slot = MlpUpdSlot<F, FF, ST>;
-  const rsrc_t rUP = make_rsrc(static_cast<const char*>(p.upd) + (size_t)chain * NC * Slot::BYTES,
+  // the forward's saved values of this chain, [NC] slots
+  const rsrc_t rSV = make_rsrc(static_cast<const char*>(p.saved) + (size_t)chain * NC * Slot::BYTES,
                                (unsigned)(NC * Slot::BYTES));
-  const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST
-  const int g2l = l * 4 * ST;                       // + c * 256 * ST (+ Slot::G2E)
-  const int b1l = (hs + n) * 4;                     // + 64 * o (+ Slot::B1D)
-  const int b2l = n * 4;                            // + 64 * c (+ Slot::B2D)
+  const int hl = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST: this wave's [16 x 64] slice, lane order
+  const int fl = l * 4 * ST;                       // + c * 256 * ST: [16 x F] frags, lane order
+  const int f4l = l * 16;                          // + c * 1024: fp32 tiles, lane order
+  const int a2l = (4 * g * 16 + n) * 4;            // C-layout tile of a row-major [16 x 16] fp32 block
+  const int a2tl = (n * 16 + 4 * g) * 4;           // the same block transposed (row n, columns 4g..4g+3)
 
-  // checkpoints [NK][...] of this chain; lane offsets include the wave's slice
+  // checkpoints [NK][...] and the final state of this chain
   const rsrc_t rW1c = make_rsrc(p.W1_ckpt + (size_t)chain * NK * F * FF, (unsigned)((size_t)NK * F * FF * 4));
   const rsrc_t rW2c = make_rsrc(p.W2_ckpt + (size_t)chain * NK * FF * F, (unsigned)((size_t)NK * FF * F * 4));
-  const rsrc_t rB1c = make_rsrc(p.b1_ckpt + (size_t)chain * NK * FF, (unsigned)((size_t)NK * FF * 4));
-  const rsrc_t rB2c = make_rsrc(p.b2_ckpt + (size_t)chain * NK * F, (unsigned)((size_t)NK * F * 4));
-  // the forward's final state
   const rsrc_t rW1l = make_rsrc(p.W1_last + (size_t)chain * F * FF, (unsigned)(F * FF * 4));
   const rsrc_t rW2l = make_rsrc(p.W2_last + (size_t)chain * FF * F, (unsigned)(FF * F * 4));
-  const rsrc_t rB1l = make_rsrc(p.b1_last + (size_t)chain * FF, (unsigned)(FF * 4));
-  const rsrc_t rB2l = make_rsrc(p.b2_last + (size_t)chain * F, (unsigned)(F * 4));
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
 
@@ -123,7 +119,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   for (int o = 0; o < HT; ++o) db1[o] = 0.f;
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
-  // LDS state accessors (this wave's hidden columns only)
+  // LDS state views (this wave's hidden columns only)
   LdsMat<FF> W1s(sh.w1, hs), W2t(sh.w2t, hs);
   // W1 tile [F block kb x hidden block o]: frag (free = hidden, k = feature)
   auto w1_tile = [&](int kb, int o) { return W1s.tile(16 * kb, 16 * o); };
@@ -149,6 +145,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         asm volatile("" : "+a"(dW2[o_][q_].v));
       }
   };
+  // saved activations
+  auto ld_hid = [&](int o, int off, int us) { return frag_to_f4(bload_frag<T>(rSV, hl + o * 256 * ST, us + off)); };
+  auto ld_f32 = [&](int c, int off, int us) { return bload_frag<float>(rSV, f4l + c * 1024, us + off).v; };
 
   float lnw_tm[FT], lnb_tm[FT];
 #pragma unroll
@@ -156,7 +155,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
     lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
   }
-  const float eps = p.eps;
   const Frag<T> I = identity_frag<T>();
 
   float dlnw[FT], dlnb[FT];  // LN-parameter gradient partials (wave 0)
@@ -165,7 +163,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     dlnw[o] = 0.f;
     dlnb[o] = 0.f;
   }
-  float b1[HT], b2[FT];
 
   for (int kk = NK - 1; kk >= 0; --kk) {
     const int s0 = kk * G, s1 = min(s0 + G, NC);
@@ -174,7 +171,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     {
       const bool last = kk + 1 == NK;
       const rsrc_t r1 = last ? rW1l : rW1c, r2 = last ? rW2l : rW2c;
-      const rsrc_t q1 = last ? rB1l : rB1c, q2 = last ? rB2l : rB2c;
       const int k1 = last ? 0 : kk + 1;
 #pragma unroll
       for (int i = 0; i < FT; ++i)
@@ -184,34 +180,29 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       for (int i = 0; i < HT; ++i)
 #pragma unroll
         for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(r2, w2l, k1 * F * FF * 4, F, 16 * i, 16 * o));
-#pragma unroll
-      for (int o = 0; o < HT; ++o) b1[o] = bload_f32(q1, (hs + n) * 4, (k1 * FF + 16 * o) * 4);
-#pragma unroll
-      for (int o = 0; o < FT; ++o) b2[o] = bload_f32(q2, n * 4, (k1 * F + 16 * o) * 4);
     }
 
     // ===================== reverse through the group
-    // Regions between barriers:   R1-R2 | R3 | R4-B1 | B2 | B3
-    // exchange area:              Z2 partials; Z2b, A2 partials; dG2, dN1, de
-    //                             partials; dXQ, dXK partials
+    // Regions between barriers:   A-B1 | B2 | B3
+    // exchange area:              dG2, dN1, de partials; dXQ, dXK partials
     for (int s = s1 - 1; s >= s0; --s) {
       const int us = s * Slot::BYTES;
       pin_dW();
       W1s.pin();
       W2t.pin();
 
-      Frag<T> g1e[HT];
-#pragma unroll
-      for (int o = 0; o < HT; ++o) g1e[o] = bload_frag<T>(rUP, g1l + o * 256 * ST, us + Slot::G1E);
       Frag<T> xk[FT], xkTf[FT], xqTf[FT];
       f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
-      Tile z1[HT], zq[HT];
+      Frag<T> x2f[HT];
       {
         Frag<T> xq[FT];
 #pragma unroll
         for (int q = 0; q < FT; ++q) {
           xq[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
           xk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
+        }
+#pragma unroll
+        for (int q = 0; q < FT; ++q) {
           xkTf[q] = to_frag<T>(transpose16(xk[q], I).v);
           xqTf[q] = to_frag<T>(transpose16(xq[q], I).v);
         }
@@ -220,370 +211,259 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           mma32(at, xk[q], xk[q + 1], xq[q], xq[q + 1]);  // A1^T [t_k x t_q]
           mma32(a, xq[q], xq[q + 1], xk[q], xk[q + 1]);   // A1   [t_q x t_k]
         }
-        // ---- R1: rebuild W1_s (this slice) and use it at once for
-        //      Z1 = XK W1 + b1 and Zq = XQ W1 + b1
-#pragma unroll
-        for (int o = 0; o < HT; ++o) b1[o] += bload_f32(rUP, b1l + 64 * o, us + Slot::B1D);
+        // ---- A: rebuild W1_s and W2_s (this slice) from the forward's update operands
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          z1[o].v = f4{b1[o], b1[o], b1[o], b1[o]};
-          zq[o].v = z1[o].v;
-          const Frag<T> ng = negate(g1e[o]);
+          const Frag<T> ng = negate(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E));
 #pragma unroll
-          for (int q = 0; q < FT; q += 2) {
-            Tile w0 = w1_tile(q, o), w1 = w1_tile(q + 1, o);
-            mma16(w0.v, xkTf[q], ng);
-            mma16(w1.v, xkTf[q + 1], ng);
-            w1_put(q, o, w0);
-            w1_put(q + 1, o, w1);
-            const Frag<T> f0 = to_frag<T>(w0.v), f1 = to_frag<T>(w1.v);
-            mma32(z1[o].v, xk[q], xk[q + 1], f0, f1);
-            mma32(zq[o].v, xq[q], xq[q + 1], f0, f1);
+          for (int q = 0; q < FT; ++q) {
+            Tile w = w1_tile(q, o);
+            mma16(w.v, xkTf[q], ng);
+            w1_put(q, o, w);
+          }
+        }
+#pragma unroll
+        for (int o = 0; o < HT; ++o) x2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2);
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          const Frag<T> ng = negate(bload_frag<T>(rSV, fl + c * 256 * ST, us + Slot::G2E));
+#pragma unroll
+          for (int o = 0; o < HT; ++o) {
+            Tile w = w2_tile(o, c);
+            mma16(w.v, x2f[o], ng);
+            w2_put(o, c, w);
           }
         }
       }
-      Frag<T> x2f[HT], x2F[HT];
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        f4 x2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x2[j] = gelu_tanh(z1[o].v[j]);
-        x2f[o] = to_frag<T>(x2);
-        x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
-      }
-      // ---- R2: rebuild W2_s and b2_s, and the Z2 partial over this slice with it
-#pragma unroll
-      for (int c = 0; c < FT; ++c) b2[c] += bload_f32(rUP, b2l + 64 * c, us + Slot::B2D);
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        const Frag<T> ng = negate(bload_frag<T>(rUP, g2l + c * 256 * ST, us + Slot::G2E));
-        f4 z = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; o += 2) {
-          Tile w0 = w2_tile(o, c), w1 = w2_tile(o + 1, c);
-          mma16(w0.v, x2f[o], ng);
-          mma16(w1.v, x2f[o + 1], ng);
-          w2_put(o, c, w0);
-          w2_put(o + 1, c, w1);
-          mma32(z, x2F[o], x2F[o + 1], to_frag<T>(w0.v), to_frag<T>(w1.v));
-        }
-        sh.x.a.part[wave][c][l] = z;
-      }
-      __syncthreads();  // (1) Z2 partials in
 
-      // ---- R3: G2 (every wave), G1 and the readout of layer 1 (per slice)
-      LnL2Lite<FT> ln2;
-      Tile G2[FT];
-      {
-        Tile z2[FT];
-#pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          z2[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
-#pragma unroll
-          for (int w = 0; w < NW; ++w) z2[c].v += sh.x.a.part[w][c][l];
-        }
-        f4 tgt[FT];
-#pragma unroll
-        for (int q = 0; q < FT; ++q)
-          tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - frag_to_f4(xkTf[q]);
-        ln2.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
-      }
-      __syncthreads();  // (1x) exchange area free
-      pin_dW();
-      Frag<T> g2f[FT], g2F[FT];
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        g2f[c] = to_frag<T>(G2[c].v);
-        g2F[c] = to_frag<T>(transpose16(g2f[c], I).v);
-      }
-      Tile Pm[HT];  // G2 W2^T; G1 = Pm (.) gelu'(Z1)
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        Pm[o].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < FT; c += 2) mma32(Pm[o].v, g2F[c], g2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-      }
-      auto G1_of = [&](int o) {
-        f4 sp;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sp[j] = gelu_bwd(z1[o].v[j]);
-        return Pm[o].v * sp;
-      };
-
+      // ---- readout layer 2 LayerNorm backward (every wave): dZ2b from dout
       const f4 etaT = frag_to_f4(bload_frag<T>(rET, el, es(s)));  // [t_k x t_q]: eta[n][4g+j]
       f4 eta_n;                                                   // [t_q x t_k]: eta[4g+j][n]
 #pragma unroll
       for (int j = 0; j < 4; ++j) eta_n[j] = bload1<T>(rET, en + j * K * ST, es(s));
-      Frag<T> x2bf[HT];
-      f4 sp1b[HT];
+      const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
+      const f4 a2 = bload_frag<float>(rSV, a2tl, us + Slot::A2T).v;    // A2   [t_q x t_k]
+      Frag<T> dz2bf[FT], dz2bF[FT];
+      float dz2b_cs[FT];  // column sums of dZ2b (fp32)
       {
-        f4 m1T;
+        const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
+        f4 xhb[FT], gy[FT];
+        f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) m1T[j] = etaT[j] * at[j] + etaT[j];
-        const Frag<T> mnf = to_frag<T>(-m1T);
-        Frag<T> x2bF[HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          mma16(zq[o].v, mnf, to_frag<T>(G1_of(o)));  // Z1b = XQ W1 + b1 - M1 G1
-          f4 x2b;
+        for (int c = 0; c < FT; ++c) {
+          xhb[c] = ld_f32(c, Slot::XHB, us);
+          const f4 dT = transpose16(bload_frag<T>(rDO, xl + 16 * c * ST, xs(s)), I).v;  // dout, token-major
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            x2b[j] = gelu_tanh(zq[o].v[j]);
-            sp1b[o][j] = gelu_bwd(zq[o].v[j]);
+            gy[c][j] = dT[j] * lnw_tm[c];
+            s1[j] += gy[c][j];
+            s2[j] += gy[c][j] * xhb[c][j];
           }
-          x2bf[o] = to_frag<T>(x2b);
-          x2bF[o] = to_frag<T>(transpose16(x2bf[o], I).v);
+          if (wave == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dlnw[c] += dT[j] * xhb[c][j];
+              dlnb[c] += dT[j];
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s1[j] = sum_row16(s1[j]) * invF;
+          s2[j] = sum_row16(s2[j]) * invF;
         }
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          f4 z = f4{0.f, 0.f, 0.f, 0.f};
+          f4 dz;
+          float cs = 0.f;
 #pragma unroll
-          for (int o = 0; o < HT; o += 2)
-            mma32(z, x2bF[o], x2bF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
-          sh.x.a.part[wave][c][l] = z;
+          for (int j = 0; j < 4; ++j) {
+            dz[j] = rsb[j] * (gy[c][j] - s1[j] - xhb[c][j] * s2[j]);
+            cs += dz[j];
+          }
+          dz2b_cs[c] = sum_col4(cs);
+          dz2bf[c] = to_frag<T>(dz);
+          dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
         }
-        f4 a2Tp = f4{0.f, 0.f, 0.f, 0.f}, a2p = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; o += 2) {
-          mma32(a2Tp, x2F[o], x2F[o + 1], x2bF[o], x2bF[o + 1]);  // A2^T [t_k x t_q]
-          mma32(a2p, x2bF[o], x2bF[o + 1], x2F[o], x2F[o + 1]);   // A2   [t_q x t_k]
-        }
-        sh.x.a.sm[0][wave][l] = a2Tp;
-        sh.x.a.sm[1][wave][l] = a2p;
       }
-      __syncthreads();  // (2) Z2b, A2 partials in
-
-      // ---- R4: readout layer 2 and its LayerNorm backward (every wave)
-      f4 a2T = f4{0.f, 0.f, 0.f, 0.f}, a2 = f4{0.f, 0.f, 0.f, 0.f};
-      Tile z2b[FT];
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        a2T += sh.x.a.sm[0][w][l];
-        a2 += sh.x.a.sm[1][w][l];
-      }
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        z2b[c].v = f4{b2[c], b2[c], b2[c], b2[c]};
-#pragma unroll
-        for (int w = 0; w < NW; ++w) z2b[c].v += sh.x.a.part[w][c][l];
-      }
-      __syncthreads();  // (2x) exchange area free
-      pin_dW();
-      Frag<T> dz1bf[HT], dz1bF[HT];
-      float dz1b_cs[HT], dz2b_cs[FT];  // column sums of dZ1b, dZ2b (fp32)
-      f4 detT;
-      Tile dX2[HT], dZ1[HT];
+      // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
+      f4 detT, dA2T, dA2;
       {
-        Frag<T> dz2bf[FT], dz2bF[FT];
-        f4 m2T, m2;
+        Frag<T> g2F[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) g2F[c] = to_frag<T>(transpose16(to_frag<T>(ld_f32(c, Slot::G2, us)), I).v);
+        f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < FT; c += 2) {
+          mma32(dn, dz2bF[c], dz2bF[c + 1], g2F[c], g2F[c + 1]);   // dZ2b G2^T [t_q x t_k]
+          mma32(dnT, g2F[c], g2F[c + 1], dz2bF[c], dz2bF[c + 1]);  // G2 dZ2b^T [t_k x t_q]
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          m2T[j] = etaT[j] * a2T[j] + etaT[j];
-          m2[j] = eta_n[j] * a2[j] + eta_n[j];
+          detT[j] = -dnT[j] * (1.0f + a2T[j]);
+          dA2T[j] = -dnT[j] * etaT[j];
+          dA2[j] = -dn[j] * eta_n[j];
         }
-        {
-          const Frag<T> mnf = to_frag<T>(-m2T);
-#pragma unroll
-          for (int c = 0; c < FT; ++c) mma16(z2b[c].v, mnf, g2f[c]);
-          f4 mb, rsb;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < FT; ++c) acc += z2b[c].v[j];
-            mb[j] = sum_row16(acc) * invF;
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < FT; ++c) {
-              const float d = z2b[c].v[j] - mb[j];
-              acc += d * d;
-            }
-            rsb[j] = rsqrt_f(sum_row16(acc) * invF + eps);
-          }
-          f4 xhb[FT], gy[FT];
-          f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            const f4 dT = transpose16(bload_frag<T>(rDO, xl + 16 * c * ST, xs(s)), I).v;  // dout, token-major
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              xhb[c][j] = (z2b[c].v[j] - mb[j]) * rsb[j];
-              gy[c][j] = dT[j] * lnw_tm[c];
-              s1[j] += gy[c][j];
-              s2[j] += gy[c][j] * xhb[c][j];
-            }
-            if (wave == 0) {
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                dlnw[c] += dT[j] * xhb[c][j];
-                dlnb[c] += dT[j];
-              }
-            }
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            s1[j] = sum_row16(s1[j]) * invF;
-            s2[j] = sum_row16(s2[j]) * invF;
-          }
-#pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            f4 dz;
-            float cs = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              dz[j] = rsb[j] * (gy[c][j] - s1[j] - xhb[c][j] * s2[j]);
-              cs += dz[j];
-            }
-            dz2b_cs[c] = sum_col4(cs);
-            dz2bf[c] = to_frag<T>(dz);
-            dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
-          }
-        }
-        // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
-        f4 dA2T, dA2;
-        {
-          f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < FT; c += 2) {
-            mma32(dn, dz2bF[c], dz2bF[c + 1], g2F[c], g2F[c + 1]);   // dZ2b G2^T [t_q x t_k]
-            mma32(dnT, g2F[c], g2F[c + 1], dz2bF[c], dz2bF[c + 1]);  // G2 dZ2b^T [t_k x t_q]
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            detT[j] = -dnT[j] * (1.0f + a2T[j]);
-            dA2T[j] = -dnT[j] * etaT[j];
-            dA2[j] = -dn[j] * eta_n[j];
-          }
-        }
+      }
+      pin_dW();
 
-        // ---- B1: readout layer 1 backward (per slice)
-        {
-          const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
-#pragma unroll
-          for (int o = 0; o < HT; ++o) {
-            f4 dx2b = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < FT; c += 2) mma32(dx2b, dz2bF[c], dz2bF[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-            mma16(dx2b, dA2Tf, x2f[o]);  // + dA2 X2
-            const f4 dz = dx2b * sp1b[o];
-            dz1b_cs[o] = sum_col4(dz[0] + dz[1] + dz[2] + dz[3]);
-            dz1bf[o] = to_frag<T>(dz);
-            dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
-            dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
-            mma16(dX2[o].v, dA2f, x2bf[o]);  // dA2^T X2b
-          }
-        }
-        // dN1 = dZ1b G1^T (both layouts)
-        {
-          Frag<T> g1F[HT];
-#pragma unroll
-          for (int o = 0; o < HT; ++o) g1F[o] = to_frag<T>(transpose16(to_frag<T>(G1_of(o)), I).v);
-          f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int o = 0; o < HT; o += 2) {
-            mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
-            mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
-          }
-          sh.x.a.sm[0][wave][l] = dn;
-          sh.x.a.sm[1][wave][l] = dnT;
-        }
-        // dG1 = -M1^T dZ1b - e (XK dW1' + db1'); eta-row gradient partial (G1 . Q1 + G2 . Q2)
-        const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
-        Tile dG1[HT];
-        f4 eq2[FT];  // this slice's share of -e Q2, Q2 = X2 dW2' + db2'
-        {
-          f4 m1;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
-          const Frag<T> mf = to_frag<T>(-m1);
-          f4 dep = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int o = 0; o < HT; ++o) {
-            f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
-#pragma unroll
-            for (int q = 0; q < FT; q += 2)
-              mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
-            dG1[o].v = f4{0.f, 0.f, 0.f, 0.f};
-            mma16(dG1[o].v, mf, dz1bf[o]);
-            const f4 g1 = G1_of(o);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              dG1[o].v[j] -= e[j] * q1[j];
-              dep[j] += g1[j] * q1[j];
-            }
-          }
-          // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2; both are
-          // linear in Q2, so this slice's share goes into the partials as it is
-          // (wave 0's share carries db2')
-#pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int o = 0; o < HT; o += 2)
-              mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
-            if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              dep[j] += G2[c].v[j] * q2[j];
-              eq2[c][j] = -e[j] * q2[j];
-            }
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
-          sh.x.a.sm[2][wave][l] = dep;
-        }
-        // dX2 += (-e G2) dW2'^T  (contraction over features; dW2'^T frags by transposes)
-        {
-          Frag<T> eg2F[FT];
-#pragma unroll
-          for (int c = 0; c < FT; ++c)
-            eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rUP, g2l + c * 256 * ST, us + Slot::G2E), I).v);
-#pragma unroll
-          for (int o = 0; o < HT; ++o)
-#pragma unroll
-            for (int c = 0; c < FT; c += 2) {
-              const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c].v), I).v);
-              const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c + 1].v), I).v);
-              mma32(dX2[o].v, eg2F[c], eg2F[c + 1], u0, u1);
-            }
-        }
-        // dP = dG1 (.) gelu'(Z1), dZ1 <- dG1 (.) Pm (.) gelu''(Z1); dG2 partial over this
-        // slice: dP W2 - e Q2 (- M2^T dZ2b, which every wave holds, added once by wave 0)
-        Frag<T> dPf[HT], dPF[HT];
+      // ---- B1: readout layer 1 backward (per slice)
+      Frag<T> dz1bf[HT], dz1bF[HT], x2bf[HT];
+      float dz1b_cs[HT];  // column sums of dZ1b (fp32)
+      Tile dX2[HT], dZ1[HT];
+      {
+        const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          f4 sp, spp;
+          f4 x2b, sp1b;
+          {
+            const f4 z = ld_hid(o, Slot::Z1B, us);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              float y, dy;
+              gelu_fwd_bwd(z[j], y, dy);
+              x2b[j] = y;
+              sp1b[j] = dy;
+            }
+          }
+          x2bf[o] = to_frag<T>(x2b);
+          f4 dx2b = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < FT; c += 2) mma32(dx2b, dz2bF[c], dz2bF[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+          mma16(dx2b, dA2Tf, x2f[o]);  // + dA2 X2
+          const f4 dz = dx2b * sp1b;
+          dz1b_cs[o] = sum_col4(dz[0] + dz[1] + dz[2] + dz[3]);
+          dz1bf[o] = to_frag<T>(dz);
+          dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
+          dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
+          mma16(dX2[o].v, dA2f, x2bf[o]);  // dA2^T X2b
+        }
+      }
+      // G1 = Pm (.) gelu'(Z1) (Pm = G2 W2^T); the derivatives of gelu at Z1
+      f4 sp1[HT], spp1[HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        const f4 z = ld_hid(o, Slot::Z1, us);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float dy, ddy;
+          gelu_d1_d2(z[j], dy, ddy);
+          sp1[o][j] = dy;
+          spp1[o][j] = ddy;
+        }
+      }
+      // dN1 = dZ1b G1^T (both layouts)
+      {
+        Frag<T> g1F[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o)
+          g1F[o] = to_frag<T>(transpose16(to_frag<T>(ld_hid(o, Slot::PM, us) * sp1[o]), I).v);
+        f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; o += 2) {
+          mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
+          mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
+        }
+        sh.x.a.sm[0][wave][l] = dn;
+        sh.x.a.sm[1][wave][l] = dnT;
+      }
+      // dG1 = -M1^T dZ1b - e (XK dW1' + db1'); eta-row gradient partial (G1 . Q1 + G2 . Q2)
+      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+      Tile dG1[HT];
+      f4 eq2[FT];  // this slice's share of -e Q2, Q2 = X2 dW2' + db2'
+      {
+        f4 m1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
+        const Frag<T> mf = to_frag<T>(-m1);
+        f4 dep = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
+#pragma unroll
+          for (int q = 0; q < FT; q += 2)
+            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
+          dG1[o].v = f4{0.f, 0.f, 0.f, 0.f};
+          mma16(dG1[o].v, mf, dz1bf[o]);
+          const f4 g1 = ld_hid(o, Slot::PM, us) * sp1[o];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            sp[j] = gelu_bwd(z1[o].v[j]);
-            spp[j] = gelu_bwd2(z1[o].v[j]);
-          }
-          dZ1[o].v = dG1[o].v * Pm[o].v * spp;
-          dPf[o] = to_frag<T>(dG1[o].v * sp);
-          dPF[o] = to_frag<T>(transpose16(dPf[o], I).v);
-        }
-        {
-          const Frag<T> mf = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            f4 z = eq2[c];
-            mma16(z, mf, dz2bf[c]);
-#pragma unroll
-            for (int o = 0; o < HT; o += 2)
-              mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
-            sh.x.a.part[wave][c][l] = z;
+            dG1[o].v[j] -= e[j] * q1[j];
+            dep[j] += g1[j] * q1[j];
           }
         }
-        // two terms of the layer-2 state gradient (dW2' has been used)
+        // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2; both are
+        // linear in Q2, so this slice's share goes into the partials as it is
+        // (wave 0's share carries db2')
+        Frag<T> x2F[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int o = 0; o < HT; o += 2)
+            mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
+          if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
+          const f4 g2 = ld_f32(c, Slot::G2, us);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dep[j] += g2[j] * q2[j];
+            eq2[c][j] = -e[j] * q2[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
+        sh.x.a.sm[2][wave][l] = dep;
+      }
+      // dX2 += (-e G2) dW2'^T  (contraction over features; dW2'^T frags by transposes)
+      {
+        Frag<T> eg2F[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c)
+          eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rSV, fl + c * 256 * ST, us + Slot::G2E), I).v);
 #pragma unroll
         for (int o = 0; o < HT; ++o)
 #pragma unroll
-          for (int c = 0; c < FT; ++c) mma32(dW2[o][c].v, x2bf[o], dPf[o], dz2bf[c], g2f[c]);
+          for (int c = 0; c < FT; c += 2) {
+            const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c].v), I).v);
+            const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW2[o][c + 1].v), I).v);
+            mma32(dX2[o].v, eg2F[c], eg2F[c + 1], u0, u1);
+          }
       }
-      __syncthreads();  // (3) dG2, dN1, eta-row partials in
+      // dP = dG1 (.) gelu'(Z1), dZ1 <- dG1 (.) Pm (.) gelu''(Z1); dG2 partial over this
+      // slice: dP W2 - e Q2 (- M2^T dZ2b, which every wave holds, added once by wave 0)
+      {
+        Frag<T> dPf[HT], dPF[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          dZ1[o].v = dG1[o].v * ld_hid(o, Slot::PM, us) * spp1[o];
+          dPf[o] = to_frag<T>(dG1[o].v * sp1[o]);
+          dPF[o] = to_frag<T>(transpose16(dPf[o], I).v);
+        }
+        f4 m2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m2[j] = eta_n[j] * a2[j] + eta_n[j];
+        const Frag<T> mf = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          f4 z = eq2[c];
+          mma16(z, mf, dz2bf[c]);
+#pragma unroll
+          for (int o = 0; o < HT; o += 2)
+            mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
+          sh.x.a.part[wave][c][l] = z;
+        }
+        // two terms of the layer-2 state gradient, X2b^T dZ2b + dP^T G2 (dW2' has
+        // been used)
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          const Frag<T> g2f = to_frag<T>(ld_f32(c, Slot::G2, us));
+#pragma unroll
+          for (int o = 0; o < HT; ++o) mma32(dW2[o][c].v, x2bf[o], dPf[o], dz2bf[c], g2f);
+        }
+      }
+      __syncthreads();  // (1) dG2, dN1, eta-row partials in
 
       // ---- B2: assemble dN1, de; deta (wave 0); G2 backward (every wave); dX2, dZ1;
       //      dXQ and dXK partials; the rest of the state gradient
@@ -619,7 +499,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           bstore_frag<T>(rDET, el, es(s), to_frag<T>(detT));
         }
       }
-      __syncthreads();  // (3x) exchange area free
+      __syncthreads();  // (1x) exchange area free
       pin_dW();
       f4 dz2[FT], dtgt[FT];
       {
@@ -629,10 +509,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           lw_i[c] = 0.f;
           lb_i[c] = 0.f;
         }
+        LnL2Lite<FT> ln2;
+        ln2.rstd = bload_frag<float>(rSV, f4l, us + Slot::RSTD).v;
+        ln2.c = bload_frag<float>(rSV, f4l, us + Slot::CC).v;
+        Tile G2[FT];
         f4 tgt[FT];
 #pragma unroll
-        for (int q = 0; q < FT; ++q)
-          tgt[q] = transpose16(bload_frag<T>(rXV, xl + 16 * q * ST, xs(s)), I).v - frag_to_f4(xkTf[q]);
+        for (int c = 0; c < FT; ++c) {
+          ln2.xh[c] = ld_f32(c, Slot::XH, us);
+          G2[c].v = ld_f32(c, Slot::G2, us);
+          tgt[c] = transpose16(bload_frag<T>(rXV, xl + 16 * c * ST, xs(s)), I).v - frag_to_f4(xkTf[c]);
+        }
         ln2.backward(dG2, G2, tgt, lnw_tm, lnb_tm, dz2, dtgt, lw_i, lb_i);
         if (wave == 0) {
 #pragma unroll
@@ -657,13 +544,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int o = 0; o < HT; ++o) {
 #pragma unroll
           for (int c = 0; c < FT; c += 2) mma32(dX2[o].v, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-          f4 sp;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) sp[j] = gelu_bwd(z1[o].v[j]);
-          dZ1[o].v += dX2[o].v * sp;
+          dZ1[o].v += dX2[o].v * sp1[o];
           dz1f[o] = to_frag<T>(dZ1[o].v);
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
-          eg1F[o] = to_frag<T>(transpose16(g1e[o], I).v);
+          eg1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E), I).v);
         }
         // dXQ partial = dZ1b W1^T, dXK partial = dZ1 W1^T + (-e G1) dW1'^T (this slice)
 #pragma unroll
@@ -701,7 +585,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int j = 0; j < 4; ++j) acc += dz2[c][j];
         db2[c] += sum_col4(acc) + dz2b_cs[c];
       }
-      __syncthreads();  // (4) dXQ, dXK partials in
+      __syncthreads();  // (2) dXQ, dXK partials in
 
       // ---- B3: dXQ, dXK, dXV (tile owners)
       {
@@ -723,7 +607,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dtgt[f]), I).v));
         }
       }
-      __syncthreads();  // (4x) exchange area free for the next mini-batch
+      __syncthreads();  // (2x) exchange area free for the next mini-batch
     }
   }
 

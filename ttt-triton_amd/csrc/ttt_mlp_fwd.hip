@@ -17,11 +17,12 @@
 //
 // Checkpoints hold the state entering mini-batch k*G
 // (kernels/mlp_forward.py:84-117); memo snapshot s holds the state after
-// mini-batch s*M is applied (kernels/mlp_forward.py:193-226).  When `upd` is
-// given, the update operands -e*G1, -e*G2 and the bias decrements of every
-// mini-batch are written there (MlpUpdSlot layout): the backward rebuilds the
-// state of each mini-batch in reverse from them instead of re-running the
-// forward from a checkpoint.
+// mini-batch s*M is applied (kernels/mlp_forward.py:193-226).  When `saved`
+// is given, every mini-batch's update operands -e*G1, -e*G2 and bias
+// decrements, and the activations its backward needs (Z1, X2, Z1b, G2 W2^T, G2,
+// the two LayerNorms' normalised rows and statistics, X2b X2^T) are written
+// there (MlpSavedSlot layout): the backward rebuilds the state in reverse
+// from the update operands and never re-runs the forward.
 //
 // Slabs are read through buffer resources; the next mini-batch's XQ and XK
 // are requested right after the first barrier of the current one, before its
@@ -33,9 +34,8 @@
 
 namespace ttt {
 
-size_t mlp_upd_slot_bytes(int F, int FF, int dtype) {
-  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
-  return (size_t)(FF + F) * 16 * t + (size_t)(FF + F) * sizeof(float);
+size_t mlp_saved_slot_bytes(int F, int FF, int dtype) {
+  return mlp_saved_slot_bytes_of(F, FF, dtype == TTT_DTYPE_BF16 ? 2 : 4);
 }
 
 template <int FT, int NW> struct MlpFwdShared {
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   constexpr int HT = 4;  // hidden tiles per wave
   constexpr int FF = 64 * NW;
   constexpr int ST = (int)sizeof(T);
-  using Slot = MlpUpdSlot<F, FF, ST>;
+  using Slot = MlpSavedSlot<F, FF, ST>;
   __shared__ MlpFwdShared<FT, NW> sh;
 
   const int chain = blockIdx.x;
@@ -75,11 +75,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const int e4 = ((K - 1) * K + 4 * g) * ST;  // eta[K-1][4g .. 4g+3]
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
-  const bool want_upd = p.upd != nullptr;
-  const rsrc_t rUP = make_rsrc(want_upd ? static_cast<char*>(p.upd) + (size_t)chain * NC * Slot::BYTES : nullptr,
-                               want_upd ? (unsigned)(NC * Slot::BYTES) : 0u);
-  const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST
-  const int g2l = l * 4 * ST;                       // + c * 256 * ST + Slot::G2E
+  const bool want_saved = p.saved != nullptr;
+  const rsrc_t rSV = make_rsrc(want_saved ? static_cast<char*>(p.saved) + (size_t)chain * NC * Slot::BYTES : nullptr,
+                               want_saved ? (unsigned)(NC * Slot::BYTES) : 0u);
+  const int g1l = ((wave * HT) * 64 + l) * 4 * ST;  // + o * 256 * ST: this wave's [16 x 64] slice, lane order
+  const int g2l = l * 4 * ST;                       // + c * 256 * ST: [16 x F], lane order
+  const int f4l = l * 16;                           // + c * 1024: fp32 tiles, lane order
+  const int a2l = (4 * g * 16 + n) * 4;             // C-layout tile of a row-major [16 x 16] fp32 block
 
   // state slice: W1[:, hs:hs+64] as tiles [f block][hidden block], W2[hs:hs+64, :]
   Tile W1[FT][HT], W2[HT][FT];
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt + k * FF, p.W2_ckpt + k * FF * F, p.b2_ckpt + k * F);
     }
     const int xo = s * K * F * ST, eo = s * K * K * ST;
+    const int us = s * Slot::BYTES;
     Frag<T> xv[FT];
 #pragma unroll
     for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
@@ -160,6 +163,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       gemm_pt<1, HT, FT>(z1, xk, W1);
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
+        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::Z1, to_frag<T>(z1[0][o].v));
         f4 x2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -169,6 +173,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           gp[o][j] = dy;
         }
         x2f[o] = to_frag<T>(x2);
+        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
         x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
       }
     }
@@ -213,6 +218,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       }
       LnL2Lite<FT> ln;
       ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
+      if (want_saved) {
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          if (c % NW != wave) continue;
+          bstore_frag<float>(rSV, f4l + c * 1024, us + Slot::G2, Frag<float>{G2[c].v});
+          bstore_frag<float>(rSV, f4l + c * 1024, us + Slot::XH, Frag<float>{ln.xh[c]});
+        }
+        if (wave == 0) {
+          bstore_frag<float>(rSV, f4l, us + Slot::RSTD, Frag<float>{ln.rstd});
+          bstore_frag<float>(rSV, f4l, us + Slot::CC, Frag<float>{ln.c});
+        }
+      }
     }
 
     // ---- G1 = (G2 W2^T) (.) gelu'(Z1); W2^T blocks by exact transposes
@@ -230,6 +247,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
           mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
         }
+        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::PM, to_frag<T>(G1[i].v));
         G1[i].v *= gp[i];
       }
     }
@@ -252,6 +270,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
         mma16(zb[0][o].v, m1f, to_frag<T>(G1[o].v));
+        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::Z1B, to_frag<T>(zb[0][o].v));
         f4 x2b;
 #pragma unroll
         for (int j = 0; j < 4; ++j) x2b[j] = gelu_tanh(zb[0][o].v[j]);
@@ -276,7 +295,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
     for (int o = 0; o < FT; ++o) b2_old[o] = b2_tm[o];
     {
-      const int us = s * Slot::BYTES;
       Frag<T> g1e[HT], g2e[FT];
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
@@ -290,9 +308,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g1e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b1_tm[o] -= d;
-        if (want_upd) {
-          bstore_frag<T>(rUP, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
-          if (g == 0) bstore_f32(rUP, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);
+        if (want_saved) {
+          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
+          if (g == 0) bstore_f32(rSV, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);
         }
       }
 #pragma unroll
@@ -307,9 +325,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g2e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b2_tm[o] -= d;
-        if (want_upd && wave == 0) {
-          bstore_frag<T>(rUP, g2l + o * 256 * ST, us + Slot::G2E, g2e[o]);
-          if (g == 0) bstore_f32(rUP, n * 4 + 64 * o, us + Slot::B2D, d);
+        if (want_saved && wave == 0) {
+          bstore_frag<T>(rSV, g2l + o * 256 * ST, us + Slot::G2E, g2e[o]);
+          if (g == 0) bstore_f32(rSV, n * 4 + 64 * o, us + Slot::B2D, d);
         }
       }
 #pragma unroll
@@ -329,6 +347,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       a2[0].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NW; ++w) a2[0].v += sh.a2p[w][l];
+      if (want_saved && wave == 0) bstore_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0, a2[0]);
       f4 m2;
 #pragma unroll
       for (int j = 0; j < 4; ++j) m2[j] = -(etaT[j] * a2[0].v[j] + etaT[j]);
@@ -361,13 +380,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         }
         rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
+      if (want_saved && wave == 0) bstore_frag<float>(rSV, f4l, us + Slot::RSB, Frag<float>{rs});
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
         if (o % NW != wave) continue;  // static indices keep these arrays in registers
         const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
-        f4 y;
+        f4 xhb, y;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) y[j] = q[j] + lnw_tm[o] * ((z2b[o].v[j] - mu[j]) * rs[j]) + lnb_tm[o];
+        for (int j = 0; j < 4; ++j) {
+          xhb[j] = (z2b[o].v[j] - mu[j]) * rs[j];
+          y[j] = q[j] + lnw_tm[o] * xhb[j] + lnb_tm[o];
+        }
+        if (want_saved) bstore_frag<float>(rSV, f4l + o * 1024, us + Slot::XHB, Frag<float>{xhb});
         bstore_frag<T>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
       }
     }
@@ -391,9 +415,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 
 template <typename T, int FT, int NW>
 static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
-  static_assert(MlpUpdSlot<16 * FT, 64 * NW, (int)sizeof(T)>::BYTES ==
-                    (64 * NW + 16 * FT) * 16 * (int)sizeof(T) + (64 * NW + 16 * FT) * 4,
-                "update slot layout");
+  static_assert(MlpSavedSlot<16 * FT, 64 * NW, (int)sizeof(T)>::BYTES ==
+                    (int)mlp_saved_slot_bytes_of(16 * FT, 64 * NW, (int)sizeof(T)),
+                "saved slot layout");
   hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }

@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -31,7 +31,7 @@ SIGNATURES = {
     "ttt_linear_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),
     "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 13 + [_P, _S, _P]),
-    "ttt_mlp_upd_bytes": (_S, [_I] * 7),
+    "ttt_mlp_saved_bytes": (_S, [_I] * 7),
     "ttt_mlp_bwd": (_I, [_P] * 15 + [_I] * 8 + [_F] + [_P] * 10 + [_P, _S, _P]),
     "ttt_mlp_cached_readout": (_I, [_P] * 7 + [_I] * 8 + [_F] + [_P, _P]),
 }

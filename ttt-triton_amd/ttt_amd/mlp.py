@@ -49,12 +49,13 @@ def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
 
 
 def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0, eps: float = LN_EPS,
-                want_ckpt: bool = True, want_last: bool = False, want_upd: bool = False):
+                want_ckpt: bool = True, want_last: bool = False, want_saved: bool = False):
     """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
     ckpt (W1,b1,W2,b2) or None, memo (W1,b1,W2,b2) or None, last or None,
-    upd or None).  ckpt, last and upd are what mlp_backward needs: the
+    saved or None).  ckpt, last and saved are what mlp_backward needs: the
     checkpoints every G mini-batches, the final state, and each mini-batch's
-    state-update operands (a flat uint8 buffer of ttt_mlp_upd_bytes)."""
+    state-update operands and activations (a flat uint8 buffer of
+    ttt_mlp_saved_bytes)."""
     B, H, NC, K, F, FF = _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta)
     dev = check_device(XQ, XK, XV, eta, W1, b1, W2, b2, ln_w, ln_b)
     mp = XQ.dtype
@@ -77,9 +78,9 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     last = state(None) if want_last else None
     none4 = (None, None, None, None)
     lib = _lib.load()
-    upd = None
-    if want_upd:
-        upd = torch.empty(lib.ttt_mlp_upd_bytes(B, H, NC, K, F, FF, code), device=dev, dtype=torch.uint8)
+    saved = None
+    if want_saved:
+        saved = torch.empty(lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, code), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_fwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb1), ptr(w2), ptr(bb2),
@@ -87,20 +88,20 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
             *(tuple(ptr(t) for t in last) if last else none4),
             *(tuple(ptr(t) for t in ck) if ck else none4),
             *(tuple(ptr(t) for t in memo) if memo else none4),
-            ptr(upd) if upd is not None else None, upd.numel() if upd is not None else 0,
+            ptr(saved) if saved is not None else None, saved.numel() if saved is not None else 0,
             stream_of(dev))
     _lib.check(st, "ttt_mlp_fwd")
-    return out, ck, memo, last, upd
+    return out, ck, memo, last, saved
 
 
-def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, upd, dout, G: int, eps: float = LN_EPS):
+def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, eps: float = LN_EPS):
     """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints, last =
-    the final state and upd = the update operands, all from one mlp_forward
+    the final state and saved = the saved buffer, all from one mlp_forward
     call with the same G.  Returns fp32 (dln_w [H,F], dln_b [H,F], dW1, db1,
     dW2, db2) and (dXQ, dXV, dXK, deta) in XQ.dtype."""
     B, H, NC, K, F = XQ.shape
     FF = ckpt[0].shape[-1]
-    dev = check_device(XQ, XK, XV, eta, dout, *ckpt, *last, upd)
+    dev = check_device(XQ, XK, XV, eta, dout, *ckpt, *last, saved)
     mp = XQ.dtype
     code = dtype_code(mp)
     xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
@@ -118,7 +119,7 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, upd, dout, G: int, eps
             *(ptr(t) for t in last), ptr(do),
             B, H, NC, K, F, FF, int(G), code, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
-            ptr(upd), upd.numel(), stream_of(dev))
+            ptr(saved), saved.numel(), stream_of(dev))
     _lib.check(st, "ttt_mlp_bwd")
     return (dlw.sum(0), dlb.sum(0), dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
 
@@ -135,11 +136,11 @@ class TTTMLPFunction(torch.autograd.Function):
         NC = XQ_batch.shape[2]
         G = min(max(int(checkpoint_group_size), 1), NC)
         M = int(memo_segment_size)
-        out, ck, memo, last, upd = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
+        out, ck, memo, last, saved = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
                                                XQ_batch, XV_batch, XK_batch, eta_batch, G, M=M, eps=eps,
-                                               want_ckpt=True, want_last=True, want_upd=True)
+                                               want_ckpt=True, want_last=True, want_saved=True)
         ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck, *last,
-                              upd)
+                              saved)
         ctx.G, ctx.eps = G, eps
         ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype, W2_init.dtype,
                       b2_init.dtype, XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
@@ -151,9 +152,9 @@ class TTTMLPFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out, *unused):
         XQ, XV, XK, eta, lw, lb = ctx.saved_tensors[:6]
-        ck, last, upd = ctx.saved_tensors[6:10], ctx.saved_tensors[10:14], ctx.saved_tensors[14]
+        ck, last, saved = ctx.saved_tensors[6:10], ctx.saved_tensors[10:14], ctx.saved_tensors[14]
         (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
-            lw, lb, XQ, XV, XK, eta, ck, last, upd, grad_out, ctx.G, ctx.eps)
+            lw, lb, XQ, XV, XK, eta, ck, last, saved, grad_out, ctx.G, ctx.eps)
         grads = (dlw, dlb, dW1, db1, dW2, db2, dxq, dxv, dxk, deta)
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
         return grads + (None, None, None)
