@@ -164,14 +164,33 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     dlnb[o] = 0.f;
   }
 
-  for (int kk = NK - 1; kk >= 0; --kk) {
-    const int s0 = kk * G, s1 = min(s0 + G, NC);
+  // inputs of the first phase of a mini-batch, requested one mini-batch ahead
+  Frag<T> nxq[FT], nxk[FT], ng1e[HT], nx2f[HT], ng2e[FT];
+  auto prefetch = [&](int s) {
+    const int u = s * Slot::BYTES;
+#pragma unroll
+    for (int q = 0; q < FT; ++q) {
+      nxq[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
+      nxk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
+      ng2e[q] = bload_frag<T>(rSV, fl + q * 256 * ST, u + Slot::G2E);
+    }
+#pragma unroll
+    for (int o = 0; o < HT; ++o) {
+      ng1e[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::G1E);
+      nx2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::X2);
+    }
+  };
+  prefetch(NC - 1);
 
-    // ===================== the state after the group's last mini-batch
-    {
-      const bool last = kk + 1 == NK;
+  // Reverse sweep.  Regions between barriers:   A-B1 | B2 | B3
+  // exchange area:                              dG2, dN1, de partials; dXQ, dXK partials
+  for (int s = NC - 1; s >= 0; --s) {
+    // the state after mini-batch s at the end of a checkpoint group: the next
+    // group's checkpoint, or the final state
+    if (s == NC - 1 || (s + 1) % G == 0) {
+      const bool last = s == NC - 1;
       const rsrc_t r1 = last ? rW1l : rW1c, r2 = last ? rW2l : rW2c;
-      const int k1 = last ? 0 : kk + 1;
+      const int k1 = last ? 0 : (s + 1) / G;
 #pragma unroll
       for (int i = 0; i < FT; ++i)
 #pragma unroll
@@ -181,25 +200,45 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
         for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(r2, w2l, k1 * F * FF * 4, F, 16 * i, 16 * o));
     }
-
-    // ===================== reverse through the group
-    // Regions between barriers:   A-B1 | B2 | B3
-    // exchange area:              dG2, dN1, de partials; dXQ, dXK partials
-    for (int s = s1 - 1; s >= s0; --s) {
+    {
       const int us = s * Slot::BYTES;
       pin_dW();
       W1s.pin();
       W2t.pin();
 
+      // inputs of the readout LayerNorm backward, requested before the state
+      // rebuild so that it hides their latency
+      const f4 etaT = frag_to_f4(bload_frag<T>(rET, el, es(s)));  // [t_k x t_q]: eta[n][4g+j]
+      f4 eta_n;                                                   // [t_q x t_k]: eta[4g+j][n]
+#pragma unroll
+      for (int j = 0; j < 4; ++j) eta_n[j] = bload1<T>(rET, en + j * K * ST, es(s));
+      const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
+      const f4 a2 = bload_frag<float>(rSV, a2tl, us + Slot::A2T).v;    // A2   [t_q x t_k]
+      const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
+      f4 xhb[FT], g2v[FT];
+      Frag<T> dof[FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        xhb[c] = ld_f32(c, Slot::XHB, us);
+        dof[c] = bload_frag<T>(rDO, xl + 16 * c * ST, xs(s));
+        g2v[c] = ld_f32(c, Slot::G2, us);
+      }
+
       Frag<T> xk[FT], xkTf[FT], xqTf[FT];
       f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
       Frag<T> x2f[HT];
       {
-        Frag<T> xq[FT];
+        Frag<T> xq[FT], g1e[HT], g2e[FT];
 #pragma unroll
         for (int q = 0; q < FT; ++q) {
-          xq[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
-          xk[q] = bload_frag<T>(rXK, xl + 16 * q * ST, xs(s));
+          xq[q] = nxq[q];
+          xk[q] = nxk[q];
+          g2e[q] = ng2e[q];
+        }
+#pragma unroll
+        for (int o = 0; o < HT; ++o) {
+          g1e[o] = ng1e[o];
+          x2f[o] = nx2f[o];
         }
 #pragma unroll
         for (int q = 0; q < FT; ++q) {
@@ -211,48 +250,42 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           mma32(at, xk[q], xk[q + 1], xq[q], xq[q + 1]);  // A1^T [t_k x t_q]
           mma32(a, xq[q], xq[q + 1], xk[q], xk[q + 1]);   // A1   [t_q x t_k]
         }
-        // ---- A: rebuild W1_s and W2_s (this slice) from the forward's update operands
+        // ---- A: rebuild W1_s and W2_s (this slice) from the forward's update
+        //      operands; the tiles of one hidden (feature) block are read before
+        //      any is written back, so the LDS reads overlap
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          const Frag<T> ng = negate(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E));
+          const Frag<T> ng = negate(g1e[o]);
+          Tile w[FT];
 #pragma unroll
-          for (int q = 0; q < FT; ++q) {
-            Tile w = w1_tile(q, o);
-            mma16(w.v, xkTf[q], ng);
-            w1_put(q, o, w);
-          }
+          for (int q = 0; q < FT; ++q) w[q] = w1_tile(q, o);
+#pragma unroll
+          for (int q = 0; q < FT; ++q) mma16(w[q].v, xkTf[q], ng);
+#pragma unroll
+          for (int q = 0; q < FT; ++q) w1_put(q, o, w[q]);
         }
 #pragma unroll
-        for (int o = 0; o < HT; ++o) x2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2);
-#pragma unroll
         for (int c = 0; c < FT; ++c) {
-          const Frag<T> ng = negate(bload_frag<T>(rSV, fl + c * 256 * ST, us + Slot::G2E));
+          const Frag<T> ng = negate(g2e[c]);
+          Tile w[HT];
 #pragma unroll
-          for (int o = 0; o < HT; ++o) {
-            Tile w = w2_tile(o, c);
-            mma16(w.v, x2f[o], ng);
-            w2_put(o, c, w);
-          }
+          for (int o = 0; o < HT; ++o) w[o] = w2_tile(o, c);
+#pragma unroll
+          for (int o = 0; o < HT; ++o) mma16(w[o].v, x2f[o], ng);
+#pragma unroll
+          for (int o = 0; o < HT; ++o) w2_put(o, c, w[o]);
         }
       }
 
       // ---- readout layer 2 LayerNorm backward (every wave): dZ2b from dout
-      const f4 etaT = frag_to_f4(bload_frag<T>(rET, el, es(s)));  // [t_k x t_q]: eta[n][4g+j]
-      f4 eta_n;                                                   // [t_q x t_k]: eta[4g+j][n]
-#pragma unroll
-      for (int j = 0; j < 4; ++j) eta_n[j] = bload1<T>(rET, en + j * K * ST, es(s));
-      const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
-      const f4 a2 = bload_frag<float>(rSV, a2tl, us + Slot::A2T).v;    // A2   [t_q x t_k]
       Frag<T> dz2bf[FT], dz2bF[FT];
       float dz2b_cs[FT];  // column sums of dZ2b (fp32)
       {
-        const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
-        f4 xhb[FT], gy[FT];
+        f4 gy[FT];
         f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          xhb[c] = ld_f32(c, Slot::XHB, us);
-          const f4 dT = transpose16(bload_frag<T>(rDO, xl + 16 * c * ST, xs(s)), I).v;  // dout, token-major
+          const f4 dT = transpose16(dof[c], I).v;  // dout, token-major
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             gy[c][j] = dT[j] * lnw_tm[c];
@@ -291,7 +324,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       {
         Frag<T> g2F[FT];
 #pragma unroll
-        for (int c = 0; c < FT; ++c) g2F[c] = to_frag<T>(transpose16(to_frag<T>(ld_f32(c, Slot::G2, us)), I).v);
+        for (int c = 0; c < FT; ++c) g2F[c] = to_frag<T>(transpose16(to_frag<T>(g2v[c]), I).v);
         f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < FT; c += 2) {
@@ -566,6 +599,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           sh.x.b.dxk[wave][f][l] = zk_;
         }
       }
+      prefetch(s > 0 ? s - 1 : 0);
       // the layer-1 state gradient: dW1 += XQ^T dZ1b + XK^T dZ1; biases
 #pragma unroll
       for (int q = 0; q < FT; ++q)
