@@ -111,7 +111,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 void* saved, size_t saved_bytes, void* stream);
 
 /* Bytes of the saved buffer of ttt_mlp_fwd / ttt_mlp_bwd: B*H*NC mini-batches
- * x ((5 FF + F) * K * sizeof(dtype) + (FF + F) * 4 + 3 * F * 64 + 4096). */
+ * x ((7 FF + F) * K * sizeof(dtype) + (FF + F) * 4 + 3 * F * 64 + 4096). */
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final

@@ -123,11 +123,11 @@ def test_mlp_saved_buffer(lib):
     n16 = lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, BF16)
     n32 = lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, F32)
     # per mini-batch: the update operands -e*G1 [K x FF] and -e*G2 [K x F] and
-    # the activations Z1, X2, Z1b, G2 W2^T [K x FF] in the activation type; the
-    # fp32 bias decrements, G2 and the two normalised [K x F] rows; four
-    # [K x K]-sized fp32 blocks (row statistics, X2b X2^T)
+    # six [K x FF] activations (gelu(Z1), gelu'(Z1), G1, Pm gelu''(Z1), gelu(Z1b),
+    # gelu'(Z1b)) in the activation type; the fp32 bias decrements, G2 and the
+    # two normalised [K x F] rows; four 1 KB fp32 blocks (row statistics, X2b X2^T)
     for n, st in ((n16, 2), (n32, 4)):
-        assert n == B * H * NC * ((5 * FF + F) * K * st + (FF + F) * 4 + 3 * K * F * 4 + 4 * 1024)
+        assert n == B * H * NC * ((7 * FF + F) * K * st + (FF + F) * 4 + 3 * K * F * 4 + 4 * 1024)
     assert lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, 9) == 0
     assert lib.ttt_mlp_saved_bytes(0, H, NC, K, F, FF, BF16) == 0
     args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10

@@ -89,7 +89,8 @@ def test_mlp_fwd_headdim32():
 def test_mlp_fwd_saved_buffer(dt):
     """Saving for the backward leaves every forward output unchanged; the saved
     bias decrements add up to the bias change over the sequence,
-    b_init - sum_s b_dec[s] = b_last; the saved X2 is gelu of the saved Z1."""
+    b_init - sum_s b_dec[s] = b_last; the saved update operand -e*G1 is -e
+    times the saved G1."""
     _say("mlp fwd saved buffer", dt)
     B, H, NC, F_, FF = 2, 2, 7, 64, 128
     d = _perturb(O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=11, dtype=dt), H, F_, FF, 12)
@@ -100,7 +101,7 @@ def test_mlp_fwd_saved_buffer(dt):
     for a, b in zip(ck0 + last0, ck1 + last1):
         assert torch.equal(a, b)
     st = 2 if dt == torch.bfloat16 else 4
-    slot = (5 * FF + F_) * 16 * st + (FF + F_) * 4 + 3 * F_ * 64 + 4096
+    slot = (7 * FF + F_) * 16 * st + (FF + F_) * 4 + 3 * F_ * 64 + 4096
     assert saved.numel() == B * H * NC * slot
     u = saved.view(B * H, NC, slot)
     b1d = u[:, :, (FF + F_) * 16 * st:(FF + F_) * 16 * st + FF * 4].contiguous().view(torch.float32)
@@ -110,16 +111,20 @@ def test_mlp_fwd_saved_buffer(dt):
     b2 = g["b2"].reshape(B * H, F_) - b2d.sum(1)
     assert max_abs(b1, last1[1].reshape(B * H, FF)) <= 1e-5 * max(1.0, float(b1.abs().max()))
     assert max_abs(b2, last1[3].reshape(B * H, F_)) <= 1e-5 * max(1.0, float(b2.abs().max()))
-    # Z1 and X2 of the slice of wave w, tile o, lane l sit at the same place in
-    # their two regions (lane order, 4 values per lane): X2 = gelu_tanh(Z1)
-    z1o = (FF + F_) * 16 * st + (FF + F_) * 4
-    x2o = z1o + 3 * FF * 16 * st
+    # the update operand -e*G1 and the saved G1 agree: both hidden-wide regions
+    # hold, for wave w, tile o and lane l = 16 g + n, four values (j) of row
+    # t = 4 g + j, hidden unit 64 w + 16 o + n
+    def hidden(off):
+        r = u[:, :, off:off + FF * 16 * st].contiguous().view(dt_).float()
+        r = r.reshape(B * H, NC, FF // 64, 4, 4, 16, 4)      # [chain, s, w, o, g, n, j]
+        return r.permute(0, 1, 4, 6, 2, 3, 5).reshape(B * H, NC, 16, FF)
     dt_ = torch.bfloat16 if st == 2 else torch.float32
-    z1 = u[:, :, z1o:z1o + FF * 16 * st].contiguous().view(dt_).float()
-    x2 = u[:, :, x2o:x2o + FF * 16 * st].contiguous().view(dt_).float()
-    ref = torch.nn.functional.gelu(z1, approximate="tanh")
-    tol = 2e-2 if st == 2 else 1e-5
-    assert float((x2 - ref).abs().max()) <= tol * max(1.0, float(ref.abs().max()))
+    g1e = hidden(0)
+    g1 = hidden((FF + F_) * 16 * st + (FF + F_) * 4 + 2 * FF * 16 * st)
+    e = g["eta"].reshape(B * H, NC, 16, 16)[:, :, 15, :].float()
+    ref = -e[..., None] * g1
+    tol = 1e-2 if st == 2 else 1e-6
+    assert float((g1e - ref).abs().max()) <= tol * max(1.0, float(ref.abs().max()))
 
 
 def _bwd(d, G):

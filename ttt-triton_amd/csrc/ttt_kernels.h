@@ -69,9 +69,11 @@ int mlp_readout_chunk_tokens();
 //     G1E [FF/64][4][64] x 4 ST   -e*G1 as W1-update operand frags, per 64-unit slice
 //     G2E [F/16][64] x 4 ST       -e*G2 as W2-update operand frags
 //     B1D [FF], B2D [F] fp32      bias decrements (b -= G^T e)
-//   forward activations (token-major C-layout tiles, lane order):
-//     Z1, Z1B, PM  [FF/64][4][64] x 4 ST   XK W1 + b1, the readout's Z1b, G2 W2^T
-//     X2           [FF/64][4][64] x 4 ST   gelu(Z1) as the W2-update operand frags
+//   forward activations (token-major C-layout tiles, lane order), with
+//   Z1 = XK W1 + b1, Pm = G2 W2^T and the readout's Z1b:
+//     X2, SP1, G1, H1    [FF/64][4][64] x 4 ST   gelu(Z1) (the W2-update operand
+//                        frags), gelu'(Z1), G1 = Pm gelu'(Z1), Pm gelu''(Z1)
+//     X2B, SP1B          [FF/64][4][64] x 4 ST   gelu(Z1b), gelu'(Z1b)
 //     G2, XH, XHB  [F/16][64] x 4 fp32     G2, normalised Z2, normalised Z2b
 //     RSTD, CC, RSB [64] x 4 fp32          per-row 1/sigma(Z2), mean(gx * xh), 1/sigma(Z2b)
 //     A2T [16][16] fp32 row-major          (X2b X2^T)^T
@@ -80,11 +82,13 @@ template <int F, int FF, int ST> struct MlpSavedSlot {
   static constexpr int G2E = G1E + FF * 16 * ST;
   static constexpr int B1D = G2E + F * 16 * ST;
   static constexpr int B2D = B1D + FF * 4;
-  static constexpr int Z1 = B2D + F * 4;
-  static constexpr int Z1B = Z1 + FF * 16 * ST;
-  static constexpr int PM = Z1B + FF * 16 * ST;
-  static constexpr int X2 = PM + FF * 16 * ST;
-  static constexpr int G2 = X2 + FF * 16 * ST;
+  static constexpr int X2 = B2D + F * 4;
+  static constexpr int SP1 = X2 + FF * 16 * ST;
+  static constexpr int G1 = SP1 + FF * 16 * ST;
+  static constexpr int H1 = G1 + FF * 16 * ST;
+  static constexpr int X2B = H1 + FF * 16 * ST;
+  static constexpr int SP1B = X2B + FF * 16 * ST;
+  static constexpr int G2 = SP1B + FF * 16 * ST;
   static constexpr int XH = G2 + F * 64;
   static constexpr int XHB = XH + F * 64;
   static constexpr int RSTD = XHB + F * 64;
@@ -94,7 +98,7 @@ template <int F, int FF, int ST> struct MlpSavedSlot {
   static constexpr int BYTES = A2T + 1024;
 };
 constexpr size_t mlp_saved_slot_bytes_of(int F, int FF, int ST) {
-  return (size_t)(5 * FF + F) * 16 * ST + (size_t)(FF + F) * 4 + (size_t)3 * F * 64 + 4 * 1024;
+  return (size_t)(7 * FF + F) * 16 * ST + (size_t)(FF + F) * 4 + (size_t)3 * F * 64 + 4 * 1024;
 }
 
 hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);

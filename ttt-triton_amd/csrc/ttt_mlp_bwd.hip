@@ -27,6 +27,9 @@
 // every wave.  Contractions over the hidden units are split by slice; their
 // [16 x F] partials meet in one 32 KB LDS exchange area, fenced by a barrier
 // after the writes and one after the reads: four barriers per mini-batch.
+// The per-slice [16 x 64] temporaries are consumed in the order they are made
+// (dX2 folds into dZ1, dG1 into dP and dZ1, the -e Q2 share straight into the
+// exchange area) so that the loop runs without spilling.
 #include "ttt_buf.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   };
   prefetch(NC - 1);
 
-  // Reverse sweep.  Regions between barriers:   A-B1 | B2 | B3
+  // Reverse sweep.  Regions between barriers:   A..P | B2a | LN2..B2b | B3
   // exchange area:                              dG2, dN1, de partials; dXQ, dXK partials
   for (int s = NC - 1; s >= 0; --s) {
     // the state after mini-batch s at the end of a checkpoint group: the next
@@ -277,7 +280,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         }
       }
 
-      // ---- readout layer 2 LayerNorm backward (every wave): dZ2b from dout
+      // ---- L: readout layer 2 LayerNorm backward (every wave): dZ2b from dout
       Frag<T> dz2bf[FT], dz2bF[FT];
       float dz2b_cs[FT];  // column sums of dZ2b (fp32)
       {
@@ -340,26 +343,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       pin_dW();
 
-      // ---- B1: readout layer 1 backward (per slice)
-      Frag<T> dz1bf[HT], dz1bF[HT], x2bf[HT];
+      // ---- B1: readout layer 1 backward (per slice): dZ1b, and dX2 = dA2^T X2b
+      Frag<T> dz1bf[HT], dz1bF[HT];
       float dz1b_cs[HT];  // column sums of dZ1b (fp32)
-      Tile dX2[HT], dZ1[HT];
+      Tile dX2[HT];
       {
         const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          f4 x2b, sp1b;
-          {
-            const f4 z = ld_hid(o, Slot::Z1B, us);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              float y, dy;
-              gelu_fwd_bwd(z[j], y, dy);
-              x2b[j] = y;
-              sp1b[j] = dy;
-            }
-          }
-          x2bf[o] = to_frag<T>(x2b);
+          const Frag<T> x2bf = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2B);
+          const f4 sp1b = ld_hid(o, Slot::SP1B, us);
           f4 dx2b = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < FT; c += 2) mma32(dx2b, dz2bF[c], dz2bF[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
@@ -369,87 +362,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dz1bf[o] = to_frag<T>(dz);
           dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
           dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
-          mma16(dX2[o].v, dA2f, x2bf[o]);  // dA2^T X2b
+          mma16(dX2[o].v, dA2f, x2bf);  // dA2^T X2b
         }
       }
-      // G1 = Pm (.) gelu'(Z1) (Pm = G2 W2^T); the derivatives of gelu at Z1
-      f4 sp1[HT], spp1[HT];
-#pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        const f4 z = ld_hid(o, Slot::Z1, us);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float dy, ddy;
-          gelu_d1_d2(z[j], dy, ddy);
-          sp1[o][j] = dy;
-          spp1[o][j] = ddy;
-        }
-      }
-      // dN1 = dZ1b G1^T (both layouts)
-      {
-        Frag<T> g1F[HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o)
-          g1F[o] = to_frag<T>(transpose16(to_frag<T>(ld_hid(o, Slot::PM, us) * sp1[o]), I).v);
-        f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; o += 2) {
-          mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
-          mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
-        }
-        sh.x.a.sm[0][wave][l] = dn;
-        sh.x.a.sm[1][wave][l] = dnT;
-      }
-      // dG1 = -M1^T dZ1b - e (XK dW1' + db1'); eta-row gradient partial (G1 . Q1 + G2 . Q2)
-      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
-      Tile dG1[HT];
-      f4 eq2[FT];  // this slice's share of -e Q2, Q2 = X2 dW2' + db2'
-      {
-        f4 m1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
-        const Frag<T> mf = to_frag<T>(-m1);
-        f4 dep = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
-#pragma unroll
-          for (int q = 0; q < FT; q += 2)
-            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
-          dG1[o].v = f4{0.f, 0.f, 0.f, 0.f};
-          mma16(dG1[o].v, mf, dz1bf[o]);
-          const f4 g1 = ld_hid(o, Slot::PM, us) * sp1[o];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dG1[o].v[j] -= e[j] * q1[j];
-            dep[j] += g1[j] * q1[j];
-          }
-        }
-        // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2; both are
-        // linear in Q2, so this slice's share goes into the partials as it is
-        // (wave 0's share carries db2')
-        Frag<T> x2F[HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
-#pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int o = 0; o < HT; o += 2)
-            mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
-          if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
-          const f4 g2 = ld_f32(c, Slot::G2, us);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dep[j] += g2[j] * q2[j];
-            eq2[c][j] = -e[j] * q2[j];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
-        sh.x.a.sm[2][wave][l] = dep;
-      }
-      // dX2 += (-e G2) dW2'^T  (contraction over features; dW2'^T frags by transposes)
+      // ---- X: dX2 += (-e G2) dW2'^T (contraction over features; dW2'^T frags by
+      //      transposes; dW2' is the gradient wrt the state after s, not yet updated)
       {
         Frag<T> eg2F[FT];
 #pragma unroll
@@ -464,31 +381,95 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
             mma32(dX2[o].v, eg2F[c], eg2F[c + 1], u0, u1);
           }
       }
-      // dP = dG1 (.) gelu'(Z1), dZ1 <- dG1 (.) Pm (.) gelu''(Z1); dG2 partial over this
-      // slice: dP W2 - e Q2 (- M2^T dZ2b, which every wave holds, added once by wave 0)
+      // ---- N: dN1 = dZ1b G1^T (both layouts), partial over this slice
       {
-        Frag<T> dPf[HT], dPF[HT];
+        Frag<T> g1F[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o)
+          g1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1), I).v);
+        f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < HT; o += 2) {
+          mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
+          mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
+        }
+        sh.x.a.sm[0][wave][l] = dn;
+        sh.x.a.sm[1][wave][l] = dnT;
+      }
+      // ---- Q: dG1 = -M1^T dZ1b - e (XK dW1' + db1'), then at once
+      //      dP = dG1 (.) gelu'(Z1) and dZ1 = dG1 (.) Pm gelu''(Z1) + dX2 (.) gelu'(Z1)
+      //      (the dZ2 W2^T part of dX2 is added after the inner-loss backward)
+      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+      Tile dZ1[HT];
+      Frag<T> dPf[HT], dPF[HT];
+      f4 dep = f4{0.f, 0.f, 0.f, 0.f};  // eta-row gradient partial (G1 . Q1 + G2 . Q2)
+      {
+        f4 m1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
+        const Frag<T> mf = to_frag<T>(-m1);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          dZ1[o].v = dG1[o].v * ld_hid(o, Slot::PM, us) * spp1[o];
-          dPf[o] = to_frag<T>(dG1[o].v * sp1[o]);
+          f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
+#pragma unroll
+          for (int q = 0; q < FT; q += 2)
+            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
+          f4 dg1 = f4{0.f, 0.f, 0.f, 0.f};
+          mma16(dg1, mf, dz1bf[o]);
+          const f4 g1 = ld_hid(o, Slot::G1, us), sp = ld_hid(o, Slot::SP1, us), h1 = ld_hid(o, Slot::H1, us);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dg1[j] -= e[j] * q1[j];
+            dep[j] += g1[j] * q1[j];
+          }
+          dZ1[o].v = dg1 * h1 + dX2[o].v * sp;
+          dPf[o] = to_frag<T>(dg1 * sp);
           dPF[o] = to_frag<T>(transpose16(dPf[o], I).v);
         }
+      }
+      // ---- P: Q2 = X2 dW2' + db2' per feature tile; dG2 partial over this slice:
+      //      dP W2 - e Q2 (- M2^T dZ2b, which every wave holds, added once by wave 0)
+      {
+        Frag<T> x2F[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
         f4 m2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) m2[j] = eta_n[j] * a2[j] + eta_n[j];
         const Frag<T> mf = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          f4 z = eq2[c];
+          f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int o = 0; o < HT; o += 2)
+            mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
+          // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2, both
+          // linear in Q2: this slice's share goes into the partials as it is
+          // (wave 0's share carries db2')
+          if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
+          const f4 g2 = ld_f32(c, Slot::G2, us);
+          f4 z;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dep[j] += g2[j] * q2[j];
+            z[j] = -e[j] * q2[j];
+          }
           mma16(z, mf, dz2bf[c]);
 #pragma unroll
           for (int o = 0; o < HT; o += 2)
             mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
           sh.x.a.part[wave][c][l] = z;
         }
-        // two terms of the layer-2 state gradient, X2b^T dZ2b + dP^T G2 (dW2' has
-        // been used)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
+        sh.x.a.sm[2][wave][l] = dep;
+      }
+      // two terms of the layer-2 state gradient, X2b^T dZ2b + dP^T G2 (dW2' has
+      // been used)
+      {
+        Frag<T> x2bf[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) x2bf[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2B);
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
           const Frag<T> g2f = to_frag<T>(ld_f32(c, Slot::G2, us));
@@ -498,8 +479,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       __syncthreads();  // (1) dG2, dN1, eta-row partials in
 
-      // ---- B2: assemble dN1, de; deta (wave 0); G2 backward (every wave); dX2, dZ1;
-      //      dXQ and dXK partials; the rest of the state gradient
+      // ---- B2a: assemble dN1, de; deta (wave 0); dG2
       f4 dA1T, dA1;
       Tile dG2[FT];
       {
@@ -534,6 +514,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       __syncthreads();  // (1x) exchange area free
       pin_dW();
+      // ---- LN2: backward of G2 = ln_fused_l2_bwd(Z2, XV - XK) (every wave)
       f4 dz2[FT], dtgt[FT];
       {
         float lw_i[FT], lb_i[FT];
@@ -562,6 +543,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           }
         }
       }
+      // ---- B2b: dZ2 into the state gradient and dX2; dZ1; dXQ and dXK partials
       Frag<T> dz1f[HT];
       {
         Frag<T> dz2F[FT];
@@ -575,9 +557,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> dz1F[HT], eg1F[HT];
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
+          f4 dx2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < FT; c += 2) mma32(dX2[o].v, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-          dZ1[o].v += dX2[o].v * sp1[o];
+          for (int c = 0; c < FT; c += 2) mma32(dx2, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+          dZ1[o].v += dx2 * ld_hid(o, Slot::SP1, us);
           dz1f[o] = to_frag<T>(dZ1[o].v);
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
           eg1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E), I).v);

@@ -19,8 +19,9 @@
 // (kernels/mlp_forward.py:84-117); memo snapshot s holds the state after
 // mini-batch s*M is applied (kernels/mlp_forward.py:193-226).  When `saved`
 // is given, every mini-batch's update operands -e*G1, -e*G2 and bias
-// decrements, and the activations its backward needs (Z1, X2, Z1b, G2 W2^T, G2,
-// the two LayerNorms' normalised rows and statistics, X2b X2^T) are written
+// decrements, and the activations its backward needs (gelu(Z1) and its first
+// two derivatives folded with G2 W2^T, gelu(Z1b) and its derivative, G2, the
+// two LayerNorms' normalised rows and statistics, X2b X2^T) are written
 // there (MlpSavedSlot layout): the backward rebuilds the state in reverse
 // from the update operands and never re-runs the forward.
 //
@@ -156,6 +157,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     Frag<T> x2f[HT];     // token-major frags of X2 (free = hidden, k = t)
     Frag<T> x2F[1][HT];  // feature-major frags of X2 (free = t, k = hidden)
     f4 gp[HT];           // gelu'(Z1)
+    f4 gpp[HT];          // gelu''(Z1)
     {
       Tile z1[1][HT];
 #pragma unroll
@@ -163,15 +165,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       gemm_pt<1, HT, FT>(z1, xk, W1);
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
-        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::Z1, to_frag<T>(z1[0][o].v));
         f4 x2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float y, dy;
-          gelu_fwd_bwd(z1[0][o].v[j], y, dy);
+          float y, dy, ddy;
+          gelu_all(z1[0][o].v[j], y, dy, ddy);
           x2[j] = y;
           gp[o][j] = dy;
+          gpp[o][j] = ddy;
         }
+        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1, to_frag<T>(gp[o]));
         x2f[o] = to_frag<T>(x2);
         if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
         x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
@@ -247,8 +250,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
           mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
         }
-        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::PM, to_frag<T>(G1[i].v));
+        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::H1, to_frag<T>(G1[i].v * gpp[i]));
         G1[i].v *= gp[i];
+        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::G1, to_frag<T>(G1[i].v));
       }
     }
 
@@ -270,10 +274,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
         mma16(zb[0][o].v, m1f, to_frag<T>(G1[o].v));
-        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::Z1B, to_frag<T>(zb[0][o].v));
-        f4 x2b;
+        f4 x2b, sp;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x2b[j] = gelu_tanh(zb[0][o].v[j]);
+        for (int j = 0; j < 4; ++j) {
+          float y, dy;
+          gelu_fwd_bwd(zb[0][o].v[j], y, dy);
+          x2b[j] = y;
+          sp[j] = dy;
+        }
+        if (want_saved) {
+          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2B, to_frag<T>(x2b));
+          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1B, to_frag<T>(sp));
+        }
         x2bF[0][o] = to_frag<T>(transpose16(to_frag<T>(x2b), I).v);
       }
     }

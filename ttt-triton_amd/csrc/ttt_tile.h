@@ -379,6 +379,18 @@ __device__ __forceinline__ void gelu_fwd_bwd(float x, float& y, float& dy) {
   y = 0.5f * x * (1.0f + t);
   dy = 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
 }
+// gelu_tanh(x), gelu_bwd(x) and gelu_bwd2(x) from one tanh evaluation
+__device__ __forceinline__ void gelu_all(float x, float& y, float& dy, float& ddy) {
+  const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
+  const float x2 = x * x;
+  const float t = tanh_f(k * x * (1.0f + c * x2));
+  const float s = 1.0f - t * t;
+  const float D = k + c3 * x2;
+  const float du = k * (1.0f + 3.0f * c * x2);
+  y = 0.5f * x * (1.0f + t);
+  dy = 0.5f * x * (s * D) + 0.5f * (1.0f + t);
+  ddy = 0.5f * s * D + 0.5f * s * du - x * t * s * du * D + c3 * x2 * s;
+}
 // gelu_bwd(x) and gelu_bwd2(x) from one tanh evaluation
 __device__ __forceinline__ void gelu_d1_d2(float x, float& dy, float& ddy) {
   const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
