@@ -36,15 +36,16 @@
 
 namespace ttt {
 
-template <int FT, int NW> union MlpBwdExchange {
-  struct {
-    f4 part[NW][FT][64];  // [16 x F] partials, one per wave
-    f4 sm[3][NW][64];     // [16 x 16] partials
-  } a;
-  struct {
-    f4 dxq[NW][FT][64];  // dXQ partials
-    f4 dxk[NW][FT][64];  // dXK partials
-  } b;
+// Exchange area, in lane order (f4 per lane), byte offsets:
+//   [16 x F] partials of wave w, feature tile c   at (w * FT + c) * 1024
+//   [16 x 16] partial k of wave w                 at PART + (k * NW + w) * 1024
+//   after the second barrier the same area holds the dXQ partials at the first
+//   offsets and the dXK partials at DXK + (w * FT + c) * 1024
+template <int FT, int NW> struct MlpBwdExchange {
+  static constexpr int PART = NW * FT * 1024;
+  static constexpr int DXK = NW * FT * 1024;
+  static constexpr int BYTES = (2 * NW * FT > NW * FT + 3 * NW ? 2 * NW * FT : NW * FT + 3 * NW) * 1024;
+  f4 mem[BYTES / 16];
 };
 
 template <int FT, int NW> struct MlpBwdShared {
@@ -108,6 +109,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
 
+  // exchange-area lane slots: all blocks, this wave's [16 x F] blocks, this
+  // wave's [16 x 16] blocks
+  using Xch = MlpBwdExchange<FT, NW>;
+  LdsLane xa(sh.x.mem, 0), xw(sh.x.mem, wave * FT * 1024), xs16(sh.x.mem, Xch::PART + wave * 1024);
+
   // gradient wrt the state after the current mini-batch (this wave's slice)
   Tile dW1[FT][HT], dW2[HT][FT];
   float db1[HT], db2[FT];
@@ -152,12 +158,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   auto ld_hid = [&](int o, int off, int us) { return frag_to_f4(bload_frag<T>(rSV, hl + o * 256 * ST, us + off)); };
   auto ld_f32 = [&](int c, int off, int us) { return bload_frag<float>(rSV, f4l + c * 1024, us + off).v; };
 
-  float lnw_tm[FT], lnb_tm[FT];
+  // LayerNorm parameters of this head, re-read (L1/L2 resident) where used
+  const rsrc_t rLW = make_rsrc(p.ln_w + (size_t)h * F, F * 4), rLB = make_rsrc(p.ln_b + (size_t)h * F, F * 4);
+  auto ln_param = [&](rsrc_t r, float (&v)[FT]) {
 #pragma unroll
-  for (int o = 0; o < FT; ++o) {
-    lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
-    lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
-  }
+    for (int o = 0; o < FT; ++o) v[o] = bload_f32(r, n * 4, o * 64);
+  };
   const Frag<T> I = identity_frag<T>();
 
   float dlnw[FT], dlnb[FT];  // LN-parameter gradient partials (wave 0)
@@ -208,6 +214,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       pin_dW();
       W1s.pin();
       W2t.pin();
+      xa.pin();
+      xw.pin();
+      xs16.pin();
 
       // inputs of the readout LayerNorm backward, requested before the state
       // rebuild so that it hides their latency
@@ -220,6 +229,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
       f4 xhb[FT], g2v[FT];
       Frag<T> dof[FT];
+      float lnw_tm[FT];
+      ln_param(rLW, lnw_tm);
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         xhb[c] = ld_f32(c, Slot::XHB, us);
@@ -227,7 +238,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         g2v[c] = ld_f32(c, Slot::G2, us);
       }
 
-      Frag<T> xk[FT], xkTf[FT], xqTf[FT];
+      Frag<T> xk[FT], xkTf[FT];
       f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
       Frag<T> x2f[HT];
       {
@@ -244,10 +255,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           x2f[o] = nx2f[o];
         }
 #pragma unroll
-        for (int q = 0; q < FT; ++q) {
-          xkTf[q] = to_frag<T>(transpose16(xk[q], I).v);
-          xqTf[q] = to_frag<T>(transpose16(xq[q], I).v);
-        }
+        for (int q = 0; q < FT; ++q) xkTf[q] = to_frag<T>(transpose16(xk[q], I).v);
 #pragma unroll
         for (int q = 0; q < FT; q += 2) {
           mma32(at, xk[q], xk[q + 1], xq[q], xq[q + 1]);  // A1^T [t_k x t_q]
@@ -324,6 +332,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
       f4 detT, dA2T, dA2;
+      Frag<T> m2f;  // -(eta o A2 + eta) for wave 0, zero for the others
+      {
+        f4 m2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m2[j] = eta_n[j] * a2[j] + eta_n[j];
+        m2f = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
+      }
       {
         Frag<T> g2F[FT];
 #pragma unroll
@@ -344,7 +359,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       pin_dW();
 
       // ---- B1: readout layer 1 backward (per slice): dZ1b, and dX2 = dA2^T X2b
-      Frag<T> dz1bf[HT], dz1bF[HT];
+      Frag<T> dz1bf[HT];
       float dz1b_cs[HT];  // column sums of dZ1b (fp32)
       Tile dX2[HT];
       {
@@ -360,7 +375,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           const f4 dz = dx2b * sp1b;
           dz1b_cs[o] = sum_col4(dz[0] + dz[1] + dz[2] + dz[3]);
           dz1bf[o] = to_frag<T>(dz);
-          dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
           dX2[o].v = f4{0.f, 0.f, 0.f, 0.f};
           mma16(dX2[o].v, dA2f, x2bf);  // dA2^T X2b
         }
@@ -387,14 +401,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
         for (int o = 0; o < HT; ++o)
           g1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1), I).v);
+        Frag<T> dz1bF[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
         f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int o = 0; o < HT; o += 2) {
           mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
           mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
         }
-        sh.x.a.sm[0][wave][l] = dn;
-        sh.x.a.sm[1][wave][l] = dnT;
+        xs16.put(0, dn);
+        xs16.put(NW * 1024, dnT);
       }
       // ---- Q: dG1 = -M1^T dZ1b - e (XK dW1' + db1'), then at once
       //      dP = dG1 (.) gelu'(Z1) and dZ1 = dG1 (.) Pm gelu''(Z1) + dX2 (.) gelu'(Z1)
@@ -425,6 +442,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dZ1[o].v = dg1 * h1 + dX2[o].v * sp;
           dPf[o] = to_frag<T>(dg1 * sp);
           dPF[o] = to_frag<T>(transpose16(dPf[o], I).v);
+          db1[o] += dz1b_cs[o];  // db1' has been used
         }
       }
       // ---- P: Q2 = X2 dW2' + db2' per feature tile; dG2 partial over this slice:
@@ -433,10 +451,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> x2F[HT];
 #pragma unroll
         for (int o = 0; o < HT; ++o) x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
-        f4 m2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) m2[j] = eta_n[j] * a2[j] + eta_n[j];
-        const Frag<T> mf = to_frag<T>(wave == 0 ? -m2 : f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
           f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
@@ -454,15 +468,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
             dep[j] += g2[j] * q2[j];
             z[j] = -e[j] * q2[j];
           }
-          mma16(z, mf, dz2bf[c]);
+          mma16(z, m2f, dz2bf[c]);
 #pragma unroll
           for (int o = 0; o < HT; o += 2)
             mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
-          sh.x.a.part[wave][c][l] = z;
+          xw.put(c * 1024, z);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) dep[j] = sum_row16(dep[j]);
-        sh.x.a.sm[2][wave][l] = dep;
+        xs16.put(2 * NW * 1024, dep);
+#pragma unroll
+        for (int c = 0; c < FT; ++c) db2[c] += dz2b_cs[c];  // db2' has been used
       }
       // two terms of the layer-2 state gradient, X2b^T dZ2b + dP^T G2 (dW2' has
       // been used)
@@ -486,15 +502,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         f4 dn1 = f4{0.f, 0.f, 0.f, 0.f}, dn1T = f4{0.f, 0.f, 0.f, 0.f}, de = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-          dn1 += sh.x.a.sm[0][w][l];
-          dn1T += sh.x.a.sm[1][w][l];
-          de += sh.x.a.sm[2][w][l];
+          dn1 += xa.get(Xch::PART + w * 1024);
+          dn1T += xa.get(Xch::PART + (NW + w) * 1024);
+          de += xa.get(Xch::PART + (2 * NW + w) * 1024);
         }
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
           dG2[c].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int w = 0; w < NW; ++w) dG2[c].v += sh.x.a.part[w][c][l];
+          for (int w = 0; w < NW; ++w) dG2[c].v += xa.get((w * FT + c) * 1024);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -514,6 +530,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       __syncthreads();  // (1x) exchange area free
       pin_dW();
+      Frag<T> xqf[FT];  // XQ again (L2-resident), for the layer-1 state gradient
+#pragma unroll
+      for (int q = 0; q < FT; ++q) xqf[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
       // ---- LN2: backward of G2 = ln_fused_l2_bwd(Z2, XV - XK) (every wave)
       f4 dz2[FT], dtgt[FT];
       {
@@ -523,6 +542,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           lw_i[c] = 0.f;
           lb_i[c] = 0.f;
         }
+        float lnw_tm[FT], lnb_tm[FT];
+        ln_param(rLW, lnw_tm);
+        ln_param(rLB, lnb_tm);
         LnL2Lite<FT> ln2;
         ln2.rstd = bload_frag<float>(rSV, f4l, us + Slot::RSTD).v;
         ln2.c = bload_frag<float>(rSV, f4l, us + Slot::CC).v;
@@ -565,6 +587,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
           eg1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E), I).v);
         }
+        Frag<T> dz1bF[HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
         // dXQ partial = dZ1b W1^T, dXK partial = dZ1 W1^T + (-e G1) dW1'^T (this slice)
 #pragma unroll
         for (int f = 0; f < FT; ++f) {
@@ -578,10 +603,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
             const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW1[f][c + 1].v), I).v);
             mma32(zk_, eg1F[c], eg1F[c + 1], u0, u1);
           }
-          sh.x.b.dxq[wave][f][l] = zq_;
-          sh.x.b.dxk[wave][f][l] = zk_;
+          xw.put(f * 1024, zq_);
+          xw.put(Xch::DXK + f * 1024, zk_);
         }
       }
+      Frag<T> xqTf[FT];
+#pragma unroll
+      for (int q = 0; q < FT; ++q) xqTf[q] = to_frag<T>(transpose16(xqf[q], I).v);
       prefetch(s > 0 ? s - 1 : 0);
       // the layer-1 state gradient: dW1 += XQ^T dZ1b + XK^T dZ1; biases
 #pragma unroll
@@ -593,14 +621,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc += dZ1[o].v[j];
-        db1[o] += sum_col4(acc) + dz1b_cs[o];
+        db1[o] += sum_col4(acc);
       }
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc += dz2[c][j];
-        db2[c] += sum_col4(acc) + dz2b_cs[c];
+        db2[c] += sum_col4(acc);
       }
       __syncthreads();  // (2) dXQ, dXK partials in
 
@@ -614,8 +642,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           f4 dxk = -dtgt[f];
 #pragma unroll
           for (int w = 0; w < NW; ++w) {
-            dxq += sh.x.b.dxq[w][f][l];
-            dxk += sh.x.b.dxk[w][f][l];
+            dxq += xa.get((w * FT + f) * 1024);
+            dxk += xa.get(Xch::DXK + (w * FT + f) * 1024);
           }
           mma16(dxq, dA1Tf, xkTf[f]);  // + dA1 XK
           mma16(dxk, dA1f, xqTf[f]);   // + dA1^T XQ

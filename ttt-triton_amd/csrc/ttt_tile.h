@@ -340,6 +340,21 @@ template <int COLS> struct LdsMat {
   }
 };
 
+// One lane's 16-byte slot in an LDS region laid out in lane order ([...][64]
+// x 16 bytes): the lane's address is a single register and every block of the
+// region a compile-time immediate offset (< 64 KB).  `pin()` as for LdsMat.
+struct LdsLane {
+  unsigned a;
+  __device__ __forceinline__ LdsLane(void* base, int byte_off) {
+    a = (unsigned)(uintptr_t)(lds_f32*)base + (unsigned)byte_off + 16u * (unsigned)lane_id();
+  }
+  __device__ __forceinline__ void pin() { asm volatile("" : "+v"(a)); }
+  __device__ __forceinline__ f4 get(int off) const { return *reinterpret_cast<lds_f4*>((lds_f32*)(uintptr_t)a + off / 4); }
+  __device__ __forceinline__ void put(int off, f4 v) const {
+    *reinterpret_cast<lds_f4*>((lds_f32*)(uintptr_t)a + off / 4) = v;
+  }
+};
+
 // Tile registers <-> scratch in register order (fully coalesced float4 per lane)
 __device__ __forceinline__ void spill_tile(float* __restrict__ x, Tile t) {
   reinterpret_cast<f4*>(x)[lane_id()] = t.v;
