@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 3
+#define TTT_AMD_ABI_VERSION 4
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -114,6 +114,10 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
  * x ((7 FF + F) * K * sizeof(dtype) + (FF + F) * 4 + 3 * F * 64 + 4096). */
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
+/* Bytes of device workspace ttt_mlp_bwd needs: B*H*NC mini-batches x
+ * (2 * FF * K * sizeof(dtype) + 2 * F * 64). */
+size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
+
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
  * state's gradient zero, as in the ops path).  Replaces ttt_mlp_scan_backward
  * (kernels/mlp_backward.py:247-651) as launched by TritonMLP._backward_core
@@ -125,14 +129,18 @@ size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype
  *   dW1, db1, dW2, db2  fp32, shapes of W1_init ... (gradient wrt the initial state)
  *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
  *   saved            the saved buffer written by that ttt_mlp_fwd call
- *                    (saved_bytes >= ttt_mlp_saved_bytes(...)) */
+ *                    (saved_bytes >= ttt_mlp_saved_bytes(...))
+ *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes of scratch
+ *                    (dZ1b, dZ1 and partial dXQ/dXK per mini-batch, handed
+ *                    from the reverse sweep to the launch that forms dXQ/dXK) */
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
                 const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,
                 const float* W2_last, const float* b2_last, const void* dout,
                 int B, int H, int NC, int K, int F, int FF, int G, int dtype, float eps,
                 void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
-                float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream);
+                float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /* Fixed-weight TTT-MLP readout over a segment of NS mini-batches:
  *   out = XQ + LN_eps(gelu(XQ W1 + b1) W2 + b2)   (no state update)

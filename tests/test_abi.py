@@ -39,6 +39,7 @@ def test_header_declares_the_abi():
     decls = _declarations()
     for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
                  "ttt_linear_bwd_workspace_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
+                 "ttt_mlp_bwd_workspace_bytes",
                  "ttt_mlp_cached_readout"):
         assert name in decls, name
 
@@ -130,13 +131,18 @@ def test_mlp_saved_buffer(lib):
         assert n == B * H * NC * ((7 * FF + F) * K * st + (FF + F) * 4 + 3 * K * F * 4 + 4 * 1024)
     assert lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, 9) == 0
     assert lib.ttt_mlp_saved_bytes(0, H, NC, K, F, FF, BF16) == 0
+    w16 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, BF16)
+    # per mini-batch: dZ1b and dZ1 [K x FF] in the activation type, two fp32 [K x F] partials
+    assert w16 == B * H * NC * (2 * FF * K * 2 + 2 * K * F * 4)
     args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
-    assert lib.ttt_mlp_bwd(*args, P, n16 - 1, None) == E_WS
-    assert lib.ttt_mlp_bwd(*args, None, n16, None) == E_WS
-    assert lib.ttt_mlp_bwd(*args, Q, n16, None) == E_ALIGN
+    assert lib.ttt_mlp_bwd(*args, P, n16 - 1, P, w16, None) == E_WS
+    assert lib.ttt_mlp_bwd(*args, None, n16, P, w16, None) == E_WS
+    assert lib.ttt_mlp_bwd(*args, Q, n16, P, w16, None) == E_ALIGN
+    assert lib.ttt_mlp_bwd(*args, P, n16, P, w16 - 1, None) == E_WS
+    assert lib.ttt_mlp_bwd(*args, P, n16, None, w16, None) == E_WS
     bad = list(args)
     bad[10] = None  # W1_last
-    assert lib.ttt_mlp_bwd(*bad, P, n16, None) == E_NULL
+    assert lib.ttt_mlp_bwd(*bad, P, n16, P, w16, None) == E_NULL
 
 
 def _readout(lib, **kw):

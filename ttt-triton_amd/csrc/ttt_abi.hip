@@ -251,12 +251,19 @@ size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype
   return (size_t)B * H * NC * ttt::mlp_saved_slot_bytes(F, FF, dtype);
 }
 
+size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
+  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
+  return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype);
+}
+
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                 const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
                 const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
                 const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
                 float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
-                float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream) {
+                float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* workspace,
+                size_t workspace_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
@@ -268,6 +275,9 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   if (saved == nullptr) return TTT_ERR_WORKSPACE;
   if (!aligned16(saved)) return TTT_ERR_ALIGN;
   if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return TTT_ERR_ALIGN;
+  if (workspace_bytes < ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
 
   ttt::MlpBwdParams p;
   p.XQ = XQ;
@@ -286,6 +296,7 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.W2_last = W2_last;
   p.b2_last = b2_last;
   p.saved = saved;
+  p.ws = workspace;
   p.dXQ = dXQ;
   p.dXK = dXK;
   p.dXV = dXV;

@@ -74,4 +74,35 @@ __device__ __forceinline__ void bstore_tile(rsrc_t r, int lane, int soff, int ld
   for (int j = 0; j < 4; ++j) bstore_f32(r, lane, soff + ((r0 + j) * ld + c0) * 4, t.v[j]);
 }
 
+// C-layout tile of a row-major [16 x ld] block in the activation type: lane
+// (g, n) gets rows 4g + j, column n (four element loads).  `voff` =
+// ((4g) * ld + n) * sizeof(T) plus any column offset; the rest is uniform.
+template <typename T> __device__ __forceinline__ Frag<T> bload_ctile(rsrc_t r, int voff, int soff, int ld);
+template <> __device__ __forceinline__ Frag<__bf16> bload_ctile<__bf16>(rsrc_t r, int voff, int soff, int ld) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  us4 u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) u[j] = __builtin_amdgcn_raw_buffer_load_b16(r, voff + j * ld * 2, soff, 0);
+  Frag<__bf16> f;
+  f.v = __builtin_bit_cast(bf4, u);
+  return f;
+}
+template <> __device__ __forceinline__ Frag<float> bload_ctile<float>(rsrc_t r, int voff, int soff, int ld) {
+  Frag<float> f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f.v[j] = bload_f32(r, voff + j * ld * 4, soff);
+  return f;
+}
+template <typename T> __device__ __forceinline__ void bstore_ctile(rsrc_t r, int voff, int soff, int ld, Frag<T> f);
+template <> __device__ __forceinline__ void bstore_ctile<__bf16>(rsrc_t r, int voff, int soff, int ld, Frag<__bf16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 u = __builtin_bit_cast(us4, f.v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(u[j], r, voff + j * ld * 2, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_ctile<float>(rsrc_t r, int voff, int soff, int ld, Frag<float> f) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bstore_f32(r, voff + j * ld * 4, soff, f.v[j]);
+}
+
 }  // namespace ttt

@@ -44,6 +44,7 @@ struct MlpBwdParams {
   const float *ln_w, *ln_b, *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
   const float *W1_last, *b1_last, *W2_last, *b2_last;
   const void* saved;  // per mini-batch values written by the forward
+  void* ws;           // per mini-batch handoff from the reverse sweep to the dXQ/dXK pass (MlpBwdWsSlot)
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   int B, H, NC, F, FF, G, NK;
@@ -100,6 +101,19 @@ template <int F, int FF, int ST> struct MlpSavedSlot {
 constexpr size_t mlp_saved_slot_bytes_of(int F, int FF, int ST) {
   return (size_t)(7 * FF + F) * 16 * ST + (size_t)(FF + F) * 4 + (size_t)3 * F * 64 + 4 * 1024;
 }
+
+// The MLP backward's handoff per (chain, mini-batch) from its reverse sweep to
+// the pass that forms dXQ and dXK (byte offsets, lane order):
+//   DZ1BF, DZ1F [FF/64][4][64] x 4 ST   dZ1b and dZ1 as frags of [16 x FF] (free = token)
+//   XQP, XKP    [F/16][64] x 4 fp32      the dXQ / dXK terms that do not involve W1
+template <int F, int FF, int ST> struct MlpBwdWsSlot {
+  static constexpr int DZ1BF = 0;
+  static constexpr int DZ1F = FF * 16 * ST;
+  static constexpr int XQP = 2 * FF * 16 * ST;
+  static constexpr int XKP = XQP + F * 64;
+  static constexpr int BYTES = XKP + F * 64;
+};
+size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype);
 
 hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
 // bytes of one (chain, mini-batch) slot of the forward's saved buffer

@@ -1,34 +1,36 @@
-// TTT-MLP backward on gfx950: one workgroup of NW = FF/64 wavefronts per
-// (batch, head) chain; wave w owns hidden units S = [64w, 64w+64).
+// TTT-MLP backward on gfx950, in two launches.
 //
-// Inputs besides the sequence: the forward's checkpoints, its final state and
-// its saved buffer, which holds for every mini-batch the state-update
-// operands and the activations the gradient needs (MlpSavedSlot).  Nothing of
-// the forward is recomputed here: each mini-batch loads its activations and
-// runs only the backward (ops/ttt_mlp.py:9-67 differentiated by hand).
+// 1. mlp_bwd_kernel: one workgroup of NW = FF/64 wavefronts per (batch, head)
+//    chain, wave w owning hidden units S = [64w, 64w+64), walks the sequence
+//    in reverse and carries the gradient wrt the state, dW1, db1, dW2, db2.
+//    Inputs besides the sequence: the forward's checkpoints, its final state
+//    and its saved buffer, which holds for every mini-batch the state-update
+//    operands and the activations the gradient needs (MlpSavedSlot): nothing
+//    of the forward is recomputed (ops/ttt_mlp.py:9-67 differentiated by hand).
+//    The products with W1 (dXQ += dZ1b W1^T, dXK += dZ1 W1^T) do not feed the
+//    recurrence, so this pass hands dZ1b and dZ1 over instead (MlpBwdWsSlot)
+//    and never needs W1.
+// 2. mlp_bwd_dx_kernel: one wave per (chain, checkpoint group, feature tile),
+//    all independent: it walks its group forward from the checkpoint, W1^T in
+//    registers, and forms dXQ and dXK.
 //
-// The fast weights are still needed (the gradient flows through products
-// with W1 and W2), so they are kept in LDS in fp32, W1 as [F][FF] and W2
-// transposed, W2^T [F][FF] (columns XOR-swizzled so both access shapes are
-// bank-conflict free): every operand orientation is a direct read, a C-layout
-// tile or a row vector.  Each wave only touches its own hidden columns of
-// both, so no barrier guards them.  Registers hold the gradient accumulators
-// dW1[:, S], dW2[S, :], db1[S], db2 -- the gradient wrt the state after the
-// mini-batch being processed -- pinned to the MFMA accumulator registers.
-//
-// Reverse sweep over checkpoint groups (kernels/mlp_backward.py:340 walks the
-// same groups; the algorithm and data flow here are our own).  A group starts
-// from the state after its last mini-batch: the next group's checkpoint, or
-// the forward's final state for the last group.  Mini-batch s first rebuilds
-// the state entering it, W1_s = W1_{s+1} + XK_s^T (e G1_s) and W2_s = W2_{s+1}
-// + X2_s^T (e G2_s), with the exact operands the forward's update used.
+// In the reverse sweep W2 is needed (the gradient flows through products with
+// it): W2^T [F][FF] lives in LDS in fp32, columns XOR-swizzled so both access
+// shapes are bank-conflict free, rebuilt per mini-batch as W2_s = W2_{s+1} +
+// X2_s^T (e G2_s) from the exact operands the forward's update used; a group
+// starts from the next group's checkpoint or the final state
+// (kernels/mlp_backward.py:340 walks the same groups; the algorithm and data
+// flow here are our own).  dW1 is accumulated in LDS as dW1^T [FF][F], so both
+// orientations it is read in are direct LDS reads; dW2 lives in the MFMA
+// accumulator registers.  Each wave only touches its own hidden rows/columns
+// of these, so no barrier guards them.
 //
 // Row-wise work on [16 x F] tiles (LayerNorm backwards) is done redundantly by
 // every wave.  Contractions over the hidden units are split by slice; their
-// [16 x F] partials meet in one 32 KB LDS exchange area, fenced by a barrier
-// after the writes and one after the reads: four barriers per mini-batch.
-// The per-slice [16 x 64] temporaries are consumed in the order they are made
-// (dX2 folds into dZ1, dG1 into dP and dZ1, the -e Q2 share straight into the
+// [16 x F] partials meet in one LDS exchange area, fenced by a barrier after
+// the writes and one after the reads: four barriers per mini-batch.  The
+// per-slice [16 x 64] temporaries are consumed in the order they are made (dX2
+// folds into dZ1, dG1 into dP and dZ1, the -e Q2 share straight into the
 // exchange area) so that the loop runs without spilling.
 #include "ttt_buf.h"
 #include "ttt_kernels.h"
@@ -39,20 +41,23 @@ namespace ttt {
 // Exchange area, in lane order (f4 per lane), byte offsets:
 //   [16 x F] partials of wave w, feature tile c   at (w * FT + c) * 1024
 //   [16 x 16] partial k of wave w                 at PART + (k * NW + w) * 1024
-//   after the second barrier the same area holds the dXQ partials at the first
-//   offsets and the dXK partials at DXK + (w * FT + c) * 1024
+//   after the second barrier the [16 x F] blocks hold the dXK partials
 template <int FT, int NW> struct MlpBwdExchange {
   static constexpr int PART = NW * FT * 1024;
-  static constexpr int DXK = NW * FT * 1024;
-  static constexpr int BYTES = (2 * NW * FT > NW * FT + 3 * NW ? 2 * NW * FT : NW * FT + 3 * NW) * 1024;
+  static constexpr int BYTES = (NW * FT + 3 * NW) * 1024;
   f4 mem[BYTES / 16];
 };
 
 template <int FT, int NW> struct MlpBwdShared {
-  float w1[16 * FT * 64 * NW];   // W1   [F][FF], swizzled
-  float w2t[16 * FT * 64 * NW];  // W2^T [F][FF], swizzled
+  float w2t[16 * FT * 64 * NW];   // W2^T  [F][FF], swizzled
+  float dw1t[16 * FT * 64 * NW];  // dW1^T [FF][F], swizzled
   MlpBwdExchange<FT, NW> x;
 };
+
+size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
+  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
+  return (size_t)2 * FF * 16 * t + (size_t)2 * F * 64;
+}
 
 template <typename T, int FT, int NW>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
@@ -81,8 +86,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
   const rsrc_t rDO = make_rsrc(static_cast<const T*>(p.dout) + xoff, xbytes);
   const rsrc_t rET = make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
-  const rsrc_t rDXQ = make_rsrc(static_cast<T*>(p.dXQ) + xoff, xbytes);
-  const rsrc_t rDXK = make_rsrc(static_cast<T*>(p.dXK) + xoff, xbytes);
   const rsrc_t rDXV = make_rsrc(static_cast<T*>(p.dXV) + xoff, xbytes);
   const rsrc_t rDET = make_rsrc(static_cast<T*>(p.deta) + eoff, ebytes);
   const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
@@ -101,10 +104,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const int a2l = (4 * g * 16 + n) * 4;            // C-layout tile of a row-major [16 x 16] fp32 block
   const int a2tl = (n * 16 + 4 * g) * 4;           // the same block transposed (row n, columns 4g..4g+3)
 
-  // checkpoints [NK][...] and the final state of this chain
-  const rsrc_t rW1c = make_rsrc(p.W1_ckpt + (size_t)chain * NK * F * FF, (unsigned)((size_t)NK * F * FF * 4));
+  // handoff to the dXQ/dXK pass, [NC] slots of this chain
+  using WS = MlpBwdWsSlot<F, FF, ST>;
+  const rsrc_t rWS = make_rsrc(static_cast<char*>(p.ws) + (size_t)chain * NC * WS::BYTES, (unsigned)(NC * WS::BYTES));
+
+  // W2 checkpoints [NK][...] and the final W2 of this chain
   const rsrc_t rW2c = make_rsrc(p.W2_ckpt + (size_t)chain * NK * FF * F, (unsigned)((size_t)NK * FF * F * 4));
-  const rsrc_t rW1l = make_rsrc(p.W1_last + (size_t)chain * F * FF, (unsigned)(F * FF * 4));
   const rsrc_t rW2l = make_rsrc(p.W2_last + (size_t)chain * FF * F, (unsigned)(FF * F * 4));
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
@@ -114,27 +119,34 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   using Xch = MlpBwdExchange<FT, NW>;
   LdsLane xa(sh.x.mem, 0), xw(sh.x.mem, wave * FT * 1024), xs16(sh.x.mem, Xch::PART + wave * 1024);
 
-  // gradient wrt the state after the current mini-batch (this wave's slice)
-  Tile dW1[FT][HT], dW2[HT][FT];
+  // gradient wrt the state after the current mini-batch (this wave's slice):
+  // dW2[S, :] in registers, dW1[:, S] in LDS (below)
+  Tile dW2[HT][FT];
   float db1[HT], db2[FT];
 #pragma unroll
   for (int i = 0; i < FT; ++i)
 #pragma unroll
-    for (int o = 0; o < HT; ++o) {
-      dW1[i][o].v = f4{0.f, 0.f, 0.f, 0.f};
-      dW2[o][i].v = f4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int o = 0; o < HT; ++o) dW2[o][i].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int o = 0; o < HT; ++o) db1[o] = 0.f;
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
-  // LDS state views (this wave's hidden columns only)
-  LdsMat<FF> W1s(sh.w1, hs), W2t(sh.w2t, hs);
-  // W1 tile [F block kb x hidden block o]: frag (free = hidden, k = feature)
-  auto w1_tile = [&](int kb, int o) { return W1s.tile(16 * kb, 16 * o); };
-  auto w1_put = [&](int kb, int o, Tile t) { W1s.put_tile(16 * kb, 16 * o, t); };
-  // W1^T frag (free = feature block f, k = hidden block c)
-  auto w1T_frag = [&](int f, int c) { return to_frag<T>(W1s.row4(16 * f, 16 * c)); };
+  // LDS views (this wave's hidden columns of W2^T, its hidden rows of dW1^T)
+  LdsMat<FF> W2t(sh.w2t, hs);
+  LdsMat<F> dW1s(sh.dw1t + hs * F, 0);
+  // dW1 tile [F block q x hidden block o] (C layout), also its frag (free = hidden, k = feature)
+  auto dw1_get = [&](int q, int o) {
+    Tile t;
+    t.v = dW1s.row4(16 * o, 16 * q);
+    return t;
+  };
+  auto dw1_put = [&](int q, int o, Tile t) { dW1s.put_row4(16 * o, 16 * q, t.v); };
+  // dW1^T frag (free = feature block q, k = hidden block o)
+  auto dw1T_frag = [&](int q, int o) { return to_frag<T>(dW1s.tile(16 * o, 16 * q).v); };
+#pragma unroll
+  for (int i = 0; i < FT; ++i)
+#pragma unroll
+    for (int o = 0; o < HT; ++o) dw1_put(i, o, Tile{f4{0.f, 0.f, 0.f, 0.f}});
   // W2 tile [hidden block o x F block c] (C layout): frag (free = feature, k = hidden)
   auto w2_tile = [&](int o, int c) {
     Tile t;
@@ -149,10 +161,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
     for (int q_ = 0; q_ < FT; ++q_)
 #pragma unroll
-      for (int o_ = 0; o_ < HT; ++o_) {
-        asm volatile("" : "+a"(dW1[q_][o_].v));
-        asm volatile("" : "+a"(dW2[o_][q_].v));
-      }
+      for (int o_ = 0; o_ < HT; ++o_) asm volatile("" : "+a"(dW2[o_][q_].v));
   };
   // saved activations
   auto ld_hid = [&](int o, int off, int us) { return frag_to_f4(bload_frag<T>(rSV, hl + o * 256 * ST, us + off)); };
@@ -174,7 +183,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   }
 
   // inputs of the first phase of a mini-batch, requested one mini-batch ahead
-  Frag<T> nxq[FT], nxk[FT], ng1e[HT], nx2f[HT], ng2e[FT];
+  Frag<T> nxq[FT], nxk[FT], nx2f[HT], ng2e[FT];
   auto prefetch = [&](int s) {
     const int u = s * Slot::BYTES;
 #pragma unroll
@@ -184,10 +193,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       ng2e[q] = bload_frag<T>(rSV, fl + q * 256 * ST, u + Slot::G2E);
     }
 #pragma unroll
-    for (int o = 0; o < HT; ++o) {
-      ng1e[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::G1E);
-      nx2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::X2);
-    }
+    for (int o = 0; o < HT; ++o) nx2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::X2);
   };
   prefetch(NC - 1);
 
@@ -198,12 +204,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     // group's checkpoint, or the final state
     if (s == NC - 1 || (s + 1) % G == 0) {
       const bool last = s == NC - 1;
-      const rsrc_t r1 = last ? rW1l : rW1c, r2 = last ? rW2l : rW2c;
+      const rsrc_t r2 = last ? rW2l : rW2c;
       const int k1 = last ? 0 : (s + 1) / G;
-#pragma unroll
-      for (int i = 0; i < FT; ++i)
-#pragma unroll
-        for (int o = 0; o < HT; ++o) w1_put(i, o, bload_tile(r1, w1l, k1 * F * FF * 4, FF, 16 * i, 16 * o));
 #pragma unroll
       for (int i = 0; i < HT; ++i)
 #pragma unroll
@@ -211,9 +213,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     }
     {
       const int us = s * Slot::BYTES;
+      const int ws_ = s * WS::BYTES;
       pin_dW();
-      W1s.pin();
       W2t.pin();
+      dW1s.pin();
       xa.pin();
       xw.pin();
       xs16.pin();
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       f4 at = f4{0.f, 0.f, 0.f, 0.f}, a = f4{0.f, 0.f, 0.f, 0.f};
       Frag<T> x2f[HT];
       {
-        Frag<T> xq[FT], g1e[HT], g2e[FT];
+        Frag<T> xq[FT], g2e[FT];
 #pragma unroll
         for (int q = 0; q < FT; ++q) {
           xq[q] = nxq[q];
@@ -250,10 +253,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           g2e[q] = ng2e[q];
         }
 #pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          g1e[o] = ng1e[o];
-          x2f[o] = nx2f[o];
-        }
+        for (int o = 0; o < HT; ++o) x2f[o] = nx2f[o];
 #pragma unroll
         for (int q = 0; q < FT; ++q) xkTf[q] = to_frag<T>(transpose16(xk[q], I).v);
 #pragma unroll
@@ -261,20 +261,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           mma32(at, xk[q], xk[q + 1], xq[q], xq[q + 1]);  // A1^T [t_k x t_q]
           mma32(a, xq[q], xq[q + 1], xk[q], xk[q + 1]);   // A1   [t_q x t_k]
         }
-        // ---- A: rebuild W1_s and W2_s (this slice) from the forward's update
-        //      operands; the tiles of one hidden (feature) block are read before
-        //      any is written back, so the LDS reads overlap
-#pragma unroll
-        for (int o = 0; o < HT; ++o) {
-          const Frag<T> ng = negate(g1e[o]);
-          Tile w[FT];
-#pragma unroll
-          for (int q = 0; q < FT; ++q) w[q] = w1_tile(q, o);
-#pragma unroll
-          for (int q = 0; q < FT; ++q) mma16(w[q].v, xkTf[q], ng);
-#pragma unroll
-          for (int q = 0; q < FT; ++q) w1_put(q, o, w[q]);
-        }
+        // ---- A: rebuild W2_s (this slice) from the forward's update operands;
+        //      the tiles of one feature block are read before any is written
+        //      back, so the LDS reads overlap
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
           const Frag<T> ng = negate(g2e[c]);
@@ -358,6 +347,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
       pin_dW();
 
+      // inputs of the layer-1 gradient phases (G1, gelu'(Z1), Pm gelu''(Z1)),
+      // requested a phase ahead
+      Frag<T> g1s[HT], sp1s[HT], h1s[HT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        g1s[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1);
+        sp1s[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::SP1);
+        h1s[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::H1);
+      }
       // ---- B1: readout layer 1 backward (per slice): dZ1b, and dX2 = dA2^T X2b
       Frag<T> dz1bf[HT];
       float dz1b_cs[HT];  // column sums of dZ1b (fp32)
@@ -400,10 +398,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> g1F[HT];
 #pragma unroll
         for (int o = 0; o < HT; ++o)
-          g1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1), I).v);
+          g1F[o] = to_frag<T>(transpose16(g1s[o], I).v);
         Frag<T> dz1bF[HT];
 #pragma unroll
-        for (int o = 0; o < HT; ++o) dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
+        for (int o = 0; o < HT; ++o) {
+          dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
+          bstore_frag<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1BF, dz1bF[o]);
+        }
         f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int o = 0; o < HT; o += 2) {
@@ -430,10 +431,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
 #pragma unroll
           for (int q = 0; q < FT; q += 2)
-            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dW1[q][o].v), to_frag<T>(dW1[q + 1][o].v));
+            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dw1_get(q, o).v), to_frag<T>(dw1_get(q + 1, o).v));
           f4 dg1 = f4{0.f, 0.f, 0.f, 0.f};
           mma16(dg1, mf, dz1bf[o]);
-          const f4 g1 = ld_hid(o, Slot::G1, us), sp = ld_hid(o, Slot::SP1, us), h1 = ld_hid(o, Slot::H1, us);
+          const f4 g1 = frag_to_f4(g1s[o]), sp = frag_to_f4(sp1s[o]), h1 = frag_to_f4(h1s[o]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             dg1[j] -= e[j] * q1[j];
@@ -493,6 +494,19 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           for (int o = 0; o < HT; ++o) mma32(dW2[o][c].v, x2bf[o], dPf[o], dz2bf[c], g2f);
         }
       }
+      // inputs of the inner-loss backward and of B2b, requested before the barrier
+      const f4 rstd2 = bload_frag<float>(rSV, f4l, us + Slot::RSTD).v;
+      const f4 cc2 = bload_frag<float>(rSV, f4l, us + Slot::CC).v;
+      f4 xh2[FT], g22[FT];
+      Frag<T> xvf[FT], g1ef[HT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        xh2[c] = ld_f32(c, Slot::XH, us);
+        g22[c] = ld_f32(c, Slot::G2, us);
+        xvf[c] = bload_frag<T>(rXV, xl + 16 * c * ST, xs(s));
+      }
+#pragma unroll
+      for (int o = 0; o < HT; ++o) g1ef[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E);
       __syncthreads();  // (1) dG2, dN1, eta-row partials in
 
       // ---- B2a: assemble dN1, de; deta (wave 0); dG2
@@ -546,15 +560,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         ln_param(rLW, lnw_tm);
         ln_param(rLB, lnb_tm);
         LnL2Lite<FT> ln2;
-        ln2.rstd = bload_frag<float>(rSV, f4l, us + Slot::RSTD).v;
-        ln2.c = bload_frag<float>(rSV, f4l, us + Slot::CC).v;
+        ln2.rstd = rstd2;
+        ln2.c = cc2;
         Tile G2[FT];
         f4 tgt[FT];
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          ln2.xh[c] = ld_f32(c, Slot::XH, us);
-          G2[c].v = ld_f32(c, Slot::G2, us);
-          tgt[c] = transpose16(bload_frag<T>(rXV, xl + 16 * c * ST, xs(s)), I).v - frag_to_f4(xkTf[c]);
+          ln2.xh[c] = xh2[c];
+          G2[c].v = g22[c];
+          tgt[c] = transpose16(xvf[c], I).v - frag_to_f4(xkTf[c]);
         }
         ln2.backward(dG2, G2, tgt, lnw_tm, lnb_tm, dz2, dtgt, lw_i, lb_i);
         if (wave == 0) {
@@ -582,29 +596,19 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           f4 dx2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < FT; c += 2) mma32(dx2, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
-          dZ1[o].v += dx2 * ld_hid(o, Slot::SP1, us);
+          dZ1[o].v += dx2 * frag_to_f4(sp1s[o]);
           dz1f[o] = to_frag<T>(dZ1[o].v);
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
-          eg1F[o] = to_frag<T>(transpose16(bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E), I).v);
+          bstore_frag<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1F, dz1F[o]);
+          eg1F[o] = to_frag<T>(transpose16(g1ef[o], I).v);
         }
-        Frag<T> dz1bF[HT];
-#pragma unroll
-        for (int o = 0; o < HT; ++o) dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
-        // dXQ partial = dZ1b W1^T, dXK partial = dZ1 W1^T + (-e G1) dW1'^T (this slice)
+        // dXK partial over this slice: (-e G1) dW1'^T (dW1' not yet updated)
 #pragma unroll
         for (int f = 0; f < FT; ++f) {
-          f4 zq_ = f4{0.f, 0.f, 0.f, 0.f}, zk_ = f4{0.f, 0.f, 0.f, 0.f};
+          f4 zk_ = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < HT; c += 2) {
-            const Frag<T> v0 = w1T_frag(f, c), v1 = w1T_frag(f, c + 1);
-            mma32(zq_, dz1bF[c], dz1bF[c + 1], v0, v1);
-            mma32(zk_, dz1F[c], dz1F[c + 1], v0, v1);
-            const Frag<T> u0 = to_frag<T>(transpose16(to_frag<T>(dW1[f][c].v), I).v);
-            const Frag<T> u1 = to_frag<T>(transpose16(to_frag<T>(dW1[f][c + 1].v), I).v);
-            mma32(zk_, eg1F[c], eg1F[c + 1], u0, u1);
-          }
-          xw.put(f * 1024, zq_);
-          xw.put(Xch::DXK + f * 1024, zk_);
+          for (int c = 0; c < HT; c += 2) mma32(zk_, eg1F[c], eg1F[c + 1], dw1T_frag(f, c), dw1T_frag(f, c + 1));
+          xw.put(f * 1024, zk_);
         }
       }
       Frag<T> xqTf[FT];
@@ -613,9 +617,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       prefetch(s > 0 ? s - 1 : 0);
       // the layer-1 state gradient: dW1 += XQ^T dZ1b + XK^T dZ1; biases
 #pragma unroll
-      for (int q = 0; q < FT; ++q)
+      for (int o = 0; o < HT; ++o) {
+        Tile w[FT];
 #pragma unroll
-        for (int o = 0; o < HT; ++o) mma32(dW1[q][o].v, xqTf[q], xkTf[q], dz1bf[o], dz1f[o]);
+        for (int q = 0; q < FT; ++q) w[q] = dw1_get(q, o);
+#pragma unroll
+        for (int q = 0; q < FT; ++q) mma32(w[q].v, xqTf[q], xkTf[q], dz1bf[o], dz1f[o]);
+#pragma unroll
+        for (int q = 0; q < FT; ++q) dw1_put(q, o, w[q]);
+      }
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
         float acc = 0.f;
@@ -630,9 +640,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int j = 0; j < 4; ++j) acc += dz2[c][j];
         db2[c] += sum_col4(acc);
       }
-      __syncthreads();  // (2) dXQ, dXK partials in
+      __syncthreads();  // (2) dXK partials in
 
-      // ---- B3: dXQ, dXK, dXV (tile owners)
+      // ---- B3: the dXQ / dXK terms without W1 (to the handoff), dXV (tile owners)
       {
         const Frag<T> dA1Tf = to_frag<T>(dA1T), dA1f = to_frag<T>(dA1);
 #pragma unroll
@@ -641,14 +651,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           f4 dxq = transpose16(bload_frag<T>(rDO, xl + 16 * f * ST, xs(s)), I).v;
           f4 dxk = -dtgt[f];
 #pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            dxq += xa.get((w * FT + f) * 1024);
-            dxk += xa.get(Xch::DXK + (w * FT + f) * 1024);
-          }
+          for (int w = 0; w < NW; ++w) dxk += xa.get((w * FT + f) * 1024);
           mma16(dxq, dA1Tf, xkTf[f]);  // + dA1 XK
           mma16(dxk, dA1f, xqTf[f]);   // + dA1^T XQ
-          bstore_frag<T>(rDXQ, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dxq), I).v));
-          bstore_frag<T>(rDXK, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dxk), I).v));
+          bstore_frag<float>(rWS, f4l + f * 1024, ws_ + WS::XQP, Frag<float>{dxq});
+          bstore_frag<float>(rWS, f4l + f * 1024, ws_ + WS::XKP, Frag<float>{dxk});
           bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dtgt[f]), I).v));
         }
       }
@@ -663,7 +670,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < HT; ++o) bstore_tile(rdW1, w1l, 0, FF, 16 * i, 16 * o, dW1[i][o]);
+      for (int o = 0; o < HT; ++o) bstore_tile(rdW1, w1l, 0, FF, 16 * i, 16 * o, dw1_get(i, o));
 #pragma unroll
     for (int i = 0; i < HT; ++i)
 #pragma unroll
@@ -687,9 +694,101 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   }
 }
 
+// dXQ = (dout + dA1 XK) + dZ1b W1_s^T and dXK = (-dtgt + dA1^T XQ - e G1 dW1'^T)
+// + dZ1 W1_s^T for every mini-batch s, the bracketed terms from the reverse
+// sweep's handoff.  One wave per (chain, checkpoint group, feature tile c):
+// W1_s^T[:, c] (FF/16 tiles [16 hidden x 16 features]) starts from the group's
+// checkpoint and steps forward with the saved update operands,
+// W1_{s+1}^T = W1_s^T + (-e G1_s)^T XK_s.
+template <typename T, int FT, int NW>
+__global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
+  constexpr int F = 16 * FT;
+  constexpr int K = 16;
+  constexpr int FF = 64 * NW;
+  constexpr int HB = FF / 16;  // hidden blocks
+  constexpr int ST = (int)sizeof(T);
+  using Slot = MlpSavedSlot<F, FF, ST>;
+  using WS = MlpBwdWsSlot<F, FF, ST>;
+  const int NC = p.NC, G = p.G, NK = p.NK;
+  const int chain = blockIdx.x / NK, kk = blockIdx.x - chain * NK;
+  const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // feature tile
+  const int l = lane_id(), g = l >> 4, n = l & 15;
+
+  const size_t xoff = (size_t)chain * NC * K * F;
+  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST);
+  const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
+  const rsrc_t rDXQ = make_rsrc(static_cast<T*>(p.dXQ) + xoff, xbytes);
+  const rsrc_t rDXK = make_rsrc(static_cast<T*>(p.dXK) + xoff, xbytes);
+  const rsrc_t rSV = make_rsrc(static_cast<const char*>(p.saved) + (size_t)chain * NC * Slot::BYTES,
+                               (unsigned)(NC * Slot::BYTES));
+  const rsrc_t rWS = make_rsrc(static_cast<const char*>(p.ws) + (size_t)chain * NC * WS::BYTES,
+                               (unsigned)(NC * WS::BYTES));
+  const int xcl = (4 * g * F + n) * ST + 16 * c * ST;  // C-layout tile of feature tile c in a [16 x F] block
+  const int hl = l * 4 * ST;                           // + hb * 256 * ST: hidden block hb, lane order
+  const int f4l = l * 16 + c * 1024;                   // fp32 tile c, lane order
+
+  // W1^T tiles [hidden block hb x feature tile c]: lane (g, n) holds
+  // W1[16c + n][16 hb + 4g + j], one 16-byte read per tile from the [F][FF] checkpoint
+  Tile w[HB];
+  {
+    const rsrc_t rW1c = make_rsrc(p.W1_ckpt + (size_t)chain * NK * F * FF, (unsigned)((size_t)NK * F * FF * 4));
+    const int wl = ((16 * c + n) * FF + 4 * g) * 4;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) w[hb].v = bload_frag<float>(rW1c, wl + hb * 64, kk * F * FF * 4).v;
+  }
+  // per mini-batch inputs, requested one mini-batch ahead
+  struct In {
+    f4 aq, ak;
+    Frag<T> zb[HB], zk[HB];
+  };
+  auto load_in = [&](int s, In& in) {
+    const int ws_ = s * WS::BYTES;
+    in.aq = bload_frag<float>(rWS, f4l, ws_ + WS::XQP).v;
+    in.ak = bload_frag<float>(rWS, f4l, ws_ + WS::XKP).v;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      in.zb[hb] = bload_frag<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1BF);
+      in.zk[hb] = bload_frag<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1F);
+    }
+  };
+  const int s0 = kk * G, s1 = min(s0 + G, NC);
+  In cur;
+  load_in(s0, cur);
+  for (int s = s0; s < s1; ++s) {
+    const int us = s * Slot::BYTES, xo = s * K * F * ST;
+    In nxt;
+    load_in(s + 1 < s1 ? s + 1 : s, nxt);
+    Frag<T> g1e[HB];
+    Frag<T> xkT;
+    const bool step = s + 1 < s1;
+    if (step) {
+      xkT = bload_ctile<T>(rXK, xcl, xo, F);  // XK^T frag of feature tile c
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) g1e[hb] = bload_frag<T>(rSV, hl + hb * 256 * ST, us + Slot::G1E);
+    }
+    f4 aq = cur.aq, ak = cur.ak;
+#pragma unroll
+    for (int hb = 0; hb < HB; hb += 2) {
+      const Frag<T> w0 = to_frag<T>(w[hb].v), w1 = to_frag<T>(w[hb + 1].v);
+      mma32(aq, cur.zb[hb], cur.zb[hb + 1], w0, w1);
+      mma32(ak, cur.zk[hb], cur.zk[hb + 1], w0, w1);
+    }
+    bstore_ctile<T>(rDXQ, xcl, xo, F, to_frag<T>(aq));
+    bstore_ctile<T>(rDXK, xcl, xo, F, to_frag<T>(ak));
+    if (step) {
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) mma16(w[hb].v, g1e[hb], xkT);
+    }
+    cur = nxt;
+  }
+}
+
 template <typename T, int FT, int NW>
 static hipError_t launch_mlp_bwd_t(const MlpBwdParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW>), dim3(p.B * p.H * p.NK), dim3(64 * FT), 0, stream, p);
   return hipGetLastError();
 }
 

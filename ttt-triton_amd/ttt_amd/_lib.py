@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -32,7 +32,8 @@ SIGNATURES = {
                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),
     "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 13 + [_P, _S, _P]),
     "ttt_mlp_saved_bytes": (_S, [_I] * 7),
-    "ttt_mlp_bwd": (_I, [_P] * 15 + [_I] * 8 + [_F] + [_P] * 10 + [_P, _S, _P]),
+    "ttt_mlp_bwd_workspace_bytes": (_S, [_I] * 7),
+    "ttt_mlp_bwd": (_I, [_P] * 15 + [_I] * 8 + [_F] + [_P] * 10 + [_P, _S, _P, _S, _P]),
     "ttt_mlp_cached_readout": (_I, [_P] * 7 + [_I] * 8 + [_F] + [_P, _P]),
 }
 

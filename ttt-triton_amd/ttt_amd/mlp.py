@@ -113,13 +113,14 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     dW2, db2 = torch.empty((B, H, FF, F), **f32), torch.empty((B, H, 1, F), **f32)
     dlw, dlb = torch.empty((B, H, F), **f32), torch.empty((B, H, F), **f32)
     lib = _lib.load()
+    ws = torch.empty(lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, code), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_bwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), *(ptr(t) for t in ckpt),
             *(ptr(t) for t in last), ptr(do),
             B, H, NC, K, F, FF, int(G), code, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
-            ptr(saved), saved.numel(), stream_of(dev))
+            ptr(saved), saved.numel(), ptr(ws), ws.numel(), stream_of(dev))
     _lib.check(st, "ttt_mlp_bwd")
     return (dlw.sum(0), dlb.sum(0), dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
 
