@@ -277,6 +277,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         }
       }
 
+      // inputs of B1 and X, requested before the LayerNorm backward
+      Frag<T> x2bs[HT], sp1bs[HT], g2es[FT];
+#pragma unroll
+      for (int o = 0; o < HT; ++o) {
+        x2bs[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2B);
+        sp1bs[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::SP1B);
+      }
+#pragma unroll
+      for (int c = 0; c < FT; ++c) g2es[c] = bload_frag<T>(rSV, fl + c * 256 * ST, us + Slot::G2E);
+
       // ---- L: readout layer 2 LayerNorm backward (every wave): dZ2b from dout
       Frag<T> dz2bf[FT], dz2bF[FT];
       float dz2b_cs[FT];  // column sums of dZ2b (fp32)
@@ -364,8 +374,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         const Frag<T> dA2Tf = to_frag<T>(dA2T), dA2f = to_frag<T>(dA2);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
-          const Frag<T> x2bf = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2B);
-          const f4 sp1b = ld_hid(o, Slot::SP1B, us);
+          const Frag<T> x2bf = x2bs[o];
+          const f4 sp1b = frag_to_f4(sp1bs[o]);
           f4 dx2b = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < FT; c += 2) mma32(dx2b, dz2bF[c], dz2bF[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
@@ -383,7 +393,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> eg2F[FT];
 #pragma unroll
         for (int c = 0; c < FT; ++c)
-          eg2F[c] = to_frag<T>(transpose16(bload_frag<T>(rSV, fl + c * 256 * ST, us + Slot::G2E), I).v);
+          eg2F[c] = to_frag<T>(transpose16(g2es[c], I).v);
 #pragma unroll
         for (int o = 0; o < HT; ++o)
 #pragma unroll
@@ -414,6 +424,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         xs16.put(0, dn);
         xs16.put(NW * 1024, dnT);
       }
+      f4 g2p[FT];  // G2, for P and the layer-2 state gradient
+#pragma unroll
+      for (int c = 0; c < FT; ++c) g2p[c] = ld_f32(c, Slot::G2, us);
       // ---- Q: dG1 = -M1^T dZ1b - e (XK dW1' + db1'), then at once
       //      dP = dG1 (.) gelu'(Z1) and dZ1 = dG1 (.) Pm gelu''(Z1) + dX2 (.) gelu'(Z1)
       //      (the dZ2 W2^T part of dX2 is added after the inner-loss backward)
@@ -462,7 +475,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           // linear in Q2: this slice's share goes into the partials as it is
           // (wave 0's share carries db2')
           if (wave == 0) q2 += f4{db2[c], db2[c], db2[c], db2[c]};
-          const f4 g2 = ld_f32(c, Slot::G2, us);
+          const f4 g2 = g2p[c];
           f4 z;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -486,10 +499,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       {
         Frag<T> x2bf[HT];
 #pragma unroll
-        for (int o = 0; o < HT; ++o) x2bf[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::X2B);
+        for (int o = 0; o < HT; ++o) x2bf[o] = x2bs[o];
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          const Frag<T> g2f = to_frag<T>(ld_f32(c, Slot::G2, us));
+          const Frag<T> g2f = to_frag<T>(g2p[c]);
 #pragma unroll
           for (int o = 0; o < HT; ++o) mma32(dW2[o][c].v, x2bf[o], dPf[o], dz2bf[c], g2f);
         }
@@ -507,6 +520,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       }
 #pragma unroll
       for (int o = 0; o < HT; ++o) g1ef[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E);
+      float lnw2[FT], lnb2[FT];
+      ln_param(rLW, lnw2);
+      ln_param(rLB, lnb2);
       __syncthreads();  // (1) dG2, dN1, eta-row partials in
 
       // ---- B2a: assemble dN1, de; deta (wave 0); dG2
@@ -557,8 +573,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           lb_i[c] = 0.f;
         }
         float lnw_tm[FT], lnb_tm[FT];
-        ln_param(rLW, lnw_tm);
-        ln_param(rLB, lnb_tm);
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          lnw_tm[c] = lnw2[c];
+          lnb_tm[c] = lnb2[c];
+        }
         LnL2Lite<FT> ln2;
         ln2.rstd = rstd2;
         ln2.c = cc2;
