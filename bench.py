@@ -218,12 +218,12 @@ def run_linear(torch, O, steps, warmup, only=None):
     keys = ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")
 
     def fwd():
-        out, ck, _ = linear_forward(*(g[k] for k in keys), G_LIN, want_ckpt=True)
-        return out, ck
+        out, ck, last, saved = linear_forward(*(g[k] for k in keys), G_LIN, want_ckpt=True, want_last=True,
+                                              want_saved=True)
+        return out, (ck[0], last[0], saved)
 
     def bwd(ck):
-        return linear_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck[0], ck[1],
-                               g["dOut"], G_LIN)
+        return linear_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], *ck, g["dOut"], G_LIN)
 
     _, ck = fwd()
     for _ in range(warmup):

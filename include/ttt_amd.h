@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 4
+#define TTT_AMD_ABI_VERSION 5
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -58,31 +58,43 @@ const char* ttt_error_string(int status);
  *   out         [B,H,NC,K,F] dtype      (XQ + LN(Z1_bar) per mini-batch)
  *   W1_last, b1_last  [B,H,F,F], [B,H,1,F] fp32, final state (both or neither)
  *   W1_ckpt, b1_ckpt  [B,H,NK,F,F], [B,H,NK,1,F] fp32, state entering
- *                     mini-batch k*G (both or neither; needed by the backward) */
+ *                     mini-batch k*G (both or neither; needed by the backward)
+ *   saved             NULL, or >= ttt_linear_saved_bytes(...) bytes: receives,
+ *                     for every mini-batch, the inner-loss gradient and the
+ *                     normalised pre-LN values with their statistics that
+ *                     ttt_linear_bwd needs.  It has no counterpart in the
+ *                     reference, whose backward re-runs each checkpoint group
+ *                     forward to recover them.
+ * NC times the per-mini-batch saved size must stay below 2^31 bytes. */
 int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                    const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
                    int B, int H, int NC, int K, int F, int G, int dtype, float eps,
                    void* out, float* W1_last, float* b1_last, float* W1_ckpt, float* b1_ckpt,
-                   void* stream);
+                   void* saved, size_t saved_bytes, void* stream);
 
-/* Bytes of device workspace ttt_linear_bwd needs for these sizes. */
-size_t ttt_linear_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int G);
+/* Bytes of the saved buffer of ttt_linear_fwd / ttt_linear_bwd: B*H*NC
+ * mini-batches x (3 * F * 64 + 256); 0 for unsupported sizes. */
+size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F);
 
 /* TTT-Linear backward: gradients of sum(out * dout) wrt every input, the
  * final state's gradient taken as zero (the ops path discards W_last).
  * Replaces ttt_linear_scan_backward (kernels/linear_backward.py:207-520) as
  * launched by TritonLinear._backward_core (linear_triton.py:146-265).
- *   W1_ckpt, b1_ckpt   checkpoints written by ttt_linear_fwd with the same G
- *   dout               [B,H,NC,K,F] dtype
- *   dXQ, dXK, dXV      [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
- *   dW1, db1           [B,H,F,F], [B,H,1,F] fp32 (gradient wrt W1_init, b1_init)
- *   dln_w, dln_b       [B,H,F] fp32 per-chain partials; sum over B for [H,F]
- *   workspace          >= ttt_linear_bwd_workspace_bytes(...) bytes */
+ *   W1_ckpt           weight checkpoints written by ttt_linear_fwd with the same G
+ *   W1_last           the final weight written by that ttt_linear_fwd call
+ *   dout              [B,H,NC,K,F] dtype
+ *   dXQ, dXK, dXV     [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
+ *   dW1, db1          [B,H,F,F], [B,H,1,F] fp32 (gradient wrt W1_init, b1_init)
+ *   dln_w, dln_b      [B,H,F] fp32 per-chain partials; sum over B for [H,F]
+ *   saved             the saved buffer written by that ttt_linear_fwd call
+ *                     (saved_bytes >= ttt_linear_saved_bytes(...))
+ * The bias checkpoints are not needed: the saved values carry everything the
+ * bias entered. */
 int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
-                   const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
+                   const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* W1_last,
                    const void* dout, int B, int H, int NC, int K, int F, int G, int dtype, float eps,
                    void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1,
-                   float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes, void* stream);
+                   float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream);
 
 /* TTT-MLP forward (2-layer GELU(tanh) fast-weight MLP) over all NC
  * mini-batches.  Replaces ttt_mlp_scan_forward (kernels/mlp_forward.py:6-237)

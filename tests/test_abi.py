@@ -38,7 +38,7 @@ def lib():
 def test_header_declares_the_abi():
     decls = _declarations()
     for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
-                 "ttt_linear_bwd_workspace_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
+                 "ttt_linear_saved_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
                  "ttt_mlp_bwd_workspace_bytes",
                  "ttt_mlp_cached_readout"):
         assert name in decls, name
@@ -63,7 +63,7 @@ def test_version_and_error_strings(lib):
 
 def _lin_fwd(lib, **kw):
     a = dict(XQ=P, XK=P, XV=P, eta=P, lw=P, lb=P, W=P, b=P, B=2, H=4, NC=16, K=16, F=64, G=4, dtype=F32,
-             eps=1e-8, out=P, Wl=None, bl=None, Wc=None, bc=None, stream=None)
+             eps=1e-8, out=P, Wl=None, bl=None, Wc=None, bc=None, saved=None, saved_bytes=0, stream=None)
     a.update(kw)
     return lib.ttt_linear_fwd(*a.values())
 
@@ -83,18 +83,25 @@ def test_linear_fwd_validation(lib):
     assert _lin_fwd(lib, Wl=P, bl=None, Wc=Q, bc=P, XQ=P, K=16) in (E_NULL, E_ALIGN)
 
 
-def test_linear_bwd_workspace(lib):
-    B, H, NC, K, F, G = 2, 4, 16, 16, 64, 4
-    need = lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, G)
-    assert need == B * H * G * K * F * 4
-    assert lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, 99) == B * H * NC * K * F * 4
-    assert lib.ttt_linear_bwd_workspace_bytes(0, H, NC, K, F, G) == 0
-    args = [P] * 9 + [B, H, NC, K, F, G, F32, 1e-8] + [P] * 8
+def test_linear_saved_buffer(lib):
+    B, H, NC, K, F = 2, 4, 16, 16, 64
+    need = lib.ttt_linear_saved_bytes(B, H, NC, K, F)
+    # per mini-batch: G, normalised Z1 and Zb (fp32, K x F each) and 3 x 16 statistics padded to 256 bytes
+    assert need == B * H * NC * (3 * K * F * 4 + 256)
+    assert lib.ttt_linear_saved_bytes(B, H, NC, K, 32) == B * H * NC * (3 * K * 32 * 4 + 256)
+    assert lib.ttt_linear_saved_bytes(0, H, NC, K, F) == 0
+    assert lib.ttt_linear_saved_bytes(B, H, NC, 8, F) == 0
+    assert _lin_fwd(lib, saved=P, saved_bytes=need - 4) == E_WS
+    assert _lin_fwd(lib, saved=Q, saved_bytes=need) == E_ALIGN
+    args = [P] * 9 + [B, H, NC, K, F, 4, F32, 1e-8] + [P] * 8
     assert lib.ttt_linear_bwd(*args, P, need - 4, None) == E_WS
     assert lib.ttt_linear_bwd(*args, None, need, None) == E_WS
     assert lib.ttt_linear_bwd(*args, Q, need, None) == E_ALIGN
     bad = list(args)
     bad[8] = None  # dout
+    assert lib.ttt_linear_bwd(*bad, P, need, None) == E_NULL
+    bad = list(args)
+    bad[7] = None  # W1_last
     assert lib.ttt_linear_bwd(*bad, P, need, None) == E_NULL
 
 

@@ -29,11 +29,63 @@ def _say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _fwd(d, G, want_last=True):
+def _fwd(d, G, want_last=True, want_saved=False):
     from ttt_amd.linear import linear_forward
     g = to_dev(d)
-    return linear_forward(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["XQ"], g["XV"], g["XK"], g["eta"], G,
-                          want_ckpt=True, want_last=want_last)
+    res = linear_forward(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["XQ"], g["XV"], g["XK"], g["eta"], G,
+                         want_ckpt=True, want_last=want_last, want_saved=want_saved)
+    return res if want_saved else res[:3]
+
+
+def _unpack_saved(saved, B, H, NC, F_):
+    """Saved slots -> per mini-batch G, XH, XHB [B,H,NC,16,F] and RSTD, CC, RSB [B,H,NC,16].
+    G and XH are token-major tiles in lane order (tile o, lane (g, n), register j
+    holds row 4g + j, column 16o + n); XHB is feature-major (token n, feature
+    16o + 4g + j)."""
+    FT = F_ // 16
+    slot = 3 * F_ * 64 + 256
+    raw = saved.view(torch.float32).reshape(B, H, NC, slot // 4)
+    tiles = raw[..., : 3 * F_ * 16].reshape(B, H, NC, 3, FT, 4, 16, 4)  # [.., part, o, g, n, j]
+    tm = tiles.permute(0, 1, 2, 3, 5, 7, 4, 6).reshape(B, H, NC, 3, 16, F_)   # [g, j, o, n]
+    fm = tiles.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, NC, 3, 16, F_)   # [n, o, g, j]
+    stats = raw[..., 3 * F_ * 16:3 * F_ * 16 + 48].reshape(B, H, NC, 3, 16)
+    return dict(G=tm[:, :, :, 0], XH=tm[:, :, :, 1], XHB=fm[:, :, :, 2], RSTD=stats[:, :, :, 0],
+                CC=stats[:, :, :, 1], RSB=stats[:, :, :, 2])
+
+
+def test_linear_fwd_saved_buffer():
+    """The saved values reproduce the state update and the readout, and saving
+    leaves every output unchanged."""
+    _say("linear fwd saved buffer fp32")
+    B, H, NC, F_ = 2, 2, 6, 64
+    d = O.make_inputs(B, H, NC, 16, F_, seed=11, dtype=torch.float32, eta_kind="layer")
+    gen = torch.Generator().manual_seed(12)
+    d["ln_w"] = 1 + 0.2 * torch.randn(H, F_, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(H, F_, generator=gen)
+    out0, (Wc0, bc0), (Wl0, bl0) = _fwd(d, G=4)
+    out, (Wc, bc), (Wl, bl), saved = _fwd(d, G=4, want_saved=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out0) and torch.equal(Wl, Wl0) and torch.equal(bl, bl0) and torch.equal(Wc, Wc0)
+    sv = {k: v.cpu().double() for k, v in _unpack_saved(saved, B, H, NC, F_).items()}
+    XK, XV, XQ = d["XK"].double(), d["XV"].double(), d["XQ"].double()
+    e = d["eta"].double()[..., -1, :]                                   # [B,H,NC,K]
+    # W_last = W_init - sum_s XK_s^T diag(e_s) G_s ; b_last = b_init - sum_s G_s^T e_s
+    dW = torch.einsum("bhstf,bhst,bhsto->bhfo", XK, e, sv["G"])
+    assert max_abs(Wl, d["W1"].double() - dW) <= 1e-4
+    db = torch.einsum("bhst,bhsto->bho", e, sv["G"]).unsqueeze(2)
+    assert max_abs(bl, d["b1"].double() - db) <= 1e-4
+    # G from the saved normalised Z1 and its statistics (ops/ttt_utils.py:21-48)
+    lw, lb = d["ln_w"].double()[None, :, None, None, :], d["ln_b"].double()[None, :, None, None, :]
+    xh = sv["XH"]
+    gx = (lw * xh + lb - (XV - XK)) * lw
+    G = (gx - gx.mean(-1, keepdim=True) - xh * sv["CC"][..., None]) * sv["RSTD"][..., None]
+    assert max_abs(G, sv["G"]) <= 1e-4
+    assert max_abs(sv["CC"], (gx * xh).mean(-1)) <= 1e-4
+    assert max_abs(xh.mean(-1), torch.zeros_like(sv["RSTD"])) <= 1e-4
+    # readout: out = XQ + ln_w * XHB + ln_b, XHB normalised per token
+    assert max_abs(out, XQ + lw * sv["XHB"] + lb) <= 1e-4
+    assert max_abs(sv["XHB"].pow(2).mean(-1), torch.ones_like(sv["RSB"])) <= 1e-3
+    assert bool((sv["RSB"] > 0).all()) and bool((sv["RSTD"] > 0).all())
 
 
 @pytest.mark.parametrize("kind", ["causal", "layer"])
@@ -97,9 +149,9 @@ def test_linear_fwd_deterministic():
 def _bwd(d, dout, G):
     from ttt_amd.linear import linear_backward
     g = to_dev(d)
-    _, (Wc, bc), _ = _fwd(d, G, want_last=False)
+    _, (Wc, _), (Wl, _), saved = _fwd(d, G, want_saved=True)
     (dlw, dlb, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
-        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, bc, dout.cuda(), G)
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, Wl, saved, dout.cuda(), G)
     return dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW, db1=db, dln_w=dlw, dln_b=dlb)
 
 

@@ -42,6 +42,12 @@ int check_mlp(int NC, int F, int FF, int dtype) {
   return TTT_OK;
 }
 
+// TTT-Linear: per-chain saved slots addressed with 32-bit byte offsets
+int check_linear(int NC, int F) {
+  if ((long long)NC * ttt::linear_saved_slot_bytes(F) > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return TTT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -62,11 +68,18 @@ const char* ttt_error_string(int status) {
   }
 }
 
+size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K != 16 || (F != 32 && F != 64)) return 0;
+  return (size_t)B * H * NC * ttt::linear_saved_slot_bytes(F);
+}
+
 int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                    const float* ln_b, const float* W1_init, const float* b1_init, int B, int H, int NC, int K,
                    int F, int G, int dtype, float eps, void* out, float* W1_last, float* b1_last, float* W1_ckpt,
-                   float* b1_ckpt, void* stream) {
+                   float* b1_ckpt, void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  st = check_linear(NC, F);
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
@@ -83,6 +96,10 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   OPTIONAL_PTR(b1_ckpt);
   if ((W1_last == nullptr) != (b1_last == nullptr)) return TTT_ERR_NULL;
   if ((W1_ckpt == nullptr) != (b1_ckpt == nullptr)) return TTT_ERR_NULL;
+  if (saved != nullptr) {
+    if (!aligned16(saved)) return TTT_ERR_ALIGN;
+    if (saved_bytes < ttt_linear_saved_bytes(B, H, NC, K, F)) return TTT_ERR_WORKSPACE;
+  }
 
   ttt::LinearFwdParams p;
   p.XQ = XQ;
@@ -98,6 +115,7 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   p.b_last = b1_last;
   p.W_ckpt = W1_ckpt;
   p.b_ckpt = b1_ckpt;
+  p.saved = saved;
   p.B = B;
   p.H = H;
   p.NC = NC;
@@ -108,18 +126,14 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   return hip_status(ttt::launch_linear_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
-size_t ttt_linear_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int G) {
-  if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || G <= 0) return 0;
-  const int g = G < NC ? G : NC;
-  return (size_t)B * H * g * K * F * sizeof(float);
-}
-
 int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
-                   const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const void* dout, int B, int H,
+                   const float* ln_b, const float* W1_ckpt, const float* W1_last, const void* dout, int B, int H,
                    int NC, int K, int F, int G, int dtype, float eps, void* dXQ, void* dXK, void* dXV, void* deta,
-                   float* dW1, float* db1, float* dln_w, float* dln_b, void* workspace, size_t workspace_bytes,
+                   float* dW1, float* db1, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes,
                    void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
+  if (st != TTT_OK) return st;
+  st = check_linear(NC, F);
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
@@ -128,7 +142,7 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   REQUIRE_PTR(ln_w);
   REQUIRE_PTR(ln_b);
   REQUIRE_PTR(W1_ckpt);
-  REQUIRE_PTR(b1_ckpt);
+  REQUIRE_PTR(W1_last);
   REQUIRE_PTR(dout);
   REQUIRE_PTR(dXQ);
   REQUIRE_PTR(dXK);
@@ -138,9 +152,9 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   REQUIRE_PTR(db1);
   REQUIRE_PTR(dln_w);
   REQUIRE_PTR(dln_b);
-  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return TTT_ERR_ALIGN;
-  if (workspace_bytes < ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, G)) return TTT_ERR_WORKSPACE;
+  if (saved == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(saved)) return TTT_ERR_ALIGN;
+  if (saved_bytes < ttt_linear_saved_bytes(B, H, NC, K, F)) return TTT_ERR_WORKSPACE;
 
   ttt::LinearBwdParams p;
   p.XQ = XQ;
@@ -151,7 +165,8 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   p.ln_w = ln_w;
   p.ln_b = ln_b;
   p.W_ckpt = W1_ckpt;
-  p.b_ckpt = b1_ckpt;
+  p.W_last = W1_last;
+  p.saved = saved;
   p.dXQ = dXQ;
   p.dXK = dXK;
   p.dXV = dXV;
@@ -160,14 +175,12 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   p.db = db1;
   p.dln_w = dln_w;
   p.dln_b = dln_b;
-  p.ws = static_cast<float*>(workspace);
   p.B = B;
   p.H = H;
   p.NC = NC;
   p.F = F;
   p.G = G;
   p.NK = (NC + G - 1) / G;
-  p.eps = eps;
   return hip_status(ttt::launch_linear_bwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 

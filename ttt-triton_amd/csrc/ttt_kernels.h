@@ -13,19 +13,41 @@ struct LinearFwdParams {
   const float *ln_w, *ln_b, *W_init, *b_init;
   void* out;
   float *W_last, *b_last, *W_ckpt, *b_ckpt;
+  void* saved;  // per mini-batch values for the backward, LinSavedSlot layout (may be null)
   int B, H, NC, F, G, NK;
   float eps;
 };
 
 struct LinearBwdParams {
   const void *XQ, *XK, *XV, *eta, *dout;
-  const float *ln_w, *ln_b, *W_ckpt, *b_ckpt;
+  const float *ln_w, *ln_b, *W_ckpt, *W_last;
+  const void* saved;  // per mini-batch values written by the forward (LinSavedSlot)
   void *dXQ, *dXK, *dXV, *deta;
   float *dW, *db, *dln_w, *dln_b;
-  float* ws;  // per-chain scratch: G mini-batches of the inner-loss gradient
   int B, H, NC, F, G, NK;
-  float eps;
 };
+
+// What the TTT-Linear forward saves per mini-batch for the backward, one slot
+// per (chain, mini-batch) in the saved buffer [B*H][NC][slot].  Byte offsets,
+// fp32; tiles in lane order (each lane's 4 registers contiguous):
+//   G    [F/16][64] x 4   inner-loss gradient, token-major C-layout tiles
+//   XH   [F/16][64] x 4   normalised Z1 = XK W + b, token-major
+//   XHB  [F/16][64] x 4   normalised readout Zb, feature-major (lane (g, n)
+//                         holds features 16o + 4g + j of token n)
+//   RSTD [16], CC [16]    per token: 1/sigma(Z1) and mean(gx * xh) of the
+//                         inner-loss LayerNorm
+//   RSB  [16]             per token: 1/sigma(Zb)
+template <int F> struct LinSavedSlot {
+  static constexpr int G = 0;
+  static constexpr int XH = F * 64;
+  static constexpr int XHB = 2 * F * 64;
+  static constexpr int RSTD = 3 * F * 64;
+  static constexpr int CC = RSTD + 64;
+  static constexpr int RSB = CC + 64;
+  static constexpr int BYTES = RSTD + 256;
+};
+constexpr size_t lin_saved_slot_bytes(int F) { return (size_t)3 * F * 64 + 256; }
+size_t linear_saved_slot_bytes(int F);
 
 struct MlpFwdParams {
   const void *XQ, *XK, *XV, *eta;

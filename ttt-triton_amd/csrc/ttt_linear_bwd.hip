@@ -1,247 +1,187 @@
-// TTT-Linear backward on gfx950: one workgroup of two wavefronts per
-// (batch, head) chain.
+// TTT-Linear backward on gfx950: one workgroup of three wavefronts per
+// (batch, head) chain, one reverse sweep over all NC mini-batches.
 //
-// Reverse sweep over checkpoint groups (kernels/linear_backward.py:278 walks
-// the same groups; the algorithm here is our own):
-//   phase 1  (wave 0) reload W, b from the checkpoint entering the group, run
-//            the group's mini-batches forward computing only the inner-loss
-//            gradient G_s = ln_fused_l2_bwd(XK_s W_s + b_s, XV_s - XK_s), park
-//            G_s in the per-chain workspace, and apply the state update;
-//   phase 2  walk the group backwards.  Wave 0 owns the fast weight: it
-//            rebuilds the state entering mini-batch s from the one after it,
-//            W_s = W_{s+1} + XK_s^T diag(e_s) G_s (the forward's MFMA operands),
-//            recomputes the mini-batch forward and applies its gradient
-//            (ops/ttt_linear.py:8-54 differentiated by hand).  Wave 1 owns the
-//            gradient wrt the state, dW and db: per mini-batch it first
-//            produces XK dW' + db' and -(e G) dW'^T, which wave 0 needs, and
-//            after wave 0 has the mini-batch's dZb and dZ1 it applies
-//            dW += XQ^T dZb + XK^T dZ1.  Two barriers per mini-batch; wave 0's
-//            recompute of mini-batch s-1 overlaps wave 1's work on s.
-// Products that contract W or dW over their column index use operand frags
-// transposed exactly with identity MFMAs, so neither wave keeps a transposed
-// copy of its 16*F*F-byte state.
+// The forward saves, per mini-batch, the inner-loss gradient G_s, the
+// normalised Z1 with its row statistics and the normalised readout Zb with its
+// token statistics (LinSavedSlot).  With those the backward needs the fast
+// weight only for the products dZb W_s^T and dZ1 W_s^T, and the only
+// sequential dependency left is the gradient wrt the state after mini-batch s,
+// dW' and db' (ops/ttt_linear.py:8-54 differentiated by hand):
+//   dG_s = -M^T dZb - diag(e) (XK dW' + db')      (e = eta[K-1])
+//   dZ1  = backward of ln_fused_l2_bwd at dG_s     (dtgt = dXV alongside)
+//   dW   = dW' + XQ^T dZb + XK^T dZ1 ;  db = db' + colsum(dZb + dZ1)
+// The three waves form a pipeline with one barrier per iteration: in
+// iteration it, wave P works on mini-batch NC-1-it, wave S on NC-it and wave X
+// on NC+1-it.
+//   P (prepare)  everything that involves neither W nor dW: the readout-LN
+//                backward (dZb), the dual-form terms (dM, dA, deta),
+//                dout + dA XK, dA^T XQ, -M^T dZb and the exact transposes the
+//                other two waves consume;
+//   S (state)    owns dW and db: XK dW' + db', the inner-loss LN backward,
+//                -(e G) dW'^T, the dW/db update;
+//   X (weights)  owns W^T, rebuilt backwards from the checkpoint after each
+//                group (kernels/linear_backward.py:278 walks the same groups):
+//                W_s = W_{s+1} + XK_s^T diag(e) G_s with the forward's MFMA
+//                operands; forms dXQ, dXK, dXV and deta and writes them.
+// Feature-major tiles ("FM": lane (g, n) holds features 16o + 4g + j of token
+// n) are what the outputs are written from, 4 contiguous elements per lane.
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
 namespace ttt {
 
 template <typename T, int FT> struct LinBwdShared {
-  float vlds[16 * FT];                 // wave 0: b in feature-major reads
-  float lnacc[2][4 * FT][64];          // wave 0: readout-LN gradient partials per lane
-  float dbz[16 * FT];                  // wave 0: column sums of dZb for the current step
-  float red[2 * 16 * FT];              // wave 0: final reductions
-  f4 qd[FT][64];                       // wave 1 -> 0: XK dW' + db'   (token-major tiles)
-  f4 tr[FT][64];                       // wave 1 -> 0: -(e G) dW'^T   (token-major tiles)
-  Frag<T> xq[2][FT][64];               // wave 0 -> 1: XQ token-major frags (by step parity)
-  Frag<T> xk[2][FT][64];               // wave 0 -> 1: XK token-major frags
-  Frag<T> dzb[2][FT][64];              // wave 0 -> 1: dZb token-major frags
-  Frag<T> dz1[FT][64];                 // wave 0 -> 1: dZ1 token-major frags
-  float db[16 * FT];                   // wave 0 -> 1: column sums of dZb + dZ1
-  f4 dxq[FT][64];                      // wave 0: dXQ partial carried across the barrier
-  float lnw[16 * FT];                  // wave 0: LN weight of this head
+  // P -> S, by mini-batch parity
+  struct PS {
+    Frag<T> xk[FT][64];     // XK row-major frags (free = token)
+    Frag<T> xq_t[FT][64];   // XQ token-major tiles as frags (free = feature)
+    Frag<T> dzb_t[FT][64];  // dZb token-major tiles as frags (free = feature)
+    Frag<T> egn[FT][64];    // -(e G) row-major frags (free = token)
+    f4 dg0[FT][64];         // -M^T dZb, token-major
+    f4 tgt[FT][64];         // XV - XK, token-major
+    f4 e[64];               // eta[K-1][4g + j]
+    float dbz[16 * FT];     // column sums of dZb
+  } ps[2];
+  // P -> S and X, by mini-batch mod 3
+  struct PX {
+    Frag<T> xk_t[FT][64];   // XK token-major tiles as frags (free = feature)
+    Frag<T> dzb[FT][64];    // dZb row-major frags (free = token)
+    Frag<T> eg_t[FT][64];   // e G token-major tiles as frags (free = feature)
+    f4 xqp[FT][64];         // (dout + dA XK)^T, FM
+    f4 xkp[FT][64];         // (dA^T XQ)^T, FM
+    f4 det[64];             // deta without the last-row term: lane (g, n) holds deta[n][4g + j]
+  } px[3];
+  // S -> X, by mini-batch parity
+  struct SX {
+    Frag<T> dz1_t[FT][64];   // dZ1 token-major tiles as frags
+    Frag<T> dtgt_t[FT][64];  // dtgt (= dXV) token-major tiles as frags
+    f4 tr[FT][64];           // (-(e G) dW'^T)^T, FM
+    f4 de[64];               // last-row eta gradient of token 4g + j
+  } sx[2];
+  float red[2 * 16 * FT];    // readout-LN parameter gradients, P -> S at the end
 };
 
 template <typename T, int FT> struct LinBwdCtx {
   const T *XQ, *XK, *XV, *DO, *ETA;
   T *DXQ, *DXK, *DXV, *DETA;
-  float* WS;
+  const char* SV;  // this chain's saved slots
   int NC, G, NK, chain, h;
 };
 
-// ------------------------------------------------------------------ wave 0
-template <typename T, int FT> struct Wave0 {
+// ------------------------------------------------------------------ wave P
+template <typename T, int FT> struct WaveP {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
-  const LinearBwdParams& p;
+  using Slot = LinSavedSlot<F>;
   const LinBwdCtx<T, FT>& c;
   LinBwdShared<T, FT>& sh;
   int l, g, n;
-  float eps;
   Frag<T> I;
-  float lnw_tm[FT], lnb_tm[FT];
-  float dlnw_tm[FT], dlnb_tm[FT];
-  Tile W[FT][FT];
-  float b_tm[FT];
-  // carried from the first half of a step to the second
-  Tile dG[FT], dxk[1][FT];
-  f4 e, detT;
-  Frag<T> dZbF[1][FT];
-  LnL2TM<FT> ln;
+  f4 lnw_fm[FT];
+  f4 aw[FT], ab[FT];  // readout-LN parameter gradient partials (features 16o + 4g + j, tokens of this lane)
+  struct In {
+    Frag<T> xq[1][FT], xk[1][FT], xv[FT], dof[FT];
+    Frag<T> etaT, e;  // raw: converted where used, so the prefetch is not waited for
+    f4 G[FT], xhb[FT];
+    float rsb;
+  } in;
 
-  __device__ Wave0(const LinearBwdParams& p_, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_)
-      : p(p_), c(c_), sh(sh_) {
+  __device__ WaveP(const LinearBwdParams& p, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_) : c(c_), sh(sh_) {
     l = lane_id();
     g = l >> 4;
     n = l & 15;
-    eps = p.eps;
     I = identity_frag<T>();
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
-      lnw_tm[o] = p.ln_w[c.h * F + 16 * o + n];
-      lnb_tm[o] = p.ln_b[c.h * F + 16 * o + n];
-      dlnw_tm[o] = 0.f;
-      dlnb_tm[o] = 0.f;
-    }
-    for (int q = 0; q < 4 * FT; ++q) {
-      sh.lnacc[0][q][l] = 0.f;
-      sh.lnacc[1][q][l] = 0.f;
-    }
-    for (int f = l; f < F; f += 64) sh.lnw[f] = p.ln_w[c.h * F + f];
-  }
-
-  // phase 1: forward through mini-batches [s0, s1), parking G_s
-  __device__ void recompute_group(int kk, int s0, int s1) {
-    const float* wc = p.W_ckpt + ((size_t)c.chain * c.NK + kk) * F * F;
 #pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < FT; ++o) W[i][o] = load_tile(wc, F, 16 * i, 16 * o);
-#pragma unroll
-    for (int o = 0; o < FT; ++o) b_tm[o] = p.b_ckpt[((size_t)c.chain * c.NK + kk) * F + 16 * o + n];
-
-    for (int s = s0; s < s1; ++s) {
-      const T* xks = c.XK + (size_t)s * K * F;
-      const T* xvs = c.XV + (size_t)s * K * F;
-      Frag<T> xk[1][FT], xkTf[FT];
-      f4 tgt[FT];
-#pragma unroll
-      for (int q = 0; q < FT; ++q) {
-        xk[0][q] = load_frag(xks, F, 16 * q);
-        const Tile xkT = transpose16(xk[0][q], I);
-        xkTf[q] = to_frag<T>(xkT.v);
-        tgt[q] = transpose16(load_frag(xvs, F, 16 * q), I).v - xkT.v;
-      }
-      const f4 ee = load4(c.ETA + (size_t)s * K * K + (K - 1) * K + 4 * g);
-      Tile z1[1][FT];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) z1[0][o].v = f4{b_tm[o], b_tm[o], b_tm[o], b_tm[o]};
-      gemm_pt<1, FT, FT>(z1, xk, W);
-      LnL2TM<FT> l1;
-      Tile Gs[FT];
-      l1.forward(z1[0], tgt, lnw_tm, lnb_tm, eps, Gs);
-      float* slot = c.WS + (size_t)(s - s0) * K * F;
-#pragma unroll
-      for (int o = 0; o < FT; ++o) spill_tile(slot + o * 256, Gs[o]);
-      Frag<T> ge[FT];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        f4 v;
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = -ee[j] * Gs[o].v[j];
-          acc += ee[j] * Gs[o].v[j];
-        }
-        ge[o] = to_frag<T>(v);
-        b_tm[o] -= sum_col4(acc);
-      }
-#pragma unroll
-      for (int i = 0; i < FT; ++i)
-#pragma unroll
-        for (int o = 0; o < FT; ++o) mma16(W[i][o].v, xkTf[i], ge[o]);
+      for (int j = 0; j < 4; ++j) lnw_fm[o][j] = p.ln_w[c.h * F + 16 * o + 4 * g + j];
+      aw[o] = f4{0.f, 0.f, 0.f, 0.f};
+      ab[o] = f4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
-  // first half of the reverse step: rebuild the state entering s, recompute
-  // the forward, readout-LN backward, everything that does not need dW'
-  __device__ void step_a(int s, int s0) {
+  __device__ void load(int s) {
     const size_t xo = (size_t)s * K * F;
-    const T* etas = c.ETA + (size_t)s * K * K;
-    const int par = s & 1;
-    Frag<T> xq[1][FT], xk[1][FT], dof[1][FT], xqTf[FT], xkTf[FT];
-    f4 tgt[FT];
 #pragma unroll
     for (int q = 0; q < FT; ++q) {
-      xq[0][q] = load_frag(c.XQ + xo, F, 16 * q);
-      xk[0][q] = load_frag(c.XK + xo, F, 16 * q);
-      dof[0][q] = load_frag(c.DO + xo, F, 16 * q);
-      xqTf[q] = to_frag<T>(transpose16(xq[0][q], I).v);
-      const Tile xkT = transpose16(xk[0][q], I);
-      xkTf[q] = to_frag<T>(xkT.v);
-      tgt[q] = transpose16(load_frag(c.XV + xo, F, 16 * q), I).v - xkT.v;
-      sh.xq[par][q][l] = xqTf[q];
-      sh.xk[par][q][l] = xkTf[q];
+      in.xq[0][q] = load_frag(c.XQ + xo, F, 16 * q);
+      in.xk[0][q] = load_frag(c.XK + xo, F, 16 * q);
+      in.xv[q] = load_frag(c.XV + xo, F, 16 * q);
+      in.dof[q] = load_frag(c.DO + xo, F, 16 * q);
     }
-    const f4 etaT = load_f4(etas, K, 0);  // [t_k x t_q]: eta[n][4g+j]
-    f4 eta_n;                             // [t_q x t_k]: eta[4g+j][n]
+    const T* etas = c.ETA + (size_t)s * K * K;
+    in.etaT = load_frag(etas, K, 0);            // lane (g, n): eta[n][4g + j]
+    in.e = load_frag(etas + (K - 1) * K, 0, 0);  // eta[K-1][4g + j]
+    const float* sv = reinterpret_cast<const float*>(c.SV + (size_t)s * Slot::BYTES);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) eta_n[j] = (float)etas[(4 * g + j) * K + n];
-    e = load4(etas + (K - 1) * K + 4 * g);
+    for (int o = 0; o < FT; ++o) {
+      in.G[o] = fill_tile(sv + Slot::G / 4 + o * 256).v;
+      in.xhb[o] = fill_tile(sv + Slot::XHB / 4 + o * 256).v;
+    }
+    in.rsb = sv[Slot::RSB / 4 + n];
+  }
 
-    Tile Gt[FT];
-    {
-      const float* slot = c.WS + (size_t)(s - s0) * K * F;
+  __device__ void step(int s, int m3) {
+    const In x = in;
+    load(s > 0 ? s - 1 : 0);  // unconditional, so that the wait for it is exact
+    auto& ps = sh.ps[s & 1];
+    auto& px = sh.px[m3];
+    const f4 etaT = frag_to_f4(x.etaT), e = frag_to_f4(x.e);
+
+    Frag<T> xqTf[FT], xkTf[FT];
 #pragma unroll
-      for (int o = 0; o < FT; ++o) Gt[o] = fill_tile(slot + o * 256);
+    for (int q = 0; q < FT; ++q) {
+      const Tile xkT = transpose16(x.xk[0][q], I);
+      xkTf[q] = to_frag<T>(xkT.v);
+      xqTf[q] = to_frag<T>(transpose16(x.xq[0][q], I).v);
+      ps.tgt[q][l] = transpose16(x.xv[q], I).v - xkT.v;
+      ps.xk[q][l] = x.xk[0][q];
+      ps.xq_t[q][l] = xqTf[q];
+      px.xk_t[q][l] = xkTf[q];
     }
-    // rebuild the state entering s: W += XK^T (e G), b += G^T e
+    ps.e[l] = e;
+
+    // e G (the forward's update operand with the sign flipped), -(e G) and G
+    // as row-major frags
+    Frag<T> GF[1][FT];
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
       f4 v;
-      float acc = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = e[j] * Gt[o].v[j];
-        acc += v[j];
-      }
-      const Frag<T> eg = to_frag<T>(v);
-#pragma unroll
-      for (int i = 0; i < FT; ++i) mma16(W[i][o].v, xkTf[i], eg);
-      b_tm[o] += sum_col4(acc);
-      if (g == 0) sh.vlds[16 * o + n] = b_tm[o];
+      for (int j = 0; j < 4; ++j) v[j] = e[j] * x.G[o][j];
+      const Frag<T> ge = to_frag<T>(v);
+      px.eg_t[o][l] = ge;
+      ps.egn[o][l] = negate(to_frag<T>(transpose16(ge, I).v));
+      GF[0][o] = to_frag<T>(transpose16(to_frag<T>(x.G[o]), I).v);
     }
 
-    // recompute the mini-batch forward
-    {
-      Tile z1[1][FT];
-#pragma unroll
-      for (int o = 0; o < FT; ++o) z1[0][o].v = f4{b_tm[o], b_tm[o], b_tm[o], b_tm[o]};
-      gemm_pt<1, FT, FT>(z1, xk, W);
-      Tile Gre[FT];
-      ln.forward(z1[0], tgt, lnw_tm, lnb_tm, eps, Gre);
-    }
+    // A^T = XK XQ^T [t_k x t_q], A = XQ XK^T [t_q x t_k]; M = eta (.) A + eta
     Tile at[1][1], a[1][1];
     at[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
     a[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-    gemm<1, 1, FT>(at, xk, xq);  // A^T [t_k x t_q]
-    gemm<1, 1, FT>(a, xq, xk);   // A   [t_q x t_k]
-    f4 mT, m;
+    gemm<1, 1, FT>(at, x.xk, x.xq);
+    gemm<1, 1, FT>(a, x.xq, x.xk);
+    const f4 eta_n = transpose16(x.etaT, I).v;  // lane (g, n): eta[4g + j][n]
+    f4 m;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mT[j] = etaT[j] * at[0][0].v[j] + etaT[j];
-      m[j] = eta_n[j] * a[0][0].v[j] + eta_n[j];
-    }
-    Tile zb[FT][1];
-#pragma unroll
-    for (int o = 0; o < FT; ++o)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) zb[o][0].v[j] = sh.vlds[16 * o + 4 * g + j];
-    gemm_tp<FT, 1, FT>(zb, W, xq);
-    {
-      const Frag<T> mtf = to_frag<T>(mT);
-#pragma unroll
-      for (int o = 0; o < FT; ++o) mma16(zb[o][0].v, to_frag<T>(-Gt[o].v), mtf);
-    }
-    float mb, rsb;
-    ln_stats_fm<FT>(zb, eps, mb, rsb);
+    for (int j = 0; j < 4; ++j) m[j] = eta_n[j] * a[0][0].v[j] + eta_n[j];
 
-    // readout LayerNorm backward (feature-major)
-    Frag<T> dZbTf[FT];
+    // readout LayerNorm backward (FM)
+    Frag<T> dZbF[1][FT], dZbTf[FT];
     {
       constexpr float invF = 1.0f / F;
-      f4 xhb[FT], gy[FT];
+      f4 gy[FT];
       float a1 = 0.f, a2 = 0.f;
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
-        const f4 d = frag_to_f4(dof[0][o]);
+        const f4 d = frag_to_f4(x.dof[o]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          xhb[o][j] = (zb[o][0].v[j] - mb) * rsb;
-          gy[o][j] = d[j] * sh.lnw[16 * o + 4 * g + j];
-          sh.lnacc[0][4 * o + j][l] += d[j] * xhb[o][j];
-          sh.lnacc[1][4 * o + j][l] += d[j];
+          gy[o][j] = d[j] * lnw_fm[o][j];
+          aw[o][j] += d[j] * x.xhb[o][j];
+          ab[o][j] += d[j];
           a1 += gy[o][j];
-          a2 += gy[o][j] * xhb[o][j];
+          a2 += gy[o][j] * x.xhb[o][j];
         }
       }
       a1 = sum_col4(a1) * invF;
@@ -250,141 +190,217 @@ template <typename T, int FT> struct Wave0 {
       for (int o = 0; o < FT; ++o) {
         f4 dz;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dz[j] = rsb * (gy[o][j] - a1 - xhb[o][j] * a2);
+        for (int j = 0; j < 4; ++j) dz[j] = x.rsb * (gy[o][j] - a1 - x.xhb[o][j] * a2);
         dZbF[0][o] = to_frag<T>(dz);
+        px.dzb[o][l] = dZbF[0][o];
         dZbTf[o] = to_frag<T>(transpose16(dZbF[0][o], I).v);
-        sh.dzb[par][o][l] = dZbTf[o];
-        // column sums over tokens (fp32) for db
+        ps.dzb_t[o][l] = dZbTf[o];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float cs = sum_row16(dz[j]);
-          if (n == 0) sh.dbz[16 * o + 4 * g + j] = cs;
+          if (n == 0) ps.dbz[16 * o + 4 * g + j] = cs;
         }
       }
     }
 
-    // dXQ = dout + dA XK (+ dZb W^T later); dM = -dZb G^T; dA = dM (.) eta
-    Tile dxq[1][FT];
+    // dM = -dZb G^T; dA = dM (.) eta; deta = dM (.) (A + 1) (+ the last-row term in S)
+    Tile dm[1][1], dmT[1][1];
+    dm[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
+    dmT[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
+    gemm<1, 1, FT>(dm, dZbF, GF);   // dZb G^T  [t_q x t_k]
+    gemm<1, 1, FT>(dmT, GF, dZbF);  // G dZb^T  [t_k x t_q]
+    f4 det, daT, da;
 #pragma unroll
-    for (int q = 0; q < FT; ++q) dxq[0][q] = transpose16(dof[0][q], I);
-    {
-      Frag<T> GF[1][FT];
+    for (int j = 0; j < 4; ++j) {
+      det[j] = -dmT[0][0].v[j] * (1.0f + at[0][0].v[j]);
+      daT[j] = -dmT[0][0].v[j] * etaT[j];
+      da[j] = -dm[0][0].v[j] * eta_n[j];
+    }
+    px.det[l] = det;
+    const Frag<T> daTf = to_frag<T>(daT), daf = to_frag<T>(da), mf = to_frag<T>(-m);
 #pragma unroll
-      for (int o = 0; o < FT; ++o) GF[0][o] = to_frag<T>(transpose16(to_frag<T>(Gt[o].v), I).v);
-      Tile dm[1][1], dmT[1][1];
-      dm[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-      dmT[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-      gemm<1, 1, FT>(dm, dZbF, GF);   // dZb G^T  [t_q x t_k]
-      gemm<1, 1, FT>(dmT, GF, dZbF);  // G dZb^T  [t_k x t_q]
-      f4 daT, da;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        detT[j] = -dmT[0][0].v[j] * (1.0f + at[0][0].v[j]);
-        daT[j] = -dmT[0][0].v[j] * etaT[j];
-        da[j] = -dm[0][0].v[j] * eta_n[j];
-      }
-      const Frag<T> daTf = to_frag<T>(daT), daf = to_frag<T>(da);
-      const Frag<T> mf = to_frag<T>(-m);
-#pragma unroll
-      for (int q = 0; q < FT; ++q) {
-        mma16(dxq[0][q].v, daTf, xkTf[q]);  // dA XK
-        dxk[0][q].v = f4{0.f, 0.f, 0.f, 0.f};
-        mma16(dxk[0][q].v, daf, xqTf[q]);   // dA^T XQ
-        dG[q].v = f4{0.f, 0.f, 0.f, 0.f};
-        mma16(dG[q].v, mf, dZbTf[q]);       // -M^T dZb
-        sh.dxq[q][l] = dxq[0][q].v;
-      }
+    for (int q = 0; q < FT; ++q) {
+      f4 xqp = frag_to_f4(x.dof[q]);
+      mma16(xqp, xkTf[q], daTf);  // + (dA XK)^T
+      px.xqp[q][l] = xqp;
+      f4 xkp = f4{0.f, 0.f, 0.f, 0.f};
+      mma16(xkp, xqTf[q], daf);  // (dA^T XQ)^T
+      px.xkp[q][l] = xkp;
+      f4 dg = f4{0.f, 0.f, 0.f, 0.f};
+      mma16(dg, mf, dZbTf[q]);  // -M^T dZb
+      ps.dg0[q][l] = dg;
     }
   }
 
-  // second half: needs XK dW' + db' and -(e G) dW'^T from wave 1
-  __device__ void step_b(int s, int s0) {
-    const size_t xo = (size_t)s * K * F;
-    Tile Gt[FT], dxq[1][FT];
-    {
-      const float* slot = c.WS + (size_t)(s - s0) * K * F;
+  // readout-LN parameter gradients summed over the chain's tokens
+  __device__ void finish() {
 #pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        Gt[o] = fill_tile(slot + o * 256);
-        dxq[0][o].v = sh.dxq[o][l];
-      }
-    }
-    float de[4] = {0.f, 0.f, 0.f, 0.f};
-    {
-      f4 dep = f4{0.f, 0.f, 0.f, 0.f};
+    for (int o = 0; o < FT; ++o)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        const f4 qd = sh.qd[o][l];
-        dxk[0][o].v += sh.tr[o][l];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          dG[o].v[j] -= e[j] * qd[j];
-          dep[j] += Gt[o].v[j] * qd[j];
+      for (int j = 0; j < 4; ++j) {
+        const float w = sum_row16(aw[o][j]);
+        const float b = sum_row16(ab[o][j]);
+        if (n == 0) {
+          sh.red[16 * o + 4 * g + j] = w;
+          sh.red[F + 16 * o + 4 * g + j] = b;
         }
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) de[j] = -sum_row16(dep[j]);
-    }
-    f4 dz1[FT], dtgt[FT];
-    ln.backward(dG, Gt, lnw_tm, dz1, dtgt, dlnw_tm, dlnb_tm);
-    Frag<T> dz1F[1][FT];
+  }
+};
+
+// ------------------------------------------------------------------ wave S
+template <typename T, int FT> struct WaveS {
+  static constexpr int F = 16 * FT;
+  static constexpr int K = 16;
+  using Slot = LinSavedSlot<F>;
+  const LinBwdCtx<T, FT>& c;
+  LinBwdShared<T, FT>& sh;
+  int l, g, n;
+  Frag<T> I;
+  float lnw_tm[FT], lnb_tm[FT];
+  float dlnw_tm[FT], dlnb_tm[FT];
+  Tile dW[FT][FT];
+  float db_tm[FT];
+  struct In {
+    f4 G[FT], xh[FT];
+    f4 rstd, cc;
+  } in;
+
+  __device__ WaveS(const LinearBwdParams& p, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_) : c(c_), sh(sh_) {
+    l = lane_id();
+    g = l >> 4;
+    n = l & 15;
+    I = identity_frag<T>();
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
-      const Frag<T> f = to_frag<T>(dz1[o]);
-      sh.dz1[o][l] = f;
-      dz1F[0][o] = to_frag<T>(transpose16(f, I).v);
-      dxk[0][o].v -= dtgt[o];
+      lnw_tm[o] = p.ln_w[c.h * F + 16 * o + n];
+      lnb_tm[o] = p.ln_b[c.h * F + 16 * o + n];
+      dlnw_tm[o] = 0.f;
+      dlnb_tm[o] = 0.f;
+      db_tm[o] = 0.f;
+#pragma unroll
+      for (int i = 0; i < FT; ++i) dW[i][o].v = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  __device__ void load(int s) {
+    const float* sv = reinterpret_cast<const float*>(c.SV + (size_t)s * Slot::BYTES);
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      in.G[o] = fill_tile(sv + Slot::G / 4 + o * 256).v;
+      in.xh[o] = fill_tile(sv + Slot::XH / 4 + o * 256).v;
+    }
+    in.rstd = load4(sv + Slot::RSTD / 4 + 4 * g);
+    in.cc = load4(sv + Slot::CC / 4 + 4 * g);
+  }
+
+  __device__ void step(int s, int m3) {
+    const In x = in;
+    load(s > 0 ? s - 1 : 0);  // unconditional, so that the wait for it is exact
+    const auto& ps = sh.ps[s & 1];
+    const auto& px = sh.px[m3];
+    auto& sx = sh.sx[s & 1];
+
+    // XK dW' + db'
+    Frag<T> xk[1][FT];
+#pragma unroll
+    for (int q = 0; q < FT; ++q) xk[0][q] = ps.xk[q][l];
+    Tile qm[1][FT];
+#pragma unroll
+    for (int o = 0; o < FT; ++o) qm[0][o].v = f4{db_tm[o], db_tm[o], db_tm[o], db_tm[o]};
+    gemm_pt<1, FT, FT>(qm, xk, dW);
+
+    // dG = -M^T dZb - e (XK dW' + db');  de = -rowsum(G (XK dW' + db'))
+    const f4 e = ps.e[l];
+    Tile dG[FT], Gt[FT];
+    f4 dep = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      const f4 d0 = ps.dg0[o][l];
+      Gt[o].v = x.G[o];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dG[o].v[j] = d0[j] - e[j] * qm[0][o].v[j];
+        dep[j] += x.G[o][j] * qm[0][o].v[j];
+      }
+    }
+    {
+      f4 de;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) de[j] = -sum_row16(dep[j]);
+      sx.de[l] = de;
+    }
+
+    // (-(e G) dW'^T)^T from the transposed dW' blocks (FM)
+    {
+      Frag<T> egn[FT];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) egn[o] = ps.egn[o][l];
+#pragma unroll
+      for (int i = 0; i < FT; ++i) {
+        f4 t = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < FT; o += 2) {
+          const Frag<T> t0 = to_frag<T>(transpose16(to_frag<T>(dW[i][o].v), I).v);
+          const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(dW[i][o + 1].v), I).v);
+          mma32(t, t0, t1, egn[o], egn[o + 1]);
+        }
+        sx.tr[i][l] = t;
+      }
+    }
+
+    // backward of the inner-loss LayerNorm
+    LnL2Lite<FT> ln;
+    ln.rstd = x.rstd;
+    ln.c = x.cc;
+    f4 tgt[FT];
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      ln.xh[o] = x.xh[o];
+      tgt[o] = ps.tgt[o][l];
+    }
+    f4 dz1[FT], dtgt[FT];
+    ln.backward(dG, Gt, tgt, lnw_tm, lnb_tm, dz1, dtgt, dlnw_tm, dlnb_tm);
+
+    // dW += XQ^T dZb + XK^T dZ1 ;  db += colsum(dZb + dZ1)
+    Frag<T> dz1f[FT], dzbf[FT];
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      dz1f[o] = to_frag<T>(dz1[o]);
+      dzbf[o] = ps.dzb_t[o][l];
+      sx.dz1_t[o][l] = dz1f[o];
+      sx.dtgt_t[o][l] = to_frag<T>(dtgt[o]);
+    }
+#pragma unroll
+    for (int i = 0; i < FT; ++i) {
+      const Frag<T> xqTf = ps.xq_t[i][l], xkTf = px.xk_t[i][l];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) mma32(dW[i][o].v, xqTf, xkTf, dzbf[o], dz1f[o]);
+    }
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc += dz1[o][j];
-      acc = sum_col4(acc);
-      if (g == 0) sh.db[16 * o + n] = acc + sh.dbz[16 * o + n];
+      db_tm[o] += sum_col4(acc) + ps.dbz[16 * o + n];
     }
-    // dZb W^T into dXQ and dZ1 W^T into dXK, one transposed W block at a time
+  }
+
+  __device__ void finish(const LinearBwdParams& p) {
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int q = 0; q < FT; q += 2) {
-        const Frag<T> t0 = to_frag<T>(transpose16(to_frag<T>(W[i][q].v), I).v);
-        const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W[i][q + 1].v), I).v);
-        mma32(dxq[0][i].v, dZbF[0][q], dZbF[0][q + 1], t0, t1);
-        mma32(dxk[0][i].v, dz1F[0][q], dz1F[0][q + 1], t0, t1);
-      }
-    // write the mini-batch's gradients (feature-major: 4 contiguous elements per lane)
-#pragma unroll
-    for (int q = 0; q < FT; ++q) {
-      store_f4(c.DXQ + xo, F, 16 * q, transpose16(to_frag<T>(dxq[0][q].v), I).v);
-      store_f4(c.DXK + xo, F, 16 * q, transpose16(to_frag<T>(dxk[0][q].v), I).v);
-      store_f4(c.DXV + xo, F, 16 * q, transpose16(to_frag<T>(dtgt[q]), I).v);
-    }
-    if (n == K - 1) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) detT[j] += de[j];
-    }
-    store_f4(c.DETA + (size_t)s * K * K, K, 0, detT);
-  }
-
-  __device__ void finish() {
+      for (int o = 0; o < FT; ++o) store_tile(p.dW + (size_t)c.chain * F * F, F, 16 * i, 16 * o, dW[i][o]);
     float lw_t[FT], lb_t[FT];
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
       lw_t[o] = sum_col4(dlnw_tm[o]);
       lb_t[o] = sum_col4(dlnb_tm[o]);
     }
-#pragma unroll
-    for (int o = 0; o < FT; ++o)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float w = sum_row16(sh.lnacc[0][4 * o + j][l]);
-        const float b = sum_row16(sh.lnacc[1][4 * o + j][l]);
-        if (n == 0) {
-          sh.red[16 * o + 4 * g + j] = w;
-          sh.red[F + 16 * o + 4 * g + j] = b;
-        }
-      }
     if (g == 0) {
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
+        p.db[(size_t)c.chain * F + 16 * o + n] = db_tm[o];
         p.dln_w[(size_t)c.chain * F + 16 * o + n] = lw_t[o] + sh.red[16 * o + n];
         p.dln_b[(size_t)c.chain * F + 16 * o + n] = lb_t[o] + sh.red[F + 16 * o + n];
       }
@@ -392,8 +408,8 @@ template <typename T, int FT> struct Wave0 {
   }
 };
 
-// ------------------------------------------------------------------ wave 1
-template <typename T, int FT> struct Wave1 {
+// ------------------------------------------------------------------ wave X
+template <typename T, int FT> struct WaveX {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
   const LinearBwdParams& p;
@@ -401,93 +417,83 @@ template <typename T, int FT> struct Wave1 {
   LinBwdShared<T, FT>& sh;
   int l, g, n;
   Frag<T> I;
-  Tile dW[FT][FT];
-  float db_tm[FT];
+  Tile WT[FT][FT];  // WT[o][i]: lane (g, n) holds W[16i + n][16o + 4g + j]
+  Tile WN[FT][FT];  // the checkpoint the next group starts from
 
-  __device__ Wave1(const LinearBwdParams& p_, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_)
+  __device__ WaveX(const LinearBwdParams& p_, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_)
       : p(p_), c(c_), sh(sh_) {
     l = lane_id();
     g = l >> 4;
     n = l & 15;
     I = identity_frag<T>();
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < FT; ++o) dW[i][o].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int o = 0; o < FT; ++o) db_tm[o] = 0.f;
   }
 
-  // XK dW' + db' and -(e G) dW'^T for mini-batch s (dW' = gradient after s)
-  __device__ void carry_terms(int s, int s0) {
-    const T* xks = c.XK + (size_t)s * K * F;
-    Frag<T> xk[1][FT];
+  __device__ void load_w(Tile (&w)[FT][FT], const float* src) {
 #pragma unroll
-    for (int q = 0; q < FT; ++q) xk[0][q] = load_frag(xks, F, 16 * q);
-    const f4 e = load4(c.ETA + (size_t)s * K * K + (K - 1) * K + 4 * g);
-    const float* slot = c.WS + (size_t)(s - s0) * K * F;
-    Frag<T> eGF[1][FT];
+    for (int o = 0; o < FT; ++o)
+#pragma unroll
+      for (int i = 0; i < FT; ++i) w[o][i].v = load4(src + (16 * i + n) * F + 16 * o + 4 * g);
+  }
+
+  __device__ void step(int s, int m3) {
+    // W entering step s+1: the final state, or the checkpoint prefetched in
+    // the previous step, at the end of each group
+    if (s + 1 < c.NC && (s + 1) % c.G == 0) {
+#pragma unroll
+      for (int o = 0; o < FT; ++o)
+#pragma unroll
+        for (int i = 0; i < FT; ++i) WT[o][i] = WN[o][i];
+    }
+    // prefetch the checkpoint entering this group when s starts one
+    if (s > 0 && s % c.G == 0) load_w(WN, p.W_ckpt + ((size_t)c.chain * c.NK + s / c.G) * F * F);
+
+    const auto& px = sh.px[m3];
+    const auto& sx = sh.sx[s & 1];
+    // W_s = W_{s+1} + XK^T diag(e) G:  W^T[o][i] += sum_t (e G)[t][o] XK[t][i]
+    {
+      Frag<T> xkTf[FT];
+#pragma unroll
+      for (int i = 0; i < FT; ++i) xkTf[i] = px.xk_t[i][l];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        const Frag<T> ge = px.eg_t[o][l];
+#pragma unroll
+        for (int i = 0; i < FT; ++i) mma16(WT[o][i].v, ge, xkTf[i]);
+      }
+    }
+
+    // dXQ^T = (dout + dA XK)^T + W dZb^T
+    // dXK^T = (dA^T XQ)^T - dtgt^T + (-(e G) dW'^T)^T + W dZ1^T
+    Frag<T> dzbF[FT], dz1F[FT];
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
-      const Tile gt = fill_tile(slot + o * 256);
-      f4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = e[j] * gt.v[j];
-      eGF[0][o] = to_frag<T>(-transpose16(to_frag<T>(v), I).v);
+      dzbF[o] = px.dzb[o][l];
+      dz1F[o] = to_frag<T>(transpose16(sx.dz1_t[o][l], I).v);
     }
-    Tile qm[1][FT];
-#pragma unroll
-    for (int o = 0; o < FT; ++o) qm[0][o].v = f4{db_tm[o], db_tm[o], db_tm[o], db_tm[o]};
-    gemm_pt<1, FT, FT>(qm, xk, dW);
-#pragma unroll
-    for (int o = 0; o < FT; ++o) sh.qd[o][l] = qm[0][o].v;
+    const size_t xo = (size_t)s * K * F;
 #pragma unroll
     for (int i = 0; i < FT; ++i) {
-      Tile t;
-      t.v = f4{0.f, 0.f, 0.f, 0.f};
+      const f4 dv = transpose16(sx.dtgt_t[i][l], I).v;
+      f4 q = px.xqp[i][l];
+      f4 k = px.xkp[i][l] + sx.tr[i][l] - dv;
 #pragma unroll
-      for (int q = 0; q < FT; q += 2) {
-        const Frag<T> t0 = to_frag<T>(transpose16(to_frag<T>(dW[i][q].v), I).v);
-        const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(dW[i][q + 1].v), I).v);
-        mma32(t.v, eGF[0][q], eGF[0][q + 1], t0, t1);
+      for (int o = 0; o < FT; o += 2) {
+        const Frag<T> w0 = to_frag<T>(WT[o][i].v), w1 = to_frag<T>(WT[o + 1][i].v);
+        mma32(q, w0, w1, dzbF[o], dzbF[o + 1]);
+        mma32(k, w0, w1, dz1F[o], dz1F[o + 1]);
       }
-      sh.tr[i][l] = t.v;
+      store_f4(c.DXQ + xo, F, 16 * i, q);
+      store_f4(c.DXK + xo, F, 16 * i, k);
+      store_f4(c.DXV + xo, F, 16 * i, dv);
     }
-  }
-
-  // dW += XQ^T dZb + XK^T dZ1 ; db += colsum(dZb + dZ1)
-  __device__ void accumulate(int s) {
-    const int par = s & 1;
-    Frag<T> xqTf[FT], xkTf[FT], dzbf[FT], dz1f[FT];
-#pragma unroll
-    for (int q = 0; q < FT; ++q) {
-      xqTf[q] = sh.xq[par][q][l];
-      xkTf[q] = sh.xk[par][q][l];
-      dzbf[q] = sh.dzb[par][q][l];
-      dz1f[q] = sh.dz1[q][l];
-    }
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < FT; ++o) mma32(dW[i][o].v, xqTf[i], xkTf[i], dzbf[o], dz1f[o]);
-#pragma unroll
-    for (int o = 0; o < FT; ++o) db_tm[o] += sh.db[16 * o + n];
-  }
-
-  __device__ void finish() {
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < FT; ++o) store_tile(p.dW + (size_t)c.chain * F * F, F, 16 * i, 16 * o, dW[i][o]);
-    if (g == 0) {
-#pragma unroll
-      for (int o = 0; o < FT; ++o) p.db[(size_t)c.chain * F + 16 * o + n] = db_tm[o];
-    }
+    f4 det = px.det[l];
+    if (n == K - 1) det += sx.de[l];
+    store_f4(c.DETA + (size_t)s * K * K, K, 0, det);
   }
 };
 
 template <typename T, int FT>
-__global__ __launch_bounds__(128) void linear_bwd_kernel(LinearBwdParams p) {
+__global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   __shared__ LinBwdShared<T, FT> sh;
@@ -508,44 +514,52 @@ __global__ __launch_bounds__(128) void linear_bwd_kernel(LinearBwdParams p) {
   c.DXK = static_cast<T*>(p.dXK) + xoff;
   c.DXV = static_cast<T*>(p.dXV) + xoff;
   c.DETA = static_cast<T*>(p.deta) + eoff;
-  c.WS = p.ws + (size_t)c.chain * c.G * K * F;
+  c.SV = static_cast<const char*>(p.saved) + (size_t)c.chain * c.NC * LinSavedSlot<F>::BYTES;
 
-  // Both waves execute the same sequence of barriers: per group one after
-  // phase 1, then two per mini-batch.
-  if (threadIdx.x < 64) {
-    Wave0<T, FT> w(p, c, sh);
-    for (int kk = c.NK - 1; kk >= 0; --kk) {
-      const int s0 = kk * c.G, s1 = min(s0 + c.G, c.NC);
-      w.recompute_group(kk, s0, s1);
+  // Every wave passes NC + 3 barriers: one per pipeline iteration, one before
+  // the final reductions.  Each wave retires its first loads before its loop:
+  // loads still pending on loop entry make the wait-count pass wait for every
+  // outstanding access in each iteration.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int NC = c.NC;
+  if (wave == 0) {
+    WaveP<T, FT> w(p, c, sh);
+    w.load(NC - 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int it = 0; it < NC + 2; ++it) {
+      const int s = NC - 1 - it;
+      if (s >= 0) w.step(s, s % 3);
       __syncthreads();
-      w.step_a(s1 - 1, s0);
-      for (int s = s1 - 1; s >= s0; --s) {
-        __syncthreads();  // wave 1 has posted the carry terms of s
-        w.step_b(s, s0);
-        __syncthreads();  // dZb, dZ1 of s posted
-        if (s > s0) w.step_a(s - 1, s0);
-      }
     }
     w.finish();
+    __syncthreads();
+  } else if (wave == 1) {
+    WaveS<T, FT> w(p, c, sh);
+    w.load(NC - 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int it = 0; it < NC + 2; ++it) {
+      const int s = NC - it;
+      if (s >= 0 && s < NC) w.step(s, s % 3);
+      __syncthreads();
+    }
+    __syncthreads();
+    w.finish(p);
   } else {
-    Wave1<T, FT> w(p, c, sh);
-    for (int kk = c.NK - 1; kk >= 0; --kk) {
-      const int s0 = kk * c.G, s1 = min(s0 + c.G, c.NC);
+    WaveX<T, FT> w(p, c, sh);
+    w.load_w(w.WT, p.W_last + (size_t)c.chain * F * F);
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int it = 0; it < NC + 2; ++it) {
+      const int s = NC + 1 - it;
+      if (s >= 0 && s < NC) w.step(s, s % 3);
       __syncthreads();
-      for (int s = s1 - 1; s >= s0; --s) {
-        w.carry_terms(s, s0);
-        __syncthreads();
-        __syncthreads();
-        w.accumulate(s);
-      }
     }
-    w.finish();
+    __syncthreads();
   }
 }
 
 template <typename T, int FT>
 static hipError_t launch_bwd(const LinearBwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_bwd_kernel<T, FT>), dim3(p.B * p.H), dim3(128), 0, stream, p);
+  hipLaunchKernelGGL((linear_bwd_kernel<T, FT>), dim3(p.B * p.H), dim3(192), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -559,5 +573,7 @@ hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t st
   }
   return hipErrorInvalidValue;
 }
+
+size_t linear_saved_slot_bytes(int F) { return lin_saved_slot_bytes(F); }
 
 }  // namespace ttt

@@ -15,6 +15,9 @@
 // Inputs for mini-batch s+1 are loaded while mini-batch s computes.  The state
 // entering mini-batch k*G is written to the checkpoint buffers
 // (kernels/linear_forward.py:55-73 convention) and the final state to W_last.
+// With a saved buffer, every mini-batch's G, normalised Z1 and Zb and their
+// statistics go to its LinSavedSlot for the backward.
+#include "ttt_buf.h"
 #include "ttt_kernels.h"
 
 namespace ttt {
@@ -33,6 +36,14 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
   const T* __restrict__ XV = static_cast<const T*>(p.XV) + (size_t)chain * NC * K * F;
   const T* __restrict__ ETA = static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
   T* __restrict__ OUT = static_cast<T*>(p.out) + (size_t)chain * NC * K * F;
+  using Slot = LinSavedSlot<F>;
+  // Saved values go through a buffer resource whose size is zero when there is
+  // no saved buffer: the stores are then dropped by the range check, and being
+  // unconditional they keep the wait counts before the next mini-batch's
+  // prefetched inputs exact.
+  const rsrc_t SV = p.saved ? make_rsrc(static_cast<char*>(p.saved) + (size_t)chain * NC * Slot::BYTES,
+                                        (unsigned)(NC * Slot::BYTES))
+                            : make_rsrc(p.out, 0u);
 
   __shared__ float b_lds[F];
 
@@ -64,7 +75,7 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
 
   // prefetched inputs of the next mini-batch
   Frag<T> nq[1][FT], nk[1][FT], nv[1][FT];
-  f4 n_etaT, n_e;
+  Frag<T> n_etaT, n_e;  // raw: converted where used, so the prefetch is not waited for
   auto load_step = [&](int s) {
     const T* q = XQ + (size_t)s * K * F;
     const T* k = XK + (size_t)s * K * F;
@@ -76,10 +87,14 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
       nv[0][c] = load_frag(v, F, 16 * c);
     }
     const T* e = ETA + (size_t)s * K * K;
-    n_etaT = load_f4(e, K, 0);               // lane (g,n): eta[n][4g+j]
-    n_e = load4(e + (K - 1) * K + 4 * g);        // lane (g,*): eta[K-1][4g+j]
+    n_etaT = load_frag(e, K, 0);            // lane (g,n): eta[n][4g+j]
+    n_e = load_frag(e + (K - 1) * K, 0, 0);  // lane (g,*): eta[K-1][4g+j]
   };
   load_step(0);
+  // Retire the first loads before the loop: with them pending on entry the
+  // wait-count pass cannot order them against the loop's own loads and stores
+  // and waits for every outstanding access in each iteration.
+  __builtin_amdgcn_s_waitcnt(0);
 
   for (int s = 0; s < NC; ++s) {
     if (p.W_ckpt != nullptr && (s % p.G) == 0) {
@@ -102,7 +117,7 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
       xk[0][c] = nk[0][c];
       xv[0][c] = nv[0][c];
     }
-    const f4 etaT = n_etaT, e = n_e;
+    const Frag<T> etaT_raw = n_etaT, e_raw = n_e;
     if (s + 1 < NC) load_step(s + 1);
 
     // W as operand frags: Wf[o][i] (free = f_out block o, contraction = f_in block i)
@@ -178,10 +193,20 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
     for (int o = 0; o < FT; ++o)
 #pragma unroll
       for (int j = 0; j < 4; ++j) G[o].v[j] = (gx[o][j] - s1[j] - xh[o][j] * s2[j]) * rstd[j];
+    const int sv = s * Slot::BYTES;
+#pragma unroll
+    for (int o = 0; o < FT; ++o) {
+      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::G, Frag<float>{G[o].v});
+      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XH, Frag<float>{xh[o]});
+    }
+    // per-row values: the 16 lanes of a group store the same 4 rows
+    bstore_frag<float>(SV, 16 * g, sv + Slot::RSTD, Frag<float>{rstd});
+    bstore_frag<float>(SV, 16 * g, sv + Slot::CC, Frag<float>{s2});
 
     // ---- readout: Zb^T -= G^T (eta o A + eta)^T ; + b
     {
       f4 mt;
+      const f4 etaT = frag_to_f4(etaT_raw);
 #pragma unroll
       for (int j = 0; j < 4; ++j) mt[j] = etaT[j] * at[0][0].v[j] + etaT[j];
       const Frag<T> mtf = to_frag<T>(mt);
@@ -196,6 +221,7 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
 
     // ---- state update: W -= XK^T diag(e) G ; b -= G^T e
     {
+      const f4 e = frag_to_f4(e_raw);
       Frag<T> xkf[FT], ge[FT];
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
@@ -240,11 +266,16 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
         const f4 q = frag_to_f4(xq[0][o]);
-        f4 y;
+        f4 xhb, y;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) y[j] = q[j] + lnw_fm[o][j] * ((zb[o][0].v[j] - m) * rs) + lnb_fm[o][j];
+        for (int j = 0; j < 4; ++j) {
+          xhb[j] = (zb[o][0].v[j] - m) * rs;
+          y[j] = q[j] + lnw_fm[o][j] * xhb[j] + lnb_fm[o][j];
+        }
         store_f4(o_s, F, 16 * o, y);
+        bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XHB, Frag<float>{xhb});
       }
+      bstore_f32(SV, 4 * n, sv + Slot::RSB, rs);  // per token: the 4 lanes of token n agree
     }
   }
 

@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -25,11 +25,9 @@ _S = ctypes.c_size_t
 SIGNATURES = {
     "ttt_abi_version": (_I, []),
     "ttt_error_string": (ctypes.c_char_p, [_I]),
-    "ttt_linear_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
-                            _P, _P, _P, _P, _P, _P]),
-    "ttt_linear_bwd_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I]),
-    "ttt_linear_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
-                            _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P]),
+    "ttt_linear_fwd": (_I, [_P] * 8 + [_I] * 7 + [_F] + [_P] * 5 + [_P, _S, _P]),
+    "ttt_linear_saved_bytes": (_S, [_I] * 5),
+    "ttt_linear_bwd": (_I, [_P] * 9 + [_I] * 7 + [_F] + [_P] * 8 + [_P, _S, _P]),
     "ttt_mlp_fwd": (_I, [_P] * 10 + [_I] * 9 + [_F] + [_P] * 13 + [_P, _S, _P]),
     "ttt_mlp_saved_bytes": (_S, [_I] * 7),
     "ttt_mlp_bwd_workspace_bytes": (_S, [_I] * 7),

@@ -38,9 +38,13 @@ def _check_shapes(ln_w, ln_b, W1, b1, XQ, XV, XK, eta):
 
 
 def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_EPS,
-                   want_ckpt: bool = True, want_last: bool = False):
+                   want_ckpt: bool = True, want_last: bool = False, want_saved: bool = False):
     """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
-    (W1_ckpt, b1_ckpt) or None, (W1_last, b1_last) or None)."""
+    (W1_ckpt, b1_ckpt) or None, (W1_last, b1_last) or None, saved or None).
+
+    `saved` (uint8, ttt_linear_saved_bytes long) holds what linear_backward
+    reads instead of re-running the forward; the backward needs it together
+    with W1_ckpt and W1_last."""
     B, H, NC, K, F = _check_shapes(ln_w, ln_b, W1, b1, XQ, XV, XK, eta)
     dev = check_device(XQ, XK, XV, eta, W1, b1, ln_w, ln_b)
     mp = XQ.dtype
@@ -61,21 +65,28 @@ def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_
         last = (torch.empty((B, H, F, F), device=dev, dtype=torch.float32),
                 torch.empty((B, H, 1, F), device=dev, dtype=torch.float32))
     lib = _lib.load()
+    saved = None
+    if want_saved:
+        nbytes = lib.ttt_linear_saved_bytes(B, H, NC, K, F)
+        saved = torch.empty(nbytes, device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         st = lib.ttt_linear_fwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb),
             B, H, NC, K, F, G, code, float(eps), ptr(out),
             ptr(last[0]) if last else None, ptr(last[1]) if last else None,
-            ptr(ck[0]) if ck else None, ptr(ck[1]) if ck else None, stream_of(dev))
+            ptr(ck[0]) if ck else None, ptr(ck[1]) if ck else None,
+            ptr(saved) if saved is not None else None, saved.numel() if saved is not None else 0,
+            stream_of(dev))
     _lib.check(st, "ttt_linear_fwd")
-    return out, ck, last
+    return out, ck, last, saved
 
 
-def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, b1_ckpt, dout, G: int, eps: float = LN_EPS):
-    """Run the backward kernel.  Returns fp32 (dln_w [H,F], dln_b [H,F],
+def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, G: int, eps: float = LN_EPS):
+    """Run the backward kernel on what linear_forward(want_ckpt, want_last,
+    want_saved) returned.  Returns fp32 (dln_w [H,F], dln_b [H,F],
     dW1 [B,H,F,F], db1 [B,H,1,F]) and (dXQ, dXV, dXK, deta) in XQ.dtype."""
     B, H, NC, K, F = XQ.shape
-    dev = check_device(XQ, XK, XV, eta, W1_ckpt, b1_ckpt, dout)
+    dev = check_device(XQ, XK, XV, eta, W1_ckpt, W1_last, saved, dout)
     mp = XQ.dtype
     code = dtype_code(mp)
     xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
@@ -90,14 +101,12 @@ def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, b1_ckpt, dout, G: int,
     dlw = torch.empty((B, H, F), device=dev, dtype=torch.float32)
     dlb = torch.empty((B, H, F), device=dev, dtype=torch.float32)
     lib = _lib.load()
-    nbytes = lib.ttt_linear_bwd_workspace_bytes(B, H, NC, K, F, int(G))
-    ws = torch.empty((max(nbytes, 16) + 3) // 4, device=dev, dtype=torch.float32)
     with torch.cuda.device(dev):
         st = lib.ttt_linear_bwd(
-            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(W1_ckpt), ptr(b1_ckpt), ptr(do),
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(W1_ckpt), ptr(W1_last), ptr(do),
             B, H, NC, K, F, int(G), code, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW), ptr(db), ptr(dlw), ptr(dlb),
-            ptr(ws), ws.numel() * 4, stream_of(dev))
+            ptr(saved), saved.numel(), stream_of(dev))
     _lib.check(st, "ttt_linear_bwd")
     return (dlw.sum(0), dlb.sum(0), dW, db), (dxq, dxv, dxk, deta)
 
@@ -112,9 +121,11 @@ class TTTLinearFunction(torch.autograd.Function):
                 checkpoint_group_size, eps=LN_EPS):
         NC = XQ_batch.shape[2]
         G = min(max(int(checkpoint_group_size), 1), NC)
-        out, ck, _ = linear_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, XQ_batch, XV_batch,
-                                    XK_batch, eta_batch, G, eps, want_ckpt=True)
-        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck)
+        out, ck, last, saved = linear_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, XQ_batch,
+                                              XV_batch, XK_batch, eta_batch, G, eps, want_ckpt=True,
+                                              want_last=True, want_saved=True)
+        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, ck[0],
+                              last[0], saved)
         ctx.G, ctx.eps = G, eps
         ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype,
                       XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
@@ -122,9 +133,9 @@ class TTTLinearFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        XQ, XV, XK, eta, lw, lb, Wc, bc = ctx.saved_tensors
+        XQ, XV, XK, eta, lw, lb, Wc, Wl, saved = ctx.saved_tensors
         (dlw, dlb, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
-            lw, lb, XQ, XV, XK, eta, Wc, bc, grad_out, ctx.G, ctx.eps)
+            lw, lb, XQ, XV, XK, eta, Wc, Wl, saved, grad_out, ctx.G, ctx.eps)
         grads = (dlw, dlb, dW, db, dxq, dxv, dxk, deta)
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
         return grads + (None, None)
