@@ -22,6 +22,15 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* p, unsigned int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferWord3);
 }
 
+// A lane offset that the range check drops when `keep` is false: offsets of
+// 2^31 and more lie past every slab these kernels address (each is checked to
+// stay below 2^31 bytes).  Stores that only some waves or lanes should make go
+// through this instead of a branch, so that every wave issues the same memory
+// operations and the compiler's wait counts for earlier loads stay exact.
+__device__ __forceinline__ int keep_or_drop(int voff, bool keep) {
+  return (int)((unsigned)voff | (keep ? 0u : 0x80000000u));
+}
+
 // four consecutive elements at byte offset voff + soff
 template <typename T> __device__ __forceinline__ Frag<T> bload_frag(rsrc_t r, int voff, int soff);
 template <> __device__ __forceinline__ Frag<__bf16> bload_frag<__bf16>(rsrc_t r, int voff, int soff) {

@@ -3,8 +3,8 @@
 // 1. mlp_bwd_kernel: one workgroup of NW = FF/64 wavefronts per (batch, head)
 //    chain, wave w owning hidden units S = [64w, 64w+64), walks the sequence
 //    in reverse and carries the gradient wrt the state, dW1, db1, dW2, db2.
-//    Inputs besides the sequence: the forward's checkpoints, its final state
-//    and its saved buffer, which holds for every mini-batch the state-update
+//    Inputs besides the sequence: the forward's final W2 and its saved
+//    buffer, which holds for every mini-batch the state-update
 //    operands and the activations the gradient needs (MlpSavedSlot): nothing
 //    of the forward is recomputed (ops/ttt_mlp.py:9-67 differentiated by hand).
 //    The products with W1 (dXQ += dZ1b W1^T, dXK += dZ1 W1^T) do not feed the
@@ -17,10 +17,10 @@
 // In the reverse sweep W2 is needed (the gradient flows through products with
 // it): W2^T [F][FF] lives in LDS in fp32, columns XOR-swizzled so both access
 // shapes are bank-conflict free, rebuilt per mini-batch as W2_s = W2_{s+1} +
-// X2_s^T (e G2_s) from the exact operands the forward's update used; a group
-// starts from the next group's checkpoint or the final state
-// (kernels/mlp_backward.py:340 walks the same groups; the algorithm and data
-// flow here are our own).  dW1 is accumulated in LDS as dW1^T [FF][F], so both
+// X2_s^T (e G2_s) from the exact operands the forward's update used, starting
+// from the final state: the rebuild undoes each update up to fp32 rounding, so
+// no checkpoint reload is needed (kernels/mlp_backward.py:340 instead restarts
+// every checkpoint group; the algorithm and data flow here are our own).  dW1 is accumulated in LDS as dW1^T [FF][F], so both
 // orientations it is read in are direct LDS reads; dW2 lives in the MFMA
 // accumulator registers.  Each wave only touches its own hidden rows/columns
 // of these, so no barrier guards them.
@@ -109,7 +109,6 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const rsrc_t rWS = make_rsrc(static_cast<char*>(p.ws) + (size_t)chain * NC * WS::BYTES, (unsigned)(NC * WS::BYTES));
 
   // W2 checkpoints [NK][...] and the final W2 of this chain
-  const rsrc_t rW2c = make_rsrc(p.W2_ckpt + (size_t)chain * NK * FF * F, (unsigned)((size_t)NK * FF * F * 4));
   const rsrc_t rW2l = make_rsrc(p.W2_last + (size_t)chain * FF * F, (unsigned)(FF * F * 4));
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
@@ -196,21 +195,21 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     for (int o = 0; o < HT; ++o) nx2f[o] = bload_frag<T>(rSV, hl + o * 256 * ST, u + Slot::X2);
   };
   prefetch(NC - 1);
+  // W2 (this slice) after the last mini-batch; each step below rebuilds the
+  // state entering it exactly from the saved update operands, so the
+  // checkpoints are not needed here (rounding drift over a whole sequence is
+  // a few fp32 ulps of W2)
+#pragma unroll
+  for (int i = 0; i < HT; ++i)
+#pragma unroll
+    for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(rW2l, w2l, 0, F, 16 * i, 16 * o));
+  // retire the loads issued so far: pending on loop entry, they make the
+  // wait-count pass wait for every outstanding access in each iteration
+  __builtin_amdgcn_s_waitcnt(0);
 
   // Reverse sweep.  Regions between barriers:   A..P | B2a | LN2..B2b | B3
   // exchange area:                              dG2, dN1, de partials; dXQ, dXK partials
   for (int s = NC - 1; s >= 0; --s) {
-    // the state after mini-batch s at the end of a checkpoint group: the next
-    // group's checkpoint, or the final state
-    if (s == NC - 1 || (s + 1) % G == 0) {
-      const bool last = s == NC - 1;
-      const rsrc_t r2 = last ? rW2l : rW2c;
-      const int k1 = last ? 0 : (s + 1) / G;
-#pragma unroll
-      for (int i = 0; i < HT; ++i)
-#pragma unroll
-        for (int o = 0; o < FT; ++o) w2_put(i, o, bload_tile(r2, w2l, k1 * F * FF * 4, F, 16 * i, 16 * o));
-    }
     {
       const int us = s * Slot::BYTES;
       const int ws_ = s * WS::BYTES;
@@ -223,10 +222,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 
       // inputs of the readout LayerNorm backward, requested before the state
       // rebuild so that it hides their latency
-      const f4 etaT = frag_to_f4(bload_frag<T>(rET, el, es(s)));  // [t_k x t_q]: eta[n][4g+j]
-      f4 eta_n;                                                   // [t_q x t_k]: eta[4g+j][n]
-#pragma unroll
-      for (int j = 0; j < 4; ++j) eta_n[j] = bload1<T>(rET, en + j * K * ST, es(s));
+      // (eta raw: converted where first used, so that the conversion does not
+      // wait for the load here)
+      const Frag<T> etaT_r = bload_frag<T>(rET, el, es(s));      // [t_k x t_q]: eta[n][4g+j]
+      const Frag<T> etan_r = bload_ctile<T>(rET, en, es(s), K);  // [t_q x t_k]: eta[4g+j][n]
+      // dout of this wave's feature tile for B3 (one tile per wave when NW >= FT)
+      const Frag<T> dob = bload_frag<T>(rDO, xl + 16 * (wave % FT) * ST, xs(s));
       const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
       const f4 a2 = bload_frag<float>(rSV, a2tl, us + Slot::A2T).v;    // A2   [t_q x t_k]
       const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
@@ -329,6 +330,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
         }
       }
+      const f4 etaT = frag_to_f4(etaT_r), eta_n = frag_to_f4(etan_r);
       // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
       f4 detT, dA2T, dA2;
       Frag<T> m2f;  // -(eta o A2 + eta) for wave 0, zero for the others
@@ -550,13 +552,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dA1T[j] = dn1T[j] * etaT[j];
           dA1[j] = dn1[j] * eta_n[j];
         }
-        if (wave == 0) {
-          if (n == K - 1) {
+        if (n == K - 1) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) detT[j] -= de[j];
-          }
-          bstore_frag<T>(rDET, el, es(s), to_frag<T>(detT));
+          for (int j = 0; j < 4; ++j) detT[j] -= de[j];
         }
+        bstore_frag<T>(rDET, keep_or_drop(el, wave == 0), es(s), to_frag<T>(detT));
       }
       __syncthreads();  // (1x) exchange area free
       pin_dW();
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
         for (int f = 0; f < FT; ++f) {
           if (f % NW != wave) continue;
-          f4 dxq = transpose16(bload_frag<T>(rDO, xl + 16 * f * ST, xs(s)), I).v;
+          f4 dxq = transpose16(NW >= FT ? dob : dof[f], I).v;  // (f == wave when NW >= FT)
           f4 dxk = -dtgt[f];
 #pragma unroll
           for (int w = 0; w < NW; ++w) dxk += xa.get((w * FT + f) * 1024);
@@ -773,6 +773,9 @@ __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
   const int s0 = kk * G, s1 = min(s0 + G, NC);
   In cur;
   load_in(s0, cur);
+  // retire the loads issued so far: pending on loop entry, they make the
+  // wait-count pass wait for every outstanding access in each iteration
+  __builtin_amdgcn_s_waitcnt(0);
   for (int s = s0; s < s1; ++s) {
     const int us = s * Slot::BYTES, xo = s * K * F * ST;
     In nxt;

@@ -139,6 +139,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     xq[0][q] = bload_frag<T>(rXQ, xl + 16 * q * ST, 0);
     xk[0][q] = bload_frag<T>(rXK, xl + 16 * q * ST, 0);
   }
+  // retire the loads issued so far: pending on loop entry, they make the
+  // wait-count pass wait for every outstanding access in each iteration
+  __builtin_amdgcn_s_waitcnt(0);
 
   for (int s = 0; s < NC; ++s) {
     if (p.W1_ckpt != nullptr && (s % p.G) == 0) {
@@ -174,9 +177,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           gp[o][j] = dy;
           gpp[o][j] = ddy;
         }
-        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1, to_frag<T>(gp[o]));
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1, to_frag<T>(gp[o]));
         x2f[o] = to_frag<T>(x2);
-        if (want_saved) bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
         x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
       }
     }
@@ -221,18 +224,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       }
       LnL2Lite<FT> ln;
       ln.forward(z2, tgt, lnw_tm, lnb_tm, eps, G2);
-      if (want_saved) {
 #pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          if (c % NW != wave) continue;
-          bstore_frag<float>(rSV, f4l + c * 1024, us + Slot::G2, Frag<float>{G2[c].v});
-          bstore_frag<float>(rSV, f4l + c * 1024, us + Slot::XH, Frag<float>{ln.xh[c]});
-        }
-        if (wave == 0) {
-          bstore_frag<float>(rSV, f4l, us + Slot::RSTD, Frag<float>{ln.rstd});
-          bstore_frag<float>(rSV, f4l, us + Slot::CC, Frag<float>{ln.c});
-        }
+      for (int c = 0; c < FT; ++c) {
+        const int v = keep_or_drop(f4l + c * 1024, c % NW == wave);
+        bstore_frag<float>(rSV, v, us + Slot::G2, Frag<float>{G2[c].v});
+        bstore_frag<float>(rSV, v, us + Slot::XH, Frag<float>{ln.xh[c]});
       }
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSTD, Frag<float>{ln.rstd});
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::CC, Frag<float>{ln.c});
     }
 
     // ---- G1 = (G2 W2^T) (.) gelu'(Z1); W2^T blocks by exact transposes
@@ -250,9 +249,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
           mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
         }
-        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::H1, to_frag<T>(G1[i].v * gpp[i]));
+        bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::H1, to_frag<T>(G1[i].v * gpp[i]));
         G1[i].v *= gp[i];
-        if (want_saved) bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::G1, to_frag<T>(G1[i].v));
+        bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::G1, to_frag<T>(G1[i].v));
       }
     }
 
@@ -282,10 +281,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           x2b[j] = y;
           sp[j] = dy;
         }
-        if (want_saved) {
-          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2B, to_frag<T>(x2b));
-          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1B, to_frag<T>(sp));
-        }
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2B, to_frag<T>(x2b));
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1B, to_frag<T>(sp));
         x2bF[0][o] = to_frag<T>(transpose16(to_frag<T>(x2b), I).v);
       }
     }
@@ -320,10 +317,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g1e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b1_tm[o] -= d;
-        if (want_saved) {
-          bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
-          if (g == 0) bstore_f32(rSV, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);
-        }
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
+        bstore_f32(rSV, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);  // the 4 lanes of column n agree
       }
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
@@ -337,10 +332,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g2e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b2_tm[o] -= d;
-        if (want_saved && wave == 0) {
-          bstore_frag<T>(rSV, g2l + o * 256 * ST, us + Slot::G2E, g2e[o]);
-          if (g == 0) bstore_f32(rSV, n * 4 + 64 * o, us + Slot::B2D, d);
-        }
+        bstore_frag<T>(rSV, keep_or_drop(g2l + o * 256 * ST, wave == 0), us + Slot::G2E, g2e[o]);
+        bstore_f32(rSV, keep_or_drop(n * 4 + 64 * o, wave == 0), us + Slot::B2D, d);
       }
 #pragma unroll
       for (int i = 0; i < FT; ++i)
@@ -359,7 +352,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       a2[0].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NW; ++w) a2[0].v += sh.a2p[w][l];
-      if (want_saved && wave == 0) bstore_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0, a2[0]);
+      bstore_tile(rSV, keep_or_drop(a2l, wave == 0), us + Slot::A2T, 16, 0, 0, a2[0]);
       f4 m2;
 #pragma unroll
       for (int j = 0; j < 4; ++j) m2[j] = -(etaT[j] * a2[0].v[j] + etaT[j]);
@@ -392,10 +385,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         }
         rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
-      if (want_saved && wave == 0) bstore_frag<float>(rSV, f4l, us + Slot::RSB, Frag<float>{rs});
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSB, Frag<float>{rs});
+      // every wave forms every tile; tile o is written by wave o % NW
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
-        if (o % NW != wave) continue;  // static indices keep these arrays in registers
+        const bool mine = o % NW == wave;
         const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
         f4 xhb, y;
 #pragma unroll
@@ -403,8 +397,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           xhb[j] = (z2b[o].v[j] - mu[j]) * rs[j];
           y[j] = q[j] + lnw_tm[o] * xhb[j] + lnb_tm[o];
         }
-        if (want_saved) bstore_frag<float>(rSV, f4l + o * 1024, us + Slot::XHB, Frag<float>{xhb});
-        bstore_frag<T>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
+        bstore_frag<float>(rSV, keep_or_drop(f4l + o * 1024, mine), us + Slot::XHB, Frag<float>{xhb});
+        bstore_frag<T>(rOUT, keep_or_drop(xl + 16 * o * ST, mine), xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
       }
     }
 
