@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 5
+#define TTT_AMD_ABI_VERSION 6
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -171,6 +171,41 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
                            const float* b2, const float* ln_w, const float* ln_b,
                            int B, int H, int NS, int K, int F, int FF, int S, int dtype, float eps,
                            float* out, void* stream);
+
+/* Bytes of the gates buffer of ttt_mlp_memo_combine / _bwd: B*H chains x
+ * (2*NS*NC*K + NC*K + NS*F) floats (rounded up to 16 bytes), NS = ceil(NC/M);
+ * 0 for unsupported sizes. */
+size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M);
+
+/* TTT-MLP memory-cache combiner: the segment loop of TTTMLP.ttt
+ * (ttt_layer.py:506-561, its cached-readout calls ttt_layer.py:542-552) in
+ * three launches.  Segments of M mini-batches; for a token of segment i >= 1,
+ * gamma = softmax over j = 0..i of XU . mean(XK over segment j), and
+ *   out = gamma_i XQW + sum_{j<i} gamma_j (XQ + LN_eps(gelu(XQ W1_j + b1_j) W2_j + b2_j) ln_w + ln_b);
+ * segment 0 keeps XQW.  Each (b,h) chain uses its own memo states.
+ *   XQ, XK, XU, XQW   [B,H,NC,K,F] dtype      out [B,H,NC,K,F] dtype
+ *   W1_memo ...       [B,H,NS,F,FF], [B,H,NS,1,FF], [B,H,NS,FF,F], [B,H,NS,1,F] fp32
+ *                     (the memo output of ttt_mlp_fwd with the same M)
+ *   ln_w, ln_b        [H,F] fp32;  eps: the cached readout's (1e-6 there)
+ *   gates             >= ttt_mlp_memo_gates_bytes(...) bytes; receives the gates
+ *                     and segment summaries, which ttt_mlp_memo_combine_bwd reads
+ * NS = ceil(NC/M) <= 256.  No counterpart in the reference's C-level code (it is
+ * Python there); replaces the loop body, not a kernel. */
+int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const void* XQW,
+                         const float* W1_memo, const float* b1_memo, const float* W2_memo,
+                         const float* b2_memo, const float* ln_w, const float* ln_b,
+                         int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
+                         void* out, float* gates, size_t gates_bytes, void* stream);
+
+/* Backward of ttt_mlp_memo_combine: gradients wrt XU and XQW only (the
+ * reference detaches the summaries and runs the cached readouts without
+ * gradient).  `gates` as written by the forward call (its gate-gradient part
+ * is overwritten); dXU, dXQW [B,H,NC,K,F] dtype. */
+int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XQW, const float* W1_memo,
+                             const float* b1_memo, const float* W2_memo, const float* b2_memo,
+                             const float* ln_w, const float* ln_b, const void* dout,
+                             int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
+                             float* gates, size_t gates_bytes, void* dXU, void* dXQW, void* stream);
 
 #ifdef __cplusplus
 }

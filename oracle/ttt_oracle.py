@@ -18,6 +18,9 @@ What it restates (reference file:line):
   ttt_mlp            ops/ttt_mlp.py:70-99
   cached_readout     kernels/mlp_cached_readout.py:88-109,143 semantics with the
                      (b,h) indexing the reference kernel drops (its out[0,0] race)
+  memo_combine       ttt_layer.py:506-561 (softmax gates over segment summaries,
+                     cached readouts of the memo states), with correct (b,h)
+                     indexing of the cached readouts
   side outputs       checkpoints = state entering mini-batch k*G
                      (kernels/linear_forward.py:55-73, kernels/mlp_forward.py:84-117);
                      memo = state after mini-batch s*M (kernels/mlp_forward.py:193-226);
@@ -35,6 +38,10 @@ How each function is pinned (tests/test_oracle.py):
   scan              forward invariant to the checkpoint group size
   backward          autograd of this restatement == fp64 finite differences (gradcheck)
   cached_readout    == mlp_mini_batch readout with eta = 0 (no update), eps 1e-8
+  memo_combine      one segment == identity; XU = 0 gives the uniform average of
+                    XQW and the cached readouts (closed form); identical memo states
+                    with XQW = their readout leave the output unchanged (convex
+                    combination); gradients == fp64 finite differences
   side outputs      checkpoints / memo / W_last == states of an independent step loop
 There is no reference-held golden vector for this path (the reference ships no
 tests or fixtures), so parity is pinned only by the checks above.
@@ -291,21 +298,64 @@ def mlp_forward_full(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G, M: int = 0,
     return res
 
 
-def cached_readout(XQ_seg, W1, b1, W2, b2, ln_w, ln_b, eps: float = 1e-6):
+def cached_readout(XQ_seg, W1, b1, W2, b2, ln_w, ln_b, eps: float = 1e-6, dtype=torch.float32):
     """Fixed-weight MLP readout XQ + LN(gelu(XQ W1 + b1) W2 + b2), with the
     per-(b,h) weights the reference kernel meant to use.
     kernels/mlp_cached_readout.py:88-109,143 (eps 1e-6 there).
 
     XQ_seg [B,H,S,K,F]; W1 [B,H,F,FF]; b1 [B,H,1,FF]; W2 [B,H,FF,F]; b2 [B,H,1,F]; ln [H,F].
-    Returns XQ_seg + readout, in float32 (the reference's type promotion).
+    Returns XQ_seg + readout, in float32 (the reference's type promotion) unless
+    `dtype` asks for another compute type.
     """
     H, Fd = XQ_seg.shape[1], XQ_seg.shape[-1]
-    x = XQ_seg.float()
-    Z1 = x @ W1.float()[:, :, None] + b1.float()[:, :, None]
-    Z2 = gelu_tanh(Z1) @ W2.float()[:, :, None] + b2.float()[:, :, None]
-    g = ln_w.float().reshape(1, H, 1, 1, Fd)
-    bt = ln_b.float().reshape(1, H, 1, 1, Fd)
+    x = XQ_seg.to(dtype)
+    Z1 = x @ W1.to(dtype)[:, :, None] + b1.to(dtype)[:, :, None]
+    Z2 = gelu_tanh(Z1) @ W2.to(dtype)[:, :, None] + b2.to(dtype)[:, :, None]
+    g = ln_w.to(dtype).reshape(1, H, 1, 1, Fd)
+    bt = ln_b.to(dtype).reshape(1, H, 1, 1, Fd)
     return x + ln_fwd(Z2, g, bt, eps)
+
+
+def memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M: int,
+                 eps: float = 1e-6, dtype=torch.float64):
+    """The TTT-MLP memory-cache combiner of TTTMLP.ttt, ttt_layer.py:506-561.
+
+    The sequence is cut into segments of M mini-batches.  Segment 0 keeps its
+    output.  For a token t of segment i >= 1, with summary_j = mean of XK over
+    segment j (no gradient), sims_j = XU_t . summary_j for j = 0..i and
+    gamma = softmax(sims):
+        out_t = gamma_i XQW_t + sum_{j<i} gamma_j R_j(XQ_t)
+    where R_j is the cached readout with the memo state j (no gradient).
+    Gradients flow into XQW and XU only, as in the reference.
+
+    XQ, XK, XU, XQW [B,H,NC,K,F]; *_memo [B,H,NS,...] with NS = ceil(NC/M);
+    ln_w, ln_b [H,F].  Computes in `dtype` (the reference's bf16 casts of gamma
+    and of the cached sum are not reproduced).  Returns [B,H,NC,K,F].
+    """
+    NC = XQ.shape[2]
+    NS = ceil_div(NC, M)
+    outs, summaries = [], []
+    for i in range(NS):
+        s0, s1 = i * M, min((i + 1) * M, NC)
+        xq = XQ[:, :, s0:s1].to(dtype)
+        xu = XU[:, :, s0:s1].to(dtype)
+        xqw = XQW[:, :, s0:s1].to(dtype)
+        summ = XK[:, :, s0:s1].to(dtype).mean(dim=(2, 3)).detach()  # [B,H,F]
+        if i == 0:
+            summaries.append(summ)
+            outs.append(xqw)
+            continue
+        sims = torch.stack([(xu * sm[:, :, None, None, :]).sum(-1) for sm in summaries + [summ]], dim=-1)
+        gam = torch.softmax(sims, dim=-1)  # [B,H,nc,K,i+1]
+        acc = gam[..., i:i + 1] * xqw
+        for j in range(i):
+            with torch.no_grad():
+                r = cached_readout(xq, W1_memo[:, :, j], b1_memo[:, :, j], W2_memo[:, :, j], b2_memo[:, :, j],
+                                   ln_w, ln_b, eps, dtype=dtype)
+            acc = acc + gam[..., j:j + 1] * r
+        outs.append(acc)
+        summaries.append(summ)
+    return torch.cat(outs, dim=2)
 
 
 # ----------------------------------------------------------------------------

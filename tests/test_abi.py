@@ -40,7 +40,8 @@ def test_header_declares_the_abi():
     for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
                  "ttt_linear_saved_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
                  "ttt_mlp_bwd_workspace_bytes",
-                 "ttt_mlp_cached_readout"):
+                 "ttt_mlp_cached_readout", "ttt_mlp_memo_gates_bytes", "ttt_mlp_memo_combine",
+                 "ttt_mlp_memo_combine_bwd"):
         assert name in decls, name
 
 
@@ -184,3 +185,32 @@ def test_product_fails_loudly_without_a_gpu():
     with pytest.raises(ValueError, match="GPU"):
         W = torch.zeros(1, 1, 64, 64)
         mlp_cached_readout(d["XQ"], W, torch.zeros(1, 1, 1, 64), W, torch.zeros(1, 1, 1, 64), d["ln_w"], d["ln_b"])
+
+
+def test_memo_combine_validation(lib):
+    B, H, NC, K, F, FF, M = 2, 3, 10, 16, 64, 256, 3
+    NS = -(-NC // M)
+    need = lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M)
+    per_chain = 2 * NS * NC * K + NC * K + NS * F
+    assert need == B * H * ((per_chain + 3) // 4 * 4) * 4
+    assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, 0) == 0
+    assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, 48, M) == 0
+
+    def fwd(**kw):
+        a = dict(ptrs=[P] * 10, B=B, H=H, NC=NC, K=K, F=F, FF=FF, M=M, dtype=BF16, eps=1e-6, out=P, gates=P,
+                 gb=need, stream=None)
+        a.update(kw)
+        return lib.ttt_mlp_memo_combine(*a["ptrs"], a["B"], a["H"], a["NC"], a["K"], a["F"], a["FF"], a["M"],
+                                        a["dtype"], a["eps"], a["out"], a["gates"], a["gb"], a["stream"])
+    assert fwd(FF=96) == E_SHAPE
+    assert fwd(M=0) == E_ARG
+    assert fwd(NC=300, M=1) == E_SHAPE  # more than 256 memo states
+    assert fwd(gb=need - 4) == E_WS
+    assert fwd(gates=None) == E_WS
+    assert fwd(gates=Q) == E_ALIGN
+    assert fwd(out=None) == E_NULL
+    assert fwd(ptrs=[P] * 2 + [None] + [P] * 7) == E_NULL
+    assert fwd(dtype=5) == E_DTYPE
+    bwd = [P] * 9 + [B, H, NC, K, F, FF, M, BF16, 1e-6]
+    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need - 4, P, P, None) == E_WS
+    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, None, P, None) == E_NULL

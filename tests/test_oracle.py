@@ -4,6 +4,8 @@ vectors for this path, so these checks are what fixes the oracle: each one is
 chosen so that a plausible slip (dropped term, wrong sign, transposed operand,
 wrong eta row, wrong eps) fails it."""
 
+import math
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -243,6 +245,95 @@ def test_cached_readout_uses_each_chain_weights():
     o0 = O.cached_readout(d["XQ"], d["W1"], d["b1"], d["W2"], d["b2"], d["ln_w"], d["ln_b"])
     assert (o1[1, 1] - o0[1, 1]).abs().max() > 1e-3
     torch.testing.assert_close(o1[0], o0[0], rtol=0, atol=0)
+
+
+# --- memo combiner (ttt_layer.py:506-561) -------------------------------------------
+
+def _memo_inputs(B=1, H=2, NC=6, M=2, F_=16, FF=32, seed=50):
+    g = torch.Generator().manual_seed(seed)
+    NS = O.ceil_div(NC, M)
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DT)
+    return dict(XQ=r(B, H, NC, 16, F_), XK=r(B, H, NC, 16, F_), XU=r(B, H, NC, 16, F_, sc=0.3),
+                XQW=r(B, H, NC, 16, F_), W1=r(B, H, NS, F_, FF, sc=0.2), b1=r(B, H, NS, 1, FF, sc=0.1),
+                W2=r(B, H, NS, FF, F_, sc=0.2), b2=r(B, H, NS, 1, F_, sc=0.1),
+                ln_w=1 + r(H, F_, sc=0.1), ln_b=r(H, F_, sc=0.1)), M
+
+
+def _combine(d, M):
+    return O.memo_combine(d["XQ"], d["XK"], d["XU"], d["XQW"], d["W1"], d["b1"], d["W2"], d["b2"],
+                          d["ln_w"], d["ln_b"], M)
+
+
+def test_memo_combine_one_segment_is_identity():
+    d, _ = _memo_inputs(NC=3, M=3)
+    torch.testing.assert_close(_combine(d, 3), d["XQW"], rtol=0, atol=0)
+
+
+def test_memo_combine_zero_gate_input_averages_uniformly():
+    """XU = 0: every gate is 1/(i+1), so a token of segment i gets the plain mean
+    of XQW and the readouts of memo states 0..i-1 (each state distinct, so a
+    wrong state index or range fails)."""
+    d, M = _memo_inputs(NC=7, M=2)
+    d["XU"] = torch.zeros_like(d["XU"])
+    out = _combine(d, M)
+    NC = d["XQ"].shape[2]
+    for s in range(NC):
+        i = s // M
+        q = d["XQ"][:, :, s:s + 1]
+        tot = d["XQW"][:, :, s:s + 1].clone()
+        for j in range(i):
+            tot = tot + O.cached_readout(q, d["W1"][:, :, j], d["b1"][:, :, j], d["W2"][:, :, j], d["b2"][:, :, j],
+                                         d["ln_w"], d["ln_b"], dtype=DT)
+        torch.testing.assert_close(out[:, :, s:s + 1], tot / (i + 1), rtol=0, atol=1e-12)
+
+
+def test_memo_combine_is_a_convex_combination():
+    """Identical memo states and XQW equal to their readout: any gates give back XQW."""
+    d, M = _memo_inputs(NC=6, M=2, seed=51)
+    for k in ("W1", "b1", "W2", "b2"):
+        d[k] = d[k][:, :, :1].expand_as(d[k]).contiguous()
+    d["XQW"] = O.cached_readout(d["XQ"], d["W1"][:, :, 0], d["b1"][:, :, 0], d["W2"][:, :, 0], d["b2"][:, :, 0],
+                                d["ln_w"], d["ln_b"], dtype=DT)
+    d["XU"] = d["XU"] * 5  # far from uniform gates
+    torch.testing.assert_close(_combine(d, M), d["XQW"], rtol=0, atol=1e-12)
+
+
+def test_memo_combine_gates_of_one_token_by_hand():
+    """The gates of one token recomputed from scalar loops (summary = mean of XK
+    over the segment's tokens, sims = dot products, softmax = exp / sum)."""
+    d, M = _memo_inputs(NC=6, M=2, seed=52)
+    d["XU"] = d["XU"] * 3
+    b, h, s, t = 0, 1, 5, 7  # segment 2
+    i = s // M
+    F_ = d["XQ"].shape[-1]
+    summ = []
+    for j in range(i + 1):
+        acc = [0.0] * F_
+        toks = [(ss, tt) for ss in range(j * M, (j + 1) * M) for tt in range(16)]
+        for ss, tt in toks:
+            for f in range(F_):
+                acc[f] += float(d["XK"][b, h, ss, tt, f])
+        summ.append([a / len(toks) for a in acc])
+    sims = [sum(float(d["XU"][b, h, s, t, f]) * summ[j][f] for f in range(F_)) for j in range(i + 1)]
+    e = [math.exp(x - max(sims)) for x in sims]
+    gam = [x / sum(e) for x in e]
+    q = d["XQ"][b:b + 1, h:h + 1, s:s + 1, t:t + 1]
+    ref = gam[i] * d["XQW"][b, h, s, t]
+    for j in range(i):
+        r = O.cached_readout(q, d["W1"][b:b + 1, h:h + 1, j], d["b1"][b:b + 1, h:h + 1, j], d["W2"][b:b + 1, h:h + 1, j],
+                             d["b2"][b:b + 1, h:h + 1, j], d["ln_w"][h:h + 1], d["ln_b"][h:h + 1], dtype=DT)
+        ref = ref + gam[j] * r[0, 0, 0, 0]
+    torch.testing.assert_close(_combine(d, M)[b, h, s, t], ref, rtol=0, atol=1e-12)
+
+
+def test_memo_combine_gradients_match_finite_differences():
+    d, M = _memo_inputs(NC=5, M=2, F_=8, FF=16, seed=53)
+    XU = d["XU"].clone().requires_grad_(True)
+    XQW = d["XQW"].clone().requires_grad_(True)
+
+    def f(xu, xqw):
+        return O.memo_combine(d["XQ"], d["XK"], xu, xqw, d["W1"], d["b1"], d["W2"], d["b2"], d["ln_w"], d["ln_b"], M)
+    assert torch.autograd.gradcheck(f, (XU, XQW), eps=1e-6, atol=1e-6, rtol=1e-5)
 
 
 # --- backward -------------------------------------------------------------------

@@ -364,4 +364,84 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
   return hip_status(ttt::launch_mlp_readout(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M) {
+  if (B <= 0 || H <= 0 || NC <= 0 || K != 16 || (F != 32 && F != 64) || M < 1) return 0;
+  return (size_t)B * H * ttt::memo_gate_floats_per_chain(NC, K, F, M) * sizeof(float);
+}
+
+namespace {
+int check_memo(int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps, size_t gates_bytes,
+               const float* gates) {
+  int st = check_common(B, H, NC, K, F, 1, dtype, eps);
+  if (st != TTT_OK) return st;
+  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  if (M < 1) return TTT_ERR_ARG;
+  if ((NC + M - 1) / M > ttt::kMemoMaxStates) return TTT_ERR_SHAPE;
+  if ((long long)NC * K * F > 0x7fffffffLL / 4) return TTT_ERR_SHAPE;
+  if (gates == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(gates)) return TTT_ERR_ALIGN;
+  if (gates_bytes < ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M)) return TTT_ERR_WORKSPACE;
+  return TTT_OK;
+}
+
+ttt::MlpMemoParams memo_params(const void* XQ, const void* XQW, const float* W1, const float* b1, const float* W2,
+                               const float* b2, const float* ln_w, const float* ln_b, int B, int H, int NC, int F,
+                               int FF, int M, float eps, float* gates) {
+  ttt::MlpMemoParams p{};
+  p.XQ = XQ;
+  p.XQW = XQW;
+  p.W1 = W1;
+  p.b1 = b1;
+  p.W2 = W2;
+  p.b2 = b2;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.gates = gates;
+  p.B = B;
+  p.H = H;
+  p.NC = NC;
+  p.F = F;
+  p.FF = FF;
+  p.M = M;
+  p.NS = (NC + M - 1) / M;
+  p.nchunk = (NC + ttt::mlp_memo_chunk_tiles() - 1) / ttt::mlp_memo_chunk_tiles();
+  p.eps = eps;
+  return p;
+}
+}  // namespace
+
+int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const void* XQW, const float* W1_memo,
+                         const float* b1_memo, const float* W2_memo, const float* b2_memo, const float* ln_w,
+                         const float* ln_b, int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
+                         void* out, float* gates, size_t gates_bytes, void* stream) {
+  int st = check_memo(B, H, NC, K, F, FF, M, dtype, eps, gates_bytes, gates);
+  if (st != TTT_OK) return st;
+  const void* req[] = {XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, out};
+  for (const void* q : req) REQUIRE_PTR(q);
+  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC, F, FF, M,
+                                     eps, gates);
+  p.XK = XK;
+  p.XU = XU;
+  p.out = out;
+  if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return hip_status(ttt::launch_mlp_memo(p, dtype, false, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XQW, const float* W1_memo, const float* b1_memo,
+                             const float* W2_memo, const float* b2_memo, const float* ln_w, const float* ln_b,
+                             const void* dout, int B, int H, int NC, int K, int F, int FF, int M, int dtype,
+                             float eps, float* gates, size_t gates_bytes, void* dXU, void* dXQW, void* stream) {
+  int st = check_memo(B, H, NC, K, F, FF, M, dtype, eps, gates_bytes, gates);
+  if (st != TTT_OK) return st;
+  const void* req[] = {XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, dout, dXU, dXQW};
+  for (const void* q : req) REQUIRE_PTR(q);
+  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC, F, FF, M,
+                                     eps, gates);
+  p.dout = dout;
+  p.dXU = dXU;
+  p.dXQW = dXQW;
+  if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return hip_status(ttt::launch_mlp_memo(p, dtype, true, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

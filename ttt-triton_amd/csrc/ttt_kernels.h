@@ -84,6 +84,21 @@ struct MlpReadoutParams {
 hipError_t launch_mlp_readout(const MlpReadoutParams& p, int dtype, hipStream_t stream);
 int mlp_readout_chunk_tokens();
 
+// Memory-cache combiner (ttt_layer.py:506-561): memo states [B,H,NS,...],
+// gates buffer of memo_gate_floats_per_chain() floats per chain.
+constexpr int kMemoMaxStates = 256;
+struct MlpMemoParams {
+  const void *XQ, *XK, *XU, *XQW, *dout;
+  const float *W1, *b1, *W2, *b2, *ln_w, *ln_b;
+  void *out, *dXU, *dXQW;
+  float* gates;
+  int B, H, NC, F, FF, M, NS, nchunk;
+  float eps;
+};
+size_t memo_gate_floats_per_chain(int NC, int K, int F, int M);
+hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStream_t stream);
+int mlp_memo_chunk_tiles();
+
 // What the TTT-MLP forward saves per mini-batch for the backward, one slot
 // per (chain, mini-batch) in the saved buffer [B*H][NC][slot].  Byte offsets;
 // ST = bytes of the activation type; "lane order" = each lane's registers

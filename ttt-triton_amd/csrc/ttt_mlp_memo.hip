@@ -1,0 +1,414 @@
+// TTT-MLP memory-cache combiner on gfx950 (ttt_layer.py:506-561).
+//
+// The sequence is cut into segments of M mini-batches; memo state j is the
+// fast weight the forward snapshot after mini-batch j*M.  For a token t of
+// segment i >= 1, with summary_j = mean of XK over segment j and
+// gamma = softmax_j(XU_t . summary_j) over j = 0..i,
+//
+//   out_t = gamma_i XQW_t + sum_{j<i} gamma_j R_j(XQ_t),
+//   R_j(x) = x + LN_eps(gelu(x W1_j + b1_j) W2_j + b2_j) * ln_w + ln_b,
+//
+// and segment 0 keeps XQW.  The reference runs this as a Python loop with one
+// cached-readout launch per (segment, memo state) pair; here it is three
+// launches per direction:
+//
+//   memo_gate_kernel      one workgroup per chain: the segment summaries (LDS),
+//                         then per token the gates (written as gamma^T [NS][tokens]
+//                         plus the current-segment gate);
+//   memo_combine_kernel   one workgroup per (chain, 256-token chunk): for each
+//                         memo state j below the chunk's last segment, stage
+//                         W1_j/W2_j into LDS in MFMA operand order (as the cached
+//                         readout does), run the chunk's tiles of later
+//                         segments through R_j and accumulate gamma_j R_j (forward)
+//                         or dOut . R_j (backward: the gate gradients);
+//   memo_finish_kernel    (backward) one workgroup per chain: the softmax
+//                         backward, dXU = sum_j dsims_j summary_j and
+//                         dXQW = gamma_i dOut.
+//
+// Gradients flow into XQW and XU only (the summaries and the cached readouts
+// carry none in the reference).  The gates buffer per chain (fp32) holds
+// gamma^T [NS][NT], the current gate [NT], the summaries [NS][F] and, in the
+// backward, the gate gradients [NS][NT] (NT = NC * 16 tokens).
+#include "ttt_kernels.h"
+
+namespace ttt {
+
+constexpr int kMemoThreads = 256;
+
+struct MemoGateLayout {
+  size_t gam, gcur, summ, dgam, stride;  // float offsets within a chain's block
+  __host__ __device__ MemoGateLayout(int NC, int K, int F, int NS) {
+    const size_t NT = (size_t)NC * K;
+    gam = 0;
+    gcur = gam + (size_t)NS * NT;
+    summ = gcur + NT;
+    dgam = summ + (size_t)NS * F;
+    stride = (dgam + (size_t)NS * NT + 3) & ~(size_t)3;
+  }
+};
+
+size_t memo_gate_floats_per_chain(int NC, int K, int F, int M) {
+  const int NS = (NC + M - 1) / M;
+  return MemoGateLayout(NC, K, F, NS).stride;
+}
+
+// ------------------------------------------------------------------ gates
+template <typename T, int F>
+__global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p) {
+  constexpr int K = 16;
+  const int chain = blockIdx.x;
+  const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const MemoGateLayout L(NC, K, F, NS);
+  const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NT * F;
+  const T* __restrict__ XU = static_cast<const T*>(p.XU) + (size_t)chain * NT * F;
+  float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
+  __shared__ float summ[kMemoMaxStates * F];
+
+  // segment summaries: mean of XK over the segment's tokens
+  for (int q = threadIdx.x; q < NS * F; q += kMemoThreads) {
+    const int j = q / F, f = q - j * F;
+    const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
+    float acc = 0.f;
+    for (int t = t0; t < t1; ++t) acc += (float)XK[(size_t)t * F + f];
+    const float v = acc / (float)(t1 - t0);
+    summ[q] = v;
+    gb[L.summ + q] = v;
+  }
+  __syncthreads();
+
+  // gates of every token: softmax over the summaries of segments 0..i
+  float* __restrict__ gam = gb + L.gam;
+  for (int t = threadIdx.x; t < NT; t += kMemoThreads) {
+    const int i = (t / K) / M;
+    if (i == 0) {
+      gb[L.gcur + t] = 1.0f;
+      continue;
+    }
+    float xu[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) xu[f] = (float)XU[(size_t)t * F + f];
+    float mx = -3.0e38f;
+    for (int j = 0; j <= i; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int f = 0; f < F; ++f) s += xu[f] * summ[j * F + f];
+      gam[(size_t)j * NT + t] = s;
+      mx = fmaxf(mx, s);
+    }
+    float sum = 0.f;
+    for (int j = 0; j <= i; ++j) {
+      const float e = __expf(gam[(size_t)j * NT + t] - mx);
+      gam[(size_t)j * NT + t] = e;
+      sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (int j = 0; j < i; ++j) gam[(size_t)j * NT + t] *= inv;
+    gb[L.gcur + t] = gam[(size_t)i * NT + t] * inv;
+  }
+}
+
+// ------------------------------------------------------------------ R_j over a chunk
+constexpr int kMemoWaves = 4;
+constexpr int kMemoTilesPerWave = 4;
+constexpr int kMemoChunkTiles = kMemoWaves * kMemoTilesPerWave;  // mini-batches (16 tokens each) per workgroup
+
+template <typename T, int FT, int HTT> struct MemoShared {
+  typename FragT<T>::type w1[FT * HTT][64];  // block (kb, ht): W1[16kb + 4g + j][16ht + n]
+  typename FragT<T>::type w2[HTT * FT][64];  // block (ht, ct): W2[16ht + 4g + j][16ct + n]
+  float b1[16 * HTT];
+  float b2[16 * FT];
+};
+
+template <typename T, int FT, int HTT, bool BWD>
+__global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoParams p) {
+  constexpr int F = 16 * FT;
+  constexpr int FF = 16 * HTT;
+  constexpr int K = 16;
+  constexpr int NTW = kMemoTilesPerWave;
+  __shared__ MemoShared<T, FT, HTT> sh;
+
+  // blockIdx -> (chain, chunk), the chunks of one chain on one XCD (shared L2)
+  const int total = gridDim.x;
+  int lin = blockIdx.x;
+  if ((total & 7) == 0) lin = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+  const int chain = lin / p.nchunk;
+  const int chunk = lin - chain * p.nchunk;
+  const int h = chain % p.H;
+  const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const MemoGateLayout L(NC, K, F, NS);
+
+  const int wave = threadIdx.x >> 6;
+  const int l = lane_id(), g = l >> 4, n = l & 15;
+
+  const int c0 = chunk * kMemoChunkTiles;                      // first mini-batch of the chunk
+  const int clast = min(c0 + kMemoChunkTiles, NC) - 1;         // last mini-batch of the chunk
+  const int jmax = clast / M;                                  // memo states 0..jmax-1 serve this chunk
+  const int t0 = c0 + wave * NTW;                              // first mini-batch of this wave
+  const int nv = max(0, min(NTW, NC - t0));                    // valid tiles of this wave
+  const int tl = min(t0 + max(nv, 1) - 1, NC - 1);             // a valid tile index for padding
+
+  const size_t xoff = (size_t)chain * NT * F;
+  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
+  float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
+
+  // XQ operand frags (free = token, k = feature) and XQ in C layout (token rows)
+  Frag<T> xq[NTW][FT];
+  f4 xqc[NTW][FT];
+  int seg[NTW];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) {
+    const int tt = t < nv ? t0 + t : tl;
+    seg[t] = t < nv ? tt / M : -1;
+    const T* x = XQ + (size_t)tt * K * F;
+#pragma unroll
+    for (int kb = 0; kb < FT; ++kb) {
+      xq[t][kb] = load_frag(x, F, 16 * kb);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xqc[t][kb][j] = (float)x[(4 * g + j) * F + 16 * kb + n];
+    }
+  }
+  float lw[FT], lb[FT];
+#pragma unroll
+  for (int c = 0; c < FT; ++c) {
+    lw[c] = p.ln_w[h * F + 16 * c + n];
+    lb[c] = p.ln_b[h * F + 16 * c + n];
+  }
+
+  // forward: sum_j gamma_j R_j; backward: dOut (C layout)
+  f4 oacc[NTW][FT];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) {
+#pragma unroll
+    for (int c = 0; c < FT; ++c) {
+      if constexpr (BWD) {
+        const T* d = static_cast<const T*>(p.dout) + xoff + (size_t)(t < nv ? t0 + t : tl) * K * F;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) oacc[t][c][j] = (float)d[(4 * g + j) * F + 16 * c + n];
+      } else {
+        oacc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+
+  const float invF = 1.0f / (float)F;
+#pragma unroll 1
+  for (int jm = 0; jm < jmax; ++jm) {
+    // ---- stage memo state jm (the previous state's reads are done)
+    __syncthreads();
+    {
+      const size_t st = (size_t)chain * NS + jm;
+      const float* __restrict__ w1 = p.W1 + st * F * FF;
+      const float* __restrict__ w2 = p.W2 + st * FF * F;
+      for (int blk = wave; blk < FT * HTT; blk += kMemoWaves) {
+        const int kb = blk / HTT, ht = blk - kb * HTT;
+        f4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
+        sh.w1[blk][l] = to_frag<T>(x).v;
+      }
+      for (int blk = wave; blk < HTT * FT; blk += kMemoWaves) {
+        const int ht = blk / FT, ct = blk - ht * FT;
+        f4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
+        sh.w2[blk][l] = to_frag<T>(x).v;
+      }
+      for (int i = threadIdx.x; i < FF; i += 64 * kMemoWaves) sh.b1[i] = p.b1[st * FF + i];
+      for (int i = threadIdx.x; i < F; i += 64 * kMemoWaves) sh.b2[i] = p.b2[st * F + i];
+    }
+    __syncthreads();
+
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
+    if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
+
+    Tile acc[NTW][FT];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+      for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int ht = 0; ht < HTT; ht += 2) {
+      Frag<T> x2[2][NTW];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        Frag<T> w1f[FT];
+#pragma unroll
+        for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
+        const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) {
+          Tile z;
+          z.v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
+          f4 a;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
+          x2[hh][t] = to_frag<T>(a);
+        }
+      }
+      Frag<T> q0[FT], q1[FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        q0[c].v = sh.w2[ht * FT + c][l];
+        q1[c].v = sh.w2[(ht + 1) * FT + c][l];
+      }
+#pragma unroll
+      for (int t = 0; t < NTW; ++t)
+#pragma unroll
+        for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
+    }
+
+    // ---- R_jm = XQ + LN(Z2 + b2) * ln_w + ln_b per token row; fold it in
+    float b2v[FT];
+#pragma unroll
+    for (int c = 0; c < FT; ++c) b2v[c] = sh.b2[16 * c + n];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      if (seg[t] <= jm) continue;
+      const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
+      const f4 gj = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + tok0);
+      f4 dg = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[FT], s = 0.f;
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          v[c] = acc[t][c].v[j] + b2v[c];
+          s += v[c];
+        }
+        const float mean = sum_row16(s) * invF;
+        float q = 0.f;
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          v[c] -= mean;
+          q += v[c] * v[c];
+        }
+        const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          const float r = xqc[t][c][j] + lw[c] * (v[c] * rstd) + lb[c];
+          if constexpr (BWD) {
+            d += oacc[t][c][j] * r;
+          } else {
+            oacc[t][c][j] += gj[j] * r;
+          }
+        }
+        if constexpr (BWD) dg[j] = sum_row16(d);
+      }
+      if constexpr (BWD) {
+        if (n == 0) *reinterpret_cast<f4*>(gb + L.dgam + (size_t)jm * NT + tok0) = dg;
+      }
+    }
+  }
+
+  if constexpr (!BWD) {
+    // out = gamma_i XQW + sum_j gamma_j R_j (segment 0: gamma_i = 1, no cached terms)
+    const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
+    T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      if (t >= nv) continue;
+      const int tok0 = (t0 + t) * K + 4 * g;
+      const f4 gc = *reinterpret_cast<const f4*>(gb + L.gcur + tok0);
+#pragma unroll
+      for (int c = 0; c < FT; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const size_t e = (size_t)(tok0 + j) * F + 16 * c + n;
+          OUT[e] = (T)(gc[j] * (float)XQW[e] + oacc[t][c][j]);
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ backward: softmax, dXU, dXQW
+template <typename T, int F>
+__global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams p) {
+  constexpr int K = 16;
+  const int chain = blockIdx.x;
+  const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const MemoGateLayout L(NC, K, F, NS);
+  const size_t xoff = (size_t)chain * NT * F;
+  const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
+  const T* __restrict__ DO = static_cast<const T*>(p.dout) + xoff;
+  T* __restrict__ DXU = static_cast<T*>(p.dXU) + xoff;
+  T* __restrict__ DXQW = static_cast<T*>(p.dXQW) + xoff;
+  const float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
+  __shared__ float summ[kMemoMaxStates * F];
+  for (int q = threadIdx.x; q < NS * F; q += kMemoThreads) summ[q] = gb[L.summ + q];
+  __syncthreads();
+
+  for (int t = threadIdx.x; t < NT; t += kMemoThreads) {
+    const int i = (t / K) / M;
+    const float gc = gb[L.gcur + t];
+    float dout[F], dxu[F];
+    float dgc = 0.f;
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      dout[f] = (float)DO[(size_t)t * F + f];
+      dgc += dout[f] * (float)XQW[(size_t)t * F + f];
+      DXQW[(size_t)t * F + f] = (T)(gc * dout[f]);
+      dxu[f] = 0.f;
+    }
+    if (i > 0) {
+      // softmax backward: dsims_j = gamma_j (dgamma_j - sum_k gamma_k dgamma_k)
+      float S = gc * dgc;
+      for (int j = 0; j < i; ++j) S += gb[L.gam + (size_t)j * NT + t] * gb[L.dgam + (size_t)j * NT + t];
+      for (int j = 0; j <= i; ++j) {
+        const float ds = j < i ? gb[L.gam + (size_t)j * NT + t] * (gb[L.dgam + (size_t)j * NT + t] - S)
+                               : gc * (dgc - S);
+#pragma unroll
+        for (int f = 0; f < F; ++f) dxu[f] += ds * summ[j * F + f];
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < F; ++f) DXU[(size_t)t * F + f] = (T)dxu[f];
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+template <typename T, int FT, int HTT>
+static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
+  const dim3 grid(p.B * p.H * p.nchunk), block(64 * kMemoWaves);
+  if (bwd) {
+    hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, true>), grid, block, 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H), dim3(kMemoThreads), 0, stream, p);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H), dim3(kMemoThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, false>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T, int FT>
+static hipError_t launch_memo_f(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
+  switch (p.FF) {
+    case 64: return launch_memo_t<T, FT, 4>(p, bwd, stream);
+    case 128: return launch_memo_t<T, FT, 8>(p, bwd, stream);
+    case 256: return launch_memo_t<T, FT, 16>(p, bwd, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStream_t stream) {
+  if (dtype == TTT_DTYPE_BF16) {
+    if (p.F == 64) return launch_memo_f<__bf16, 4>(p, bwd, stream);
+    if (p.F == 32) return launch_memo_f<__bf16, 2>(p, bwd, stream);
+  } else {
+    if (p.F == 64) return launch_memo_f<float, 4>(p, bwd, stream);
+    if (p.F == 32) return launch_memo_f<float, 2>(p, bwd, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+int mlp_memo_chunk_tiles() { return kMemoChunkTiles; }
+
+}  // namespace ttt
