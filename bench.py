@@ -21,7 +21,11 @@ reference's ops path, fp32, autograd for the backward) on one batch row
 (B=1, all 12 heads, all 2048 tokens) on this host's cores.
 
 Other modes (for counter collection):
-    --only mlp_fwd|mlp_bwd|linear_fwd|linear_bwd|readout   run that kernel alone
+    --only mlp_fwd|mlp_bwd|linear_fwd|linear_bwd|readout|memo_fwd|memo_bwd   run that kernel alone
+
+The memory-cache combiner (the segment loop of TTTMLP.ttt) is timed at the
+same B/H/T/F/FF with memo segments of MEMO_M mini-batches, on synthetic memo
+states, forward and backward.
     --copy-calibration     copy 1 GiB device-to-device (a kernel of known traffic)
 """
 
@@ -48,6 +52,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
 B, H, T, K, F, FF = 16, 12, 2048, 16, 64, 256
 NC = T // K
 G_MLP, G_LIN = 8, 16
+MEMO_M = 8  # memo segment size (mini-batches) of the combiner leg
 
 
 def parse():
@@ -57,7 +62,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
-    ap.add_argument("--only", choices=["mlp_fwd", "mlp_bwd", "linear_fwd", "linear_bwd", "readout"])
+    ap.add_argument("--only", choices=["mlp_fwd", "mlp_bwd", "linear_fwd", "linear_bwd", "readout", "memo_fwd",
+                                       "memo_bwd"])
     ap.add_argument("--copy-calibration", action="store_true")
     return ap.parse_args()
 
@@ -264,6 +270,43 @@ def run_readout(torch, steps, warmup):
     return statistics.mean(sp["ttt_mlp_cached_readout"])
 
 
+def memo_pairs(M=MEMO_M):
+    """(token, memo state) pairs the combiner evaluates per chain: tokens of
+    segment i use the i states before it."""
+    NS = math.ceil(NC / M)
+    return sum(i * (min((i + 1) * M, NC) - i * M) * K for i in range(NS))
+
+
+def run_memo(torch, steps, warmup, only=None):
+    from ttt_amd.memo import memo_combine_backward, memo_combine_forward
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(5)
+    NS = math.ceil(NC / MEMO_M)
+    act = [torch.randn(B, H, NC, K, F, generator=gen).to(torch.bfloat16).to(dev) for _ in range(5)]
+    xq, xk, xu, xqw, dout = act
+    xu = (0.3 * xu.float()).to(torch.bfloat16)
+    ws = [0.02 * torch.randn(B, H, NS, F, FF, generator=gen), torch.zeros(B, H, NS, 1, FF),
+          0.02 * torch.randn(B, H, NS, FF, F, generator=gen), torch.zeros(B, H, NS, 1, F)]
+    ws = [w.to(dev) for w in ws]
+    lw, lb = torch.ones(H, F, device=dev), torch.zeros(H, F, device=dev)
+    _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
+    for _ in range(warmup):
+        _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
+        memo_combine_backward(xq, xqw, *ws, lw, lb, MEMO_M, gates, dout)
+    torch.cuda.synchronize()
+    tm = Timer(torch)
+    for _ in range(steps):
+        if only != "memo_bwd":
+            tm.mark("ttt_mlp_memo_combine")
+            _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
+        if only != "memo_fwd":
+            tm.mark("ttt_mlp_memo_combine_bwd")
+            memo_combine_backward(xq, xqw, *ws, lw, lb, MEMO_M, gates, dout)
+    tm.mark(None)
+    sp = tm.spans()
+    return {k: statistics.mean(v) for k, v in sp.items()}
+
+
 def roofline(kernel, sec, flops, nbytes, mfma_peak):
     """Binding roofline of one kernel: whichever of MFMA and HBM gives the
     longer ideal time for its algorithmic work."""
@@ -319,6 +362,8 @@ def main():
             k, _, _ = run_mlp(torch, O, args.steps, args.warmup, only=args.only)
         elif args.only.startswith("linear"):
             k, _ = run_linear(torch, O, args.steps, args.warmup, only=args.only)
+        elif args.only.startswith("memo"):
+            k = run_memo(torch, args.steps, args.warmup, only=args.only)
         else:
             k = {"ttt_mlp_cached_readout": run_readout(torch, args.steps, args.warmup)}
         print(json.dumps({"only": args.only, "avg_launch_us": {n: round(v * 1e6, 2) for n, v in k.items()}}),
@@ -335,6 +380,8 @@ def main():
     lk, ltotal = run_linear(torch, O, args.steps, args.warmup)
     print("[bench] cached readout", file=sys.stderr, flush=True)
     ro = run_readout(torch, args.steps, args.warmup)
+    print(f"[bench] memory-cache combiner (M={MEMO_M})", file=sys.stderr, flush=True)
+    mk = run_memo(torch, args.steps, args.warmup)
 
     state = mlp_state_floats()
     kernels = {
@@ -381,6 +428,13 @@ def main():
                         "hbm_frac": r["algorithmic"]["hbm_frac"]} for n, r in kernels.items()},
         "linear_fwd_bwd": {"value": round(B * T / (ltotal / args.steps), 1), "unit": "tokens/s",
                            "ms_per_step": round(ltotal / args.steps * 1e3, 4), "checkpoint_group": G_LIN},
+        "memo_combine": {
+            "value": round(B * T / (mk["ttt_mlp_memo_combine"] + mk["ttt_mlp_memo_combine_bwd"]), 1),
+            "unit": "tokens/s", "fwd_ms": round(mk["ttt_mlp_memo_combine"] * 1e3, 4),
+            "bwd_ms": round(mk["ttt_mlp_memo_combine_bwd"] * 1e3, 4), "memo_segment": MEMO_M,
+            "readouts_per_chain": memo_pairs(),
+            "mfma_frac_fwd": round(4 * F * FF * memo_pairs() * B * H / mk["ttt_mlp_memo_combine"] / MFMA_PEAK_BF16, 4),
+            "shape": f"B{B} H{H} T{T} F{F} FF{FF}, {math.ceil(NC / MEMO_M)} memo states per chain, bf16"},
         "cached_readout": {"value": round(B * T / ro, 1), "unit": "tokens/s",
                            "ms_per_launch": round(ro * 1e3, 4),
                            "shape": f"XQ [{B},{H},{NC},{K},{F}] bf16, one fixed state per chain"},

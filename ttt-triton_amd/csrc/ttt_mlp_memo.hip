@@ -10,18 +10,18 @@
 //
 // and segment 0 keeps XQW.  The reference runs this as a Python loop with one
 // cached-readout launch per (segment, memo state) pair; here it is three
-// launches per direction:
+// launches forward and two backward:
 //
-//   memo_gate_kernel      one workgroup per chain: the segment summaries (LDS),
-//                         then per token the gates (written as gamma^T [NS][tokens]
-//                         plus the current-segment gate);
+//   memo_summary_kernel   one workgroup per (chain, segment): the segment summaries;
+//   memo_gate_kernel      one thread per token: the gates (written as
+//                         gamma^T [NS][tokens] plus the current-segment gate);
 //   memo_combine_kernel   one workgroup per (chain, 256-token chunk): for each
 //                         memo state j below the chunk's last segment, stage
 //                         W1_j/W2_j into LDS in MFMA operand order (as the cached
 //                         readout does), run the chunk's tiles of later
 //                         segments through R_j and accumulate gamma_j R_j (forward)
 //                         or dOut . R_j (backward: the gate gradients);
-//   memo_finish_kernel    (backward) one workgroup per chain: the softmax
+//   memo_finish_kernel    (backward) one thread per token: the softmax
 //                         backward, dXU = sum_j dsims_j summary_j and
 //                         dXQW = gamma_i dOut.
 //
@@ -52,59 +52,68 @@ size_t memo_gate_floats_per_chain(int NC, int K, int F, int M) {
   return MemoGateLayout(NC, K, F, NS).stride;
 }
 
-// ------------------------------------------------------------------ gates
+// ------------------------------------------------------------------ summaries and gates
+// one workgroup of F threads per (chain, segment): mean of XK over the segment
 template <typename T, int F>
-__global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p) {
+__global__ __launch_bounds__(F) void memo_summary_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  const int chain = blockIdx.x;
+  const int chain = blockIdx.x / p.NS, j = blockIdx.x - chain * p.NS;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
   const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NT * F;
-  const T* __restrict__ XU = static_cast<const T*>(p.XU) + (size_t)chain * NT * F;
+  const int f = threadIdx.x;
+  const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
+  float acc = 0.f;
+  for (int t = t0; t < t1; ++t) acc += (float)XK[(size_t)t * F + f];
+  p.gates[(size_t)chain * L.stride + L.summ + (size_t)j * F + f] = acc / (float)(t1 - t0);
+}
+
+// one workgroup per (chain, block of kMemoThreads tokens), one token per thread:
+// the softmax over the summaries of segments 0..i
+template <typename T, int F>
+__global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p) {
+  constexpr int K = 16;
+  const int nblk = (p.NC * K + kMemoThreads - 1) / kMemoThreads;
+  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
+  const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const MemoGateLayout L(NC, K, F, NS);
   float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
-  __shared__ float summ[kMemoMaxStates * F];
-
-  // segment summaries: mean of XK over the segment's tokens
-  for (int q = threadIdx.x; q < NS * F; q += kMemoThreads) {
-    const int j = q / F, f = q - j * F;
-    const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
-    float acc = 0.f;
-    for (int t = t0; t < t1; ++t) acc += (float)XK[(size_t)t * F + f];
-    const float v = acc / (float)(t1 - t0);
-    summ[q] = v;
-    gb[L.summ + q] = v;
-  }
+  __shared__ f4 summ[kMemoMaxStates * F / 4];
+  const int t = blk * kMemoThreads + threadIdx.x;
+  const int tmax = min(NT, (blk + 1) * kMemoThreads) - 1;
+  const int ns = (tmax / K) / M + 1;  // segments this block's tokens can reach
+  for (int q = threadIdx.x; q < ns * F / 4; q += kMemoThreads)
+    summ[q] = *reinterpret_cast<const f4*>(gb + L.summ + 4 * (size_t)q);
   __syncthreads();
-
-  // gates of every token: softmax over the summaries of segments 0..i
-  float* __restrict__ gam = gb + L.gam;
-  for (int t = threadIdx.x; t < NT; t += kMemoThreads) {
-    const int i = (t / K) / M;
-    if (i == 0) {
-      gb[L.gcur + t] = 1.0f;
-      continue;
-    }
-    float xu[F];
-#pragma unroll
-    for (int f = 0; f < F; ++f) xu[f] = (float)XU[(size_t)t * F + f];
-    float mx = -3.0e38f;
-    for (int j = 0; j <= i; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int f = 0; f < F; ++f) s += xu[f] * summ[j * F + f];
-      gam[(size_t)j * NT + t] = s;
-      mx = fmaxf(mx, s);
-    }
-    float sum = 0.f;
-    for (int j = 0; j <= i; ++j) {
-      const float e = __expf(gam[(size_t)j * NT + t] - mx);
-      gam[(size_t)j * NT + t] = e;
-      sum += e;
-    }
-    const float inv = 1.0f / sum;
-    for (int j = 0; j < i; ++j) gam[(size_t)j * NT + t] *= inv;
-    gb[L.gcur + t] = gam[(size_t)i * NT + t] * inv;
+  if (t >= NT) return;  // (no barrier follows)
+  const int i = (t / K) / M;
+  if (i == 0) {
+    gb[L.gcur + t] = 1.0f;
+    return;
   }
+  const T* __restrict__ xu_row = static_cast<const T*>(p.XU) + ((size_t)chain * NT + t) * F;
+  f4 xu[F / 4];
+#pragma unroll
+  for (int q = 0; q < F / 4; ++q) xu[q] = load4(xu_row + 4 * q);
+  float* __restrict__ gam = gb + L.gam;
+  float mx = -3.0e38f;
+  for (int j = 0; j <= i; ++j) {
+    f4 s4 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < F / 4; ++q) s4 += xu[q] * summ[j * (F / 4) + q];
+    const float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    gam[(size_t)j * NT + t] = s;
+    mx = fmaxf(mx, s);
+  }
+  float sum = 0.f;
+  for (int j = 0; j <= i; ++j) {
+    const float e = __expf(gam[(size_t)j * NT + t] - mx);
+    gam[(size_t)j * NT + t] = e;
+    sum += e;
+  }
+  const float inv = 1.0f / sum;
+  for (int j = 0; j < i; ++j) gam[(size_t)j * NT + t] *= inv;
+  gb[L.gcur + t] = gam[(size_t)i * NT + t] * inv;
 }
 
 // ------------------------------------------------------------------ R_j over a chunk
@@ -193,8 +202,15 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
   const float invF = 1.0f / (float)F;
 #pragma unroll 1
   for (int jm = 0; jm < jmax; ++jm) {
-    // ---- stage memo state jm (the previous state's reads are done)
+    // ---- stage memo state jm (the previous state's reads are done); request
+    //      this state's gates of the wave's tokens first (forward)
     __syncthreads();
+    f4 gjv[NTW];
+    if constexpr (!BWD) {
+#pragma unroll
+      for (int t = 0; t < NTW; ++t)
+        gjv[t] = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + 4 * g);
+    }
     {
       const size_t st = (size_t)chain * NS + jm;
       const float* __restrict__ w1 = p.W1 + st * F * FF;
@@ -269,7 +285,8 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
     for (int t = 0; t < NTW; ++t) {
       if (seg[t] <= jm) continue;
       const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
-      const f4 gj = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + tok0);
+      f4 gj = f4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (!BWD) gj = gjv[t];
       f4 dg = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -326,47 +343,54 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
 }
 
 // ------------------------------------------------------------------ backward: softmax, dXU, dXQW
+// one workgroup per (chain, block of kMemoThreads tokens), one token per thread
 template <typename T, int F>
 __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  const int chain = blockIdx.x;
+  const int nblk = (p.NC * K + kMemoThreads - 1) / kMemoThreads;
+  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
-  const size_t xoff = (size_t)chain * NT * F;
-  const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
-  const T* __restrict__ DO = static_cast<const T*>(p.dout) + xoff;
-  T* __restrict__ DXU = static_cast<T*>(p.dXU) + xoff;
-  T* __restrict__ DXQW = static_cast<T*>(p.dXQW) + xoff;
   const float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
-  __shared__ float summ[kMemoMaxStates * F];
-  for (int q = threadIdx.x; q < NS * F; q += kMemoThreads) summ[q] = gb[L.summ + q];
+  __shared__ f4 summ[kMemoMaxStates * F / 4];
+  const int t = blk * kMemoThreads + threadIdx.x;
+  const int tmax = min(NT, (blk + 1) * kMemoThreads) - 1;
+  const int ns = (tmax / K) / M + 1;
+  for (int q = threadIdx.x; q < ns * F / 4; q += kMemoThreads)
+    summ[q] = *reinterpret_cast<const f4*>(gb + L.summ + 4 * (size_t)q);
   __syncthreads();
-
-  for (int t = threadIdx.x; t < NT; t += kMemoThreads) {
-    const int i = (t / K) / M;
-    const float gc = gb[L.gcur + t];
-    float dout[F], dxu[F];
-    float dgc = 0.f;
+  if (t >= NT) return;  // (no barrier follows)
+  const size_t row = ((size_t)chain * NT + t) * F;
+  const T* __restrict__ xqw_row = static_cast<const T*>(p.XQW) + row;
+  const T* __restrict__ do_row = static_cast<const T*>(p.dout) + row;
+  T* __restrict__ dxu_row = static_cast<T*>(p.dXU) + row;
+  T* __restrict__ dxqw_row = static_cast<T*>(p.dXQW) + row;
+  const int i = (t / K) / M;
+  const float gc = gb[L.gcur + t];
+  f4 dout[F / 4], dxu[F / 4];
+  f4 dg4 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int f = 0; f < F; ++f) {
-      dout[f] = (float)DO[(size_t)t * F + f];
-      dgc += dout[f] * (float)XQW[(size_t)t * F + f];
-      DXQW[(size_t)t * F + f] = (T)(gc * dout[f]);
-      dxu[f] = 0.f;
+  for (int q = 0; q < F / 4; ++q) {
+    dout[q] = load4(do_row + 4 * q);
+    dg4 += dout[q] * load4(xqw_row + 4 * q);
+    dxu[q] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float dgc = (dg4[0] + dg4[1]) + (dg4[2] + dg4[3]);
+  if (i > 0) {
+    // softmax backward: dsims_j = gamma_j (dgamma_j - sum_k gamma_k dgamma_k)
+    float S = gc * dgc;
+    for (int j = 0; j < i; ++j) S += gb[L.gam + (size_t)j * NT + t] * gb[L.dgam + (size_t)j * NT + t];
+    for (int j = 0; j <= i; ++j) {
+      const float ds = j < i ? gb[L.gam + (size_t)j * NT + t] * (gb[L.dgam + (size_t)j * NT + t] - S)
+                             : gc * (dgc - S);
+#pragma unroll
+      for (int q = 0; q < F / 4; ++q) dxu[q] += ds * summ[j * (F / 4) + q];
     }
-    if (i > 0) {
-      // softmax backward: dsims_j = gamma_j (dgamma_j - sum_k gamma_k dgamma_k)
-      float S = gc * dgc;
-      for (int j = 0; j < i; ++j) S += gb[L.gam + (size_t)j * NT + t] * gb[L.dgam + (size_t)j * NT + t];
-      for (int j = 0; j <= i; ++j) {
-        const float ds = j < i ? gb[L.gam + (size_t)j * NT + t] * (gb[L.dgam + (size_t)j * NT + t] - S)
-                               : gc * (dgc - S);
+  }
 #pragma unroll
-        for (int f = 0; f < F; ++f) dxu[f] += ds * summ[j * F + f];
-      }
-    }
-#pragma unroll
-    for (int f = 0; f < F; ++f) DXU[(size_t)t * F + f] = (T)dxu[f];
+  for (int q = 0; q < F / 4; ++q) {
+    store4(dxu_row + 4 * q, dxu[q]);
+    store4(dxqw_row + 4 * q, gc * dout[q]);
   }
 }
 
@@ -374,15 +398,19 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
 template <typename T, int FT, int HTT>
 static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
   const dim3 grid(p.B * p.H * p.nchunk), block(64 * kMemoWaves);
+  const int nblk = (p.NC * 16 + kMemoThreads - 1) / kMemoThreads;
   if (bwd) {
     hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, true>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H), dim3(kMemoThreads), 0, stream, p);
+    hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H), dim3(kMemoThreads), 0, stream, p);
+  hipLaunchKernelGGL((memo_summary_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(16 * FT), 0, stream, p);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, false>), grid, block, 0, stream, p);
   return hipGetLastError();

@@ -247,6 +247,11 @@ __device__ __forceinline__ f4 load4(const __bf16* __restrict__ p) {
   return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 __device__ __forceinline__ f4 load4(const float* __restrict__ p) { return *reinterpret_cast<const f4*>(p); }
+// four consecutive values at p from fp32
+__device__ __forceinline__ void store4(__bf16* __restrict__ p, f4 v) {
+  *reinterpret_cast<bf4*>(p) = to_frag<__bf16>(v).v;
+}
+__device__ __forceinline__ void store4(float* __restrict__ p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 
 // Store four values to X[r][c0 + 4g + j]
 __device__ __forceinline__ void store_f4(__bf16* __restrict__ x, int ld, int c0, f4 v) {
