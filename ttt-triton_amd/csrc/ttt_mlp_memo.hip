@@ -15,8 +15,8 @@
 //   memo_summary_kernel   one workgroup per (chain, segment): the segment summaries;
 //   memo_gate_kernel      one thread per token: the gates (written as
 //                         gamma^T [NS][tokens] plus the current-segment gate);
-//   memo_combine_kernel   one workgroup per (chain, 256-token chunk): for each
-//                         memo state j below the chunk's last segment, stage
+//   memo_combine_kernel   one workgroup per (chain, pair of 256-token chunks):
+//                         for each memo state j below a chunk's last segment, stage
 //                         W1_j/W2_j into LDS in MFMA operand order (as the cached
 //                         readout does), run the chunk's tiles of later
 //                         segments through R_j and accumulate gamma_j R_j (forward)
@@ -117,8 +117,8 @@ __global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p
 }
 
 // ------------------------------------------------------------------ R_j over a chunk
-constexpr int kMemoWaves = 4;
-constexpr int kMemoTilesPerWave = 4;
+constexpr int kMemoWaves = 8;
+constexpr int kMemoTilesPerWave = 2;
 constexpr int kMemoChunkTiles = kMemoWaves * kMemoTilesPerWave;  // mini-batches (16 tokens each) per workgroup
 
 template <typename T, int FT, int HTT> struct MemoShared {
@@ -134,212 +134,235 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
   constexpr int FF = 16 * HTT;
   constexpr int K = 16;
   constexpr int NTW = kMemoTilesPerWave;
+  constexpr int NB = FT * HTT / kMemoWaves;  // W1 (and W2) blocks each wave stages
   __shared__ MemoShared<T, FT, HTT> sh;
 
-  // blockIdx -> (chain, chunk), the chunks of one chain on one XCD (shared L2)
+  // blockIdx -> (chain, chunk pair), the pairs of one chain on one XCD (shared
+  // L2).  Chunk c needs about 2c+1 memo states, so a workgroup takes chunks c
+  // and nchunk-1-c: every workgroup then does about the same work, which keeps
+  // the in-order dispatch from waiting on a few long workgroups.
+  const int npair = (p.nchunk + 1) >> 1;
   const int total = gridDim.x;
   int lin = blockIdx.x;
   if ((total & 7) == 0) lin = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int chain = lin / p.nchunk;
-  const int chunk = lin - chain * p.nchunk;
+  const int chain = lin / npair;
+  const int pair = lin - chain * npair;
   const int h = chain % p.H;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
 
   const int wave = threadIdx.x >> 6;
   const int l = lane_id(), g = l >> 4, n = l & 15;
-
-  const int c0 = chunk * kMemoChunkTiles;                      // first mini-batch of the chunk
-  const int clast = min(c0 + kMemoChunkTiles, NC) - 1;         // last mini-batch of the chunk
-  const int jmax = clast / M;                                  // memo states 0..jmax-1 serve this chunk
-  const int t0 = c0 + wave * NTW;                              // first mini-batch of this wave
-  const int nv = max(0, min(NTW, NC - t0));                    // valid tiles of this wave
-  const int tl = min(t0 + max(nv, 1) - 1, NC - 1);             // a valid tile index for padding
-
   const size_t xoff = (size_t)chain * NT * F;
   const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
   float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
 
-  // XQ operand frags (free = token, k = feature) and XQ in C layout (token rows)
-  Frag<T> xq[NTW][FT];
-  f4 xqc[NTW][FT];
-  int seg[NTW];
-#pragma unroll
-  for (int t = 0; t < NTW; ++t) {
-    const int tt = t < nv ? t0 + t : tl;
-    seg[t] = t < nv ? tt / M : -1;
-    const T* x = XQ + (size_t)tt * K * F;
-#pragma unroll
-    for (int kb = 0; kb < FT; ++kb) {
-      xq[t][kb] = load_frag(x, F, 16 * kb);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xqc[t][kb][j] = (float)x[(4 * g + j) * F + 16 * kb + n];
-    }
-  }
-  float lw[FT], lb[FT];
-#pragma unroll
-  for (int c = 0; c < FT; ++c) {
-    lw[c] = p.ln_w[h * F + 16 * c + n];
-    lb[c] = p.ln_b[h * F + 16 * c + n];
-  }
-
-  // forward: sum_j gamma_j R_j; backward: dOut (C layout)
-  f4 oacc[NTW][FT];
-#pragma unroll
-  for (int t = 0; t < NTW; ++t) {
-#pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      if constexpr (BWD) {
-        const T* d = static_cast<const T*>(p.dout) + xoff + (size_t)(t < nv ? t0 + t : tl) * K * F;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) oacc[t][c][j] = (float)d[(4 * g + j) * F + 16 * c + n];
-      } else {
-        oacc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
-  }
-
-  const float invF = 1.0f / (float)F;
 #pragma unroll 1
-  for (int jm = 0; jm < jmax; ++jm) {
-    // ---- stage memo state jm (the previous state's reads are done); request
-    //      this state's gates of the wave's tokens first (forward)
-    __syncthreads();
-    f4 gjv[NTW];
-    if constexpr (!BWD) {
-#pragma unroll
-      for (int t = 0; t < NTW; ++t)
-        gjv[t] = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + 4 * g);
-    }
-    {
-      const size_t st = (size_t)chain * NS + jm;
-      const float* __restrict__ w1 = p.W1 + st * F * FF;
-      const float* __restrict__ w2 = p.W2 + st * FF * F;
-      for (int blk = wave; blk < FT * HTT; blk += kMemoWaves) {
-        const int kb = blk / HTT, ht = blk - kb * HTT;
-        f4 x;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
-        sh.w1[blk][l] = to_frag<T>(x).v;
-      }
-      for (int blk = wave; blk < HTT * FT; blk += kMemoWaves) {
-        const int ht = blk / FT, ct = blk - ht * FT;
-        f4 x;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
-        sh.w2[blk][l] = to_frag<T>(x).v;
-      }
-      for (int i = threadIdx.x; i < FF; i += 64 * kMemoWaves) sh.b1[i] = p.b1[st * FF + i];
-      for (int i = threadIdx.x; i < F; i += 64 * kMemoWaves) sh.b2[i] = p.b2[st * F + i];
-    }
-    __syncthreads();
+  for (int half = 0; half < 2; ++half) {
+    const int chunk = half == 0 ? pair : p.nchunk - 1 - pair;
+    if (half == 1 && chunk == pair) break;  // (uniform: the middle chunk of an odd count)
+    const int c0 = chunk * kMemoChunkTiles;                      // first mini-batch of the chunk
+    const int clast = min(c0 + kMemoChunkTiles, NC) - 1;         // last mini-batch of the chunk
+    const int jmax = clast / M;                                  // memo states 0..jmax-1 serve this chunk
+    const int t0 = c0 + wave * NTW;                              // first mini-batch of this wave
+    const int nv = max(0, min(NTW, NC - t0));                    // valid tiles of this wave
+    const int tl = min(t0 + max(nv, 1) - 1, NC - 1);             // a valid tile index for padding
 
-    bool any = false;
+    // R_j = (XQ + ln_b) + ln_w * N_j with N_j the normalised rows of
+    // gelu(XQ W1_j + b1_j) W2_j + b2_j.  The loop accumulates only the N_j terms:
+    //   forward   acc_N = sum_{j<i} gamma_j N_j, and sum_{j<i} gamma_j = 1 - gamma_i
+    //             multiplies (XQ + ln_b) once at the end;
+    //   backward  dgamma_j = dOut . R_j = base + (dOut * ln_w) . N_j with the
+    //             j-independent base = dOut . (XQ + ln_b) per token.
+    Frag<T> xq[NTW][FT];  // XQ operand frags (free = token, k = feature)
+    int seg[NTW];
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
-    if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
+    for (int t = 0; t < NTW; ++t) {
+      const int tt = t < nv ? t0 + t : tl;
+      seg[t] = t < nv ? tt / M : -1;
+#pragma unroll
+      for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(XQ + (size_t)tt * K * F, F, 16 * kb);
+    }
 
-    Tile acc[NTW][FT];
+    f4 oacc[NTW][FT];  // forward: acc_N; backward: dOut * ln_w (C layout, token rows)
+    f4 base[NTW];      // backward: dOut . (XQ + ln_b) of token rows 4g + j
 #pragma unroll
-    for (int t = 0; t < NTW; ++t)
-#pragma unroll
-      for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-    for (int ht = 0; ht < HTT; ht += 2) {
-      Frag<T> x2[2][NTW];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        Frag<T> w1f[FT];
-#pragma unroll
-        for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
-        const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
-#pragma unroll
-        for (int t = 0; t < NTW; ++t) {
-          Tile z;
-          z.v = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
-          f4 a;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
-          x2[hh][t] = to_frag<T>(a);
-        }
-      }
-      Frag<T> q0[FT], q1[FT];
+    for (int t = 0; t < NTW; ++t) {
+      base[t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        q0[c].v = sh.w2[ht * FT + c][l];
-        q1[c].v = sh.w2[(ht + 1) * FT + c][l];
+        if constexpr (BWD) {
+          const size_t r0 = (size_t)(t < nv ? t0 + t : tl) * K * F + 16 * c + n;
+          const T* d = static_cast<const T*>(p.dout) + xoff + r0;
+          const float w = p.ln_w[h * F + 16 * c + n], b = p.ln_b[h * F + 16 * c + n];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float dv = (float)d[(4 * g + j) * F];
+            oacc[t][c][j] = dv * w;
+            base[t][j] += dv * ((float)XQ[r0 + (4 * g + j) * F] + b);
+          }
+        } else {
+          oacc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
+        }
       }
+      if constexpr (BWD) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) base[t][j] = sum_row16(base[t][j]);
+      }
+    }
+
+    const float invF = 1.0f / (float)F;
+#pragma unroll 1
+    for (int jm = 0; jm < jmax; ++jm) {
+      // ---- stage memo state jm (the previous state's reads are done); request
+      //      this state's gates of the wave's tokens first (forward).  Each wave
+      //      stages NB blocks of W1 and of W2, every load of a matrix issued
+      //      before the first conversion.
+      __syncthreads();
+      f4 gjv[NTW];
+      if constexpr (!BWD) {
+#pragma unroll
+        for (int t = 0; t < NTW; ++t)
+          gjv[t] = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + 4 * g);
+      }
+      {
+        const size_t st = (size_t)chain * NS + jm;
+        const float* __restrict__ w1 = p.W1 + st * F * FF;
+        const float* __restrict__ w2 = p.W2 + st * FF * F;
+        f4 x[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int blk = wave + kMemoWaves * b, kb = blk / HTT, ht = blk - kb * HTT;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[b][j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) sh.w1[wave + kMemoWaves * b][l] = to_frag<T>(x[b]).v;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int blk = wave + kMemoWaves * b, ht = blk / FT, ct = blk - ht * FT;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[b][j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) sh.w2[wave + kMemoWaves * b][l] = to_frag<T>(x[b]).v;
+        for (int i = threadIdx.x; i < FF; i += 64 * kMemoWaves) sh.b1[i] = p.b1[st * FF + i];
+        for (int i = threadIdx.x; i < F; i += 64 * kMemoWaves) sh.b2[i] = p.b2[st * F + i];
+      }
+      __syncthreads();
+
+      bool any = false;
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
+      if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
+
+      Tile acc[NTW][FT];
 #pragma unroll
       for (int t = 0; t < NTW; ++t)
 #pragma unroll
-        for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
-    }
-
-    // ---- R_jm = XQ + LN(Z2 + b2) * ln_w + ln_b per token row; fold it in
-    float b2v[FT];
+        for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+      for (int ht = 0; ht < HTT; ht += 2) {
+        Frag<T> x2[2][NTW];
 #pragma unroll
-    for (int c = 0; c < FT; ++c) b2v[c] = sh.b2[16 * c + n];
+        for (int hh = 0; hh < 2; ++hh) {
+          Frag<T> w1f[FT];
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) {
-      if (seg[t] <= jm) continue;
-      const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
-      f4 gj = f4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (!BWD) gj = gjv[t];
-      f4 dg = f4{0.f, 0.f, 0.f, 0.f};
+          for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
+          const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v[FT], s = 0.f;
+          for (int t = 0; t < NTW; ++t) {
+            Tile z;
+            z.v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          v[c] = acc[t][c].v[j] + b2v[c];
-          s += v[c];
-        }
-        const float mean = sum_row16(s) * invF;
-        float q = 0.f;
+            for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
+            f4 a;
 #pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          v[c] -= mean;
-          q += v[c] * v[c];
-        }
-        const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
-        float d = 0.f;
-#pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          const float r = xqc[t][c][j] + lw[c] * (v[c] * rstd) + lb[c];
-          if constexpr (BWD) {
-            d += oacc[t][c][j] * r;
-          } else {
-            oacc[t][c][j] += gj[j] * r;
+            for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
+            x2[hh][t] = to_frag<T>(a);
           }
         }
-        if constexpr (BWD) dg[j] = sum_row16(d);
+        Frag<T> q0[FT], q1[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          q0[c].v = sh.w2[ht * FT + c][l];
+          q1[c].v = sh.w2[(ht + 1) * FT + c][l];
+        }
+#pragma unroll
+        for (int t = 0; t < NTW; ++t)
+#pragma unroll
+          for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
       }
-      if constexpr (BWD) {
-        if (n == 0) *reinterpret_cast<f4*>(gb + L.dgam + (size_t)jm * NT + tok0) = dg;
-      }
-    }
-  }
 
-  if constexpr (!BWD) {
-    // out = gamma_i XQW + sum_j gamma_j R_j (segment 0: gamma_i = 1, no cached terms)
-    const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
-    T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
+      // ---- N_jm = LN-normalised (Z2 + b2) per token row; fold it in
+      float b2v[FT];
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) {
-      if (t >= nv) continue;
-      const int tok0 = (t0 + t) * K + 4 * g;
-      const f4 gc = *reinterpret_cast<const f4*>(gb + L.gcur + tok0);
+      for (int c = 0; c < FT; ++c) b2v[c] = sh.b2[16 * c + n];
 #pragma unroll
-      for (int c = 0; c < FT; ++c)
+      for (int t = 0; t < NTW; ++t) {
+        if (seg[t] <= jm) continue;
+        f4 dg;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const size_t e = (size_t)(tok0 + j) * F + 16 * c + n;
-          OUT[e] = (T)(gc[j] * (float)XQW[e] + oacc[t][c][j]);
+          float v[FT], s = 0.f;
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            v[c] = acc[t][c].v[j] + b2v[c];
+            s += v[c];
+          }
+          const float mean = sum_row16(s) * invF;
+          float q = 0.f;
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            v[c] -= mean;
+            q += v[c] * v[c];
+          }
+          const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
+          if constexpr (BWD) {
+            float d = 0.f;
+#pragma unroll
+            for (int c = 0; c < FT; ++c) d += oacc[t][c][j] * v[c];
+            dg[j] = base[t][j] + rstd * sum_row16(d);
+          } else {
+            const float gr = gjv[t][j] * rstd;
+#pragma unroll
+            for (int c = 0; c < FT; ++c) oacc[t][c][j] += gr * v[c];
+          }
         }
+        if constexpr (BWD) {
+          const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
+          if (n == 0) *reinterpret_cast<f4*>(gb + L.dgam + (size_t)jm * NT + tok0) = dg;
+        }
+      }
     }
-  }
+
+    if constexpr (!BWD) {
+      // out = gamma_i XQW + (1 - gamma_i)(XQ + ln_b) + ln_w acc_N  (segment 0:
+      // gamma_i = 1 and acc_N = 0, so out = XQW)
+      const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
+      T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
+      float lw[FT], lb[FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        lw[c] = p.ln_w[h * F + 16 * c + n];
+        lb[c] = p.ln_b[h * F + 16 * c + n];
+      }
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) {
+        if (t >= nv) continue;
+        const int tok0 = (t0 + t) * K + 4 * g;
+        const f4 gc = *reinterpret_cast<const f4*>(gb + L.gcur + tok0);
+#pragma unroll
+        for (int c = 0; c < FT; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const size_t e = (size_t)(tok0 + j) * F + 16 * c + n;
+            const float rest = seg[t] > 0 ? (1.0f - gc[j]) * ((float)XQ[e] + lb[c]) + lw[c] * oacc[t][c][j] : 0.0f;
+            OUT[e] = (T)(gc[j] * (float)XQW[e] + rest);
+          }
+      }
+    }
+  }  // half
 }
 
 // ------------------------------------------------------------------ backward: softmax, dXU, dXQW
@@ -397,7 +420,7 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
 // ------------------------------------------------------------------ launchers
 template <typename T, int FT, int HTT>
 static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
-  const dim3 grid(p.B * p.H * p.nchunk), block(64 * kMemoWaves);
+  const dim3 grid(p.B * p.H * ((p.nchunk + 1) / 2)), block(64 * kMemoWaves);
   const int nblk = (p.NC * 16 + kMemoThreads - 1) / kMemoThreads;
   if (bwd) {
     hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, true>), grid, block, 0, stream, p);

@@ -377,61 +377,45 @@ __device__ __forceinline__ float rcp_f(float x) { return __builtin_amdgcn_rcpf(x
 __device__ __forceinline__ float rsqrt_f(float x) { return __builtin_amdgcn_rsqf(x); }
 
 // ---------------------------------------------------------------- GELU (tanh form)
-// tanh via exp: t = 1 - 2/(exp(2x)+1); saturates correctly for large |x|
-// (exp -> inf gives t = 1, exp -> 0 gives t = -1).
-__device__ __forceinline__ float tanh_f(float x) {
-  const float e = __expf(2.0f * x);
-  return 1.0f - 2.0f * rcp_f(e + 1.0f);
+// F.gelu(x, approximate="tanh") = 0.5 x (1 + tanh(u)), u = k x (1 + c x^2),
+// rewritten with 0.5 (1 + tanh(u)) = sigma(2u) = 1 / (1 + 2^(-2 log2(e) u)):
+// one v_exp_f32 and one v_rcp_f32, no cancellation in 1 + tanh for negative
+// x, and the right limits (2^(+big) = inf gives sigma = 0, 2^(-big) = 0 gives
+// sigma = 1).  With s = sigma(2u), q = s (1 - s) and D = du/dx = k + 3 c k x^2:
+//   gelu    = x s
+//   gelu'   = s + 2 x q D                          (ops/ttt_utils.py:51-54)
+//   gelu''  = 4 q (D + x (1 - 2 s) D^2 + 3 c k x^2)
+// the derivatives of 0.5 x (1 + tanh u) written in s (tanh u = 2 s - 1,
+// 1 - tanh^2 u = 4 q).
+constexpr float kGeluK = 0.7978845608028654f;                     // sqrt(2 / pi)
+constexpr float kGeluC = 0.044715f;
+constexpr float kGeluC3 = 3.0f * kGeluC * kGeluK;                  // 0.1070322243
+constexpr float kGeluA = -2.0f * 1.4426950408889634f * kGeluK;     // -2 log2(e) k
+constexpr float kGeluB = kGeluA * kGeluC;
+
+// sigma(2u) given x and x^2
+__device__ __forceinline__ float gelu_sig(float x, float x2) {
+  return rcp_f(1.0f + __builtin_amdgcn_exp2f(x * __builtin_fmaf(kGeluB, x2, kGeluA)));
 }
-// F.gelu(x, approximate="tanh"): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
-__device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;
-  return 0.5f * x * (1.0f + tanh_f(k0 * (x + 0.044715f * x * x * x)));
-}
-// derivative with the ops path's constants (ops/ttt_utils.py:51-54)
-__device__ __forceinline__ float gelu_bwd(float x) {
-  const float t = tanh_f(0.79788456f * x * (1.0f + 0.044715f * x * x));
-  return 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
-}
-// gelu_tanh(x) and gelu_bwd(x) from one tanh evaluation
+__device__ __forceinline__ float gelu_tanh(float x) { return x * gelu_sig(x, x * x); }
+// gelu(x) and gelu'(x)
 __device__ __forceinline__ void gelu_fwd_bwd(float x, float& y, float& dy) {
-  const float t = tanh_f(0.79788456f * x * (1.0f + 0.044715f * x * x));
-  y = 0.5f * x * (1.0f + t);
-  dy = 0.5f * x * ((1.0f - t * t) * (0.79788456f + 0.1070322243f * x * x)) + 0.5f * (1.0f + t);
+  const float x2 = x * x;
+  const float s = gelu_sig(x, x2);
+  const float D = __builtin_fmaf(kGeluC3, x2, kGeluK);
+  y = x * s;
+  dy = __builtin_fmaf(2.0f * x * D, s - s * s, s);
 }
-// gelu_tanh(x), gelu_bwd(x) and gelu_bwd2(x) from one tanh evaluation
+// gelu(x), gelu'(x) and gelu''(x)
 __device__ __forceinline__ void gelu_all(float x, float& y, float& dy, float& ddy) {
-  const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
   const float x2 = x * x;
-  const float t = tanh_f(k * x * (1.0f + c * x2));
-  const float s = 1.0f - t * t;
-  const float D = k + c3 * x2;
-  const float du = k * (1.0f + 3.0f * c * x2);
-  y = 0.5f * x * (1.0f + t);
-  dy = 0.5f * x * (s * D) + 0.5f * (1.0f + t);
-  ddy = 0.5f * s * D + 0.5f * s * du - x * t * s * du * D + c3 * x2 * s;
-}
-// gelu_bwd(x) and gelu_bwd2(x) from one tanh evaluation
-__device__ __forceinline__ void gelu_d1_d2(float x, float& dy, float& ddy) {
-  const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
-  const float x2 = x * x;
-  const float t = tanh_f(k * x * (1.0f + c * x2));
-  const float s = 1.0f - t * t;
-  const float D = k + c3 * x2;
-  const float du = k * (1.0f + 3.0f * c * x2);
-  dy = 0.5f * x * (s * D) + 0.5f * (1.0f + t);
-  ddy = 0.5f * s * D + 0.5f * s * du - x * t * s * du * D + c3 * x2 * s;
-}
-// d/dx of gelu_bwd above, differentiating the same expression:
-//   gelu_bwd = 0.5 x s D + 0.5 (1 + t),  t = tanh(u), u = k x (1 + c x^2),
-//   s = 1 - t^2, D = k + c3 x^2, du/dx = k (1 + 3 c x^2)
-__device__ __forceinline__ float gelu_bwd2(float x) {
-  const float k = 0.79788456f, c = 0.044715f, c3 = 0.1070322243f;
-  const float t = tanh_f(k * x * (1.0f + c * x * x));
-  const float s = 1.0f - t * t;
-  const float D = k + c3 * x * x;
-  const float du = k * (1.0f + 3.0f * c * x * x);
-  return 0.5f * s * D + 0.5f * s * du - x * t * s * du * D + c3 * x * x * s;
+  const float s = gelu_sig(x, x2);
+  const float D = __builtin_fmaf(kGeluC3, x2, kGeluK);
+  const float q = s - s * s;
+  const float xD = x * D;
+  y = x * s;
+  dy = __builtin_fmaf(2.0f * xD, q, s);
+  ddy = 4.0f * q * (D + __builtin_fmaf(kGeluC3, x2, xD * D * (1.0f - 2.0f * s)));
 }
 
 }  // namespace ttt
