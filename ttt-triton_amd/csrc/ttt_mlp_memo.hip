@@ -256,11 +256,13 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
       if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
 
-      Tile acc[NTW][FT];
+      Tile acc[NTW][FT];  // Z2 + b2 (b2 rides in the accumulator)
 #pragma unroll
-      for (int t = 0; t < NTW; ++t)
+      for (int c = 0; c < FT; ++c) {
+        const float b2 = sh.b2[16 * c + n];
 #pragma unroll
-        for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < NTW; ++t) acc[t][c].v = f4{b2, b2, b2, b2};
+      }
 #pragma unroll 1
       for (int ht = 0; ht < HTT; ht += 2) {
         Frag<T> x2[2][NTW];
@@ -273,12 +275,12 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
 #pragma unroll
           for (int t = 0; t < NTW; ++t) {
             Tile z;
-            z.v = f4{0.f, 0.f, 0.f, 0.f};
+            z.v = bias;  // b1 rides in the accumulator
 #pragma unroll
             for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
             f4 a;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
+            for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j]);
             x2[hh][t] = to_frag<T>(a);
           }
         }
@@ -295,9 +297,6 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       }
 
       // ---- N_jm = LN-normalised (Z2 + b2) per token row; fold it in
-      float b2v[FT];
-#pragma unroll
-      for (int c = 0; c < FT; ++c) b2v[c] = sh.b2[16 * c + n];
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {
         if (seg[t] <= jm) continue;
@@ -307,7 +306,7 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
           float v[FT], s = 0.f;
 #pragma unroll
           for (int c = 0; c < FT; ++c) {
-            v[c] = acc[t][c].v[j] + b2v[c];
+            v[c] = acc[t][c].v[j];
             s += v[c];
           }
           const float mean = sum_row16(s) * invF;

@@ -101,11 +101,13 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
     for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(x, F, 16 * kb);
   }
 
-  Tile acc[NT][FT];
+  Tile acc[NT][FT];  // Z2 + b2 (b2 rides in the accumulator)
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int c = 0; c < FT; ++c) {
+    const float b2 = sh.b2[16 * c + n];
 #pragma unroll
-    for (int c = 0; c < FT; ++c) acc[t][c].v = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NT; ++t) acc[t][c].v = f4{b2, b2, b2, b2};
+  }
 
 #pragma unroll 1
   for (int ht = 0; ht < HTT; ht += 2) {
@@ -119,12 +121,12 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         Tile z;
-        z.v = f4{0.f, 0.f, 0.f, 0.f};
+        z.v = bias;  // b1 rides in the accumulator
 #pragma unroll
         for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
         f4 a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j] + bias[j]);
+        for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j]);
         x2[hh][t] = to_frag<T>(a);
       }
     }
@@ -140,11 +142,10 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
       for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
   }
 
-  // ---- b2, LayerNorm over the F features of each token row, residual, store
-  float b2v[FT], lwv[FT], lbv[FT];
+  // ---- LayerNorm over the F features of each token row, residual, store
+  float lwv[FT], lbv[FT];
 #pragma unroll
   for (int c = 0; c < FT; ++c) {
-    b2v[c] = sh.b2[16 * c + n];
     lwv[c] = sh.lnw[16 * c + n];
     lbv[c] = sh.lnb[16 * c + n];
   }
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
       float v[FT], s = 0.f;
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        v[c] = acc[t][c].v[j] + b2v[c];
+        v[c] = acc[t][c].v[j];
         s += v[c];
       }
       const float mean = sum_row16(s) * invF;
