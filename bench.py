@@ -292,7 +292,7 @@ def run_memo(torch, steps, warmup, only=None):
     _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
     for _ in range(warmup):
         _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
-        memo_combine_backward(xq, xqw, *ws, lw, lb, MEMO_M, gates, dout)
+        memo_combine_backward(xq, xu, xqw, *ws, lw, lb, MEMO_M, gates, dout)
     torch.cuda.synchronize()
     tm = Timer(torch)
     for _ in range(steps):
@@ -301,7 +301,7 @@ def run_memo(torch, steps, warmup, only=None):
             _, gates = memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M)
         if only != "memo_fwd":
             tm.mark("ttt_mlp_memo_combine_bwd")
-            memo_combine_backward(xq, xqw, *ws, lw, lb, MEMO_M, gates, dout)
+            memo_combine_backward(xq, xu, xqw, *ws, lw, lb, MEMO_M, gates, dout)
     tm.mark(None)
     sp = tm.spans()
     return {k: statistics.mean(v) for k, v in sp.items()}

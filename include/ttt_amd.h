@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 6
+#define TTT_AMD_ABI_VERSION 7
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -173,7 +173,7 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
                            float* out, void* stream);
 
 /* Bytes of the gates buffer of ttt_mlp_memo_combine / _bwd: B*H chains x
- * (2*NS*NC*K + NC*K + NS*F) floats (rounded up to 16 bytes), NS = ceil(NC/M);
+ * (2*NS*NC*K + 2*NC*K + NS*F) floats (rounded up to 16 bytes), NS = ceil(NC/M);
  * 0 for unsupported sizes. */
 size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M);
 
@@ -197,15 +197,19 @@ int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const v
                          int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
                          void* out, float* gates, size_t gates_bytes, void* stream);
 
-/* Backward of ttt_mlp_memo_combine: gradients wrt XU and XQW only (the
- * reference detaches the summaries and runs the cached readouts without
- * gradient).  `gates` as written by the forward call (its gate-gradient part
- * is overwritten); dXU, dXQW [B,H,NC,K,F] dtype. */
-int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XQW, const float* W1_memo,
+/* Backward of ttt_mlp_memo_combine: gradients wrt XK, XU and XQW.  As in
+ * the reference, the cached readouts carry no gradient and a segment's
+ * summary carries one only as the current summary of its own tokens' gates
+ * (ttt_layer.py:519,528; it is cached detached, :521,559): dXK is the same
+ * for every token of a segment, and 0 in segment 0.  `gates` as written by
+ * the forward call (its gradient part is overwritten); dXK, dXU, dXQW
+ * [B,H,NC,K,F] dtype. */
+int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, const float* W1_memo,
                              const float* b1_memo, const float* W2_memo, const float* b2_memo,
                              const float* ln_w, const float* ln_b, const void* dout,
                              int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
-                             float* gates, size_t gates_bytes, void* dXU, void* dXQW, void* stream);
+                             float* gates, size_t gates_bytes, void* dXK, void* dXU, void* dXQW,
+                             void* stream);
 
 #ifdef __cplusplus
 }

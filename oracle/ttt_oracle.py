@@ -322,11 +322,13 @@ def memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b
 
     The sequence is cut into segments of M mini-batches.  Segment 0 keeps its
     output.  For a token t of segment i >= 1, with summary_j = mean of XK over
-    segment j (no gradient), sims_j = XU_t . summary_j for j = 0..i and
-    gamma = softmax(sims):
+    segment j, sims_j = XU_t . summary_j for j = 0..i and gamma = softmax(sims):
         out_t = gamma_i XQW_t + sum_{j<i} gamma_j R_j(XQ_t)
     where R_j is the cached readout with the memo state j (no gradient).
-    Gradients flow into XQW and XU only, as in the reference.
+    Gradients flow into XQW, XU and XK, as in the reference: the current
+    segment's summary enters its own sims without detach (ttt_layer.py:519,528)
+    and is cached detached (:521,559), so XK of segment i gets a gradient only
+    through segment i's current-summary term.
 
     XQ, XK, XU, XQW [B,H,NC,K,F]; *_memo [B,H,NS,...] with NS = ceil(NC/M);
     ln_w, ln_b [H,F].  Computes in `dtype` (the reference's bf16 casts of gamma
@@ -340,9 +342,9 @@ def memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b
         xq = XQ[:, :, s0:s1].to(dtype)
         xu = XU[:, :, s0:s1].to(dtype)
         xqw = XQW[:, :, s0:s1].to(dtype)
-        summ = XK[:, :, s0:s1].to(dtype).mean(dim=(2, 3)).detach()  # [B,H,F]
+        summ = XK[:, :, s0:s1].to(dtype).mean(dim=(2, 3))  # [B,H,F]
         if i == 0:
-            summaries.append(summ)
+            summaries.append(summ.detach())
             outs.append(xqw)
             continue
         sims = torch.stack([(xu * sm[:, :, None, None, :]).sum(-1) for sm in summaries + [summ]], dim=-1)
@@ -354,7 +356,7 @@ def memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b
                                    ln_w, ln_b, eps, dtype=dtype)
             acc = acc + gam[..., j:j + 1] * r
         outs.append(acc)
-        summaries.append(summ)
+        summaries.append(summ.detach())
     return torch.cat(outs, dim=2)
 
 

@@ -191,7 +191,7 @@ def test_memo_combine_validation(lib):
     B, H, NC, K, F, FF, M = 2, 3, 10, 16, 64, 256, 3
     NS = -(-NC // M)
     need = lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M)
-    per_chain = 2 * NS * NC * K + NC * K + NS * F
+    per_chain = 2 * NS * NC * K + 2 * NC * K + NS * F
     assert need == B * H * ((per_chain + 3) // 4 * 4) * 4
     assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, 0) == 0
     assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, 48, M) == 0
@@ -211,6 +211,8 @@ def test_memo_combine_validation(lib):
     assert fwd(out=None) == E_NULL
     assert fwd(ptrs=[P] * 2 + [None] + [P] * 7) == E_NULL
     assert fwd(dtype=5) == E_DTYPE
-    bwd = [P] * 9 + [B, H, NC, K, F, FF, M, BF16, 1e-6]
-    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need - 4, P, P, None) == E_WS
-    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, None, P, None) == E_NULL
+    bwd = [P] * 10 + [B, H, NC, K, F, FF, M, BF16, 1e-6]
+    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need - 4, P, P, P, None) == E_WS
+    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, None, P, P, None) == E_NULL
+    assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, P, None, P, None) == E_NULL
+    assert lib.ttt_mlp_memo_combine_bwd(*([P, None] + [P] * 8 + bwd[10:]), P, need, P, P, P, None) == E_NULL

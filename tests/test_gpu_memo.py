@@ -3,8 +3,8 @@
 The oracle (`memo_combine`, ttt_layer.py:506-561 restated) runs in fp64 on the
 same (rounded) inputs.  Tolerances: fp32 max-abs <= 1e-4, scaled by the
 tensor's magnitude above 1; bf16 inputs rel-L2 <= 2e-2.  Gradients are those
-of the oracle's autograd wrt XU and XQW (the only inputs the reference's loop
-differentiates)."""
+of the oracle's autograd wrt XK, XU and XQW (the inputs the reference's loop
+differentiates; XK only through each segment's current summary)."""
 
 import sys
 
@@ -40,24 +40,27 @@ def _inputs(B, H, NC, F_, FF, M, seed, dtype=torch.float32, xu_scale=0.3):
 KEYS = ("XQ", "XK", "XU", "XQW", "W1", "b1", "W2", "b2", "ln_w", "ln_b")
 
 
+GRADS = ("XK", "XU", "XQW")
+
+
 def _oracle(d, M):
     a = {k: d[k].double() for k in KEYS}
-    a["XU"].requires_grad_(True)
-    a["XQW"].requires_grad_(True)
+    for k in GRADS:
+        a[k].requires_grad_(True)
     out = O.memo_combine(*(a[k] for k in KEYS), M)
     out.backward(d["dOut"].double())
-    return out.detach(), a["XU"].grad, a["XQW"].grad
+    return (out.detach(),) + tuple(a[k].grad for k in GRADS)
 
 
 def _gpu(d, M):
     from ttt_amd.memo import mlp_memo_combine
     g = {k: d[k].cuda() for k in KEYS}
-    g["XU"].requires_grad_(True)
-    g["XQW"].requires_grad_(True)
+    for k in GRADS:
+        g[k].requires_grad_(True)
     out = mlp_memo_combine(*(g[k] for k in KEYS), M)
     out.backward(d["dOut"].cuda())
     torch.cuda.synchronize()
-    return out.detach(), g["XU"].grad, g["XQW"].grad
+    return (out.detach(),) + tuple(g[k].grad for k in GRADS)
 
 
 @pytest.mark.parametrize("B,H,NC,F_,FF,M", [
@@ -69,10 +72,10 @@ def _gpu(d, M):
 def test_memo_combine_fp32(B, H, NC, F_, FF, M):
     _say(f"memo combine fp32 B{B} H{H} NC{NC} F{F_} FF{FF} M{M}")
     d = _inputs(B, H, NC, F_, FF, M, seed=NC * 10 + M)
-    out, dxu, dxqw = _gpu(d, M)
-    ref, rdxu, rdxqw = _oracle(d, M)
+    out, dxk, dxu, dxqw = _gpu(d, M)
+    ref, rdxk, rdxu, rdxqw = _oracle(d, M)
     bad = []
-    for name, a, b in (("out", out, ref), ("dXU", dxu, rdxu), ("dXQW", dxqw, rdxqw)):
+    for name, a, b in (("out", out, ref), ("dXK", dxk, rdxk), ("dXU", dxu, rdxu), ("dXQW", dxqw, rdxqw)):
         err, bound = max_abs(a, b), FP32_ATOL * max(1.0, float(b.abs().max()))
         _say(f"  {name}: max-abs {err:.3e} (bound {bound:.3e})")
         if err > bound:
@@ -85,13 +88,13 @@ def test_memo_combine_bf16(FF):
     B, H, NC, F_, M = 2, 3, 40, 64, 2
     _say(f"memo combine bf16 NC{NC} FF{FF} M{M}")
     d = _inputs(B, H, NC, F_, FF, M, seed=7 + FF, dtype=torch.bfloat16)
-    out, dxu, dxqw = _gpu(d, M)
-    ref, rdxu, rdxqw = _oracle(d, M)
-    assert out.dtype == torch.bfloat16 and dxu.dtype == torch.bfloat16
+    out, dxk, dxu, dxqw = _gpu(d, M)
+    ref, rdxk, rdxu, rdxqw = _oracle(d, M)
+    assert out.dtype == torch.bfloat16 and dxu.dtype == torch.bfloat16 and dxk.dtype == torch.bfloat16
     bad = []
     for name, a, b in (("out", out, ref), ("out - XQW", out.float().cpu() - d["XQW"].float(),
                                             ref - d["XQW"].double()),
-                       ("dXU", dxu, rdxu), ("dXQW", dxqw, rdxqw)):
+                       ("dXK", dxk, rdxk), ("dXU", dxu, rdxu), ("dXQW", dxqw, rdxqw)):
         err = rel_l2(a, b)
         _say(f"  {name}: rel-L2 {err:.3e}")
         if err > BF16_RTOL:
@@ -101,9 +104,10 @@ def test_memo_combine_bf16(FF):
 
 def test_memo_combine_one_segment_is_identity():
     d = _inputs(1, 2, 5, 64, 64, 8, seed=3)
-    out, dxu, dxqw = _gpu(d, 8)
+    out, dxk, dxu, dxqw = _gpu(d, 8)
     torch.testing.assert_close(out.cpu(), d["XQW"], rtol=0, atol=0)
     assert float(dxu.abs().max()) == 0.0
+    assert float(dxk.abs().max()) == 0.0
     torch.testing.assert_close(dxqw.cpu(), d["dOut"], rtol=0, atol=0)
 
 

@@ -336,6 +336,39 @@ def test_memo_combine_gradients_match_finite_differences():
     assert torch.autograd.gradcheck(f, (XU, XQW), eps=1e-6, atol=1e-6, rtol=1e-5)
 
 
+def test_memo_combine_xk_gradient_is_through_the_current_summary_only():
+    """The reference differentiates segment i's summary only where it is the
+    current one (ttt_layer.py:519,528; the cached copy is detached, :521,559).
+    XK of segment i moves the outputs of segments i..NS-1, so its reference
+    gradient is the finite-difference derivative of segment i's outputs alone;
+    segment 0's summary is never differentiated."""
+    d, M = _memo_inputs(NC=7, M=2, F_=8, FF=16, seed=54)
+    d["XU"] = d["XU"] * 3
+    XK = d["XK"].clone().requires_grad_(True)
+    w = torch.randn(d["XQ"].shape, generator=torch.Generator().manual_seed(55), dtype=DT)
+    out = O.memo_combine(d["XQ"], XK, d["XU"], d["XQW"], d["W1"], d["b1"], d["W2"], d["b2"], d["ln_w"], d["ln_b"], M)
+    (out * w).sum().backward()
+    NC = d["XQ"].shape[2]
+    assert float(XK.grad[:, :, :M].abs().max()) == 0.0
+    v = torch.randn(d["XK"].shape, generator=torch.Generator().manual_seed(56), dtype=DT)
+    h = 1e-6
+    for i in range(1, O.ceil_div(NC, M)):
+        s0, s1 = i * M, min((i + 1) * M, NC)
+        vi = torch.zeros_like(v)
+        vi[:, :, s0:s1] = v[:, :, s0:s1]
+
+        def seg_loss(xk):
+            o = O.memo_combine(d["XQ"], xk, d["XU"], d["XQW"], d["W1"], d["b1"], d["W2"], d["b2"], d["ln_w"],
+                               d["ln_b"], M)
+            return float((o[:, :, s0:s1] * w[:, :, s0:s1]).sum())
+        fd = (seg_loss(d["XK"] + h * vi) - seg_loss(d["XK"] - h * vi)) / (2 * h)
+        ad = float((XK.grad * vi).sum())
+        assert abs(fd - ad) <= 1e-6 * max(1.0, abs(fd)), (i, fd, ad)
+        # every token of the segment gets the same gradient (a mean's derivative)
+        gseg = XK.grad[:, :, s0:s1]
+        torch.testing.assert_close(gseg, gseg[:, :, :1, :1].expand_as(gseg), rtol=0, atol=1e-14)
+
+
 # --- backward -------------------------------------------------------------------
 
 def test_linear_backward_autograd_matches_finite_differences():

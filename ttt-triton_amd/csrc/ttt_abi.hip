@@ -427,17 +427,20 @@ int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const v
   return hip_status(ttt::launch_mlp_memo(p, dtype, false, static_cast<hipStream_t>(stream)));
 }
 
-int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XQW, const float* W1_memo, const float* b1_memo,
-                             const float* W2_memo, const float* b2_memo, const float* ln_w, const float* ln_b,
-                             const void* dout, int B, int H, int NC, int K, int F, int FF, int M, int dtype,
-                             float eps, float* gates, size_t gates_bytes, void* dXU, void* dXQW, void* stream) {
+int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, const float* W1_memo,
+                             const float* b1_memo, const float* W2_memo, const float* b2_memo, const float* ln_w,
+                             const float* ln_b, const void* dout, int B, int H, int NC, int K, int F, int FF, int M,
+                             int dtype, float eps, float* gates, size_t gates_bytes, void* dXK, void* dXU,
+                             void* dXQW, void* stream) {
   int st = check_memo(B, H, NC, K, F, FF, M, dtype, eps, gates_bytes, gates);
   if (st != TTT_OK) return st;
-  const void* req[] = {XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, dout, dXU, dXQW};
+  const void* req[] = {XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, dout, dXK, dXU, dXQW};
   for (const void* q : req) REQUIRE_PTR(q);
   ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC, F, FF, M,
                                      eps, gates);
+  p.XU = XU;
   p.dout = dout;
+  p.dXK = dXK;
   p.dXU = dXU;
   p.dXQW = dXQW;
   if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;

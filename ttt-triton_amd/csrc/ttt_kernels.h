@@ -90,7 +90,7 @@ constexpr int kMemoMaxStates = 256;
 struct MlpMemoParams {
   const void *XQ, *XK, *XU, *XQW, *dout;
   const float *W1, *b1, *W2, *b2, *ln_w, *ln_b;
-  void *out, *dXU, *dXQW;
+  void *out, *dXK, *dXU, *dXQW;
   float* gates;
   int B, H, NC, F, FF, M, NS, nchunk;
   float eps;

@@ -23,12 +23,17 @@
 //                         or dOut . R_j (backward: the gate gradients);
 //   memo_finish_kernel    (backward) one thread per token: the softmax
 //                         backward, dXU = sum_j dsims_j summary_j and
-//                         dXQW = gamma_i dOut.
+//                         dXQW = gamma_i dOut;
+//   memo_dxk_kernel       (backward) one workgroup per (chain, segment):
+//                         dXK = mean over the segment's tokens of
+//                         dsims_current XU, the same for each of its tokens.
 //
-// Gradients flow into XQW and XU only (the summaries and the cached readouts
-// carry none in the reference).  The gates buffer per chain (fp32) holds
-// gamma^T [NS][NT], the current gate [NT], the summaries [NS][F] and, in the
-// backward, the gate gradients [NS][NT] (NT = NC * 16 tokens).
+// Gradients flow into XQW, XU and XK.  The cached readouts carry none, and a
+// segment's summary carries one only as the current summary of its own
+// tokens' gates (the reference caches it detached).  The gates buffer per
+// chain (fp32) holds gamma^T [NS][NT], the current gate [NT], the summaries
+// [NS][F] and, in the backward, the gate gradients [NS][NT] and the
+// current-summary logit gradients [NT] (NT = NC * 16 tokens).
 #include "ttt_kernels.h"
 
 namespace ttt {
@@ -36,14 +41,15 @@ namespace ttt {
 constexpr int kMemoThreads = 256;
 
 struct MemoGateLayout {
-  size_t gam, gcur, summ, dgam, stride;  // float offsets within a chain's block
+  size_t gam, gcur, summ, dgam, dscur, stride;  // float offsets within a chain's block
   __host__ __device__ MemoGateLayout(int NC, int K, int F, int NS) {
     const size_t NT = (size_t)NC * K;
     gam = 0;
     gcur = gam + (size_t)NS * NT;
     summ = gcur + NT;
     dgam = summ + (size_t)NS * F;
-    stride = (dgam + (size_t)NS * NT + 3) & ~(size_t)3;
+    dscur = dgam + (size_t)NS * NT;
+    stride = (dscur + NT + 3) & ~(size_t)3;
   }
 };
 
@@ -53,19 +59,38 @@ size_t memo_gate_floats_per_chain(int NC, int K, int F, int M) {
 }
 
 // ------------------------------------------------------------------ summaries and gates
-// one workgroup of F threads per (chain, segment): mean of XK over the segment
+constexpr int kSegThreads = 256;  // threads of the per-(chain, segment) kernels
+
+// Sum over a segment's tokens t0..t1-1 of w(t) * X[t][f], for f = threadIdx.x % F,
+// kSegThreads / F token rows at a time; the block's total for column f is returned
+// to every thread of that column.
+template <typename T, int F, typename W>
+__device__ __forceinline__ float segment_column_sum(const T* __restrict__ X, int t0, int t1, W w, float* part) {
+  constexpr int R = kSegThreads / F;
+  const int f = threadIdx.x % F, r = threadIdx.x / F;
+  float acc = 0.f;
+#pragma unroll 4
+  for (int t = t0 + r; t < t1; t += R) acc += w(t) * (float)X[(size_t)t * F + f];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int q = 0; q < R; ++q) tot += part[q * F + f];
+  return tot;
+}
+
+// one workgroup per (chain, segment): mean of XK over the segment
 template <typename T, int F>
-__global__ __launch_bounds__(F) void memo_summary_kernel(MlpMemoParams p) {
+__global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams p) {
   constexpr int K = 16;
+  __shared__ float part[kSegThreads];
   const int chain = blockIdx.x / p.NS, j = blockIdx.x - chain * p.NS;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
   const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NT * F;
-  const int f = threadIdx.x;
   const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
-  float acc = 0.f;
-  for (int t = t0; t < t1; ++t) acc += (float)XK[(size_t)t * F + f];
-  p.gates[(size_t)chain * L.stride + L.summ + (size_t)j * F + f] = acc / (float)(t1 - t0);
+  const float tot = segment_column_sum<T, F>(XK, t0, t1, [](int) { return 1.0f; }, part);
+  if (threadIdx.x < F) p.gates[(size_t)chain * L.stride + L.summ + (size_t)j * F + threadIdx.x] = tot / (float)(t1 - t0);
 }
 
 // one workgroup per (chain, block of kMemoThreads tokens), one token per thread:
@@ -373,7 +398,7 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
   const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
-  const float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
+  float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
   __shared__ f4 summ[kMemoMaxStates * F / 4];
   const int t = blk * kMemoThreads + threadIdx.x;
   const int tmax = min(NT, (blk + 1) * kMemoThreads) - 1;
@@ -398,6 +423,7 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
     dxu[q] = f4{0.f, 0.f, 0.f, 0.f};
   }
   const float dgc = (dg4[0] + dg4[1]) + (dg4[2] + dg4[3]);
+  float dscur = 0.f;  // d loss / d (XU . current summary)
   if (i > 0) {
     // softmax backward: dsims_j = gamma_j (dgamma_j - sum_k gamma_k dgamma_k)
     float S = gc * dgc;
@@ -408,12 +434,34 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
 #pragma unroll
       for (int q = 0; q < F / 4; ++q) dxu[q] += ds * summ[j * (F / 4) + q];
     }
+    dscur = gc * (dgc - S);
   }
+  gb[L.dscur + t] = dscur;
 #pragma unroll
   for (int q = 0; q < F / 4; ++q) {
     store4(dxu_row + 4 * q, dxu[q]);
     store4(dxqw_row + 4 * q, gc * dout[q]);
   }
+}
+
+// one workgroup per (chain, segment): the summary's gradient (sum over the
+// segment's tokens of dsims_current XU) spread evenly over the segment's
+// tokens, dXK = that / (tokens in the segment); 0 for segment 0, whose
+// summary is never a current one with gates (its dsims_current are 0).
+template <typename T, int F>
+__global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) {
+  constexpr int K = 16;
+  __shared__ float part[kSegThreads];
+  const int chain = blockIdx.x / p.NS, j = blockIdx.x - chain * p.NS;
+  const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const MemoGateLayout L(NC, K, F, NS);
+  const float* __restrict__ ds = p.gates + (size_t)chain * L.stride + L.dscur;
+  const T* __restrict__ XU = static_cast<const T*>(p.XU) + (size_t)chain * NT * F;
+  T* __restrict__ DXK = static_cast<T*>(p.dXK) + (size_t)chain * NT * F;
+  const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
+  const float tot = segment_column_sum<T, F>(XU, t0, t1, [ds](int t) { return ds[t]; }, part);
+  const T v = (T)(tot / (float)(t1 - t0));
+  for (int t = t0 + (int)threadIdx.x / F; t < t1; t += kSegThreads / F) DXK[(size_t)t * F + threadIdx.x % F] = v;
 }
 
 // ------------------------------------------------------------------ launchers
@@ -426,9 +474,12 @@ static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t st
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((memo_dxk_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(kSegThreads), 0, stream, p);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((memo_summary_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(16 * FT), 0, stream, p);
+  hipLaunchKernelGGL((memo_summary_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(kSegThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);

@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -35,7 +35,7 @@ SIGNATURES = {
     "ttt_mlp_cached_readout": (_I, [_P] * 7 + [_I] * 8 + [_F] + [_P, _P]),
     "ttt_mlp_memo_gates_bytes": (_S, [_I] * 6),
     "ttt_mlp_memo_combine": (_I, [_P] * 10 + [_I] * 8 + [_F] + [_P, _P, _S, _P]),
-    "ttt_mlp_memo_combine_bwd": (_I, [_P] * 9 + [_I] * 8 + [_F] + [_P, _S, _P, _P, _P]),
+    "ttt_mlp_memo_combine_bwd": (_I, [_P] * 10 + [_I] * 8 + [_F] + [_P, _S, _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -9,9 +9,12 @@ over j = 0..i:
     out = gamma_i XQW + sum_{j<i} gamma_j (XQ + LN_1e-6(gelu(XQ W1_j + b1_j) W2_j + b2_j) ln_w + ln_b)
 
 Segment 0 keeps XQW.  The memo states are the `TritonMLP.apply` memo outputs
-with the same M.  Gradients flow into XQW and XU only: the reference detaches
-the summaries and runs the cached readouts under `torch.no_grad`.  Unlike the
-reference's cached-readout kernel, every (b,h) chain uses its own memo states.
+with the same M.  Gradients flow into XQW, XU and XK, as in the reference: it
+runs the cached readouts under `torch.no_grad`, and a segment's summary enters
+its own tokens' gates undetached (ttt_layer.py:519,528) but is cached detached
+(:521,559), so XK of a segment gets the mean-summary gradient of its own
+segment only.  Unlike the reference's cached-readout kernel, every (b,h)
+chain uses its own memo states.
 
 Layouts follow the caller (ttt_layer.py:453-561): XQ, XK, XU, XQW
 [B,H,NC,K,F]; W1_memo [B,H,NS,F,FF], b1_memo [B,H,NS,1,FF], W2_memo
@@ -78,45 +81,44 @@ def memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln
     return out, gates
 
 
-def memo_combine_backward(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M: int, gates, dout,
+def memo_combine_backward(XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M: int, gates, dout,
                           eps: float = READOUT_EPS):
-    """Gradients (dXU, dXQW) in XQW.dtype of the combiner run that produced `gates`."""
+    """Gradients (dXK, dXU, dXQW) in XQW.dtype of the combiner run that produced `gates`."""
     B, H, NC, K, F = XQ.shape
     FF = W1_memo.shape[-1]
-    dev = check_device(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, gates, dout)
+    dev = check_device(XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, gates, dout)
     mp = XQW.dtype
     code = dtype_code(mp)
-    xq, xqw, do = (as_act(t, mp) for t in (XQ, XQW, dout))
+    xq, xu, xqw, do = (as_act(t, mp) for t in (XQ, XU, XQW, dout))
     ws = [_f32(t) for t in (W1_memo, b1_memo, W2_memo, b2_memo)]
     lw, lb = _f32(ln_w), _f32(ln_b)
-    dxu = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
-    dxqw = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
+    dxk, dxu, dxqw = (torch.empty((B, H, NC, K, F), device=dev, dtype=mp) for _ in range(3))
     lib = _lib.load()
     with torch.cuda.device(dev):
-        st = lib.ttt_mlp_memo_combine_bwd(ptr(xq), ptr(xqw), *(ptr(t) for t in ws), ptr(lw), ptr(lb), ptr(do),
-                                          B, H, NC, K, F, FF, int(M), code, float(eps), ptr(gates), gates.numel(),
-                                          ptr(dxu), ptr(dxqw), stream_of(dev))
+        st = lib.ttt_mlp_memo_combine_bwd(ptr(xq), ptr(xu), ptr(xqw), *(ptr(t) for t in ws), ptr(lw), ptr(lb),
+                                          ptr(do), B, H, NC, K, F, FF, int(M), code, float(eps), ptr(gates),
+                                          gates.numel(), ptr(dxk), ptr(dxu), ptr(dxqw), stream_of(dev))
     _lib.check(st, "ttt_mlp_memo_combine_bwd")
-    return dxu, dxqw
+    return dxk, dxu, dxqw
 
 
 class MemoCombineFunction(torch.autograd.Function):
     """apply(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M[, eps]) -> out.
-    Differentiable wrt XU and XQW (as the reference's loop is)."""
+    Differentiable wrt XK, XU and XQW (as the reference's loop is)."""
 
     @staticmethod
     def forward(ctx, XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M, eps=READOUT_EPS):
         out, gates = memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M, eps)
-        ctx.save_for_backward(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, gates)
+        ctx.save_for_backward(XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, gates)
         ctx.M, ctx.eps = int(M), eps
-        ctx.dtypes = (XU.dtype, XQW.dtype)
+        ctx.dtypes = (XK.dtype, XU.dtype, XQW.dtype)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        XQ, XQW, W1, b1, W2, b2, lw, lb, gates = ctx.saved_tensors
-        dxu, dxqw = memo_combine_backward(XQ, XQW, W1, b1, W2, b2, lw, lb, ctx.M, gates, dout, ctx.eps)
-        return (None, None, dxu.to(ctx.dtypes[0]), dxqw.to(ctx.dtypes[1])) + (None,) * 8
+        XQ, XU, XQW, W1, b1, W2, b2, lw, lb, gates = ctx.saved_tensors
+        dxk, dxu, dxqw = memo_combine_backward(XQ, XU, XQW, W1, b1, W2, b2, lw, lb, ctx.M, gates, dout, ctx.eps)
+        return (None, dxk.to(ctx.dtypes[0]), dxu.to(ctx.dtypes[1]), dxqw.to(ctx.dtypes[2])) + (None,) * 8
 
 
 def mlp_memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M: int):
