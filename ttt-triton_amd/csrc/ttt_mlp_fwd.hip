@@ -43,7 +43,15 @@ template <int FT, int NW> struct MlpFwdShared {
   f4 z2p[NW][FT][64];   // per-wave partial Z2 (token-major tiles, register order)
   f4 z2bp[NW][FT][64];  // per-wave partial X2b W2
   f4 a2p[NW][64];       // per-wave partial (X2b X2^T)^T
+  f4 g2[FT][64];        // G2 (token-major tiles, register order), rows split over the waves
 };
+
+// The inner-loss LayerNorm is split over the waves by token rows when there
+// are as many waves as 16-feature tiles and F = 64: wave w takes rows
+// 4w..4w+3 (lane group g = w of every token-major tile) with lane l on
+// feature l, so a row's reductions span the 64 lanes and each lane does 4
+// rows instead of 16; G2 is then exchanged through LDS.
+template <int FT, int NW> constexpr bool kLnRowSplit = (NW == 4 && FT == 4);
 
 template <typename T, int FT, int NW>
 __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
@@ -109,6 +117,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
     lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
   }
+  const float lnw_l = kLnRowSplit<FT, NW> ? p.ln_w[h * F + l] : 0.f;  // feature l (row-split LayerNorm)
+  const float lnb_l = kLnRowSplit<FT, NW> ? p.ln_b[h * F + l] : 0.f;
   const float eps = p.eps;
   const Frag<T> I = identity_frag<T>();
 
@@ -150,9 +160,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     }
     const int xo = s * K * F * ST, eo = s * K * K * ST;
     const int us = s * Slot::BYTES;
-    Frag<T> xv[FT];
+    // the inner loss's target XV - XK: as frags (free = token), or, split by
+    // rows, rows 4*wave+j of feature l
+    Frag<T> xv[FT], xvr, xkr;
+    if constexpr (kLnRowSplit<FT, NW>) {
+      xvr = bload_ctile<T>(rXV, l * ST, xo + 4 * wave * F * ST, F);
+      xkr = bload_ctile<T>(rXK, l * ST, xo + 4 * wave * F * ST, F);
+    } else {
 #pragma unroll
-    for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
+      for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
+    }
     const Frag<T> etaTf = bload_frag<T>(rET, el, eo);  // [t_k x t_q]: eta[n][4g+j]
     const Frag<T> ef = bload_frag<T>(rET, e4, eo);     // last eta row
 
@@ -204,10 +221,48 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       }
     }
 
-    // ---- Z2 and its inner-loss gradient (every wave, identical)
+    // ---- Z2 and its inner-loss gradient
     Frag<T> xkTf[FT];
     Tile G2[FT];
-    {
+    if constexpr (kLnRowSplit<FT, NW>) {
+#pragma unroll
+      for (int q = 0; q < FT; ++q) xkTf[q] = to_frag<T>(transpose16(xk[0][q], I).v);
+      // rows 4*wave + j, feature l (= 16 (l >> 4) + n: lane group l >> 4 reads tile l >> 4)
+      const int lo = l >> 4;
+      const float b2l = lo == 0 ? b2_tm[0] : lo == 1 ? b2_tm[1] : lo == 2 ? b2_tm[2] : b2_tm[3];
+      f4 z = f4{b2l, b2l, b2l, b2l};
+#pragma unroll
+      for (int w = 0; w < NW; ++w) z += sh.z2p[w][lo][16 * wave + n];
+      const f4 tgt = frag_to_f4(xvr) - frag_to_f4(xkr);
+      constexpr float invF = 1.0f / F;
+      f4 mu, rs, xh, gx, s1, cc, g2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mu[j] = sum_wave(z[j]) * invF;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d = z[j] - mu[j];
+        rs[j] = rsqrt_f(sum_wave(d * d) * invF + eps);
+        xh[j] = d * rs[j];
+        gx[j] = (lnw_l * xh[j] + lnb_l - tgt[j]) * lnw_l;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s1[j] = sum_wave(gx[j]) * invF;
+        cc[j] = sum_wave(gx[j] * xh[j]) * invF;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) g2[j] = (gx[j] - s1[j] - xh[j] * cc[j]) * rs[j];
+      sh.g2[lo][16 * wave + n] = g2;
+      // saved G2, XH (this wave's rows of every tile) and the row statistics
+      const int sv = (lo * 64 + 16 * wave + n) * 16;
+      bstore_frag<float>(rSV, sv, us + Slot::G2, Frag<float>{g2});
+      bstore_frag<float>(rSV, sv, us + Slot::XH, Frag<float>{xh});
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSTD, Frag<float>{rs});
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::CC, Frag<float>{cc});
+      __syncthreads();  // G2 rows of every wave in
+#pragma unroll
+      for (int o = 0; o < FT; ++o) G2[o].v = sh.g2[o][l];
+    } else {
       f4 tgt[FT];
 #pragma unroll
       for (int q = 0; q < FT; ++q) {

@@ -212,6 +212,15 @@ __device__ __forceinline__ float sum_row16(float x) {
   x += dpp<0x121>(x);  // row_ror:1
   return x;
 }
+// sum over all 64 lanes, as a wave-uniform value: the row sums are
+// accumulated into row 3 with row_bcast:15 (rows 1, 3) and row_bcast:31
+// (rows 2, 3), and lane 63 is read out
+__device__ __forceinline__ float sum_wave(float x) {
+  x = sum_row16(x);
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xC, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
 // sum over the 4 lanes that share n (lanes n, n+16, n+32, n+48)
 __device__ __forceinline__ float sum_col4(float x) {
   x += __shfl_xor(x, 16, 64);
