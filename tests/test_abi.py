@@ -140,8 +140,11 @@ def test_mlp_saved_buffer(lib):
     assert lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, 9) == 0
     assert lib.ttt_mlp_saved_bytes(0, H, NC, K, F, FF, BF16) == 0
     w16 = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, BF16)
-    # per mini-batch: dZ1b and dZ1 [K x FF] in the activation type, two fp32 [K x F] partials
-    assert w16 == B * H * NC * (2 * FF * K * 2 + 2 * K * F * 4)
+    # per mini-batch: dZ1b and dZ1 [K x FF] in the activation type, two fp32 [K x F] partials;
+    # then the dXQ/dXK workers' control words (4 + one flag per chain and mini-batch, in
+    # 256-byte units)
+    ctrl = ((4 + B * H * NC) * 4 + 255) // 256 * 256
+    assert w16 == B * H * NC * (2 * FF * K * 2 + 2 * K * F * 4) + ctrl
     args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
     assert lib.ttt_mlp_bwd(*args, P, n16 - 1, P, w16, None) == E_WS
     assert lib.ttt_mlp_bwd(*args, None, n16, P, w16, None) == E_WS

@@ -188,3 +188,35 @@ def test_mlp_bwd_edges(NC, G, F_, FF, dt):
         if err > bound:
             bad.append(k)
     assert not bad
+
+
+@pytest.mark.parametrize("F_,FF", [(64, 256), (32, 128)])
+def test_mlp_bwd_fused_workers_finish_every_group(F_, FF):
+    """Where the dXQ/dXK pass runs inside the sweep's launch (as many waves per
+    chain as feature tiles), every (chain, checkpoint group) flag is raised,
+    every task was taken and no worker gave up waiting; the gradients match a
+    run whose workspace held stale control words from an earlier call."""
+    from ttt_amd import _lib
+    from ttt_amd.mlp import mlp_backward
+    B, H, NC, G = 2, 3, 11, 4
+    NK = -(-NC // G)
+    _say(f"fused dXQ/dXK workers bf16 F{F_} FF{FF} NC{NC} G{G}")
+    d = O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=31, dtype=torch.bfloat16, with_grad=True)
+    out, ck, _, last, saved = _fwd(d, G)
+    g = to_dev(d)
+    lib = _lib.load()
+    nws = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, 16, F_, FF, 1)
+    ws = torch.full((nws,), 0x7F, device="cuda", dtype=torch.uint8)  # stale control words
+    args = (g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    first = mlp_backward(*args, workspace=ws)
+    torch.cuda.synchronize()
+    slot = 2 * FF * 16 * 2 + 2 * F_ * 64
+    ctrl = ws[B * H * NC * slot:].view(torch.int32).cpu()
+    ntask = B * H * NK
+    assert int(ctrl[1]) == 0, "a worker timed out waiting for a group"
+    assert int(ctrl[0]) >= ntask
+    assert bool((ctrl[4:4 + ntask] == 1).all())
+    second = mlp_backward(*args, workspace=ws)
+    torch.cuda.synchronize()
+    for a, b in zip(first[0] + first[1], second[0] + second[1]):
+        assert torch.equal(a, b)

@@ -267,7 +267,7 @@ size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
-  return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype);
+  return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
 }
 
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
@@ -310,6 +310,9 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.b2_last = b2_last;
   p.saved = saved;
   p.ws = workspace;
+  // control words behind the handoff slots (sized for G = 1, the most groups)
+  p.dx_ctrl = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                     (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype));
   p.dXQ = dXQ;
   p.dXK = dXK;
   p.dXV = dXV;

@@ -52,6 +52,32 @@ template <> __device__ __forceinline__ void bstore_frag<float>(rsrc_t r, int vof
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f.v), r, voff, soff, 0);
 }
 
+// Device-coherent stores (cache policy sc1): written through to memory, so a
+// workgroup on another XCD that sees a later flag reads them without an L2
+// writeback by the writer.
+constexpr int kCpolDevice = 16;  // sc1
+template <typename T> __device__ __forceinline__ void bstore_frag_dev(rsrc_t r, int voff, int soff, Frag<T> f);
+template <> __device__ __forceinline__ void bstore_frag_dev<__bf16>(rsrc_t r, int voff, int soff, Frag<__bf16> f) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, kCpolDevice);
+}
+template <> __device__ __forceinline__ void bstore_frag_dev<float>(rsrc_t r, int voff, int soff, Frag<float> f) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f.v), r, voff, soff, kCpolDevice);
+}
+
+// Device-coherent loads (sc1): not served from a cache line that another
+// XCD's writes may have made stale.
+template <typename T> __device__ __forceinline__ Frag<T> bload_frag_dev(rsrc_t r, int voff, int soff);
+template <> __device__ __forceinline__ Frag<__bf16> bload_frag_dev<__bf16>(rsrc_t r, int voff, int soff) {
+  Frag<__bf16> f;
+  f.v = __builtin_bit_cast(bf4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kCpolDevice));
+  return f;
+}
+template <> __device__ __forceinline__ Frag<float> bload_frag_dev<float>(rsrc_t r, int voff, int soff) {
+  Frag<float> f;
+  f.v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCpolDevice));
+  return f;
+}
+
 // one element, as float
 template <typename T> __device__ __forceinline__ float bload1(rsrc_t r, int voff, int soff);
 template <> __device__ __forceinline__ float bload1<__bf16>(rsrc_t r, int voff, int soff) {

@@ -67,6 +67,8 @@ struct MlpBwdParams {
   const float *W1_last, *b1_last, *W2_last, *b2_last;
   const void* saved;  // per mini-batch values written by the forward
   void* ws;           // per mini-batch handoff from the reverse sweep to the dXQ/dXK pass (MlpBwdWsSlot)
+  int* dx_ctrl;       // fused dXQ/dXK workers: [task counter, timeout flag, pad, pad, group flags [B*H][NK]];
+                      // nullptr = a second launch after the sweep
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   int B, H, NC, F, FF, G, NK;
@@ -151,6 +153,8 @@ template <int F, int FF, int ST> struct MlpBwdWsSlot {
   static constexpr int BYTES = XKP + F * 64;
 };
 size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype);
+// bytes of the control words after the B*H*NC handoff slots of the MLP backward workspace
+size_t mlp_bwd_ctrl_bytes(int B, int H, int NC, int G);
 
 hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
 // bytes of one (chain, mini-batch) slot of the forward's saved buffer

@@ -1,4 +1,4 @@
-// TTT-MLP backward on gfx950, in two launches.
+// TTT-MLP backward on gfx950: a reverse sweep per chain and a dXQ/dXK pass.
 //
 // 1. mlp_bwd_kernel: one workgroup of NW = FF/64 wavefronts per (batch, head)
 //    chain, wave w owning hidden units S = [64w, 64w+64), walks the sequence
@@ -10,9 +10,13 @@
 //    The products with W1 (dXQ += dZ1b W1^T, dXK += dZ1 W1^T) do not feed the
 //    recurrence, so this pass hands dZ1b and dZ1 over instead (MlpBwdWsSlot)
 //    and never needs W1.
-// 2. mlp_bwd_dx_kernel: one wave per (chain, checkpoint group, feature tile),
+// 2. the dXQ/dXK pass: one wave per (chain, checkpoint group, feature tile),
 //    all independent: it walks its group forward from the checkpoint, W1^T in
-//    registers, and forms dXQ and dXK.
+//    registers, and forms dXQ and dXK.  With one wave per feature tile per
+//    chain (NW == F/16) and a CU to spare per chain, it runs inside the
+//    sweep's launch on the CUs the 192-odd sweeps leave idle, group by group
+//    as the sweeps publish them (mlp_bwd_dx_worker); otherwise it is a second
+//    launch (mlp_bwd_dx_kernel).
 //
 // In the reverse sweep W2 is needed (the gradient flows through products with
 // it): W2^T [F][FF] lives in LDS in fp32, columns XOR-swizzled so both access
@@ -59,8 +63,71 @@ size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
   return (size_t)2 * FF * 16 * t + (size_t)2 * F * 64;
 }
 
+// Control words of the fused dXQ/dXK workers: [0] next task, [1] set when a
+// worker gave up waiting for a group, then one flag per (chain, checkpoint group).
+constexpr int kDxCtrlHead = 4;
+size_t mlp_bwd_ctrl_bytes(int B, int H, int NC, int G) {
+  const size_t words = kDxCtrlHead + (size_t)B * H * ((NC + G - 1) / G);
+  return (words * 4 + 255) & ~(size_t)255;
+}
+
+// Polls of a group flag before a worker gives up (s_sleep 8 between polls:
+// about a second, against ~2 ms for a whole sweep).
+constexpr int kDxMaxPolls = 1 << 22;
+
+template <typename T, int FT, int NW>
+__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk);
+
+// Fused mode: workgroups B*H.. of the sweep's launch.  Each takes (chain,
+// checkpoint group) tasks in the order the sweep finishes them (last group
+// first), waits until the chain's sweep has published the group, and forms
+// that group's dXQ/dXK (mlp_bwd_dx_body, wave = feature tile).  Blocks are
+// dispatched in index order, so a worker only becomes resident after every
+// sweep workgroup has; the sweeps never wait for the workers, so every wait
+// ends (and a wait that exceeds kDxMaxPolls raises the timeout word instead
+// of spinning on).
+//
+// Visibility across XCDs without cache maintenance: the sweep writes the
+// handoff with device-coherent (sc1, written-through) stores, waits for them
+// to be acknowledged, then raises the group's flag with a device-scope
+// store; the worker polls the flag with device-scope loads and reads the
+// handoff with device-coherent (sc1) loads, which no stale L1 or L2 line
+// serves.  Neither side writes back or invalidates a whole L2.
+template <typename T, int FT, int NW>
+__device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
+  __shared__ int task_sh;
+  const int nchain = p.B * p.H, ntask = nchain * p.NK;
+  int* __restrict__ flags = p.dx_ctrl + kDxCtrlHead;
+  for (;;) {
+    if (threadIdx.x == 0) task_sh = atomicAdd(p.dx_ctrl, 1);
+    __syncthreads();
+    const int t = task_sh;
+    __syncthreads();  // every wave has read the task before thread 0 takes the next
+    if (t >= ntask) return;
+    const int kk = p.NK - 1 - t / nchain, chain = t - (t / nchain) * nchain;
+    if (threadIdx.x == 0) {
+      int polls = 0;
+      while (__hip_atomic_load(flags + chain * p.NK + kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        if (++polls > kDxMaxPolls) {
+          __hip_atomic_store(p.dx_ctrl + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+      }
+    }
+    __syncthreads();  // the group's flag was seen: its handoff stores are complete
+    mlp_bwd_dx_body<T, FT, NW>(p, chain, kk);
+  }
+}
+
 template <typename T, int FT, int NW>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
+  if constexpr (NW == FT) {
+    if ((int)blockIdx.x >= p.B * p.H) {
+      mlp_bwd_dx_worker<T, FT, NW>(p);
+      return;
+    }
+  }
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   constexpr int HT = 4;
@@ -415,7 +482,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
           dz1bF[o] = to_frag<T>(transpose16(dz1bf[o], I).v);
-          bstore_frag<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1BF, dz1bF[o]);
+          bstore_frag_dev<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1BF, dz1bF[o]);
         }
         f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -618,7 +685,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dZ1[o].v += dx2 * frag_to_f4(sp1s[o]);
           dz1f[o] = to_frag<T>(dZ1[o].v);
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
-          bstore_frag<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1F, dz1F[o]);
+          bstore_frag_dev<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1F, dz1F[o]);
           eg1F[o] = to_frag<T>(transpose16(g1ef[o], I).v);
         }
         // dXK partial over this slice: (-e G1) dW1'^T (dW1' not yet updated)
@@ -673,12 +740,23 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           for (int w = 0; w < NW; ++w) dxk += xa.get((w * FT + f) * 1024);
           mma16(dxq, dA1Tf, xkTf[f]);  // + dA1 XK
           mma16(dxk, dA1f, xqTf[f]);   // + dA1^T XQ
-          bstore_frag<float>(rWS, f4l + f * 1024, ws_ + WS::XQP, Frag<float>{dxq});
-          bstore_frag<float>(rWS, f4l + f * 1024, ws_ + WS::XKP, Frag<float>{dxk});
+          bstore_frag_dev<float>(rWS, f4l + f * 1024, ws_ + WS::XQP, Frag<float>{dxq});
+          bstore_frag_dev<float>(rWS, f4l + f * 1024, ws_ + WS::XKP, Frag<float>{dxk});
           bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dtgt[f]), I).v));
         }
       }
       __syncthreads();  // (2x) exchange area free for the next mini-batch
+      if (p.dx_ctrl != nullptr && s % G == 0) {
+        // checkpoint group s / G is complete: every wave's handoff stores
+        // (device-coherent, written through) acknowledged, then the group's
+        // flag raised for the workers.  (An agent-scope release fence would
+        // also write back the whole L2: ~20 us per group.)
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+          __hip_atomic_store(p.dx_ctrl + kDxCtrlHead + chain * NK + s / G, 1, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 
@@ -720,7 +798,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 // checkpoint and steps forward with the saved update operands,
 // W1_{s+1}^T = W1_s^T + (-e G1_s)^T XK_s.
 template <typename T, int FT, int NW>
-__global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
+__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   constexpr int FF = 64 * NW;
@@ -729,7 +807,6 @@ __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
   using Slot = MlpSavedSlot<F, FF, ST>;
   using WS = MlpBwdWsSlot<F, FF, ST>;
   const int NC = p.NC, G = p.G, NK = p.NK;
-  const int chain = blockIdx.x / NK, kk = blockIdx.x - chain * NK;
   const int c = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // feature tile
   const int l = lane_id(), g = l >> 4, n = l & 15;
 
@@ -762,12 +839,12 @@ __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
   };
   auto load_in = [&](int s, In& in) {
     const int ws_ = s * WS::BYTES;
-    in.aq = bload_frag<float>(rWS, f4l, ws_ + WS::XQP).v;
-    in.ak = bload_frag<float>(rWS, f4l, ws_ + WS::XKP).v;
+    in.aq = bload_frag_dev<float>(rWS, f4l, ws_ + WS::XQP).v;
+    in.ak = bload_frag_dev<float>(rWS, f4l, ws_ + WS::XKP).v;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
-      in.zb[hb] = bload_frag<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1BF);
-      in.zk[hb] = bload_frag<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1F);
+      in.zb[hb] = bload_frag_dev<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1BF);
+      in.zk[hb] = bload_frag_dev<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1F);
     }
   };
   const int s0 = kk * G, s1 = min(s0 + G, NC);
@@ -806,11 +883,50 @@ __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
 }
 
 template <typename T, int FT, int NW>
-static hipError_t launch_mlp_bwd_t(const MlpBwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+__global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
+  const int chain = blockIdx.x / p.NK, kk = blockIdx.x - chain * p.NK;
+  mlp_bwd_dx_body<T, FT, NW>(p, chain, kk);
+}
+
+__global__ void mlp_bwd_ctrl_clear_kernel(int* ctrl, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) ctrl[i] = 0;
+}
+
+// compute units of the current device (cached per device)
+static int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// Fused when the workgroups are alike (one wave per 64 hidden units = one per
+// feature tile) and every chain's sweep fits on the device at once with CUs to
+// spare for workers; otherwise the dXQ/dXK pass is a second launch.
+template <typename T, int FT, int NW>
+static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
+  const int chains = p.B * p.H, cus = device_cus();
+  const bool fused = NW == FT && p.dx_ctrl != nullptr && cus >= chains + 16;
+  if (!fused) {
+    p.dx_ctrl = nullptr;
+    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(chains), dim3(64 * NW), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW>), dim3(chains * p.NK), dim3(64 * FT), 0, stream, p);
+    return hipGetLastError();
+  }
+  const int nctrl = kDxCtrlHead + chains * p.NK;
+  hipLaunchKernelGGL(mlp_bwd_ctrl_clear_kernel, dim3((nctrl + 255) / 256), dim3(256), 0, stream, p.dx_ctrl, nctrl);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW>), dim3(p.B * p.H * p.NK), dim3(64 * FT), 0, stream, p);
+  // the sweeps, then one worker per CU: the first cus - chains run beside the
+  // sweeps, the rest start on the CUs the sweeps leave
+  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }
 

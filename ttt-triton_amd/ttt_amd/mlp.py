@@ -94,11 +94,14 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     return out, ck, memo, last, saved
 
 
-def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, eps: float = LN_EPS):
+def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, eps: float = LN_EPS,
+                 workspace=None):
     """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints, last =
     the final state and saved = the saved buffer, all from one mlp_forward
-    call with the same G.  Returns fp32 (dln_w [H,F], dln_b [H,F], dW1, db1,
-    dW2, db2) and (dXQ, dXV, dXK, deta) in XQ.dtype."""
+    call with the same G.  `workspace` (uint8, at least
+    ttt_mlp_bwd_workspace_bytes) is allocated here when not given.  Returns
+    fp32 (dln_w [H,F], dln_b [H,F], dW1, db1, dW2, db2) and (dXQ, dXV, dXK,
+    deta) in XQ.dtype."""
     B, H, NC, K, F = XQ.shape
     FF = ckpt[0].shape[-1]
     dev = check_device(XQ, XK, XV, eta, dout, *ckpt, *last, saved)
@@ -113,7 +116,8 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     dW2, db2 = torch.empty((B, H, FF, F), **f32), torch.empty((B, H, 1, F), **f32)
     dlw, dlb = torch.empty((B, H, F), **f32), torch.empty((B, H, F), **f32)
     lib = _lib.load()
-    ws = torch.empty(lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, code), device=dev, dtype=torch.uint8)
+    nws = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, code)
+    ws = torch.empty(nws, device=dev, dtype=torch.uint8) if workspace is None else workspace
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_bwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), *(ptr(t) for t in ckpt),
