@@ -1,16 +1,25 @@
 // TTT-Linear mini-batch forward on gfx950.
 //
-// One workgroup (one wavefront) owns one (batch, head) chain and keeps the
-// fast weight W [F x F] and bias b [F] resident in registers (fp32, MFMA
-// accumulator layout) across all NC sequential mini-batches.  Per mini-batch
-// of K = 16 tokens (ops/ttt_linear.py:8-54, dual form with a full KxK eta):
+// One workgroup of two wavefronts per (batch, head) chain.  Per mini-batch of
+// K = 16 tokens (ops/ttt_linear.py:8-54, dual form with a full KxK eta):
 //
 //   Z1   = XK W + b                               (token-major tiles)
 //   G    = ln_fused_l2_bwd(Z1, XV - XK)          (row reductions over F via DPP)
-//   Zb^T = W^T XQ^T - G^T (eta o A + eta)^T + b   with A^T = XK XQ^T
+//   W   -= XK^T diag(eta[K-1]) G ;  b -= G^T eta[K-1]
+//   Zb^T = W^T XQ^T - G^T (eta o A + eta)^T + b   with A^T = XK XQ^T, W and b
+//                                                  the state entering the mini-batch
 //   out  = XQ + LN(Zb)                            (feature-major tiles, written
 //                                                  4 contiguous elements per lane)
-//   W   -= XK^T diag(eta[K-1]) G ;  b -= G^T eta[K-1]
+//
+// Only the first three lines carry the recurrence.  Wave 0 (the recurrence)
+// keeps W [F x F] and b resident in registers (fp32, MFMA accumulator layout)
+// across all NC mini-batches and, per mini-batch, hands the readout what it
+// needs of the state and the inner-loss gradient through LDS: W's operand
+// frags (converted for Z1 anyway), -G as frags and b.  Wave 1 (the readout)
+// forms Zb and the output of mini-batch s while wave 0 already runs s+1; the
+// handoff is double-buffered by mini-batch parity with one barrier per
+// mini-batch, so wave 0's critical path is Z1, the LayerNorm gradient and the
+// update alone.
 //
 // Inputs for mini-batch s+1 are loaded while mini-batch s computes.  The state
 // entering mini-batch k*G is written to the checkpoint buffers
@@ -22,13 +31,20 @@
 
 namespace ttt {
 
+template <typename T, int FT> struct LinFwdHandoff {
+  typename FragT<T>::type wf[FT * FT][64];  // W operand frags Wf[o][i] (free = f_out block o, k = f_in block i)
+  typename FragT<T>::type gneg[FT][64];     // -G token-major tiles as frags
+  float b[16 * FT];                         // b entering the mini-batch
+};
+
 template <typename T, int FT>
-__global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
+__global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   const int chain = blockIdx.x;
   const int h = chain % p.H;
   const int NC = p.NC;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = lane_id(), g = l >> 4, n = l & 15;
 
   const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + (size_t)chain * NC * K * F;
@@ -44,209 +60,254 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
   const rsrc_t SV = p.saved ? make_rsrc(static_cast<char*>(p.saved) + (size_t)chain * NC * Slot::BYTES,
                                         (unsigned)(NC * Slot::BYTES))
                             : make_rsrc(p.out, 0u);
-
-  __shared__ float b_lds[F];
-
-  Tile W[FT][FT];
-#pragma unroll
-  for (int i = 0; i < FT; ++i)
-#pragma unroll
-    for (int o = 0; o < FT; ++o) W[i][o] = load_tile(p.W_init + (size_t)chain * F * F, F, 16 * i, 16 * o);
-  float b_tm[FT];
-#pragma unroll
-  for (int o = 0; o < FT; ++o) b_tm[o] = p.b_init[(size_t)chain * F + 16 * o + n];
-  for (int f = l; f < F; f += 64) b_lds[f] = p.b_init[(size_t)chain * F + f];
-
-  float lnw_tm[FT], lnb_tm[FT];
-  f4 lnw_fm[FT], lnb_fm[FT];
-#pragma unroll
-  for (int o = 0; o < FT; ++o) {
-    lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
-    lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lnw_fm[o][j] = p.ln_w[h * F + 16 * o + 4 * g + j];
-      lnb_fm[o][j] = p.ln_b[h * F + 16 * o + 4 * g + j];
-    }
-  }
+  __shared__ LinFwdHandoff<T, FT> hand[2];
   const float eps = p.eps;
   const float invF = 1.0f / F;
   const Frag<T> I = identity_frag<T>();
 
-  // prefetched inputs of the next mini-batch
-  Frag<T> nq[1][FT], nk[1][FT], nv[1][FT];
-  Frag<T> n_etaT, n_e;  // raw: converted where used, so the prefetch is not waited for
-  auto load_step = [&](int s) {
-    const T* q = XQ + (size_t)s * K * F;
-    const T* k = XK + (size_t)s * K * F;
-    const T* v = XV + (size_t)s * K * F;
-#pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      nq[0][c] = load_frag(q, F, 16 * c);
-      nk[0][c] = load_frag(k, F, 16 * c);
-      nv[0][c] = load_frag(v, F, 16 * c);
-    }
-    const T* e = ETA + (size_t)s * K * K;
-    n_etaT = load_frag(e, K, 0);            // lane (g,n): eta[n][4g+j]
-    n_e = load_frag(e + (K - 1) * K, 0, 0);  // lane (g,*): eta[K-1][4g+j]
-  };
-  load_step(0);
-  // Retire the first loads before the loop: with them pending on entry the
-  // wait-count pass cannot order them against the loop's own loads and stores
-  // and waits for every outstanding access in each iteration.
-  __builtin_amdgcn_s_waitcnt(0);
-
-  for (int s = 0; s < NC; ++s) {
-    if (p.W_ckpt != nullptr && (s % p.G) == 0) {
-      const int kk = s / p.G;
-      float* wc = p.W_ckpt + ((size_t)chain * p.NK + kk) * F * F;
-#pragma unroll
-      for (int i = 0; i < FT; ++i)
-#pragma unroll
-        for (int o = 0; o < FT; ++o) store_tile(wc, F, 16 * i, 16 * o, W[i][o]);
-      if (g == 0) {
-#pragma unroll
-        for (int o = 0; o < FT; ++o) p.b_ckpt[((size_t)chain * p.NK + kk) * F + 16 * o + n] = b_tm[o];
-      }
-    }
-
-    Frag<T> xq[1][FT], xk[1][FT], xv[1][FT];
-#pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      xq[0][c] = nq[0][c];
-      xk[0][c] = nk[0][c];
-      xv[0][c] = nv[0][c];
-    }
-    const Frag<T> etaT_raw = n_etaT, e_raw = n_e;
-    if (s + 1 < NC) load_step(s + 1);
-
-    // W as operand frags: Wf[o][i] (free = f_out block o, contraction = f_in block i)
-    Frag<T> Wf[FT][FT];
+  if (wave == 0) {
+    // ================================================================ recurrence
+    Tile W[FT][FT];
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) Wf[o][i] = to_frag<T>(W[i][o].v);
-
-    // Z1 = XK W + b (token-major)
-    Tile z1[1][FT];
+      for (int o = 0; o < FT; ++o) W[i][o] = load_tile(p.W_init + (size_t)chain * F * F, F, 16 * i, 16 * o);
+    float b_tm[FT], lnw_tm[FT], lnb_tm[FT];
 #pragma unroll
-    for (int o = 0; o < FT; ++o) z1[0][o].v = f4{b_tm[o], b_tm[o], b_tm[o], b_tm[o]};
-    gemm<1, FT, FT>(z1, xk, Wf);
-
-    // Zb^T = W^T XQ^T (feature-major), dual and bias terms added below
-    Tile zb[FT][1];
-#pragma unroll
-    for (int o = 0; o < FT; ++o) zb[o][0].v = f4{0.f, 0.f, 0.f, 0.f};
-    gemm<FT, 1, FT>(zb, Wf, xq);
-
-    // A^T = XK XQ^T : C layout [t_k x t_q]
-    Tile at[1][1];
-    at[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
-    gemm<1, 1, FT>(at, xk, xq);
-
-    // token-major XK and XV (exact transposes)
-    Tile xkT[FT], xvT[FT];
-#pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      xkT[c] = transpose16(xk[0][c], I);
-      xvT[c] = transpose16(xv[0][c], I);
+    for (int o = 0; o < FT; ++o) {
+      b_tm[o] = p.b_init[(size_t)chain * F + 16 * o + n];
+      lnw_tm[o] = p.ln_w[h * F + 16 * o + n];
+      lnb_tm[o] = p.ln_b[h * F + 16 * o + n];
     }
 
-    // ---- ln_fused_l2_bwd on Z1 rows (row t = 4g + j spans 16 lanes x FT tiles)
-    f4 mu, rstd;
+    // prefetched inputs of the next mini-batch (raw: converted where used, so
+    // the prefetch is not waited for early)
+    Frag<T> nk[1][FT], nv[1][FT], n_e;
+    auto load_step = [&](int s) {
+      const T* k = XK + (size_t)s * K * F;
+      const T* v = XV + (size_t)s * K * F;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float sacc = 0.f;
+      for (int c = 0; c < FT; ++c) {
+        nk[0][c] = load_frag(k, F, 16 * c);
+        nv[0][c] = load_frag(v, F, 16 * c);
+      }
+      n_e = load_frag(ETA + (size_t)s * K * K + (K - 1) * K, 0, 0);  // lane (g,*): eta[K-1][4g+j]
+    };
+    load_step(0);
+    // Retire the first loads before the loop: with them pending on entry the
+    // wait-count pass cannot order them against the loop's own loads and stores
+    // and waits for every outstanding access in each iteration.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    for (int s = 0; s < NC; ++s) {
+      if (p.W_ckpt != nullptr && (s % p.G) == 0) {
+        const int kk = s / p.G;
+        float* wc = p.W_ckpt + ((size_t)chain * p.NK + kk) * F * F;
 #pragma unroll
-      for (int o = 0; o < FT; ++o) sacc += z1[0][o].v[j];
-      mu[j] = sum_row16(sacc) * invF;
-    }
+        for (int i = 0; i < FT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float sacc = 0.f;
+          for (int o = 0; o < FT; ++o) store_tile(wc, F, 16 * i, 16 * o, W[i][o]);
+        if (g == 0) {
+#pragma unroll
+          for (int o = 0; o < FT; ++o) p.b_ckpt[((size_t)chain * p.NK + kk) * F + 16 * o + n] = b_tm[o];
+        }
+      }
+      Frag<T> xk[1][FT], xv[1][FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        xk[0][c] = nk[0][c];
+        xv[0][c] = nv[0][c];
+      }
+      const Frag<T> e_raw = n_e;
+      if (s + 1 < NC) load_step(s + 1);
+      LinFwdHandoff<T, FT>& hs = hand[s & 1];
+
+      // W as operand frags, handed to the readout with b
+      Frag<T> Wf[FT][FT];
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          Wf[o][i] = to_frag<T>(W[i][o].v);
+          hs.wf[o * FT + i][l] = Wf[o][i].v;
+        }
+      if (g == 0) {
+#pragma unroll
+        for (int o = 0; o < FT; ++o) hs.b[16 * o + n] = b_tm[o];
+      }
+
+      // Z1 = XK W + b (token-major)
+      Tile z1[1][FT];
+#pragma unroll
+      for (int o = 0; o < FT; ++o) z1[0][o].v = f4{b_tm[o], b_tm[o], b_tm[o], b_tm[o]};
+      gemm<1, FT, FT>(z1, xk, Wf);
+
+      // token-major XK and XV (exact transposes)
+      Tile xkT[FT], xvT[FT];
+#pragma unroll
+      for (int c = 0; c < FT; ++c) {
+        xkT[c] = transpose16(xk[0][c], I);
+        xvT[c] = transpose16(xv[0][c], I);
+      }
+
+      // ---- ln_fused_l2_bwd on Z1 rows (row t = 4g + j spans 16 lanes x FT tiles)
+      f4 mu, rstd;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int o = 0; o < FT; ++o) sacc += z1[0][o].v[j];
+        mu[j] = sum_row16(sacc) * invF;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          const float d = z1[0][o].v[j] - mu[j];
+          sacc += d * d;
+        }
+        rstd[j] = rsqrt_f(sum_row16(sacc) * invF + eps);
+      }
+      f4 xh[FT], gx[FT];
+      f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int o = 0; o < FT; ++o)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xh[o][j] = (z1[0][o].v[j] - mu[j]) * rstd[j];
+          const float tgt = xvT[o].v[j] - xkT[o].v[j];
+          gx[o][j] = (lnw_tm[o] * xh[o][j] + lnb_tm[o] - tgt) * lnw_tm[o];
+          s1[j] += gx[o][j];
+          s2[j] += gx[o][j] * xh[o][j];
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s1[j] = sum_row16(s1[j]) * invF;
+        s2[j] = sum_row16(s2[j]) * invF;
+      }
+      Tile G[FT];
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
-        const float d = z1[0][o].v[j] - mu[j];
-        sacc += d * d;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) G[o].v[j] = (gx[o][j] - s1[j] - xh[o][j] * s2[j]) * rstd[j];
+        hs.gneg[o][l] = to_frag<T>(-G[o].v).v;
       }
-      rstd[j] = rsqrt_f(sum_row16(sacc) * invF + eps);
+      const int sv = s * Slot::BYTES;
+#pragma unroll
+      for (int o = 0; o < FT; ++o) {
+        bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::G, Frag<float>{G[o].v});
+        bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XH, Frag<float>{xh[o]});
+      }
+      // per-row values: the 16 lanes of a group store the same 4 rows
+      bstore_frag<float>(SV, 16 * g, sv + Slot::RSTD, Frag<float>{rstd});
+      bstore_frag<float>(SV, 16 * g, sv + Slot::CC, Frag<float>{s2});
+
+      // ---- state update: W -= XK^T diag(e) G ; b -= G^T e
+      {
+        const f4 e = frag_to_f4(e_raw);
+        Frag<T> xkf[FT], ge[FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          xkf[c] = to_frag<T>(xkT[c].v);
+          f4 v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = -e[j] * G[c].v[j];
+          ge[c] = to_frag<T>(v);
+        }
+#pragma unroll
+        for (int i = 0; i < FT; ++i)
+#pragma unroll
+          for (int o = 0; o < FT; ++o) mma16(W[i][o].v, xkf[i], ge[o]);
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc += e[j] * G[o].v[j];
+          b_tm[o] -= sum_col4(acc);
+        }
+      }
+      __syncthreads();  // mini-batch s handed over
     }
-    f4 xh[FT], gx[FT];
-    f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
+
+    if (p.W_last != nullptr) {
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int o = 0; o < FT; ++o) store_tile(p.W_last + (size_t)chain * F * F, F, 16 * i, 16 * o, W[i][o]);
+      if (g == 0) {
+#pragma unroll
+        for (int o = 0; o < FT; ++o) p.b_last[(size_t)chain * F + 16 * o + n] = b_tm[o];
+      }
+    }
+  } else {
+    // ================================================================ readout
+    f4 lnw_fm[FT], lnb_fm[FT];
 #pragma unroll
     for (int o = 0; o < FT; ++o)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        xh[o][j] = (z1[0][o].v[j] - mu[j]) * rstd[j];
-        const float tgt = xvT[o].v[j] - xkT[o].v[j];
-        gx[o][j] = (lnw_tm[o] * xh[o][j] + lnb_tm[o] - tgt) * lnw_tm[o];
-        s1[j] += gx[o][j];
-        s2[j] += gx[o][j] * xh[o][j];
+        lnw_fm[o][j] = p.ln_w[h * F + 16 * o + 4 * g + j];
+        lnb_fm[o][j] = p.ln_b[h * F + 16 * o + 4 * g + j];
       }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s1[j] = sum_row16(s1[j]) * invF;
-      s2[j] = sum_row16(s2[j]) * invF;
-    }
-    Tile G[FT];
-#pragma unroll
-    for (int o = 0; o < FT; ++o)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) G[o].v[j] = (gx[o][j] - s1[j] - xh[o][j] * s2[j]) * rstd[j];
-    const int sv = s * Slot::BYTES;
-#pragma unroll
-    for (int o = 0; o < FT; ++o) {
-      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::G, Frag<float>{G[o].v});
-      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XH, Frag<float>{xh[o]});
-    }
-    // per-row values: the 16 lanes of a group store the same 4 rows
-    bstore_frag<float>(SV, 16 * g, sv + Slot::RSTD, Frag<float>{rstd});
-    bstore_frag<float>(SV, 16 * g, sv + Slot::CC, Frag<float>{s2});
-
-    // ---- readout: Zb^T -= G^T (eta o A + eta)^T ; + b
-    {
-      f4 mt;
-      const f4 etaT = frag_to_f4(etaT_raw);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mt[j] = etaT[j] * at[0][0].v[j] + etaT[j];
-      const Frag<T> mtf = to_frag<T>(mt);
-#pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        const Frag<T> gneg = to_frag<T>(-G[o].v);
-        mma16(zb[o][0].v, gneg, mtf);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) zb[o][0].v[j] += b_lds[16 * o + 4 * g + j];
-      }
-    }
-
-    // ---- state update: W -= XK^T diag(e) G ; b -= G^T e
-    {
-      const f4 e = frag_to_f4(e_raw);
-      Frag<T> xkf[FT], ge[FT];
+    Frag<T> nq[1][FT], nk[1][FT], n_etaT;
+    auto load_step = [&](int s) {
+      const T* q = XQ + (size_t)s * K * F;
+      const T* k = XK + (size_t)s * K * F;
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        xkf[c] = to_frag<T>(xkT[c].v);
-        f4 v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = -e[j] * G[c].v[j];
-        ge[c] = to_frag<T>(v);
+        nq[0][c] = load_frag(q, F, 16 * c);
+        nk[0][c] = load_frag(k, F, 16 * c);
       }
+      n_etaT = load_frag(ETA + (size_t)s * K * K, K, 0);  // lane (g,n): eta[n][4g+j]
+    };
+    load_step(0);
+    __builtin_amdgcn_s_waitcnt(0);
+
+    for (int s = 0; s < NC; ++s) {
+      Frag<T> xq[1][FT], xk[1][FT];
 #pragma unroll
-      for (int i = 0; i < FT; ++i)
+      for (int c = 0; c < FT; ++c) {
+        xq[0][c] = nq[0][c];
+        xk[0][c] = nk[0][c];
+      }
+      const Frag<T> etaT_raw = n_etaT;
+      if (s + 1 < NC) load_step(s + 1);
+      __syncthreads();  // mini-batch s handed over
+      const LinFwdHandoff<T, FT>& hs = hand[s & 1];
+
+      // Zb^T = W^T XQ^T (feature-major) - G^T (eta o A + eta)^T + b
+      Frag<T> Wf[FT][FT];
 #pragma unroll
-        for (int o = 0; o < FT; ++o) mma16(W[i][o].v, xkf[i], ge[o]);
+      for (int o = 0; o < FT; ++o)
+#pragma unroll
+        for (int i = 0; i < FT; ++i) Wf[o][i].v = hs.wf[o * FT + i][l];
+      Tile zb[FT][1];
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc += e[j] * G[o].v[j];
-        b_tm[o] -= sum_col4(acc);
-        if (g == 0) b_lds[16 * o + n] = b_tm[o];
+        const f4 bo = *reinterpret_cast<const f4*>(&hs.b[16 * o + 4 * g]);
+        zb[o][0].v = bo;
       }
-    }
+      gemm<FT, 1, FT>(zb, Wf, xq);
+      Tile at[1][1];  // A^T = XK XQ^T : C layout [t_k x t_q]
+      at[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
+      gemm<1, 1, FT>(at, xk, xq);
+      {
+        f4 mt;
+        const f4 etaT = frag_to_f4(etaT_raw);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mt[j] = etaT[j] * at[0][0].v[j] + etaT[j];
+        const Frag<T> mtf = to_frag<T>(mt);
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          Frag<T> gneg;
+          gneg.v = hs.gneg[o][l];
+          mma16(zb[o][0].v, gneg, mtf);
+        }
+      }
 
-    // ---- LN over features of each token (token n lives in lanes n, n+16, n+32, n+48)
-    {
+      // ---- LN over features of each token (token n lives in lanes n, n+16, n+32, n+48)
+      const int sv = s * Slot::BYTES;
       float sacc = 0.f;
 #pragma unroll
       for (int o = 0; o < FT; ++o)
@@ -278,22 +339,11 @@ __global__ __launch_bounds__(64) void linear_fwd_kernel(LinearFwdParams p) {
       bstore_f32(SV, 4 * n, sv + Slot::RSB, rs);  // per token: the 4 lanes of token n agree
     }
   }
-
-  if (p.W_last != nullptr) {
-#pragma unroll
-    for (int i = 0; i < FT; ++i)
-#pragma unroll
-      for (int o = 0; o < FT; ++o) store_tile(p.W_last + (size_t)chain * F * F, F, 16 * i, 16 * o, W[i][o]);
-    if (g == 0) {
-#pragma unroll
-      for (int o = 0; o < FT; ++o) p.b_last[(size_t)chain * F + 16 * o + n] = b_tm[o];
-    }
-  }
 }
 
 template <typename T, int FT>
 static hipError_t launch_fwd(const LinearFwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_fwd_kernel<T, FT>), dim3(p.B * p.H), dim3(64), 0, stream, p);
+  hipLaunchKernelGGL((linear_fwd_kernel<T, FT>), dim3(p.B * p.H), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -222,10 +222,18 @@ __device__ __forceinline__ float sum_wave(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 // sum over the 4 lanes that share n (lanes n, n+16, n+32, n+48)
+// with gfx950's lane swaps (VALU, no trip through the LDS crossbar):
+// v_permlane32_swap exchanges the upper half of its first operand with the
+// lower half of its second, so with both operands x the two results hold x and
+// x^32 in every lane (in either order) and their sum is x + x^32;
+// v_permlane16_swap does the same for odd and even 16-lane rows.
 __device__ __forceinline__ float sum_col4(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float y = __builtin_bit_cast(float, (unsigned)h[0]) + __builtin_bit_cast(float, (unsigned)h[1]);
+  const unsigned v = __builtin_bit_cast(unsigned, y);
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
 // ---------------------------------------------------------------- loads / stores
