@@ -85,17 +85,18 @@ def lin_fwd_flops():
     return (6 * F * F + 6 * K * F) * B * H * T
 
 
-def fwd_bytes(state, G, sx=2, seta=2):
-    """inputs XQ, XK, XV, eta read + out written + state read/written + checkpoints written"""
+def fwd_bytes(state, G, ckpt, sx=2, seta=2):
+    """inputs XQ, XK, XV, eta read + out written + state read/written + checkpoints
+    written (`ckpt` floats each: what the backward reads of the state)"""
     return (B * H * T * (3 * F * sx + K * seta + F * sx) + B * H * state * 4 * 2
-            + B * H * math.ceil(NC / G) * state * 4)
+            + B * H * math.ceil(NC / G) * ckpt * 4)
 
 
-def bwd_bytes(state, G, sx=2, seta=2):
+def bwd_bytes(state, G, ckpt, sx=2, seta=2):
     """XQ, XK, XV, dout, eta read + dXQ, dXK, dXV, deta written + checkpoints read
     + state gradients written (and the per-chain LN partials)"""
     return (B * H * T * (4 * F * sx + K * seta) + B * H * T * (3 * F * sx + K * seta)
-            + B * H * math.ceil(NC / G) * state * 4 + B * H * (state + 2 * F) * 4 * 2)
+            + B * H * math.ceil(NC / G) * ckpt * 4 + B * H * (state + 2 * F) * 4 * 2)
 
 
 def readout_flops():
@@ -189,7 +190,7 @@ def run_mlp(torch, O, steps, warmup, only=None):
 
     def fwd():
         out, ck, _, last, saved = mlp_forward(*(g[k] for k in keys), G_MLP, want_ckpt=True, want_last=True,
-                                              want_saved=True)
+                                              want_saved=True, ckpt_w1_only=True)
         return out, (ck, last, saved)
 
     def bwd(saved):
@@ -385,14 +386,14 @@ def main():
 
     state = mlp_state_floats()
     kernels = {
-        "ttt_mlp_fwd": roofline("ttt_mlp_fwd", kern["ttt_mlp_fwd"], mlp_fwd_flops(), fwd_bytes(state, G_MLP),
+        "ttt_mlp_fwd": roofline("ttt_mlp_fwd", kern["ttt_mlp_fwd"], mlp_fwd_flops(), fwd_bytes(state, G_MLP, F * FF),
                                 MFMA_PEAK_BF16),
         "ttt_mlp_bwd": roofline("ttt_mlp_bwd", kern["ttt_mlp_bwd"], 2 * mlp_fwd_flops(),
-                                bwd_bytes(state, G_MLP), MFMA_PEAK_BF16),
+                                bwd_bytes(state, G_MLP, F * FF), MFMA_PEAK_BF16),
         "ttt_linear_fwd": roofline("ttt_linear_fwd", lk["ttt_linear_fwd"], lin_fwd_flops(),
-                                   fwd_bytes(lin_state_floats(), G_LIN), MFMA_PEAK_BF16),
+                                   fwd_bytes(lin_state_floats(), G_LIN, lin_state_floats()), MFMA_PEAK_BF16),
         "ttt_linear_bwd": roofline("ttt_linear_bwd", lk["ttt_linear_bwd"], 2 * lin_fwd_flops(),
-                                   bwd_bytes(lin_state_floats(), G_LIN), MFMA_PEAK_BF16),
+                                   bwd_bytes(lin_state_floats(), G_LIN, lin_state_floats()), MFMA_PEAK_BF16),
         "ttt_mlp_cached_readout": roofline("ttt_mlp_cached_readout", ro, readout_flops(), readout_bytes(),
                                            MFMA_PEAK_BF16),
     }

@@ -103,7 +103,9 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
  *   W1_init [B,H,F,FF], b1_init [B,H,1,FF], W2_init [B,H,FF,F], b2_init [B,H,1,F] fp32
  *   out               [B,H,NC,K,F] dtype
  *   *_last            final state, shapes of *_init (all four or none)
- *   *_ckpt            [B,H,NK,...] state entering mini-batch k*G (all four or none)
+ *   *_ckpt            [B,H,NK,...] state entering mini-batch k*G: W1_ckpt, or
+ *                     none; b1_ckpt, W2_ckpt and b2_ckpt are each optional (the
+ *                     backward reads W1's only)
  *   *_memo            [B,H,NS,...], NS = ceil(NC/M): state after mini-batch
  *                     s*M has been applied (all four or none; M >= 1 then)
  *   saved             NULL, or >= ttt_mlp_saved_bytes(...) bytes: receives, for
@@ -127,14 +129,16 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* Bytes of device workspace ttt_mlp_bwd needs: B*H*NC mini-batches x
- * (2 * FF * K * sizeof(dtype) + 2 * F * 64). */
+ * (2 * FF * K * sizeof(dtype) + 2 * F * 64), then (4 + B*H*NC) 4-byte control
+ * words rounded up to 256 bytes. */
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
  * state's gradient zero, as in the ops path).  Replaces ttt_mlp_scan_backward
  * (kernels/mlp_backward.py:247-651) as launched by TritonMLP._backward_core
  * (mlp_triton.py:200-351).
- *   *_ckpt           checkpoints written by ttt_mlp_fwd with the same G
+ *   W1_ckpt          weight checkpoints written by ttt_mlp_fwd with the same G
+ *                    (b1_ckpt, W2_ckpt, b2_ckpt are not read and may be NULL)
  *   *_last           the final state written by that ttt_mlp_fwd call
  *   dout             [B,H,NC,K,F] dtype
  *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
@@ -144,7 +148,8 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
  *                    (saved_bytes >= ttt_mlp_saved_bytes(...))
  *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes of scratch
  *                    (dZ1b, dZ1 and partial dXQ/dXK per mini-batch, handed
- *                    from the reverse sweep to the launch that forms dXQ/dXK) */
+ *                    from the reverse sweep to the pass that forms dXQ/dXK,
+ *                    and that pass's control words) */
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
                 const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,

@@ -106,9 +106,9 @@ def test_linear_saved_buffer(lib):
     assert lib.ttt_linear_bwd(*bad, P, need, None) == E_NULL
 
 
-def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, saved=None, saved_bytes=0, NC=16, **kw):
-    a = ([P] * 10 + [2, 4, NC, 16, 64, FF, 4, M, kw.get("dtype", BF16), 1e-8, P] + [None] * 8 + list(memo)
-         + [saved, saved_bytes, None])
+def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, saved=None, saved_bytes=0, NC=16, ckpt=(None,) * 4, **kw):
+    a = ([P] * 10 + [2, 4, NC, 16, 64, FF, 4, M, kw.get("dtype", BF16), 1e-8, P] + [None] * 4 + list(ckpt)
+         + list(memo) + [saved, saved_bytes, None])
     return lib.ttt_mlp_fwd(*a)
 
 
@@ -120,6 +120,10 @@ def test_mlp_fwd_validation(lib):
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=0) == E_ARG
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=17) == E_ARG
     assert _mlp_fwd(lib, memo=(P, P, Q, P), M=2) == E_ALIGN
+    # checkpoints: W1's, optionally with any of the other three
+    assert _mlp_fwd(lib, ckpt=(None, P, None, None)) == E_NULL
+    assert _mlp_fwd(lib, ckpt=(None, None, P, P)) == E_NULL
+    assert _mlp_fwd(lib, ckpt=(Q, None, None, None)) == E_ALIGN
     need = lib.ttt_mlp_saved_bytes(2, 4, 16, 16, 64, 256, BF16)
     assert _mlp_fwd(lib, saved=P, saved_bytes=need - 1) == E_WS
     assert _mlp_fwd(lib, saved=Q, saved_bytes=need) == E_ALIGN

@@ -205,15 +205,16 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   REQUIRE_PTR(W2_init);
   REQUIRE_PTR(b2_init);
   REQUIRE_PTR(out);
-  const float* groups[3][4] = {{W1_last, b1_last, W2_last, b2_last},
-                               {W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt},
-                               {W1_memo, b1_memo, W2_memo, b2_memo}};
+  const float* groups[2][4] = {{W1_last, b1_last, W2_last, b2_last}, {W1_memo, b1_memo, W2_memo, b2_memo}};
   for (auto& grp : groups) {
     const bool any = grp[0] || grp[1] || grp[2] || grp[3];
     const bool all = grp[0] && grp[1] && grp[2] && grp[3];
     if (any && !all) return TTT_ERR_NULL;
     for (const float* q : grp) OPTIONAL_PTR(q);
   }
+  // checkpoints: W1's, and any of the other three beside it
+  if (W1_ckpt == nullptr && (b1_ckpt || W2_ckpt || b2_ckpt)) return TTT_ERR_NULL;
+  for (const float* q : {W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt}) OPTIONAL_PTR(q);
   if (W1_memo != nullptr && (M < 1 || M > NC)) return TTT_ERR_ARG;
   if (saved != nullptr) {
     if (!aligned16(saved)) return TTT_ERR_ALIGN;
@@ -281,7 +282,10 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
   if (st != TTT_OK) return st;
-  const void* req[] = {XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt,
+  (void)b1_ckpt;  // not read: the saved values carry the rest of the state
+  (void)W2_ckpt;
+  (void)b2_ckpt;
+  const void* req[] = {XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt,
                        W1_last, b1_last, W2_last, b2_last, dout,
                        dXQ, dXK, dXV, deta, dW1, db1, dW2, db2, dln_w, dln_b};
   for (const void* q : req) REQUIRE_PTR(q);

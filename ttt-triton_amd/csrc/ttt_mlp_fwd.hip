@@ -122,23 +122,27 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const float eps = p.eps;
   const Frag<T> I = identity_frag<T>();
 
+  // writes the state to its non-null destinations
   auto store_state = [&](float* w1d, float* b1d, float* w2d, float* b2d) {
-    const rsrc_t r1 = make_rsrc(w1d, F * FF * 4), r2 = make_rsrc(w2d, FF * F * 4);
+    const rsrc_t r1 = make_rsrc(w1d, F * FF * 4);
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
       for (int o = 0; o < HT; ++o) bstore_tile(r1, w1l, 0, FF, 16 * i, 16 * o, W1[i][o]);
+    if (w2d != nullptr) {
+      const rsrc_t r2 = make_rsrc(w2d, FF * F * 4);
 #pragma unroll
-    for (int i = 0; i < HT; ++i)
+      for (int i = 0; i < HT; ++i)
 #pragma unroll
-      for (int o = 0; o < FT; ++o) bstore_tile(r2, w2l, 0, F, 16 * i, 16 * o, W2[i][o]);
-    if (g == 0) {
+        for (int o = 0; o < FT; ++o) bstore_tile(r2, w2l, 0, F, 16 * i, 16 * o, W2[i][o]);
+    }
+    if (g == 0 && b1d != nullptr) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) b1d[hs + 16 * o + n] = b1_tm[o];
-      if (wave == 0) {
+    }
+    if (g == 0 && wave == 0 && b2d != nullptr) {
 #pragma unroll
-        for (int o = 0; o < FT; ++o) b2d[16 * o + n] = b2_tm[o];
-      }
+      for (int o = 0; o < FT; ++o) b2d[16 * o + n] = b2_tm[o];
     }
   };
 
@@ -156,7 +160,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   for (int s = 0; s < NC; ++s) {
     if (p.W1_ckpt != nullptr && (s % p.G) == 0) {
       const size_t k = (size_t)chain * p.NK + s / p.G;
-      store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt + k * FF, p.W2_ckpt + k * FF * F, p.b2_ckpt + k * F);
+      store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt ? p.b1_ckpt + k * FF : nullptr,
+                  p.W2_ckpt ? p.W2_ckpt + k * FF * F : nullptr, p.b2_ckpt ? p.b2_ckpt + k * F : nullptr);
     }
     const int xo = s * K * F * ST, eo = s * K * K * ST;
     const int us = s * Slot::BYTES;

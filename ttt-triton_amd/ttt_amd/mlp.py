@@ -49,13 +49,15 @@ def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
 
 
 def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0, eps: float = LN_EPS,
-                want_ckpt: bool = True, want_last: bool = False, want_saved: bool = False):
+                want_ckpt: bool = True, want_last: bool = False, want_saved: bool = False,
+                ckpt_w1_only: bool = False):
     """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
     ckpt (W1,b1,W2,b2) or None, memo (W1,b1,W2,b2) or None, last or None,
     saved or None).  ckpt, last and saved are what mlp_backward needs: the
     checkpoints every G mini-batches, the final state, and each mini-batch's
     state-update operands and activations (a flat uint8 buffer of
-    ttt_mlp_saved_bytes)."""
+    ttt_mlp_saved_bytes).  The backward reads only W1's checkpoints: with
+    ckpt_w1_only the other three are neither allocated nor written (None)."""
     B, H, NC, K, F, FF = _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta)
     dev = check_device(XQ, XK, XV, eta, W1, b1, W2, b2, ln_w, ln_b)
     mp = XQ.dtype
@@ -74,6 +76,8 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
                 torch.empty(lead + (1, F), device=dev, dtype=torch.float32))
 
     ck = state(NK) if want_ckpt else None
+    if ck is not None and ckpt_w1_only:
+        ck = (ck[0], None, None, None)
     memo = state(math.ceil(NC / M)) if M and M > 0 else None
     last = state(None) if want_last else None
     none4 = (None, None, None, None)
@@ -86,7 +90,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb1), ptr(w2), ptr(bb2),
             B, H, NC, K, F, FF, G, int(M) if M else 0, code, float(eps), ptr(out),
             *(tuple(ptr(t) for t in last) if last else none4),
-            *(tuple(ptr(t) for t in ck) if ck else none4),
+            *(tuple(ptr(t) if t is not None else None for t in ck) if ck else none4),
             *(tuple(ptr(t) for t in memo) if memo else none4),
             ptr(saved) if saved is not None else None, saved.numel() if saved is not None else 0,
             stream_of(dev))
@@ -104,7 +108,7 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     deta) in XQ.dtype."""
     B, H, NC, K, F = XQ.shape
     FF = ckpt[0].shape[-1]
-    dev = check_device(XQ, XK, XV, eta, dout, *ckpt, *last, saved)
+    dev = check_device(XQ, XK, XV, eta, dout, *(t for t in ckpt if t is not None), *last, saved)
     mp = XQ.dtype
     code = dtype_code(mp)
     xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
@@ -120,7 +124,8 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     ws = torch.empty(nws, device=dev, dtype=torch.uint8) if workspace is None else workspace
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_bwd(
-            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), *(ptr(t) for t in ckpt),
+            ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb),
+            *(ptr(t) if t is not None else None for t in ckpt),
             *(ptr(t) for t in last), ptr(do),
             B, H, NC, K, F, FF, int(G), code, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
@@ -143,7 +148,8 @@ class TTTMLPFunction(torch.autograd.Function):
         M = int(memo_segment_size)
         out, ck, memo, last, saved = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
                                                XQ_batch, XV_batch, XK_batch, eta_batch, G, M=M, eps=eps,
-                                               want_ckpt=True, want_last=True, want_saved=True)
+                                               want_ckpt=True, want_last=True, want_saved=True,
+                                               ckpt_w1_only=True)
         ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck, *last,
                               saved)
         ctx.G, ctx.eps = G, eps
