@@ -122,13 +122,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const float eps = p.eps;
   const Frag<T> I = identity_frag<T>();
 
-  // writes the state to its non-null destinations
+  // writes the state to its non-null destinations; W1's tiles are first
+  // transposed exactly (fp32 MFMA against the identity) into row order, so
+  // each lane stores 4 consecutive floats of one row with one 16-byte store
   auto store_state = [&](float* w1d, float* b1d, float* w2d, float* b2d) {
     const rsrc_t r1 = make_rsrc(w1d, F * FF * 4);
+    const Frag<float> I32 = identity_frag<float>();
+    const int w1r = (n * FF + hs + 4 * g) * 4;  // row n, columns hs + 4g .. +3 of a tile
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
-      for (int o = 0; o < HT; ++o) bstore_tile(r1, w1l, 0, FF, 16 * i, 16 * o, W1[i][o]);
+      for (int o = 0; o < HT; ++o)
+        bstore_frag<float>(r1, w1r, (16 * i * FF + 16 * o) * 4, Frag<float>{transpose16(Frag<float>{W1[i][o].v}, I32).v});
     if (w2d != nullptr) {
       const rsrc_t r2 = make_rsrc(w2d, FF * F * 4);
 #pragma unroll
