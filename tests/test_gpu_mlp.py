@@ -220,3 +220,20 @@ def test_mlp_bwd_fused_workers_finish_every_group(F_, FF):
     torch.cuda.synchronize()
     for a, b in zip(first[0] + first[1], second[0] + second[1]):
         assert torch.equal(a, b)
+
+
+def test_mlp_bwd_more_chains_than_cus():
+    """More chains than the device has CUs to spare: the dXQ/dXK pass of the
+    4-wave shape falls back to its own launch after the sweeps."""
+    B, H, NC, G = 66, 4, 3, 2  # 264 chains
+    _say(f"mlp bwd bf16 B{B} H{H} NC{NC} (two launches)")
+    d = O.make_inputs(B, H, NC, 16, 64, FF=256, seed=51, dtype=torch.bfloat16, with_grad=True)
+    mine = _bwd(d, G=G)
+    ref = oracle_mlp_grads(d, d["dOut"], G=0)
+    bad = []
+    for k in mine:
+        err = rel_l2(mine[k], ref[k])
+        _say(f"  {k}: rel-L2 {err:.3e}")
+        if err > BF16_RTOL:
+            bad.append(k)
+    assert not bad
