@@ -119,6 +119,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   }
   const float lnw_l = kLnRowSplit<FT, NW> ? p.ln_w[h * F + l] : 0.f;  // feature l (row-split LayerNorm)
   const float lnb_l = kLnRowSplit<FT, NW> ? p.ln_b[h * F + l] : 0.f;
+  // feature 16 wave + n: the readout's output tile of this wave when NW == FT
+  const float lnw_own = NW == FT ? p.ln_w[h * F + 16 * wave + n] : 0.f;
+  const float lnb_own = NW == FT ? p.ln_b[h * F + 16 * wave + n] : 0.f;
   const float eps = p.eps;
   const Frag<T> I = identity_frag<T>();
 
@@ -451,19 +454,44 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
       bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSB, Frag<float>{rs});
-      // every wave forms every tile; tile o is written by wave o % NW
+      if constexpr (NW == FT) {
+        // one tile per wave: tile o = wave, picked out of the register arrays
+        // by uniform selects
+        const int o = wave;
+        f4 zo = z2b[0].v;
+        Frag<T> xqo = xq[0][0];
 #pragma unroll
-      for (int o = 0; o < FT; ++o) {
-        const bool mine = o % NW == wave;
-        const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
+        for (int c = 1; c < FT; ++c) {
+          if (o == c) {
+            zo = z2b[c].v;
+            xqo = xq[0][c];
+          }
+        }
+        const f4 q = transpose16(xqo, I).v;  // XQ token-major
         f4 xhb, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          xhb[j] = (z2b[o].v[j] - mu[j]) * rs[j];
-          y[j] = q[j] + lnw_tm[o] * xhb[j] + lnb_tm[o];
+          xhb[j] = (zo[j] - mu[j]) * rs[j];
+          y[j] = q[j] + lnw_own * xhb[j] + lnb_own;
         }
-        bstore_frag<float>(rSV, keep_or_drop(f4l + o * 1024, mine), us + Slot::XHB, Frag<float>{xhb});
-        bstore_frag<T>(rOUT, keep_or_drop(xl + 16 * o * ST, mine), xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
+        bstore_frag<float>(rSV, f4l + o * 1024, us + Slot::XHB, Frag<float>{xhb});
+        bstore_frag<T>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
+      } else {
+        // every wave forms every tile; tile o is written by wave o % NW
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          const bool mine = o % NW == wave;
+          const f4 q = transpose16(xq[0][o], I).v;  // XQ token-major
+          f4 xhb, y;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            xhb[j] = (z2b[o].v[j] - mu[j]) * rs[j];
+            y[j] = q[j] + lnw_tm[o] * xhb[j] + lnb_tm[o];
+          }
+          bstore_frag<float>(rSV, keep_or_drop(f4l + o * 1024, mine), us + Slot::XHB, Frag<float>{xhb});
+          bstore_frag<T>(rOUT, keep_or_drop(xl + 16 * o * ST, mine), xo,
+                         to_frag<T>(transpose16(to_frag<T>(y), I).v));
+        }
       }
     }
 
