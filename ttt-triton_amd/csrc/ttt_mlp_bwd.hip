@@ -665,6 +665,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           }
         }
       }
+      // The checkpoint group that the previous mini-batch closed: this wave's
+      // handoff stores for it (device-coherent, written through) have long been
+      // issued, so waiting for them here costs little; barrier (2) then has
+      // every wave's, and thread 0 raises the group's flag for the workers.
+      // (Waiting right after a group's last stores stalls on their write-through;
+      // an agent-scope release fence would also write back the whole L2.)
+      const bool publish = p.dx_ctrl != nullptr && (s + 1) % G == 0 && s + 1 < NC;
+      if (publish) __builtin_amdgcn_s_waitcnt(0);
       // ---- B2b: dZ2 into the state gradient and dX2; dZ1; dXQ and dXK partials
       Frag<T> dz1f[HT];
       {
@@ -727,6 +735,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         db2[c] += sum_col4(acc);
       }
       __syncthreads();  // (2) dXK partials in
+      if (publish && threadIdx.x == 0)
+        __hip_atomic_store(p.dx_ctrl + kDxCtrlHead + chain * NK + (s + 1) / G, 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 
       // ---- B3: the dXQ / dXK terms without W1 (to the handoff), dXV (tile owners)
       {
@@ -746,18 +757,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         }
       }
       __syncthreads();  // (2x) exchange area free for the next mini-batch
-      if (p.dx_ctrl != nullptr && s % G == 0) {
-        // checkpoint group s / G is complete: every wave's handoff stores
-        // (device-coherent, written through) acknowledged, then the group's
-        // flag raised for the workers.  (An agent-scope release fence would
-        // also write back the whole L2: ~20 us per group.)
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0)
-          __hip_atomic_store(p.dx_ctrl + kDxCtrlHead + chain * NK + s / G, 1, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
+  }
+  if (p.dx_ctrl != nullptr) {
+    // group 0, closed by the last mini-batch: every wave's handoff stores
+    // acknowledged, then its flag
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(p.dx_ctrl + kDxCtrlHead + chain * NK, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- outputs: gradient wrt the initial state, LN parameters
