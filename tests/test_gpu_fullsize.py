@@ -1,0 +1,108 @@
+"""Parity at the benchmark's full size: B=16, H=12, T=2048 (NC=128 mini-batches
+of K=16), F=64, bf16 activations with fp32 state; TTT-MLP with FF=256 and
+checkpoint group 8, TTT-Linear with group 16.
+
+The oracle needs about a second per chain at this length, so the full launch
+(192 chains) is checked through properties that do not depend on its size, and against the
+oracle on whole chains:
+  * determinism: the same launch twice gives the same bits;
+  * chain independence: the recurrence never mixes (batch, head) chains, so
+    every per-chain output of the full launch (the readout, dXQ, dXV, dXK,
+    deta and the gradient wrt the chain's initial state) equals, bit for bit,
+    that chain's output in a launch of its batch row alone (H chains);
+  * two whole chains (all 128 mini-batches, first and last of the grid)
+    against the fp64 oracle at the bf16 bar, rel-L2 <= 2e-2.
+The LayerNorm-parameter gradients are sums over the batch, so they are only
+covered by the smaller tests."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import ttt_oracle as O
+from tests._util import oracle_linear_grads, oracle_mlp_grads, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_RTOL = 2e-2
+B, H, NC, K, F = 16, 12, 128, 16, 64
+ROWS = (0, B - 1)                 # batch rows launched on their own
+CHAINS = ((0, 0), (B - 1, H - 1))  # (b, h) checked against the oracle
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _mlp(d, G):
+    from ttt_amd.mlp import mlp_backward, mlp_forward
+    g = to_dev(d)
+    out, ck, _, last, saved = mlp_forward(*(g[k] for k in ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV",
+                                                          "XK", "eta")),
+                                          G, want_ckpt=True, want_last=True, want_saved=True, ckpt_w1_only=True)
+    (_, _, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    torch.cuda.synchronize()
+    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2)
+
+
+def _linear(d, G):
+    from ttt_amd.linear import linear_backward, linear_forward
+    g = to_dev(d)
+    out, (Wc, _), (Wl, _), saved = linear_forward(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["XQ"], g["XV"], g["XK"],
+                                                  g["eta"], G, want_ckpt=True, want_last=True, want_saved=True)
+    (_, _, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, Wl, saved, g["dOut"], G)
+    torch.cuda.synchronize()
+    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW, db1=db)
+
+
+def _row(d, b):
+    return {k: v if k in ("ln_w", "ln_b") else v[b:b + 1] for k, v in d.items()}
+
+
+def _chain(d, b, h):
+    return {k: v[h:h + 1] if k in ("ln_w", "ln_b") else v[b:b + 1, h:h + 1] for k, v in d.items()}
+
+
+def _check(d, run, oracle, G):
+    full = {k: v.cpu() for k, v in run(d, G).items()}
+    again = {k: v.cpu() for k, v in run(d, G).items()}
+    bad = [k for k in full if not torch.equal(full[k], again[k])]
+    _say("  determinism: differing outputs", bad)
+    assert not bad, f"not deterministic: {bad}"
+
+    for b in ROWS:
+        row = {k: v.cpu() for k, v in run(_row(d, b), G).items()}
+        bad = []
+        for k in row:
+            same = torch.equal(row[k][0], full[k][b])
+            if not same:
+                diff = float((row[k][0].double() - full[k][b].double()).abs().max())
+                bad.append(f"{k} (max diff {diff:.3e})")
+        _say(f"  batch row {b} alone vs the full launch: differing", bad)
+        assert not bad, f"chains of row {b} depend on the rest of the launch: {bad}"
+
+    for b, h in CHAINS:
+        dc = _chain(d, b, h)
+        ref = oracle(dc, dc["dOut"], G=0)
+        bad = []
+        for k in full:
+            err = rel_l2(full[k][b:b + 1, h:h + 1], ref[k])
+            _say(f"  chain ({b},{h}) {k}: rel-L2 {err:.3e}")
+            if err > BF16_RTOL:
+                bad.append(k)
+        assert not bad, f"chain ({b},{h}) off the oracle: {bad}"
+
+
+def test_mlp_fwd_bwd_full_size():
+    _say(f"mlp fwd+bwd full size B{B} H{H} NC{NC} F{F} FF256 G8 bf16")
+    d = O.make_inputs(B, H, NC, K, F, FF=256, seed=3, dtype=torch.bfloat16, with_grad=True)
+    _check(d, _mlp, oracle_mlp_grads, G=8)
+
+
+def test_linear_fwd_bwd_full_size():
+    _say(f"linear fwd+bwd full size B{B} H{H} NC{NC} F{F} G16 bf16")
+    d = O.make_inputs(B, H, NC, K, F, seed=2, dtype=torch.bfloat16, with_grad=True)
+    _check(d, _linear, oracle_linear_grads, G=16)
