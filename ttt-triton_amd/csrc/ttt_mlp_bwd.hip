@@ -56,6 +56,7 @@ template <int FT, int NW> struct MlpBwdShared {
   float w2t[16 * FT * 64 * NW];   // W2^T  [F][FF], swizzled
   float dw1t[16 * FT * 64 * NW];  // dW1^T [FF][F], swizzled
   MlpBwdExchange<FT, NW> x;
+  float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
 };
 
 size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
@@ -233,11 +234,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   auto ld_hid = [&](int o, int off, int us) { return frag_to_f4(bload_frag<T>(rSV, hl + o * 256 * ST, us + off)); };
   auto ld_f32 = [&](int c, int off, int us) { return bload_frag<float>(rSV, f4l + c * 1024, us + off).v; };
 
-  // LayerNorm parameters of this head, re-read (L1/L2 resident) where used
-  const rsrc_t rLW = make_rsrc(p.ln_w + (size_t)h * F, F * 4), rLB = make_rsrc(p.ln_b + (size_t)h * F, F * 4);
-  auto ln_param = [&](rsrc_t r, float (&v)[FT]) {
+  // LayerNorm parameters of this head, staged in LDS once and re-read where used
+  for (int i = threadIdx.x; i < F; i += 64 * NW) {
+    sh.lnw[i] = p.ln_w[(size_t)h * F + i];
+    sh.lnb[i] = p.ln_b[(size_t)h * F + i];
+  }
+  auto ln_param = [&](const float* src, float (&v)[FT]) {
 #pragma unroll
-    for (int o = 0; o < FT; ++o) v[o] = bload_f32(r, n * 4, o * 64);
+    for (int o = 0; o < FT; ++o) v[o] = src[16 * o + n];
   };
   const Frag<T> I = identity_frag<T>();
 
@@ -273,6 +277,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // retire the loads issued so far: pending on loop entry, they make the
   // wait-count pass wait for every outstanding access in each iteration
   __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // the LayerNorm parameters are in LDS
 
   // Reverse sweep.  Regions between barriers:   A..P | B2a | LN2..B2b | B3
   // exchange area:                              dG2, dN1, de partials; dXQ, dXK partials
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       f4 xhb[FT], g2v[FT];
       Frag<T> dof[FT];
       float lnw_tm[FT];
-      ln_param(rLW, lnw_tm);
+      ln_param(sh.lnw, lnw_tm);
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         xhb[c] = ld_f32(c, Slot::XHB, us);
@@ -590,8 +595,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
       for (int o = 0; o < HT; ++o) g1ef[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E);
       float lnw2[FT], lnb2[FT];
-      ln_param(rLW, lnw2);
-      ln_param(rLB, lnb2);
+      ln_param(sh.lnw, lnw2);
+      ln_param(sh.lnb, lnb2);
       __syncthreads();  // (1) dG2, dN1, eta-row partials in
 
       // ---- B2a: assemble dN1, de; deta (wave 0); dG2
