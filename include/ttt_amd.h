@@ -7,9 +7,19 @@
  *     mini-batch (16), F head dim (32 or 64), FF MLP hidden width (F, 2F or
  *     4F, multiple of 64 up to 256), G checkpoint group size (1..NC),
  *     NK = ceil(NC / G).
- *   - Activations (XQ, XK, XV, eta, out and their gradients) share one dtype,
+ *   - Activations (XQ, XK, XV, out and their gradients) share one dtype,
  *     `dtype` (TTT_DTYPE_F32 or TTT_DTYPE_BF16).  Fast-weight state, LayerNorm
  *     parameters, checkpoints, memo snapshots and weight gradients are fp32.
+ *   - eta comes in one of two forms, chosen by `eta_rule` (enum ttt_eta_rule):
+ *     TTT_ETA_DENSE: `eta` is the full [B,H,NC,K,K] tensor in the activation
+ *     dtype, as ops/ttt_linear.py and ops/ttt_mlp.py take it, and the
+ *     backward writes the dense [B,H,NC,K,K] gradient into `deta`;
+ *     TTT_ETA_LAYER / TTT_ETA_CAUSAL: `eta` is the per-token learning rate
+ *     lr [B,H,NC,K] fp32 (TTTBase.get_eta, ttt_layer.py:151-163) that the
+ *     kernels expand on chip (LAYER: eta[i][j] = lr[j]/K for every row i, the
+ *     layer's own rule, ttt_layer.py:309; CAUSAL: eta[i][j] = lr[j]/(i+1) for
+ *     j <= i, else 0), and the backward writes dlr [B,H,NC,K] fp32
+ *     (dlr[j] = sum_i deta[i][j] * d eta[i][j] / d lr[j]) into `deta`.
  *   - The caller allocates every buffer; nothing is allocated or kept between
  *     calls.  `stream` is a hipStream_t (NULL = the null stream); launches are
  *     asynchronous on it.
@@ -28,9 +38,11 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 7
+#define TTT_AMD_ABI_VERSION 8
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
+
+enum ttt_eta_rule { TTT_ETA_DENSE = 0, TTT_ETA_LAYER = 1, TTT_ETA_CAUSAL = 2 };
 
 enum ttt_status {
   TTT_OK = 0,
@@ -40,7 +52,8 @@ enum ttt_status {
   TTT_ERR_ALIGN = -4,     /* pointer not 16-byte aligned */
   TTT_ERR_HIP = -5,       /* launch failed (hipGetLastError) */
   TTT_ERR_WORKSPACE = -6, /* workspace missing or too small */
-  TTT_ERR_ARG = -7        /* other invalid argument (eps, G, M) */
+  TTT_ERR_ARG = -7,       /* other invalid argument (eps, G, M, eta_rule, option) */
+  TTT_ERR_TIMEOUT = -8    /* ttt_mlp_bwd_check: a dXQ/dXK worker gave up waiting */
 };
 
 /* ABI version of the loaded library (TTT_AMD_ABI_VERSION). */
@@ -53,7 +66,7 @@ const char* ttt_error_string(int status);
  * Replaces ttt_linear_scan_forward (kernels/linear_forward.py:5-148) as
  * launched by TritonLinear._forward_core (linear_triton.py:62-144), and is
  * the forward of ops.ttt_linear (ops/ttt_linear.py:57-84).
- *   XQ, XK, XV  [B,H,NC,K,F] dtype      eta [B,H,NC,K,K] dtype
+ *   XQ, XK, XV  [B,H,NC,K,F] dtype      eta [B,H,NC,K,K] dtype, or lr [B,H,NC,K] fp32 (eta_rule)
  *   ln_w, ln_b  [H,F] fp32              W1_init [B,H,F,F], b1_init [B,H,1,F] fp32
  *   out         [B,H,NC,K,F] dtype      (XQ + LN(Z1_bar) per mini-batch)
  *   W1_last, b1_last  [B,H,F,F], [B,H,1,F] fp32, final state (both or neither)
@@ -68,7 +81,7 @@ const char* ttt_error_string(int status);
  * NC times the per-mini-batch saved size must stay below 2^31 bytes. */
 int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                    const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
-                   int B, int H, int NC, int K, int F, int G, int dtype, float eps,
+                   int B, int H, int NC, int K, int F, int G, int dtype, int eta_rule, float eps,
                    void* out, float* W1_last, float* b1_last, float* W1_ckpt, float* b1_ckpt,
                    void* saved, size_t saved_bytes, void* stream);
 
@@ -83,7 +96,8 @@ size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F);
  *   W1_ckpt           weight checkpoints written by ttt_linear_fwd with the same G
  *   W1_last           the final weight written by that ttt_linear_fwd call
  *   dout              [B,H,NC,K,F] dtype
- *   dXQ, dXK, dXV     [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
+ *   dXQ, dXK, dXV     [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense), or
+ *                     dlr [B,H,NC,K] fp32 (eta_rule LAYER / CAUSAL)
  *   dW1, db1          [B,H,F,F], [B,H,1,F] fp32 (gradient wrt W1_init, b1_init)
  *   dln_w, dln_b      [B,H,F] fp32 per-chain partials; sum over B for [H,F]
  *   saved             the saved buffer written by that ttt_linear_fwd call
@@ -92,7 +106,7 @@ size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F);
  * bias entered. */
 int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                    const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* W1_last,
-                   const void* dout, int B, int H, int NC, int K, int F, int G, int dtype, float eps,
+                   const void* dout, int B, int H, int NC, int K, int F, int G, int dtype, int eta_rule, float eps,
                    void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1,
                    float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* stream);
 
@@ -107,7 +121,8 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
  *                     none; b1_ckpt, W2_ckpt and b2_ckpt are each optional (the
  *                     backward reads W1's only)
  *   *_memo            [B,H,NS,...], NS = ceil(NC/M): state after mini-batch
- *                     s*M has been applied (all four or none; M >= 1 then)
+ *                     s*M has been applied (all four or none; M >= 1 then;
+ *                     M > NC gives NS = 1, as the reference's memo loop does)
  *   saved             NULL, or >= ttt_mlp_saved_bytes(...) bytes: receives, for
  *                     every mini-batch, the state-update operands and the
  *                     activations ttt_mlp_bwd needs.  It has no counterpart in
@@ -118,7 +133,7 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
 int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_init, const float* b1_init,
                 const float* W2_init, const float* b2_init,
-                int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
+                int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, int eta_rule, float eps,
                 void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last,
                 float* W1_ckpt, float* b1_ckpt, float* W2_ckpt, float* b2_ckpt,
                 float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo,
@@ -141,7 +156,8 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
  *                    (b1_ckpt, W2_ckpt, b2_ckpt are not read and may be NULL)
  *   *_last           the final state written by that ttt_mlp_fwd call
  *   dout             [B,H,NC,K,F] dtype
- *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense)
+ *   dXQ, dXK, dXV    [B,H,NC,K,F] dtype;  deta [B,H,NC,K,K] dtype (dense), or
+ *                    dlr [B,H,NC,K] fp32 (eta_rule LAYER / CAUSAL)
  *   dW1, db1, dW2, db2  fp32, shapes of W1_init ... (gradient wrt the initial state)
  *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
  *   saved            the saved buffer written by that ttt_mlp_fwd call
@@ -149,12 +165,18 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
  *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes of scratch
  *                    (dZ1b, dZ1 and partial dXQ/dXK per mini-batch, handed
  *                    from the reverse sweep to the pass that forms dXQ/dXK,
- *                    and that pass's control words) */
+ *                    and that pass's control words)
+ * When one chain's sweep fits per CU with CUs to spare (B*H + 16 <= CUs), the
+ * dXQ/dXK pass runs in the sweep's launch on the spare CUs, each worker
+ * waiting (bounded by TTT_OPT_MLP_BWD_POLL_LIMIT polls) for the checkpoint
+ * group it takes.  A worker that gives up writes NaN into that group's dXQ
+ * and dXK and raises a timeout word; ttt_mlp_bwd_check reads it.  Otherwise,
+ * or with TTT_OPT_MLP_BWD_FUSED = 0, the pass is a second launch. */
 int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
                 const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,
                 const float* W2_last, const float* b2_last, const void* dout,
-                int B, int H, int NC, int K, int F, int FF, int G, int dtype, float eps,
+                int B, int H, int NC, int K, int F, int FF, int G, int dtype, int eta_rule, float eps,
                 void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2, float* db2,
                 float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, void* stream);
@@ -215,6 +237,79 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
                              int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps,
                              float* gates, size_t gates_bytes, void* dXK, void* dXU, void* dXQW,
                              void* stream);
+
+/* ---- the producer and consumer around the inner loop (ttt_layer.py) ----
+ * Shapes: B batch, L = NC*K tokens, H heads, F head dim (32 or 64), K = 16,
+ * D = H*F <= 1024.  Activations in `dtype`, everything else fp32. */
+
+/* Bytes of the per-block LayerNorm-parameter gradient partials of
+ * ttt_qkvu_producer_bwd / ttt_post_norm_bwd: ceil(B*L/32) blocks x 2 x D
+ * floats; the caller sums them over blocks (dln_w = sum[:, 0], dln_b =
+ * sum[:, 1], each [D] = [H,F]).  0 for unsupported sizes. */
+size_t ttt_layer_io_partial_bytes(int B, int L, int H, int F);
+
+/* The layer's input preprocessing after its projections, written straight
+ * into the inner loop's layouts.  Replaces, in TTTBase.process_input
+ * (ttt_layer.py:261-309): the L2 normalisation of XQ, XK, XU (:279-281,
+ * x / max(|x|, 1e-12)), RoPE at each token's position (:287-300 with
+ * utils.py:97-123), ln_reconstruction_target (:227-243, :302; unbiased std,
+ * `eps` = 1e-8 there), reshape_to_mini_batch (:245-259) and get_eta
+ * (:151-163; lr = base_lr * sigmoid(logit) / F, before the layer's 1/K row
+ * repeat, which the inner loop's TTT_ETA_LAYER rule applies on chip).
+ *   proj     [B*L][ld] dtype: per token XQ | XK | XV | XU (D each, head-major)
+ *            | H lr logits (ttt_lr_weight . x + ttt_lr_bias) | padding;
+ *            ld >= 4*D + H, ld % 4 == 0 (one fused projection GEMM gives it)
+ *   rope     [L][F/2][2] fp32: cos, sin of the angle of pair p at position t
+ *   ln_w, ln_b  [H,F] fp32 (ttt_norm_weight / ttt_norm_bias)
+ *   XQ, XK, XV, XU  [B,H,NC,K,F] dtype (XV = the reconstruction target)
+ *   lr       [B,H,NC,K] fp32 */
+int ttt_qkvu_producer_fwd(const void* proj, int ld, const float* rope, const float* ln_w, const float* ln_b,
+                          int B, int L, int H, int K, int F, float base_lr, float eps, int dtype,
+                          void* XQ, void* XK, void* XV, void* XU, float* lr, void* stream);
+
+/* Backward of ttt_qkvu_producer_fwd (it recomputes the forward from proj):
+ * given the gradients of its outputs (dlr may be NULL: no lr gradient),
+ * writes the gradient of every proj row (padding columns zeroed) and the
+ * LayerNorm-parameter partials of the reconstruction target. */
+int ttt_qkvu_producer_bwd(const void* proj, int ld, const float* rope, const float* ln_w, const float* ln_b,
+                          const void* dXQ, const void* dXK, const void* dXV, const void* dXU, const float* dlr,
+                          int B, int L, int H, int K, int F, float base_lr, float eps, int dtype,
+                          void* dproj, float* partial, size_t partial_bytes, void* stream);
+
+/* The layer's output path before `wo`: the inner loop's output [B,H,NC,K,F]
+ * permuted and reshaped to [B, L, D] (ttt_layer.py:406,420 / :563-564) and
+ * LayerNorm-ed over D with gamma, beta [D] fp32 (post_norm, ttt_layer.py:78,349;
+ * biased variance, `eps` 1e-6 there).  out [B,L,D] dtype; stats [B*L][2] fp32
+ * (mean, 1/sigma) for the backward. */
+int ttt_post_norm_fwd(const void* XQW, const float* gamma, const float* beta, int B, int L, int H, int K, int F,
+                      float eps, int dtype, void* out, float* stats, void* stream);
+
+/* Backward of ttt_post_norm_fwd: dXQW [B,H,NC,K,F] dtype and the gamma/beta
+ * gradient partials. */
+int ttt_post_norm_bwd(const void* XQW, const float* gamma, const float* stats, const void* dout,
+                      int B, int L, int H, int K, int F, int dtype, void* dXQW, float* partial,
+                      size_t partial_bytes, void* stream);
+
+/* Process-wide options of the library (no counterpart in the reference):
+ *   TTT_OPT_MLP_BWD_POLL_LIMIT  polls of a checkpoint-group flag before a fused
+ *                               dXQ/dXK worker of ttt_mlp_bwd gives up (>= 0;
+ *                               default 4194304, about a second)
+ *   TTT_OPT_MLP_BWD_FUSED       1 (default): the dXQ/dXK pass runs inside the
+ *                               sweep's launch when it fits; 0: always a second
+ *                               launch (no waits at all)
+ * ttt_set_option returns TTT_OK or TTT_ERR_ARG; ttt_get_option returns the
+ * value, or -1 for an unknown option. */
+enum ttt_option { TTT_OPT_MLP_BWD_POLL_LIMIT = 1, TTT_OPT_MLP_BWD_FUSED = 2 };
+int ttt_set_option(int option, long long value);
+long long ttt_get_option(int option);
+
+/* Status of the last ttt_mlp_bwd call that used `workspace` (same sizes):
+ * waits for `stream`, then returns TTT_OK, or TTT_ERR_TIMEOUT if a fused
+ * dXQ/dXK worker gave up waiting for its checkpoint group (that group's dXQ
+ * and dXK rows then hold NaN).  No counterpart in the reference, whose
+ * backward has no cross-workgroup waits. */
+int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int H, int NC, int K, int F,
+                      int FF, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

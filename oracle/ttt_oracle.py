@@ -26,7 +26,7 @@ What it restates (reference file:line):
                      memo = state after mini-batch s*M (kernels/mlp_forward.py:193-226);
                      W_last = final state (kernels/linear_forward.py:147-148)
   eta builders       ttt_layer.py:151-163,306-309 (row-constant "layer" eta) and the
-                     causal variant eta[i,j] = lr[j]/(i+1) for j<=i
+                     causal variant eta[i,j] = lr[j]/(i+1) for j<=i (eta_from_lr, make_eta)
   inputs             seeded generator in the order XQ, XK, XV, u, W1, W2, dOut
 
 How each function is pinned (tests/test_oracle.py):
@@ -364,24 +364,30 @@ def memo_combine(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b
 # synthetic inputs (seeded; shapes and distributions of the benchmark configs)
 # ----------------------------------------------------------------------------
 
-def make_eta(u: torch.Tensor, F_: int, kind: str = "causal") -> torch.Tensor:
-    """Build a [B,H,NC,K,K] eta from u [B,H,NC,K]: lr = sigmoid(u)/F.
+def eta_from_lr(lr: torch.Tensor, kind: str = "causal") -> torch.Tensor:
+    """Expand per-token learning rates lr [B,H,NC,K] into a [B,H,NC,K,K] eta.
 
     kind="causal": eta[i,j] = lr[j]/(i+1) for j <= i, else 0.
-    kind="layer":  eta[i,j] = lr[j]/K for every i (ttt_layer.py:151-163,306-309).
+    kind="layer":  eta[i,j] = lr[j]/K for every i (ttt_layer.py:306-309: the
+                   layer multiplies the repeated get_eta output by 1/K).
     kind="tokens": eta[i,j] = lr[j] for every i.
     """
-    lr = torch.sigmoid(u) / F_
-    K = u.shape[-1]
+    K = lr.shape[-1]
     if kind == "layer":
-        return (lr / K)[..., None, :].expand(*u.shape[:-1], K, K).contiguous()
+        return (lr / K)[..., None, :].expand(*lr.shape[:-1], K, K).contiguous()
     if kind == "tokens":
-        return lr[..., None, :].expand(*u.shape[:-1], K, K).contiguous()
+        return lr[..., None, :].expand(*lr.shape[:-1], K, K).contiguous()
     if kind == "causal":
-        i = torch.arange(K, dtype=u.dtype)
-        scale = torch.tril(torch.ones(K, K, dtype=u.dtype)) / (i + 1)[:, None]
+        i = torch.arange(K, dtype=lr.dtype)
+        scale = torch.tril(torch.ones(K, K, dtype=lr.dtype)) / (i + 1)[:, None]
         return lr[..., None, :] * scale
     raise ValueError(kind)
+
+
+def make_eta(u: torch.Tensor, F_: int, kind: str = "causal") -> torch.Tensor:
+    """Build a [B,H,NC,K,K] eta from u [B,H,NC,K]: lr = sigmoid(u)/F, then
+    eta_from_lr(lr, kind)."""
+    return eta_from_lr(torch.sigmoid(u) / F_, kind)
 
 
 def make_inputs(B, H, NC, K, F_, FF: int = 0, seed: int = 0, dtype=torch.float32,

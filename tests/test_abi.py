@@ -11,8 +11,9 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ttt_amd.h")
 
-OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG = 0, -1, -2, -3, -4, -5, -6, -7
+OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG, E_TIMEOUT = 0, -1, -2, -3, -4, -5, -6, -7, -8
 F32, BF16 = 0, 1
+DENSE, LAYER, CAUSAL = 0, 1, 2
 P = 0x10000  # an aligned, never-dereferenced address
 Q = 0x10008  # misaligned
 
@@ -41,7 +42,7 @@ def test_header_declares_the_abi():
                  "ttt_linear_saved_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
                  "ttt_mlp_bwd_workspace_bytes",
                  "ttt_mlp_cached_readout", "ttt_mlp_memo_gates_bytes", "ttt_mlp_memo_combine",
-                 "ttt_mlp_memo_combine_bwd"):
+                 "ttt_mlp_memo_combine_bwd", "ttt_set_option", "ttt_get_option", "ttt_mlp_bwd_check"):
         assert name in decls, name
 
 
@@ -57,14 +58,14 @@ def test_every_declared_symbol_is_exported(lib):
 def test_version_and_error_strings(lib):
     from ttt_amd import _lib
     assert lib.ttt_abi_version() == _lib.ABI_VERSION
-    for code in (OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG):
+    for code in (OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG, E_TIMEOUT):
         assert lib.ttt_error_string(code)
     assert lib.ttt_error_string(-99) == b"unknown status"
 
 
 def _lin_fwd(lib, **kw):
     a = dict(XQ=P, XK=P, XV=P, eta=P, lw=P, lb=P, W=P, b=P, B=2, H=4, NC=16, K=16, F=64, G=4, dtype=F32,
-             eps=1e-8, out=P, Wl=None, bl=None, Wc=None, bc=None, saved=None, saved_bytes=0, stream=None)
+             eta_rule=DENSE, eps=1e-8, out=P, Wl=None, bl=None, Wc=None, bc=None, saved=None, saved_bytes=0, stream=None)
     a.update(kw)
     return lib.ttt_linear_fwd(*a.values())
 
@@ -80,6 +81,11 @@ def test_linear_fwd_validation(lib):
     assert _lin_fwd(lib, G=0) == E_ARG
     assert _lin_fwd(lib, G=17) == E_ARG
     assert _lin_fwd(lib, eps=0.0) == E_ARG
+    assert _lin_fwd(lib, eta_rule=3) == E_ARG
+    assert _lin_fwd(lib, eta_rule=-1) == E_ARG
+    # a valid eta rule passes on to the next check (here: a missing output)
+    assert _lin_fwd(lib, eta_rule=LAYER, out=None) == E_NULL
+    assert _lin_fwd(lib, eta_rule=CAUSAL, out=None) == E_NULL
     assert _lin_fwd(lib, Wl=P, XQ=None) == E_NULL
     assert _lin_fwd(lib, Wl=P, bl=None, Wc=Q, bc=P, XQ=P, K=16) in (E_NULL, E_ALIGN)
 
@@ -94,8 +100,11 @@ def test_linear_saved_buffer(lib):
     assert lib.ttt_linear_saved_bytes(B, H, NC, 8, F) == 0
     assert _lin_fwd(lib, saved=P, saved_bytes=need - 4) == E_WS
     assert _lin_fwd(lib, saved=Q, saved_bytes=need) == E_ALIGN
-    args = [P] * 9 + [B, H, NC, K, F, 4, F32, 1e-8] + [P] * 8
+    args = [P] * 9 + [B, H, NC, K, F, 4, F32, DENSE, 1e-8] + [P] * 8
     assert lib.ttt_linear_bwd(*args, P, need - 4, None) == E_WS
+    bad = list(args)
+    bad[16] = 5  # eta_rule
+    assert lib.ttt_linear_bwd(*bad, P, need, None) == E_ARG
     assert lib.ttt_linear_bwd(*args, None, need, None) == E_WS
     assert lib.ttt_linear_bwd(*args, Q, need, None) == E_ALIGN
     bad = list(args)
@@ -107,8 +116,8 @@ def test_linear_saved_buffer(lib):
 
 
 def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, saved=None, saved_bytes=0, NC=16, ckpt=(None,) * 4, **kw):
-    a = ([P] * 10 + [2, 4, NC, 16, 64, FF, 4, M, kw.get("dtype", BF16), 1e-8, P] + [None] * 4 + list(ckpt)
-         + list(memo) + [saved, saved_bytes, None])
+    a = ([P] * 10 + [2, 4, NC, 16, 64, FF, 4, M, kw.get("dtype", BF16), kw.get("eta_rule", DENSE), 1e-8, P]
+         + [None] * 4 + list(ckpt) + list(memo) + [saved, saved_bytes, None])
     return lib.ttt_mlp_fwd(*a)
 
 
@@ -118,7 +127,11 @@ def test_mlp_fwd_validation(lib):
     assert _mlp_fwd(lib, dtype=3) == E_DTYPE
     assert _mlp_fwd(lib, memo=(P, P, P, None), M=2) == E_NULL
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=0) == E_ARG
-    assert _mlp_fwd(lib, memo=(P, P, P, P), M=17) == E_ARG
+    assert _mlp_fwd(lib, eta_rule=7) == E_ARG
+    # M > NC is accepted (one memo state, as the reference's loop gives): the
+    # call gets past the memo check to the saved-buffer check
+    need = lib.ttt_mlp_saved_bytes(2, 4, 16, 16, 64, 256, BF16)
+    assert _mlp_fwd(lib, memo=(P, P, P, P), M=17, saved=Q, saved_bytes=need) == E_ALIGN
     assert _mlp_fwd(lib, memo=(P, P, Q, P), M=2) == E_ALIGN
     # checkpoints: W1's, optionally with any of the other three
     assert _mlp_fwd(lib, ckpt=(None, P, None, None)) == E_NULL
@@ -149,8 +162,11 @@ def test_mlp_saved_buffer(lib):
     # 256-byte units)
     ctrl = ((4 + B * H * NC) * 4 + 255) // 256 * 256
     assert w16 == B * H * NC * (2 * FF * K * 2 + 2 * K * F * 4) + ctrl
-    args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, 1e-8] + [P] * 10
+    args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, DENSE, 1e-8] + [P] * 10
     assert lib.ttt_mlp_bwd(*args, P, n16 - 1, P, w16, None) == E_WS
+    bad = list(args)
+    bad[23] = 3  # eta_rule
+    assert lib.ttt_mlp_bwd(*bad, P, n16, P, w16, None) == E_ARG
     assert lib.ttt_mlp_bwd(*args, None, n16, P, w16, None) == E_WS
     assert lib.ttt_mlp_bwd(*args, Q, n16, P, w16, None) == E_ALIGN
     assert lib.ttt_mlp_bwd(*args, P, n16, P, w16 - 1, None) == E_WS
@@ -223,3 +239,29 @@ def test_memo_combine_validation(lib):
     assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, None, P, P, None) == E_NULL
     assert lib.ttt_mlp_memo_combine_bwd(*bwd, P, need, P, None, P, None) == E_NULL
     assert lib.ttt_mlp_memo_combine_bwd(*([P, None] + [P] * 8 + bwd[10:]), P, need, P, P, P, None) == E_NULL
+
+
+def test_options(lib):
+    from ttt_amd import _lib
+    poll, fused = _lib.OPT_MLP_BWD_POLL_LIMIT, _lib.OPT_MLP_BWD_FUSED
+    old_poll, old_fused = lib.ttt_get_option(poll), lib.ttt_get_option(fused)
+    assert old_poll == 1 << 22 and old_fused == 1
+    try:
+        assert lib.ttt_set_option(poll, 0) == OK and lib.ttt_get_option(poll) == 0
+        assert lib.ttt_set_option(poll, -1) == E_ARG
+        assert lib.ttt_set_option(poll, 1 << 31) == E_ARG
+        assert lib.ttt_set_option(fused, 0) == OK and lib.ttt_get_option(fused) == 0
+        assert lib.ttt_set_option(fused, 2) == E_ARG
+        assert lib.ttt_set_option(99, 1) == E_ARG
+        assert lib.ttt_get_option(99) == -1
+    finally:
+        lib.ttt_set_option(poll, old_poll)
+        lib.ttt_set_option(fused, old_fused)
+
+
+def test_mlp_bwd_check_validation(lib):
+    B, H, NC, K, F, FF = 2, 4, 16, 16, 64, 256
+    w = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, BF16)
+    assert lib.ttt_mlp_bwd_check(None, w, B, H, NC, K, F, FF, BF16, None) == E_WS
+    assert lib.ttt_mlp_bwd_check(P, w - 1, B, H, NC, K, F, FF, BF16, None) == E_WS
+    assert lib.ttt_mlp_bwd_check(P, w, 0, H, NC, K, F, FF, BF16, None) == E_SHAPE

@@ -237,3 +237,63 @@ def test_mlp_bwd_more_chains_than_cus():
         if err > BF16_RTOL:
             bad.append(k)
     assert not bad
+
+
+def test_mlp_bwd_worker_timeout_is_loud():
+    """With the poll limit set to 0 from the host, a fused dXQ/dXK worker
+    whose checkpoint group is not yet published gives up at once (every
+    kernel still exits normally): its group's dXQ and dXK rows hold NaN and
+    ttt_mlp_bwd_check reports the timeout, so wrong gradients never pass
+    silently.  Groups computed before giving up, and everything the reverse
+    sweep writes itself, equal a normal run bit for bit.  With the fused mode
+    switched off (two launches) the gradients equal the fused run's."""
+    from ttt_amd import _lib
+    from ttt_amd.mlp import mlp_backward, mlp_bwd_status
+    B, H, NC, G, F_, FF = 2, 4, 64, 4, 64, 256
+    NK = NC // G
+    _say(f"fused worker timeout: bf16 B{B} H{H} NC{NC} G{G} poll limit 0")
+    d = O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=61, dtype=torch.bfloat16, with_grad=True)
+    out, ck, _, last, saved = _fwd(d, G)
+    g = to_dev(d)
+    lib = _lib.load()
+    nws = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, 16, F_, FF, 1)
+    ws = torch.empty(nws, device="cuda", dtype=torch.uint8)
+    args = (g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    good = mlp_backward(*args, workspace=ws, check_timeout=False)
+    assert mlp_bwd_status(ws, B, H, NC, 16, F_, FF, 1) == 0
+    old = _lib.get_option(_lib.OPT_MLP_BWD_POLL_LIMIT)
+    try:
+        _lib.set_option(_lib.OPT_MLP_BWD_POLL_LIMIT, 0)
+        bad = mlp_backward(*args, workspace=ws, check_timeout=False)
+        st = mlp_bwd_status(ws, B, H, NC, 16, F_, FF, 1)
+    finally:
+        _lib.set_option(_lib.OPT_MLP_BWD_POLL_LIMIT, old)
+    assert st == _lib.STATUS_TIMEOUT
+    # sweep outputs: dW1..db2, dln (first tuple), dXV and deta
+    for a, b in zip(good[0], bad[0]):
+        assert torch.equal(a, b)
+    assert torch.equal(good[1][1], bad[1][1]) and torch.equal(good[1][3], bad[1][3])
+    n_nan = 0
+    for gi, bi in ((good[1][0], bad[1][0]), (good[1][2], bad[1][2])):  # dXQ, dXK
+        gb = gi.reshape(B * H, NK, G * 16 * F_)
+        bb = bi.reshape(B * H, NK, G * 16 * F_)
+        for c in range(B * H):
+            for k in range(NK):
+                if torch.isnan(bb[c, k]).all():
+                    n_nan += 1
+                else:
+                    assert torch.equal(gb[c, k], bb[c, k]), (c, k)
+    _say(f"  {n_nan} of {2 * B * H * NK} (tensor, chain, group) blocks poisoned")
+    assert n_nan > 0
+    # the normal limit again: no timeout, same gradients
+    again = mlp_backward(*args, workspace=ws, check_timeout=True)
+    for a, b in zip(good[0] + good[1], again[0] + again[1]):
+        assert torch.equal(a, b)
+    # two launches instead of the fused workers
+    try:
+        _lib.set_option(_lib.OPT_MLP_BWD_FUSED, 0)
+        two = mlp_backward(*args, workspace=ws, check_timeout=True)
+    finally:
+        _lib.set_option(_lib.OPT_MLP_BWD_FUSED, 1)
+    for a, b in zip(good[0] + good[1], two[0] + two[1]):
+        assert torch.equal(a, b)

@@ -3,9 +3,17 @@
 // contracts are in include/ttt_amd.h.
 #include <stdint.h>
 
+#include <atomic>
+
 #include "ttt_kernels.h"
 
 namespace {
+
+// process-wide options (ttt_set_option)
+std::atomic<long long> g_mlp_bwd_poll_limit{1LL << 22};
+std::atomic<long long> g_mlp_bwd_fused{1};
+
+bool eta_rule_ok(int r) { return r == TTT_ETA_DENSE || r == TTT_ETA_LAYER || r == TTT_ETA_CAUSAL; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -64,6 +72,7 @@ const char* ttt_error_string(int status) {
     case TTT_ERR_HIP: return "HIP launch failed";
     case TTT_ERR_WORKSPACE: return "workspace missing or too small";
     case TTT_ERR_ARG: return "invalid argument";
+    case TTT_ERR_TIMEOUT: return "a fused dXQ/dXK worker gave up waiting (its rows hold NaN)";
     default: return "unknown status";
   }
 }
@@ -75,10 +84,11 @@ size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F) {
 
 int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                    const float* ln_b, const float* W1_init, const float* b1_init, int B, int H, int NC, int K,
-                   int F, int G, int dtype, float eps, void* out, float* W1_last, float* b1_last, float* W1_ckpt,
-                   float* b1_ckpt, void* saved, size_t saved_bytes, void* stream) {
+                   int F, int G, int dtype, int eta_rule, float eps, void* out, float* W1_last, float* b1_last,
+                   float* W1_ckpt, float* b1_ckpt, void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
+  if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   st = check_linear(NC, F);
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
@@ -122,17 +132,19 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   p.F = F;
   p.G = G;
   p.NK = (NC + G - 1) / G;
+  p.eta_rule = eta_rule;
   p.eps = eps;
   return hip_status(ttt::launch_linear_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
 int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                    const float* ln_b, const float* W1_ckpt, const float* W1_last, const void* dout, int B, int H,
-                   int NC, int K, int F, int G, int dtype, float eps, void* dXQ, void* dXK, void* dXV, void* deta,
-                   float* dW1, float* db1, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes,
-                   void* stream) {
+                   int NC, int K, int F, int G, int dtype, int eta_rule, float eps, void* dXQ, void* dXK,
+                   void* dXV, void* deta, float* dW1, float* db1, float* dln_w, float* dln_b, const void* saved,
+                   size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
+  if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   st = check_linear(NC, F);
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
@@ -181,19 +193,21 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   p.F = F;
   p.G = G;
   p.NK = (NC + G - 1) / G;
+  p.eta_rule = eta_rule;
   return hip_status(ttt::launch_linear_bwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
 int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                 const float* ln_b, const float* W1_init, const float* b1_init, const float* W2_init,
-                const float* b2_init, int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype, float eps,
-                void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last, float* W1_ckpt,
+                const float* b2_init, int B, int H, int NC, int K, int F, int FF, int G, int M, int dtype,
+                int eta_rule, float eps, void* out, float* W1_last, float* b1_last, float* W2_last, float* b2_last, float* W1_ckpt,
                 float* b1_ckpt, float* W2_ckpt, float* b2_ckpt, float* W1_memo, float* b1_memo, float* W2_memo,
                 float* b2_memo, void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
   if (st != TTT_OK) return st;
+  if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
   REQUIRE_PTR(XV);
@@ -215,7 +229,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   // checkpoints: W1's, and any of the other three beside it
   if (W1_ckpt == nullptr && (b1_ckpt || W2_ckpt || b2_ckpt)) return TTT_ERR_NULL;
   for (const float* q : {W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt}) OPTIONAL_PTR(q);
-  if (W1_memo != nullptr && (M < 1 || M > NC)) return TTT_ERR_ARG;
+  if (W1_memo != nullptr && M < 1) return TTT_ERR_ARG;
   if (saved != nullptr) {
     if (!aligned16(saved)) return TTT_ERR_ALIGN;
     if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
@@ -255,6 +269,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.NK = (NC + G - 1) / G;
   p.M = W1_memo != nullptr ? M : 1;
   p.NS = (NC + p.M - 1) / p.M;
+  p.eta_rule = eta_rule;
   p.eps = eps;
   return hip_status(ttt::launch_mlp_fwd(p, dtype, static_cast<hipStream_t>(stream)));
 }
@@ -275,13 +290,14 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
                 const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
                 const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
-                float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
+                int eta_rule, float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
                 float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes, void* workspace,
                 size_t workspace_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   st = check_mlp(NC, F, FF, dtype);
   if (st != TTT_OK) return st;
+  if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   (void)b1_ckpt;  // not read: the saved values carry the rest of the state
   (void)W2_ckpt;
   (void)b2_ckpt;
@@ -334,8 +350,49 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.FF = FF;
   p.G = G;
   p.NK = (NC + G - 1) / G;
+  p.eta_rule = eta_rule;
+  p.dx_max_polls = (int)g_mlp_bwd_poll_limit.load();
+  p.dx_fused = (int)g_mlp_bwd_fused.load();
   p.eps = eps;
   return hip_status(ttt::launch_mlp_bwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_set_option(int option, long long value) {
+  switch (option) {
+    case TTT_OPT_MLP_BWD_POLL_LIMIT:
+      if (value < 0 || value > 0x7fffffffLL) return TTT_ERR_ARG;
+      g_mlp_bwd_poll_limit.store(value);
+      return TTT_OK;
+    case TTT_OPT_MLP_BWD_FUSED:
+      if (value != 0 && value != 1) return TTT_ERR_ARG;
+      g_mlp_bwd_fused.store(value);
+      return TTT_OK;
+    default: return TTT_ERR_ARG;
+  }
+}
+
+long long ttt_get_option(int option) {
+  switch (option) {
+    case TTT_OPT_MLP_BWD_POLL_LIMIT: return g_mlp_bwd_poll_limit.load();
+    case TTT_OPT_MLP_BWD_FUSED: return g_mlp_bwd_fused.load();
+    default: return -1;
+  }
+}
+
+int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int H, int NC, int K, int F, int FF,
+                      int dtype, void* stream) {
+  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
+  const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
+  if (need == 0) return TTT_ERR_SHAPE;
+  if (workspace_bytes < need) return TTT_ERR_WORKSPACE;
+  // the timeout word: control word 1 behind the B*H*NC handoff slots
+  const int* ctrl = reinterpret_cast<const int*>(static_cast<const char*>(workspace) +
+                                                 (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype));
+  int word = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(&word, ctrl + 1, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess) return TTT_ERR_HIP;
+  if (hipStreamSynchronize(s) != hipSuccess) return TTT_ERR_HIP;
+  return word != 0 ? TTT_ERR_TIMEOUT : TTT_OK;
 }
 
 int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, const float* W2, const float* b2,
@@ -452,6 +509,134 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
   p.dXQW = dXQW;
   if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
   return hip_status(ttt::launch_mlp_memo(p, dtype, true, static_cast<hipStream_t>(stream)));
+}
+
+namespace {
+int check_layer_io(int B, int L, int H, int K, int F, int dtype) {
+  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
+  if (B <= 0 || L <= 0 || H <= 0) return TTT_ERR_SHAPE;
+  if (K != 16 || L % K != 0) return TTT_ERR_SHAPE;
+  if (F != 32 && F != 64) return TTT_ERR_SHAPE;
+  if ((long long)H * F > ttt::layer_io_max_width()) return TTT_ERR_SHAPE;
+  if ((long long)B * L > 0x7fffffffLL) return TTT_ERR_SHAPE;
+  return TTT_OK;
+}
+}  // namespace
+
+size_t ttt_layer_io_partial_bytes(int B, int L, int H, int F) {
+  if (B <= 0 || L <= 0 || H <= 0 || F <= 0) return 0;
+  return (size_t)ttt::layer_io_bwd_blocks(B, L) * 2 * H * F * sizeof(float);
+}
+
+int ttt_qkvu_producer_fwd(const void* proj, int ld, const float* rope, const float* ln_w, const float* ln_b, int B,
+                          int L, int H, int K, int F, float base_lr, float eps, int dtype, void* XQ, void* XK,
+                          void* XV, void* XU, float* lr, void* stream) {
+  int st = check_layer_io(B, L, H, K, F, dtype);
+  if (st != TTT_OK) return st;
+  if (ld < 4 * H * F + H || ld % 4 != 0) return TTT_ERR_SHAPE;
+  if (!(eps > 0.0f) || eps > 1.0f) return TTT_ERR_ARG;
+  const void* req[] = {proj, rope, ln_w, ln_b, XQ, XK, XV, XU, lr};
+  for (const void* q : req) REQUIRE_PTR(q);
+  ttt::ProducerParams p{};
+  p.proj = proj;
+  p.ld = ld;
+  p.rope = rope;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.XQ = XQ;
+  p.XK = XK;
+  p.XV = XV;
+  p.XU = XU;
+  p.lr = lr;
+  p.B = B;
+  p.L = L;
+  p.H = H;
+  p.F = F;
+  p.base_lr = base_lr;
+  p.eps = eps;
+  p.l2eps = 1e-12f;
+  return hip_status(ttt::launch_producer(p, dtype, false, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_qkvu_producer_bwd(const void* proj, int ld, const float* rope, const float* ln_w, const float* ln_b,
+                          const void* dXQ, const void* dXK, const void* dXV, const void* dXU, const float* dlr, int B,
+                          int L, int H, int K, int F, float base_lr, float eps, int dtype, void* dproj,
+                          float* partial, size_t partial_bytes, void* stream) {
+  int st = check_layer_io(B, L, H, K, F, dtype);
+  if (st != TTT_OK) return st;
+  if (ld < 4 * H * F + H || ld % 4 != 0) return TTT_ERR_SHAPE;
+  if (!(eps > 0.0f) || eps > 1.0f) return TTT_ERR_ARG;
+  const void* req[] = {proj, rope, ln_w, ln_b, dXQ, dXK, dXV, dXU, dproj};
+  for (const void* q : req) REQUIRE_PTR(q);
+  OPTIONAL_PTR(dlr);
+  if (partial == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(partial)) return TTT_ERR_ALIGN;
+  if (partial_bytes < ttt_layer_io_partial_bytes(B, L, H, F)) return TTT_ERR_WORKSPACE;
+  ttt::ProducerParams p{};
+  p.proj = proj;
+  p.ld = ld;
+  p.rope = rope;
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.dXQ = dXQ;
+  p.dXK = dXK;
+  p.dXV = dXV;
+  p.dXU = dXU;
+  p.dlr = dlr;
+  p.dproj = dproj;
+  p.partial = partial;
+  p.B = B;
+  p.L = L;
+  p.H = H;
+  p.F = F;
+  p.base_lr = base_lr;
+  p.eps = eps;
+  p.l2eps = 1e-12f;
+  return hip_status(ttt::launch_producer(p, dtype, true, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_post_norm_fwd(const void* XQW, const float* gamma, const float* beta, int B, int L, int H, int K, int F,
+                      float eps, int dtype, void* out, float* stats, void* stream) {
+  int st = check_layer_io(B, L, H, K, F, dtype);
+  if (st != TTT_OK) return st;
+  if (!(eps > 0.0f) || eps > 1.0f) return TTT_ERR_ARG;
+  const void* req[] = {XQW, gamma, beta, out, stats};
+  for (const void* q : req) REQUIRE_PTR(q);
+  ttt::PostNormParams p{};
+  p.X = XQW;
+  p.gamma = gamma;
+  p.beta = beta;
+  p.Y = out;
+  p.stats = stats;
+  p.B = B;
+  p.L = L;
+  p.H = H;
+  p.F = F;
+  p.eps = eps;
+  return hip_status(ttt::launch_post_norm(p, dtype, false, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_post_norm_bwd(const void* XQW, const float* gamma, const float* stats, const void* dout, int B, int L, int H,
+                      int K, int F, int dtype, void* dXQW, float* partial, size_t partial_bytes, void* stream) {
+  int st = check_layer_io(B, L, H, K, F, dtype);
+  if (st != TTT_OK) return st;
+  const void* req[] = {XQW, gamma, stats, dout, dXQW};
+  for (const void* q : req) REQUIRE_PTR(q);
+  if (partial == nullptr) return TTT_ERR_WORKSPACE;
+  if (!aligned16(partial)) return TTT_ERR_ALIGN;
+  if (partial_bytes < ttt_layer_io_partial_bytes(B, L, H, F)) return TTT_ERR_WORKSPACE;
+  ttt::PostNormParams p{};
+  p.X = XQW;
+  p.gamma = gamma;
+  p.stats = const_cast<float*>(stats);  // read only in the backward
+  p.dY = dout;
+  p.dX = dXQW;
+  p.partial = partial;
+  p.B = B;
+  p.L = L;
+  p.H = H;
+  p.F = F;
+  return hip_status(ttt::launch_post_norm(p, dtype, true, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

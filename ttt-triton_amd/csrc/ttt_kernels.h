@@ -15,6 +15,7 @@ struct LinearFwdParams {
   float *W_last, *b_last, *W_ckpt, *b_ckpt;
   void* saved;  // per mini-batch values for the backward, LinSavedSlot layout (may be null)
   int B, H, NC, F, G, NK;
+  int eta_rule;  // TTT_ETA_*: eta dense [NC][K][K] (activation type) or lr [NC][K] fp32
   float eps;
 };
 
@@ -25,6 +26,7 @@ struct LinearBwdParams {
   void *dXQ, *dXK, *dXV, *deta;
   float *dW, *db, *dln_w, *dln_b;
   int B, H, NC, F, G, NK;
+  int eta_rule;  // as the forward's; deta is then dlr [NC][K] fp32 unless dense
 };
 
 // What the TTT-Linear forward saves per mini-batch for the backward, one slot
@@ -58,6 +60,7 @@ struct MlpFwdParams {
   float *W1_memo, *b1_memo, *W2_memo, *b2_memo;
   void* saved;  // per mini-batch values for the backward, MlpSavedSlot layout (may be null)
   int B, H, NC, F, FF, G, NK, M, NS;
+  int eta_rule;  // TTT_ETA_*: eta dense [NC][K][K] (activation type) or lr [NC][K] fp32
   float eps;
 };
 
@@ -72,6 +75,9 @@ struct MlpBwdParams {
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   int B, H, NC, F, FF, G, NK;
+  int eta_rule;      // as the forward's; deta is then dlr [NC][K] fp32 unless dense
+  int dx_max_polls;  // fused dXQ/dXK workers: polls of a group flag before giving up
+  int dx_fused;      // 0: the dXQ/dXK pass is always a second launch
   float eps;
 };
 
@@ -161,6 +167,36 @@ hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream);
 size_t mlp_saved_slot_bytes(int F, int FF, int dtype);
 
 hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream);
+
+// Producer / consumer around the inner loop (ttt_layer_io.hip)
+struct ProducerParams {
+  const void* proj;  // [B*L][ld]: XQ | XK | XV | XU (H*F each) | H lr logits | padding
+  int ld;
+  const float *rope, *ln_w, *ln_b;  // rope [L][F/2][2] (cos, sin); ln [H][F]
+  void *XQ, *XK, *XV, *XU;          // [B,H,L,F] (= [B,H,NC,K,F])
+  float* lr;                        // [B,H,L]
+  const void *dXQ, *dXK, *dXV, *dXU;
+  const float* dlr;  // may be null
+  void* dproj;       // [B*L][ld]
+  float* partial;    // [blocks][2][H*F]: LN-parameter gradient partials
+  int B, L, H, F;
+  float base_lr, eps, l2eps;
+};
+struct PostNormParams {
+  const void* X;  // [B,H,L,F]
+  const float *gamma, *beta;
+  void* Y;        // [B,L,H*F]
+  float* stats;   // [B*L][2]: mean, 1/sigma
+  const void* dY;
+  void* dX;
+  float* partial;  // [blocks][2][H*F]
+  int B, L, H, F;
+  float eps;
+};
+hipError_t launch_producer(const ProducerParams& p, int dtype, bool bwd, hipStream_t stream);
+hipError_t launch_post_norm(const PostNormParams& p, int dtype, bool bwd, hipStream_t stream);
+int layer_io_bwd_blocks(int B, int L);
+int layer_io_max_width();
 
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t stream);

@@ -25,6 +25,7 @@
 //                operands; forms dXQ, dXK, dXV and deta and writes them.
 // Feature-major tiles ("FM": lane (g, n) holds features 16o + 4g + j of token
 // n) are what the outputs are written from, 4 contiguous elements per lane.
+#include "ttt_eta.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
@@ -64,12 +65,15 @@ template <typename T, int FT> struct LinBwdShared {
 template <typename T, int FT> struct LinBwdCtx {
   const T *XQ, *XK, *XV, *DO, *ETA;
   T *DXQ, *DXK, *DXV, *DETA;
+  const float* LRP;  // lr [NC][K] when eta is given as learning rates
+  float* DLR;        // dlr [NC][K] then
+  int eta_rule;
   const char* SV;  // this chain's saved slots
   int NC, G, NK, chain, h;
 };
 
 // ------------------------------------------------------------------ wave P
-template <typename T, int FT> struct WaveP {
+template <typename T, int FT, bool LR> struct WaveP {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
   using Slot = LinSavedSlot<F>;
@@ -82,6 +86,8 @@ template <typename T, int FT> struct WaveP {
   struct In {
     Frag<T> xq[1][FT], xk[1][FT], xv[FT], dof[FT];
     Frag<T> etaT, e;  // raw: converted where used, so the prefetch is not waited for
+    f4 lr4;           // LR: lr[4g .. 4g+3] and lr[n], expanded where used
+    float lrn;
     f4 G[FT], xhb[FT];
     float rsb;
   } in;
@@ -109,9 +115,14 @@ template <typename T, int FT> struct WaveP {
       in.xv[q] = load_frag(c.XV + xo, F, 16 * q);
       in.dof[q] = load_frag(c.DO + xo, F, 16 * q);
     }
-    const T* etas = c.ETA + (size_t)s * K * K;
-    in.etaT = load_frag(etas, K, 0);            // lane (g, n): eta[n][4g + j]
-    in.e = load_frag(etas + (K - 1) * K, 0, 0);  // eta[K-1][4g + j]
+    if constexpr (LR) {
+      in.lr4 = *reinterpret_cast<const f4*>(c.LRP + (size_t)s * K + 4 * g);
+      in.lrn = c.LRP[(size_t)s * K + n];
+    } else {
+      const T* etas = c.ETA + (size_t)s * K * K;
+      in.etaT = load_frag(etas, K, 0);            // lane (g, n): eta[n][4g + j]
+      in.e = load_frag(etas + (K - 1) * K, 0, 0);  // eta[K-1][4g + j]
+    }
     const float* sv = reinterpret_cast<const float*>(c.SV + (size_t)s * Slot::BYTES);
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
@@ -126,7 +137,8 @@ template <typename T, int FT> struct WaveP {
     load(s > 0 ? s - 1 : 0);  // unconditional, so that the wait for it is exact
     auto& ps = sh.ps[s & 1];
     auto& px = sh.px[m3];
-    const f4 etaT = frag_to_f4(x.etaT), e = frag_to_f4(x.e);
+    const f4 etaT = LR ? eta_rowfrag_from_lr(c.eta_rule, x.lr4) : frag_to_f4(x.etaT);
+    const f4 e = LR ? eta_lastrow_from_lr(x.lr4) : frag_to_f4(x.e);
 
     Frag<T> xqTf[FT], xkTf[FT];
 #pragma unroll
@@ -161,7 +173,8 @@ template <typename T, int FT> struct WaveP {
     a[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
     gemm<1, 1, FT>(at, x.xk, x.xq);
     gemm<1, 1, FT>(a, x.xq, x.xk);
-    const f4 eta_n = transpose16(x.etaT, I).v;  // lane (g, n): eta[4g + j][n]
+    // lane (g, n): eta[4g + j][n]
+    const f4 eta_n = LR ? eta_ctile_from_lr(c.eta_rule, x.lrn) : transpose16(x.etaT, I).v;
     f4 m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) m[j] = eta_n[j] * a[0][0].v[j] + eta_n[j];
@@ -409,7 +422,7 @@ template <typename T, int FT> struct WaveS {
 };
 
 // ------------------------------------------------------------------ wave X
-template <typename T, int FT> struct WaveX {
+template <typename T, int FT, bool LR> struct WaveX {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
   const LinearBwdParams& p;
@@ -488,11 +501,16 @@ template <typename T, int FT> struct WaveX {
     }
     f4 det = px.det[l];
     if (n == K - 1) det += sx.de[l];
-    store_f4(c.DETA + (size_t)s * K * K, K, 0, det);
+    if constexpr (LR) {
+      // dlr of columns 4g..4g+3: the 16 lanes of group g store the same value
+      *reinterpret_cast<f4*>(c.DLR + (size_t)s * K + 4 * g) = dlr_from_detaT(c.eta_rule, det);
+    } else {
+      store_f4(c.DETA + (size_t)s * K * K, K, 0, det);
+    }
   }
 };
 
-template <typename T, int FT>
+template <typename T, int FT, bool LR>
 __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
@@ -509,11 +527,14 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   c.XK = static_cast<const T*>(p.XK) + xoff;
   c.XV = static_cast<const T*>(p.XV) + xoff;
   c.DO = static_cast<const T*>(p.dout) + xoff;
-  c.ETA = static_cast<const T*>(p.eta) + eoff;
+  c.ETA = LR ? nullptr : static_cast<const T*>(p.eta) + eoff;
+  c.LRP = LR ? static_cast<const float*>(p.eta) + (size_t)c.chain * c.NC * K : nullptr;
+  c.DLR = LR ? static_cast<float*>(p.deta) + (size_t)c.chain * c.NC * K : nullptr;
+  c.eta_rule = p.eta_rule;
   c.DXQ = static_cast<T*>(p.dXQ) + xoff;
   c.DXK = static_cast<T*>(p.dXK) + xoff;
   c.DXV = static_cast<T*>(p.dXV) + xoff;
-  c.DETA = static_cast<T*>(p.deta) + eoff;
+  c.DETA = LR ? nullptr : static_cast<T*>(p.deta) + eoff;
   c.SV = static_cast<const char*>(p.saved) + (size_t)c.chain * c.NC * LinSavedSlot<F>::BYTES;
 
   // Every wave passes NC + 3 barriers: one per pipeline iteration, one before
@@ -523,7 +544,7 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NC = c.NC;
   if (wave == 0) {
-    WaveP<T, FT> w(p, c, sh);
+    WaveP<T, FT, LR> w(p, c, sh);
     w.load(NC - 1);
     __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it < NC + 2; ++it) {
@@ -545,7 +566,7 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
     __syncthreads();
     w.finish(p);
   } else {
-    WaveX<T, FT> w(p, c, sh);
+    WaveX<T, FT, LR> w(p, c, sh);
     w.load_w(w.WT, p.W_last + (size_t)c.chain * F * F);
     __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it < NC + 2; ++it) {
@@ -559,7 +580,10 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
 
 template <typename T, int FT>
 static hipError_t launch_bwd(const LinearBwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_bwd_kernel<T, FT>), dim3(p.B * p.H), dim3(192), 0, stream, p);
+  if (p.eta_rule == TTT_ETA_DENSE)
+    hipLaunchKernelGGL((linear_bwd_kernel<T, FT, false>), dim3(p.B * p.H), dim3(192), 0, stream, p);
+  else
+    hipLaunchKernelGGL((linear_bwd_kernel<T, FT, true>), dim3(p.B * p.H), dim3(192), 0, stream, p);
   return hipGetLastError();
 }
 

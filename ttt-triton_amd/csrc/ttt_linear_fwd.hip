@@ -26,7 +26,10 @@
 // (kernels/linear_forward.py:55-73 convention) and the final state to W_last.
 // With a saved buffer, every mini-batch's G, normalised Z1 and Zb and their
 // statistics go to its LinSavedSlot for the backward.
+#include <type_traits>
+
 #include "ttt_buf.h"
+#include "ttt_eta.h"
 #include "ttt_kernels.h"
 
 namespace ttt {
@@ -37,7 +40,7 @@ template <typename T, int FT> struct LinFwdHandoff {
   float b[16 * FT];                         // b entering the mini-batch
 };
 
-template <typename T, int FT>
+template <typename T, int FT, bool LR>
 __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
@@ -50,7 +53,12 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
   const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + (size_t)chain * NC * K * F;
   const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NC * K * F;
   const T* __restrict__ XV = static_cast<const T*>(p.XV) + (size_t)chain * NC * K * F;
-  const T* __restrict__ ETA = static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
+  // eta: dense [NC][K][K] blocks, or (LR) the learning rates lr [NC][K] fp32
+  // that the eta rule expands on chip; held raw until used
+  const T* __restrict__ ETA = LR ? nullptr : static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
+  const float* __restrict__ LRP = LR ? static_cast<const float*>(p.eta) + (size_t)chain * NC * K : nullptr;
+  using ERaw = std::conditional_t<LR, f4, Frag<T>>;
+  const int eta_rule = p.eta_rule;
   T* __restrict__ OUT = static_cast<T*>(p.out) + (size_t)chain * NC * K * F;
   using Slot = LinSavedSlot<F>;
   // Saved values go through a buffer resource whose size is zero when there is
@@ -82,7 +90,8 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
 
     // prefetched inputs of the next mini-batch (raw: converted where used, so
     // the prefetch is not waited for early)
-    Frag<T> nk[1][FT], nv[1][FT], n_e;
+    Frag<T> nk[1][FT], nv[1][FT];
+    ERaw n_e;
     auto load_step = [&](int s) {
       const T* k = XK + (size_t)s * K * F;
       const T* v = XV + (size_t)s * K * F;
@@ -91,7 +100,10 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
         nk[0][c] = load_frag(k, F, 16 * c);
         nv[0][c] = load_frag(v, F, 16 * c);
       }
-      n_e = load_frag(ETA + (size_t)s * K * K + (K - 1) * K, 0, 0);  // lane (g,*): eta[K-1][4g+j]
+      if constexpr (LR)
+        n_e = *reinterpret_cast<const f4*>(LRP + (size_t)s * K + 4 * g);  // lane (g,*): lr[4g+j]
+      else
+        n_e = load_frag(ETA + (size_t)s * K * K + (K - 1) * K, 0, 0);  // lane (g,*): eta[K-1][4g+j]
     };
     load_step(0);
     // Retire the first loads before the loop: with them pending on entry the
@@ -118,7 +130,7 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
         xk[0][c] = nk[0][c];
         xv[0][c] = nv[0][c];
       }
-      const Frag<T> e_raw = n_e;
+      const ERaw e_raw = n_e;
       if (s + 1 < NC) load_step(s + 1);
       LinFwdHandoff<T, FT>& hs = hand[s & 1];
 
@@ -205,7 +217,11 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
 
       // ---- state update: W -= XK^T diag(e) G ; b -= G^T e
       {
-        const f4 e = frag_to_f4(e_raw);
+        f4 e;
+        if constexpr (LR)
+          e = eta_lastrow_from_lr(e_raw);
+        else
+          e = frag_to_f4(e_raw);
         Frag<T> xkf[FT], ge[FT];
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
@@ -250,7 +266,8 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
         lnw_fm[o][j] = p.ln_w[h * F + 16 * o + 4 * g + j];
         lnb_fm[o][j] = p.ln_b[h * F + 16 * o + 4 * g + j];
       }
-    Frag<T> nq[1][FT], nk[1][FT], n_etaT;
+    Frag<T> nq[1][FT], nk[1][FT];
+    ERaw n_etaT;
     auto load_step = [&](int s) {
       const T* q = XQ + (size_t)s * K * F;
       const T* k = XK + (size_t)s * K * F;
@@ -259,7 +276,10 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
         nq[0][c] = load_frag(q, F, 16 * c);
         nk[0][c] = load_frag(k, F, 16 * c);
       }
-      n_etaT = load_frag(ETA + (size_t)s * K * K, K, 0);  // lane (g,n): eta[n][4g+j]
+      if constexpr (LR)
+        n_etaT = *reinterpret_cast<const f4*>(LRP + (size_t)s * K + 4 * g);  // lane (g,*): lr[4g+j]
+      else
+        n_etaT = load_frag(ETA + (size_t)s * K * K, K, 0);  // lane (g,n): eta[n][4g+j]
     };
     load_step(0);
     __builtin_amdgcn_s_waitcnt(0);
@@ -271,7 +291,7 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
         xq[0][c] = nq[0][c];
         xk[0][c] = nk[0][c];
       }
-      const Frag<T> etaT_raw = n_etaT;
+      const ERaw etaT_raw = n_etaT;
       if (s + 1 < NC) load_step(s + 1);
       __syncthreads();  // mini-batch s handed over
       const LinFwdHandoff<T, FT>& hs = hand[s & 1];
@@ -294,7 +314,11 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
       gemm<1, 1, FT>(at, xk, xq);
       {
         f4 mt;
-        const f4 etaT = frag_to_f4(etaT_raw);
+        f4 etaT;
+        if constexpr (LR)
+          etaT = eta_rowfrag_from_lr(eta_rule, etaT_raw);
+        else
+          etaT = frag_to_f4(etaT_raw);
 #pragma unroll
         for (int j = 0; j < 4; ++j) mt[j] = etaT[j] * at[0][0].v[j] + etaT[j];
         const Frag<T> mtf = to_frag<T>(mt);
@@ -343,7 +367,10 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
 
 template <typename T, int FT>
 static hipError_t launch_fwd(const LinearFwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_fwd_kernel<T, FT>), dim3(p.B * p.H), dim3(128), 0, stream, p);
+  if (p.eta_rule == TTT_ETA_DENSE)
+    hipLaunchKernelGGL((linear_fwd_kernel<T, FT, false>), dim3(p.B * p.H), dim3(128), 0, stream, p);
+  else
+    hipLaunchKernelGGL((linear_fwd_kernel<T, FT, true>), dim3(p.B * p.H), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 

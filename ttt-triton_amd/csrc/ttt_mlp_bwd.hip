@@ -37,6 +37,7 @@
 // folds into dZ1, dG1 into dP and dZ1, the -e Q2 share straight into the
 // exchange area) so that the loop runs without spilling.
 #include "ttt_buf.h"
+#include "ttt_eta.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
@@ -72,12 +73,8 @@ size_t mlp_bwd_ctrl_bytes(int B, int H, int NC, int G) {
   return (words * 4 + 255) & ~(size_t)255;
 }
 
-// Polls of a group flag before a worker gives up (s_sleep 8 between polls:
-// about a second, against ~2 ms for a whole sweep).
-constexpr int kDxMaxPolls = 1 << 22;
-
 template <typename T, int FT, int NW>
-__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk);
+__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk, bool poison);
 
 // Fused mode: workgroups B*H.. of the sweep's launch.  Each takes (chain,
 // checkpoint group) tasks in the order the sweep finishes them (last group
@@ -85,8 +82,12 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
 // that group's dXQ/dXK (mlp_bwd_dx_body, wave = feature tile).  Blocks are
 // dispatched in index order, so a worker only becomes resident after every
 // sweep workgroup has; the sweeps never wait for the workers, so every wait
-// ends (and a wait that exceeds kDxMaxPolls raises the timeout word instead
-// of spinning on).
+// ends.  Should that ordering not hold, a wait that exceeds p.dx_max_polls
+// polls (s_sleep 8 between polls; the default, 2^22, is about a second
+// against ~2 ms for a whole sweep) gives up: the worker raises the timeout
+// word and writes NaN into that group's dXQ and dXK rows instead of reading a
+// handoff that was never published, so the failure is visible in the output
+// and through ttt_mlp_bwd_check, never silent.
 //
 // Visibility across XCDs without cache maintenance: the sweep writes the
 // handoff with device-coherent (sc1, written-through) stores, waits for them
@@ -96,7 +97,7 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
 // serves.  Neither side writes back or invalidates a whole L2.
 template <typename T, int FT, int NW>
 __device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
-  __shared__ int task_sh;
+  __shared__ int task_sh, gave_up_sh;
   const int nchain = p.B * p.H, ntask = nchain * p.NK;
   int* __restrict__ flags = p.dx_ctrl + kDxCtrlHead;
   for (;;) {
@@ -107,21 +108,24 @@ __device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
     if (t >= ntask) return;
     const int kk = p.NK - 1 - t / nchain, chain = t - (t / nchain) * nchain;
     if (threadIdx.x == 0) {
-      int polls = 0;
+      int polls = 0, gave_up = 0;
       while (__hip_atomic_load(flags + chain * p.NK + kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-        if (++polls > kDxMaxPolls) {
+        if (++polls > p.dx_max_polls) {
           __hip_atomic_store(p.dx_ctrl + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          gave_up = 1;
           break;
         }
         __builtin_amdgcn_s_sleep(8);
       }
+      gave_up_sh = gave_up;
     }
-    __syncthreads();  // the group's flag was seen: its handoff stores are complete
-    mlp_bwd_dx_body<T, FT, NW>(p, chain, kk);
+    __syncthreads();  // the group's flag was seen (its handoff stores are complete), or the wait gave up
+    const bool poison = gave_up_sh != 0;
+    mlp_bwd_dx_body<T, FT, NW>(p, chain, kk, poison);
   }
 }
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, bool LR>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   if constexpr (NW == FT) {
     if ((int)blockIdx.x >= p.B * p.H) {
@@ -153,9 +157,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
   const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
   const rsrc_t rDO = make_rsrc(static_cast<const T*>(p.dout) + xoff, xbytes);
-  const rsrc_t rET = make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+  // eta and its gradient: dense [NC][K][K] blocks, or (LR) lr and dlr [NC][K] fp32
+  const unsigned lbytes = (unsigned)(NC * K * 4);
+  const rsrc_t rET = LR ? make_rsrc(static_cast<const float*>(p.eta) + (size_t)chain * NC * K, lbytes)
+                        : make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
   const rsrc_t rDXV = make_rsrc(static_cast<T*>(p.dXV) + xoff, xbytes);
-  const rsrc_t rDET = make_rsrc(static_cast<T*>(p.deta) + eoff, ebytes);
+  const rsrc_t rDET = LR ? make_rsrc(static_cast<float*>(p.deta) + (size_t)chain * NC * K, lbytes)
+                         : make_rsrc(static_cast<T*>(p.deta) + eoff, ebytes);
+  const int eta_rule = p.eta_rule;
   const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
   const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
   const int en = (4 * g * K + n) * ST;        // eta[4g + j][n]: + j * K * ST
@@ -296,8 +305,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       // rebuild so that it hides their latency
       // (eta raw: converted where first used, so that the conversion does not
       // wait for the load here)
-      const Frag<T> etaT_r = bload_frag<T>(rET, el, es(s));      // [t_k x t_q]: eta[n][4g+j]
-      const Frag<T> etan_r = bload_ctile<T>(rET, en, es(s), K);  // [t_q x t_k]: eta[4g+j][n]
+      // dense: eta[n][4g+j] ([t_k x t_q]) and eta[4g+j][n] ([t_q x t_k]);
+      // LR: lr[4g .. 4g+3] and lr[n]
+      Frag<T> etaT_r, etan_r;
+      f4 lr4;
+      float lrn;
+      if constexpr (LR) {
+        lr4 = bload_frag<float>(rET, 16 * g, s * K * 4).v;
+        lrn = bload_f32(rET, 4 * n, s * K * 4);
+      } else {
+        etaT_r = bload_frag<T>(rET, el, es(s));
+        etan_r = bload_ctile<T>(rET, en, es(s), K);
+      }
       // dout of this wave's feature tile for B3 (one tile per wave when NW >= FT)
       const Frag<T> dob = bload_frag<T>(rDO, xl + 16 * (wave % FT) * ST, xs(s));
       const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
@@ -402,7 +421,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
         }
       }
-      const f4 etaT = frag_to_f4(etaT_r), eta_n = frag_to_f4(etan_r);
+      const f4 etaT = LR ? eta_rowfrag_from_lr(eta_rule, lr4) : frag_to_f4(etaT_r);
+      const f4 eta_n = LR ? eta_ctile_from_lr(eta_rule, lrn) : frag_to_f4(etan_r);
       // dN2 = -dZ2b G2^T (both layouts): deta part, dA2
       f4 detT, dA2T, dA2;
       Frag<T> m2f;  // -(eta o A2 + eta) for wave 0, zero for the others
@@ -504,7 +524,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       // ---- Q: dG1 = -M1^T dZ1b - e (XK dW1' + db1'), then at once
       //      dP = dG1 (.) gelu'(Z1) and dZ1 = dG1 (.) Pm gelu''(Z1) + dX2 (.) gelu'(Z1)
       //      (the dZ2 W2^T part of dX2 is added after the inner-loss backward)
-      const f4 e = frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+      const f4 e = LR ? eta_lastrow_from_lr(bload_frag<float>(rET, 16 * g, s * K * 4).v)
+                      : frag_to_f4(bload_frag<T>(rET, e4, es(s)));
       Tile dZ1[HT];
       Frag<T> dPf[HT], dPF[HT];
       f4 dep = f4{0.f, 0.f, 0.f, 0.f};  // eta-row gradient partial (G1 . Q1 + G2 . Q2)
@@ -628,7 +649,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) detT[j] -= de[j];
         }
-        bstore_frag<T>(rDET, keep_or_drop(el, wave == 0), es(s), to_frag<T>(detT));
+        if constexpr (LR) {
+          // dlr of columns 4g..4g+3: lane n == 0 of each group stores
+          const f4 dl = dlr_from_detaT(eta_rule, detT);
+          bstore_frag<float>(rDET, keep_or_drop(16 * g, wave == 0 && n == 0), s * K * 4, Frag<float>{dl});
+        } else {
+          bstore_frag<T>(rDET, keep_or_drop(el, wave == 0), es(s), to_frag<T>(detT));
+        }
       }
       __syncthreads();  // (1x) exchange area free
       pin_dW();
@@ -809,9 +836,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 // sweep's handoff.  One wave per (chain, checkpoint group, feature tile c):
 // W1_s^T[:, c] (FF/16 tiles [16 hidden x 16 features]) starts from the group's
 // checkpoint and steps forward with the saved update operands,
-// W1_{s+1}^T = W1_s^T + (-e G1_s)^T XK_s.
+// W1_{s+1}^T = W1_s^T + (-e G1_s)^T XK_s.  With `poison` (a fused worker
+// that gave up waiting for the group) the group's rows get NaN instead.
 template <typename T, int FT, int NW>
-__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk) {
+__device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk, bool poison) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   constexpr int FF = 64 * NW;
@@ -835,6 +863,16 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
   const int xcl = (4 * g * F + n) * ST + 16 * c * ST;  // C-layout tile of feature tile c in a [16 x F] block
   const int hl = l * 4 * ST;                           // + hb * 256 * ST: hidden block hb, lane order
   const int f4l = l * 16 + c * 1024;                   // fp32 tile c, lane order
+  const int s0 = kk * G, s1 = min(s0 + G, NC);
+  if (poison) {
+    const float qnan = __builtin_nanf("");
+    const Frag<T> bad = to_frag<T>(f4{qnan, qnan, qnan, qnan});
+    for (int s = s0; s < s1; ++s) {
+      bstore_ctile<T>(rDXQ, xcl, s * K * F * ST, F, bad);
+      bstore_ctile<T>(rDXK, xcl, s * K * F * ST, F, bad);
+    }
+    return;
+  }
 
   // W1^T tiles [hidden block hb x feature tile c]: lane (g, n) holds
   // W1[16c + n][16 hb + 4g + j], one 16-byte read per tile from the [F][FF] checkpoint
@@ -860,7 +898,6 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
       in.zk[hb] = bload_frag_dev<T>(rWS, hl + hb * 256 * ST, ws_ + WS::DZ1F);
     }
   };
-  const int s0 = kk * G, s1 = min(s0 + G, NC);
   In cur;
   load_in(s0, cur);
   // retire the loads issued so far: pending on loop entry, they make the
@@ -898,7 +935,7 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
 template <typename T, int FT, int NW>
 __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
   const int chain = blockIdx.x / p.NK, kk = blockIdx.x - chain * p.NK;
-  mlp_bwd_dx_body<T, FT, NW>(p, chain, kk);
+  mlp_bwd_dx_body<T, FT, NW>(p, chain, kk, false);
 }
 
 __global__ void mlp_bwd_ctrl_clear_kernel(int* ctrl, int n) {
@@ -921,34 +958,42 @@ static int device_cus() {
 // Fused when the workgroups are alike (one wave per 64 hidden units = one per
 // feature tile) and every chain's sweep fits on the device at once with CUs to
 // spare for workers; otherwise the dXQ/dXK pass is a second launch.
-template <typename T, int FT, int NW>
+// The control words are cleared in both modes, so that the timeout word read
+// by ttt_mlp_bwd_check always belongs to this call.
+template <typename T, int FT, int NW, bool LR>
 static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   const int chains = p.B * p.H, cus = device_cus();
-  const bool fused = NW == FT && p.dx_ctrl != nullptr && cus >= chains + 16;
+  const bool fused = NW == FT && p.dx_fused != 0 && p.dx_ctrl != nullptr && cus >= chains + 16;
+  const int nctrl = fused ? kDxCtrlHead + chains * p.NK : kDxCtrlHead;
+  hipLaunchKernelGGL(mlp_bwd_ctrl_clear_kernel, dim3((nctrl + 255) / 256), dim3(256), 0, stream, p.dx_ctrl, nctrl);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   if (!fused) {
     p.dx_ctrl = nullptr;
-    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(chains), dim3(64 * NW), 0, stream, p);
-    hipError_t e = hipGetLastError();
+    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, LR>), dim3(chains), dim3(64 * NW), 0, stream, p);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW>), dim3(chains * p.NK), dim3(64 * FT), 0, stream, p);
     return hipGetLastError();
   }
-  const int nctrl = kDxCtrlHead + chains * p.NK;
-  hipLaunchKernelGGL(mlp_bwd_ctrl_clear_kernel, dim3((nctrl + 255) / 256), dim3(256), 0, stream, p.dx_ctrl, nctrl);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   // the sweeps, then one worker per CU: the first cus - chains run beside the
   // sweeps, the rest start on the CUs the sweeps leave
-  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
+  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, LR>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
+}
+
+template <typename T, int FT, int NW>
+static hipError_t launch_mlp_bwd_e(const MlpBwdParams& p, hipStream_t stream) {
+  return p.eta_rule == TTT_ETA_DENSE ? launch_mlp_bwd_t<T, FT, NW, false>(p, stream)
+                                     : launch_mlp_bwd_t<T, FT, NW, true>(p, stream);
 }
 
 template <typename T, int FT>
 static hipError_t launch_mlp_bwd_f(const MlpBwdParams& p, hipStream_t stream) {
   switch (p.FF) {
-    case 64: return launch_mlp_bwd_t<T, FT, 1>(p, stream);
-    case 128: return launch_mlp_bwd_t<T, FT, 2>(p, stream);
-    case 256: return launch_mlp_bwd_t<T, FT, 4>(p, stream);
+    case 64: return launch_mlp_bwd_e<T, FT, 1>(p, stream);
+    case 128: return launch_mlp_bwd_e<T, FT, 2>(p, stream);
+    case 256: return launch_mlp_bwd_e<T, FT, 4>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -25,11 +25,15 @@
 // there (MlpSavedSlot layout): the backward rebuilds the state in reverse
 // from the update operands and never re-runs the forward.
 //
+// eta is read per mini-batch either as the dense [K x K] block or, with LR,
+// as the K learning rates that the eta rule expands on chip (ttt_eta.h).
+//
 // Slabs are read through buffer resources; the next mini-batch's XQ and XK
 // are requested right after the first barrier of the current one, before its
 // stores (gfx9 retires loads and stores in issue order), so they arrive while
 // the rest of the mini-batch computes.
 #include "ttt_buf.h"
+#include "ttt_eta.h"
 #include "ttt_kernels.h"
 #include "ttt_ln.h"
 
@@ -53,7 +57,7 @@ template <int FT, int NW> struct MlpFwdShared {
 // rows instead of 16; G2 is then exchanged through LDS.
 template <int FT, int NW> constexpr bool kLnRowSplit = (NW == 4 && FT == 4);
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, bool LR>
 __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
@@ -77,7 +81,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const rsrc_t rXQ = make_rsrc(static_cast<const T*>(p.XQ) + xoff, xbytes);
   const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
   const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
-  const rsrc_t rET = make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+  const rsrc_t rET = LR ? make_rsrc(static_cast<const float*>(p.eta) + (size_t)chain * NC * K, NC * K * 4)
+                        : make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+  const int eta_rule = p.eta_rule;
   const rsrc_t rOUT = make_rsrc(static_cast<T*>(p.out) + xoff, xbytes);
   const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
   const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
@@ -183,8 +189,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
       for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
     }
-    const Frag<T> etaTf = bload_frag<T>(rET, el, eo);  // [t_k x t_q]: eta[n][4g+j]
-    const Frag<T> ef = bload_frag<T>(rET, e4, eo);     // last eta row
+    // dense: eta[n][4g+j] ([t_k x t_q]) and the last eta row; LR: lr[4g .. 4g+3]
+    Frag<T> etaTf, ef;
+    f4 lr4;
+    if constexpr (LR) {
+      lr4 = bload_frag<float>(rET, 16 * g, s * K * 4).v;
+    } else {
+      etaTf = bload_frag<T>(rET, el, eo);
+      ef = bload_frag<T>(rET, e4, eo);
+    }
 
     // ---- layer 1 on this wave's hidden units (token-major)
     Frag<T> x2f[HT];     // token-major frags of X2 (free = hidden, k = t)
@@ -324,7 +337,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     }
 
     // ---- readout layer 1: Z1b = XQ W1 - (eta o A1 + eta) G1 + b1, X2b = gelu(Z1b)
-    const f4 etaT = frag_to_f4(etaTf);
+    const f4 etaT = LR ? eta_rowfrag_from_lr(eta_rule, lr4) : frag_to_f4(etaTf);
     Frag<T> x2bF[1][HT];
     {
       Tile at[1][1];
@@ -365,7 +378,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       for (int o = 0; o < FT; ++o) sh.z2bp[wave][o][l] = z2bp[0][o].v;
       sh.a2p[wave][l] = a2p[0][0].v;
     }
-    const f4 e = frag_to_f4(ef);
+    const f4 e = LR ? eta_lastrow_from_lr(lr4) : frag_to_f4(ef);
 
     // ---- state update (the readout above used the state entering s)
     float b2_old[FT];
@@ -517,7 +530,10 @@ static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
   static_assert(MlpSavedSlot<16 * FT, 64 * NW, (int)sizeof(T)>::BYTES ==
                     (int)mlp_saved_slot_bytes_of(16 * FT, 64 * NW, (int)sizeof(T)),
                 "saved slot layout");
-  hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+  if (p.eta_rule == TTT_ETA_DENSE)
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, false>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+  else
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, true>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -11,6 +11,7 @@ W2 [B,H,FF,F], b2 [B,H,1,F]; memo snapshots [B,H,NS,...] fp32."""
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
@@ -19,12 +20,16 @@ from ._common import as_act, check_device, dtype_code, ptr, stream_of
 
 LN_EPS = 1e-8  # ops/ttt_utils.py:4,21
 
+# With TTT_AMD_CHECK=1 every backward waits for its launch and raises if a
+# fused dXQ/dXK worker gave up waiting (its rows are then NaN).
+CHECK_BWD = os.environ.get("TTT_AMD_CHECK", "0") not in ("", "0")
+
 
 def _f32(t):
     return t.detach().to(torch.float32).contiguous()
 
 
-def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
+def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, rule=_lib.ETA_DENSE):
     if XQ.dim() != 5:
         raise ValueError(f"XQ must be [B,H,NC,K,F], got {tuple(XQ.shape)}")
     B, H, NC, K, F = XQ.shape
@@ -32,8 +37,10 @@ def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
     for name, t in (("XK", XK), ("XV", XV)):
         if tuple(t.shape) != (B, H, NC, K, F):
             raise ValueError(f"{name} shape {tuple(t.shape)} != XQ shape {tuple(XQ.shape)}")
-    if tuple(eta.shape) != (B, H, NC, K, K):
+    if rule == _lib.ETA_DENSE and tuple(eta.shape) != (B, H, NC, K, K):
         raise ValueError(f"eta must be [B,H,NC,K,K]={(B, H, NC, K, K)}, got {tuple(eta.shape)}")
+    if rule != _lib.ETA_DENSE and tuple(eta.shape) != (B, H, NC, K):
+        raise ValueError(f"lr must be [B,H,NC,K]={(B, H, NC, K)}, got {tuple(eta.shape)}")
     # mlp_triton.py:91-94
     if tuple(W1.shape) != (B, H, F, FF):
         raise ValueError(f"W1 must be [B,H,F,FF]={(B, H, F, FF)}, got {tuple(W1.shape)}")
@@ -50,21 +57,26 @@ def _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta):
 
 def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0, eps: float = LN_EPS,
                 want_ckpt: bool = True, want_last: bool = False, want_saved: bool = False,
-                ckpt_w1_only: bool = False):
-    """Run the forward kernel.  Returns (out [B,H,NC,K,F] in XQ.dtype,
+                ckpt_w1_only: bool = False, eta_rule="dense"):
+    """Run the forward kernel.  `eta` is the dense [B,H,NC,K,K] tensor
+    (eta_rule "dense") or the learning rates lr [B,H,NC,K] that the kernel
+    expands by eta_rule "layer" (lr[j]/K in every row) or "causal"
+    (lr[j]/(i+1) for j <= i).  Returns (out [B,H,NC,K,F] in XQ.dtype,
     ckpt (W1,b1,W2,b2) or None, memo (W1,b1,W2,b2) or None, last or None,
     saved or None).  ckpt, last and saved are what mlp_backward needs: the
     checkpoints every G mini-batches, the final state, and each mini-batch's
     state-update operands and activations (a flat uint8 buffer of
     ttt_mlp_saved_bytes).  The backward reads only W1's checkpoints: with
     ckpt_w1_only the other three are neither allocated nor written (None)."""
-    B, H, NC, K, F, FF = _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta)
+    rule = _lib.eta_rule_code(eta_rule)
+    B, H, NC, K, F, FF = _check_shapes(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, rule)
     dev = check_device(XQ, XK, XV, eta, W1, b1, W2, b2, ln_w, ln_b)
     mp = XQ.dtype
     code = dtype_code(mp)
     G = int(G)
     NK = math.ceil(NC / G)
-    xq, xk, xv, et = (as_act(t, mp) for t in (XQ, XK, XV, eta))
+    xq, xk, xv = (as_act(t, mp) for t in (XQ, XK, XV))
+    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else _f32(eta)
     w1, bb1, w2, bb2, lw, lb = (_f32(t) for t in (W1, b1, W2, b2, ln_w, ln_b))
     out = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
 
@@ -88,7 +100,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_fwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb1), ptr(w2), ptr(bb2),
-            B, H, NC, K, F, FF, G, int(M) if M else 0, code, float(eps), ptr(out),
+            B, H, NC, K, F, FF, G, int(M) if M else 0, code, rule, float(eps), ptr(out),
             *(tuple(ptr(t) for t in last) if last else none4),
             *(tuple(ptr(t) if t is not None else None for t in ck) if ck else none4),
             *(tuple(ptr(t) for t in memo) if memo else none4),
@@ -99,19 +111,23 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
 
 
 def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, eps: float = LN_EPS,
-                 workspace=None):
+                 workspace=None, eta_rule="dense", check_timeout=None):
     """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints, last =
     the final state and saved = the saved buffer, all from one mlp_forward
-    call with the same G.  `workspace` (uint8, at least
+    call with the same G and eta form.  `workspace` (uint8, at least
     ttt_mlp_bwd_workspace_bytes) is allocated here when not given.  Returns
     fp32 (dln_w [H,F], dln_b [H,F], dW1, db1, dW2, db2) and (dXQ, dXV, dXK,
-    deta) in XQ.dtype."""
+    deta) in XQ.dtype, deta being dlr [B,H,NC,K] fp32 for an lr eta rule.
+    With check_timeout (default: TTT_AMD_CHECK set) the call waits for the
+    launch and raises TTTError if a fused dXQ/dXK worker gave up waiting."""
+    rule = _lib.eta_rule_code(eta_rule)
     B, H, NC, K, F = XQ.shape
     FF = ckpt[0].shape[-1]
     dev = check_device(XQ, XK, XV, eta, dout, *(t for t in ckpt if t is not None), *last, saved)
     mp = XQ.dtype
     code = dtype_code(mp)
-    xq, xk, xv, et, do = (as_act(t, mp) for t in (XQ, XK, XV, eta, dout))
+    xq, xk, xv, do = (as_act(t, mp) for t in (XQ, XK, XV, dout))
+    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else _f32(eta)
     lw, lb = _f32(ln_w), _f32(ln_b)
     dxq, dxk, dxv = torch.empty_like(xq), torch.empty_like(xq), torch.empty_like(xq)
     deta = torch.empty_like(et)
@@ -127,32 +143,45 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb),
             *(ptr(t) if t is not None else None for t in ckpt),
             *(ptr(t) for t in last), ptr(do),
-            B, H, NC, K, F, FF, int(G), code, float(eps),
+            B, H, NC, K, F, FF, int(G), code, rule, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
             ptr(saved), saved.numel(), ptr(ws), ws.numel(), stream_of(dev))
     _lib.check(st, "ttt_mlp_bwd")
+    if CHECK_BWD if check_timeout is None else check_timeout:
+        _lib.check(mlp_bwd_status(ws, B, H, NC, K, F, FF, code), "ttt_mlp_bwd")
     return (dlw.sum(0), dlb.sum(0), dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
+
+
+def mlp_bwd_status(workspace, B, H, NC, K, F, FF, code) -> int:
+    """ttt_mlp_bwd_check on the workspace of the last backward that used it
+    (waits for the current stream): 0, or the timeout status."""
+    dev = workspace.device
+    with torch.cuda.device(dev):
+        return _lib.load().ttt_mlp_bwd_check(ptr(workspace), workspace.numel(), B, H, NC, K, F, FF, code,
+                                             stream_of(dev))
 
 
 class TTTMLPFunction(torch.autograd.Function):
     """autograd Function with TritonMLP's signature (mlp_triton.py:15-69):
     apply(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, checkpoint_group_size,
     memo_segment_size[, eps]) -> (XQW [B,H,NC,K,F] in XQ.dtype, W1_memo, b1_memo,
-    W2_memo, b2_memo); the memo snapshots are fp32 and non-differentiable."""
+    W2_memo, b2_memo); the memo snapshots are fp32 and non-differentiable.
+    An optional last argument `eta_rule` ("layer" or "causal") makes eta_batch
+    the learning rates lr [B,H,NC,K] expanded on chip (its gradient is dlr)."""
 
     @staticmethod
     def forward(ctx, ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init, XQ_batch, XV_batch,
-                XK_batch, eta_batch, checkpoint_group_size, memo_segment_size, eps=LN_EPS):
+                XK_batch, eta_batch, checkpoint_group_size, memo_segment_size, eps=LN_EPS, eta_rule="dense"):
         NC = XQ_batch.shape[2]
         G = min(max(int(checkpoint_group_size), 1), NC)
         M = int(memo_segment_size)
         out, ck, memo, last, saved = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
                                                XQ_batch, XV_batch, XK_batch, eta_batch, G, M=M, eps=eps,
                                                want_ckpt=True, want_last=True, want_saved=True,
-                                               ckpt_w1_only=True)
+                                               ckpt_w1_only=True, eta_rule=eta_rule)
         ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck, *last,
                               saved)
-        ctx.G, ctx.eps = G, eps
+        ctx.G, ctx.eps, ctx.eta_rule = G, eps, eta_rule
         ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype, W2_init.dtype,
                       b2_init.dtype, XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
         if memo is None:
@@ -165,10 +194,10 @@ class TTTMLPFunction(torch.autograd.Function):
         XQ, XV, XK, eta, lw, lb = ctx.saved_tensors[:6]
         ck, last, saved = ctx.saved_tensors[6:10], ctx.saved_tensors[10:14], ctx.saved_tensors[14]
         (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
-            lw, lb, XQ, XV, XK, eta, ck, last, saved, grad_out, ctx.G, ctx.eps)
+            lw, lb, XQ, XV, XK, eta, ck, last, saved, grad_out, ctx.G, ctx.eps, eta_rule=ctx.eta_rule)
         grads = (dlw, dlb, dW1, db1, dW2, db2, dxq, dxv, dxk, deta)
         grads = tuple(gr.to(dt) for gr, dt in zip(grads, ctx.dtypes))
-        return grads + (None, None, None)
+        return grads + (None, None, None, None)
 
 
 READOUT_EPS = 1e-6  # kernels/mlp_cached_readout.py:98

@@ -1,0 +1,234 @@
+"""The TTT layer stack and forecaster on the HIP path: the caller side of the
+inner loop, as TTTForecaster / TTTWrapper / TTTMLP / TTTLinear use it
+(forecast.py:79-99, ttt_layer.py:20-565), built on this package's kernels.
+
+Per layer call, for hidden states x [B, L, D] (D = H*F):
+  1. one projection GEMM x @ [Wq; Wk; Wv; Wu; w_lr]^T + [bq; bk; bv; bu; b_lr]
+     (hipBLASLt through torch), the H lr-gate logits padded to an aligned row
+     width (ttt_layer.py:141-148, 151-163);
+  2. ProducerFunction: L2 norm, RoPE, reconstruction target and lr, written
+     in the inner loop's [B,H,NC,K,F] / [B,H,NC,K] layouts (ttt_layer.py:261-309);
+  3. the inner loop with eta expanded on chip from lr by the layer's rule
+     eta[i][j] = lr[j]/K (ttt_layer.py:309): TTTMLPFunction (+ the memory-cache
+     combiner, ttt_layer.py:453-565) or TTTLinearFunction (:383-421);
+  4. PostNormFunction (permute + reshape + post_norm, ttt_layer.py:349,
+     563-564) and the `wo` GEMM (:350).
+
+Parameter names and shapes are the reference's (wq ... wu, wo,
+learnable_ttt_lr_weight [H,1,D], learnable_ttt_lr_bias [H,1],
+ttt_norm_weight/bias [H,F], post_norm, W1/b1/W2/b2), so a reference state
+dict loads unchanged; the inner loop needs K = 16 and F in {32, 64}, and the
+MLP's hidden width (F, as TTTMLP builds it) in {64, 128, 256}."""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+import torch.nn.functional as Fn
+from torch import nn
+
+from .layer_io import POST_NORM_EPS, RECON_EPS, PostNormFunction, ProducerFunction, rope_table
+from .linear import TTTLinearFunction
+from .memo import mlp_memo_combine
+from .mlp import LN_EPS, TTTMLPFunction
+
+
+@dataclass
+class ModelConfig:
+    """forecast.py:31-64 (the fields the layer and forecaster read)."""
+    seq_len: int = 384
+    model_dim: int = 128
+    num_heads: int = 4
+    num_layers: int = 1
+    ssm_layer: str = "ttt_linear"
+    layer_norm_eps: float = 1e-6
+    mini_batch_size: int = 64
+    ttt_base_lr: float = 0.1
+    mem_cache_segment_n_mini_batches: int = 2
+    mem_cache_max_segments: int = 4
+    rope_theta: float = 10000.0
+    scan_checkpoint_group_size: int = 16
+    latent_height: int = 1
+    latent_width: int = 1
+    theta: float = 10000.0
+    compressed_num_frames: Optional[int] = None
+
+    def __post_init__(self):
+        if self.compressed_num_frames is None:
+            self.compressed_num_frames = self.seq_len
+        if self.model_dim % self.num_heads:
+            raise ValueError("model_dim must be a multiple of num_heads")
+        if self.seq_len % self.mini_batch_size:
+            raise ValueError("seq_len must be a multiple of mini_batch_size")
+        if (self.model_dim // self.num_heads) % 2:
+            raise ValueError("RoPE needs an even head dim")
+
+
+class TTTLayerBase(nn.Module):
+    """Projections, lr gate, TTT LayerNorm, post-norm and output projection
+    (TTTBase, ttt_layer.py:60-139), with the fused producer/consumer."""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.config = config
+        self.width = config.model_dim
+        self.num_heads = config.num_heads
+        self.head_dim = config.model_dim // config.num_heads
+        self.mini_batch_size = config.mini_batch_size
+        self.ttt_base_lr = config.ttt_base_lr
+        self.scan_checkpoint_group_size = config.scan_checkpoint_group_size
+        D, H, F = self.width, self.num_heads, self.head_dim
+        self.wq = nn.Linear(D, H * F, bias=True)
+        self.wk = nn.Linear(D, H * F, bias=True)
+        self.wv = nn.Linear(D, H * F, bias=True)
+        self.wo = nn.Linear(D, H * F, bias=True)
+        self.wu = nn.Linear(D, H * F, bias=True)
+        self.learnable_ttt_lr_weight = nn.Parameter(torch.normal(0, 0.02, size=(H, 1, D)))
+        self.learnable_ttt_lr_bias = nn.Parameter(torch.zeros(H, 1))
+        self.ttt_norm_weight = nn.Parameter(torch.ones(H, F))
+        self.ttt_norm_bias = nn.Parameter(torch.zeros(H, F))
+        self.post_norm = nn.LayerNorm(D, eps=1e-6)
+
+    def init_weights(self):
+        """ttt_layer.py:81-89"""
+        for lin in (self.wq, self.wk, self.wv, self.wo, self.wu):
+            nn.init.normal_(lin.weight, mean=0.0, std=0.02)
+        self.post_norm.reset_parameters()
+        nn.init.ones_(self.ttt_norm_weight)
+        nn.init.zeros_(self.ttt_norm_bias)
+        nn.init.normal_(self.learnable_ttt_lr_weight, mean=0.0, std=0.02)
+        nn.init.zeros_(self.learnable_ttt_lr_bias)
+
+    def _fused_projection(self, x: torch.Tensor) -> torch.Tensor:
+        """[B, L, ld]: XQ | XK | XV | XU | lr logits | zero padding (ld a
+        multiple of 8), one GEMM instead of five (ttt_layer.py:141-163)."""
+        H, D = self.num_heads, self.width
+        pad = (-(4 * D + H)) % 8
+        w = [self.wq.weight, self.wk.weight, self.wv.weight, self.wu.weight, self.learnable_ttt_lr_weight.view(H, D)]
+        b = [self.wq.bias, self.wk.bias, self.wv.bias, self.wu.bias, self.learnable_ttt_lr_bias.view(H)]
+        if pad:
+            w.append(self.wq.weight.new_zeros(pad, D))
+            b.append(self.wq.bias.new_zeros(pad))
+        return Fn.linear(x, torch.cat(w, 0), torch.cat(b, 0))
+
+    def process_input(self, x: torch.Tensor, rope: torch.Tensor):
+        """(XQ, XK, XV, XU, lr) in the inner loop's layouts (ttt_layer.py:261-329)."""
+        B, L, _ = x.shape
+        proj = self._fused_projection(x)
+        return ProducerFunction.apply(proj, rope[:L], self.ttt_norm_weight, self.ttt_norm_bias, self.num_heads,
+                                      self.mini_batch_size, float(self.ttt_base_lr), RECON_EPS)
+
+    def ttt(self, XQ, XK, XV, XU, lr):
+        raise NotImplementedError
+
+    def forward(self, x: torch.Tensor, rope: torch.Tensor):
+        if x.size(1) % self.mini_batch_size:
+            raise ValueError("sequence length must be a multiple of the mini-batch size")
+        XQ, XK, XV, XU, lr = self.process_input(x, rope)
+        out = self.ttt(XQ, XK, XV, XU, lr)                               # [B,H,NC,K,F]
+        h = PostNormFunction.apply(out, self.post_norm.weight, self.post_norm.bias, POST_NORM_EPS)
+        return self.wo(h)
+
+
+class TTTLinear(TTTLayerBase):
+    """ttt_layer.py:360-421"""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__(config)
+        H, F = self.num_heads, self.head_dim
+        self.W1 = nn.Parameter(torch.normal(0, 0.02, size=(H, F, F)))
+        self.b1 = nn.Parameter(torch.zeros(H, 1, F))
+
+    def init_weights(self):
+        super().init_weights()
+        nn.init.normal_(self.W1, mean=0.0, std=0.02)
+        nn.init.zeros_(self.b1)
+
+    def ttt(self, XQ, XK, XV, XU, lr):
+        B, NC = XQ.shape[0], XQ.shape[2]
+        G = min(max(self.scan_checkpoint_group_size, 1), NC)
+        W1 = self.W1.unsqueeze(0).expand(B, -1, -1, -1)
+        b1 = self.b1.unsqueeze(0).expand(B, -1, -1, -1)
+        return TTTLinearFunction.apply(self.ttt_norm_weight, self.ttt_norm_bias, W1, b1, XQ, XV, XK, lr, G, LN_EPS,
+                                       "layer")
+
+
+class TTTMLP(TTTLayerBase):
+    """ttt_layer.py:424-565: the two-layer fast-weight MLP (hidden width F)
+    and its memory-cache combiner over segments of M mini-batches."""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__(config)
+        H, F = self.num_heads, self.head_dim
+        self.W1 = nn.Parameter(torch.normal(0, 0.02, size=(H, F, F)))
+        self.b1 = nn.Parameter(torch.zeros(H, 1, F))
+        self.W2 = nn.Parameter(torch.normal(0, 0.02, size=(H, F, F)))
+        self.b2 = nn.Parameter(torch.zeros(H, 1, F))
+
+    def init_weights(self):
+        super().init_weights()
+        nn.init.normal_(self.W1, mean=0.0, std=0.02)
+        nn.init.zeros_(self.b1)
+        nn.init.normal_(self.W2, mean=0.0, std=0.02)
+        nn.init.zeros_(self.b2)
+
+    def ttt(self, XQ, XK, XV, XU, lr):
+        B, NC = XQ.shape[0], XQ.shape[2]
+        G = min(max(self.scan_checkpoint_group_size, 1), NC)
+        M = self.config.mem_cache_segment_n_mini_batches
+        st = [p.unsqueeze(0).expand(B, -1, -1, -1) for p in (self.W1, self.b1, self.W2, self.b2)]
+        out, W1m, b1m, W2m, b2m = TTTMLPFunction.apply(self.ttt_norm_weight, self.ttt_norm_bias, *st, XQ, XV, XK, lr,
+                                                       G, M, LN_EPS, "layer")
+        if M and math.ceil(NC / M) > 1:
+            out = mlp_memo_combine(XQ, XK, XU, out, W1m, b1m, W2m, b2m, self.ttt_norm_weight, self.ttt_norm_bias, M)
+        return out
+
+
+class TTTWrapper(nn.Module):
+    """ttt_layer.py:20-57: the layer and its rotary table."""
+
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.config = config
+        if config.ssm_layer == "ttt_linear":
+            self.ttt = TTTLinear(config)
+        elif config.ssm_layer == "ttt_mlp":
+            self.ttt = TTTMLP(config)
+        else:
+            raise TypeError(f"no ttt layer of type {config.ssm_layer}")
+        self.register_buffer("rope", self._rope(), persistent=False)
+
+    def _rope(self):
+        c = self.config
+        return rope_table(c.model_dim // c.num_heads, c.compressed_num_frames, c.latent_height, c.latent_width,
+                          c.rope_theta)
+
+    def init_freqs(self):
+        self.rope.copy_(self._rope())
+
+    def forward(self, x: torch.Tensor, seq_metadata=None):
+        return self.ttt(x, self.rope)
+
+
+class TTTForecaster(nn.Module):
+    """forecast.py:79-99: in_proj -> TTT layer -> head on the last token."""
+
+    def __init__(self, config: ModelConfig, d_in: int, d_out: int, pred_len: int):
+        super().__init__()
+        self.pred_len, self.d_out = pred_len, d_out
+        self.in_proj = nn.Linear(d_in, config.model_dim)
+        self.ttt = TTTWrapper(config)
+        self.ttt.init_freqs()
+        self.head = nn.Linear(config.model_dim, pred_len * d_out)
+
+    def forward(self, seq_x: torch.Tensor) -> torch.Tensor:
+        h = self.in_proj(seq_x)
+        h = self.ttt(h)
+        out = self.head(h[:, -1])
+        return out.view(seq_x.size(0), self.pred_len, self.d_out)
+
+
+__all__ = ["ModelConfig", "TTTLinear", "TTTMLP", "TTTWrapper", "TTTForecaster"]
