@@ -1,0 +1,173 @@
+"""The producer/consumer kernels and the end-to-end forecaster on the HIP path
+against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
+
+Tolerances: fp32 activations max-abs 1e-4 scaled by the tensor's magnitude
+above 1 for the elementwise kernels (they compute in fp32, so the observed
+error is ~1e-6); bf16 activations rel-L2 2e-2 (the north star's bar); the
+whole forecaster in fp32 rel-L2 1e-4 per tensor (a composition of four
+kernels, three GEMMs and the inner loop, each within fp32 rounding)."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import ttt_layer_oracle as LO
+from tests._util import max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+FP32_ATOL = 1e-4
+BF16_RTOL = 2e-2
+FP32_RTOL_E2E = 1e-4
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _bound_ok(mine, ref, dt):
+    if dt == torch.float32:
+        err, bound = max_abs(mine, ref), FP32_ATOL * max(1.0, float(ref.abs().max()))
+    else:
+        err, bound = rel_l2(mine, ref), BF16_RTOL
+    return err, bound
+
+
+def _producer_case(B, L, H, F_, seed):
+    g = torch.Generator().manual_seed(seed)
+    D = H * F_
+    ld = 4 * D + H + (-(4 * D + H)) % 8
+    proj = torch.randn(B, L, ld, generator=g)
+    proj[..., 4 * D + H:] = 0
+    ln_w = 1 + 0.2 * torch.randn(H, F_, generator=g)
+    ln_b = 0.2 * torch.randn(H, F_, generator=g)
+    grads = [torch.randn(B, H, L // 16, 16, F_, generator=g) for _ in range(4)]
+    dlr = torch.randn(B, H, L // 16, 16, generator=g)
+    return proj, ln_w, ln_b, grads, dlr
+
+
+def _oracle_producer(proj, ln_w, ln_b, H, F_, base_lr, grads, dlr):
+    B, L, _ = proj.shape
+    D = H * F_
+    pj = proj.double().requires_grad_(True)
+    lw, lb = ln_w.double().requires_grad_(True), ln_b.double().requires_grad_(True)
+    parts = [pj[..., i * D:(i + 1) * D].reshape(B, L, H, F_) for i in range(4)]
+    fr = LO.rope_freqs(F_, 1, 1, L)
+    outs = LO.producer(*parts, pj[..., 4 * D:4 * D + H], fr, lw, lb, 16, base_lr)
+    loss = sum((o * gr.double()).sum() for o, gr in zip(outs, list(grads) + [dlr]))
+    loss.backward()
+    return [o.detach() for o in outs], pj.grad, lw.grad, lb.grad
+
+
+@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 3)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_producer_vs_oracle(F_, H, dt):
+    from ttt_amd.layer_io import ProducerFunction, rope_table
+    B, L, base_lr = 2, 64, 0.05
+    _say(f"producer F{F_} H{H} {dt}")
+    proj, ln_w, ln_b, grads, dlr = _producer_case(B, L, H, F_, seed=81)
+    proj = proj.to(dt)
+    ref, dproj_ref, dlw_ref, dlb_ref = _oracle_producer(proj, ln_w, ln_b, H, F_, base_lr,
+                                                        [gr.to(dt) for gr in grads], dlr)
+    dev = torch.device("cuda")
+    pj = proj.to(dev).requires_grad_(True)
+    lw, lb = ln_w.to(dev).requires_grad_(True), ln_b.to(dev).requires_grad_(True)
+    outs = ProducerFunction.apply(pj, rope_table(F_, L).to(dev), lw, lb, H, 16, base_lr)
+    loss = sum((o.float() * gr.to(dev).float()).sum() for o, gr in zip(outs, [gr.to(dt) for gr in grads] + [dlr]))
+    loss.backward()
+    torch.cuda.synchronize()
+    bad = []
+    for name, mine, r in zip(("XQ", "XK", "XV", "XU", "lr"), outs, ref):
+        err, bound = _bound_ok(mine, r, dt if name != "lr" else torch.float32)
+        _say(f"  {name}: err {err:.3e} bound {bound:.3e}")
+        if err > bound:
+            bad.append(name)
+    D = H * F_
+    for name, mine, r in (("dproj", pj.grad[..., :4 * D + H], dproj_ref[..., :4 * D + H]),
+                          ("dln_w", lw.grad, dlw_ref), ("dln_b", lb.grad, dlb_ref)):
+        err, bound = _bound_ok(mine, r, dt)
+        _say(f"  {name}: err {err:.3e} bound {bound:.3e}")
+        if err > bound:
+            bad.append(name)
+    assert not bad
+    assert bool((pj.grad[..., 4 * D + H:] == 0).all())  # padding columns get a zero gradient
+
+
+@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 12)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_post_norm_vs_oracle(F_, H, dt):
+    from ttt_amd.layer_io import PostNormFunction
+    B, L = 2, 48
+    D = H * F_
+    _say(f"post-norm F{F_} H{H} {dt}")
+    g = torch.Generator().manual_seed(83)
+    x = torch.randn(B, H, L // 16, 16, F_, generator=g).to(dt)
+    gamma, beta = 1 + 0.2 * torch.randn(D, generator=g), 0.2 * torch.randn(D, generator=g)
+    dout = torch.randn(B, L, D, generator=g).to(dt)
+    xr, gr, br = (t.double().requires_grad_(True) for t in (x, gamma, beta))
+    ref = torch.nn.functional.layer_norm(xr.permute(0, 2, 3, 1, 4).reshape(B, L, D), (D,), gr, br, 1e-6)
+    ref.backward(dout.double())
+    dev = torch.device("cuda")
+    xg, gg, bg = (t.to(dev).requires_grad_(True) for t in (x, gamma, beta))
+    out = PostNormFunction.apply(xg, gg, bg)
+    out.backward(dout.to(dev))
+    torch.cuda.synchronize()
+    bad = []
+    for name, mine, r in (("out", out, ref), ("dX", xg.grad, xr.grad), ("dgamma", gg.grad, gr.grad),
+                          ("dbeta", bg.grad, br.grad)):
+        err, bound = _bound_ok(mine, r.detach(), dt)
+        _say(f"  {name}: err {err:.3e} bound {bound:.3e}")
+        if err > bound:
+            bad.append(name)
+    assert not bad
+
+
+def _forecaster(kind, B, L, H, F_, M, seed):
+    from ttt_amd import series
+    from ttt_amd.model import ModelConfig, TTTForecaster
+    cfg = ModelConfig(seq_len=L, model_dim=H * F_, num_heads=H, ssm_layer=kind, mini_batch_size=16,
+                      ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=M, scan_checkpoint_group_size=16)
+    torch.manual_seed(seed)
+    model = TTTForecaster(cfg, d_in=7, d_out=7, pred_len=96)
+    data = series.synthetic_series(seed=seed)
+    x, y = series.batch(data, B, L, 96, 96, seed=seed)
+    return cfg, model, x, y[:, -96:, :]
+
+
+@pytest.mark.parametrize("kind,M,dt", [("ttt_mlp", 2, torch.float32), ("ttt_mlp", 2, torch.bfloat16),
+                                       ("ttt_linear", 0, torch.float32)])
+def test_forecaster_train_step_vs_oracle(kind, M, dt):
+    """One training step of the end-to-end forecaster at the benchmark's
+    shape (lookback 512, horizon 96, 7 channels, H=4 heads of F=64, K=16,
+    memo segments of M=2, checkpoint groups of 16) at batch 2: the loss and
+    the gradient of every parameter against the oracle in fp64 on the same
+    weights and windows."""
+    B, L, H, F_ = 2, 512, 4, 64
+    _say(f"forecaster {kind} M{M} {dt} B{B} L{L} H{H} F{F_}")
+    cfg, model, x, y = _forecaster(kind, B, L, H, F_, M, seed=91)
+    sd = {k: v.detach().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    pred = LO.forecaster_forward(sd, x.double(), cfg, 96, 7)
+    loss_ref = torch.nn.functional.mse_loss(pred, y.double())
+    loss_ref.backward()
+    dev = torch.device("cuda")
+    model = model.to(dev)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=dt == torch.bfloat16):
+        out = model(x.to(dev))
+    loss = torch.nn.functional.mse_loss(out.float(), y.to(dev))
+    loss.backward()
+    torch.cuda.synchronize()
+    tol = FP32_RTOL_E2E if dt == torch.float32 else BF16_RTOL
+    err = abs(loss.item() - loss_ref.item()) / abs(loss_ref.item())
+    _say(f"  loss {loss.item():.6f} vs {loss_ref.item():.6f}: rel {err:.3e}")
+    bad = ["loss"] if err > tol else []
+    for name, prm in model.named_parameters():
+        r = sd[name].grad
+        if r is None:
+            assert prm.grad is None or float(prm.grad.abs().max()) == 0.0, name
+            continue
+        e = rel_l2(prm.grad, r)
+        _say(f"  d{name}: rel-L2 {e:.3e} (|ref| {float(r.norm()):.3e})")
+        if e > tol:
+            bad.append(name)
+    assert not bad
