@@ -53,7 +53,8 @@ enum ttt_status {
   TTT_ERR_HIP = -5,       /* launch failed (hipGetLastError) */
   TTT_ERR_WORKSPACE = -6, /* workspace missing or too small */
   TTT_ERR_ARG = -7,       /* other invalid argument (eps, G, M, eta_rule, option) */
-  TTT_ERR_TIMEOUT = -8    /* ttt_mlp_bwd_check: a dXQ/dXK worker gave up waiting */
+  TTT_ERR_TIMEOUT = -8,   /* ttt_mlp_bwd_check: a dXQ/dXK worker gave up waiting */
+  TTT_ERR_SCRATCH = -9    /* ttt_mlp_bwd_noalloc: problem larger than its static scratch */
 };
 
 /* ABI version of the loaded library (TTT_AMD_ABI_VERSION). */
@@ -289,6 +290,30 @@ int ttt_post_norm_fwd(const void* XQW, const float* gamma, const float* beta, in
 int ttt_post_norm_bwd(const void* XQW, const float* gamma, const float* stats, const void* dout,
                       int B, int L, int H, int K, int F, int dtype, void* dXQW, float* partial,
                       size_t partial_bytes, void* stream);
+
+/* Bytes of the static device scratch of ttt_mlp_bwd_noalloc (per GPU). */
+#define TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* ttt_mlp_bwd with no workspace argument and no allocation of any kind: the
+ * workspace (what ttt_mlp_bwd_workspace_bytes sizes) lives in a static device
+ * array of TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Problems whose workspace exceeds the scratch return
+ * TTT_ERR_SCRATCH (at F64 FF256 bf16 that is B*H*NC > 2730 mini-batch
+ * slots, e.g. B1 H12 T2048 fits and B16 H12 T2048 does not).  All calls on one
+ * GPU share its scratch, which keeps the last call's contents; the call clears
+ * the words that must start at zero itself.  Calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.
+ * Arguments and results are ttt_mlp_bwd's. */
+int ttt_mlp_bwd_noalloc(const void* XQ, const void* XK, const void* XV, const void* eta,
+                        const float* ln_w, const float* ln_b, const float* W1_ckpt, const float* b1_ckpt,
+                        const float* W2_ckpt, const float* b2_ckpt, const float* W1_last, const float* b1_last,
+                        const float* W2_last, const float* b2_last, const void* dout,
+                        int B, int H, int NC, int K, int F, int FF, int G, int dtype, int eta_rule, float eps,
+                        void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1, float* dW2,
+                        float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes,
+                        void* stream);
 
 /* Process-wide options of the library (no counterpart in the reference):
  *   TTT_OPT_MLP_BWD_POLL_LIMIT  polls of a checkpoint-group flag before a fused

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "ttt_kernels.h"
 
@@ -14,6 +15,31 @@ std::atomic<long long> g_mlp_bwd_poll_limit{1LL << 22};
 std::atomic<long long> g_mlp_bwd_fused{1};
 
 bool eta_rule_ok(int r) { return r == TTT_ETA_DENSE || r == TTT_ETA_LAYER || r == TTT_ETA_CAUSAL; }
+
+// Scratch of ttt_mlp_bwd_noalloc: the backward's workspace (the reverse
+// sweep's per-mini-batch handoff and the dXQ/dXK workers' control words) in a
+// file-scope device array instead of caller or library allocations.  Each GPU
+// holds its own copy for the life of the process; its device address is taken
+// once per device with hipGetSymbolAddress (the array's name in host code is
+// only a stand-in, never a device address) and used for every launch.
+static __device__ __align__(256) unsigned char scratch[TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of the current device's scratch, looked up on first use
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TTT_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return TTT_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TTT_OK;
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -73,6 +99,7 @@ const char* ttt_error_string(int status) {
     case TTT_ERR_WORKSPACE: return "workspace missing or too small";
     case TTT_ERR_ARG: return "invalid argument";
     case TTT_ERR_TIMEOUT: return "a fused dXQ/dXK worker gave up waiting (its rows hold NaN)";
+    case TTT_ERR_SCRATCH: return "the problem needs more workspace than the no-allocation entry point's static scratch";
     default: return "unknown status";
   }
 }
@@ -286,7 +313,7 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
   return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
 }
 
-int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                 const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
                 const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
                 const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
@@ -355,6 +382,38 @@ int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   p.dx_fused = (int)g_mlp_bwd_fused.load();
   p.eps = eps;
   return hip_status(ttt::launch_mlp_bwd(p, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int ttt_mlp_bwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
+                const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
+                const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G, int dtype,
+                int eta_rule, float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1, float* db1,
+                float* dW2, float* db2, float* dln_w, float* dln_b, const void* saved, size_t saved_bytes,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  return mlp_bwd_impl(XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt, W1_last, b1_last, W2_last,
+                      b2_last, dout, B, H, NC, K, F, FF, G, dtype, eta_rule, eps, dXQ, dXK, dXV, deta, dW1, db1, dW2,
+                      db2, dln_w, dln_b, saved, saved_bytes, workspace, workspace_bytes, stream);
+}
+
+int ttt_mlp_bwd_noalloc(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
+                        const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
+                        const float* b2_ckpt, const float* W1_last, const float* b1_last, const float* W2_last,
+                        const float* b2_last, const void* dout, int B, int H, int NC, int K, int F, int FF, int G,
+                        int dtype, int eta_rule, float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1,
+                        float* db1, float* dW2, float* db2, float* dln_w, float* dln_b, const void* saved,
+                        size_t saved_bytes, void* stream) {
+  const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
+  if (need == 0) return dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16 ? TTT_ERR_DTYPE : TTT_ERR_SHAPE;
+  if (need > TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES) return TTT_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int st = scratch_of_current_device(&ws);
+  if (st != TTT_OK) return st;
+  // the launch clears the control words it uses with a fill kernel; the
+  // handoff slots are written before they are read
+  return mlp_bwd_impl(XQ, XK, XV, eta, ln_w, ln_b, W1_ckpt, b1_ckpt, W2_ckpt, b2_ckpt, W1_last, b1_last, W2_last,
+                      b2_last, dout, B, H, NC, K, F, FF, G, dtype, eta_rule, eps, dXQ, dXK, dXV, deta, dW1, db1, dW2,
+                      db2, dln_w, dln_b, saved, saved_bytes, ws, TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int ttt_set_option(int option, long long value) {

@@ -28,6 +28,8 @@ OPT_MLP_BWD_POLL_LIMIT = 1
 OPT_MLP_BWD_FUSED = 2
 
 STATUS_TIMEOUT = -8
+STATUS_SCRATCH = -9
+MLP_BWD_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -45,6 +47,7 @@ SIGNATURES = {
     "ttt_mlp_saved_bytes": (_S, [_I] * 7),
     "ttt_mlp_bwd_workspace_bytes": (_S, [_I] * 7),
     "ttt_mlp_bwd": (_I, [_P] * 15 + [_I] * 9 + [_F] + [_P] * 10 + [_P, _S, _P, _S, _P]),
+    "ttt_mlp_bwd_noalloc": (_I, [_P] * 15 + [_I] * 9 + [_F] + [_P] * 10 + [_P, _S, _P]),
     "ttt_set_option": (_I, [_I, ctypes.c_longlong]),
     "ttt_get_option": (ctypes.c_longlong, [_I]),
     "ttt_mlp_bwd_check": (_I, [_P, _S] + [_I] * 7 + [_P]),
