@@ -41,3 +41,16 @@ def oracle_mlp_grads(d: dict, dout: torch.Tensor, G: int, dtype=torch.float64):
     res = {"out": out.detach().permute(0, 3, 1, 2, 4)}
     res.update({"d" + n: args[n].grad for n in names})
     return res
+
+
+# fp32 parity bar: the north star's max-abs 1e-4, or, for a tensor whose own
+# fp32 evaluation is less exact than that (the eta gradient reaches 1e4 on
+# unnormalised N(0,1) inputs), C_FP32 times the error of the oracle run in fp32
+# against the oracle in fp64 on the same inputs.  The kernels' fp32 error is
+# 1-2x the fp32 oracle's (different summation orders, the same precision).
+FP32_ATOL = 1e-4
+C_FP32 = 8.0
+
+
+def fp32_bound(ref64: torch.Tensor, ref32: torch.Tensor) -> float:
+    return max(FP32_ATOL, C_FP32 * max_abs(ref32, ref64))

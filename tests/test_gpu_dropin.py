@@ -1,6 +1,7 @@
 """The reference-shaped entry points (ops.ttt_linear, ops.ttt_mlp,
 TritonLinear.apply, TritonMLP.apply) through torch autograd on the GPU, vs
-autograd of the oracle.  fp32 max-abs <= 1e-4 (scaled by magnitude above 1);
+autograd of the oracle.  fp32 max-abs <= 1e-4, or C_FP32 = 8 times the fp32
+oracle's own error against fp64 where that is larger (tests/_util.fp32_bound);
 bf16 rel-L2 <= 2e-2."""
 
 import sys
@@ -9,7 +10,7 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import max_abs, rel_l2
+from tests._util import fp32_bound, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -30,10 +31,10 @@ def _grads(fn, d, names, dout_perm, dev):
     return res
 
 
-def _oracle(fn, d, names, dout_perm):
-    args = {n: d[n].double().requires_grad_(True) for n in names}
+def _oracle(fn, d, names, dout_perm, dtype=torch.float64):
+    args = {n: d[n].to(dtype).requires_grad_(True) for n in names}
     out = fn(args)
-    out.backward(dout_perm.double())
+    out.backward(dout_perm.to(dtype))
     res = {"out": out.detach()}
     res.update({"d" + n: args[n].grad for n in names})
     return res
@@ -68,6 +69,7 @@ def test_dropin_autograd(which, dt):
         f_ref = lambda a: base(a).permute(0, 3, 1, 2, 4)  # noqa: E731
     mine = _grads(f_gpu, d, names, dperm, "cuda")
     ref = _oracle(f_ref, d, names, dperm)
+    ref32 = _oracle(f_ref, d, names, dperm, torch.float32) if dt == torch.float32 else None
     # output and input gradients come back in each input's dtype
     for k in ref:
         src = "XQ" if k == "out" else k[1:]
@@ -76,7 +78,7 @@ def test_dropin_autograd(which, dt):
     bad = []
     for k in ref:
         if dt == torch.float32:
-            err, bound = max_abs(mine[k], ref[k]), 1e-4 * max(1.0, float(ref[k].abs().max()))
+            err, bound = max_abs(mine[k], ref[k]), fp32_bound(ref[k], ref32[k])
         else:
             err, bound = rel_l2(mine[k], ref[k]), 2e-2
         _say(f"  {k}: {err:.3e} (bound {bound:.3e})")
@@ -95,10 +97,11 @@ def test_tritonmlp_memo_outputs():
     outs = TritonMLP.apply(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["W2"], g["b2"], g["XQ"], g["XV"],
                            g["XK"], g["eta"], G, M)
     assert len(outs) == 5
-    ref = O.mlp_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV",
-                                                        "XK", "eta")), G=G, M=M)
+    keys = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
+    ref = O.mlp_forward_full(*(d[k].double() for k in keys), G=G, M=M)
+    ref32 = O.mlp_forward_full(*(d[k].float() for k in keys), G=G, M=M)
     for t, n in zip(outs[1:], ("W1", "b1", "W2", "b2")):
         assert t.dtype == torch.float32 and not t.requires_grad
         assert t.shape[2] == -(-NC // M)
-        assert max_abs(t, ref[n + "_memo"]) <= 1e-4 * max(1.0, float(ref[n + "_memo"].abs().max()))
+        assert max_abs(t, ref[n + "_memo"]) <= fp32_bound(ref[n + "_memo"], ref32[n + "_memo"])
     assert TritonMLP.sharded_mode is False

@@ -11,9 +11,11 @@ oracle on whole chains:
     deta and the gradient wrt the chain's initial state) equals, bit for bit,
     that chain's output in a launch of its batch row alone (H chains);
   * two whole chains (all 128 mini-batches, first and last of the grid)
-    against the fp64 oracle at the bf16 bar, rel-L2 <= 2e-2.
-The LayerNorm-parameter gradients are sums over the batch, so they are only
-covered by the smaller tests.  The memo combiner (memo segment M=8: 16 memo
+    against the fp64 oracle at the bf16 bar, rel-L2 <= 2e-2, every output
+    including the chain's LayerNorm-parameter gradient partials (the
+    launchers' per-chain [B,H,F] values before the host's sum over B).
+Both eta forms the reference builds are run: the causal expansion and the
+layer's row-constant eta[i][j] = lr[j]/K (ttt_layer.py:306-309).  The memo combiner (memo segment M=8: 16 memo
 states per chain) and the cached readout (one fixed state per chain) are
 checked the same way at the same B, H, T."""
 
@@ -43,10 +45,11 @@ def _mlp(d, G):
     out, ck, _, last, saved = mlp_forward(*(g[k] for k in ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV",
                                                           "XK", "eta")),
                                           G, want_ckpt=True, want_last=True, want_saved=True, ckpt_w1_only=True)
-    (_, _, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
-        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G, sum_ln=False)
     torch.cuda.synchronize()
-    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2)
+    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2,
+                dln_w=dlw, dln_b=dlb)
 
 
 def _linear(d, G):
@@ -54,10 +57,10 @@ def _linear(d, G):
     g = to_dev(d)
     out, (Wc, _), (Wl, _), saved = linear_forward(g["ln_w"], g["ln_b"], g["W1"], g["b1"], g["XQ"], g["XV"], g["XK"],
                                                   g["eta"], G, want_ckpt=True, want_last=True, want_saved=True)
-    (_, _, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
-        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, Wl, saved, g["dOut"], G)
+    (dlw, dlb, dW, db), (dxq, dxv, dxk, deta) = linear_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], Wc, Wl, saved, g["dOut"], G, sum_ln=False)
     torch.cuda.synchronize()
-    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW, db1=db)
+    return dict(out=out, dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW, db1=db, dln_w=dlw, dln_b=dlb)
 
 
 def _row(d, b):
@@ -98,15 +101,17 @@ def _check(d, run, oracle, G):
         assert not bad, f"chain ({b},{h}) off the oracle: {bad}"
 
 
-def test_mlp_fwd_bwd_full_size():
-    _say(f"mlp fwd+bwd full size B{B} H{H} NC{NC} F{F} FF256 G8 bf16")
-    d = O.make_inputs(B, H, NC, K, F, FF=256, seed=3, dtype=torch.bfloat16, with_grad=True)
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_mlp_fwd_bwd_full_size(kind):
+    _say(f"mlp fwd+bwd full size B{B} H{H} NC{NC} F{F} FF256 G8 bf16, {kind} eta")
+    d = O.make_inputs(B, H, NC, K, F, FF=256, seed=3, dtype=torch.bfloat16, with_grad=True, eta_kind=kind)
     _check(d, _mlp, oracle_mlp_grads, G=8)
 
 
-def test_linear_fwd_bwd_full_size():
-    _say(f"linear fwd+bwd full size B{B} H{H} NC{NC} F{F} G16 bf16")
-    d = O.make_inputs(B, H, NC, K, F, seed=2, dtype=torch.bfloat16, with_grad=True)
+@pytest.mark.parametrize("kind", ["causal", "layer"])
+def test_linear_fwd_bwd_full_size(kind):
+    _say(f"linear fwd+bwd full size B{B} H{H} NC{NC} F{F} G16 bf16, {kind} eta")
+    d = O.make_inputs(B, H, NC, K, F, seed=2, dtype=torch.bfloat16, with_grad=True, eta_kind=kind)
     _check(d, _linear, oracle_linear_grads, G=16)
 
 

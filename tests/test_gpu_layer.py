@@ -1,9 +1,8 @@
 """The producer/consumer kernels and the end-to-end forecaster on the HIP path
 against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
 
-Tolerances: fp32 activations max-abs 1e-4 scaled by the tensor's magnitude
-above 1 for the elementwise kernels (they compute in fp32, so the observed
-error is ~1e-6); bf16 activations rel-L2 2e-2 (the north star's bar); the
+Tolerances: fp32 activations max-abs 1e-4 for the elementwise kernels (they
+compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the north star's bar); the
 whole forecaster in fp32 rel-L2 1e-4 per tensor (a composition of four
 kernels, three GEMMs and the inner loop, each within fp32 rounding)."""
 
@@ -28,7 +27,7 @@ def _say(*a):
 
 def _bound_ok(mine, ref, dt):
     if dt == torch.float32:
-        err, bound = max_abs(mine, ref), FP32_ATOL * max(1.0, float(ref.abs().max()))
+        err, bound = max_abs(mine, ref), FP32_ATOL
     else:
         err, bound = rel_l2(mine, ref), BF16_RTOL
     return err, bound

@@ -1,8 +1,10 @@
 """TTT-Linear HIP kernels vs the CPU oracle (forward, side outputs, backward).
 
 Tolerances (north star): fp32 activations max-abs <= 1e-4 against the ops
-path; bf16 activations with fp32 state rel-L2 <= 2e-2.  The oracle runs in
-fp64 on the same (bf16-rounded) inputs."""
+path, or, where the tensor's own fp32 evaluation is less exact (the eta
+gradient), C_FP32 = 8 times the fp32 oracle's error against fp64
+(tests/_util.fp32_bound); bf16 activations with fp32 state rel-L2 <= 2e-2.
+The oracle runs in fp64 on the same (bf16-rounded) inputs."""
 
 import sys
 
@@ -10,19 +12,11 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import max_abs, oracle_linear_grads, rel_l2, to_dev
+from tests._util import C_FP32, FP32_ATOL, fp32_bound, max_abs, oracle_linear_grads, rel_l2, to_dev
 
 pytestmark = pytest.mark.gpu
 
-FP32_ATOL = 1e-4
 BF16_RTOL = 2e-2
-
-
-def fp32_bound(ref: torch.Tensor) -> float:
-    """max-abs bound for fp32 parity: 1e-4 on O(1) tensors, scaled by the
-    tensor's magnitude when it exceeds 1 (fp32 itself resolves ~6e-8 of it;
-    the eta gradient reaches 1e4-1e5 on unnormalised N(0,1) inputs)."""
-    return FP32_ATOL * max(1.0, float(ref.abs().max()))
 
 
 def _say(*a):
@@ -167,10 +161,10 @@ def test_linear_bwd_fp32(kind):
     ref32 = oracle_linear_grads(d, d["dOut"], G=0, dtype=torch.float32)
     bad = []
     for k in mine:
-        err = max_abs(mine[k], ref[k])
-        _say(f"  {k}: max-abs {err:.3e} (fp32 oracle {max_abs(ref32[k], ref[k]):.3e}, bound {fp32_bound(ref[k]):.3e})"
+        err, bound = max_abs(mine[k], ref[k]), fp32_bound(ref[k], ref32[k])
+        _say(f"  {k}: max-abs {err:.3e} (fp32 oracle {max_abs(ref32[k], ref[k]):.3e}, bound {bound:.3e})"
              f"  rel-L2 {rel_l2(mine[k], ref[k]):.3e}")
-        if err > fp32_bound(ref[k]):
+        if err > bound:
             bad.append(k)
     assert not bad
 
@@ -196,10 +190,11 @@ def test_linear_bwd_edges_fp32(NC, G, F_):
     d = O.make_inputs(1, 2, NC, 16, F_, seed=20 + NC, dtype=torch.float32, with_grad=True)
     mine = _bwd(d, d["dOut"], G=G)
     ref = oracle_linear_grads(d, d["dOut"], G=0)
+    ref32 = oracle_linear_grads(d, d["dOut"], G=0, dtype=torch.float32)
     bad = []
     for k in mine:
-        err = max_abs(mine[k], ref[k])
-        _say(f"  {k}: max-abs {err:.3e} bound {fp32_bound(ref[k]):.3e}")
-        if err > fp32_bound(ref[k]):
+        err, bound = max_abs(mine[k], ref[k]), fp32_bound(ref[k], ref32[k])
+        _say(f"  {k}: max-abs {err:.3e} bound {bound:.3e}")
+        if err > bound:
             bad.append(k)
     assert not bad

@@ -89,11 +89,12 @@ def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_
 
 
 def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, G: int, eps: float = LN_EPS,
-                    eta_rule="dense"):
+                    eta_rule="dense", sum_ln: bool = True):
     """Run the backward kernel on what linear_forward(want_ckpt, want_last,
     want_saved) returned.  Returns fp32 (dln_w [H,F], dln_b [H,F],
     dW1 [B,H,F,F], db1 [B,H,1,F]) and (dXQ, dXV, dXK, deta) in XQ.dtype,
-    deta being dlr [B,H,NC,K] fp32 for an lr eta rule."""
+    deta being dlr [B,H,NC,K] fp32 for an lr eta rule.  With sum_ln=False
+    dln_w and dln_b are the per-chain partials [B,H,F]."""
     rule = _lib.eta_rule_code(eta_rule)
     B, H, NC, K, F = XQ.shape
     dev = check_device(XQ, XK, XV, eta, W1_ckpt, W1_last, saved, dout)
@@ -119,7 +120,9 @@ def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, 
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW), ptr(db), ptr(dlw), ptr(dlb),
             ptr(saved), saved.numel(), stream_of(dev))
     _lib.check(st, "ttt_linear_bwd")
-    return (dlw.sum(0), dlb.sum(0), dW, db), (dxq, dxv, dxk, deta)
+    if sum_ln:
+        dlw, dlb = dlw.sum(0), dlb.sum(0)
+    return (dlw, dlb, dW, db), (dxq, dxv, dxk, deta)
 
 
 class TTTLinearFunction(torch.autograd.Function):

@@ -111,7 +111,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
 
 
 def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, eps: float = LN_EPS,
-                 workspace=None, eta_rule="dense", check_timeout=None):
+                 workspace=None, eta_rule="dense", check_timeout=None, sum_ln: bool = True):
     """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints, last =
     the final state and saved = the saved buffer, all from one mlp_forward
     call with the same G and eta form.  `workspace` (uint8, at least
@@ -119,7 +119,8 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     fp32 (dln_w [H,F], dln_b [H,F], dW1, db1, dW2, db2) and (dXQ, dXV, dXK,
     deta) in XQ.dtype, deta being dlr [B,H,NC,K] fp32 for an lr eta rule.
     With check_timeout (default: TTT_AMD_CHECK set) the call waits for the
-    launch and raises TTTError if a fused dXQ/dXK worker gave up waiting."""
+    launch and raises TTTError if a fused dXQ/dXK worker gave up waiting.
+    With sum_ln=False dln_w and dln_b are the per-chain partials [B,H,F]."""
     rule = _lib.eta_rule_code(eta_rule)
     B, H, NC, K, F = XQ.shape
     FF = ckpt[0].shape[-1]
@@ -149,7 +150,9 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     _lib.check(st, "ttt_mlp_bwd")
     if CHECK_BWD if check_timeout is None else check_timeout:
         _lib.check(mlp_bwd_status(ws, B, H, NC, K, F, FF, code), "ttt_mlp_bwd")
-    return (dlw.sum(0), dlb.sum(0), dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
+    if sum_ln:
+        dlw, dlb = dlw.sum(0), dlb.sum(0)
+    return (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta)
 
 
 def mlp_bwd_status(workspace, B, H, NC, K, F, FF, code) -> int:
