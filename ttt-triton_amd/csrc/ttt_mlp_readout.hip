@@ -52,24 +52,46 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
   const int wave = threadIdx.x >> 6;
   const int l = lane_id(), g = l >> 4, n = l & 15;
 
-  // ---- stage W1, W2, biases and LN parameters of this chain
+  const int ntiles = p.ntok >> 4;
+  const int t0 = chunk * (kReadoutChunk / 16) + wave * NT;  // first token tile of this wave
+  const int nv = min(NT, ntiles - t0);                      // valid tiles (may be <= 0)
+  const size_t xoff = (size_t)chain * p.ntok * F;
+  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
+  float* __restrict__ OUT = p.out + xoff;
+
+  // XQ^T operand frags (free = token, contraction = feature), requested
+  // first; tiles past the valid range repeat a valid one and are not stored
+  Frag<T> xq[NT][FT];
   {
+    const int tl = max(nv, 1) - 1;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const T* x = XQ + (size_t)(min(t0 + min(t, tl), ntiles - 1)) * 16 * F;
+#pragma unroll
+      for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(x, F, 16 * kb);
+    }
+  }
+
+  // ---- stage W1, W2, biases and LN parameters of this chain: every load of
+  //      a wave's blocks is issued before the first conversion, so their
+  //      latencies overlap instead of adding up block by block
+  {
+    constexpr int NB = FT * HTT / kReadoutWaves;  // blocks of W1 (and of W2) per wave
     const size_t S = (size_t)p.S;
     const float* __restrict__ w1 = p.W1 + (size_t)chain * S * F * FF;
     const float* __restrict__ w2 = p.W2 + (size_t)chain * S * FF * F;
-    for (int blk = wave; blk < FT * HTT; blk += kReadoutWaves) {
-      const int kb = blk / HTT, ht = blk - kb * HTT;
-      f4 x;
+    f4 x1[NB], x2[NB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
-      sh.w1[blk][l] = to_frag<T>(x).v;
+    for (int b = 0; b < NB; ++b) {
+      const int blk = wave + kReadoutWaves * b, kb = blk / HTT, ht = blk - kb * HTT;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x1[b][j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
     }
-    for (int blk = wave; blk < HTT * FT; blk += kReadoutWaves) {
-      const int ht = blk / FT, ct = blk - ht * FT;
-      f4 x;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
-      sh.w2[blk][l] = to_frag<T>(x).v;
+    for (int b = 0; b < NB; ++b) {
+      const int blk = wave + kReadoutWaves * b, ht = blk / FT, ct = blk - ht * FT;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x2[b][j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
     }
     const float* __restrict__ b1 = p.b1 + (size_t)chain * S * FF;
     const float* __restrict__ b2 = p.b2 + (size_t)chain * S * F;
@@ -79,27 +101,13 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
       sh.lnw[i] = p.ln_w[h * F + i];
       sh.lnb[i] = p.ln_b[h * F + i];
     }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) sh.w1[wave + kReadoutWaves * b][l] = to_frag<T>(x1[b]).v;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) sh.w2[wave + kReadoutWaves * b][l] = to_frag<T>(x2[b]).v;
   }
   __syncthreads();
-
-  const int ntiles = p.ntok >> 4;
-  const int t0 = chunk * (kReadoutChunk / 16) + wave * NT;  // first token tile of this wave
-  const int nv = min(NT, ntiles - t0);                      // valid tiles (may be <= 0)
-  if (nv <= 0) return;                                      // no barrier follows
-
-  const size_t xoff = (size_t)chain * p.ntok * F;
-  const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
-  float* __restrict__ OUT = p.out + xoff;
-
-  // XQ^T operand frags (free = token, contraction = feature); tiles past the
-  // valid range repeat the last valid one and are not stored.
-  Frag<T> xq[NT][FT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const T* x = XQ + (size_t)(t0 + min(t, nv - 1)) * 16 * F;
-#pragma unroll
-    for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(x, F, 16 * kb);
-  }
+  if (nv <= 0) return;  // no barrier follows
 
   Tile acc[NT][FT];  // Z2 + b2 (b2 rides in the accumulator)
 #pragma unroll
@@ -142,40 +150,48 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
       for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
   }
 
-  // ---- LayerNorm over the F features of each token row, residual, store
+  // ---- LayerNorm over the F features of each token row, residual, store.
+  // The residual XQ comes from the operand frags by an exact transpose (an
+  // MFMA against the identity gives XQ's C-layout tile, the layout of acc);
+  // each output tile is transposed the same way in fp32 so that a lane holds
+  // 4 consecutive features of one token and stores them with one 16-byte
+  // store.
   float lwv[FT], lbv[FT];
 #pragma unroll
   for (int c = 0; c < FT; ++c) {
     lwv[c] = sh.lnw[16 * c + n];
     lbv[c] = sh.lnb[16 * c + n];
   }
+  const Frag<T> I = identity_frag<T>();
+  const Frag<float> I32 = identity_frag<float>();
   const float invF = 1.0f / (float)F;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t >= nv) break;
-    const size_t row0 = (size_t)(t0 + t) * 16;
+    f4 mean, rstd;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float v[FT], s = 0.f;
+      float s = 0.f;
 #pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        v[c] = acc[t][c].v[j];
-        s += v[c];
-      }
-      const float mean = sum_row16(s) * invF;
+      for (int c = 0; c < FT; ++c) s += acc[t][c].v[j];
+      mean[j] = sum_row16(s) * invF;
       float q = 0.f;
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        v[c] -= mean;
-        q += v[c] * v[c];
+        const float d = acc[t][c].v[j] - mean[j];
+        q += d * d;
       }
-      const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
-      const size_t r = (row0 + 4 * g + j) * F;
+      rstd[j] = rsqrt_f(sum_row16(q) * invF + p.eps);
+    }
+    float* o = OUT + (size_t)(t0 + t) * 16 * F;
 #pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        const float x = (float)XQ[r + 16 * c + n];
-        OUT[r + 16 * c + n] = x + lwv[c] * (v[c] * rstd) + lbv[c];
-      }
+    for (int c = 0; c < FT; ++c) {
+      const f4 x = transpose16(xq[t][c], I).v;  // lane (g, n): XQ[4g + j][16c + n]
+      f4 y;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = x[j] + lwv[c] * ((acc[t][c].v[j] - mean[j]) * rstd[j]) + lbv[c];
+      // lane (g, n): out[n][16c + 4g + j]
+      store_f4(o, F, 16 * c, transpose16(Frag<float>{y}, I32).v);
     }
   }
 }
