@@ -13,7 +13,7 @@
 // launches forward and two backward:
 //
 //   memo_summary_kernel   one workgroup per (chain, segment): the segment summaries;
-//   memo_gate_kernel      one thread per token: the gates (written as
+//   memo_gate_kernel      one workgroup per 64 tokens: the gates (written as
 //                         gamma^T [NS][tokens] plus the current-segment gate);
 //   memo_combine_kernel   one workgroup per (chain, pair of 256-token chunks):
 //                         for each memo state j below a chunk's last segment, stage
@@ -21,7 +21,7 @@
 //                         readout does), run the chunk's tiles of later
 //                         segments through R_j and accumulate gamma_j R_j (forward)
 //                         or dOut . R_j (backward: the gate gradients);
-//   memo_finish_kernel    (backward) one thread per token: the softmax
+//   memo_finish_kernel    (backward) one workgroup per 64 tokens: the softmax
 //                         backward, dXU = sum_j dsims_j summary_j and
 //                         dXQW = gamma_i dOut;
 //   memo_dxk_kernel       (backward) one workgroup per (chain, segment):
@@ -34,6 +34,7 @@
 // chain (fp32) holds gamma^T [NS][NT], the current gate [NT], the summaries
 // [NS][F] and, in the backward, the gate gradients [NS][NT] and the
 // current-summary logit gradients [NT] (NT = NC * 16 tokens).
+#include "ttt_fixed_mlp.h"
 #include "ttt_kernels.h"
 
 namespace ttt {
@@ -93,52 +94,119 @@ __global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams
   if (threadIdx.x < F) p.gates[(size_t)chain * L.stride + L.summ + (size_t)j * F + threadIdx.x] = tot / (float)(t1 - t0);
 }
 
-// one workgroup per (chain, block of kMemoThreads tokens), one token per thread:
-// the softmax over the summaries of segments 0..i
+// Gate and finish kernels: a workgroup of kMemoThreads threads takes
+// kTokBlk consecutive tokens of one chain and works in two layouts:
+//   token-major  thread (sub = wave, tk = lane): token tk, segments j = sub,
+//                sub + 4, ...  Loads of per-(segment, token) gate data
+//                gam[j][t] are then coalesced over the wave's 64 tokens;
+//   row          the 16 lanes of a DPP row share a token (kRowUnroll tokens
+//                per row) and hold F/16 consecutive features each, so token
+//                rows are read and written as contiguous segments.
+// Summaries are staged per chunk of kSegChunk segments in LDS and read as
+// broadcasts (every lane of a wave at the same segment).
+constexpr int kTokBlk = 64;
+constexpr int kRowUnroll = kTokBlk / (kMemoThreads / 16);
+constexpr int kSegChunk = 64;
+
+template <int F> using RowVec = std::conditional_t<F / 16 == 4, f4, f2>;
+
+template <int F>
+__device__ __forceinline__ void stage_summaries(float (*sm)[F], const float* __restrict__ summ, int c, int NS) {
+  const int n = min(kSegChunk, NS - c * kSegChunk) * F;
+  const float* src = summ + (size_t)c * kSegChunk * F;
+  for (int idx = threadIdx.x; idx < n; idx += kMemoThreads) sm[idx / F][idx % F] = src[idx];
+}
+
+// The gates: logits s_j = XU_t . summary_j for j = 0..i and gamma =
+// softmax(s).  Each thread keeps an online (max, sum) over its segments, the
+// four partial pairs of a token are merged through LDS, and a second pass
+// recomputes each logit (the same operations, so the same value) to write the
+// normalised gate.
 template <typename T, int F>
 __global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  const int nblk = (p.NC * K + kMemoThreads - 1) / kMemoThreads;
-  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
+  constexpr int FPL = F / 16;
+  constexpr int NSUB = kMemoThreads / 64;
+  __shared__ float xs[kTokBlk][F + 1];  // XU rows in fp32 (padded: conflict-free column reads)
+  __shared__ __align__(16) float sm[kSegChunk][F];
+  __shared__ float red[2][NSUB][kTokBlk];
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const int nblk = (NT + kTokBlk - 1) / kTokBlk;
+  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
   const MemoGateLayout L(NC, K, F, NS);
   float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
-  __shared__ f4 summ[kMemoMaxStates * F / 4];
-  const int t = blk * kMemoThreads + threadIdx.x;
-  const int tmax = min(NT, (blk + 1) * kMemoThreads) - 1;
-  const int ns = (tmax / K) / M + 1;  // segments this block's tokens can reach
-  for (int q = threadIdx.x; q < ns * F / 4; q += kMemoThreads)
-    summ[q] = *reinterpret_cast<const f4*>(gb + L.summ + 4 * (size_t)q);
-  __syncthreads();
-  if (t >= NT) return;  // (no barrier follows)
-  const int i = (t / K) / M;
-  if (i == 0) {
-    gb[L.gcur + t] = 1.0f;
-    return;
-  }
-  const T* __restrict__ xu_row = static_cast<const T*>(p.XU) + ((size_t)chain * NT + t) * F;
-  f4 xu[F / 4];
-#pragma unroll
-  for (int q = 0; q < F / 4; ++q) xu[q] = load4(xu_row + 4 * q);
+  const float* __restrict__ summ = gb + L.summ;
   float* __restrict__ gam = gb + L.gam;
-  float mx = -3.0e38f;
-  for (int j = 0; j <= i; ++j) {
-    f4 s4 = f4{0.f, 0.f, 0.f, 0.f};
+  const int tb = blk * kTokBlk;
+  const int ilast = ((min(tb + kTokBlk, NT) - 1) / K) / M;  // the block's largest segment index
+  const int nch = ilast / kSegChunk + 1;
+
+  {  // XU rows -> LDS (row layout)
+    const int q = threadIdx.x & 15, row = threadIdx.x >> 4;
 #pragma unroll
-    for (int q = 0; q < F / 4; ++q) s4 += xu[q] * summ[j * (F / 4) + q];
-    const float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-    gam[(size_t)j * NT + t] = s;
-    mx = fmaxf(mx, s);
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int tk = u * (kMemoThreads / 16) + row;
+      float x[FPL];
+      load_n<FPL>(static_cast<const T*>(p.XU) + ((size_t)chain * NT + min(tb + tk, NT - 1)) * F + FPL * q, x);
+#pragma unroll
+      for (int k = 0; k < FPL; ++k) xs[tk][FPL * q + k] = x[k];
+    }
   }
+  const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
+  const int t = tb + tk;
+  const int i = t < NT ? (t / K) / M : -1;
+  if (nch == 1) stage_summaries<F>(sm, summ, 0, NS);
+  __syncthreads();
+  float x[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) x[f] = xs[tk][f];
+  auto logit = [&](int jj) {
+    const f4* sj = reinterpret_cast<const f4*>(sm[jj]);
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < F / 4; ++k) {
+      const f4 v = sj[k];
+      s += x[4 * k] * v[0] + x[4 * k + 1] * v[1] + x[4 * k + 2] * v[2] + x[4 * k + 3] * v[3];
+    }
+    return s;
+  };
+  float m = -3.0e38f, l = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    if (nch > 1) {
+      __syncthreads();
+      stage_summaries<F>(sm, summ, c, NS);
+      __syncthreads();
+    }
+    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj <= i; jj += NSUB) {
+      const float sj = logit(jj);
+      const float mn = fmaxf(m, sj);
+      l = l * __expf(m - mn) + __expf(sj - mn);
+      m = mn;
+    }
+  }
+  red[0][sub][tk] = m;
+  red[1][sub][tk] = l;
+  __syncthreads();
+  float mx = red[0][0][tk];
+#pragma unroll
+  for (int u = 1; u < NSUB; ++u) mx = fmaxf(mx, red[0][u][tk]);
   float sum = 0.f;
-  for (int j = 0; j <= i; ++j) {
-    const float e = __expf(gam[(size_t)j * NT + t] - mx);
-    gam[(size_t)j * NT + t] = e;
-    sum += e;
+#pragma unroll
+  for (int u = 0; u < NSUB; ++u) sum += red[1][u][tk] * __expf(red[0][u][tk] - mx);
+  const float inv = i >= 0 ? 1.0f / sum : 0.f;
+  for (int c = 0; c < nch; ++c) {
+    if (nch > 1) {
+      __syncthreads();
+      stage_summaries<F>(sm, summ, c, NS);
+      __syncthreads();
+    }
+    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj <= i; jj += NSUB) {
+      const int j = c * kSegChunk + jj;
+      const float gj = __expf(logit(jj) - mx) * inv;
+      gam[(size_t)j * NT + t] = gj;
+      if (j == i) gb[L.gcur + t] = gj;
+    }
   }
-  const float inv = 1.0f / sum;
-  for (int j = 0; j < i; ++j) gam[(size_t)j * NT + t] *= inv;
-  gb[L.gcur + t] = gam[(size_t)i * NT + t] * inv;
 }
 
 // ------------------------------------------------------------------ R_j over a chunk
@@ -146,21 +214,13 @@ constexpr int kMemoWaves = 8;
 constexpr int kMemoTilesPerWave = 2;
 constexpr int kMemoChunkTiles = kMemoWaves * kMemoTilesPerWave;  // mini-batches (16 tokens each) per workgroup
 
-template <typename T, int FT, int HTT> struct MemoShared {
-  typename FragT<T>::type w1[FT * HTT][64];  // block (kb, ht): W1[16kb + 4g + j][16ht + n]
-  typename FragT<T>::type w2[HTT * FT][64];  // block (ht, ct): W2[16ht + 4g + j][16ct + n]
-  float b1[16 * HTT];
-  float b2[16 * FT];
-};
-
 template <typename T, int FT, int HTT, bool BWD>
 __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoParams p) {
   constexpr int F = 16 * FT;
   constexpr int FF = 16 * HTT;
   constexpr int K = 16;
   constexpr int NTW = kMemoTilesPerWave;
-  constexpr int NB = FT * HTT / kMemoWaves;  // W1 (and W2) blocks each wave stages
-  __shared__ MemoShared<T, FT, HTT> sh;
+  __shared__ FixedMlpLds<T, FT, HTT> sh;
 
   // blockIdx -> (chain, chunk pair), the pairs of one chain on one XCD (shared
   // L2).  Chunk c needs about 2c+1 memo states, so a workgroup takes chunks c
@@ -241,8 +301,9 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
     for (int jm = 0; jm < jmax; ++jm) {
       // ---- stage memo state jm (the previous state's reads are done); request
       //      this state's gates of the wave's tokens first (forward).  Each wave
-      //      stages NB blocks of W1 and of W2, every load of a matrix issued
-      //      before the first conversion.
+      //      stages NB blocks of W1 and of W2 and a share of the biases, every
+      //      load issued before the first conversion, so that a state costs one
+      //      memory latency.
       __syncthreads();
       f4 gjv[NTW];
       if constexpr (!BWD) {
@@ -252,27 +313,8 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       }
       {
         const size_t st = (size_t)chain * NS + jm;
-        const float* __restrict__ w1 = p.W1 + st * F * FF;
-        const float* __restrict__ w2 = p.W2 + st * FF * F;
-        f4 x[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const int blk = wave + kMemoWaves * b, kb = blk / HTT, ht = blk - kb * HTT;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) x[b][j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b) sh.w1[wave + kMemoWaves * b][l] = to_frag<T>(x[b]).v;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const int blk = wave + kMemoWaves * b, ht = blk / FT, ct = blk - ht * FT;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) x[b][j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
-        }
-#pragma unroll
-        for (int b = 0; b < NB; ++b) sh.w2[wave + kMemoWaves * b][l] = to_frag<T>(x[b]).v;
-        for (int i = threadIdx.x; i < FF; i += 64 * kMemoWaves) sh.b1[i] = p.b1[st * FF + i];
-        for (int i = threadIdx.x; i < F; i += 64 * kMemoWaves) sh.b2[i] = p.b2[st * F + i];
+        stage_fixed_mlp<T, FT, HTT, kMemoWaves>(sh, p.W1 + st * F * FF, p.b1 + st * FF, p.W2 + st * FF * F,
+                                                p.b2 + st * F);
       }
       __syncthreads();
 
@@ -281,45 +323,8 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
       if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
 
-      Tile acc[NTW][FT];  // Z2 + b2 (b2 rides in the accumulator)
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        const float b2 = sh.b2[16 * c + n];
-#pragma unroll
-        for (int t = 0; t < NTW; ++t) acc[t][c].v = f4{b2, b2, b2, b2};
-      }
-#pragma unroll 1
-      for (int ht = 0; ht < HTT; ht += 2) {
-        Frag<T> x2[2][NTW];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          Frag<T> w1f[FT];
-#pragma unroll
-          for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
-          const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
-#pragma unroll
-          for (int t = 0; t < NTW; ++t) {
-            Tile z;
-            z.v = bias;  // b1 rides in the accumulator
-#pragma unroll
-            for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
-            f4 a;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j]);
-            x2[hh][t] = to_frag<T>(a);
-          }
-        }
-        Frag<T> q0[FT], q1[FT];
-#pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          q0[c].v = sh.w2[ht * FT + c][l];
-          q1[c].v = sh.w2[(ht + 1) * FT + c][l];
-        }
-#pragma unroll
-        for (int t = 0; t < NTW; ++t)
-#pragma unroll
-          for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
-      }
+      Tile acc[NTW][FT];  // Z2 + b2
+      fixed_mlp_tiles<T, FT, HTT, NTW>(sh, xq, acc);
 
       // ---- N_jm = LN-normalised (Z2 + b2) per token row; fold it in
 #pragma unroll
@@ -390,57 +395,122 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
 }
 
 // ------------------------------------------------------------------ backward: softmax, dXU, dXQW
-// one workgroup per (chain, block of kMemoThreads tokens), one token per thread
+// Layouts as in the gate kernel.  dsims_j = gamma_j (dgamma_j - S) with
+// S = sum_{k<=i} gamma_k dgamma_k: the token-major threads sum their segments'
+// gamma_j dgamma_j (coalesced loads), the four partials of a token meet in
+// LDS, and per chunk of segments the dsims go to LDS, from where the row
+// layout accumulates dXU = sum_{j<i} dsims_j summ_j + dsims_i summ_i with
+// broadcast reads only.
 template <typename T, int F>
 __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  const int nblk = (p.NC * K + kMemoThreads - 1) / kMemoThreads;
-  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
+  constexpr int FPL = F / 16;
+  constexpr int NSUB = kMemoThreads / 64;
+  constexpr int U = kRowUnroll;
+  using VT = RowVec<F>;
+  __shared__ __align__(16) float sm[kSegChunk][F];
+  __shared__ float dsl[kTokBlk][kSegChunk + 1];
+  __shared__ float sp[NSUB][kTokBlk];
+  __shared__ float dgl[kTokBlk];
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
+  const int nblk = (NT + kTokBlk - 1) / kTokBlk;
+  const int chain = blockIdx.x / nblk, blk = blockIdx.x - chain * nblk;
   const MemoGateLayout L(NC, K, F, NS);
   float* __restrict__ gb = p.gates + (size_t)chain * L.stride;
-  __shared__ f4 summ[kMemoMaxStates * F / 4];
-  const int t = blk * kMemoThreads + threadIdx.x;
-  const int tmax = min(NT, (blk + 1) * kMemoThreads) - 1;
-  const int ns = (tmax / K) / M + 1;
-  for (int q = threadIdx.x; q < ns * F / 4; q += kMemoThreads)
-    summ[q] = *reinterpret_cast<const f4*>(gb + L.summ + 4 * (size_t)q);
+  const float* __restrict__ gam = gb + L.gam;
+  const float* __restrict__ dgam = gb + L.dgam;
+  const float* __restrict__ summ = gb + L.summ;
+  const int tb = blk * kTokBlk;
+  const int ilast = ((min(tb + kTokBlk, NT) - 1) / K) / M;
+  const int nch = (ilast + kSegChunk - 1) / kSegChunk;  // chunks of segments below the block's last one
+
+  // ---- row layout: dOut, the current gate, dgamma_current = dOut . XQW
+  const int q = threadIdx.x & 15, row = threadIdx.x >> 4;
+  const int f0 = FPL * q;
+  float dout[U][FPL], gcr[U];
+  int iu[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int tk = u * (kMemoThreads / 16) + row;
+    const int tc = min(tb + tk, NT - 1);  // tokens past the end compute on the last one and store nothing
+    iu[u] = (tc / K) / M;
+    float xqw[FPL];
+    const size_t e = ((size_t)chain * NT + tc) * F + f0;
+    load_n<FPL>(static_cast<const T*>(p.dout) + e, dout[u]);
+    load_n<FPL>(static_cast<const T*>(p.XQW) + e, xqw);
+    gcr[u] = gb[L.gcur + tc];
+    float dg = 0.f;
+#pragma unroll
+    for (int k = 0; k < FPL; ++k) dg += dout[u][k] * xqw[k];
+    dg = sum_row16(dg);
+    if (q == 0) dgl[tk] = dg;
+  }
+
+  // ---- token-major: S
+  const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
+  const int tc = min(tb + tk, NT - 1);
+  const int i = (tc / K) / M;
+  {
+    float s = 0.f;
+    for (int j = sub; j < i; j += NSUB) s += gam[(size_t)j * NT + tc] * dgam[(size_t)j * NT + tc];
+    sp[sub][tk] = s;
+  }
   __syncthreads();
-  if (t >= NT) return;  // (no barrier follows)
-  const size_t row = ((size_t)chain * NT + t) * F;
-  const T* __restrict__ xqw_row = static_cast<const T*>(p.XQW) + row;
-  const T* __restrict__ do_row = static_cast<const T*>(p.dout) + row;
-  T* __restrict__ dxu_row = static_cast<T*>(p.dXU) + row;
-  T* __restrict__ dxqw_row = static_cast<T*>(p.dXQW) + row;
-  const int i = (t / K) / M;
-  const float gc = gb[L.gcur + t];
-  f4 dout[F / 4], dxu[F / 4];
-  f4 dg4 = f4{0.f, 0.f, 0.f, 0.f};
+  const float gc = gb[L.gcur + tc];
+  const float dgc = dgl[tk];
+  float S = gc * dgc;
 #pragma unroll
-  for (int q = 0; q < F / 4; ++q) {
-    dout[q] = load4(do_row + 4 * q);
-    dg4 += dout[q] * load4(xqw_row + 4 * q);
-    dxu[q] = f4{0.f, 0.f, 0.f, 0.f};
-  }
-  const float dgc = (dg4[0] + dg4[1]) + (dg4[2] + dg4[3]);
-  float dscur = 0.f;  // d loss / d (XU . current summary)
-  if (i > 0) {
-    // softmax backward: dsims_j = gamma_j (dgamma_j - sum_k gamma_k dgamma_k)
-    float S = gc * dgc;
-    for (int j = 0; j < i; ++j) S += gb[L.gam + (size_t)j * NT + t] * gb[L.dgam + (size_t)j * NT + t];
-    for (int j = 0; j <= i; ++j) {
-      const float ds = j < i ? gb[L.gam + (size_t)j * NT + t] * (gb[L.dgam + (size_t)j * NT + t] - S)
-                             : gc * (dgc - S);
+  for (int u = 0; u < NSUB; ++u) S += sp[u][tk];
+  const float dscur = i > 0 ? gc * (dgc - S) : 0.f;  // d loss / d (XU . current summary)
+  if (sub == 0 && tb + tk < NT) gb[L.dscur + tb + tk] = dscur;
+
+  float dxu[U][FPL];
 #pragma unroll
-      for (int q = 0; q < F / 4; ++q) dxu[q] += ds * summ[j * (F / 4) + q];
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int k = 0; k < FPL; ++k) dxu[u][k] = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    if (c > 0) __syncthreads();  // the previous chunk's LDS reads are done
+    stage_summaries<F>(sm, summ, c, NS);
+    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj < i; jj += NSUB) {
+      const int j = c * kSegChunk + jj;
+      dsl[tk][jj] = gam[(size_t)j * NT + tc] * (dgam[(size_t)j * NT + tc] - S);
     }
-    dscur = gc * (dgc - S);
-  }
-  gb[L.dscur + t] = dscur;
+    __syncthreads();
 #pragma unroll
-  for (int q = 0; q < F / 4; ++q) {
-    store4(dxu_row + 4 * q, dxu[q]);
-    store4(dxqw_row + 4 * q, gc * dout[q]);
+    for (int u = 0; u < U; ++u) {
+      const int tkr = u * (kMemoThreads / 16) + row;
+      const int n = min(kSegChunk, iu[u] - c * kSegChunk);  // (uniform over the row)
+#pragma unroll 4
+      for (int jj = 0; jj < n; ++jj) {
+        const float ds = dsl[tkr][jj];
+        const VT sv = *reinterpret_cast<const VT*>(&sm[jj][f0]);
+#pragma unroll
+        for (int k = 0; k < FPL; ++k) dxu[u][k] += ds * sv[k];
+      }
+    }
+  }
+  __syncthreads();
+  sp[0][tk] = dscur;  // (sub 0..3 write the same value)
+  __syncthreads();
+
+  // ---- row layout: the current segment's term and the stores
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int tkr = u * (kMemoThreads / 16) + row;
+    if (tb + tkr >= NT) continue;  // (uniform over the row)
+    const size_t e = ((size_t)chain * NT + tb + tkr) * F + f0;
+    if (iu[u] > 0) {
+      const float dsc = sp[0][tkr];
+      const VT sv = *reinterpret_cast<const VT*>(summ + (size_t)iu[u] * F + f0);
+#pragma unroll
+      for (int k = 0; k < FPL; ++k) dxu[u][k] += dsc * sv[k];
+    }
+    float dq[FPL];
+#pragma unroll
+    for (int k = 0; k < FPL; ++k) dq[k] = gcr[u] * dout[u][k];
+    store_n<FPL>(static_cast<T*>(p.dXU) + e, dxu[u]);
+    store_n<FPL>(static_cast<T*>(p.dXQW) + e, dq);
   }
 }
 
@@ -468,12 +538,12 @@ __global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) 
 template <typename T, int FT, int HTT>
 static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
   const dim3 grid(p.B * p.H * ((p.nchunk + 1) / 2)), block(64 * kMemoWaves);
-  const int nblk = (p.NC * 16 + kMemoThreads - 1) / kMemoThreads;
+  const int nrow = (p.NC * 16 + kTokBlk - 1) / kTokBlk;  // workgroups per chain of the gate and finish kernels
   if (bwd) {
     hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, true>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);
+    hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H * nrow), dim3(kMemoThreads), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((memo_dxk_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(kSegThreads), 0, stream, p);
@@ -482,7 +552,7 @@ static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t st
   hipLaunchKernelGGL((memo_summary_kernel<T, 16 * FT>), dim3(p.B * p.H * p.NS), dim3(kSegThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H * nblk), dim3(kMemoThreads), 0, stream, p);
+  hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H * nrow), dim3(kMemoThreads), 0, stream, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, false>), grid, block, 0, stream, p);

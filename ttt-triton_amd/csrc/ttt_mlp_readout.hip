@@ -16,15 +16,13 @@
 //
 // W is read from HBM once per workgroup; blocks are mapped so that the chunks
 // of one chain run on one XCD and share its L2.
+#include "ttt_fixed_mlp.h"
 #include "ttt_kernels.h"
 
 namespace ttt {
 
 template <typename T, int FT, int HTT> struct ReadoutShared {
-  typename FragT<T>::type w1[FT * HTT][64];  // block (kb, ht): W1[16kb + 4g + j][16ht + n]
-  typename FragT<T>::type w2[HTT * FT][64];  // block (ht, ct): W2[16ht + 4g + j][16ct + n]
-  float b1[16 * HTT];
-  float b2[16 * FT];
+  FixedMlpLds<T, FT, HTT> w;
   float lnw[16 * FT];
   float lnb[16 * FT];
 };
@@ -34,7 +32,7 @@ constexpr int kReadoutTilesPerWave = 4;
 constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave;  // tokens per workgroup
 
 template <typename T, int FT, int HTT>
-__global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpReadoutParams p) {
+__global__ __launch_bounds__(64 * kReadoutWaves, 2) void mlp_readout_kernel(MlpReadoutParams p) {
   constexpr int F = 16 * FT;
   constexpr int FF = 16 * HTT;
   constexpr int NT = kReadoutTilesPerWave;
@@ -72,83 +70,21 @@ __global__ __launch_bounds__(64 * kReadoutWaves) void mlp_readout_kernel(MlpRead
     }
   }
 
-  // ---- stage W1, W2, biases and LN parameters of this chain: every load of
-  //      a wave's blocks is issued before the first conversion, so their
-  //      latencies overlap instead of adding up block by block
+  // ---- stage W1, W2, biases and LN parameters of this chain
   {
-    constexpr int NB = FT * HTT / kReadoutWaves;  // blocks of W1 (and of W2) per wave
     const size_t S = (size_t)p.S;
-    const float* __restrict__ w1 = p.W1 + (size_t)chain * S * F * FF;
-    const float* __restrict__ w2 = p.W2 + (size_t)chain * S * FF * F;
-    f4 x1[NB], x2[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int blk = wave + kReadoutWaves * b, kb = blk / HTT, ht = blk - kb * HTT;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x1[b][j] = w1[(16 * kb + 4 * g + j) * FF + 16 * ht + n];
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int blk = wave + kReadoutWaves * b, ht = blk / FT, ct = blk - ht * FT;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x2[b][j] = w2[(16 * ht + 4 * g + j) * F + 16 * ct + n];
-    }
-    const float* __restrict__ b1 = p.b1 + (size_t)chain * S * FF;
-    const float* __restrict__ b2 = p.b2 + (size_t)chain * S * F;
-    for (int i = threadIdx.x; i < FF; i += 64 * kReadoutWaves) sh.b1[i] = b1[i];
+    stage_fixed_mlp<T, FT, HTT, kReadoutWaves>(sh.w, p.W1 + (size_t)chain * S * F * FF, p.b1 + (size_t)chain * S * FF,
+                                               p.W2 + (size_t)chain * S * FF * F, p.b2 + (size_t)chain * S * F);
     for (int i = threadIdx.x; i < F; i += 64 * kReadoutWaves) {
-      sh.b2[i] = b2[i];
       sh.lnw[i] = p.ln_w[h * F + i];
       sh.lnb[i] = p.ln_b[h * F + i];
     }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) sh.w1[wave + kReadoutWaves * b][l] = to_frag<T>(x1[b]).v;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) sh.w2[wave + kReadoutWaves * b][l] = to_frag<T>(x2[b]).v;
   }
   __syncthreads();
   if (nv <= 0) return;  // no barrier follows
 
-  Tile acc[NT][FT];  // Z2 + b2 (b2 rides in the accumulator)
-#pragma unroll
-  for (int c = 0; c < FT; ++c) {
-    const float b2 = sh.b2[16 * c + n];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t][c].v = f4{b2, b2, b2, b2};
-  }
-
-#pragma unroll 1
-  for (int ht = 0; ht < HTT; ht += 2) {
-    Frag<T> x2[2][NT];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      Frag<T> w1f[FT];
-#pragma unroll
-      for (int kb = 0; kb < FT; ++kb) w1f[kb].v = sh.w1[kb * HTT + ht + hh][l];
-      const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        Tile z;
-        z.v = bias;  // b1 rides in the accumulator
-#pragma unroll
-        for (int kb = 0; kb < FT; kb += 2) mma32(z.v, w1f[kb], w1f[kb + 1], xq[t][kb], xq[t][kb + 1]);
-        f4 a;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = gelu_tanh(z.v[j]);
-        x2[hh][t] = to_frag<T>(a);
-      }
-    }
-    Frag<T> q0[FT], q1[FT];
-#pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      q0[c].v = sh.w2[ht * FT + c][l];
-      q1[c].v = sh.w2[(ht + 1) * FT + c][l];
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int c = 0; c < FT; ++c) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0[c], q1[c]);
-  }
+  Tile acc[NT][FT];  // Z2 + b2
+  fixed_mlp_tiles<T, FT, HTT, NT>(sh.w, xq, acc);
 
   // ---- LayerNorm over the F features of each token row, residual, store.
   // The residual XQ comes from the operand frags by an exact transpose (an

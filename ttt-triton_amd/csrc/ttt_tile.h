@@ -38,6 +38,8 @@ namespace ttt {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
 struct Tile {
   f4 v;
@@ -212,6 +214,14 @@ __device__ __forceinline__ float sum_row16(float x) {
   x += dpp<0x121>(x);  // row_ror:1
   return x;
 }
+// max over the 16 lanes that share g (one DPP row)
+__device__ __forceinline__ float max_row16(float x) {
+  x = fmaxf(x, dpp<0x128>(x));
+  x = fmaxf(x, dpp<0x124>(x));
+  x = fmaxf(x, dpp<0x122>(x));
+  x = fmaxf(x, dpp<0x121>(x));
+  return x;
+}
 // sum over all 64 lanes, as a wave-uniform value: the row sums are
 // accumulated into row 3 with row_bcast:15 (rows 1, 3) and row_bcast:31
 // (rows 2, 3), and lane 63 is read out
@@ -269,6 +279,40 @@ __device__ __forceinline__ void store4(__bf16* __restrict__ p, f4 v) {
   *reinterpret_cast<bf4*>(p) = to_frag<__bf16>(v).v;
 }
 __device__ __forceinline__ void store4(float* __restrict__ p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+
+// N (2 or 4) consecutive values at p as fp32, one vector access
+template <int N> __device__ __forceinline__ void load_n(const float* __restrict__ p, float (&v)[N]) {
+  if constexpr (N == 4) {
+    const f4 x = *reinterpret_cast<const f4*>(p);
+    for (int k = 0; k < 4; ++k) v[k] = x[k];
+  } else {
+    const f2 x = *reinterpret_cast<const f2*>(p);
+    for (int k = 0; k < 2; ++k) v[k] = x[k];
+  }
+}
+template <int N> __device__ __forceinline__ void load_n(const __bf16* __restrict__ p, float (&v)[N]) {
+  if constexpr (N == 4) {
+    const bf4 x = *reinterpret_cast<const bf4*>(p);
+    for (int k = 0; k < 4; ++k) v[k] = (float)x[k];
+  } else {
+    const bf2 x = *reinterpret_cast<const bf2*>(p);
+    for (int k = 0; k < 2; ++k) v[k] = (float)x[k];
+  }
+}
+template <int N> __device__ __forceinline__ void store_n(float* __restrict__ p, const float (&v)[N]) {
+  if constexpr (N == 4) {
+    *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+  } else {
+    *reinterpret_cast<f2*>(p) = f2{v[0], v[1]};
+  }
+}
+template <int N> __device__ __forceinline__ void store_n(__bf16* __restrict__ p, const float (&v)[N]) {
+  if constexpr (N == 4) {
+    *reinterpret_cast<bf4*>(p) = bf4{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+  } else {
+    *reinterpret_cast<bf2*>(p) = bf2{(__bf16)v[0], (__bf16)v[1]};
+  }
+}
 
 // Store four values to X[r][c0 + 4g + j]
 __device__ __forceinline__ void store_f4(__bf16* __restrict__ x, int ld, int c0, f4 v) {
