@@ -72,7 +72,14 @@ def _lin_fwd(lib, **kw):
 
 def test_linear_fwd_validation(lib):
     assert _lin_fwd(lib, K=8) == E_SHAPE
-    assert _lin_fwd(lib, F=48) == E_SHAPE
+    assert _lin_fwd(lib, K=80) == E_SHAPE
+    assert _lin_fwd(lib, K=24) == E_SHAPE
+    assert _lin_fwd(lib, F=40) == E_SHAPE
+    assert _lin_fwd(lib, F=272) == E_SHAPE
+    # shapes outside the specialised kernels' set (K = 16, F in {32, 64}) take
+    # the general-shape kernels, whose forward needs the saved buffer
+    assert _lin_fwd(lib, K=64, F=32) == E_WS
+    assert _lin_fwd(lib, K=16, F=48) == E_WS
     assert _lin_fwd(lib, B=0) == E_SHAPE
     assert _lin_fwd(lib, dtype=7) == E_DTYPE
     assert _lin_fwd(lib, XQ=None) == E_NULL
@@ -98,6 +105,10 @@ def test_linear_saved_buffer(lib):
     assert lib.ttt_linear_saved_bytes(B, H, NC, K, 32) == B * H * NC * (3 * K * 32 * 4 + 256)
     assert lib.ttt_linear_saved_bytes(0, H, NC, K, F) == 0
     assert lib.ttt_linear_saved_bytes(B, H, NC, 8, F) == 0
+    # general shapes: the state entering every mini-batch plus fp32 scratch
+    gen = lib.ttt_linear_saved_bytes(B, H, NC, 64, 32)
+    assert gen >= B * H * NC * (32 * 32 + 32) * 4
+    assert _lin_fwd(lib, K=64, F=32, saved=P, saved_bytes=gen - 4) == E_WS
     assert _lin_fwd(lib, saved=P, saved_bytes=need - 4) == E_WS
     assert _lin_fwd(lib, saved=Q, saved_bytes=need) == E_ALIGN
     args = [P] * 9 + [B, H, NC, K, F, 4, F32, DENSE, 1e-8] + [P] * 8
@@ -122,8 +133,12 @@ def _mlp_fwd(lib, FF=256, M=0, memo=(None,) * 4, saved=None, saved_bytes=0, NC=1
 
 
 def test_mlp_fwd_validation(lib):
-    assert _mlp_fwd(lib, FF=96) == E_SHAPE
-    assert _mlp_fwd(lib, FF=512) == E_SHAPE
+    assert _mlp_fwd(lib, FF=72) == E_SHAPE
+    assert _mlp_fwd(lib, FF=2048) == E_SHAPE
+    # FF = 96 or 512, outside the specialised set, take the general-shape
+    # kernels: their forward needs the saved buffer
+    assert _mlp_fwd(lib, FF=96) == E_WS
+    assert _mlp_fwd(lib, FF=512) == E_WS
     assert _mlp_fwd(lib, dtype=3) == E_DTYPE
     assert _mlp_fwd(lib, memo=(P, P, P, None), M=2) == E_NULL
     assert _mlp_fwd(lib, memo=(P, P, P, P), M=0) == E_ARG
@@ -184,8 +199,9 @@ def _readout(lib, **kw):
 
 
 def test_readout_validation(lib):
-    assert _readout(lib, K=32) == E_SHAPE
-    assert _readout(lib, FF=32) == E_SHAPE
+    assert _readout(lib, K=8) == E_SHAPE
+    assert _readout(lib, FF=48) == E_SHAPE
+    assert _readout(lib, F=48) == E_SHAPE
     assert _readout(lib, NS=0) == E_SHAPE
     assert _readout(lib, S=0) == E_ARG
     assert _readout(lib, eps=-1.0) == E_ARG

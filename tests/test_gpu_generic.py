@@ -1,0 +1,158 @@
+"""The general-shape inner loops (mini-batch K in {32, 64}, hidden width FF =
+F = 32 as the reference's TTTMLP builds it, F = 16/48) against the CPU oracle:
+forward with every side output (out, final state, checkpoints, memo
+snapshots) and the backward's gradients of every input.  The reference's own
+model configuration (ModelConfig defaults, main.py: K = 64, model dim 128 over
+4 heads so F = 32, FF = F) is among the cases.
+
+Tolerances as for the specialised kernels: fp32 max-abs <= 1e-4, or 8 times
+the fp32 oracle's own error against fp64 where that is larger
+(tests/_util.fp32_bound); bf16 rel-L2 <= 2e-2."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import ttt_oracle as O
+from tests._util import fp32_bound, max_abs, oracle_linear_grads, oracle_mlp_grads, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_RTOL = 2e-2
+MLP_KEYS = ("ln_w", "ln_b", "W1", "b1", "W2", "b2", "XQ", "XV", "XK", "eta")
+LIN_KEYS = ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")
+
+
+def _say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _perturb(d, H, F_, seed, mlp=True):
+    gen = torch.Generator().manual_seed(seed)
+    d["ln_w"] = 1 + 0.2 * torch.randn(H, F_, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(H, F_, generator=gen)
+    d["b1"] = 0.1 * torch.randn(*d["b1"].shape, generator=gen)
+    if mlp:
+        d["b2"] = 0.1 * torch.randn(*d["b2"].shape, generator=gen)
+    return d
+
+
+def _check(mine: dict, ref: dict, ref32, dt):
+    bad = []
+    for k, v in mine.items():
+        if dt == torch.float32:
+            err, bound = max_abs(v, ref[k]), fp32_bound(ref[k], ref32[k])
+        else:
+            err, bound = rel_l2(v, ref[k]), BF16_RTOL
+        _say(f"  {k}: err {err:.3e} bound {bound:.3e}")
+        if err > bound:
+            bad.append(k)
+    assert not bad
+
+
+# (B, H, NC, K, F, FF, G, M, dtype, eta kind)
+MLP_CASES = [
+    (2, 4, 6, 64, 32, 32, 4, 2, torch.float32, "layer"),    # the reference's ModelConfig / main.py shape
+    (2, 4, 6, 64, 32, 32, 4, 2, torch.bfloat16, "layer"),
+    (1, 2, 4, 64, 64, 256, 3, 2, torch.float32, "causal"),
+    (1, 2, 4, 64, 64, 256, 3, 3, torch.bfloat16, "causal"),
+    (2, 2, 5, 32, 64, 64, 2, 2, torch.bfloat16, "causal"),
+    (1, 3, 7, 16, 32, 32, 3, 2, torch.float32, "causal"),   # FF = 32 at K = 16
+    (1, 2, 3, 48, 48, 96, 2, 1, torch.float32, "layer"),
+]
+
+
+@pytest.mark.parametrize("B,H,NC,K,F_,FF,G,M,dt,kind", MLP_CASES)
+def test_generic_mlp_forward(B, H, NC, K, F_, FF, G, M, dt, kind):
+    from ttt_amd.mlp import mlp_forward
+    _say(f"generic mlp fwd B{B} H{H} NC{NC} K{K} F{F_} FF{FF} G{G} M{M} {dt} {kind}")
+    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=FF, seed=K + F_ + FF, dtype=dt, eta_kind=kind), H, F_, 7)
+    g = to_dev(d)
+    out, ck, memo, last, _ = mlp_forward(*(g[k] for k in MLP_KEYS), G, M=M, want_ckpt=True, want_last=True)
+    torch.cuda.synchronize()
+    ref = O.mlp_forward_full(*(d[k].double() for k in MLP_KEYS), G=G, M=M)
+    ref32 = O.mlp_forward_full(*(d[k].float() for k in MLP_KEYS), G=G, M=M) if dt == torch.float32 else None
+    mine = {"out": out}
+    for i, nm in enumerate(("W1", "b1", "W2", "b2")):
+        mine[nm + "_last"] = last[i]
+        mine[nm + "_ckpt"] = ck[i]
+        mine[nm + "_memo"] = memo[i]
+    _check(mine, ref, ref32, dt)
+
+
+@pytest.mark.parametrize("B,H,NC,K,F_,FF,G,M,dt,kind", MLP_CASES)
+def test_generic_mlp_backward(B, H, NC, K, F_, FF, G, M, dt, kind):
+    from ttt_amd.mlp import mlp_backward, mlp_forward
+    _say(f"generic mlp bwd B{B} H{H} NC{NC} K{K} F{F_} FF{FF} G{G} {dt} {kind}")
+    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=FF, seed=K + F_ + FF + 1, dtype=dt, eta_kind=kind,
+                               with_grad=True), H, F_, 8)
+    g = to_dev(d)
+    out, ck, _, last, saved = mlp_forward(*(g[k] for k in MLP_KEYS), G, want_ckpt=True, want_last=True,
+                                          want_saved=True)
+    (dlw, dlb, dW1, db1, dW2, db2), (dxq, dxv, dxk, deta) = mlp_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    torch.cuda.synchronize()
+    mine = dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dW2=dW2, db2=db2, dln_w=dlw, dln_b=dlb)
+    ref = oracle_mlp_grads(d, d["dOut"], G=0)
+    ref32 = oracle_mlp_grads(d, d["dOut"], G=0, dtype=torch.float32) if dt == torch.float32 else None
+    _check(mine, ref, ref32, dt)
+
+
+LIN_CASES = [
+    (2, 4, 6, 64, 32, 4, torch.float32, "layer"),    # ModelConfig's default layer (ttt_linear) shape
+    (2, 4, 6, 64, 32, 4, torch.bfloat16, "layer"),
+    (1, 3, 5, 32, 64, 2, torch.float32, "causal"),
+    (1, 2, 4, 16, 48, 3, torch.float32, "causal"),
+    (1, 2, 3, 64, 64, 1, torch.bfloat16, "causal"),
+]
+
+
+@pytest.mark.parametrize("B,H,NC,K,F_,G,dt,kind", LIN_CASES)
+def test_generic_linear_forward_backward(B, H, NC, K, F_, G, dt, kind):
+    from ttt_amd.linear import linear_backward, linear_forward
+    _say(f"generic linear B{B} H{H} NC{NC} K{K} F{F_} G{G} {dt} {kind}")
+    d = _perturb(O.make_inputs(B, H, NC, K, F_, seed=K + F_ + 3, dtype=dt, eta_kind=kind, with_grad=True), H, F_, 9,
+                 mlp=False)
+    g = to_dev(d)
+    out, ck, last, saved = linear_forward(*(g[k] for k in LIN_KEYS), G, want_ckpt=True, want_last=True,
+                                          want_saved=True)
+    (dlw, dlb, dW1, db1), (dxq, dxv, dxk, deta) = linear_backward(
+        g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck[0], last[0], saved, g["dOut"], G)
+    torch.cuda.synchronize()
+    ref = O.linear_forward_full(*(d[k].double() for k in LIN_KEYS), G=G)
+    ref32 = O.linear_forward_full(*(d[k].float() for k in LIN_KEYS), G=G) if dt == torch.float32 else None
+    _check({"out": out, "W1_last": last[0], "b1_last": last[1], "W1_ckpt": ck[0], "b1_ckpt": ck[1]}, ref, ref32, dt)
+    gref = oracle_linear_grads(d, d["dOut"], G=0)
+    gref32 = oracle_linear_grads(d, d["dOut"], G=0, dtype=torch.float32) if dt == torch.float32 else None
+    _check(dict(dXQ=dxq, dXV=dxv, dXK=dxk, deta=deta, dW1=dW1, db1=db1, dln_w=dlw, dln_b=dlb), gref, gref32, dt)
+
+
+@pytest.mark.parametrize("kind", ["layer", "causal"])
+def test_generic_lr_rules_match_dense(kind):
+    """lr [B,H,NC,K] expanded on chip by the rule equals the dense eta the host
+    builds from the same lr (bitwise in fp32: the same coefficients), and dlr
+    is the rule's contraction of the dense deta."""
+    from ttt_amd.mlp import mlp_backward, mlp_forward
+    B, H, NC, K, F_, FF, G = 1, 2, 3, 64, 32, 32, 2
+    _say(f"generic lr rule {kind} K{K}")
+    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=FF, seed=77, with_grad=True), H, F_, 10)
+    gen = torch.Generator().manual_seed(78)
+    lr = torch.sigmoid(torch.randn(B, H, NC, K, generator=gen)) / F_
+    d["eta"] = O.eta_from_lr(lr, kind)
+    g = to_dev(d)
+    res = {}
+    for rule, eta in (("dense", g["eta"]), (kind, lr.cuda())):
+        out, ck, _, last, saved = mlp_forward(*(g[k] for k in MLP_KEYS[:-1]), eta, G, want_ckpt=True,
+                                              want_last=True, want_saved=True, eta_rule=rule)
+        grads = mlp_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], eta, ck, last, saved, g["dOut"], G,
+                             eta_rule=rule)
+        res[rule] = (out, grads)
+    torch.cuda.synchronize()
+    assert torch.equal(res["dense"][0], res[kind][0])
+    deta = res["dense"][1][1][3].double().cpu()
+    i = torch.arange(K, dtype=torch.float64)
+    coef = (torch.full((K, K), 1.0 / K, dtype=torch.float64) if kind == "layer"
+            else torch.tril(torch.ones(K, K, dtype=torch.float64)) / (i + 1)[:, None])
+    dlr_ref = (deta * coef).sum(-2)
+    assert max_abs(res[kind][1][1][3], dlr_ref) <= 1e-4 * max(1.0, float(dlr_ref.abs().max()))

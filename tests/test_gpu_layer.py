@@ -4,7 +4,8 @@ against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
 Tolerances: fp32 activations max-abs 1e-4 for the elementwise kernels (they
 compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the north star's bar); the
 whole forecaster in fp32 rel-L2 1e-4 per tensor (a composition of four
-kernels, three GEMMs and the inner loop, each within fp32 rounding)."""
+kernels, three GEMMs and the inner loop, each within fp32 rounding), in bf16
+rel-L2 2e-2 per tensor with the norm floor described at the test."""
 
 import sys
 
@@ -19,6 +20,7 @@ pytestmark = pytest.mark.gpu
 FP32_ATOL = 1e-4
 BF16_RTOL = 2e-2
 FP32_RTOL_E2E = 1e-4
+BF16_FLOOR = 1e-2
 
 
 def _say(*a):
@@ -122,10 +124,10 @@ def test_post_norm_vs_oracle(F_, H, dt):
     assert not bad
 
 
-def _forecaster(kind, B, L, H, F_, M, seed):
+def _forecaster(kind, B, L, H, F_, M, seed, K=16):
     from ttt_amd import series
     from ttt_amd.model import ModelConfig, TTTForecaster
-    cfg = ModelConfig(seq_len=L, model_dim=H * F_, num_heads=H, ssm_layer=kind, mini_batch_size=16,
+    cfg = ModelConfig(seq_len=L, model_dim=H * F_, num_heads=H, ssm_layer=kind, mini_batch_size=K,
                       ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=M, scan_checkpoint_group_size=16)
     torch.manual_seed(seed)
     model = TTTForecaster(cfg, d_in=7, d_out=7, pred_len=96)
@@ -134,17 +136,23 @@ def _forecaster(kind, B, L, H, F_, M, seed):
     return cfg, model, x, y[:, -96:, :]
 
 
-@pytest.mark.parametrize("kind,M,dt", [("ttt_mlp", 2, torch.float32), ("ttt_mlp", 2, torch.bfloat16),
-                                       ("ttt_linear", 0, torch.float32)])
-def test_forecaster_train_step_vs_oracle(kind, M, dt):
-    """One training step of the end-to-end forecaster at the benchmark's
-    shape (lookback 512, horizon 96, 7 channels, H=4 heads of F=64, K=16,
-    memo segments of M=2, checkpoint groups of 16) at batch 2: the loss and
+@pytest.mark.parametrize("kind,M,dt,K,F_", [("ttt_mlp", 2, torch.float32, 16, 64),
+                                             ("ttt_mlp", 2, torch.bfloat16, 16, 64),
+                                             ("ttt_linear", 0, torch.float32, 16, 64),
+                                             ("ttt_mlp", 2, torch.float32, 64, 32),
+                                             ("ttt_mlp", 2, torch.bfloat16, 64, 32),
+                                             ("ttt_linear", 0, torch.float32, 64, 32)])
+def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
+    """One training step of the end-to-end forecaster at batch 2: the loss and
     the gradient of every parameter against the oracle in fp64 on the same
-    weights and windows."""
-    B, L, H, F_ = 2, 512, 4, 64
-    _say(f"forecaster {kind} M{M} {dt} B{B} L{L} H{H} F{F_}")
-    cfg, model, x, y = _forecaster(kind, B, L, H, F_, M, seed=91)
+    weights and windows.  K = 16, F = 64 is the benchmark's shape (lookback
+    512, horizon 96, 7 channels, H = 4 heads, memo segments of M = 2,
+    checkpoint groups of 16); K = 64, F = 32 (model dim 128) is the
+    reference's own ModelConfig / main.py shape, on the general-shape
+    kernels."""
+    B, L, H = 2, 512, 4
+    _say(f"forecaster {kind} M{M} {dt} B{B} L{L} H{H} F{F_} K{K}")
+    cfg, model, x, y = _forecaster(kind, B, L, H, F_, M, seed=91, K=K)
     sd = {k: v.detach().double().requires_grad_(True) for k, v in model.state_dict().items()}
     pred = LO.forecaster_forward(sd, x.double(), cfg, 96, 7)
     loss_ref = torch.nn.functional.mse_loss(pred, y.double())
@@ -160,13 +168,20 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt):
     err = abs(loss.item() - loss_ref.item()) / abs(loss_ref.item())
     _say(f"  loss {loss.item():.6f} vs {loss_ref.item():.6f}: rel {err:.3e}")
     bad = ["loss"] if err > tol else []
+    # bf16: rel-L2 per tensor, against a norm floor of BF16_FLOOR times the
+    # largest parameter gradient.  The XU projection's gradient enters only
+    # through the memory-cache gates and is 1e-4 of the rest at K = 64
+    # (1e-3 at K = 16): bf16 rounding of the gate terms sets its error there,
+    # while the fp32 runs hold it to ~1e-4 relative.
+    floor = 0.0 if dt == torch.float32 else BF16_FLOOR * max(
+        float(sd[n].grad.norm()) for n, _ in model.named_parameters() if sd[n].grad is not None)
     for name, prm in model.named_parameters():
         r = sd[name].grad
         if r is None:
             assert prm.grad is None or float(prm.grad.abs().max()) == 0.0, name
             continue
-        e = rel_l2(prm.grad, r)
-        _say(f"  d{name}: rel-L2 {e:.3e} (|ref| {float(r.norm()):.3e})")
+        e = float((prm.grad.detach().double().cpu() - r.detach().double()).norm()) / max(float(r.norm()), floor)
+        _say(f"  d{name}: rel-L2 {rel_l2(prm.grad, r):.3e} (|ref| {float(r.norm()):.3e}), bound ratio {e / tol:.2f}")
         if e > tol:
             bad.append(name)
     assert not bad

@@ -46,8 +46,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int check_common(int B, int H, int NC, int K, int F, int G, int dtype, float eps) {
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
   if (B <= 0 || H <= 0 || NC <= 0) return TTT_ERR_SHAPE;
-  if (K != 16) return TTT_ERR_SHAPE;
-  if (F != 32 && F != 64) return TTT_ERR_SHAPE;
+  if (K < 16 || K > 64 || K % 16 != 0) return TTT_ERR_SHAPE;
+  if (F < 16 || F > 256 || F % 16 != 0) return TTT_ERR_SHAPE;
   if (G < 1 || G > NC) return TTT_ERR_ARG;
   if (!(eps > 0.0f) || eps > 1.0f) return TTT_ERR_ARG;
   if ((long long)B * H > 0x7fffffffLL) return TTT_ERR_SHAPE;
@@ -66,6 +66,15 @@ int check_common(int B, int H, int NC, int K, int F, int G, int dtype, float eps
   } while (0)
 
 int hip_status(hipError_t e) { return e == hipSuccess ? TTT_OK : TTT_ERR_HIP; }
+
+// Shapes of the specialised inner-loop kernels (16-token mini-batches held in
+// registers); every other valid shape takes the general-shape kernels.
+bool fast_linear_shape(int K, int F) { return K == 16 && (F == 32 || F == 64); }
+bool fast_mlp_shape(int K, int F, int FF) {
+  return fast_linear_shape(K, F) && (FF == 64 || FF == 128 || FF == 256);
+}
+// the fixed-weight kernels (readout, memo combiner): any K, F in {32, 64}
+bool fixed_mlp_shape(int F, int FF) { return (F == 32 || F == 64) && (FF == 32 || FF == 64 || FF == 128 || FF == 256); }
 
 // TTT-MLP shapes: hidden width, and per-chain slabs addressable with 32-bit
 // byte offsets (the state checkpoints are the largest, NC * F * FF * 4 bytes)
@@ -105,8 +114,10 @@ const char* ttt_error_string(int status) {
 }
 
 size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F) {
-  if (B <= 0 || H <= 0 || NC <= 0 || K != 16 || (F != 32 && F != 64)) return 0;
-  return (size_t)B * H * NC * ttt::linear_saved_slot_bytes(F);
+  if (B <= 0 || H <= 0 || NC <= 0) return 0;
+  if (fast_linear_shape(K, F)) return (size_t)B * H * NC * ttt::linear_saved_slot_bytes(F);
+  if (ttt::gen_shape_ok(K, F, F, false)) return ttt::gen_saved_bytes(B, H, NC, K, F, F, false);
+  return 0;
 }
 
 int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
@@ -116,7 +127,7 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
-  st = check_linear(NC, F);
+  st = fast_linear_shape(K, F) ? check_linear(NC, F) : TTT_OK;
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
@@ -136,6 +147,36 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   if (saved != nullptr) {
     if (!aligned16(saved)) return TTT_ERR_ALIGN;
     if (saved_bytes < ttt_linear_saved_bytes(B, H, NC, K, F)) return TTT_ERR_WORKSPACE;
+  }
+  if (!fast_linear_shape(K, F)) {
+    if (saved == nullptr) return TTT_ERR_WORKSPACE;  // the general path's states and scratch
+    ttt::GenFwdParams q{};
+    q.XQ = XQ;
+    q.XK = XK;
+    q.XV = XV;
+    q.eta = eta;
+    q.ln_w = ln_w;
+    q.ln_b = ln_b;
+    q.W1_init = W1_init;
+    q.b1_init = b1_init;
+    q.out = out;
+    q.W1_last = W1_last;
+    q.b1_last = b1_last;
+    q.W1_ckpt = W1_ckpt;
+    q.b1_ckpt = b1_ckpt;
+    q.saved = saved;
+    q.B = B;
+    q.H = H;
+    q.NC = NC;
+    q.K = K;
+    q.F = F;
+    q.FF = F;
+    q.G = G;
+    q.M = 1;
+    q.eta_rule = eta_rule;
+    q.mlp = false;
+    q.eps = eps;
+    return hip_status(ttt::launch_gen_fwd(q, dtype, static_cast<hipStream_t>(stream)));
   }
 
   ttt::LinearFwdParams p;
@@ -172,7 +213,7 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
-  st = check_linear(NC, F);
+  st = fast_linear_shape(K, F) ? check_linear(NC, F) : TTT_OK;
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
@@ -194,6 +235,35 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   if (saved == nullptr) return TTT_ERR_WORKSPACE;
   if (!aligned16(saved)) return TTT_ERR_ALIGN;
   if (saved_bytes < ttt_linear_saved_bytes(B, H, NC, K, F)) return TTT_ERR_WORKSPACE;
+  if (!fast_linear_shape(K, F)) {
+    ttt::GenBwdParams q{};
+    q.XQ = XQ;
+    q.XK = XK;
+    q.XV = XV;
+    q.eta = eta;
+    q.dout = dout;
+    q.ln_w = ln_w;
+    q.ln_b = ln_b;
+    q.dXQ = dXQ;
+    q.dXK = dXK;
+    q.dXV = dXV;
+    q.deta = deta;
+    q.dW1 = dW1;
+    q.db1 = db1;
+    q.dln_w = dln_w;
+    q.dln_b = dln_b;
+    q.saved = const_cast<void*>(saved);
+    q.B = B;
+    q.H = H;
+    q.NC = NC;
+    q.K = K;
+    q.F = F;
+    q.FF = F;
+    q.eta_rule = eta_rule;
+    q.mlp = false;
+    q.eps = eps;
+    return hip_status(ttt::launch_gen_bwd(q, dtype, static_cast<hipStream_t>(stream)));
+  }
 
   ttt::LinearBwdParams p;
   p.XQ = XQ;
@@ -232,7 +302,9 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 float* b2_memo, void* saved, size_t saved_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
-  st = check_mlp(NC, F, FF, dtype);
+  const bool fast = fast_mlp_shape(K, F, FF);
+  if (!fast && !ttt::gen_shape_ok(K, F, FF, true)) return TTT_ERR_SHAPE;
+  st = fast ? check_mlp(NC, F, FF, dtype) : TTT_OK;
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   REQUIRE_PTR(XQ);
@@ -260,6 +332,46 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   if (saved != nullptr) {
     if (!aligned16(saved)) return TTT_ERR_ALIGN;
     if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  }
+  if (!fast) {
+    if (saved == nullptr) return TTT_ERR_WORKSPACE;  // the general path's states and scratch
+    ttt::GenFwdParams q{};
+    q.XQ = XQ;
+    q.XK = XK;
+    q.XV = XV;
+    q.eta = eta;
+    q.ln_w = ln_w;
+    q.ln_b = ln_b;
+    q.W1_init = W1_init;
+    q.b1_init = b1_init;
+    q.W2_init = W2_init;
+    q.b2_init = b2_init;
+    q.out = out;
+    q.W1_last = W1_last;
+    q.b1_last = b1_last;
+    q.W2_last = W2_last;
+    q.b2_last = b2_last;
+    q.W1_ckpt = W1_ckpt;
+    q.b1_ckpt = b1_ckpt;
+    q.W2_ckpt = W2_ckpt;
+    q.b2_ckpt = b2_ckpt;
+    q.W1_memo = W1_memo;
+    q.b1_memo = b1_memo;
+    q.W2_memo = W2_memo;
+    q.b2_memo = b2_memo;
+    q.saved = saved;
+    q.B = B;
+    q.H = H;
+    q.NC = NC;
+    q.K = K;
+    q.F = F;
+    q.FF = FF;
+    q.G = G;
+    q.M = W1_memo != nullptr ? M : 1;
+    q.eta_rule = eta_rule;
+    q.mlp = true;
+    q.eps = eps;
+    return hip_status(ttt::launch_gen_fwd(q, dtype, static_cast<hipStream_t>(stream)));
   }
 
   ttt::MlpFwdParams p;
@@ -304,13 +416,18 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
-  return (size_t)B * H * NC * ttt::mlp_saved_slot_bytes(F, FF, dtype);
+  if (fast_mlp_shape(K, F, FF)) return (size_t)B * H * NC * ttt::mlp_saved_slot_bytes(F, FF, dtype);
+  if (ttt::gen_shape_ok(K, F, FF, true)) return ttt::gen_saved_bytes(B, H, NC, K, F, FF, true);
+  return 0;
 }
 
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
-  return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
+  if (fast_mlp_shape(K, F, FF))
+    return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
+  if (ttt::gen_shape_ok(K, F, FF, true)) return 256;  // (the general path keeps its scratch in `saved`)
+  return 0;
 }
 
 static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
@@ -322,7 +439,9 @@ static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const vo
                 size_t workspace_bytes, void* stream) {
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
-  st = check_mlp(NC, F, FF, dtype);
+  const bool fast = fast_mlp_shape(K, F, FF);
+  if (!fast && !ttt::gen_shape_ok(K, F, FF, true)) return TTT_ERR_SHAPE;
+  st = fast ? check_mlp(NC, F, FF, dtype) : TTT_OK;
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
   (void)b1_ckpt;  // not read: the saved values carry the rest of the state
@@ -338,6 +457,37 @@ static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const vo
   if (workspace == nullptr) return TTT_ERR_WORKSPACE;
   if (!aligned16(workspace)) return TTT_ERR_ALIGN;
   if (workspace_bytes < ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  if (!fast) {
+    ttt::GenBwdParams q{};
+    q.XQ = XQ;
+    q.XK = XK;
+    q.XV = XV;
+    q.eta = eta;
+    q.dout = dout;
+    q.ln_w = ln_w;
+    q.ln_b = ln_b;
+    q.dXQ = dXQ;
+    q.dXK = dXK;
+    q.dXV = dXV;
+    q.deta = deta;
+    q.dW1 = dW1;
+    q.db1 = db1;
+    q.dW2 = dW2;
+    q.db2 = db2;
+    q.dln_w = dln_w;
+    q.dln_b = dln_b;
+    q.saved = const_cast<void*>(saved);
+    q.B = B;
+    q.H = H;
+    q.NC = NC;
+    q.K = K;
+    q.F = F;
+    q.FF = FF;
+    q.eta_rule = eta_rule;
+    q.mlp = true;
+    q.eps = eps;
+    return hip_status(ttt::launch_gen_bwd(q, dtype, static_cast<hipStream_t>(stream)));
+  }
 
   ttt::MlpBwdParams p;
   p.XQ = XQ;
@@ -459,7 +609,7 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
                            int dtype, float eps, float* out, void* stream) {
   int st = check_common(B, H, NS, K, F, 1, dtype, eps);
   if (st != TTT_OK) return st;
-  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  if (!fixed_mlp_shape(F, FF)) return TTT_ERR_SHAPE;
   if (S < 1) return TTT_ERR_ARG;
   if ((long long)NS * K > 0x7fffffffLL / 64) return TTT_ERR_SHAPE;
   const void* req[] = {XQ, W1, b1, W2, b2, ln_w, ln_b, out};
@@ -487,9 +637,13 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
   return hip_status(ttt::launch_mlp_readout(p, dtype, static_cast<hipStream_t>(stream)));
 }
 
+// The combiner's kernels walk 16-token tiles: a mini-batch of K = 16 k tokens
+// is k tiles and a segment of M mini-batches M k tiles (same tokens, same
+// segments), so every K is handled as K = 16 with NC k mini-batches.
 size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M) {
-  if (B <= 0 || H <= 0 || NC <= 0 || K != 16 || (F != 32 && F != 64) || M < 1) return 0;
-  return (size_t)B * H * ttt::memo_gate_floats_per_chain(NC, K, F, M) * sizeof(float);
+  if (B <= 0 || H <= 0 || NC <= 0 || K < 16 || K > 64 || K % 16 != 0 || (F != 32 && F != 64) || M < 1) return 0;
+  const int k = K / 16;
+  return (size_t)B * H * ttt::memo_gate_floats_per_chain(NC * k, 16, F, M * k) * sizeof(float);
 }
 
 namespace {
@@ -497,7 +651,7 @@ int check_memo(int B, int H, int NC, int K, int F, int FF, int M, int dtype, flo
                const float* gates) {
   int st = check_common(B, H, NC, K, F, 1, dtype, eps);
   if (st != TTT_OK) return st;
-  if (FF != 64 && FF != 128 && FF != 256) return TTT_ERR_SHAPE;
+  if (!fixed_mlp_shape(F, FF)) return TTT_ERR_SHAPE;
   if (M < 1) return TTT_ERR_ARG;
   if ((NC + M - 1) / M > ttt::kMemoMaxStates) return TTT_ERR_SHAPE;
   if ((long long)NC * K * F > 0x7fffffffLL / 4) return TTT_ERR_SHAPE;
@@ -541,8 +695,9 @@ int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const v
   if (st != TTT_OK) return st;
   const void* req[] = {XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, out};
   for (const void* q : req) REQUIRE_PTR(q);
-  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC, F, FF, M,
-                                     eps, gates);
+  const int k = K / 16;  // 16-token tiles per mini-batch
+  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC * k, F, FF,
+                                     M * k, eps, gates);
   p.XK = XK;
   p.XU = XU;
   p.out = out;
@@ -559,8 +714,9 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
   if (st != TTT_OK) return st;
   const void* req[] = {XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, dout, dXK, dXU, dXQW};
   for (const void* q : req) REQUIRE_PTR(q);
-  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC, F, FF, M,
-                                     eps, gates);
+  const int k = K / 16;  // 16-token tiles per mini-batch
+  ttt::MlpMemoParams p = memo_params(XQ, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, B, H, NC * k, F, FF,
+                                     M * k, eps, gates);
   p.XU = XU;
   p.dout = dout;
   p.dXK = dXK;
@@ -574,7 +730,7 @@ namespace {
 int check_layer_io(int B, int L, int H, int K, int F, int dtype) {
   if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
   if (B <= 0 || L <= 0 || H <= 0) return TTT_ERR_SHAPE;
-  if (K != 16 || L % K != 0) return TTT_ERR_SHAPE;
+  if (K < 16 || K > 64 || K % 16 != 0 || L % K != 0) return TTT_ERR_SHAPE;
   if (F != 32 && F != 64) return TTT_ERR_SHAPE;
   if ((long long)H * F > ttt::layer_io_max_width()) return TTT_ERR_SHAPE;
   if ((long long)B * L > 0x7fffffffLL) return TTT_ERR_SHAPE;

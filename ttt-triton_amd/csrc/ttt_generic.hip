@@ -1,0 +1,720 @@
+// General-shape TTT inner loops (Linear and MLP) on gfx950: any mini-batch
+// size K, head dim F and hidden width FF that are multiples of 16 (K <= 64,
+// F <= 256, FF <= 1024), for the shapes the specialised kernels do not take
+// (those hold K = 16 and F in {32, 64} in registers, FF in {64, 128, 256}).
+// This is what the reference's own model configuration needs: TTTMLP sets
+// FF = F (ttt_layer.py:427-430) and ModelConfig defaults to K = 64 with
+// F = 32 (forecast.py:33-44).
+//
+// One workgroup of 256 threads per (batch, head) chain walks the mini-batches
+// in order (ops/ttt_linear.py:8-54, ops/ttt_mlp.py:9-67, dual form with the
+// full K x K eta).  All per-mini-batch matrices live in an fp32 scratch area
+// of the chain inside the caller's `saved` buffer (L2-resident for the small
+// shapes); every product is a cooperative fp32 GEMM in 4 x 4 register blocks,
+// every LayerNorm a row pass, with a workgroup barrier between dependent
+// steps.  The forward also stores the state entering every mini-batch there,
+// so the backward visits the mini-batches in reverse, recomputes one
+// mini-batch's forward values from its stored state and applies the
+// hand-derived gradient of that mini-batch (chain rule through the update,
+// the output LayerNorm, both dual-form attention products, the GELU and its
+// derivative, and the LayerNorm fused with the L2 loss).  Everything is fp32
+// whatever the activation type; the activations are converted on load.
+#include "ttt_eta.h"
+#include "ttt_kernels.h"
+
+namespace ttt {
+
+constexpr int kGenThreads = 256;
+constexpr int kGenMaxK = 64;
+
+__host__ __device__ GenLayout::GenLayout(int K_, int F_, int FF_, int NC_, bool mlp_) : K(K_), F(F_), FF(mlp_ ? FF_ : F_), NC(NC_), mlp(mlp_) {
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off += (n + 3) & ~(size_t)3;
+    return o;
+  };
+  state = mlp ? (size_t)F * FF + FF + (size_t)FF * F + F : (size_t)F * F + F;
+  state = (state + 3) & ~(size_t)3;
+  states = take(state * NC);
+  wfin = take(state);
+  const size_t KF = (size_t)K * F, KK = (size_t)K * K, KH = (size_t)K * FF;
+  xq = take(KF), xk = take(KF), xv = take(KF), dout = take(KF);
+  eta = take(KK), a1 = take(KK), c1 = take(KK), a2 = take(KK), c2 = take(KK);
+  deta = take(KK), da1 = take(KK), dc1 = take(KK), da2 = take(KK), dc2 = take(KK);
+  z1 = take(KH), x2 = take(KH), d1 = take(KH), dd1 = take(KH), p = take(KH), g1 = take(KH);
+  z1b = take(KH), x2b = take(KH), db = take(KH);
+  z2 = take(KF), z2h = take(KF), g2 = take(KF), z2b = take(KF), z2bh = take(KF);
+  sig2 = take(K), sigb = take(K), de = take(K);
+  t1 = take(KH), dg1 = take(KH), dx2 = take(KH), dx2b = take(KH), dz1b = take(KH), dp = take(KH), dz1 = take(KH);
+  t2 = take(KF), dg2 = take(KF), dz2b = take(KF), dz2 = take(KF), dxq = take(KF), dxk = take(KF), dxv = take(KF);
+  lnwt = take(KF), lnbt = take(KF);
+  per_chain = off;
+}
+
+namespace {
+
+// C[M x N] (row stride ldc) = alpha * op(A) op(B) (+ C when acc), with
+// op(A)[i][k] = ta ? A[k * lda + i] : A[i * lda + k] and likewise for B.
+// Thread t computes the 4 x 4 blocks t, t + 256, ...; a call that
+// accumulates into the C of an earlier call with the same M and N touches
+// the same blocks from the same thread, so no barrier is needed between the
+// two.  M, N, the strides and the pointers are multiples of 4 floats.
+__device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
+                   const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
+  const int nbj = N >> 2, nblk = (M >> 2) * nbj;
+  for (int blk = threadIdx.x; blk < nblk; blk += kGenThreads) {
+    const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
+    float c[4][4] = {};
+    for (int k = 0; k < Kd; ++k) {
+      f4 a, b;
+      if (ta) {
+        a = *reinterpret_cast<const f4*>(A + (size_t)k * lda + i0);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = A[(size_t)(i0 + r) * lda + k];
+      }
+      if (tb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[q] = B[(size_t)(j0 + q) * ldb + k];
+      } else {
+        b = *reinterpret_cast<const f4*>(B + (size_t)k * ldb + j0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[r][q] += a[r] * b[q];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      f4* out = reinterpret_cast<f4*>(C + (size_t)(i0 + r) * ldc + j0);
+      f4 v = f4{c[r][0], c[r][1], c[r][2], c[r][3]} * alpha;
+      if (acc) v += *out;
+      *out = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void copy_f(float* __restrict__ dst, const float* __restrict__ src, size_t n) {
+  for (size_t i = threadIdx.x; i < n; i += kGenThreads) dst[i] = src[i];
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p, size_t i) { return (float)p[i]; }
+
+// state views: W1 [F][FF], b1 [FF], W2 [FF][F], b2 [F] (Linear: W [F][F], b [F])
+struct State {
+  float *W1, *b1, *W2, *b2;
+  __device__ State(float* s, const GenLayout& L) {
+    W1 = s;
+    b1 = W1 + (size_t)L.F * L.FF;
+    W2 = b1 + L.FF;
+    b2 = L.mlp ? W2 + (size_t)L.FF * L.F : b1;
+  }
+};
+
+// the state given as separate tensors of one chain
+struct StatePtrs {
+  float *W1, *b1, *W2, *b2;
+};
+
+__device__ void copy_state_out(const State& s, StatePtrs d, const GenLayout& L, size_t k) {
+  const size_t F = L.F, FF = L.FF;
+  if (L.mlp) {
+    if (d.W1) copy_f(d.W1 + k * F * FF, s.W1, F * FF);
+    if (d.b1) copy_f(d.b1 + k * FF, s.b1, FF);
+    if (d.W2) copy_f(d.W2 + k * FF * F, s.W2, FF * F);
+    if (d.b2) copy_f(d.b2 + k * F, s.b2, F);
+  } else {
+    if (d.W1) copy_f(d.W1 + k * F * F, s.W1, F * F);
+    if (d.b1) copy_f(d.b1 + k * F, s.b1, F);
+  }
+}
+
+// Inner-loss LayerNorm fused with the L2 loss's gradient, row r of Z (bias
+// already added): its normalised row and sigma, and G = d loss / d Z
+// (ops/ttt_utils.py:21-48).
+__device__ void ln_l2_row(const float* z, const float* xv, const float* xk, const float* lw, const float* lb, int F,
+                          float eps, float* zh, float* sig, float* G) {
+  float mu = 0.f;
+  for (int f = 0; f < F; ++f) mu += z[f];
+  mu /= (float)F;
+  float var = 0.f;
+  for (int f = 0; f < F; ++f) var += (z[f] - mu) * (z[f] - mu);
+  var /= (float)F;
+  const float s = sqrtf(var + eps);
+  float S1 = 0.f, S2 = 0.f;
+  for (int f = 0; f < F; ++f) {
+    const float xh = (z[f] - mu) / s;
+    zh[f] = xh;
+    const float g = lw[f] * (lw[f] * xh + lb[f] - (xv[f] - xk[f]));
+    S1 += g;
+    S2 += g * xh;
+  }
+  for (int f = 0; f < F; ++f) {
+    const float xh = zh[f];
+    const float g = lw[f] * (lw[f] * xh + lb[f] - (xv[f] - xk[f]));
+    G[f] = ((float)F * g - S1 - xh * S2) / ((float)F * s);
+  }
+  *sig = s;
+}
+
+struct GenArgs {
+  const void *XQ, *XK, *XV, *eta, *dout;
+  const float *ln_w, *ln_b;
+  const float *W1_init, *b1_init, *W2_init, *b2_init;
+  void* out;
+  StatePtrs last, ckpt, memo;
+  void *dXQ, *dXK, *dXV, *deta;
+  float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
+  float* saved;
+  int B, H, NC, K, F, FF, G, M, eta_rule;
+  bool mlp;
+  float eps;
+};
+
+// Forward values of mini-batch s from state S into the chain's scratch; with
+// `emit`, also its output rows and the state after it (into `next`).
+template <typename T>
+__device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, size_t chain, int s, const State& S,
+                             bool emit, const State* next) {
+  const int K = L.K, F = L.F, FF = L.FF;
+  const int h = (int)(chain % a.H);
+  const float* lw = a.ln_w + (size_t)h * F;
+  const float* lb = a.ln_b + (size_t)h * F;
+  const size_t row0 = (chain * a.NC + s) * K;  // first token row of the mini-batch
+  float *xq = sc + L.xq, *xk = sc + L.xk, *xv = sc + L.xv, *eta = sc + L.eta;
+  const T *XQ = static_cast<const T*>(a.XQ), *XK = static_cast<const T*>(a.XK), *XV = static_cast<const T*>(a.XV);
+  for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads) {
+    xq[i] = ld(XQ, row0 * F + i);
+    xk[i] = ld(XK, row0 * F + i);
+    xv[i] = ld(XV, row0 * F + i);
+  }
+  for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
+    const int r = i / K, c = i % K;
+    if (a.eta_rule == TTT_ETA_DENSE) {
+      eta[i] = ld(static_cast<const T*>(a.eta), (chain * a.NC + s) * K * K + i);
+    } else {
+      const float lr = static_cast<const float*>(a.eta)[row0 + c];
+      eta[i] = a.eta_rule == TTT_ETA_LAYER ? lr * (1.0f / (float)K) : (c <= r ? lr * (1.0f / (float)(r + 1)) : 0.0f);
+    }
+  }
+  __syncthreads();
+  float *a1 = sc + L.a1, *c1 = sc + L.c1, *g2 = sc + L.g2, *z2 = sc + L.z2, *z2h = sc + L.z2h, *sig2 = sc + L.sig2;
+  float *z2b = sc + L.z2b, *z2bh = sc + L.z2bh, *sigb = sc + L.sigb;
+  gg(a1, K, xq, F, false, xk, F, true, K, K, F, 1.f, false);
+  if (L.mlp) {
+    float *z1 = sc + L.z1, *x2 = sc + L.x2, *d1 = sc + L.d1, *dd1 = sc + L.dd1, *p = sc + L.p, *g1 = sc + L.g1;
+    float *z1b = sc + L.z1b, *x2b = sc + L.x2b, *db = sc + L.db, *a2 = sc + L.a2, *c2 = sc + L.c2;
+    gg(z1, FF, xk, F, false, S.W1, FF, false, K, FF, F, 1.f, false);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
+      float y, dy, ddy;
+      gelu_all(z1[i] + S.b1[i % FF], y, dy, ddy);
+      x2[i] = y;
+      d1[i] = dy;
+      dd1[i] = ddy;
+    }
+    for (int i = threadIdx.x; i < K * K; i += kGenThreads) c1[i] = eta[i] * (a1[i] + 1.0f);
+    __syncthreads();
+    gg(z2, F, x2, FF, false, S.W2, F, false, K, F, FF, 1.f, false);
+    __syncthreads();
+    for (int r = threadIdx.x; r < K; r += kGenThreads) {
+      float* zr = z2 + (size_t)r * F;
+      for (int f = 0; f < F; ++f) zr[f] += S.b2[f];
+      ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
+                g2 + (size_t)r * F);
+    }
+    __syncthreads();
+    gg(p, FF, g2, F, false, S.W2, F, true, K, FF, F, 1.f, false);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * FF; i += kGenThreads) g1[i] = p[i] * d1[i];
+    __syncthreads();
+    gg(z1b, FF, xq, F, false, S.W1, FF, false, K, FF, F, 1.f, false);
+    gg(z1b, FF, c1, K, false, g1, FF, false, K, FF, K, -1.f, true);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
+      float y, dy, ddy;
+      gelu_all(z1b[i] + S.b1[i % FF], y, dy, ddy);
+      x2b[i] = y;
+      db[i] = dy;
+    }
+    __syncthreads();
+    gg(a2, K, x2b, FF, false, x2, FF, true, K, K, FF, 1.f, false);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * K; i += kGenThreads) c2[i] = eta[i] * (a2[i] + 1.0f);
+    __syncthreads();
+    gg(z2b, F, x2b, FF, false, S.W2, F, false, K, F, FF, 1.f, false);
+    gg(z2b, F, c2, K, false, g2, F, false, K, F, K, -1.f, true);
+  } else {
+    gg(z2, F, xk, F, false, S.W1, F, false, K, F, F, 1.f, false);
+    __syncthreads();
+    for (int i = threadIdx.x; i < K * K; i += kGenThreads) c1[i] = eta[i] * (a1[i] + 1.0f);
+    for (int r = threadIdx.x; r < K; r += kGenThreads) {
+      float* zr = z2 + (size_t)r * F;
+      for (int f = 0; f < F; ++f) zr[f] += S.b1[f];
+      ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
+                g2 + (size_t)r * F);
+    }
+    __syncthreads();
+    gg(z2b, F, xq, F, false, S.W1, F, false, K, F, F, 1.f, false);
+    gg(z2b, F, c1, K, false, g2, F, false, K, F, K, -1.f, true);
+  }
+  __syncthreads();
+  // output LayerNorm and residual
+  const float* bo = L.mlp ? S.b2 : S.b1;
+  for (int r = threadIdx.x; r < K; r += kGenThreads) {
+    float* zr = z2b + (size_t)r * F;
+    float mu = 0.f;
+    for (int f = 0; f < F; ++f) {
+      zr[f] += bo[f];
+      mu += zr[f];
+    }
+    mu /= (float)F;
+    float var = 0.f;
+    for (int f = 0; f < F; ++f) var += (zr[f] - mu) * (zr[f] - mu);
+    var /= (float)F;
+    const float sd = sqrtf(var + a.eps);
+    sigb[r] = sd;
+    for (int f = 0; f < F; ++f) {
+      const float xh = (zr[f] - mu) / sd;
+      z2bh[(size_t)r * F + f] = xh;
+      if (emit) static_cast<T*>(a.out)[(row0 + r) * F + f] = (T)(xq[(size_t)r * F + f] + lw[f] * xh + lb[f]);
+    }
+  }
+  if (!emit) return;
+  // state after the mini-batch: W -= X^T diag(e) G, b -= G^T e with e = eta[K-1]
+  float* u1 = sc + L.t1;  // e-scaled G1 (MLP)
+  float* u2 = sc + L.t2;  // e-scaled G2 / G
+  const float* e = eta + (size_t)(K - 1) * K;
+  for (int i = threadIdx.x; i < K * F; i += kGenThreads) u2[i] = e[i / F] * g2[i];
+  if (L.mlp)
+    for (int i = threadIdx.x; i < K * FF; i += kGenThreads) u1[i] = e[i / FF] * sc[L.g1 + i];
+  copy_f(next->W1, S.W1, L.state);  // the whole state block
+  __syncthreads();
+  if (L.mlp) {
+    gg(next->W1, FF, xk, F, true, u1, FF, false, F, FF, K, -1.f, true);
+    gg(next->W2, F, sc + L.x2, FF, true, u2, F, false, FF, F, K, -1.f, true);
+    for (int c = threadIdx.x; c < FF; c += kGenThreads) {
+      float t = 0.f;
+      for (int r = 0; r < K; ++r) t += u1[(size_t)r * FF + c];
+      next->b1[c] -= t;
+    }
+    for (int c = threadIdx.x; c < F; c += kGenThreads) {
+      float t = 0.f;
+      for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
+      next->b2[c] -= t;
+    }
+  } else {
+    gg(next->W1, F, xk, F, true, u2, F, false, F, F, K, -1.f, true);
+    for (int c = threadIdx.x; c < F; c += kGenThreads) {
+      float t = 0.f;
+      for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
+      next->b1[c] -= t;
+    }
+  }
+  __syncthreads();
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs a) {
+  const size_t chain = blockIdx.x;
+  const GenLayout L(a.K, a.F, a.FF, a.NC, a.mlp);
+  float* base = a.saved + chain * L.per_chain;
+  auto state_at = [&](int s) { return State(base + L.states + (size_t)s * L.state, L); };
+  {
+    const State s0 = state_at(0);
+    const size_t F = L.F, FF = L.FF;
+    copy_f(s0.W1, a.W1_init + chain * F * FF, F * FF);
+    copy_f(s0.b1, a.b1_init + chain * FF, FF);
+    if (L.mlp) {
+      copy_f(s0.W2, a.W2_init + chain * FF * F, FF * F);
+      copy_f(s0.b2, a.b2_init + chain * F, F);
+    }
+  }
+  __syncthreads();
+  auto off = [&](StatePtrs p, size_t k0) {  // the chain's block of a [B,H,n,...] state tensor set
+    StatePtrs q = p;
+    const size_t F = L.F, FF = L.FF;
+    if (q.W1) q.W1 += k0 * F * FF;
+    if (q.b1) q.b1 += k0 * FF;
+    if (q.W2) q.W2 += k0 * FF * F;
+    if (q.b2) q.b2 += k0 * F;
+    return q;
+  };
+  const int NK = (a.NC + a.G - 1) / a.G, NS = (a.NC + a.M - 1) / a.M;
+  const StatePtrs ck = off(a.ckpt, chain * NK), mm = off(a.memo, chain * NS), la = off(a.last, chain);
+  for (int s = 0; s < a.NC; ++s) {
+    const State S = state_at(s);
+    if (s % a.G == 0) copy_state_out(S, ck, L, s / a.G);
+    const State nxt = s + 1 < a.NC ? state_at(s + 1) : State(base + L.wfin, L);
+    gen_step_fwd<T>(a, L, base, chain, s, S, true, &nxt);
+    if (a.memo.W1 && s % a.M == 0) copy_state_out(nxt, mm, L, s / a.M);
+    if (s + 1 == a.NC && a.last.W1) copy_state_out(nxt, la, L, 0);
+    __syncthreads();
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
+  const size_t chain = blockIdx.x;
+  const GenLayout L(a.K, a.F, a.FF, a.NC, a.mlp);
+  const int K = L.K, F = L.F, FF = L.FF;
+  const int h = (int)(chain % a.H);
+  const float* lw = a.ln_w + (size_t)h * F;
+  const float* lb = a.ln_b + (size_t)h * F;
+  float* sc = a.saved + chain * L.per_chain;
+  // gradient wrt the running state: starts at zero (the final state's gradient)
+  float* dW1 = a.dW1 + chain * (size_t)F * FF;
+  float* db1 = a.db1 + chain * (size_t)FF;
+  float* dW2 = L.mlp ? a.dW2 + chain * (size_t)FF * F : nullptr;
+  float* db2 = L.mlp ? a.db2 + chain * (size_t)F : nullptr;
+  float* dlnw = a.dln_w + chain * (size_t)F;
+  float* dlnb = a.dln_b + chain * (size_t)F;
+  for (int i = threadIdx.x; i < F * FF; i += kGenThreads) dW1[i] = 0.f;
+  for (int i = threadIdx.x; i < FF; i += kGenThreads) db1[i] = 0.f;
+  if (L.mlp) {
+    for (int i = threadIdx.x; i < FF * F; i += kGenThreads) dW2[i] = 0.f;
+    for (int i = threadIdx.x; i < F; i += kGenThreads) db2[i] = 0.f;
+  }
+  for (int i = threadIdx.x; i < F; i += kGenThreads) {
+    dlnw[i] = 0.f;
+    dlnb[i] = 0.f;
+  }
+  float *xq = sc + L.xq, *xk = sc + L.xk, *xv = sc + L.xv, *eta = sc + L.eta, *dout = sc + L.dout;
+  float *a1 = sc + L.a1, *c1 = sc + L.c1, *deta = sc + L.deta, *da1 = sc + L.da1, *dc1 = sc + L.dc1;
+  float *g2 = sc + L.g2, *z2h = sc + L.z2h, *sig2 = sc + L.sig2, *z2bh = sc + L.z2bh, *sigb = sc + L.sigb;
+  float *t2 = sc + L.t2, *dg2 = sc + L.dg2, *dz2b = sc + L.dz2b, *dz2 = sc + L.dz2;
+  float *dxq = sc + L.dxq, *dxk = sc + L.dxk, *dxv = sc + L.dxv, *de = sc + L.de, *lnwt = sc + L.lnwt,
+        *lnbt = sc + L.lnbt;
+  float *x2 = sc + L.x2, *d1 = sc + L.d1, *dd1 = sc + L.dd1, *p = sc + L.p, *g1 = sc + L.g1, *x2b = sc + L.x2b,
+        *dbv = sc + L.db, *a2 = sc + L.a2, *c2 = sc + L.c2, *da2 = sc + L.da2, *dc2 = sc + L.dc2;
+  float *t1 = sc + L.t1, *dg1 = sc + L.dg1, *dx2 = sc + L.dx2, *dx2b = sc + L.dx2b, *dz1b = sc + L.dz1b,
+        *dp = sc + L.dp, *dz1 = sc + L.dz1;
+  __syncthreads();
+  for (int s = a.NC - 1; s >= 0; --s) {
+    const State S(sc + L.states + (size_t)s * L.state, L);
+    gen_step_fwd<T>(a, L, sc, chain, s, S, false, nullptr);
+    const size_t row0 = (chain * a.NC + s) * K;
+    for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads)
+      dout[i] = ld(static_cast<const T*>(a.dout), row0 * F + i);
+    __syncthreads();
+    const float* e = eta + (size_t)(K - 1) * K;
+    // ---- through the state update W' = W - X^T diag(e) G, b' = b - G^T e
+    // (the running state gradient is dL/dW' here)
+    if (L.mlp) {
+      gg(t1, FF, xk, F, false, dW1, FF, false, K, FF, F, 1.f, false);  // XK dW1'
+      gg(t2, F, x2, FF, false, dW2, F, false, K, F, FF, 1.f, false);   // X2 dW2'
+      gg(dx2, FF, g2, F, false, dW2, F, true, K, FF, F, 1.f, false);   // G2 dW2'^T
+      gg(dxk, F, g1, FF, false, dW1, FF, true, K, F, FF, 1.f, false);  // G1 dW1'^T
+    } else {
+      gg(t2, F, xk, F, false, dW1, F, false, K, F, F, 1.f, false);   // XK dW'
+      gg(dxk, F, g2, F, false, dW1, F, true, K, F, F, 1.f, false);   // G dW'^T
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < K; r += kGenThreads) {
+      const float er = e[r];
+      float d = 0.f;
+      if (L.mlp) {
+        for (int c = 0; c < FF; ++c) {
+          const size_t i = (size_t)r * FF + c;
+          const float t = t1[i] + db1[c];
+          d -= t * g1[i];
+          dg1[i] = -er * t;
+          dx2[i] *= -er;
+        }
+        for (int c = 0; c < F; ++c) {
+          const size_t i = (size_t)r * F + c;
+          const float t = t2[i] + db2[c];
+          d -= t * g2[i];
+          dg2[i] = -er * t;
+          dxk[i] *= -er;
+        }
+      } else {
+        for (int c = 0; c < F; ++c) {
+          const size_t i = (size_t)r * F + c;
+          const float t = t2[i] + db1[c];
+          d -= t * g2[i];
+          dg2[i] = -er * t;
+          dxk[i] *= -er;
+        }
+      }
+      de[r] = d;
+      // ---- output LayerNorm: out = XQ + ln_w * zbh + ln_b
+      const float sd = sigb[r];
+      float m1 = 0.f, m2 = 0.f;
+      for (int f = 0; f < F; ++f) {
+        const float dh = dout[(size_t)r * F + f] * lw[f];
+        m1 += dh;
+        m2 += dh * z2bh[(size_t)r * F + f];
+      }
+      m1 /= (float)F;
+      m2 /= (float)F;
+      for (int f = 0; f < F; ++f) {
+        const size_t i = (size_t)r * F + f;
+        const float dh = dout[i] * lw[f];
+        dz2b[i] = (dh - m1 - z2bh[i] * m2) / sd;
+        dxq[i] = dout[i];
+      }
+    }
+    __syncthreads();
+    float* dbo = L.mlp ? db2 : db1;
+    for (int f = threadIdx.x; f < F; f += kGenThreads) {
+      float sw = 0.f, sb = 0.f, sz = 0.f;
+      for (int r = 0; r < K; ++r) {
+        const size_t i = (size_t)r * F + f;
+        sw += dout[i] * z2bh[i];
+        sb += dout[i];
+        sz += dz2b[i];
+      }
+      dlnw[f] += sw;
+      dlnb[f] += sb;
+      dbo[f] += sz;
+    }
+    if (L.mlp) {
+      // ---- Z2b = X2b W2 + b2 - (eta o (X2b X2^T + 1)) G2
+      gg(dW2, F, x2b, FF, true, dz2b, F, false, FF, F, K, 1.f, true);
+      gg(dx2b, FF, dz2b, F, false, S.W2, F, true, K, FF, F, 1.f, false);
+      gg(dc2, K, dz2b, F, false, g2, F, true, K, K, F, -1.f, false);
+      __syncthreads();
+      gg(dg2, F, c2, K, true, dz2b, F, false, K, F, K, -1.f, true);
+      for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
+        deta[i] = dc2[i] * (a2[i] + 1.0f);
+        da2[i] = dc2[i] * eta[i];
+      }
+      __syncthreads();
+      gg(dx2b, FF, da2, K, false, x2, FF, false, K, FF, K, 1.f, true);
+      gg(dx2, FF, da2, K, true, x2b, FF, false, K, FF, K, 1.f, true);
+      __syncthreads();
+      for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1b[i] = dx2b[i] * dbv[i];
+      __syncthreads();
+      // ---- Z1b = XQ W1 + b1 - (eta o (XQ XK^T + 1)) G1
+      for (int c = threadIdx.x; c < FF; c += kGenThreads) {
+        float t = 0.f;
+        for (int r = 0; r < K; ++r) t += dz1b[(size_t)r * FF + c];
+        db1[c] += t;
+      }
+      gg(dxq, F, dz1b, FF, false, S.W1, FF, true, K, F, FF, 1.f, true);
+      gg(dW1, FF, xq, F, true, dz1b, FF, false, F, FF, K, 1.f, true);
+      gg(dc1, K, dz1b, FF, false, g1, FF, true, K, K, FF, -1.f, false);
+      __syncthreads();
+      gg(dg1, FF, c1, K, true, dz1b, FF, false, K, FF, K, -1.f, true);
+      for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
+        deta[i] += dc1[i] * (a1[i] + 1.0f);
+        da1[i] = dc1[i] * eta[i];
+      }
+      __syncthreads();
+      gg(dxq, F, da1, K, false, xk, F, false, K, F, K, 1.f, true);
+      gg(dxk, F, da1, K, true, xq, F, false, K, F, K, 1.f, true);
+      // ---- G1 = (G2 W2^T) o gelu'(Z1)
+      for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
+        dp[i] = dg1[i] * d1[i];
+        dz1[i] = dg1[i] * p[i] * dd1[i];
+      }
+      __syncthreads();
+      gg(dg2, F, dp, FF, false, S.W2, F, false, K, F, FF, 1.f, true);
+      gg(dW2, F, dp, FF, true, g2, F, false, FF, F, K, 1.f, true);
+      __syncthreads();
+    } else {
+      // ---- Zb = XQ W + b - (eta o (XQ XK^T + 1)) G
+      gg(dW1, F, xq, F, true, dz2b, F, false, F, F, K, 1.f, true);
+      gg(dxq, F, dz2b, F, false, S.W1, F, true, K, F, F, 1.f, true);
+      gg(dc1, K, dz2b, F, false, g2, F, true, K, K, F, -1.f, false);
+      __syncthreads();
+      gg(dg2, F, c1, K, true, dz2b, F, false, K, F, K, -1.f, true);
+      for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
+        deta[i] = dc1[i] * (a1[i] + 1.0f);
+        da1[i] = dc1[i] * eta[i];
+      }
+      __syncthreads();
+      gg(dxq, F, da1, K, false, xk, F, false, K, F, K, 1.f, true);
+      gg(dxk, F, da1, K, true, xq, F, false, K, F, K, 1.f, true);
+      __syncthreads();
+    }
+    // ---- G = LN-fused-L2 gradient of Z (Z2 for the MLP): its backward
+    for (int r = threadIdx.x; r < K; r += kGenThreads) {
+      const float sd = sig2[r];
+      const float* xh = z2h + (size_t)r * F;
+      const float* q = dg2 + (size_t)r * F;
+      const float* Gr = g2 + (size_t)r * F;
+      float S2 = 0.f, Q1 = 0.f, Q2 = 0.f, QG = 0.f;
+      for (int f = 0; f < F; ++f) {
+        const size_t i = (size_t)r * F + f;
+        const float g = lw[f] * (lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]));
+        S2 += g * xh[f];
+        Q1 += q[f];
+        Q2 += q[f] * xh[f];
+        QG += q[f] * Gr[f];
+      }
+      const float inv = 1.0f / ((float)F * sd);
+      const float dsig = -QG / sd;
+      float m1 = 0.f, m2 = 0.f;
+      // pass 1: dg, dt, the LN-parameter terms and dxh (kept in dz2)
+      for (int f = 0; f < F; ++f) {
+        const size_t i = (size_t)r * F + f;
+        const float rr = lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]);
+        const float g = lw[f] * rr;
+        const float dg = ((float)F * q[f] - Q1 - xh[f] * Q2) * inv;
+        const float dxh = (-q[f] * S2 - g * Q2) * inv + dg * lw[f] * lw[f];
+        const float dt = -dg * lw[f];
+        dxv[i] = dt;
+        dxk[i] -= dt;
+        lnwt[i] = dg * (rr + lw[f] * xh[f]);
+        lnbt[i] = dg * lw[f];
+        dz2[i] = dxh;
+        m1 += dxh;
+        m2 += dxh * xh[f];
+      }
+      m1 /= (float)F;
+      m2 /= (float)F;
+      for (int f = 0; f < F; ++f) {
+        const size_t i = (size_t)r * F + f;
+        dz2[i] = (dz2[i] - m1 - xh[f] * m2) / sd + dsig * xh[f] / (float)F;
+      }
+    }
+    __syncthreads();
+    for (int f = threadIdx.x; f < F; f += kGenThreads) {
+      float sw = 0.f, sb = 0.f, sz = 0.f;
+      for (int r = 0; r < K; ++r) {
+        const size_t i = (size_t)r * F + f;
+        sw += lnwt[i];
+        sb += lnbt[i];
+        sz += dz2[i];
+      }
+      dlnw[f] += sw;
+      dlnb[f] += sb;
+      dbo[f] += sz;
+    }
+    if (L.mlp) {
+      // ---- Z2 = X2 W2 + b2, X2 = gelu(Z1), Z1 = XK W1 + b1
+      gg(dx2, FF, dz2, F, false, S.W2, F, true, K, FF, F, 1.f, true);
+      gg(dW2, F, x2, FF, true, dz2, F, false, FF, F, K, 1.f, true);
+      __syncthreads();
+      for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1[i] += dx2[i] * d1[i];
+      __syncthreads();
+      for (int c = threadIdx.x; c < FF; c += kGenThreads) {
+        float t = 0.f;
+        for (int r = 0; r < K; ++r) t += dz1[(size_t)r * FF + c];
+        db1[c] += t;
+      }
+      gg(dxk, F, dz1, FF, false, S.W1, FF, true, K, F, FF, 1.f, true);
+      gg(dW1, FF, xk, F, true, dz1, FF, false, F, FF, K, 1.f, true);
+    } else {
+      // ---- Z = XK W + b
+      gg(dxk, F, dz2, F, false, S.W1, F, true, K, F, F, 1.f, true);
+      gg(dW1, F, xk, F, true, dz2, F, false, F, F, K, 1.f, true);
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < K; j += kGenThreads) deta[(size_t)(K - 1) * K + j] += de[j];
+    __syncthreads();
+    // ---- this mini-batch's input gradients
+    T *DXQ = static_cast<T*>(a.dXQ), *DXK = static_cast<T*>(a.dXK), *DXV = static_cast<T*>(a.dXV);
+    for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads) {
+      DXQ[row0 * F + i] = (T)dxq[i];
+      DXK[row0 * F + i] = (T)dxk[i];
+      DXV[row0 * F + i] = (T)dxv[i];
+    }
+    if (a.eta_rule == TTT_ETA_DENSE) {
+      T* DE = static_cast<T*>(a.deta) + (chain * a.NC + s) * K * K;
+      for (int i = threadIdx.x; i < K * K; i += kGenThreads) DE[i] = (T)deta[i];
+    } else {
+      float* DL = static_cast<float*>(a.deta) + row0;
+      for (int j = threadIdx.x; j < K; j += kGenThreads) {
+        float t = 0.f;
+        for (int i = 0; i < K; ++i) {
+          const float coef = a.eta_rule == TTT_ETA_LAYER ? 1.0f / (float)K : (j <= i ? 1.0f / (float)(i + 1) : 0.f);
+          t += deta[(size_t)i * K + j] * coef;
+        }
+        DL[j] = t;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T> hipError_t launch_gen(const GenArgs& a, bool bwd, hipStream_t stream) {
+  if (bwd)
+    hipLaunchKernelGGL(gen_bwd_kernel<T>, dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(gen_fwd_kernel<T>, dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gen_shape_ok(int K, int F, int FF, bool mlp) {
+  if (K < 16 || K > kGenMaxK || K % 16) return false;
+  if (F < 16 || F > 256 || F % 16) return false;
+  if (mlp && (FF < 16 || FF > 1024 || FF % 16)) return false;
+  return true;
+}
+
+size_t gen_saved_bytes(int B, int H, int NC, int K, int F, int FF, bool mlp) {
+  return (size_t)B * H * GenLayout(K, F, FF, NC, mlp).per_chain * sizeof(float);
+}
+
+hipError_t launch_gen_fwd(const GenFwdParams& q, int dtype, hipStream_t stream) {
+  GenArgs a{};
+  a.XQ = q.XQ;
+  a.XK = q.XK;
+  a.XV = q.XV;
+  a.eta = q.eta;
+  a.ln_w = q.ln_w;
+  a.ln_b = q.ln_b;
+  a.W1_init = q.W1_init;
+  a.b1_init = q.b1_init;
+  a.W2_init = q.W2_init;
+  a.b2_init = q.b2_init;
+  a.out = q.out;
+  a.last = StatePtrs{q.W1_last, q.b1_last, q.W2_last, q.b2_last};
+  a.ckpt = StatePtrs{q.W1_ckpt, q.b1_ckpt, q.W2_ckpt, q.b2_ckpt};
+  a.memo = StatePtrs{q.W1_memo, q.b1_memo, q.W2_memo, q.b2_memo};
+  a.saved = static_cast<float*>(q.saved);
+  a.B = q.B;
+  a.H = q.H;
+  a.NC = q.NC;
+  a.K = q.K;
+  a.F = q.F;
+  a.FF = q.mlp ? q.FF : q.F;
+  a.G = q.G;
+  a.M = q.M;
+  a.eta_rule = q.eta_rule;
+  a.mlp = q.mlp;
+  a.eps = q.eps;
+  return dtype == TTT_DTYPE_BF16 ? launch_gen<__bf16>(a, false, stream) : launch_gen<float>(a, false, stream);
+}
+
+hipError_t launch_gen_bwd(const GenBwdParams& q, int dtype, hipStream_t stream) {
+  GenArgs a{};
+  a.XQ = q.XQ;
+  a.XK = q.XK;
+  a.XV = q.XV;
+  a.eta = q.eta;
+  a.dout = q.dout;
+  a.ln_w = q.ln_w;
+  a.ln_b = q.ln_b;
+  a.dXQ = q.dXQ;
+  a.dXK = q.dXK;
+  a.dXV = q.dXV;
+  a.deta = q.deta;
+  a.dW1 = q.dW1;
+  a.db1 = q.db1;
+  a.dW2 = q.dW2;
+  a.db2 = q.db2;
+  a.dln_w = q.dln_w;
+  a.dln_b = q.dln_b;
+  a.saved = static_cast<float*>(q.saved);
+  a.B = q.B;
+  a.H = q.H;
+  a.NC = q.NC;
+  a.K = q.K;
+  a.F = q.F;
+  a.FF = q.mlp ? q.FF : q.F;
+  a.G = 1;
+  a.M = 1;
+  a.eta_rule = q.eta_rule;
+  a.mlp = q.mlp;
+  a.eps = q.eps;
+  return dtype == TTT_DTYPE_BF16 ? launch_gen<__bf16>(a, true, stream) : launch_gen<float>(a, true, stream);
+}
+
+}  // namespace ttt

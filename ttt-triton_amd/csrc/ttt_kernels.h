@@ -201,4 +201,47 @@ int layer_io_max_width();
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t stream);
 
+// ---- general-shape inner loops (ttt_generic.hip): K, F, FF multiples of 16
+// outside the specialised kernels' set.  The `saved` buffer holds, per chain,
+// the state entering every mini-batch and the per-mini-batch fp32 scratch
+// (offsets in floats from the chain's block).
+struct GenLayout {
+  int K, F, FF, NC;
+  bool mlp;
+  size_t state;  // floats of one state (W1, b1[, W2, b2]), padded to 4
+  size_t states, wfin;
+  size_t xq, xk, xv, dout, eta, a1, c1, a2, c2, deta, da1, dc1, da2, dc2;
+  size_t z1, x2, d1, dd1, p, g1, z1b, x2b, db;
+  size_t z2, z2h, g2, z2b, z2bh, sig2, sigb, de;
+  size_t t1, dg1, dx2, dx2b, dz1b, dp, dz1, t2, dg2, dz2b, dz2, dxq, dxk, dxv, lnwt, lnbt;
+  size_t per_chain;
+  __host__ __device__ GenLayout(int K, int F, int FF, int NC, bool mlp);
+};
+struct GenFwdParams {
+  const void *XQ, *XK, *XV, *eta;
+  const float *ln_w, *ln_b, *W1_init, *b1_init, *W2_init, *b2_init;
+  void* out;
+  float *W1_last, *b1_last, *W2_last, *b2_last;
+  float *W1_ckpt, *b1_ckpt, *W2_ckpt, *b2_ckpt;
+  float *W1_memo, *b1_memo, *W2_memo, *b2_memo;
+  void* saved;
+  int B, H, NC, K, F, FF, G, M, eta_rule;
+  bool mlp;
+  float eps;
+};
+struct GenBwdParams {
+  const void *XQ, *XK, *XV, *eta, *dout;
+  const float *ln_w, *ln_b;
+  void *dXQ, *dXK, *dXV, *deta;
+  float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
+  void* saved;  // written by the forward with the same shapes
+  int B, H, NC, K, F, FF, eta_rule;
+  bool mlp;
+  float eps;
+};
+bool gen_shape_ok(int K, int F, int FF, bool mlp);
+size_t gen_saved_bytes(int B, int H, int NC, int K, int F, int FF, bool mlp);
+hipError_t launch_gen_fwd(const GenFwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_gen_bwd(const GenBwdParams& p, int dtype, hipStream_t stream);
+
 }  // namespace ttt

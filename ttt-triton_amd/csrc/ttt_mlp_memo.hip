@@ -562,6 +562,7 @@ static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t st
 template <typename T, int FT>
 static hipError_t launch_memo_f(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
   switch (p.FF) {
+    case 32: return launch_memo_t<T, FT, 2>(p, bwd, stream);
     case 64: return launch_memo_t<T, FT, 4>(p, bwd, stream);
     case 128: return launch_memo_t<T, FT, 8>(p, bwd, stream);
     case 256: return launch_memo_t<T, FT, 16>(p, bwd, stream);

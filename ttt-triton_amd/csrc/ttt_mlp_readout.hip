@@ -32,7 +32,7 @@ constexpr int kReadoutTilesPerWave = 4;
 constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave;  // tokens per workgroup
 
 template <typename T, int FT, int HTT>
-__global__ __launch_bounds__(64 * kReadoutWaves, 2) void mlp_readout_kernel(MlpReadoutParams p) {
+__global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void mlp_readout_kernel(MlpReadoutParams p) {
   constexpr int F = 16 * FT;
   constexpr int FF = 16 * HTT;
   constexpr int NT = kReadoutTilesPerWave;
@@ -142,6 +142,7 @@ static hipError_t launch_readout_t(const MlpReadoutParams& p, hipStream_t stream
 template <typename T, int FT>
 static hipError_t launch_readout_f(const MlpReadoutParams& p, hipStream_t stream) {
   switch (p.FF) {
+    case 32: return launch_readout_t<T, FT, 2>(p, stream);
     case 64: return launch_readout_t<T, FT, 4>(p, stream);
     case 128: return launch_readout_t<T, FT, 8>(p, stream);
     case 256: return launch_readout_t<T, FT, 16>(p, stream);

@@ -98,6 +98,17 @@ def check(status: int, what: str) -> None:
         raise ValueError(f"{what}: {msg} (status {status})")
 
 
+def fast_linear_shape(K: int, F: int) -> bool:
+    """Shapes of the specialised TTT-Linear kernels (16-token mini-batches in
+    registers); every other valid shape takes the general-shape kernels, whose
+    forward needs the saved buffer as scratch even without a backward."""
+    return K == 16 and F in (32, 64)
+
+
+def fast_mlp_shape(K: int, F: int, FF: int) -> bool:
+    return fast_linear_shape(K, F) and FF in (64, 128, 256)
+
+
 def eta_rule_code(rule) -> int:
     """ttt_eta_rule code of `rule` ("dense", "layer", "causal" or the code)."""
     if isinstance(rule, str):

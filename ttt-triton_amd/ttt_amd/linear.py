@@ -73,7 +73,7 @@ def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_
                 torch.empty((B, H, 1, F), device=dev, dtype=torch.float32))
     lib = _lib.load()
     saved = None
-    if want_saved:
+    if want_saved or not _lib.fast_linear_shape(K, F):
         nbytes = lib.ttt_linear_saved_bytes(B, H, NC, K, F)
         saved = torch.empty(nbytes, device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):

@@ -95,7 +95,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     none4 = (None, None, None, None)
     lib = _lib.load()
     saved = None
-    if want_saved:
+    if want_saved or not _lib.fast_mlp_shape(K, F, FF):
         saved = torch.empty(lib.ttt_mlp_saved_bytes(B, H, NC, K, F, FF, code), device=dev, dtype=torch.uint8)
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_fwd(

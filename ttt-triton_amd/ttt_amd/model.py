@@ -17,8 +17,11 @@ Per layer call, for hidden states x [B, L, D] (D = H*F):
 Parameter names and shapes are the reference's (wq ... wu, wo,
 learnable_ttt_lr_weight [H,1,D], learnable_ttt_lr_bias [H,1],
 ttt_norm_weight/bias [H,F], post_norm, W1/b1/W2/b2), so a reference state
-dict loads unchanged; the inner loop needs K = 16 and F in {32, 64}, and the
-MLP's hidden width (F, as TTTMLP builds it) in {64, 128, 256}."""
+dict loads unchanged.  Mini-batch size K and head dim F are multiples of 16
+(K <= 64); K = 16 with F in {32, 64} (and the MLP's hidden width F, as TTTMLP
+builds it, in {64, 128, 256}) runs on the specialised kernels, any other
+shape on the general-shape ones; the memory-cache combiner needs F in
+{32, 64}."""
 
 from __future__ import annotations
 
