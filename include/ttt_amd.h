@@ -4,9 +4,15 @@
  * Conventions shared by every entry point
  *   - Every pointer is device memory, contiguous, row-major, with the layouts
  *     given per argument.  B batch, H heads, NC mini-batches, K tokens per
- *     mini-batch (16), F head dim (32 or 64), FF MLP hidden width (F, 2F or
- *     4F, multiple of 64 up to 256), G checkpoint group size (1..NC),
- *     NK = ceil(NC / G).
+ *     mini-batch, F head dim, FF MLP hidden width, G checkpoint group size
+ *     (1..NC), NK = ceil(NC / G).  K, F and FF are multiples of 16 with
+ *     K <= 64, F <= 256, FF <= 1024.  K = 16 with F in {32, 64} (and, for the
+ *     MLP, FF in {64, 128, 256}) runs the specialised kernels; every other
+ *     shape runs the general-shape kernels, whose forward also needs the
+ *     `saved` buffer (it holds the state entering every mini-batch and the
+ *     per-mini-batch scratch; the backward reads it).  The fixed-weight
+ *     kernels (cached readout, memo combiner) take any K, F in {32, 64} and
+ *     FF in {32, 64, 128, 256}.
  *   - Activations (XQ, XK, XV, out and their gradients) share one dtype,
  *     `dtype` (TTT_DTYPE_F32 or TTT_DTYPE_BF16).  Fast-weight state, LayerNorm
  *     parameters, checkpoints, memo snapshots and weight gradients are fp32.
@@ -38,7 +44,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 8
+#define TTT_AMD_ABI_VERSION 9
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -86,8 +92,10 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
                    void* out, float* W1_last, float* b1_last, float* W1_ckpt, float* b1_ckpt,
                    void* saved, size_t saved_bytes, void* stream);
 
-/* Bytes of the saved buffer of ttt_linear_fwd / ttt_linear_bwd: B*H*NC
- * mini-batches x (3 * F * 64 + 256); 0 for unsupported sizes. */
+/* Bytes of the saved buffer of ttt_linear_fwd / ttt_linear_bwd: with the
+ * specialised kernels B*H*NC mini-batches x (3 * F * 64 + 256); with the
+ * general-shape kernels, per chain, the state entering every mini-batch and
+ * the fp32 scratch of one mini-batch; 0 for unsupported sizes. */
 size_t ttt_linear_saved_bytes(int B, int H, int NC, int K, int F);
 
 /* TTT-Linear backward: gradients of sum(out * dout) wrt every input, the
@@ -114,7 +122,7 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
 /* TTT-MLP forward (2-layer GELU(tanh) fast-weight MLP) over all NC
  * mini-batches.  Replaces ttt_mlp_scan_forward (kernels/mlp_forward.py:6-237)
  * as launched by TritonMLP._forward_core (mlp_triton.py:71-197), and is the
- * forward of ops.ttt_mlp (ops/ttt_mlp.py:70-99).  FF in {64, 128, 256}.
+ * forward of ops.ttt_mlp (ops/ttt_mlp.py:70-99).
  *   W1_init [B,H,F,FF], b1_init [B,H,1,FF], W2_init [B,H,FF,F], b2_init [B,H,1,F] fp32
  *   out               [B,H,NC,K,F] dtype
  *   *_last            final state, shapes of *_init (all four or none)
@@ -140,13 +148,17 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
                 float* W1_memo, float* b1_memo, float* W2_memo, float* b2_memo,
                 void* saved, size_t saved_bytes, void* stream);
 
-/* Bytes of the saved buffer of ttt_mlp_fwd / ttt_mlp_bwd: B*H*NC mini-batches
- * x ((7 FF + F) * K * sizeof(dtype) + (FF + F) * 4 + 3 * F * 64 + 4096). */
+/* Bytes of the saved buffer of ttt_mlp_fwd / ttt_mlp_bwd: with the
+ * specialised kernels B*H*NC mini-batches x ((7 FF + F) * K * sizeof(dtype)
+ * + (FF + F) * 4 + 3 * F * 64 + 4096); with the general-shape kernels, per
+ * chain, the state entering every mini-batch and the fp32 scratch of one
+ * mini-batch. */
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* Bytes of device workspace ttt_mlp_bwd needs: B*H*NC mini-batches x
  * (2 * FF * K * sizeof(dtype) + 2 * F * 64), then (4 + B*H*NC) 4-byte control
- * words rounded up to 256 bytes. */
+ * words rounded up to 256 bytes (specialised kernels); 256 with the
+ * general-shape kernels, which keep their scratch in `saved`. */
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
@@ -240,8 +252,8 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
                              void* stream);
 
 /* ---- the producer and consumer around the inner loop (ttt_layer.py) ----
- * Shapes: B batch, L = NC*K tokens, H heads, F head dim (32 or 64), K = 16,
- * D = H*F <= 1024.  Activations in `dtype`, everything else fp32. */
+ * Shapes: B batch, L = NC*K tokens, H heads, F head dim (32 or 64), K a
+ * multiple of 16 up to 64, D = H*F <= 1024.  Activations in `dtype`, everything else fp32. */
 
 /* Bytes of the per-block LayerNorm-parameter gradient partials of
  * ttt_qkvu_producer_bwd / ttt_post_norm_bwd: ceil(B*L/32) blocks x 2 x D

@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
