@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--eta lr|dense]
 
-Headline workload (configs[3]): TTT-MLP forward+backward, B=16, H=12,
+Headline workload: TTT-MLP forward+backward, B=16, H=12,
 T=2048 (NC=128 mini-batches of K=16), F=64, hidden 256, bf16 activations,
 fp32 fast-weight state, checkpoints every G=8 mini-batches; eta is the
 causal expansion eta[i][j] = lr[j]/(i+1) (j <= i) of the per-token learning
@@ -18,12 +18,12 @@ the per-kernel averages behind `roofline` come from the timed steps.
 MFMA-busy fraction of the launch) are read from the committed rocprofv3
 counter summaries under profiles/ when they exist for the kernel.
 
-Also measured, one line each in the JSON: configs[2] (TTT-Linear fwd+bwd,
-G=16), configs[1] (TTT-MLP forward at B=8, with and without memo M=2),
-configs[0] (TTT-Linear forward fp32 at B2 H4 T256), configs[4] (the
-end-to-end forecaster: one AdamW training step and inference at batch 32,
-lookback 512, horizon 96, 7 channels, H=4 heads of F=64, K=16, memo M=2,
-bf16 autocast), the cached readout and the memory-cache combiner.
+Also measured, one line each in the JSON: TTT-Linear fwd+bwd at the same
+shape (G=16), TTT-MLP forward at B=8 (with and without memo M=2), TTT-Linear
+forward fp32 at B2 H4 T256, the end-to-end forecaster (one AdamW training
+step and inference at batch 32, lookback 512, horizon 96, 7 channels, H=4
+heads of F=64, K=16, memo M=2, bf16 autocast), the cached readout and the
+memory-cache combiner.
 
 The CPU baselines time the oracle (the eager-PyTorch restatement of the
 reference's ops path, fp32, autograd for the backward) on this host's usable
@@ -59,7 +59,7 @@ B, H, T, K, F, FF = 16, 12, 2048, 16, 64, 256
 NC = T // K
 G_MLP, G_LIN = 8, 16
 MEMO_M = 8  # memo segment size (mini-batches) of the combiner leg
-# forecaster
+# the end-to-end forecaster (lookback 512, horizon 96, 7 channels, batch 32)
 FC_B, FC_L, FC_H, FC_F, FC_PRED, FC_CH, FC_M, FC_G = 32, 512, 4, 64, 96, 7, 2, 16
 
 
@@ -236,7 +236,7 @@ def cpu_baselines(budget_s, eta):
         res[key] = {"value": v, "unit": "tokens/s", "cores": cores, "kind": "port",
                     "sample": f"oracle {sample}, median of {n} runs, {med:.3f} s each"}
 
-    # configs[4]: the forecaster's training step (forward + backward) on 2 of the 32 windows
+    # the forecaster's training step (forward + backward) on 2 of the 32 windows
     print("[bench] CPU baseline c4", file=sys.stderr, flush=True)
     cfg, model, x, y = forecaster_setup(torch, 2)
     sd0 = {k: v.detach().float() for k, v in model.state_dict().items()}
@@ -388,7 +388,7 @@ def run_memo(torch, steps, warmup, only=None):
 
 
 def forecaster_setup(torch, batch):
-    """The configs[4] model (random init) and one batch of windows of the
+    """The end-to-end forecaster (random init) and one batch of windows of the
     synthetic ETTh1-shaped series (lookback 512, horizon 96, 7 channels)."""
     from ttt_amd import series
     from ttt_amd.model import ModelConfig, TTTForecaster
@@ -526,17 +526,17 @@ def main():
 
     print("[bench] TTT-Linear fwd+bwd", file=sys.stderr, flush=True)
     lk, ltotal = run_linear(torch, args.steps, args.warmup, eta)
-    print("[bench] configs[1]: TTT-MLP forward B8 (no memo, memo M=2)", file=sys.stderr, flush=True)
+    print("[bench] TTT-MLP forward B8 (no memo, memo M=2)", file=sys.stderr, flush=True)
     c1, c1_total, _ = run_mlp(torch, args.steps, args.warmup, eta, Bn=8, fwd_only=True, ckpt=False)
     c1m, c1m_total, _ = run_mlp(torch, args.steps, args.warmup, eta, Bn=8, memo=2, fwd_only=True, ckpt=False)
-    print("[bench] configs[0]: TTT-Linear forward fp32 B2 H4 T256", file=sys.stderr, flush=True)
+    print("[bench] TTT-Linear forward fp32 B2 H4 T256", file=sys.stderr, flush=True)
     c0, c0_total = run_linear(torch, args.steps, args.warmup, eta, Bn=2, H_=4, NC_=16, dtype=torch.float32,
                               fwd_only=True)
     print("[bench] cached readout", file=sys.stderr, flush=True)
     ro = run_readout(torch, args.steps, args.warmup)
     print(f"[bench] memory-cache combiner (M={MEMO_M})", file=sys.stderr, flush=True)
     mk = run_memo(torch, args.steps, args.warmup)
-    print("[bench] configs[4]: forecaster train step + inference", file=sys.stderr, flush=True)
+    print("[bench] forecaster train step + inference", file=sys.stderr, flush=True)
     fc_train, fc_inf, fc_wall_train, fc_wall_inf, fc_loss, _ = run_forecaster(torch, args.steps, args.warmup)
 
     state = mlp_state_floats()

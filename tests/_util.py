@@ -43,7 +43,7 @@ def oracle_mlp_grads(d: dict, dout: torch.Tensor, G: int, dtype=torch.float64):
     return res
 
 
-# fp32 parity bar: the north star's max-abs 1e-4, or, for a tensor whose own
+# fp32 parity bar: the required max-abs 1e-4, or, for a tensor whose own
 # fp32 evaluation is less exact than that (the eta gradient reaches 1e4 on
 # unnormalised N(0,1) inputs), C_FP32 times the error of the oracle run in fp32
 # against the oracle in fp64 on the same inputs.  The kernels' fp32 error is

@@ -2,7 +2,7 @@
 against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
 
 Tolerances: fp32 activations max-abs 1e-4 for the elementwise kernels (they
-compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the north star's bar); the
+compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the required bar); the
 whole forecaster in fp32 rel-L2 1e-4 per tensor (a composition of four
 kernels, three GEMMs and the inner loop, each within fp32 rounding), in bf16
 rel-L2 2e-2 per tensor with the norm floor described at the test."""

@@ -1,6 +1,6 @@
 """TTT-Linear HIP kernels vs the CPU oracle (forward, side outputs, backward).
 
-Tolerances (north star): fp32 activations max-abs <= 1e-4 against the ops
+Tolerances: fp32 activations max-abs <= 1e-4 against the ops
 path, or, where the tensor's own fp32 evaluation is less exact (the eta
 gradient), C_FP32 = 8 times the fp32 oracle's error against fp64
 (tests/_util.fp32_bound); bf16 activations with fp32 state rel-L2 <= 2e-2.
@@ -84,7 +84,7 @@ def test_linear_fwd_saved_buffer():
 
 @pytest.mark.parametrize("kind", ["causal", "layer"])
 def test_linear_fwd_fp32_config0(kind):
-    """B2 H4 T256 (NC16 K16) F64, fp32."""
+    """The CPU-runnable small case: B2 H4 T256 (NC16 K16) F64, fp32."""
     _say("linear fwd fp32 config0", kind)
     d = O.make_inputs(2, 4, 16, 16, 64, seed=0, dtype=torch.float32, eta_kind=kind)
     out, (Wc, bc), (Wl, bl) = _fwd(d, G=4)
