@@ -387,13 +387,14 @@ def run_memo(torch, steps, warmup, only=None):
     return {k: statistics.mean(v) for k, v in sp.items()}
 
 
-def forecaster_setup(torch, batch):
+def forecaster_setup(torch, batch, head_dim=FC_F, mini_batch=K):
     """The end-to-end forecaster (random init) and one batch of windows of the
     synthetic ETTh1-shaped series (lookback 512, horizon 96, 7 channels)."""
     from ttt_amd import series
     from ttt_amd.model import ModelConfig, TTTForecaster
-    cfg = ModelConfig(seq_len=FC_L, model_dim=FC_H * FC_F, num_heads=FC_H, ssm_layer="ttt_mlp", mini_batch_size=K,
-                      ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=FC_M, scan_checkpoint_group_size=FC_G)
+    cfg = ModelConfig(seq_len=FC_L, model_dim=FC_H * head_dim, num_heads=FC_H, ssm_layer="ttt_mlp",
+                      mini_batch_size=mini_batch, ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=FC_M,
+                      scan_checkpoint_group_size=FC_G)
     torch.manual_seed(0)
     model = TTTForecaster(cfg, d_in=FC_CH, d_out=FC_CH, pred_len=FC_PRED)
     data = series.synthetic_series(seed=0)
@@ -401,12 +402,12 @@ def forecaster_setup(torch, batch):
     return cfg, model, x, y[:, -FC_PRED:, :]
 
 
-def run_forecaster(torch, steps, warmup):
+def run_forecaster(torch, steps, warmup, head_dim=FC_F, mini_batch=K):
     """One AdamW training step (forward, loss, backward, gradient clipping,
     optimizer step; main.py:73-95 with bf16 autocast, no grad scaler needed)
     and one inference forward, at batch 32."""
     dev = torch.device("cuda:0")
-    cfg, model, x, y = forecaster_setup(torch, FC_B)
+    cfg, model, x, y = forecaster_setup(torch, FC_B, head_dim, mini_batch)
     model = model.to(dev)
     x, y = x.to(dev), y.to(dev)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=1e-2)
@@ -538,6 +539,8 @@ def main():
     mk = run_memo(torch, args.steps, args.warmup)
     print("[bench] forecaster train step + inference", file=sys.stderr, flush=True)
     fc_train, fc_inf, fc_wall_train, fc_wall_inf, fc_loss, _ = run_forecaster(torch, args.steps, args.warmup)
+    print("[bench] forecaster at the reference ModelConfig shape (K=64, F=FF=32)", file=sys.stderr, flush=True)
+    rc_train, rc_inf, _, _, rc_loss, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=32, mini_batch=64)
 
     state = mlp_state_floats()
     kernels = {
@@ -612,6 +615,12 @@ def main():
                 "shape": f"batch {FC_B}, lookback {FC_L}, horizon {FC_PRED}, {FC_CH} channels, TTT-MLP H={FC_H} "
                          f"F={FC_F} (model_dim {FC_H * FC_F}), K={K}, memo M={FC_M}, G={FC_G}, bf16 autocast, AdamW",
                 "cpu_baseline": cpu["c4"] if cpu else None},
+            "forecaster_reference_model_shape": {
+                "train_step_ms": round(rc_train * 1e3, 3), "train_tokens_per_s": round(FC_B * FC_L / rc_train, 1),
+                "inference_ms": round(rc_inf * 1e3, 3), "inference_tokens_per_s": round(FC_B * FC_L / rc_inf, 1),
+                "loss": round(rc_loss, 5),
+                "shape": f"as c4 with ModelConfig's defaults of main.py: model_dim 128 over H={FC_H} heads (F=32, "
+                         f"FF=32), K=64 (the general-shape kernels), memo M={FC_M}, G={FC_G}"},
         },
         "memo_combine": {
             "value": round(B * T / (mk["ttt_mlp_memo_combine"] + mk["ttt_mlp_memo_combine_bwd"]), 1),

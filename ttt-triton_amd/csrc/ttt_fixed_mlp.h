@@ -3,9 +3,11 @@
 //
 //   Z2 = gelu(X W1 + b1) W2 + b2        X: 16-token tiles, W1 [F x FF], W2 [FF x F]
 //
-// W1 and W2 sit in LDS in MFMA operand order, two K16 blocks of one lane
-// adjacent (FragPair), so the 32-deep operand of every MFMA is one 16-byte LDS
-// read (bf16).  The hidden dimension is walked two 16-unit tiles at a time:
+// W1 and W2 sit in LDS in MFMA operand order: the two K16 blocks that form
+// one 32-deep operand are stored as consecutive 64-lane blocks, so the operand
+// is one ds_read2st64 (two contiguous wave-wide reads, conflict-free) into
+// consecutive registers.  The hidden dimension is walked two 16-unit tiles at
+// a time:
 //
 //   Z1^T(pair) = W1^T X^T + b1      hidden x token (C layout = the A operand of
 //   X2^T       = gelu(Z1^T)          the next product, no transpose)
@@ -19,14 +21,10 @@
 
 namespace ttt {
 
-// Two K16 operand frags of one lane, adjacent.
-template <typename T> struct FragPair {
-  typename FragT<T>::type a, b;
-};
-
 template <typename T, int FT, int HTT> struct FixedMlpLds {
-  FragPair<T> w1[HTT][FT / 2][64];  // [ht][kp]: W1 blocks (2kp, ht), (2kp+1, ht); block (kb, ht) = W1[16kb + 4g + j][16ht + n]
-  FragPair<T> w2[HTT / 2][FT][64];  // [hp][ct]: W2 blocks (2hp, ct), (2hp+1, ct); block (ht, ct) = W2[16ht + 4g + j][16ct + n]
+  using V = typename FragT<T>::type;
+  V w1[HTT][FT / 2][2][64];  // [ht][kp][h]: W1 block (2kp + h, ht) = W1[16kb + 4g + j][16ht + n]
+  V w2[HTT / 2][FT][2][64];  // [hp][ct][h]: W2 block (2hp + h, ct) = W2[16ht + 4g + j][16ct + n]
   float b1[16 * HTT];
   float b2[16 * FT];
 };
@@ -66,16 +64,14 @@ __device__ __forceinline__ void stage_fixed_mlp(FixedMlpLds<T, FT, HTT>& sh, con
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int blk = wave + NWAVES * b, kb = blk / HTT, ht = blk - kb * HTT;
-      if (blk < NBLK)  // (uniform over the wave)
-        reinterpret_cast<typename FragT<T>::type*>(&sh.w1[ht][kb >> 1][l])[kb & 1] = to_frag<T>(x[b]).v;
+      if (blk < NBLK) sh.w1[ht][kb >> 1][kb & 1][l] = to_frag<T>(x[b]).v;  // (uniform over the wave)
     }
   };
   auto put_w2 = [&](const f4(&x)[NB]) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int blk = wave + NWAVES * b, ht = blk / FT, ct = blk - ht * FT;
-      if (blk < NBLK)
-        reinterpret_cast<typename FragT<T>::type*>(&sh.w2[ht >> 1][ct][l])[ht & 1] = to_frag<T>(x[b]).v;
+      if (blk < NBLK) sh.w2[ht >> 1][ct][ht & 1][l] = to_frag<T>(x[b]).v;
     }
   };
   if constexpr (sizeof(T) == 2) {
@@ -116,9 +112,8 @@ __device__ __forceinline__ void fixed_mlp_tiles(const FixedMlpLds<T, FT, HTT>& s
       Frag<T> w[FT];
 #pragma unroll
       for (int kp = 0; kp < FT / 2; ++kp) {
-        const FragPair<T> pr = sh.w1[ht + hh][kp][l];
-        w[2 * kp].v = pr.a;
-        w[2 * kp + 1].v = pr.b;
+        w[2 * kp].v = sh.w1[ht + hh][kp][0][l];
+        w[2 * kp + 1].v = sh.w1[ht + hh][kp][1][l];
       }
       const f4 bias = *reinterpret_cast<const f4*>(&sh.b1[16 * (ht + hh) + 4 * g]);
 #pragma unroll
@@ -145,10 +140,9 @@ __device__ __forceinline__ void fixed_mlp_tiles(const FixedMlpLds<T, FT, HTT>& s
       }
 #pragma unroll
     for (int c = 0; c < FT; ++c) {
-      const FragPair<T> pr = sh.w2[ht >> 1][c][l];
       Frag<T> q0, q1;
-      q0.v = pr.a;
-      q1.v = pr.b;
+      q0.v = sh.w2[ht >> 1][c][0][l];
+      q1.v = sh.w2[ht >> 1][c][1][l];
 #pragma unroll
       for (int t = 0; t < NT; ++t) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0, q1);
     }
