@@ -30,7 +30,7 @@ reference's ops path, fp32, autograd for the backward) on this host's usable
 cores, on a bounded sample of each config's batch.
 
 Other modes (for counter collection):
-    --only mlp_fwd|mlp_bwd|linear_fwd|linear_bwd|readout|memo_fwd|memo_bwd|forecaster
+    --only mlp_fwd|mlp_bwd|linear_fwd|linear_bwd|readout|memo_fwd|memo_bwd|forecaster|forecaster_ref
     --copy-calibration     copy 1 GiB device-to-device (a kernel of known traffic)
 """
 
@@ -72,7 +72,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU time budget per config")
     ap.add_argument("--eta", choices=["lr", "dense"], default="dense")
     ap.add_argument("--only", choices=["mlp_fwd", "mlp_bwd", "linear_fwd", "linear_bwd", "readout", "memo_fwd",
-                                       "memo_bwd", "forecaster"])
+                                       "memo_bwd", "forecaster", "forecaster_ref"])
     ap.add_argument("--copy-calibration", action="store_true")
     return ap.parse_args()
 
@@ -507,8 +507,10 @@ def main():
             k, _ = run_linear(torch, args.steps, args.warmup, args.eta, only=args.only)
         elif args.only.startswith("memo"):
             k = run_memo(torch, args.steps, args.warmup, only=args.only)
-        elif args.only == "forecaster":
-            tr, inf, _, _, _, _ = run_forecaster(torch, args.steps, args.warmup)
+        elif args.only in ("forecaster", "forecaster_ref"):
+            ref = args.only == "forecaster_ref"
+            tr, inf, _, _, _, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=32 if ref else FC_F,
+                                                 mini_batch=64 if ref else K)
             k = {"train_step": tr, "inference": inf}
         else:
             k = {"ttt_mlp_cached_readout": run_readout(torch, args.steps, args.warmup)}

@@ -54,44 +54,76 @@ __host__ __device__ GenLayout::GenLayout(int K_, int F_, int FF_, int NC_, bool 
 
 namespace {
 
+constexpr int kGenStage = 16384;  // floats of LDS staging for one product's operands (64 KB)
+
 // C[M x N] (row stride ldc) = alpha * op(A) op(B) (+ C when acc), with
 // op(A)[i][k] = ta ? A[k * lda + i] : A[i * lda + k] and likewise for B.
-// Thread t computes the 4 x 4 blocks t, t + 256, ...; a call that
-// accumulates into the C of an earlier call with the same M and N touches
-// the same blocks from the same thread, so no barrier is needed between the
-// two.  M, N, the strides and the pointers are multiples of 4 floats.
+// The operands are staged through LDS in chunks of kc contraction steps
+// (k-major: As[k][i], Bs[k][j]; all of a chunk's global loads in flight
+// together, read along the operand's contiguous dimension), then thread t
+// computes the 4 x 4 output blocks t, t + 256, ... from LDS.  Every thread
+// of the workgroup calls it (it holds barriers); a call that accumulates
+// into the C of an earlier call with the same M and N touches the same
+// blocks from the same thread.  M, N, the strides and the pointers are
+// multiples of 4 floats; Kd is a multiple of 8.
 __device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
                    const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
+  __shared__ float st[kGenStage];
+  const int sa = M + 4, sb = N + 4;  // padded k-row strides: the transposing stores spread over the banks
+  const int kc = min(Kd, (kGenStage / (sa + sb)) & ~7);
+  float* As = st;
   const int nbj = N >> 2, nblk = (M >> 2) * nbj;
-  for (int blk = threadIdx.x; blk < nblk; blk += kGenThreads) {
-    const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
-    float c[4][4] = {};
-    for (int k = 0; k < Kd; ++k) {
-      f4 a, b;
-      if (ta) {
-        a = *reinterpret_cast<const f4*>(A + (size_t)k * lda + i0);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = A[(size_t)(i0 + r) * lda + k];
+  for (int k0 = 0; k0 < Kd; k0 += kc) {
+    const int kk = min(kc, Kd - k0);
+    float* Bs = st + kk * sa;
+    if (ta) {  // A[(k0 + k) * lda + i]: i contiguous
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < kk * M; idx += kGenThreads) {
+        const int k = idx / M, i = idx - k * M;
+        As[k * sa + i] = A[(size_t)(k0 + k) * lda + i];
       }
-      if (tb) {
+    } else {  // A[i * lda + k0 + k]: k contiguous
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < kk * M; idx += kGenThreads) {
+        const int i = idx / kk, k = idx - i * kk;
+        As[k * sa + i] = A[(size_t)i * lda + k0 + k];
+      }
+    }
+    if (tb) {  // B[j * ldb + k0 + k]: k contiguous
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < kk * N; idx += kGenThreads) {
+        const int j = idx / kk, k = idx - j * kk;
+        Bs[k * sb + j] = B[(size_t)j * ldb + k0 + k];
+      }
+    } else {  // B[(k0 + k) * ldb + j]: j contiguous
+#pragma unroll 4
+      for (int idx = threadIdx.x; idx < kk * N; idx += kGenThreads) {
+        const int k = idx / N, j = idx - k * N;
+        Bs[k * sb + j] = B[(size_t)(k0 + k) * ldb + j];
+      }
+    }
+    __syncthreads();
+    for (int blk = threadIdx.x; blk < nblk; blk += kGenThreads) {
+      const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
+      float c[4][4] = {};
+#pragma unroll 8
+      for (int k = 0; k < kk; ++k) {
+        const f4 a = *reinterpret_cast<const f4*>(As + k * sa + i0);
+        const f4 b = *reinterpret_cast<const f4*>(Bs + k * sb + j0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[q] = B[(size_t)(j0 + q) * ldb + k];
-      } else {
-        b = *reinterpret_cast<const f4*>(B + (size_t)k * ldb + j0);
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) c[r][q] += a[r] * b[q];
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) c[r][q] += a[r] * b[q];
+      for (int r = 0; r < 4; ++r) {
+        f4* out = reinterpret_cast<f4*>(C + (size_t)(i0 + r) * ldc + j0);
+        f4 v = f4{c[r][0], c[r][1], c[r][2], c[r][3]} * alpha;
+        if (acc || k0 > 0) v += *out;
+        *out = v;
+      }
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      f4* out = reinterpret_cast<f4*>(C + (size_t)(i0 + r) * ldc + j0);
-      f4 v = f4{c[r][0], c[r][1], c[r][2], c[r][3]} * alpha;
-      if (acc) v += *out;
-      *out = v;
-    }
+    __syncthreads();  // the staging area is free for the next chunk or product
   }
 }
 
@@ -136,13 +168,16 @@ __device__ void copy_state_out(const State& s, StatePtrs d, const GenLayout& L, 
 __device__ void ln_l2_row(const float* z, const float* xv, const float* xk, const float* lw, const float* lb, int F,
                           float eps, float* zh, float* sig, float* G) {
   float mu = 0.f;
+  #pragma unroll 8
   for (int f = 0; f < F; ++f) mu += z[f];
   mu /= (float)F;
   float var = 0.f;
+  #pragma unroll 8
   for (int f = 0; f < F; ++f) var += (z[f] - mu) * (z[f] - mu);
   var /= (float)F;
   const float s = sqrtf(var + eps);
   float S1 = 0.f, S2 = 0.f;
+  #pragma unroll 8
   for (int f = 0; f < F; ++f) {
     const float xh = (z[f] - mu) / s;
     zh[f] = xh;
@@ -150,6 +185,7 @@ __device__ void ln_l2_row(const float* z, const float* xv, const float* xk, cons
     S1 += g;
     S2 += g * xh;
   }
+  #pragma unroll 8
   for (int f = 0; f < F; ++f) {
     const float xh = zh[f];
     const float g = lw[f] * (lw[f] * xh + lb[f] - (xv[f] - xk[f]));
@@ -184,11 +220,13 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   const size_t row0 = (chain * a.NC + s) * K;  // first token row of the mini-batch
   float *xq = sc + L.xq, *xk = sc + L.xk, *xv = sc + L.xv, *eta = sc + L.eta;
   const T *XQ = static_cast<const T*>(a.XQ), *XK = static_cast<const T*>(a.XK), *XV = static_cast<const T*>(a.XV);
+  #pragma unroll 4
   for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads) {
     xq[i] = ld(XQ, row0 * F + i);
     xk[i] = ld(XK, row0 * F + i);
     xv[i] = ld(XV, row0 * F + i);
   }
+  #pragma unroll 4
   for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
     const int r = i / K, c = i % K;
     if (a.eta_rule == TTT_ETA_DENSE) {
@@ -207,6 +245,7 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     float *z1b = sc + L.z1b, *x2b = sc + L.x2b, *db = sc + L.db, *a2 = sc + L.a2, *c2 = sc + L.c2;
     gg(z1, FF, xk, F, false, S.W1, FF, false, K, FF, F, 1.f, false);
     __syncthreads();
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
       float y, dy, ddy;
       gelu_all(z1[i] + S.b1[i % FF], y, dy, ddy);
@@ -214,12 +253,14 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
       d1[i] = dy;
       dd1[i] = ddy;
     }
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * K; i += kGenThreads) c1[i] = eta[i] * (a1[i] + 1.0f);
     __syncthreads();
     gg(z2, F, x2, FF, false, S.W2, F, false, K, F, FF, 1.f, false);
     __syncthreads();
     for (int r = threadIdx.x; r < K; r += kGenThreads) {
       float* zr = z2 + (size_t)r * F;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) zr[f] += S.b2[f];
       ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
                 g2 + (size_t)r * F);
@@ -227,11 +268,13 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     __syncthreads();
     gg(p, FF, g2, F, false, S.W2, F, true, K, FF, F, 1.f, false);
     __syncthreads();
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * FF; i += kGenThreads) g1[i] = p[i] * d1[i];
     __syncthreads();
     gg(z1b, FF, xq, F, false, S.W1, FF, false, K, FF, F, 1.f, false);
     gg(z1b, FF, c1, K, false, g1, FF, false, K, FF, K, -1.f, true);
     __syncthreads();
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
       float y, dy, ddy;
       gelu_all(z1b[i] + S.b1[i % FF], y, dy, ddy);
@@ -241,6 +284,7 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     __syncthreads();
     gg(a2, K, x2b, FF, false, x2, FF, true, K, K, FF, 1.f, false);
     __syncthreads();
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * K; i += kGenThreads) c2[i] = eta[i] * (a2[i] + 1.0f);
     __syncthreads();
     gg(z2b, F, x2b, FF, false, S.W2, F, false, K, F, FF, 1.f, false);
@@ -248,9 +292,11 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   } else {
     gg(z2, F, xk, F, false, S.W1, F, false, K, F, F, 1.f, false);
     __syncthreads();
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * K; i += kGenThreads) c1[i] = eta[i] * (a1[i] + 1.0f);
     for (int r = threadIdx.x; r < K; r += kGenThreads) {
       float* zr = z2 + (size_t)r * F;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) zr[f] += S.b1[f];
       ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
                 g2 + (size_t)r * F);
@@ -265,16 +311,19 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   for (int r = threadIdx.x; r < K; r += kGenThreads) {
     float* zr = z2b + (size_t)r * F;
     float mu = 0.f;
+    #pragma unroll 8
     for (int f = 0; f < F; ++f) {
       zr[f] += bo[f];
       mu += zr[f];
     }
     mu /= (float)F;
     float var = 0.f;
+    #pragma unroll 8
     for (int f = 0; f < F; ++f) var += (zr[f] - mu) * (zr[f] - mu);
     var /= (float)F;
     const float sd = sqrtf(var + a.eps);
     sigb[r] = sd;
+    #pragma unroll 8
     for (int f = 0; f < F; ++f) {
       const float xh = (zr[f] - mu) / sd;
       z2bh[(size_t)r * F + f] = xh;
@@ -286,8 +335,10 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   float* u1 = sc + L.t1;  // e-scaled G1 (MLP)
   float* u2 = sc + L.t2;  // e-scaled G2 / G
   const float* e = eta + (size_t)(K - 1) * K;
+  #pragma unroll 4
   for (int i = threadIdx.x; i < K * F; i += kGenThreads) u2[i] = e[i / F] * g2[i];
   if (L.mlp)
+    #pragma unroll 4
     for (int i = threadIdx.x; i < K * FF; i += kGenThreads) u1[i] = e[i / FF] * sc[L.g1 + i];
   copy_f(next->W1, S.W1, L.state);  // the whole state block
   __syncthreads();
@@ -296,11 +347,13 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     gg(next->W2, F, sc + L.x2, FF, true, u2, F, false, FF, F, K, -1.f, true);
     for (int c = threadIdx.x; c < FF; c += kGenThreads) {
       float t = 0.f;
+      #pragma unroll 8
       for (int r = 0; r < K; ++r) t += u1[(size_t)r * FF + c];
       next->b1[c] -= t;
     }
     for (int c = threadIdx.x; c < F; c += kGenThreads) {
       float t = 0.f;
+      #pragma unroll 8
       for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
       next->b2[c] -= t;
     }
@@ -308,6 +361,7 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     gg(next->W1, F, xk, F, true, u2, F, false, F, F, K, -1.f, true);
     for (int c = threadIdx.x; c < F; c += kGenThreads) {
       float t = 0.f;
+      #pragma unroll 8
       for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
       next->b1[c] -= t;
     }
@@ -395,6 +449,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
     const State S(sc + L.states + (size_t)s * L.state, L);
     gen_step_fwd<T>(a, L, sc, chain, s, S, false, nullptr);
     const size_t row0 = (chain * a.NC + s) * K;
+    #pragma unroll 4
     for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads)
       dout[i] = ld(static_cast<const T*>(a.dout), row0 * F + i);
     __syncthreads();
@@ -415,6 +470,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       const float er = e[r];
       float d = 0.f;
       if (L.mlp) {
+        #pragma unroll 8
         for (int c = 0; c < FF; ++c) {
           const size_t i = (size_t)r * FF + c;
           const float t = t1[i] + db1[c];
@@ -422,6 +478,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
           dg1[i] = -er * t;
           dx2[i] *= -er;
         }
+        #pragma unroll 8
         for (int c = 0; c < F; ++c) {
           const size_t i = (size_t)r * F + c;
           const float t = t2[i] + db2[c];
@@ -430,6 +487,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
           dxk[i] *= -er;
         }
       } else {
+        #pragma unroll 8
         for (int c = 0; c < F; ++c) {
           const size_t i = (size_t)r * F + c;
           const float t = t2[i] + db1[c];
@@ -442,6 +500,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       // ---- output LayerNorm: out = XQ + ln_w * zbh + ln_b
       const float sd = sigb[r];
       float m1 = 0.f, m2 = 0.f;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) {
         const float dh = dout[(size_t)r * F + f] * lw[f];
         m1 += dh;
@@ -449,6 +508,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       }
       m1 /= (float)F;
       m2 /= (float)F;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) {
         const size_t i = (size_t)r * F + f;
         const float dh = dout[i] * lw[f];
@@ -460,6 +520,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
     float* dbo = L.mlp ? db2 : db1;
     for (int f = threadIdx.x; f < F; f += kGenThreads) {
       float sw = 0.f, sb = 0.f, sz = 0.f;
+      #pragma unroll 8
       for (int r = 0; r < K; ++r) {
         const size_t i = (size_t)r * F + f;
         sw += dout[i] * z2bh[i];
@@ -477,6 +538,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dc2, K, dz2b, F, false, g2, F, true, K, K, F, -1.f, false);
       __syncthreads();
       gg(dg2, F, c2, K, true, dz2b, F, false, K, F, K, -1.f, true);
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
         deta[i] = dc2[i] * (a2[i] + 1.0f);
         da2[i] = dc2[i] * eta[i];
@@ -485,11 +547,13 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dx2b, FF, da2, K, false, x2, FF, false, K, FF, K, 1.f, true);
       gg(dx2, FF, da2, K, true, x2b, FF, false, K, FF, K, 1.f, true);
       __syncthreads();
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1b[i] = dx2b[i] * dbv[i];
       __syncthreads();
       // ---- Z1b = XQ W1 + b1 - (eta o (XQ XK^T + 1)) G1
       for (int c = threadIdx.x; c < FF; c += kGenThreads) {
         float t = 0.f;
+        #pragma unroll 8
         for (int r = 0; r < K; ++r) t += dz1b[(size_t)r * FF + c];
         db1[c] += t;
       }
@@ -498,6 +562,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dc1, K, dz1b, FF, false, g1, FF, true, K, K, FF, -1.f, false);
       __syncthreads();
       gg(dg1, FF, c1, K, true, dz1b, FF, false, K, FF, K, -1.f, true);
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
         deta[i] += dc1[i] * (a1[i] + 1.0f);
         da1[i] = dc1[i] * eta[i];
@@ -506,6 +571,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dxq, F, da1, K, false, xk, F, false, K, F, K, 1.f, true);
       gg(dxk, F, da1, K, true, xq, F, false, K, F, K, 1.f, true);
       // ---- G1 = (G2 W2^T) o gelu'(Z1)
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * FF; i += kGenThreads) {
         dp[i] = dg1[i] * d1[i];
         dz1[i] = dg1[i] * p[i] * dd1[i];
@@ -521,6 +587,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dc1, K, dz2b, F, false, g2, F, true, K, K, F, -1.f, false);
       __syncthreads();
       gg(dg2, F, c1, K, true, dz2b, F, false, K, F, K, -1.f, true);
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) {
         deta[i] = dc1[i] * (a1[i] + 1.0f);
         da1[i] = dc1[i] * eta[i];
@@ -537,6 +604,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       const float* q = dg2 + (size_t)r * F;
       const float* Gr = g2 + (size_t)r * F;
       float S2 = 0.f, Q1 = 0.f, Q2 = 0.f, QG = 0.f;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) {
         const size_t i = (size_t)r * F + f;
         const float g = lw[f] * (lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]));
@@ -549,6 +617,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       const float dsig = -QG / sd;
       float m1 = 0.f, m2 = 0.f;
       // pass 1: dg, dt, the LN-parameter terms and dxh (kept in dz2)
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) {
         const size_t i = (size_t)r * F + f;
         const float rr = lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]);
@@ -566,6 +635,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       }
       m1 /= (float)F;
       m2 /= (float)F;
+      #pragma unroll 8
       for (int f = 0; f < F; ++f) {
         const size_t i = (size_t)r * F + f;
         dz2[i] = (dz2[i] - m1 - xh[f] * m2) / sd + dsig * xh[f] / (float)F;
@@ -574,6 +644,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
     __syncthreads();
     for (int f = threadIdx.x; f < F; f += kGenThreads) {
       float sw = 0.f, sb = 0.f, sz = 0.f;
+      #pragma unroll 8
       for (int r = 0; r < K; ++r) {
         const size_t i = (size_t)r * F + f;
         sw += lnwt[i];
@@ -589,10 +660,12 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dx2, FF, dz2, F, false, S.W2, F, true, K, FF, F, 1.f, true);
       gg(dW2, F, x2, FF, true, dz2, F, false, FF, F, K, 1.f, true);
       __syncthreads();
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1[i] += dx2[i] * d1[i];
       __syncthreads();
       for (int c = threadIdx.x; c < FF; c += kGenThreads) {
         float t = 0.f;
+        #pragma unroll 8
         for (int r = 0; r < K; ++r) t += dz1[(size_t)r * FF + c];
         db1[c] += t;
       }
@@ -608,6 +681,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
     __syncthreads();
     // ---- this mini-batch's input gradients
     T *DXQ = static_cast<T*>(a.dXQ), *DXK = static_cast<T*>(a.dXK), *DXV = static_cast<T*>(a.dXV);
+    #pragma unroll 4
     for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads) {
       DXQ[row0 * F + i] = (T)dxq[i];
       DXK[row0 * F + i] = (T)dxk[i];
@@ -615,11 +689,13 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
     }
     if (a.eta_rule == TTT_ETA_DENSE) {
       T* DE = static_cast<T*>(a.deta) + (chain * a.NC + s) * K * K;
+      #pragma unroll 4
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) DE[i] = (T)deta[i];
     } else {
       float* DL = static_cast<float*>(a.deta) + row0;
       for (int j = threadIdx.x; j < K; j += kGenThreads) {
         float t = 0.f;
+        #pragma unroll 8
         for (int i = 0; i < K; ++i) {
           const float coef = a.eta_rule == TTT_ETA_LAYER ? 1.0f / (float)K : (j <= i ? 1.0f / (float)(i + 1) : 0.f);
           t += deta[(size_t)i * K + j] * coef;
