@@ -3,8 +3,9 @@ against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
 
 Tolerances: fp32 activations max-abs 1e-4 for the elementwise kernels (they
 compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the required bar); the
-whole forecaster in fp32 rel-L2 1e-4 per tensor (a composition of four
-kernels, three GEMMs and the inner loop, each within fp32 rounding), in bf16
+whole forecaster in fp32 rel-L2 per tensor within max(1e-4, C_FP32 times the
+fp32 oracle's own rel-L2 error against fp64) (a composition of four kernels,
+three GEMMs and the inner loop, each within fp32 rounding), in bf16
 rel-L2 2e-2 per tensor with the norm floor described at the test."""
 
 import sys
@@ -13,7 +14,7 @@ import pytest
 import torch
 
 from oracle import ttt_layer_oracle as LO
-from tests._util import max_abs, rel_l2
+from tests._util import C_FP32, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -157,6 +158,14 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
     pred = LO.forecaster_forward(sd, x.double(), cfg, 96, 7)
     loss_ref = torch.nn.functional.mse_loss(pred, y.double())
     loss_ref.backward()
+    # fp32: the same oracle in fp32 measures what fp32 rounding alone does to
+    # each gradient (the XU projection's, formed by cancellation through the
+    # memory-cache gates, is the most sensitive)
+    rtol32 = {}
+    if dt == torch.float32:
+        sd32 = {k: v.detach().float().requires_grad_(True) for k, v in model.state_dict().items()}
+        torch.nn.functional.mse_loss(LO.forecaster_forward(sd32, x.float(), cfg, 96, 7), y.float()).backward()
+        rtol32 = {k: rel_l2(sd32[k].grad, sd[k].grad) for k in sd if sd[k].grad is not None}
     dev = torch.device("cuda")
     model = model.to(dev)
     with torch.autocast("cuda", dtype=torch.bfloat16, enabled=dt == torch.bfloat16):
@@ -181,7 +190,8 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
             assert prm.grad is None or float(prm.grad.abs().max()) == 0.0, name
             continue
         e = float((prm.grad.detach().double().cpu() - r.detach().double()).norm()) / max(float(r.norm()), floor)
-        _say(f"  d{name}: rel-L2 {rel_l2(prm.grad, r):.3e} (|ref| {float(r.norm()):.3e}), bound ratio {e / tol:.2f}")
-        if e > tol:
+        tp = max(tol, C_FP32 * rtol32[name]) if dt == torch.float32 else tol
+        _say(f"  d{name}: rel-L2 {rel_l2(prm.grad, r):.3e} (|ref| {float(r.norm()):.3e}), bound ratio {e / tp:.2f}")
+        if e > tp:
             bad.append(name)
     assert not bad

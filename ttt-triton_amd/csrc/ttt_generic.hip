@@ -59,20 +59,21 @@ constexpr int kGenStage = 16384;  // floats of LDS staging for one product's ope
 // C[M x N] (row stride ldc) = alpha * op(A) op(B) (+ C when acc), with
 // op(A)[i][k] = ta ? A[k * lda + i] : A[i * lda + k] and likewise for B.
 // The operands are staged through LDS in chunks of kc contraction steps
-// (k-major: As[k][i], Bs[k][j]; all of a chunk's global loads in flight
-// together, read along the operand's contiguous dimension), then thread t
-// computes the 4 x 4 output blocks t, t + 256, ... from LDS.  Every thread
-// of the workgroup calls it (it holds barriers); a call that accumulates
-// into the C of an earlier call with the same M and N touches the same
-// blocks from the same thread.  M, N, the strides and the pointers are
-// multiples of 4 floats; Kd is a multiple of 8.
+// (k-major: As[k][i], Bs[k][j], rows padded by 4 floats; all of a chunk's
+// global loads in flight together, read along the operand's contiguous
+// dimension), then wave w forms the 16 x 16 output tiles w, w + 4, ... with
+// fp32 MFMA (v_mfma_f32_16x16x4_f32: exact products, fp32 sums), its operand
+// frags read from LDS (the padding puts the four lane groups of a read on
+// distinct banks).  Every thread of the workgroup calls it (it holds
+// barriers).  M, N and Kd are multiples of 16.
 __device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
                    const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
   __shared__ float st[kGenStage];
   const int sa = M + 4, sb = N + 4;  // padded k-row strides: the transposing stores spread over the banks
-  const int kc = min(Kd, (kGenStage / (sa + sb)) & ~7);
+  const int kc = min(Kd, (kGenStage / (sa + sb)) & ~15);
   float* As = st;
-  const int nbj = N >> 2, nblk = (M >> 2) * nbj;
+  const int wave = threadIdx.x >> 6, l = lane_id(), g = l >> 4, r = l & 15;
+  const int nt = N >> 4, ntile = (M >> 4) * nt;
   for (int k0 = 0; k0 < Kd; k0 += kc) {
     const int kk = min(kc, Kd - k0);
     float* Bs = st + kk * sa;
@@ -103,22 +104,25 @@ __device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, 
       }
     }
     __syncthreads();
-    for (int blk = threadIdx.x; blk < nblk; blk += kGenThreads) {
-      const int i0 = (blk / nbj) * 4, j0 = (blk % nbj) * 4;
-      float c[4][4] = {};
-#pragma unroll 8
-      for (int k = 0; k < kk; ++k) {
-        const f4 a = *reinterpret_cast<const f4*>(As + k * sa + i0);
-        const f4 b = *reinterpret_cast<const f4*>(Bs + k * sb + j0);
+    for (int t = wave; t < ntile; t += kGenThreads / 64) {
+      const int i0 = (t / nt) * 16, j0 = (t - (t / nt) * nt) * 16;
+      const float* ap = As + i0 + r;  // lane (g, r): op(A)[i0 + r][k + 4g + j]
+      const float* bp = Bs + j0 + r;  //              op(B)[k + 4g + j][j0 + r]
+      f4 c = f4{0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < kk; k += 16) {
+        Frag<float> fa, fb;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) c[r][q] += a[r] * b[q];
+        for (int j = 0; j < 4; ++j) {
+          fa.v[j] = ap[(k + 4 * g + j) * sa];
+          fb.v[j] = bp[(k + 4 * g + j) * sb];
+        }
+        mma16(c, fa, fb);
       }
+      // lane (g, r) holds C[i0 + 4g + j][j0 + r]
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        f4* out = reinterpret_cast<f4*>(C + (size_t)(i0 + r) * ldc + j0);
-        f4 v = f4{c[r][0], c[r][1], c[r][2], c[r][3]} * alpha;
+      for (int j = 0; j < 4; ++j) {
+        float* out = C + (size_t)(i0 + 4 * g + j) * ldc + j0 + r;
+        float v = c[j] * alpha;
         if (acc || k0 > 0) v += *out;
         *out = v;
       }
