@@ -166,36 +166,102 @@ __device__ void copy_state_out(const State& s, StatePtrs d, const GenLayout& L, 
   }
 }
 
-// Inner-loss LayerNorm fused with the L2 loss's gradient, row r of Z (bias
-// already added): its normalised row and sigma, and G = d loss / d Z
-// (ops/ttt_utils.py:21-48).
-__device__ void ln_l2_row(const float* z, const float* xv, const float* xk, const float* lw, const float* lb, int F,
-                          float eps, float* zh, float* sig, float* G) {
-  float mu = 0.f;
-  #pragma unroll 8
-  for (int f = 0; f < F; ++f) mu += z[f];
-  mu /= (float)F;
-  float var = 0.f;
-  #pragma unroll 8
-  for (int f = 0; f < F; ++f) var += (z[f] - mu) * (z[f] - mu);
-  var /= (float)F;
-  const float s = sqrtf(var + eps);
-  float S1 = 0.f, S2 = 0.f;
-  #pragma unroll 8
-  for (int f = 0; f < F; ++f) {
-    const float xh = (z[f] - mu) / s;
-    zh[f] = xh;
-    const float g = lw[f] * (lw[f] * xh + lb[f] - (xv[f] - xk[f]));
-    S1 += g;
-    S2 += g * xh;
+// Row passes over [K x C] blocks: each 16-lane DPP row of the workgroup
+// (kRowGroups of them) takes one token row at a time (rows q, q + kRowGroups,
+// ...), lane u covering columns u, u + 16, ...; row sums are sum_row16 of the
+// lanes' partials.  K is a multiple of 16, so every group makes the same
+// number of iterations and all 16 lanes of a DPP row take part in every
+// reduction.  Rows held in registers have at most RM columns per lane (the
+// kernels are instantiated with RM = 4 for F <= 64 and RM = 16 for F <= 256).
+constexpr int kRowGroups = kGenThreads / 16;
+
+__device__ __forceinline__ int row_grp() { return threadIdx.x >> 4; }
+__device__ __forceinline__ int row_lane() { return threadIdx.x & 15; }
+
+// Inner-loss LayerNorm fused with the L2 loss's gradient over the K rows of
+// Z (the bias added here and written back): normalised rows zh, sigma, and
+// G = d loss / d Z (ops/ttt_utils.py:21-48).
+template <int RM>
+__device__ void ln_l2_rows(float* z, const float* bias, const float* xv, const float* xk, const float* lw,
+                           const float* lb, int K, int F, float eps, float* zh, float* sig, float* G) {
+  const int u = row_lane(), nf = F >> 4;
+  for (int r = row_grp(); r < K; r += kRowGroups) {
+    float v[RM], tg[RM];
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < RM; ++q) {
+      if (q < nf) {
+        const int f = u + 16 * q;
+        const size_t i = (size_t)r * F + f;
+        v[q] = z[i] + bias[f];
+        z[i] = v[q];
+        tg[q] = xv[i] - xk[i];
+        acc += v[q];
+      }
+    }
+    const float mu = sum_row16(acc) / (float)F;
+    acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < RM; ++q)
+      if (q < nf) acc += (v[q] - mu) * (v[q] - mu);
+    const float sd = sqrtf(sum_row16(acc) / (float)F + eps);
+    float S1 = 0.f, S2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < RM; ++q) {
+      if (q < nf) {
+        const int f = u + 16 * q;
+        const float xh = (v[q] - mu) / sd;
+        const float g = lw[f] * (lw[f] * xh + lb[f] - tg[q]);
+        zh[(size_t)r * F + f] = xh;
+        v[q] = xh;
+        tg[q] = g;
+        S1 += g;
+        S2 += g * xh;
+      }
+    }
+    S1 = sum_row16(S1);
+    S2 = sum_row16(S2);
+#pragma unroll
+    for (int q = 0; q < RM; ++q)
+      if (q < nf) G[(size_t)r * F + u + 16 * q] = ((float)F * tg[q] - S1 - v[q] * S2) / ((float)F * sd);
+    if (u == 0) sig[r] = sd;
   }
-  #pragma unroll 8
-  for (int f = 0; f < F; ++f) {
-    const float xh = zh[f];
-    const float g = lw[f] * (lw[f] * xh + lb[f] - (xv[f] - xk[f]));
-    G[f] = ((float)F * g - S1 - xh * S2) / ((float)F * s);
+}
+
+// Column sums over the K rows of a [K x C] block: for every column c < C,
+// put(c, t) with t[v] = sum_r val(r, c)[v].  For C < 256 the threads split
+// the rows into kGenThreads / C phases whose partials meet in LDS; every
+// thread of the workgroup calls it (it holds a barrier).
+template <int NV, typename Val, typename Put>
+__device__ void col_sums(int K, int C, Val val, Put put) {
+  __shared__ float red[NV][kGenThreads];
+  if (C >= kGenThreads) {
+    for (int c = threadIdx.x; c < C; c += kGenThreads) {
+      float t[NV] = {};
+#pragma unroll 8
+      for (int r = 0; r < K; ++r) val(r, c, t);
+      put(c, t);
+    }
+    return;
   }
-  *sig = s;
+  const int P = kGenThreads / C;  // row phases
+  const int c = threadIdx.x % C, ph = threadIdx.x / C;
+  float t[NV] = {};
+  if (ph < P) {
+#pragma unroll 4
+    for (int r = ph; r < K; r += P) val(r, c, t);
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) red[v][threadIdx.x] = t[v];
+  __syncthreads();
+  if (threadIdx.x < C) {
+    float tot[NV] = {};
+    for (int q = 0; q < P; ++q)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) tot[v] += red[v][q * C + threadIdx.x];
+    put(threadIdx.x, tot);
+  }
+  __syncthreads();  // red is free for the next call
 }
 
 struct GenArgs {
@@ -214,7 +280,7 @@ struct GenArgs {
 
 // Forward values of mini-batch s from state S into the chain's scratch; with
 // `emit`, also its output rows and the state after it (into `next`).
-template <typename T>
+template <typename T, int RM>
 __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, size_t chain, int s, const State& S,
                              bool emit, const State* next) {
   const int K = L.K, F = L.F, FF = L.FF;
@@ -262,13 +328,7 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     __syncthreads();
     gg(z2, F, x2, FF, false, S.W2, F, false, K, F, FF, 1.f, false);
     __syncthreads();
-    for (int r = threadIdx.x; r < K; r += kGenThreads) {
-      float* zr = z2 + (size_t)r * F;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) zr[f] += S.b2[f];
-      ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
-                g2 + (size_t)r * F);
-    }
+    ln_l2_rows<RM>(z2, S.b2, xv, xk, lw, lb, K, F, a.eps, z2h, sig2, g2);
     __syncthreads();
     gg(p, FF, g2, F, false, S.W2, F, true, K, FF, F, 1.f, false);
     __syncthreads();
@@ -298,13 +358,7 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     __syncthreads();
     #pragma unroll 4
     for (int i = threadIdx.x; i < K * K; i += kGenThreads) c1[i] = eta[i] * (a1[i] + 1.0f);
-    for (int r = threadIdx.x; r < K; r += kGenThreads) {
-      float* zr = z2 + (size_t)r * F;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) zr[f] += S.b1[f];
-      ln_l2_row(zr, xv + (size_t)r * F, xk + (size_t)r * F, lw, lb, F, a.eps, z2h + (size_t)r * F, sig2 + r,
-                g2 + (size_t)r * F);
-    }
+    ln_l2_rows<RM>(z2, S.b1, xv, xk, lw, lb, K, F, a.eps, z2h, sig2, g2);
     __syncthreads();
     gg(z2b, F, xq, F, false, S.W1, F, false, K, F, F, 1.f, false);
     gg(z2b, F, c1, K, false, g2, F, false, K, F, K, -1.f, true);
@@ -312,26 +366,37 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   __syncthreads();
   // output LayerNorm and residual
   const float* bo = L.mlp ? S.b2 : S.b1;
-  for (int r = threadIdx.x; r < K; r += kGenThreads) {
-    float* zr = z2b + (size_t)r * F;
-    float mu = 0.f;
-    #pragma unroll 8
-    for (int f = 0; f < F; ++f) {
-      zr[f] += bo[f];
-      mu += zr[f];
-    }
-    mu /= (float)F;
-    float var = 0.f;
-    #pragma unroll 8
-    for (int f = 0; f < F; ++f) var += (zr[f] - mu) * (zr[f] - mu);
-    var /= (float)F;
-    const float sd = sqrtf(var + a.eps);
-    sigb[r] = sd;
-    #pragma unroll 8
-    for (int f = 0; f < F; ++f) {
-      const float xh = (zr[f] - mu) / sd;
-      z2bh[(size_t)r * F + f] = xh;
-      if (emit) static_cast<T*>(a.out)[(row0 + r) * F + f] = (T)(xq[(size_t)r * F + f] + lw[f] * xh + lb[f]);
+  {
+    const int u = row_lane(), nf = F >> 4;
+    for (int r = row_grp(); r < K; r += kRowGroups) {
+      float v[RM];
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < RM; ++q) {
+        if (q < nf) {
+          const size_t i = (size_t)r * F + u + 16 * q;
+          v[q] = z2b[i] + bo[u + 16 * q];
+          z2b[i] = v[q];
+          acc += v[q];
+        }
+      }
+      const float mu = sum_row16(acc) / (float)F;
+      acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < RM; ++q)
+        if (q < nf) acc += (v[q] - mu) * (v[q] - mu);
+      const float sd = sqrtf(sum_row16(acc) / (float)F + a.eps);
+      if (u == 0) sigb[r] = sd;
+#pragma unroll
+      for (int q = 0; q < RM; ++q) {
+        if (q < nf) {
+          const int f = u + 16 * q;
+          const size_t i = (size_t)r * F + f;
+          const float xh = (v[q] - mu) / sd;
+          z2bh[i] = xh;
+          if (emit) static_cast<T*>(a.out)[(row0 + r) * F + f] = (T)(xq[i] + lw[f] * xh + lb[f]);
+        }
+      }
     }
   }
   if (!emit) return;
@@ -349,32 +414,20 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
   if (L.mlp) {
     gg(next->W1, FF, xk, F, true, u1, FF, false, F, FF, K, -1.f, true);
     gg(next->W2, F, sc + L.x2, FF, true, u2, F, false, FF, F, K, -1.f, true);
-    for (int c = threadIdx.x; c < FF; c += kGenThreads) {
-      float t = 0.f;
-      #pragma unroll 8
-      for (int r = 0; r < K; ++r) t += u1[(size_t)r * FF + c];
-      next->b1[c] -= t;
-    }
-    for (int c = threadIdx.x; c < F; c += kGenThreads) {
-      float t = 0.f;
-      #pragma unroll 8
-      for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
-      next->b2[c] -= t;
-    }
+    col_sums<1>(K, FF, [&](int r, int c, float(&t)[1]) { t[0] += u1[(size_t)r * FF + c]; },
+                [&](int c, const float(&t)[1]) { next->b1[c] -= t[0]; });
+    col_sums<1>(K, F, [&](int r, int c, float(&t)[1]) { t[0] += u2[(size_t)r * F + c]; },
+                [&](int c, const float(&t)[1]) { next->b2[c] -= t[0]; });
   } else {
     gg(next->W1, F, xk, F, true, u2, F, false, F, F, K, -1.f, true);
-    for (int c = threadIdx.x; c < F; c += kGenThreads) {
-      float t = 0.f;
-      #pragma unroll 8
-      for (int r = 0; r < K; ++r) t += u2[(size_t)r * F + c];
-      next->b1[c] -= t;
-    }
+    col_sums<1>(K, F, [&](int r, int c, float(&t)[1]) { t[0] += u2[(size_t)r * F + c]; },
+                [&](int c, const float(&t)[1]) { next->b1[c] -= t[0]; });
   }
   __syncthreads();
 }
 
-template <typename T>
-__global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs a) {
+template <typename T, int RM>
+__global__ __launch_bounds__(kGenThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gen_fwd_kernel(GenArgs a) {
   const size_t chain = blockIdx.x;
   const GenLayout L(a.K, a.F, a.FF, a.NC, a.mlp);
   float* base = a.saved + chain * L.per_chain;
@@ -405,15 +458,15 @@ __global__ __launch_bounds__(kGenThreads) void gen_fwd_kernel(GenArgs a) {
     const State S = state_at(s);
     if (s % a.G == 0) copy_state_out(S, ck, L, s / a.G);
     const State nxt = s + 1 < a.NC ? state_at(s + 1) : State(base + L.wfin, L);
-    gen_step_fwd<T>(a, L, base, chain, s, S, true, &nxt);
+    gen_step_fwd<T, RM>(a, L, base, chain, s, S, true, &nxt);
     if (a.memo.W1 && s % a.M == 0) copy_state_out(nxt, mm, L, s / a.M);
     if (s + 1 == a.NC && a.last.W1) copy_state_out(nxt, la, L, 0);
     __syncthreads();
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
+template <typename T, int RM>
+__global__ __launch_bounds__(kGenThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gen_bwd_kernel(GenArgs a) {
   const size_t chain = blockIdx.x;
   const GenLayout L(a.K, a.F, a.FF, a.NC, a.mlp);
   const int K = L.K, F = L.F, FF = L.FF;
@@ -451,7 +504,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
   __syncthreads();
   for (int s = a.NC - 1; s >= 0; --s) {
     const State S(sc + L.states + (size_t)s * L.state, L);
-    gen_step_fwd<T>(a, L, sc, chain, s, S, false, nullptr);
+    gen_step_fwd<T, RM>(a, L, sc, chain, s, S, false, nullptr);
     const size_t row0 = (chain * a.NC + s) * K;
     #pragma unroll 4
     for (size_t i = threadIdx.x; i < (size_t)K * F; i += kGenThreads)
@@ -470,71 +523,82 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       gg(dxk, F, g2, F, false, dW1, F, true, K, F, F, 1.f, false);   // G dW'^T
     }
     __syncthreads();
-    for (int r = threadIdx.x; r < K; r += kGenThreads) {
-      const float er = e[r];
-      float d = 0.f;
-      if (L.mlp) {
-        #pragma unroll 8
-        for (int c = 0; c < FF; ++c) {
-          const size_t i = (size_t)r * FF + c;
-          const float t = t1[i] + db1[c];
-          d -= t * g1[i];
-          dg1[i] = -er * t;
-          dx2[i] *= -er;
+    {
+      const int u = row_lane(), nf = F >> 4;
+      for (int r = row_grp(); r < K; r += kRowGroups) {
+        const float er = e[r];
+        float d = 0.f;
+        if (L.mlp) {
+#pragma unroll 4
+          for (int c = u; c < FF; c += 16) {
+            const size_t i = (size_t)r * FF + c;
+            const float t = t1[i] + db1[c];
+            d -= t * g1[i];
+            dg1[i] = -er * t;
+            dx2[i] *= -er;
+          }
+#pragma unroll 4
+          for (int c = u; c < F; c += 16) {
+            const size_t i = (size_t)r * F + c;
+            const float t = t2[i] + db2[c];
+            d -= t * g2[i];
+            dg2[i] = -er * t;
+            dxk[i] *= -er;
+          }
+        } else {
+#pragma unroll 4
+          for (int c = u; c < F; c += 16) {
+            const size_t i = (size_t)r * F + c;
+            const float t = t2[i] + db1[c];
+            d -= t * g2[i];
+            dg2[i] = -er * t;
+            dxk[i] *= -er;
+          }
         }
-        #pragma unroll 8
-        for (int c = 0; c < F; ++c) {
-          const size_t i = (size_t)r * F + c;
-          const float t = t2[i] + db2[c];
-          d -= t * g2[i];
-          dg2[i] = -er * t;
-          dxk[i] *= -er;
+        d = sum_row16(d);
+        if (u == 0) de[r] = d;
+        // ---- output LayerNorm: out = XQ + ln_w * zbh + ln_b
+        const float sd = sigb[r];
+        float dh[RM], zh[RM];
+        float m1 = 0.f, m2 = 0.f;
+#pragma unroll
+        for (int q = 0; q < RM; ++q) {
+          if (q < nf) {
+            const int f = u + 16 * q;
+            const size_t i = (size_t)r * F + f;
+            dh[q] = dout[i] * lw[f];
+            zh[q] = z2bh[i];
+            m1 += dh[q];
+            m2 += dh[q] * zh[q];
+          }
         }
-      } else {
-        #pragma unroll 8
-        for (int c = 0; c < F; ++c) {
-          const size_t i = (size_t)r * F + c;
-          const float t = t2[i] + db1[c];
-          d -= t * g2[i];
-          dg2[i] = -er * t;
-          dxk[i] *= -er;
+        m1 = sum_row16(m1) / (float)F;
+        m2 = sum_row16(m2) / (float)F;
+#pragma unroll
+        for (int q = 0; q < RM; ++q) {
+          if (q < nf) {
+            const size_t i = (size_t)r * F + u + 16 * q;
+            dz2b[i] = (dh[q] - m1 - zh[q] * m2) / sd;
+            dxq[i] = dout[i];
+          }
         }
-      }
-      de[r] = d;
-      // ---- output LayerNorm: out = XQ + ln_w * zbh + ln_b
-      const float sd = sigb[r];
-      float m1 = 0.f, m2 = 0.f;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) {
-        const float dh = dout[(size_t)r * F + f] * lw[f];
-        m1 += dh;
-        m2 += dh * z2bh[(size_t)r * F + f];
-      }
-      m1 /= (float)F;
-      m2 /= (float)F;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) {
-        const size_t i = (size_t)r * F + f;
-        const float dh = dout[i] * lw[f];
-        dz2b[i] = (dh - m1 - z2bh[i] * m2) / sd;
-        dxq[i] = dout[i];
       }
     }
     __syncthreads();
     float* dbo = L.mlp ? db2 : db1;
-    for (int f = threadIdx.x; f < F; f += kGenThreads) {
-      float sw = 0.f, sb = 0.f, sz = 0.f;
-      #pragma unroll 8
-      for (int r = 0; r < K; ++r) {
-        const size_t i = (size_t)r * F + f;
-        sw += dout[i] * z2bh[i];
-        sb += dout[i];
-        sz += dz2b[i];
-      }
-      dlnw[f] += sw;
-      dlnb[f] += sb;
-      dbo[f] += sz;
-    }
+    col_sums<3>(
+        K, F,
+        [&](int r, int f, float(&t)[3]) {
+          const size_t i = (size_t)r * F + f;
+          t[0] += dout[i] * z2bh[i];
+          t[1] += dout[i];
+          t[2] += dz2b[i];
+        },
+        [&](int f, const float(&t)[3]) {
+          dlnw[f] += t[0];
+          dlnb[f] += t[1];
+          dbo[f] += t[2];
+        });
     if (L.mlp) {
       // ---- Z2b = X2b W2 + b2 - (eta o (X2b X2^T + 1)) G2
       gg(dW2, F, x2b, FF, true, dz2b, F, false, FF, F, K, 1.f, true);
@@ -555,12 +619,8 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1b[i] = dx2b[i] * dbv[i];
       __syncthreads();
       // ---- Z1b = XQ W1 + b1 - (eta o (XQ XK^T + 1)) G1
-      for (int c = threadIdx.x; c < FF; c += kGenThreads) {
-        float t = 0.f;
-        #pragma unroll 8
-        for (int r = 0; r < K; ++r) t += dz1b[(size_t)r * FF + c];
-        db1[c] += t;
-      }
+      col_sums<1>(K, FF, [&](int r, int c, float(&t)[1]) { t[0] += dz1b[(size_t)r * FF + c]; },
+                  [&](int c, const float(&t)[1]) { db1[c] += t[0]; });
       gg(dxq, F, dz1b, FF, false, S.W1, FF, true, K, F, FF, 1.f, true);
       gg(dW1, FF, xq, F, true, dz1b, FF, false, F, FF, K, 1.f, true);
       gg(dc1, K, dz1b, FF, false, g1, FF, true, K, K, FF, -1.f, false);
@@ -602,63 +662,75 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       __syncthreads();
     }
     // ---- G = LN-fused-L2 gradient of Z (Z2 for the MLP): its backward
-    for (int r = threadIdx.x; r < K; r += kGenThreads) {
-      const float sd = sig2[r];
-      const float* xh = z2h + (size_t)r * F;
-      const float* q = dg2 + (size_t)r * F;
-      const float* Gr = g2 + (size_t)r * F;
-      float S2 = 0.f, Q1 = 0.f, Q2 = 0.f, QG = 0.f;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) {
-        const size_t i = (size_t)r * F + f;
-        const float g = lw[f] * (lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]));
-        S2 += g * xh[f];
-        Q1 += q[f];
-        Q2 += q[f] * xh[f];
-        QG += q[f] * Gr[f];
-      }
-      const float inv = 1.0f / ((float)F * sd);
-      const float dsig = -QG / sd;
-      float m1 = 0.f, m2 = 0.f;
-      // pass 1: dg, dt, the LN-parameter terms and dxh (kept in dz2)
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) {
-        const size_t i = (size_t)r * F + f;
-        const float rr = lw[f] * xh[f] + lb[f] - (xv[i] - xk[i]);
-        const float g = lw[f] * rr;
-        const float dg = ((float)F * q[f] - Q1 - xh[f] * Q2) * inv;
-        const float dxh = (-q[f] * S2 - g * Q2) * inv + dg * lw[f] * lw[f];
-        const float dt = -dg * lw[f];
-        dxv[i] = dt;
-        dxk[i] -= dt;
-        lnwt[i] = dg * (rr + lw[f] * xh[f]);
-        lnbt[i] = dg * lw[f];
-        dz2[i] = dxh;
-        m1 += dxh;
-        m2 += dxh * xh[f];
-      }
-      m1 /= (float)F;
-      m2 /= (float)F;
-      #pragma unroll 8
-      for (int f = 0; f < F; ++f) {
-        const size_t i = (size_t)r * F + f;
-        dz2[i] = (dz2[i] - m1 - xh[f] * m2) / sd + dsig * xh[f] / (float)F;
+    {
+      const int u = row_lane(), nf = F >> 4;
+      for (int r = row_grp(); r < K; r += kRowGroups) {
+        const float sd = sig2[r];
+        float xh[RM], qv[RM], rr[RM];
+        float S2 = 0.f, Q1 = 0.f, Q2 = 0.f, QG = 0.f;
+#pragma unroll
+        for (int q = 0; q < RM; ++q) {
+          if (q < nf) {
+            const int f = u + 16 * q;
+            const size_t i = (size_t)r * F + f;
+            xh[q] = z2h[i];
+            qv[q] = dg2[i];
+            rr[q] = lw[f] * xh[q] + lb[f] - (xv[i] - xk[i]);
+            const float g = lw[f] * rr[q];
+            S2 += g * xh[q];
+            Q1 += qv[q];
+            Q2 += qv[q] * xh[q];
+            QG += qv[q] * g2[i];
+          }
+        }
+        S2 = sum_row16(S2);
+        Q1 = sum_row16(Q1);
+        Q2 = sum_row16(Q2);
+        QG = sum_row16(QG);
+        const float inv = 1.0f / ((float)F * sd);
+        const float dsig = -QG / sd;
+        float m1 = 0.f, m2 = 0.f;
+        // pass 1: dg, dt, the LN-parameter terms and dxh (kept in qv)
+#pragma unroll
+        for (int q = 0; q < RM; ++q) {
+          if (q < nf) {
+            const int f = u + 16 * q;
+            const size_t i = (size_t)r * F + f;
+            const float g = lw[f] * rr[q];
+            const float dg = ((float)F * qv[q] - Q1 - xh[q] * Q2) * inv;
+            const float dxh = (-qv[q] * S2 - g * Q2) * inv + dg * lw[f] * lw[f];
+            const float dt = -dg * lw[f];
+            dxv[i] = dt;
+            dxk[i] -= dt;
+            lnwt[i] = dg * (rr[q] + lw[f] * xh[q]);
+            lnbt[i] = dg * lw[f];
+            qv[q] = dxh;
+            m1 += dxh;
+            m2 += dxh * xh[q];
+          }
+        }
+        m1 = sum_row16(m1) / (float)F;
+        m2 = sum_row16(m2) / (float)F;
+#pragma unroll
+        for (int q = 0; q < RM; ++q)
+          if (q < nf)
+            dz2[(size_t)r * F + u + 16 * q] = (qv[q] - m1 - xh[q] * m2) / sd + dsig * xh[q] / (float)F;
       }
     }
     __syncthreads();
-    for (int f = threadIdx.x; f < F; f += kGenThreads) {
-      float sw = 0.f, sb = 0.f, sz = 0.f;
-      #pragma unroll 8
-      for (int r = 0; r < K; ++r) {
-        const size_t i = (size_t)r * F + f;
-        sw += lnwt[i];
-        sb += lnbt[i];
-        sz += dz2[i];
-      }
-      dlnw[f] += sw;
-      dlnb[f] += sb;
-      dbo[f] += sz;
-    }
+    col_sums<3>(
+        K, F,
+        [&](int r, int f, float(&t)[3]) {
+          const size_t i = (size_t)r * F + f;
+          t[0] += lnwt[i];
+          t[1] += lnbt[i];
+          t[2] += dz2[i];
+        },
+        [&](int f, const float(&t)[3]) {
+          dlnw[f] += t[0];
+          dlnb[f] += t[1];
+          dbo[f] += t[2];
+        });
     if (L.mlp) {
       // ---- Z2 = X2 W2 + b2, X2 = gelu(Z1), Z1 = XK W1 + b1
       gg(dx2, FF, dz2, F, false, S.W2, F, true, K, FF, F, 1.f, true);
@@ -667,12 +739,8 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       #pragma unroll 4
       for (int i = threadIdx.x; i < K * FF; i += kGenThreads) dz1[i] += dx2[i] * d1[i];
       __syncthreads();
-      for (int c = threadIdx.x; c < FF; c += kGenThreads) {
-        float t = 0.f;
-        #pragma unroll 8
-        for (int r = 0; r < K; ++r) t += dz1[(size_t)r * FF + c];
-        db1[c] += t;
-      }
+      col_sums<1>(K, FF, [&](int r, int c, float(&t)[1]) { t[0] += dz1[(size_t)r * FF + c]; },
+                  [&](int c, const float(&t)[1]) { db1[c] += t[0]; });
       gg(dxk, F, dz1, FF, false, S.W1, FF, true, K, F, FF, 1.f, true);
       gg(dW1, FF, xk, F, true, dz1, FF, false, F, FF, K, 1.f, true);
     } else {
@@ -697,26 +765,28 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(GenArgs a) {
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) DE[i] = (T)deta[i];
     } else {
       float* DL = static_cast<float*>(a.deta) + row0;
-      for (int j = threadIdx.x; j < K; j += kGenThreads) {
-        float t = 0.f;
-        #pragma unroll 8
-        for (int i = 0; i < K; ++i) {
-          const float coef = a.eta_rule == TTT_ETA_LAYER ? 1.0f / (float)K : (j <= i ? 1.0f / (float)(i + 1) : 0.f);
-          t += deta[(size_t)i * K + j] * coef;
-        }
-        DL[j] = t;
-      }
+      const bool layer = a.eta_rule == TTT_ETA_LAYER;
+      col_sums<1>(
+          K, K,
+          [&](int i, int j, float(&t)[1]) {
+            const float coef = layer ? 1.0f / (float)K : (j <= i ? 1.0f / (float)(i + 1) : 0.f);
+            t[0] += deta[(size_t)i * K + j] * coef;
+          },
+          [&](int j, const float(&t)[1]) { DL[j] = t[0]; });
     }
     __syncthreads();
   }
 }
 
-template <typename T> hipError_t launch_gen(const GenArgs& a, bool bwd, hipStream_t stream) {
+template <typename T, int RM> hipError_t launch_gen_rm(const GenArgs& a, bool bwd, hipStream_t stream) {
   if (bwd)
-    hipLaunchKernelGGL(gen_bwd_kernel<T>, dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
+    hipLaunchKernelGGL((gen_bwd_kernel<T, RM>), dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(gen_fwd_kernel<T>, dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
+    hipLaunchKernelGGL((gen_fwd_kernel<T, RM>), dim3(a.B * a.H), dim3(kGenThreads), 0, stream, a);
   return hipGetLastError();
+}
+template <typename T> hipError_t launch_gen(const GenArgs& a, bool bwd, hipStream_t stream) {
+  return a.F <= 64 ? launch_gen_rm<T, 4>(a, bwd, stream) : launch_gen_rm<T, 16>(a, bwd, stream);
 }
 
 }  // namespace
