@@ -382,6 +382,10 @@ def run_memo(torch, steps, warmup, only=None):
         if only != "memo_fwd":
             tm.mark("ttt_mlp_memo_combine_bwd")
             memo_combine_backward(xq, xu, xqw, *ws, lw, lb, MEMO_M, gates, dout)
+        if only is None:
+            # the inference form: no backward follows, so no memo-state images
+            tm.mark("ttt_mlp_memo_combine_inference")
+            memo_combine_forward(xq, xk, xu, xqw, *ws, lw, lb, MEMO_M, images=False)
     tm.mark(None)
     sp = tm.spans()
     return {k: statistics.mean(v) for k, v in sp.items()}
@@ -627,7 +631,8 @@ def main():
         "memo_combine": {
             "value": round(B * T / (mk["ttt_mlp_memo_combine"] + mk["ttt_mlp_memo_combine_bwd"]), 1),
             "unit": "tokens/s", "fwd_ms": round(mk["ttt_mlp_memo_combine"] * 1e3, 4),
-            "bwd_ms": round(mk["ttt_mlp_memo_combine_bwd"] * 1e3, 4), "memo_segment": MEMO_M,
+            "bwd_ms": round(mk["ttt_mlp_memo_combine_bwd"] * 1e3, 4),
+            "inference_fwd_ms": round(mk["ttt_mlp_memo_combine_inference"] * 1e3, 4), "memo_segment": MEMO_M,
             "readouts_per_chain": memo_pairs(),
             "mfma_frac_fwd": round(4 * F * FF * memo_pairs() * B * H / mk["ttt_mlp_memo_combine"] / MFMA_PEAK_BF16, 4),
             "shape": f"B{B} H{H} T{T} F{F} FF{FF}, {math.ceil(NC / MEMO_M)} memo states per chain, bf16"},

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 9
+#define TTT_AMD_ABI_VERSION 10
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
 
@@ -217,6 +217,17 @@ int ttt_mlp_cached_readout(const void* XQ, const float* W1, const float* b1, con
  * 0 for unsupported sizes. */
 size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M);
 
+/* Bytes of the full workspace of ttt_mlp_memo_combine / _bwd: the gates
+ * buffer and, for bf16, behind it (at the gates' size rounded up to 256
+ * bytes) one LDS image per memo state (B*H*NS of them: the state's W1 and W2
+ * as bf16 MFMA operand frags and its biases), which the forward call writes
+ * once and both calls copy straight into LDS instead of converting every
+ * state for every workgroup.  A gates buffer of at least this size takes
+ * that path; one of at least ttt_mlp_memo_gates_bytes the converting one
+ * (the same results).  0 for unsupported sizes.  No counterpart in the
+ * reference. */
+size_t ttt_mlp_memo_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int M, int dtype);
+
 /* TTT-MLP memory-cache combiner: the segment loop of TTTMLP.ttt
  * (ttt_layer.py:506-561, its cached-readout calls ttt_layer.py:542-552) in
  * three launches.  Segments of M mini-batches; for a token of segment i >= 1,
@@ -227,8 +238,10 @@ size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M);
  *   W1_memo ...       [B,H,NS,F,FF], [B,H,NS,1,FF], [B,H,NS,FF,F], [B,H,NS,1,F] fp32
  *                     (the memo output of ttt_mlp_fwd with the same M)
  *   ln_w, ln_b        [H,F] fp32;  eps: the cached readout's (1e-6 there)
- *   gates             >= ttt_mlp_memo_gates_bytes(...) bytes; receives the gates
- *                     and segment summaries, which ttt_mlp_memo_combine_bwd reads
+ *   gates             >= ttt_mlp_memo_gates_bytes(...) bytes (better
+ *                     ttt_mlp_memo_workspace_bytes(...)); receives the gates,
+ *                     segment summaries and memo-state images, which
+ *                     ttt_mlp_memo_combine_bwd reads
  * NS = ceil(NC/M) <= 256.  No counterpart in the reference's C-level code (it is
  * Python there); replaces the loop body, not a kernel. */
 int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const void* XQW,
@@ -241,8 +254,9 @@ int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const v
  * the reference, the cached readouts carry no gradient and a segment's
  * summary carries one only as the current summary of its own tokens' gates
  * (ttt_layer.py:519,528; it is cached detached, :521,559): dXK is the same
- * for every token of a segment, and 0 in segment 0.  `gates` as written by
- * the forward call (its gradient part is overwritten); dXK, dXU, dXQW
+ * for every token of a segment, and 0 in segment 0.  `gates` and
+ * `gates_bytes` as given to the forward call (its gradient part is
+ * overwritten); dXK, dXU, dXQW
  * [B,H,NC,K,F] dtype. */
 int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, const float* W1_memo,
                              const float* b1_memo, const float* W2_memo, const float* b2_memo,

@@ -41,7 +41,8 @@ def test_header_declares_the_abi():
     for name in ("ttt_abi_version", "ttt_error_string", "ttt_linear_fwd", "ttt_linear_bwd",
                  "ttt_linear_saved_bytes", "ttt_mlp_fwd", "ttt_mlp_bwd", "ttt_mlp_saved_bytes",
                  "ttt_mlp_bwd_workspace_bytes",
-                 "ttt_mlp_cached_readout", "ttt_mlp_memo_gates_bytes", "ttt_mlp_memo_combine",
+                 "ttt_mlp_cached_readout", "ttt_mlp_memo_gates_bytes", "ttt_mlp_memo_workspace_bytes",
+                 "ttt_mlp_memo_combine",
                  "ttt_mlp_memo_combine_bwd", "ttt_set_option", "ttt_get_option", "ttt_mlp_bwd_check"):
         assert name in decls, name
 
@@ -234,6 +235,12 @@ def test_memo_combine_validation(lib):
     assert need == B * H * ((per_chain + 3) // 4 * 4) * 4
     assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, 0) == 0
     assert lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, 48, M) == 0
+    # the full workspace: bf16 adds one LDS image per memo state (W1, W2 as bf16
+    # operand frags, fp32 biases, padded to whole kilobytes) behind the gates
+    img = -(-(2 * F * FF * 2 + (FF + F) * 4) // 1024) * 1024
+    assert lib.ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, FF, M, BF16) == -(-need // 256) * 256 + B * H * NS * img
+    assert lib.ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, FF, M, F32) == need
+    assert lib.ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, 96, M, BF16) == 0
 
     def fwd(**kw):
         a = dict(ptrs=[P] * 10, B=B, H=H, NC=NC, K=K, F=F, FF=FF, M=M, dtype=BF16, eps=1e-6, out=P, gates=P,

@@ -148,3 +148,35 @@ def test_memo_combine_after_the_mlp_forward():
     err, bound = max_abs(comb, ref), fp32_bound(ref, ref32)
     _say(f"  max-abs {err:.3e} bound {bound:.3e}")
     assert err <= bound
+
+
+@pytest.mark.parametrize("F_,FF", [(64, 256), (32, 64)])
+def test_memo_packed_images_match_the_converting_path(monkeypatch, F_, FF):
+    """bf16: a workspace with room for the memo states' LDS images (written
+    once by the forward, copied straight into LDS by both calls) gives bitwise
+    the results of a gates-only workspace, where every workgroup converts each
+    state it stages."""
+    from ttt_amd import _lib
+    from ttt_amd.memo import memo_combine_backward, memo_combine_forward
+    lib = _lib.load()
+    M = 3
+    _say(f"memo packed vs converting F{F_} FF{FF}")
+    d = _inputs(2, 3, 13, F_, FF, M, seed=F_ + FF, dtype=torch.bfloat16)
+    g = {k: d[k].cuda() for k in KEYS}
+    dout = d["dOut"].cuda()
+
+    def run():
+        out, gates = memo_combine_forward(*(g[k] for k in KEYS), M)
+        grads = memo_combine_backward(g["XQ"], g["XU"], g["XQW"], g["W1"], g["b1"], g["W2"], g["b2"], g["ln_w"],
+                                      g["ln_b"], M, gates, dout)
+        torch.cuda.synchronize()
+        return out, grads, gates.numel()
+
+    out_p, gr_p, n_p = run()
+    monkeypatch.setattr(lib, "ttt_mlp_memo_workspace_bytes",
+                        lambda B, H, NC, K, F, FF, M, code: lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M))
+    out_c, gr_c, n_c = run()
+    assert n_p > n_c
+    assert torch.equal(out_p, out_c)
+    for a, b in zip(gr_p, gr_c):
+        assert torch.equal(a, b)

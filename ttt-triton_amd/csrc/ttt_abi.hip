@@ -646,7 +646,24 @@ size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M) {
   return (size_t)B * H * ttt::memo_gate_floats_per_chain(NC * k, 16, F, M * k) * sizeof(float);
 }
 
+size_t ttt_mlp_memo_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int M, int dtype) {
+  const size_t gb = ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M);
+  if (gb == 0 || !fixed_mlp_shape(F, FF) || (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16)) return 0;
+  if (dtype != TTT_DTYPE_BF16) return gb;
+  const size_t NS = (size_t)(NC + M - 1) / M;
+  return ((gb + 255) & ~(size_t)255) + (size_t)B * H * NS * ttt::mlp_memo_image_bytes(F, FF);
+}
+
 namespace {
+// the packed memo-state images behind the gates, when the workspace holds them
+unsigned char* memo_packed(float* gates, size_t gates_bytes, int B, int H, int NC, int K, int F, int FF, int M,
+                           int dtype) {
+  if (dtype != TTT_DTYPE_BF16) return nullptr;
+  const size_t need = ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, FF, M, dtype);
+  if (need == 0 || gates_bytes < need) return nullptr;
+  return reinterpret_cast<unsigned char*>(gates) + ((ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M) + 255) & ~(size_t)255);
+}
+
 int check_memo(int B, int H, int NC, int K, int F, int FF, int M, int dtype, float eps, size_t gates_bytes,
                const float* gates) {
   int st = check_common(B, H, NC, K, F, 1, dtype, eps);
@@ -701,6 +718,7 @@ int ttt_mlp_memo_combine(const void* XQ, const void* XK, const void* XU, const v
   p.XK = XK;
   p.XU = XU;
   p.out = out;
+  p.packed = memo_packed(gates, gates_bytes, B, H, NC, K, F, FF, M, dtype);
   if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
   return hip_status(ttt::launch_mlp_memo(p, dtype, false, static_cast<hipStream_t>(stream)));
 }
@@ -722,6 +740,7 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
   p.dXK = dXK;
   p.dXU = dXU;
   p.dXQW = dXQW;
+  p.packed = memo_packed(gates, gates_bytes, B, H, NC, K, F, FF, M, dtype);
   if ((long long)B * H * p.nchunk > 0x7fffffffLL) return TTT_ERR_SHAPE;
   return hip_status(ttt::launch_mlp_memo(p, dtype, true, static_cast<hipStream_t>(stream)));
 }

@@ -100,10 +100,12 @@ struct MlpMemoParams {
   const float *W1, *b1, *W2, *b2, *ln_w, *ln_b;
   void *out, *dXK, *dXU, *dXQW;
   float* gates;
+  unsigned char* packed;  // bf16: [B*H][NS] LDS images of the memo states (mlp_memo_image_bytes each), or null
   int B, H, NC, F, FF, M, NS, nchunk;
   float eps;
 };
 size_t memo_gate_floats_per_chain(int NC, int K, int F, int M);
+size_t mlp_memo_image_bytes(int F, int FF);
 hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStream_t stream);
 int mlp_memo_chunk_tiles();
 

@@ -34,6 +34,7 @@
 // chain (fp32) holds gamma^T [NS][NT], the current gate [NT], the summaries
 // [NS][F] and, in the backward, the gate gradients [NS][NT] and the
 // current-summary logit gradients [NT] (NT = NC * 16 tokens).
+#include "ttt_buf.h"
 #include "ttt_fixed_mlp.h"
 #include "ttt_kernels.h"
 
@@ -214,13 +215,37 @@ constexpr int kMemoWaves = 8;
 constexpr int kMemoTilesPerWave = 2;
 constexpr int kMemoChunkTiles = kMemoWaves * kMemoTilesPerWave;  // mini-batches (16 tokens each) per workgroup
 
-template <typename T, int FT, int HTT, bool BWD>
+// Packed memo states (bf16): each state's LDS image -- the FixedMlpLds struct
+// the staging builds, operand frags and biases -- written once by
+// memo_pack_kernel, padded to whole kilobytes so that a wave copies it 1 KB
+// (64 lanes x 16 bytes) at a time with direct-to-LDS loads.
+template <typename T, int FT, int HTT> constexpr int kMemoImg = (int)((sizeof(FixedMlpLds<T, FT, HTT>) + 1023) & ~1023);
+
+// one workgroup per (chain, state): stage the state as the combiner would,
+// then copy the LDS image out
+template <typename T, int FT, int HTT>
+__global__ __launch_bounds__(256) void memo_pack_kernel(MlpMemoParams p) {
+  constexpr int F = 16 * FT, FF = 16 * HTT, IMG = kMemoImg<T, FT, HTT>;
+  __shared__ __align__(16) unsigned char img[IMG];
+  auto& sh = *reinterpret_cast<FixedMlpLds<T, FT, HTT>*>(img);
+  const size_t st = blockIdx.x;  // chain * NS + state
+  stage_fixed_mlp<T, FT, HTT, 4>(sh, p.W1 + st * F * FF, p.b1 + st * FF, p.W2 + st * FF * F, p.b2 + st * F);
+  __syncthreads();
+  const u4v* src = reinterpret_cast<const u4v*>(img);
+  u4v* dst = reinterpret_cast<u4v*>(p.packed + st * IMG);
+  for (int i = threadIdx.x; i < IMG / 16; i += 256) dst[i] = src[i];
+}
+
+template <typename T, int FT, int HTT, bool BWD, bool PK>
 __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoParams p) {
   constexpr int F = 16 * FT;
   constexpr int FF = 16 * HTT;
   constexpr int K = 16;
   constexpr int NTW = kMemoTilesPerWave;
-  __shared__ FixedMlpLds<T, FT, HTT> sh;
+  constexpr int IMG = kMemoImg<T, FT, HTT>;
+  // unpacked: one staging area, filled between two barriers per state;
+  // packed: two images, the next state's copied in while the current one is used
+  __shared__ __align__(16) unsigned char lds[PK ? 2 * IMG : (int)sizeof(FixedMlpLds<T, FT, HTT>)];
 
   // blockIdx -> (chain, chunk pair), the pairs of one chain on one XCD (shared
   // L2).  Chunk c needs about 2c+1 memo states, so a workgroup takes chunks c
@@ -297,31 +322,55 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
     }
 
     const float invF = 1.0f / (float)F;
+    // packed: copy state jm's image into buffer b, 1 KB per wave and copy
+    auto dma_state = [&](int jm, int b) {
+      const unsigned char* src = p.packed + ((size_t)chain * NS + jm) * IMG + 16 * l;
+      for (int c = wave; c < IMG / 1024; c += kMemoWaves)
+        __builtin_amdgcn_global_load_lds(src + c * 1024, (__attribute__((address_space(3))) void*)(lds + b * IMG + c * 1024),
+                                         16, 0, 0);
+    };
+    if constexpr (PK) {
+      __syncthreads();  // (the other chunk's last reads of the buffers are done)
+      if (jmax > 0) dma_state(0, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
 #pragma unroll 1
     for (int jm = 0; jm < jmax; ++jm) {
-      // ---- stage memo state jm (the previous state's reads are done); request
-      //      this state's gates of the wave's tokens first (forward).  Each wave
-      //      stages NB blocks of W1 and of W2 and a share of the biases, every
-      //      load issued before the first conversion, so that a state costs one
-      //      memory latency.
-      __syncthreads();
+      // ---- memo state jm in LDS.  This state's gates of the wave's tokens are
+      //      requested first (forward).  Unpacked: each wave stages NB blocks
+      //      of W1 and of W2 and a share of the biases between two barriers,
+      //      every load issued before the first conversion, so that a state
+      //      costs one memory latency.  Packed: state jm's image arrived during
+      //      the previous state; state jm + 1's copy is requested now, into the
+      //      buffer the previous state used.
+      if constexpr (!PK) __syncthreads();
       f4 gjv[NTW];
       if constexpr (!BWD) {
 #pragma unroll
         for (int t = 0; t < NTW; ++t)
           gjv[t] = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + 4 * g);
       }
-      {
+      if constexpr (PK) {
+        if (jm + 1 < jmax) dma_state(jm + 1, (jm + 1) & 1);
+      } else {
         const size_t st = (size_t)chain * NS + jm;
-        stage_fixed_mlp<T, FT, HTT, kMemoWaves>(sh, p.W1 + st * F * FF, p.b1 + st * FF, p.W2 + st * FF * F,
-                                                p.b2 + st * F);
+        stage_fixed_mlp<T, FT, HTT, kMemoWaves>(*reinterpret_cast<FixedMlpLds<T, FT, HTT>*>(lds), p.W1 + st * F * FF,
+                                                p.b1 + st * FF, p.W2 + st * FF * F, p.b2 + st * F);
+        __syncthreads();
       }
-      __syncthreads();
+      const auto& sh = *reinterpret_cast<const FixedMlpLds<T, FT, HTT>*>(lds + (PK ? (jm & 1) * IMG : 0));
 
       bool any = false;
 #pragma unroll
       for (int t = 0; t < NTW; ++t) any |= seg[t] > jm;
-      if (!any) continue;  // (no barrier until the loop's next iteration, which every wave reaches)
+      if (!any) {
+        if constexpr (PK) {
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+        }
+        continue;  // (unpacked: no barrier until the loop's next iteration, which every wave reaches)
+      }
 
       Tile acc[NTW][FT];  // Z2 + b2
       fixed_mlp_tiles<T, FT, HTT, NTW>(sh, xq, acc);
@@ -362,6 +411,11 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
           const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
           if (n == 0) *reinterpret_cast<f4*>(gb + L.dgam + (size_t)jm * NT + tok0) = dg;
         }
+      }
+      if constexpr (PK) {
+        // state jm + 1's image complete in every wave; state jm's buffer free
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
       }
     }
 
@@ -535,13 +589,24 @@ __global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) 
 }
 
 // ------------------------------------------------------------------ launchers
+template <typename T, int FT, int HTT, bool BWD>
+static hipError_t launch_combine(const MlpMemoParams& p, hipStream_t stream) {
+  const dim3 grid(p.B * p.H * ((p.nchunk + 1) / 2)), block(64 * kMemoWaves);
+  if constexpr (sizeof(T) == 2) {
+    if (p.packed != nullptr) {
+      hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, true>), grid, block, 0, stream, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, false>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
 template <typename T, int FT, int HTT>
 static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t stream) {
-  const dim3 grid(p.B * p.H * ((p.nchunk + 1) / 2)), block(64 * kMemoWaves);
   const int nrow = (p.NC * 16 + kTokBlk - 1) / kTokBlk;  // workgroups per chain of the gate and finish kernels
   if (bwd) {
-    hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, true>), grid, block, 0, stream, p);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_combine<T, FT, HTT, true>(p, stream);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((memo_finish_kernel<T, 16 * FT>), dim3(p.B * p.H * nrow), dim3(kMemoThreads), 0, stream, p);
     e = hipGetLastError();
@@ -555,8 +620,14 @@ static hipError_t launch_memo_t(const MlpMemoParams& p, bool bwd, hipStream_t st
   hipLaunchKernelGGL((memo_gate_kernel<T, 16 * FT>), dim3(p.B * p.H * nrow), dim3(kMemoThreads), 0, stream, p);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, false>), grid, block, 0, stream, p);
-  return hipGetLastError();
+  if constexpr (sizeof(T) == 2) {
+    if (p.packed != nullptr) {
+      hipLaunchKernelGGL((memo_pack_kernel<T, FT, HTT>), dim3(p.B * p.H * p.NS), dim3(256), 0, stream, p);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+  }
+  return launch_combine<T, FT, HTT, false>(p, stream);
 }
 
 template <typename T, int FT>
@@ -582,5 +653,16 @@ hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStrea
 }
 
 int mlp_memo_chunk_tiles() { return kMemoChunkTiles; }
+
+size_t mlp_memo_image_bytes(int F, int FF) {
+  const int FT = F / 16;
+  switch (FF) {
+    case 32: return FT == 4 ? kMemoImg<__bf16, 4, 2> : kMemoImg<__bf16, 2, 2>;
+    case 64: return FT == 4 ? kMemoImg<__bf16, 4, 4> : kMemoImg<__bf16, 2, 4>;
+    case 128: return FT == 4 ? kMemoImg<__bf16, 4, 8> : kMemoImg<__bf16, 2, 8>;
+    case 256: return FT == 4 ? kMemoImg<__bf16, 4, 16> : kMemoImg<__bf16, 2, 16>;
+    default: return 0;
+  }
+}
 
 }  // namespace ttt

@@ -11,7 +11,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -58,6 +58,7 @@ SIGNATURES = {
     "ttt_post_norm_bwd": (_I, [_P] * 4 + [_I] * 6 + [_P, _P, _S, _P]),
     "ttt_mlp_cached_readout": (_I, [_P] * 7 + [_I] * 8 + [_F] + [_P, _P]),
     "ttt_mlp_memo_gates_bytes": (_S, [_I] * 6),
+    "ttt_mlp_memo_workspace_bytes": (_S, [_I] * 8),
     "ttt_mlp_memo_combine": (_I, [_P] * 10 + [_I] * 8 + [_F] + [_P, _P, _S, _P]),
     "ttt_mlp_memo_combine_bwd": (_I, [_P] * 10 + [_I] * 8 + [_F] + [_P, _S, _P, _P, _P, _P]),
 }

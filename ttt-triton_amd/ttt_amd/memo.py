@@ -59,9 +59,13 @@ def _f32(t):
 
 
 def memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M: int,
-                         eps: float = READOUT_EPS):
+                         eps: float = READOUT_EPS, images: bool = True):
     """Run the combiner.  Returns (out [B,H,NC,K,F] in XQW.dtype, gates) where
-    `gates` (uint8 device buffer) is what memo_combine_backward needs."""
+    `gates` (uint8 device buffer) is what memo_combine_backward needs.  With
+    `images` (bf16), the workspace also holds each memo state's LDS image,
+    written once here and copied straight into LDS by this call and the
+    backward: worth its one conversion pass when a backward follows; without
+    it every workgroup converts the states it stages (the same results)."""
     B, H, NC, K, F, FF, M = _check(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M)
     dev = check_device(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b)
     mp = XQW.dtype
@@ -70,7 +74,9 @@ def memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln
     ws = [_f32(t) for t in (W1_memo, b1_memo, W2_memo, b2_memo)]
     lw, lb = _f32(ln_w), _f32(ln_b)
     lib = _lib.load()
-    nbytes = lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M)
+    # the gates and, for bf16, the memo states' LDS images that both calls copy in
+    nbytes = (lib.ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, FF, M, code) if images
+              else lib.ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M))
     gates = torch.empty(nbytes, device=dev, dtype=torch.uint8)
     out = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
     with torch.cuda.device(dev):
@@ -108,7 +114,10 @@ class MemoCombineFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M, eps=READOUT_EPS):
-        out, gates = memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M, eps)
+        # the memo-state images pay off only when the backward runs too
+        training = any(ctx.needs_input_grad[1:4])
+        out, gates = memo_combine_forward(XQ, XK, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, M, eps,
+                                          images=training)
         ctx.save_for_backward(XQ, XU, XQW, W1_memo, b1_memo, W2_memo, b2_memo, ln_w, ln_b, gates)
         ctx.M, ctx.eps = int(M), eps
         ctx.dtypes = (XK.dtype, XU.dtype, XQW.dtype)
