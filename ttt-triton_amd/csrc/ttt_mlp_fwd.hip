@@ -13,6 +13,7 @@
 //   Z1b = XQ W1 - (eta o XQ XK^T + eta) G1 + b1, X2b = gelu(Z1b)
 //   Z2b = sum_w X2b_w W2_w - (eta o X2b X2^T + eta) G2 + b2
 //   out = XQ + LN(Z2b)                            wave w writes feature tiles w, w+NW, ...
+//                                                 (token rows 4w..4w+3 when split by rows)
 //   W1 -= XK^T diag(e) G1, W2 -= X2^T diag(e) G2, b -= G^T e   (e = eta[K-1])
 //
 // Checkpoints hold the state entering mini-batch k*G
@@ -54,7 +55,10 @@ template <int FT, int NW> struct MlpFwdShared {
 // are as many waves as 16-feature tiles and F = 64: wave w takes rows
 // 4w..4w+3 (lane group g = w of every token-major tile) with lane l on
 // feature l, so a row's reductions span the 64 lanes and each lane does 4
-// rows instead of 16; G2 is then exchanged through LDS.
+// rows instead of 16; G2 is then exchanged through LDS.  The readout's output
+// LayerNorm is split the same way: each wave folds its share of the
+// -(eta o A2 + eta) G2 term into its partial X2b W2 before the exchange, so
+// the four partials of a row add up to Z2b and no wave forms all of it.
 template <int FT, int NW> constexpr bool kLnRowSplit = (NW == 4 && FT == 4);
 
 template <typename T, int FT, int NW, bool LR>
@@ -180,11 +184,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     const int xo = s * K * F * ST, eo = s * K * K * ST;
     const int us = s * Slot::BYTES;
     // the inner loss's target XV - XK: as frags (free = token), or, split by
-    // rows, rows 4*wave+j of feature l
-    Frag<T> xv[FT], xvr, xkr;
+    // rows, rows 4*wave+j of feature l (and XQ's for the output's residual)
+    Frag<T> xv[FT], xvr, xkr, xqr;
     if constexpr (kLnRowSplit<FT, NW>) {
       xvr = bload_ctile<T>(rXV, l * ST, xo + 4 * wave * F * ST, F);
       xkr = bload_ctile<T>(rXK, l * ST, xo + 4 * wave * F * ST, F);
+      xqr = bload_ctile<T>(rXQ, l * ST, xo + 4 * wave * F * ST, F);
     } else {
 #pragma unroll
       for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
@@ -261,21 +266,18 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       for (int w = 0; w < NW; ++w) z += sh.z2p[w][lo][16 * wave + n];
       const f4 tgt = frag_to_f4(xvr) - frag_to_f4(xkr);
       constexpr float invF = 1.0f / F;
-      f4 mu, rs, xh, gx, s1, cc, g2;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mu[j] = sum_wave(z[j]) * invF;
+      f4 rs, xh, gx, g2;
+      const f4 mu = sum4_wave(z) * invF;
+      const f4 d = z - mu;
+      const f4 var = sum4_wave(d * d) * invF;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float d = z[j] - mu[j];
-        rs[j] = rsqrt_f(sum_wave(d * d) * invF + eps);
-        xh[j] = d * rs[j];
+        rs[j] = rsqrt_f(var[j] + eps);
+        xh[j] = d[j] * rs[j];
         gx[j] = (lnw_l * xh[j] + lnb_l - tgt[j]) * lnw_l;
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        s1[j] = sum_wave(gx[j]) * invF;
-        cc[j] = sum_wave(gx[j] * xh[j]) * invF;
-      }
+      const f4 s1 = sum4_wave(gx) * invF;
+      const f4 cc = sum4_wave(gx * xh) * invF;
 #pragma unroll
       for (int j = 0; j < 4; ++j) g2[j] = (gx[j] - s1[j] - xh[j] * cc[j]) * rs[j];
       sh.g2[lo][16 * wave + n] = g2;
@@ -374,6 +376,20 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       a2p[0][0].v = f4{0.f, 0.f, 0.f, 0.f};
       gemm_pt<1, FT, HT>(z2bp, x2bF, W2);   // uses W2 before the update
       gemm<1, 1, HT>(a2p, x2F, x2bF);       // (X2b X2^T)^T over this wave's units
+      if constexpr (kLnRowSplit<FT, NW>) {
+        // Z2b = sum_w (X2b_w W2_w - (eta o A2_w) G2) - eta G2 + b2: the term
+        // in A2 = sum_w A2_w is linear in it, so each wave adds its share and
+        // wave 0 the rest; the sum of the partials is then Z2b itself
+        f4 m2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m2[j] = -(etaT[j] * a2p[0][0].v[j] + (wave == 0 ? etaT[j] : 0.f));
+        const Frag<T> m2f = to_frag<T>(m2);
+#pragma unroll
+        for (int o = 0; o < FT; ++o) {
+          if (wave == 0) z2bp[0][o].v += f4{b2_tm[o], b2_tm[o], b2_tm[o], b2_tm[o]};
+          mma16(z2bp[0][o].v, m2f, to_frag<T>(G2[o].v));
+        }
+      }
 #pragma unroll
       for (int o = 0; o < FT; ++o) sh.z2bp[wave][o][l] = z2bp[0][o].v;
       sh.a2p[wave][l] = a2p[0][0].v;
@@ -428,7 +444,35 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     __syncthreads();
 
     // ---- readout layer 2, LayerNorm, residual
-    {
+    if constexpr (kLnRowSplit<FT, NW>) {
+      // rows 4*wave + j, feature l, as in the inner loss's LayerNorm; the
+      // last wave, which has no bias share above, saves A2
+      if (wave == NW - 1) {
+        f4 a2 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) a2 += sh.a2p[w][l];
+        bstore_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0, Tile{a2});
+      }
+      const int lo = l >> 4;
+      f4 z = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NW; ++w) z += sh.z2bp[w][lo][16 * wave + n];
+      constexpr float invF = 1.0f / F;
+      const f4 mu = sum4_wave(z) * invF;
+      const f4 d = z - mu;
+      const f4 var = sum4_wave(d * d) * invF;
+      const f4 q = frag_to_f4(xqr);
+      f4 rs, xhb, y;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        rs[j] = rsqrt_f(var[j] + eps);
+        xhb[j] = d[j] * rs[j];
+        y[j] = q[j] + lnw_l * xhb[j] + lnb_l;
+      }
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSB, Frag<float>{rs});
+      bstore_frag<float>(rSV, (lo * 64 + 16 * wave + n) * 16, us + Slot::XHB, Frag<float>{xhb});
+      bstore_ctile<T>(rOUT, l * ST, xo + 4 * wave * F * ST, F, to_frag<T>(y));
+    } else {
       Tile a2[1];
       a2[0].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll

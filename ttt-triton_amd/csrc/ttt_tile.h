@@ -222,15 +222,6 @@ __device__ __forceinline__ float max_row16(float x) {
   x = fmaxf(x, dpp<0x121>(x));
   return x;
 }
-// sum over all 64 lanes, as a wave-uniform value: the row sums are
-// accumulated into row 3 with row_bcast:15 (rows 1, 3) and row_bcast:31
-// (rows 2, 3), and lane 63 is read out
-__device__ __forceinline__ float sum_wave(float x) {
-  x = sum_row16(x);
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x142, 0xA, 0xF, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x143, 0xC, 0xF, false));
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
 // sum over the 4 lanes that share n (lanes n, n+16, n+32, n+48)
 // with gfx950's lane swaps (VALU, no trip through the LDS crossbar):
 // v_permlane32_swap exchanges the upper half of its first operand with the
@@ -244,6 +235,35 @@ __device__ __forceinline__ float sum_col4(float x) {
   const unsigned v = __builtin_bit_cast(unsigned, y);
   const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+// sum over all 64 lanes, in every lane: the row sums (sum_row16, equal in
+// the 16 lanes of a row) are added across rows with the two lane swaps of
+// sum_col4.  Each step adds a pair of lanes that then hold the same sum, so
+// every lane ends with the bitwise same value, and nothing goes through a
+// scalar register.
+__device__ __forceinline__ float sum_wave(float x) { return sum_col4(sum_row16(x)); }
+// v[j] summed over all 64 lanes for j = 0..3 at once, in every lane.  The four
+// reductions share their steps: the first lane swap of v[0] against v[1]
+// (v[2] against v[3]) leaves lanes 0-31 with v[0] (v[2]) and lanes 32-63
+// with v[1] (v[3]) summed over lanes l, l^32; the second swap of those two
+// against each other leaves 16-lane rows 0..3 with v[0], v[2], v[1], v[3]
+// summed over the four lanes l, l^16, l^32, l^48; sum_row16 finishes each row,
+// and two more swaps broadcast the four row totals to every lane.  13
+// instructions instead of 4 x 8, each result bitwise equal in all lanes.
+__device__ __forceinline__ f4 sum4_wave(f4 v) {
+  auto bits = [](float x) { return __builtin_bit_cast(unsigned, x); };
+  auto flt = [](unsigned x) { return __builtin_bit_cast(float, x); };
+  const auto a = __builtin_amdgcn_permlane32_swap(bits(v[0]), bits(v[1]), false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(bits(v[2]), bits(v[3]), false, false);
+  const float p = flt((unsigned)a[0]) + flt((unsigned)a[1]);  // lanes < 32: v[0], else v[1]
+  const float q = flt((unsigned)b[0]) + flt((unsigned)b[1]);  // lanes < 32: v[2], else v[3]
+  const auto c = __builtin_amdgcn_permlane16_swap(bits(p), bits(q), false, false);
+  // rows 0, 1, 2, 3: v[0], v[2], v[1], v[3]
+  const unsigned r = bits(sum_row16(flt((unsigned)c[0]) + flt((unsigned)c[1])));
+  const auto d = __builtin_amdgcn_permlane16_swap(r, r, false, false);  // [0]: v[0] | v[1], [1]: v[2] | v[3]
+  const auto e0 = __builtin_amdgcn_permlane32_swap((unsigned)d[0], (unsigned)d[0], false, false);
+  const auto e1 = __builtin_amdgcn_permlane32_swap((unsigned)d[1], (unsigned)d[1], false, false);
+  return f4{flt((unsigned)e0[0]), flt((unsigned)e0[1]), flt((unsigned)e1[0]), flt((unsigned)e1[1])};
 }
 
 // ---------------------------------------------------------------- loads / stores
