@@ -60,6 +60,38 @@ template <int FT, int NW> struct MlpBwdShared {
   float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
 };
 
+// The inner-loss LayerNorm backward is split over the waves by token rows
+// when there are four waves and F = 64, as in the forward: wave w takes rows
+// 4w..4w+3 with lane l on feature l, and the rows of dZ2 and dtgt meet in the
+// exchange area's [16 x 16] partial region, which is free from the barrier
+// after the dN1 / de / dG2 partials are read until the next mini-batch (dZ2 in
+// C layout and as the transposed operand frags of its products, dtgt in C
+// layout for the tile owners).
+template <int FT, int NW> constexpr bool kBwdRowSplit = (NW == 4 && FT == 4);
+constexpr int kRsDz2 = 0, kRsDtgt = 4096, kRsDz2T = 8192;  // byte offsets in the partial region
+
+typedef __attribute__((address_space(3))) unsigned short lds_u16;
+typedef __attribute__((address_space(3))) bf4 lds_bf4;
+// element (row r, feature 16c + q) of a [16 x F] matrix into its transposed
+// operand frags (free = row, k = feature): position q & 3 of lane 16 (q >> 2) + r
+// of tile c, tiles of 64 lanes x 4 elements
+template <typename T> __device__ __forceinline__ void lds_put_tfrag(unsigned base, int c, int r, int q, float v);
+template <> __device__ __forceinline__ void lds_put_tfrag<__bf16>(unsigned base, int c, int r, int q, float v) {
+  const unsigned a = base + 2u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
+  *(lds_u16*)(uintptr_t)a = __builtin_bit_cast(unsigned short, (__bf16)v);
+}
+template <> __device__ __forceinline__ void lds_put_tfrag<float>(unsigned base, int c, int r, int q, float v) {
+  const unsigned a = base + 4u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
+  *(lds_f32*)(uintptr_t)a = v;
+}
+template <typename T> __device__ __forceinline__ Frag<T> lds_get_tfrag(unsigned base, int c);
+template <> __device__ __forceinline__ Frag<__bf16> lds_get_tfrag<__bf16>(unsigned base, int c) {
+  return Frag<__bf16>{*(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)(c * 64 + lane_id()))};
+}
+template <> __device__ __forceinline__ Frag<float> lds_get_tfrag<float>(unsigned base, int c) {
+  return Frag<float>{*(lds_f4*)(uintptr_t)(base + 16u * (unsigned)(c * 64 + lane_id()))};
+}
+
 size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
   const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
   return (size_t)2 * FF * 16 * t + (size_t)2 * F * 64;
@@ -194,6 +226,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // wave's [16 x 16] blocks
   using Xch = MlpBwdExchange<FT, NW>;
   LdsLane xa(sh.x.mem, 0), xw(sh.x.mem, wave * FT * 1024), xs16(sh.x.mem, Xch::PART + wave * 1024);
+  // row split: lane l on feature l of rows 4*wave + j; xr.get(b * 1024) reads
+  // slot 16 wave + n of block b + l / 16, i.e. those rows of a lane-order tile set
+  constexpr bool RS = kBwdRowSplit<FT, NW>;
+  const int lo = l >> 4;
+  const int srow = (lo * 64 + 16 * wave + n) * 16;
+  LdsLane xr(sh.x.mem, 768 * lo + 256 * wave);
+  const unsigned dz2t_base = (unsigned)(uintptr_t)(lds_f32*)sh.x.mem + (unsigned)(Xch::PART + kRsDz2T);
 
   // gradient wrt the state after the current mini-batch (this wave's slice):
   // dW2[S, :] in registers, dW1[:, S] in LDS (below)
@@ -260,6 +299,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     dlnw[o] = 0.f;
     dlnb[o] = 0.f;
   }
+  // row split: the inner-loss LayerNorm's parameters and gradient partials of
+  // feature l over this wave's rows
+  float dlnw_l = 0.f, dlnb_l = 0.f;
+  const float lnw_l = RS ? p.ln_w[(size_t)h * F + l] : 0.f;
+  const float lnb_l = RS ? p.ln_b[(size_t)h * F + l] : 0.f;
 
   // inputs of the first phase of a mini-batch, requested one mini-batch ahead
   Frag<T> nxq[FT], nxk[FT], nx2f[HT], ng2e[FT];
@@ -603,15 +647,24 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         }
       }
       // inputs of the inner-loss backward and of B2b, requested before the barrier
-      const f4 rstd2 = bload_frag<float>(rSV, f4l, us + Slot::RSTD).v;
-      const f4 cc2 = bload_frag<float>(rSV, f4l, us + Slot::CC).v;
-      f4 xh2[FT], g22[FT];
-      Frag<T> xvf[FT], g1ef[HT];
+      // (split by rows: the statistics of rows 4*wave + j, XV and XK rows)
+      const int rsl = RS ? (16 * wave + n) * 16 : f4l;
+      const f4 rstd2 = bload_frag<float>(rSV, rsl, us + Slot::RSTD).v;
+      const f4 cc2 = bload_frag<float>(rSV, rsl, us + Slot::CC).v;
+      f4 xh2[RS ? 1 : FT], g22[RS ? 1 : FT];
+      Frag<T> xvf[RS ? 2 : FT], g1ef[HT];
+      if constexpr (RS) {
+        xh2[0] = bload_frag<float>(rSV, srow, us + Slot::XH).v;
+        g22[0] = bload_frag<float>(rSV, srow, us + Slot::G2).v;
+        xvf[0] = bload_ctile<T>(rXV, l * ST, xs(s) + 4 * wave * F * ST, F);
+        xvf[1] = bload_ctile<T>(rXK, l * ST, xs(s) + 4 * wave * F * ST, F);
+      } else {
 #pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        xh2[c] = ld_f32(c, Slot::XH, us);
-        g22[c] = ld_f32(c, Slot::G2, us);
-        xvf[c] = bload_frag<T>(rXV, xl + 16 * c * ST, xs(s));
+        for (int c = 0; c < FT; ++c) {
+          xh2[c] = ld_f32(c, Slot::XH, us);
+          g22[c] = ld_f32(c, Slot::G2, us);
+          xvf[c] = bload_frag<T>(rXV, xl + 16 * c * ST, xs(s));
+        }
       }
 #pragma unroll
       for (int o = 0; o < HT; ++o) g1ef[o] = bload_frag<T>(rSV, hl + o * 256 * ST, us + Slot::G1E);
@@ -622,7 +675,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 
       // ---- B2a: assemble dN1, de; deta (wave 0); dG2
       f4 dA1T, dA1;
-      Tile dG2[FT];
+      Tile dG2[RS ? 1 : FT];  // row split: rows 4*wave + j of feature l
       {
         f4 dn1 = f4{0.f, 0.f, 0.f, 0.f}, dn1T = f4{0.f, 0.f, 0.f, 0.f}, de = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -631,11 +684,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           dn1T += xa.get(Xch::PART + (NW + w) * 1024);
           de += xa.get(Xch::PART + (2 * NW + w) * 1024);
         }
+        if constexpr (RS) {
+          dG2[0].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < FT; ++c) {
-          dG2[c].v = f4{0.f, 0.f, 0.f, 0.f};
+          for (int w = 0; w < NW; ++w) dG2[0].v += xr.get(w * FT * 1024);
+        } else {
 #pragma unroll
-          for (int w = 0; w < NW; ++w) dG2[c].v += xa.get((w * FT + c) * 1024);
+          for (int c = 0; c < FT; ++c) {
+            dG2[c].v = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < NW; ++w) dG2[c].v += xa.get((w * FT + c) * 1024);
+          }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -662,9 +721,41 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       Frag<T> xqf[FT];  // XQ again (L2-resident), for the layer-1 state gradient
 #pragma unroll
       for (int q = 0; q < FT; ++q) xqf[q] = bload_frag<T>(rXQ, xl + 16 * q * ST, xs(s));
-      // ---- LN2: backward of G2 = ln_fused_l2_bwd(Z2, XV - XK) (every wave)
-      f4 dz2[FT], dtgt[FT];
-      {
+      // ---- LN2: backward of G2 = ln_fused_l2_bwd(Z2, XV - XK) (every wave, or
+      //      split by rows)
+      f4 dz2[RS ? 1 : FT], dtgt[RS ? 1 : FT];
+      if constexpr (RS) {
+        // ln_fused_l2_bwd's backward for rows 4*wave + j (the same terms as
+        // LnL2Lite::backward, with the row sums over the 64 lanes)
+        const f4 xh = xh2[0], G = g22[0];
+        const f4 tgt = frag_to_f4(xvf[0]) - frag_to_f4(xvf[1]);
+        const f4 u = dG2[0].v * rstd2;
+        const f4 mu_u = sum4_wave(u) * invF, mu_ux = sum4_wave(u * xh) * invF, dsig = -sum4_wave(u * G);
+        f4 dxh, dtg;
+        float aw = 0.f, ab = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float go = lnw_l * xh[j] + lnb_l - tgt[j];
+          const float gx = go * lnw_l;
+          const float d_gx = u[j] - mu_u[j] - xh[j] * mu_ux[j];
+          const float d_go = d_gx * lnw_l;
+          aw += d_gx * go + d_go * xh[j];
+          ab += d_go;
+          dtg[j] = -d_go;
+          dxh[j] = -cc2[j] * u[j] - mu_ux[j] * gx + d_go * lnw_l;
+        }
+        dlnw_l += aw;
+        dlnb_l += ab;
+        const f4 m1 = sum4_wave(dxh) * invF, m2 = sum4_wave(dxh * xh) * invF;
+        f4 dz;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dz[j] = rstd2[j] * (dxh[j] - m1[j] - xh[j] * m2[j]) + dsig[j] * xh[j] * invF;
+        xr.put(Xch::PART + kRsDz2, dz);
+        xr.put(Xch::PART + kRsDtgt, dtg);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds_put_tfrag<T>(dz2t_base, lo, 4 * wave + j, n, dz[j]);
+        bstore_ctile<T>(rDXV, l * ST, xs(s) + 4 * wave * F * ST, F, to_frag<T>(dtg));  // dXV rows
+      } else {
         float lw_i[FT], lb_i[FT];
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
@@ -697,6 +788,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           }
         }
       }
+      if constexpr (RS) __syncthreads();  // (1y) the rows of dZ2 and dtgt of every wave in
       // The checkpoint group that the previous mini-batch closed: this wave's
       // handoff stores for it (device-coherent, written through) have long been
       // issued, so waiting for them here costs little; barrier (2) then has
@@ -711,8 +803,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> dz2F[FT];
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          const Frag<T> dz2f = to_frag<T>(dz2[c]);
-          dz2F[c] = to_frag<T>(transpose16(dz2f, I).v);
+          Frag<T> dz2f;
+          if constexpr (RS) {
+            const f4 z = xa.get(Xch::PART + kRsDz2 + c * 1024);
+            dz2f = to_frag<T>(z);
+            dz2F[c] = lds_get_tfrag<T>(dz2t_base, c);
+            db2[c] += sum_col4(z[0] + z[1] + z[2] + z[3]);  // db2' was used in P
+          } else {
+            dz2f = to_frag<T>(dz2[c]);
+            dz2F[c] = to_frag<T>(transpose16(dz2f, I).v);
+          }
 #pragma unroll
           for (int o = 0; o < HT; ++o) mma16(dW2[o][c].v, x2f[o], dz2f);  // + X2^T dZ2
         }
@@ -759,12 +859,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int j = 0; j < 4; ++j) acc += dZ1[o].v[j];
         db1[o] += sum_col4(acc);
       }
+      if constexpr (!RS) {
 #pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        float acc = 0.f;
+        for (int c = 0; c < FT; ++c) {
+          float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc += dz2[c][j];
-        db2[c] += sum_col4(acc);
+          for (int j = 0; j < 4; ++j) acc += dz2[c][j];
+          db2[c] += sum_col4(acc);
+        }
       }
       __syncthreads();  // (2) dXK partials in
       if (publish && threadIdx.x == 0)
@@ -778,14 +880,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int f = 0; f < FT; ++f) {
           if (f % NW != wave) continue;
           f4 dxq = transpose16(NW >= FT ? dob : dof[f], I).v;  // (f == wave when NW >= FT)
-          f4 dxk = -dtgt[f];
+          const f4 dt = RS ? xa.get(Xch::PART + kRsDtgt + f * 1024) : dtgt[f];
+          f4 dxk = -dt;
 #pragma unroll
           for (int w = 0; w < NW; ++w) dxk += xa.get((w * FT + f) * 1024);
           mma16(dxq, dA1Tf, xkTf[f]);  // + dA1 XK
           mma16(dxk, dA1f, xqTf[f]);   // + dA1^T XQ
           bstore_frag_dev<float>(rWS, f4l + f * 1024, ws_ + WS::XQP, Frag<float>{dxq});
           bstore_frag_dev<float>(rWS, f4l + f * 1024, ws_ + WS::XKP, Frag<float>{dxk});
-          bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dtgt[f]), I).v));
+          if constexpr (!RS)
+            bstore_frag<T>(rDXV, xl + 16 * f * ST, xs(s), to_frag<T>(transpose16(to_frag<T>(dt), I).v));
         }
       }
       __syncthreads();  // (2x) exchange area free for the next mini-batch
@@ -817,11 +921,26 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       for (int o = 0; o < HT; ++o) p.db1[(size_t)chain * FF + hs + 16 * o + n] = db1[o];
     }
   }
+  // row split: every wave's partials of feature l through the exchange area
+  // (free since the last barrier of the sweep)
+  float* const red = reinterpret_cast<float*>(sh.x.mem);
+  if constexpr (RS) {
+    red[wave * 64 + l] = dlnw_l;
+    red[(NW + wave) * 64 + l] = dlnb_l;
+    __syncthreads();
+  }
   if (wave == 0) {
 #pragma unroll
     for (int o = 0; o < FT; ++o) {
-      const float w = sum_col4(dlnw[o]);
-      const float b = sum_col4(dlnb[o]);
+      float w = sum_col4(dlnw[o]);
+      float b = sum_col4(dlnb[o]);
+      if constexpr (RS) {
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+          w += red[v * 64 + 16 * o + n];
+          b += red[(NW + v) * 64 + 16 * o + n];
+        }
+      }
       if (g == 0) {
         p.db2[(size_t)chain * F + 16 * o + n] = db2[o];
         p.dln_w[(size_t)chain * F + 16 * o + n] = w;
