@@ -53,13 +53,6 @@ template <int FT, int NW> struct MlpBwdExchange {
   f4 mem[BYTES / 16];
 };
 
-template <int FT, int NW> struct MlpBwdShared {
-  float w2t[16 * FT * 64 * NW];   // W2^T  [F][FF], swizzled
-  float dw1t[16 * FT * 64 * NW];  // dW1^T [FF][F], swizzled
-  MlpBwdExchange<FT, NW> x;
-  float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
-};
-
 // The inner-loss LayerNorm backward is split over the waves by token rows
 // when there are four waves and F = 64, as in the forward: wave w takes rows
 // 4w..4w+3 with lane l on feature l, and the rows of dZ2 and dtgt meet in the
@@ -68,6 +61,20 @@ template <int FT, int NW> struct MlpBwdShared {
 // C layout and as the transposed operand frags of its products, dtgt in C
 // layout for the tile owners).
 template <int FT, int NW> constexpr bool kBwdRowSplit = (NW == 4 && FT == 4);
+// In bf16 the readout LayerNorm's backward (dZ2b from dout) is split the same
+// way; its rows meet in a region of their own (dZ2b in bf16 C-layout tiles,
+// then per-wave column sums), written after the last barrier of a mini-batch
+// and read after the first of the next, so no other phase touches it.
+constexpr int kRsL = 3072, kRsLCol = 2048;
+
+template <int FT, int NW> struct MlpBwdShared {
+  float w2t[16 * FT * 64 * NW];   // W2^T  [F][FF], swizzled
+  float dw1t[16 * FT * 64 * NW];  // dW1^T [FF][F], swizzled
+  MlpBwdExchange<FT, NW> x;
+  float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
+  alignas(16) unsigned char lx[kBwdRowSplit<FT, NW> ? kRsL : 16];  // readout LayerNorm rows (row split, bf16)
+};
+
 constexpr int kRsDz2 = 0, kRsDtgt = 4096, kRsDz2T = 8192;  // byte offsets in the partial region
 
 typedef __attribute__((address_space(3))) unsigned short lds_u16;
@@ -229,6 +236,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // row split: lane l on feature l of rows 4*wave + j; xr.get(b * 1024) reads
   // slot 16 wave + n of block b + l / 16, i.e. those rows of a lane-order tile set
   constexpr bool RS = kBwdRowSplit<FT, NW>;
+  constexpr bool RSL = RS && ST == 2;
   const int lo = l >> 4;
   const int srow = (lo * 64 + 16 * wave + n) * 16;
   LdsLane xr(sh.x.mem, 768 * lo + 256 * wave);
@@ -299,11 +307,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
     dlnw[o] = 0.f;
     dlnb[o] = 0.f;
   }
-  // row split: the inner-loss LayerNorm's parameters and gradient partials of
-  // feature l over this wave's rows
+  // row split: the LayerNorm parameter gradient partials of feature l over
+  // this wave's rows (the parameters themselves are re-read from LDS where used)
   float dlnw_l = 0.f, dlnb_l = 0.f;
-  const float lnw_l = RS ? p.ln_w[(size_t)h * F + l] : 0.f;
-  const float lnb_l = RS ? p.ln_b[(size_t)h * F + l] : 0.f;
 
   // inputs of the first phase of a mini-batch, requested one mini-batch ahead
   Frag<T> nxq[FT], nxk[FT], nx2f[HT], ng2e[FT];
@@ -365,15 +371,23 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       const Frag<T> dob = bload_frag<T>(rDO, xl + 16 * (wave % FT) * ST, xs(s));
       const f4 a2T = bload_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0).v;  // A2^T [t_k x t_q]
       const f4 a2 = bload_frag<float>(rSV, a2tl, us + Slot::A2T).v;    // A2   [t_q x t_k]
-      const f4 rsb = bload_frag<float>(rSV, f4l, us + Slot::RSB).v;
-      f4 xhb[FT], g2v[FT];
-      Frag<T> dof[FT];
+      // (split by rows: dout, the normalised rows and their statistics of rows
+      // 4*wave + j)
+      const f4 rsb = bload_frag<float>(rSV, RSL ? (16 * wave + n) * 16 : f4l, us + Slot::RSB).v;
+      f4 xhb[RSL ? 1 : FT], g2v[FT];
+      Frag<T> dof[RSL ? 1 : FT];
       float lnw_tm[FT];
       ln_param(sh.lnw, lnw_tm);
+      if constexpr (RSL) {
+        xhb[0] = bload_frag<float>(rSV, srow, us + Slot::XHB).v;
+        dof[0] = bload_ctile<T>(rDO, l * ST, xs(s) + 4 * wave * F * ST, F);
+      }
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
-        xhb[c] = ld_f32(c, Slot::XHB, us);
-        dof[c] = bload_frag<T>(rDO, xl + 16 * c * ST, xs(s));
+        if constexpr (!RSL) {
+          xhb[c] = ld_f32(c, Slot::XHB, us);
+          dof[c] = bload_frag<T>(rDO, xl + 16 * c * ST, xs(s));
+        }
         g2v[c] = ld_f32(c, Slot::G2, us);
       }
 
@@ -426,7 +440,36 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       // ---- L: readout layer 2 LayerNorm backward (every wave): dZ2b from dout
       Frag<T> dz2bf[FT], dz2bF[FT];
       float dz2b_cs[FT];  // column sums of dZ2b (fp32)
-      {
+      if constexpr (RSL) {
+        // rows 4*wave + j of feature l
+        const f4 dT = frag_to_f4(dof[0]), xh = xhb[0];
+        const f4 gy = dT * sh.lnw[l];
+        const f4 s1 = sum4_wave(gy) * invF, s2 = sum4_wave(gy * xh) * invF;
+        f4 dz;
+        float aw = 0.f, ab = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          aw += dT[j] * xh[j];
+          ab += dT[j];
+          dz[j] = rsb[j] * (gy[j] - s1[j] - xh[j] * s2[j]);
+        }
+        dlnw_l += aw;
+        dlnb_l += ab;
+        const unsigned lxb = (unsigned)(uintptr_t)(lds_f32*)sh.lx;
+        *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(lo * 64 + 16 * wave + n)) = to_frag<T>(dz).v;
+        *(lds_f32*)(uintptr_t)(lxb + kRsLCol + 4u * (unsigned)(wave * 64 + n * 4 + lo)) = dz[0] + dz[1] + dz[2] + dz[3];
+        __syncthreads();  // (L) the rows of dZ2b of every wave in
+#pragma unroll
+        for (int c = 0; c < FT; ++c) {
+          dz2bf[c].v = *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(c * 64 + l));
+          dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
+        }
+        f4 cs = f4{0.f, 0.f, 0.f, 0.f};  // column sums of features 16c + n
+#pragma unroll
+        for (int w = 0; w < NW; ++w) cs += *(lds_f4*)(uintptr_t)(lxb + kRsLCol + 16u * (unsigned)(w * 16 + n));
+#pragma unroll
+        for (int c = 0; c < FT; ++c) dz2b_cs[c] = cs[c];
+      } else {
         f4 gy[FT];
         f4 s1 = f4{0.f, 0.f, 0.f, 0.f}, s2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -729,6 +772,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         // LnL2Lite::backward, with the row sums over the 64 lanes)
         const f4 xh = xh2[0], G = g22[0];
         const f4 tgt = frag_to_f4(xvf[0]) - frag_to_f4(xvf[1]);
+        const float lnw_l = sh.lnw[l], lnb_l = sh.lnb[l];
         const f4 u = dG2[0].v * rstd2;
         const f4 mu_u = sum4_wave(u) * invF, mu_ux = sum4_wave(u * xh) * invF, dsig = -sum4_wave(u * G);
         f4 dxh, dtg;
