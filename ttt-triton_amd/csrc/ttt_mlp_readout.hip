@@ -3,11 +3,11 @@
 // for every token of a segment, with one (W1, b1, W2, b2) per (batch, head)
 // chain (kernels/mlp_cached_readout.py:88-109,143, indexed per chain).
 //
-// The weights are fixed, so tokens are independent: a workgroup of four waves
+// The weights are fixed, so tokens are independent: a workgroup of eight waves
 // takes one chain and a chunk of up to 256 tokens.  It stages the chain's W1
 // and W2 once into LDS, already in MFMA operand order (one 4-element vector
 // per lane per 16x16 block, so every operand read is one conflict-free
-// ds_read), then each wave runs up to four 16-token tiles through
+// ds_read), then each wave runs up to two 16-token tiles through
 //
 //   Z1^T = W1^T XQ^T           (hidden x token: its C layout is the A operand
 //   X2^T = gelu(Z1^T + b1)      of the next product with no transpose)
@@ -15,7 +15,9 @@
 //   out  = XQ + ln_w * (Z2 - mean) / sqrt(var + eps) + ln_b
 //
 // W is read from HBM once per workgroup; blocks are mapped so that the chunks
-// of one chain run on one XCD and share its L2.
+// of one chain run on one XCD and share its L2.  Two workgroups fit a CU's LDS
+// and the waves stay within 128 registers, so each SIMD interleaves four
+// waves (measured 5% faster at B16 H12 T2048 than four waves of four tiles).
 #include "ttt_fixed_mlp.h"
 #include "ttt_kernels.h"
 
@@ -27,8 +29,8 @@ template <typename T, int FT, int HTT> struct ReadoutShared {
   float lnb[16 * FT];
 };
 
-constexpr int kReadoutWaves = 4;
-constexpr int kReadoutTilesPerWave = 4;
+constexpr int kReadoutWaves = 8;
+constexpr int kReadoutTilesPerWave = 2;
 constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave;  // tokens per workgroup
 
 template <typename T, int FT, int HTT>
