@@ -1,7 +1,8 @@
 // TTT-MLP backward on gfx950: a reverse sweep per chain and a dXQ/dXK pass.
 //
-// 1. mlp_bwd_kernel: one workgroup of NW = FF/64 wavefronts per (batch, head)
-//    chain, wave w owning hidden units S = [64w, 64w+64), walks the sequence
+// 1. mlp_bwd_kernel: one workgroup of NW wavefronts per (batch, head) chain,
+//    wave w owning HT hidden tiles S = [16 HT w, 16 HT (w+1)) (HT = 4, or
+//    four waves of one tile for FF = F = 64, as in the forward), walks the sequence
 //    in reverse and carries the gradient wrt the state, dW1, db1, dW2, db2.
 //    Inputs besides the sequence: the forward's final W2 and its saved
 //    buffer, which holds for every mini-batch the state-update
@@ -36,6 +37,8 @@
 // per-slice [16 x 64] temporaries are consumed in the order they are made (dX2
 // folds into dZ1, dG1 into dP and dZ1, the -e Q2 share straight into the
 // exchange area) so that the loop runs without spilling.
+#include <type_traits>
+
 #include "ttt_buf.h"
 #include "ttt_eta.h"
 #include "ttt_kernels.h"
@@ -67,9 +70,9 @@ template <int FT, int NW> constexpr bool kBwdRowSplit = (NW == 4 && FT == 4);
 // and read after the first of the next, so no other phase touches it.
 constexpr int kRsL = 3072, kRsLCol = 2048;
 
-template <int FT, int NW> struct MlpBwdShared {
-  float w2t[16 * FT * 64 * NW];   // W2^T  [F][FF], swizzled
-  float dw1t[16 * FT * 64 * NW];  // dW1^T [FF][F], swizzled
+template <int FT, int NW, int HT> struct MlpBwdShared {
+  float w2t[16 * FT * 16 * HT * NW];   // W2^T [F][FF] (or W2 [FF][F] by the waves' rows), swizzled
+  float dw1t[16 * FT * 16 * HT * NW];  // dW1^T [FF][F], swizzled
   MlpBwdExchange<FT, NW> x;
   float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
   alignas(16) unsigned char lx[kBwdRowSplit<FT, NW> ? kRsL : 16];  // readout LayerNorm rows (row split, bf16)
@@ -112,7 +115,7 @@ size_t mlp_bwd_ctrl_bytes(int B, int H, int NC, int G) {
   return (words * 4 + 255) & ~(size_t)255;
 }
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk, bool poison);
 
 // Fused mode: workgroups B*H.. of the sweep's launch.  Each takes (chain,
@@ -134,7 +137,7 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
 // store; the worker polls the flag with device-scope loads and reads the
 // handoff with device-coherent (sc1) loads, which no stale L1 or L2 line
 // serves.  Neither side writes back or invalidates a whole L2.
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 __device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
   __shared__ int task_sh, gave_up_sh;
   const int nchain = p.B * p.H, ntask = nchain * p.NK;
@@ -160,33 +163,32 @@ __device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
     }
     __syncthreads();  // the group's flag was seen (its handoff stores are complete), or the wait gave up
     const bool poison = gave_up_sh != 0;
-    mlp_bwd_dx_body<T, FT, NW>(p, chain, kk, poison);
+    mlp_bwd_dx_body<T, FT, NW, HT>(p, chain, kk, poison);
   }
 }
 
-template <typename T, int FT, int NW, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   if constexpr (NW == FT) {
     if ((int)blockIdx.x >= p.B * p.H) {
-      mlp_bwd_dx_worker<T, FT, NW>(p);
+      mlp_bwd_dx_worker<T, FT, NW, HT>(p);
       return;
     }
   }
   constexpr int F = 16 * FT;
   constexpr int K = 16;
-  constexpr int HT = 4;
-  constexpr int FF = 64 * NW;
+  constexpr int FF = 16 * HT * NW;  // HT hidden tiles per wave
   constexpr float invF = 1.0f / F;
   constexpr int ST = (int)sizeof(T);
   using Slot = MlpSavedSlot<F, FF, ST>;
-  __shared__ MlpBwdShared<FT, NW> sh;
+  __shared__ MlpBwdShared<FT, NW, HT> sh;
 
   const int chain = blockIdx.x;
   const int h = chain % p.H;
   const int NC = p.NC, G = p.G, NK = p.NK;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int l = lane_id(), g = l >> 4, n = l & 15;
-  const int hs = 64 * wave;
+  const int hs = 16 * HT * wave;
 
   // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
@@ -255,7 +257,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
   // LDS views (this wave's hidden columns of W2^T, its hidden rows of dW1^T)
-  LdsMat<FF> W2t(sh.w2t, hs);
+  // (a slice of one tile is narrower than LdsMat's 32-column swizzle groups:
+  // then W2 is kept by rows, this wave's [16 HT x F] rows, and the two access
+  // shapes swap)
+  constexpr bool W2ROWS = (HT & 1) != 0;
+  using W2Mat = std::conditional_t<W2ROWS, LdsMat<F>, LdsMat<FF>>;
+  W2Mat W2t(W2ROWS ? sh.w2t + hs * F : sh.w2t, W2ROWS ? 0 : hs);
   LdsMat<F> dW1s(sh.dw1t + hs * F, 0);
   // dW1 tile [F block q x hidden block o] (C layout), also its frag (free = hidden, k = feature)
   auto dw1_get = [&](int q, int o) {
@@ -273,12 +280,25 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // W2 tile [hidden block o x F block c] (C layout): frag (free = feature, k = hidden)
   auto w2_tile = [&](int o, int c) {
     Tile t;
-    t.v = W2t.row4(16 * c, 16 * o);
+    if constexpr (W2ROWS)
+      t = W2t.tile(16 * o, 16 * c);
+    else
+      t.v = W2t.row4(16 * c, 16 * o);
     return t;
   };
-  auto w2_put = [&](int o, int c, Tile t) { W2t.put_row4(16 * c, 16 * o, t.v); };
+  auto w2_put = [&](int o, int c, Tile t) {
+    if constexpr (W2ROWS)
+      W2t.put_tile(16 * o, 16 * c, t);
+    else
+      W2t.put_row4(16 * c, 16 * o, t.v);
+  };
   // W2^T frag (free = hidden block o, k = feature block c)
-  auto w2T_frag = [&](int o, int c) { return to_frag<T>(W2t.tile(16 * c, 16 * o).v); };
+  auto w2T_frag = [&](int o, int c) {
+    if constexpr (W2ROWS)
+      return to_frag<T>(W2t.row4(16 * o, 16 * c));
+    else
+      return to_frag<T>(W2t.tile(16 * c, 16 * o).v);
+  };
   // keep the gradient accumulators in the MFMA accumulator registers
   auto pin_dW = [&]() {
 #pragma unroll
@@ -598,9 +618,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         }
         f4 dn = f4{0.f, 0.f, 0.f, 0.f}, dnT = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int o = 0; o < HT; o += 2) {
+        for (int o = 0; o + 1 < HT; o += 2) {
           mma32(dn, dz1bF[o], dz1bF[o + 1], g1F[o], g1F[o + 1]);
           mma32(dnT, g1F[o], g1F[o + 1], dz1bF[o], dz1bF[o + 1]);
+        }
+        if constexpr (HT & 1) {
+          mma16(dn, dz1bF[HT - 1], g1F[HT - 1]);
+          mma16(dnT, g1F[HT - 1], dz1bF[HT - 1]);
         }
         xs16.put(0, dn);
         xs16.put(NW * 1024, dnT);
@@ -651,8 +675,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int c = 0; c < FT; ++c) {
           f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int o = 0; o < HT; o += 2)
+          for (int o = 0; o + 1 < HT; o += 2)
             mma32(q2, x2F[o], x2F[o + 1], to_frag<T>(dW2[o][c].v), to_frag<T>(dW2[o + 1][c].v));
+          if constexpr (HT & 1) mma16(q2, x2F[HT - 1], to_frag<T>(dW2[HT - 1][c].v));
           // Q2 enters dG2 as -e Q2 and the eta-row gradient as G2 . Q2, both
           // linear in Q2: this slice's share goes into the partials as it is
           // (wave 0's share carries db2')
@@ -666,8 +691,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           }
           mma16(z, m2f, dz2bf[c]);
 #pragma unroll
-          for (int o = 0; o < HT; o += 2)
+          for (int o = 0; o + 1 < HT; o += 2)
             mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
+          if constexpr (HT & 1) mma16(z, dPF[HT - 1], to_frag<T>(w2_tile(HT - 1, c).v));
           xw.put(c * 1024, z);
         }
 #pragma unroll
@@ -877,7 +903,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         for (int f = 0; f < FT; ++f) {
           f4 zk_ = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < HT; c += 2) mma32(zk_, eg1F[c], eg1F[c + 1], dw1T_frag(f, c), dw1T_frag(f, c + 1));
+          for (int c = 0; c + 1 < HT; c += 2) mma32(zk_, eg1F[c], eg1F[c + 1], dw1T_frag(f, c), dw1T_frag(f, c + 1));
+          if constexpr (HT & 1) mma16(zk_, eg1F[HT - 1], dw1T_frag(f, HT - 1));
           xw.put(f * 1024, zk_);
         }
       }
@@ -1001,11 +1028,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 // checkpoint and steps forward with the saved update operands,
 // W1_{s+1}^T = W1_s^T + (-e G1_s)^T XK_s.  With `poison` (a fused worker
 // that gave up waiting for the group) the group's rows get NaN instead.
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain, int kk, bool poison) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
-  constexpr int FF = 64 * NW;
+  constexpr int FF = 16 * HT * NW;
   constexpr int HB = FF / 16;  // hidden blocks
   constexpr int ST = (int)sizeof(T);
   using Slot = MlpSavedSlot<F, FF, ST>;
@@ -1095,10 +1122,10 @@ __device__ __forceinline__ void mlp_bwd_dx_body(const MlpBwdParams& p, int chain
   }
 }
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 __global__ __launch_bounds__(64 * FT) void mlp_bwd_dx_kernel(MlpBwdParams p) {
   const int chain = blockIdx.x / p.NK, kk = blockIdx.x - chain * p.NK;
-  mlp_bwd_dx_body<T, FT, NW>(p, chain, kk, false);
+  mlp_bwd_dx_body<T, FT, NW, HT>(p, chain, kk, false);
 }
 
 __global__ void mlp_bwd_ctrl_clear_kernel(int* ctrl, int n) {
@@ -1118,12 +1145,12 @@ static int device_cus() {
   return cus[dev];
 }
 
-// Fused when the workgroups are alike (one wave per 64 hidden units = one per
-// feature tile) and every chain's sweep fits on the device at once with CUs to
-// spare for workers; otherwise the dXQ/dXK pass is a second launch.
+// Fused when the workgroups are alike (as many sweep waves as feature tiles)
+// and every chain's sweep fits on the device at once with CUs to spare for
+// workers; otherwise the dXQ/dXK pass is a second launch.
 // The control words are cleared in both modes, so that the timeout word read
 // by ttt_mlp_bwd_check always belongs to this call.
-template <typename T, int FT, int NW, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR>
 static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   const int chains = p.B * p.H, cus = device_cus();
   const bool fused = NW == FT && p.dx_fused != 0 && p.dx_ctrl != nullptr && cus >= chains + 16;
@@ -1133,30 +1160,32 @@ static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if (!fused) {
     p.dx_ctrl = nullptr;
-    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, LR>), dim3(chains), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR>), dim3(chains), dim3(64 * NW), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW>), dim3(chains * p.NK), dim3(64 * FT), 0, stream, p);
+    hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW, HT>), dim3(chains * p.NK), dim3(64 * FT), 0, stream, p);
     return hipGetLastError();
   }
   // the sweeps, then one worker per CU: the first cus - chains run beside the
   // sweeps, the rest start on the CUs the sweeps leave
-  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, LR>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
+  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 static hipError_t launch_mlp_bwd_e(const MlpBwdParams& p, hipStream_t stream) {
-  return p.eta_rule == TTT_ETA_DENSE ? launch_mlp_bwd_t<T, FT, NW, false>(p, stream)
-                                     : launch_mlp_bwd_t<T, FT, NW, true>(p, stream);
+  return p.eta_rule == TTT_ETA_DENSE ? launch_mlp_bwd_t<T, FT, NW, HT, false>(p, stream)
+                                     : launch_mlp_bwd_t<T, FT, NW, HT, true>(p, stream);
 }
 
 template <typename T, int FT>
 static hipError_t launch_mlp_bwd_f(const MlpBwdParams& p, hipStream_t stream) {
   switch (p.FF) {
-    case 64: return launch_mlp_bwd_e<T, FT, 1>(p, stream);
-    case 128: return launch_mlp_bwd_e<T, FT, 2>(p, stream);
-    case 256: return launch_mlp_bwd_e<T, FT, 4>(p, stream);
+    case 64:  // four waves of one hidden tile where the LayerNorms split by rows (F = 64)
+      if constexpr (FT == 4) return launch_mlp_bwd_e<T, FT, 4, 1>(p, stream);
+      else return launch_mlp_bwd_e<T, FT, 1, 4>(p, stream);
+    case 128: return launch_mlp_bwd_e<T, FT, 2, 4>(p, stream);
+    case 256: return launch_mlp_bwd_e<T, FT, 4, 4>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -1,9 +1,11 @@
 // TTT-MLP mini-batch forward on gfx950.
 //
-// One workgroup per (batch, head) chain with NW = FF/64 wavefronts.  Wave w
-// owns hidden units [64w, 64w+64): its slice of W1 (F x 64) and W2 (64 x F)
-// stays in registers (fp32, MFMA accumulator layout) for all NC mini-batches;
-// b2 is replicated in every wave.  Per mini-batch of K = 16 tokens
+// One workgroup per (batch, head) chain with NW wavefronts of HT hidden tiles
+// each (FF = 16 HT NW: HT = 4 for FF = 128, 256 and for FF = 64 at F = 32;
+// four waves of one tile for FF = 64 at F = 64, so that the LayerNorms split
+// by rows as below).  Wave w owns hidden units [16 HT w, 16 HT (w+1)): its
+// slice of W1 (F x 16HT) and W2 (16HT x F) stays in registers (fp32, MFMA
+// accumulator layout) for all NC mini-batches; b2 is replicated in every wave.  Per mini-batch of K = 16 tokens
 // (ops/ttt_mlp.py:9-67, dual form with a full KxK eta):
 //
 //   Z1 = XK W1 + b1, X2 = gelu(Z1)               per wave, its 64 hidden units
@@ -61,12 +63,11 @@ template <int FT, int NW> struct MlpFwdShared {
 // the four partials of a row add up to Z2b and no wave forms all of it.
 template <int FT, int NW> constexpr bool kLnRowSplit = (NW == 4 && FT == 4);
 
-template <typename T, int FT, int NW, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR>
 __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
-  constexpr int HT = 4;  // hidden tiles per wave
-  constexpr int FF = 64 * NW;
+  constexpr int FF = 16 * HT * NW;  // HT hidden tiles per wave
   constexpr int ST = (int)sizeof(T);
   using Slot = MlpSavedSlot<F, FF, ST>;
   __shared__ MlpFwdShared<FT, NW> sh;
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   const int NC = p.NC;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int l = lane_id(), g = l >> 4, n = l & 15;
-  const int hs = 64 * wave;  // first hidden unit of this wave
+  const int hs = 16 * HT * wave;  // first hidden unit of this wave
 
   // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
@@ -569,24 +570,26 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   }
 }
 
-template <typename T, int FT, int NW>
+template <typename T, int FT, int NW, int HT>
 static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
-  static_assert(MlpSavedSlot<16 * FT, 64 * NW, (int)sizeof(T)>::BYTES ==
-                    (int)mlp_saved_slot_bytes_of(16 * FT, 64 * NW, (int)sizeof(T)),
+  static_assert(MlpSavedSlot<16 * FT, 16 * HT * NW, (int)sizeof(T)>::BYTES ==
+                    (int)mlp_saved_slot_bytes_of(16 * FT, 16 * HT * NW, (int)sizeof(T)),
                 "saved slot layout");
   if (p.eta_rule == TTT_ETA_DENSE)
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, false>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, HT, false>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   else
-    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, true>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, HT, true>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }
 
 template <typename T, int FT>
 static hipError_t launch_mlp_fwd_f(const MlpFwdParams& p, hipStream_t stream) {
   switch (p.FF) {
-    case 64: return launch_mlp_fwd_t<T, FT, 1>(p, stream);
-    case 128: return launch_mlp_fwd_t<T, FT, 2>(p, stream);
-    case 256: return launch_mlp_fwd_t<T, FT, 4>(p, stream);
+    case 64:  // four waves of one hidden tile where the LayerNorms split by rows (F = 64)
+      if constexpr (FT == 4) return launch_mlp_fwd_t<T, FT, 4, 1>(p, stream);
+      else return launch_mlp_fwd_t<T, FT, 1, 4>(p, stream);
+    case 128: return launch_mlp_fwd_t<T, FT, 2, 4>(p, stream);
+    case 256: return launch_mlp_fwd_t<T, FT, 4, 4>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
