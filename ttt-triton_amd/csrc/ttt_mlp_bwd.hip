@@ -1181,10 +1181,12 @@ static hipError_t launch_mlp_bwd_e(const MlpBwdParams& p, hipStream_t stream) {
 template <typename T, int FT>
 static hipError_t launch_mlp_bwd_f(const MlpBwdParams& p, hipStream_t stream) {
   switch (p.FF) {
-    case 64:  // four waves of one hidden tile where the LayerNorms split by rows (F = 64)
+    case 64:  // at F = 64 four waves of FF/64 hidden tiles, so that the LayerNorms split by rows
       if constexpr (FT == 4) return launch_mlp_bwd_e<T, FT, 4, 1>(p, stream);
       else return launch_mlp_bwd_e<T, FT, 1, 4>(p, stream);
-    case 128: return launch_mlp_bwd_e<T, FT, 2, 4>(p, stream);
+    case 128:
+      if constexpr (FT == 4) return launch_mlp_bwd_e<T, FT, 4, 2>(p, stream);
+      else return launch_mlp_bwd_e<T, FT, 2, 4>(p, stream);
     case 256: return launch_mlp_bwd_e<T, FT, 4, 4>(p, stream);
     default: return hipErrorInvalidValue;
   }

@@ -1,9 +1,8 @@
 // TTT-MLP mini-batch forward on gfx950.
 //
 // One workgroup per (batch, head) chain with NW wavefronts of HT hidden tiles
-// each (FF = 16 HT NW: HT = 4 for FF = 128, 256 and for FF = 64 at F = 32;
-// four waves of one tile for FF = 64 at F = 64, so that the LayerNorms split
-// by rows as below).  Wave w owns hidden units [16 HT w, 16 HT (w+1)): its
+// each (FF = 16 HT NW): at F = 64 always four waves (HT = FF/64), so that the
+// LayerNorms split by rows as below; at F = 32 waves of four tiles.  Wave w owns hidden units [16 HT w, 16 HT (w+1)): its
 // slice of W1 (F x 16HT) and W2 (16HT x F) stays in registers (fp32, MFMA
 // accumulator layout) for all NC mini-batches; b2 is replicated in every wave.  Per mini-batch of K = 16 tokens
 // (ops/ttt_mlp.py:9-67, dual form with a full KxK eta):
@@ -585,10 +584,12 @@ static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
 template <typename T, int FT>
 static hipError_t launch_mlp_fwd_f(const MlpFwdParams& p, hipStream_t stream) {
   switch (p.FF) {
-    case 64:  // four waves of one hidden tile where the LayerNorms split by rows (F = 64)
+    case 64:  // at F = 64 four waves of FF/64 hidden tiles, so that the LayerNorms split by rows
       if constexpr (FT == 4) return launch_mlp_fwd_t<T, FT, 4, 1>(p, stream);
       else return launch_mlp_fwd_t<T, FT, 1, 4>(p, stream);
-    case 128: return launch_mlp_fwd_t<T, FT, 2, 4>(p, stream);
+    case 128:
+      if constexpr (FT == 4) return launch_mlp_fwd_t<T, FT, 4, 2>(p, stream);
+      else return launch_mlp_fwd_t<T, FT, 2, 4>(p, stream);
     case 256: return launch_mlp_fwd_t<T, FT, 4, 4>(p, stream);
     default: return hipErrorInvalidValue;
   }
