@@ -454,6 +454,59 @@ def run_forecaster(torch, steps, warmup, head_dim=FC_F, mini_batch=K):
             float(loss.item()), cfg)
 
 
+def run_forecaster_graph(torch, steps, warmup, head_dim=FC_F, mini_batch=K):
+    """The same training step and inference forward, each captured once in a
+    HIP graph (torch.cuda.CUDAGraph; AdamW with capturable state) and timed
+    by replays: the launches' host cost leaves the step.  Replays equal eager
+    steps bitwise (tests/test_gpu_layer.py checks it at batch 2)."""
+    dev = torch.device("cuda:0")
+    cfg, model, x, y = forecaster_setup(torch, FC_B, head_dim, mini_batch)
+    model = model.to(dev)
+    sx, sy = x.to(dev), y.to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=1e-2, capturable=True)
+
+    def train_step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            pred = model(sx)
+        loss = torch.nn.functional.mse_loss(pred.float(), sy)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        return loss
+
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(warmup, 2)):
+            opt.zero_grad(set_to_none=True)
+            train_step()
+    torch.cuda.current_stream().wait_stream(side)
+    g_train = torch.cuda.CUDAGraph()
+    opt.zero_grad(set_to_none=True)
+    with torch.cuda.graph(g_train):
+        loss = train_step()
+    g_inf = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                model(sx)
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(g_inf):
+            model(sx)
+    out = []
+    for g in (g_train, g_inf):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        out.append((time.perf_counter() - t0) / steps)
+    return out[0], out[1], float(loss.item())
+
+
 def roofline(kernel, sec, flops, nbytes, mfma_peak):
     """Binding roofline of one kernel: whichever of MFMA and HBM gives the
     longer ideal time for its algorithmic work."""
@@ -545,6 +598,8 @@ def main():
     mk = run_memo(torch, args.steps, args.warmup)
     print("[bench] forecaster train step + inference", file=sys.stderr, flush=True)
     fc_train, fc_inf, fc_wall_train, fc_wall_inf, fc_loss, _ = run_forecaster(torch, args.steps, args.warmup)
+    print("[bench] forecaster train step + inference, each one HIP graph", file=sys.stderr, flush=True)
+    fg_train, fg_inf, _ = run_forecaster_graph(torch, args.steps, args.warmup)
     print("[bench] forecaster at the reference ModelConfig shape (K=64, F=FF=32)", file=sys.stderr, flush=True)
     rc_train, rc_inf, _, _, rc_loss, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=32, mini_batch=64)
 
@@ -617,6 +672,8 @@ def main():
                 "train_step_ms": round(fc_train * 1e3, 3), "train_tokens_per_s": round(FC_B * FC_L / fc_train, 1),
                 "inference_ms": round(fc_inf * 1e3, 3), "inference_tokens_per_s": round(FC_B * FC_L / fc_inf, 1),
                 "wall_ms_train": round(fc_wall_train * 1e3, 3), "wall_ms_inference": round(fc_wall_inf * 1e3, 3),
+                "graph_train_step_ms": round(fg_train * 1e3, 3), "graph_train_tokens_per_s": round(FC_B * FC_L / fg_train, 1),
+                "graph_inference_ms": round(fg_inf * 1e3, 3), "graph_inference_tokens_per_s": round(FC_B * FC_L / fg_inf, 1),
                 "loss": round(fc_loss, 5),
                 "shape": f"batch {FC_B}, lookback {FC_L}, horizon {FC_PRED}, {FC_CH} channels, TTT-MLP H={FC_H} "
                          f"F={FC_F} (model_dim {FC_H * FC_F}), K={K}, memo M={FC_M}, G={FC_G}, bf16 autocast, AdamW",

@@ -195,3 +195,71 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
         if e > tp:
             bad.append(name)
     assert not bad
+
+
+def test_forecaster_step_in_a_graph_matches_eager():
+    """The config-4 training step (forward, loss, backward, gradient clipping,
+    AdamW) and an inference forward captured once each in a HIP graph
+    (torch.cuda.CUDAGraph): every replay, with eager steps of a copy of the
+    model between the replays, matches those eager steps (loss, every
+    parameter, the inference output).  The library's launches go to the
+    current stream and allocate nothing outside torch, so they capture."""
+    import copy
+    B, L, H, F_ = 2, 512, 4, 64
+    _say(f"forecaster graph B{B} L{L} H{H} F{F_}")
+    cfg, model, x, y = _forecaster("ttt_mlp", B, L, H, F_, 2, seed=93)
+    dev = torch.device("cuda")
+    model = model.to(dev)
+    sx, sy = x.to(dev), y.to(dev)
+    model_e = copy.deepcopy(model)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=1e-2, capturable=True)
+    opt_e = torch.optim.AdamW(model_e.parameters(), lr=1e-3, weight_decay=1e-2, capturable=True)
+
+    def step(m, o):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            pred = m(sx)
+        loss = torch.nn.functional.mse_loss(pred.float(), sy)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
+        o.step()
+        return loss
+
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            opt.zero_grad(set_to_none=True)
+            step(model, opt)
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(2):
+        opt_e.zero_grad(set_to_none=True)
+        step(model_e, opt_e)
+    g = torch.cuda.CUDAGraph()
+    opt.zero_grad(set_to_none=True)
+    with torch.cuda.graph(g):
+        sloss = step(model, opt)
+    for r in range(3):
+        g.replay()
+        opt_e.zero_grad(set_to_none=True)
+        le = step(model_e, opt_e)
+        torch.cuda.synchronize()
+        dl = abs(float(sloss.detach()) - float(le.detach())) / abs(float(le.detach()))
+        dp = max(float((a - b).abs().max() / (b.abs().max() + 1e-12))
+                 for a, b in zip(model.parameters(), model_e.parameters()))
+        _say(f"  replay {r}: loss rel {dl:.2e}, parameters max rel {dp:.2e}")
+        assert dl <= 1e-6 and dp <= 1e-6
+    gi = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            model(sx)
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(gi):
+            sout = model(sx)
+        for r in range(2):
+            gi.replay()
+            eo = model_e(sx)  # the eager copy holds the same parameters
+            torch.cuda.synchronize()
+            d = float((sout.float() - eo.float()).abs().max() / (eo.float().abs().max() + 1e-12))
+            _say(f"  inference replay {r}: max rel {d:.2e}")
+            assert d <= 1e-6
