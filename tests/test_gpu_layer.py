@@ -244,8 +244,9 @@ def test_forecaster_step_in_a_graph_matches_eager():
         le = step(model_e, opt_e)
         torch.cuda.synchronize()
         dl = abs(float(sloss.detach()) - float(le.detach())) / abs(float(le.detach()))
-        dp = max(float((a - b).abs().max() / (b.abs().max() + 1e-12))
-                 for a, b in zip(model.parameters(), model_e.parameters()))
+        with torch.no_grad():
+            dp = max(float((a - b).abs().max() / (b.abs().max() + 1e-12))
+                     for a, b in zip(model.parameters(), model_e.parameters()))
         _say(f"  replay {r}: loss rel {dl:.2e}, parameters max rel {dp:.2e}")
         assert dl <= 1e-6 and dp <= 1e-6
     gi = torch.cuda.CUDAGraph()
