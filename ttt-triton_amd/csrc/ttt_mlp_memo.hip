@@ -104,10 +104,13 @@ __global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams
 //                per row) and hold F/16 consecutive features each, so token
 //                rows are read and written as contiguous segments.
 // Summaries are staged per chunk of kSegChunk segments in LDS and read as
-// broadcasts (every lane of a wave at the same segment).
+// broadcasts (every lane of a wave at the same segment).  Chunks of 16 keep
+// the workgroups' LDS small enough for five per CU (the gate kernel's
+// registers are held to that occupancy too): finish 84 -> 76 us, gate
+// 52 -> 46 us at B16 H12 T2048 with 16 segments.
 constexpr int kTokBlk = 64;
 constexpr int kRowUnroll = kTokBlk / (kMemoThreads / 16);
-constexpr int kSegChunk = 64;
+constexpr int kSegChunk = 16;
 
 template <int F> using RowVec = std::conditional_t<F / 16 == 4, f4, f2>;
 
@@ -124,7 +127,7 @@ __device__ __forceinline__ void stage_summaries(float (*sm)[F], const float* __r
 // recomputes each logit (the same operations, so the same value) to write the
 // normalised gate.
 template <typename T, int F>
-__global__ __launch_bounds__(kMemoThreads) void memo_gate_kernel(MlpMemoParams p) {
+__global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParams p) {
   constexpr int K = 16;
   constexpr int FPL = F / 16;
   constexpr int NSUB = kMemoThreads / 64;
