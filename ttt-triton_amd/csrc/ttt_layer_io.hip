@@ -36,7 +36,7 @@ namespace ttt {
 
 namespace {
 
-constexpr int kRowsPerBlockBwd = 32;  // token rows per workgroup in the backwards (LN-parameter partials)
+constexpr int kRowsPerBlockBwd = 16;  // token rows per workgroup in the backwards (LN-parameter partials)
 constexpr int kMaxD = 1024;           // H * F
 
 // sum over groups of W consecutive lanes (W = 8 or 16), every lane of a group
@@ -80,6 +80,7 @@ template <int F> struct ProducerRow {
   f4 q, k, u;                      // raw projections
   f4 qn, kn, un;                   // L2-normalised
   float dq, dk, du;                // max(|x|, eps)
+  float iq, ik, iu;                // their reciprocals
   f4 qr, kr, ur;                   // rotated
   f4 c;                            // d - mean(d), d = XV - XK_rotated
   float sd;                        // unbiased std of d
@@ -92,9 +93,12 @@ template <int F> struct ProducerRow {
     dq = fmaxf(sqrtf(group_sum<W>(hsum(q * q))), l2eps);
     dk = fmaxf(sqrtf(group_sum<W>(hsum(k * k))), l2eps);
     du = fmaxf(sqrtf(group_sum<W>(hsum(u * u))), l2eps);
-    qn = q / dq;
-    kn = k / dk;
-    un = u / du;
+    iq = 1.0f / dq;
+    ik = 1.0f / dk;
+    iu = 1.0f / du;
+    qn = q * iq;
+    kn = k * ik;
+    un = u * iu;
     qr = rotate(qn, cs, false);
     kr = rotate(kn, cs, false);
     ur = rotate(un, cs, false);
@@ -102,7 +106,7 @@ template <int F> struct ProducerRow {
     const float mean = group_sum<W>(hsum(d)) / (float)F;
     c = d - splat(mean);
     sd = sqrtf(group_sum<W>(hsum(c * c)) / (float)(F - 1));
-    xv = lw * (c / (sd + eps)) + lb + kr;
+    xv = lw * (c * (1.0f / (sd + eps))) + lb + kr;
   }
 };
 
@@ -141,16 +145,16 @@ __global__ __launch_bounds__(256) void qkvu_producer_fwd_kernel(ProducerParams p
   }
 }
 
-template <typename T, int F>
+template <typename T, int F, int NCH>
 __global__ __launch_bounds__(256) void qkvu_producer_bwd_kernel(ProducerParams p) {
   constexpr int W = F / 4;
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const long long rows = (long long)p.B * p.L;
   const int D = p.H * F;
-  __shared__ float red[4][2][kMaxD];
-  f4 aw[kMaxD / 256], ab[kMaxD / 256];  // LN-parameter gradient partials per 256-feature chunk
+  __shared__ float red[4][2][256 * NCH];
+  f4 aw[NCH], ab[NCH];  // LN-parameter gradient partials per 256-feature chunk
 #pragma unroll
-  for (int i = 0; i < kMaxD / 256; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     aw[i] = splat(0.f);
     ab[i] = splat(0.f);
   }
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(256) void qkvu_producer_bwd_kernel(ProducerParams p
     const T* __restrict__ pr = static_cast<const T*>(p.proj) + row * p.ld;
     T* __restrict__ dpr = static_cast<T*>(p.dproj) + row * p.ld;
 #pragma unroll
-    for (int i = 0; i < kMaxD / 256; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = 256 * i + 4 * l;
       if (256 * i >= D) break;  // uniform
       const bool act = c < D;
@@ -177,8 +181,8 @@ __global__ __launch_bounds__(256) void qkvu_producer_bwd_kernel(ProducerParams p
       const f4 gv = ld4(static_cast<const T*>(p.dXV) + o, act);
       const f4 gu = ld4(static_cast<const T*>(p.dXU) + o, act);
       // reconstruction target: xv = lw * c / (sd + eps) + lb + kr
-      const float den = r.sd + p.eps;
-      const f4 xhat = r.c / den;
+      const float den = r.sd + p.eps, iden = 1.0f / den;
+      const f4 xhat = r.c * iden;
       aw[i] += gv * xhat;
       ab[i] += gv;
       const f4 y = gv * lw;  // gradient wrt xhat
@@ -186,21 +190,21 @@ __global__ __launch_bounds__(256) void qkvu_producer_bwd_kernel(ProducerParams p
       const float yc = group_sum<W>(hsum(y * r.c));
       // d xhat_i / d d_j = (delta_ij - 1/F) / den - c_i c_j / (den^2 sd (F - 1))
       const float k2 = r.sd > 0.f ? yc / (den * den * r.sd * (float)(F - 1)) : 0.f;
-      const f4 dd = (y - splat(ymean)) / den - r.c * k2;
+      const f4 dd = (y - splat(ymean)) * iden - r.c * k2;
       const f4 gkr = gk + gv - dd;  // XK enters the target directly and through d = XV - XK
-      // rotations back, then the L2 normalisations: d(x / n) = (g - xn (xn . g)) / n for |x| > eps
+      // rotations back, then the L2 normalisations: d(x / n) = (g - xn (xn . g)) / n where
+      // |x| > eps, g / eps elsewhere (n = max(|x|, eps) > eps exactly when |x| > eps)
       const f4 gqn = rotate(gq, cs, true), gkn = rotate(gkr, cs, true), gun = rotate(gu, cs, true);
-      auto l2back = [&](f4 xn, f4 g, float n, f4 x) {
-        const float nx = sqrtf(group_sum<W>(hsum(x * x)));
-        if (nx > p.l2eps) {
+      auto l2back = [&](f4 xn, f4 g, float n, float in) {
+        if (n > p.l2eps) {
           const float dot = group_sum<W>(hsum(xn * g));
-          return (g - xn * dot) / n;
+          return (g - xn * dot) * in;
         }
-        return g / n;
+        return g * in;
       };
-      const f4 dq = l2back(r.qn, gqn, r.dq, r.q);
-      const f4 dk = l2back(r.kn, gkn, r.dk, r.k);
-      const f4 du = l2back(r.un, gun, r.du, r.u);
+      const f4 dq = l2back(r.qn, gqn, r.dq, r.iq);
+      const f4 dk = l2back(r.kn, gkn, r.dk, r.ik);
+      const f4 du = l2back(r.un, gun, r.du, r.iu);
       if (act) {
         store4(dpr + c, dq);
         store4(dpr + D + c, dk);
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(256) void qkvu_producer_bwd_kernel(ProducerParams p
   }
   // per-block LN-parameter partials: waves in fixed order (deterministic)
 #pragma unroll
-  for (int i = 0; i < kMaxD / 256; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = 256 * i + 4 * l;
     if (c < D) {
       *reinterpret_cast<f4*>(&red[wave][0][c]) = aw[i];
@@ -276,15 +280,15 @@ __global__ __launch_bounds__(256) void post_norm_fwd_kernel(PostNormParams p) {
   }
 }
 
-template <typename T, int F>
+template <typename T, int F, int NCH>
 __global__ __launch_bounds__(256) void post_norm_bwd_kernel(PostNormParams p) {
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const long long rows = (long long)p.B * p.L;
   const int D = p.H * F;
-  __shared__ float red[4][2][kMaxD];
-  f4 aw[kMaxD / 256], ab[kMaxD / 256];
+  __shared__ float red[4][2][256 * NCH];
+  f4 aw[NCH], ab[NCH];
 #pragma unroll
-  for (int i = 0; i < kMaxD / 256; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     aw[i] = splat(0.f);
     ab[i] = splat(0.f);
   }
@@ -292,10 +296,10 @@ __global__ __launch_bounds__(256) void post_norm_bwd_kernel(PostNormParams p) {
   for (long long row = r0 + wave; row < r0 + kRowsPerBlockBwd && row < rows; row += 4) {
     const int b = (int)(row / p.L), t = (int)(row - (long long)b * p.L);
     const float mean = p.stats[2 * row], rstd = p.stats[2 * row + 1];
-    f4 xh[kMaxD / 256], g[kMaxD / 256];
+    f4 xh[NCH], g[NCH];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMaxD / 256; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = 256 * i + 4 * l;
       const bool act = c < D;
       const int h = c / F, f = c - h * F;
@@ -311,7 +315,7 @@ __global__ __launch_bounds__(256) void post_norm_bwd_kernel(PostNormParams p) {
     }
     const float m1 = sum_wave(s1) / (float)D, m2 = sum_wave(s2) / (float)D;
 #pragma unroll
-    for (int i = 0; i < kMaxD / 256; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = 256 * i + 4 * l;
       if (c < D) {
         const int h = c / F, f = c - h * F;
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(256) void post_norm_bwd_kernel(PostNormParams p) {
     }
   }
 #pragma unroll
-  for (int i = 0; i < kMaxD / 256; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = 256 * i + 4 * l;
     if (c < D) {
       *reinterpret_cast<f4*>(&red[wave][0][c]) = aw[i];
@@ -344,9 +348,14 @@ int layer_io_max_width() { return kMaxD; }
 template <typename T, int F>
 static hipError_t launch_producer_t(const ProducerParams& p, bool bwd, hipStream_t stream) {
   const long long rows = (long long)p.B * p.L;
-  if (bwd)
-    hipLaunchKernelGGL((qkvu_producer_bwd_kernel<T, F>), dim3(layer_io_bwd_blocks(p.B, p.L)), dim3(256), 0, stream,
-                       p);
+  const dim3 grid(layer_io_bwd_blocks(p.B, p.L)), block(256);
+  const int D = p.H * F;  // the backwards' per-lane arrays cover D in 256-feature chunks
+  if (bwd && D <= 256)
+    hipLaunchKernelGGL((qkvu_producer_bwd_kernel<T, F, 1>), grid, block, 0, stream, p);
+  else if (bwd && D <= 512)
+    hipLaunchKernelGGL((qkvu_producer_bwd_kernel<T, F, 2>), grid, block, 0, stream, p);
+  else if (bwd)
+    hipLaunchKernelGGL((qkvu_producer_bwd_kernel<T, F, kMaxD / 256>), grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL((qkvu_producer_fwd_kernel<T, F>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, p);
   return hipGetLastError();
@@ -366,8 +375,14 @@ hipError_t launch_producer(const ProducerParams& p, int dtype, bool bwd, hipStre
 template <typename T, int F>
 static hipError_t launch_post_norm_t(const PostNormParams& p, bool bwd, hipStream_t stream) {
   const long long rows = (long long)p.B * p.L;
-  if (bwd)
-    hipLaunchKernelGGL((post_norm_bwd_kernel<T, F>), dim3(layer_io_bwd_blocks(p.B, p.L)), dim3(256), 0, stream, p);
+  const dim3 grid(layer_io_bwd_blocks(p.B, p.L)), block(256);
+  const int D = p.H * F;
+  if (bwd && D <= 256)
+    hipLaunchKernelGGL((post_norm_bwd_kernel<T, F, 1>), grid, block, 0, stream, p);
+  else if (bwd && D <= 512)
+    hipLaunchKernelGGL((post_norm_bwd_kernel<T, F, 2>), grid, block, 0, stream, p);
+  else if (bwd)
+    hipLaunchKernelGGL((post_norm_bwd_kernel<T, F, kMaxD / 256>), grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL((post_norm_fwd_kernel<T, F>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, p);
   return hipGetLastError();
