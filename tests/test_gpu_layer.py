@@ -264,3 +264,40 @@ def test_forecaster_step_in_a_graph_matches_eager():
             d = float((sout.float() - eo.float()).abs().max() / (eo.float().abs().max() + 1e-12))
             _say(f"  inference replay {r}: max rel {d:.2e}")
             assert d <= 1e-6
+
+
+@pytest.mark.parametrize("kind", ["ttt_mlp", "ttt_linear"])
+def test_last_token_path_matches_full_output(kind):
+    """TTTWrapper(last_only=True), the path the forecaster takes for its
+    head, against the full [B, L, D] output's last row in fp32: the output and
+    the gradient of every parameter under a loss on that row agree to fp32
+    GEMM rounding (post-norm and `wo` run on the last mini-batch only; the
+    other rows' outputs are never read, so their gradients are exact zeros)."""
+    from ttt_amd.model import ModelConfig, TTTWrapper
+    B, L, H, F_ = 2, 256, 4, 64
+    _say(f"last-token path {kind} B{B} L{L} H{H} F{F_}")
+    cfg = ModelConfig(seq_len=L, model_dim=H * F_, num_heads=H, ssm_layer=kind, mini_batch_size=16,
+                      ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=2 if kind == "ttt_mlp" else 0,
+                      scan_checkpoint_group_size=16)
+    torch.manual_seed(5)
+    dev = torch.device("cuda")
+    layer = TTTWrapper(cfg).to(dev)
+    x = torch.randn(B, L, H * F_, device=dev)
+    w = torch.randn(B, H * F_, device=dev)
+    grads = []
+    outs = []
+    for last in (False, True):
+        layer.zero_grad(set_to_none=True)
+        h = layer(x, last_only=True) if last else layer(x)[:, -1]
+        (h * w).sum().backward()
+        outs.append(h.detach())
+        grads.append({n: p.grad.detach().clone() for n, p in layer.named_parameters() if p.grad is not None})
+    torch.cuda.synchronize()
+    e = rel_l2(outs[1], outs[0])
+    _say(f"  output rel-L2 {e:.2e}")
+    assert e <= 1e-5
+    assert grads[0].keys() == grads[1].keys()
+    for n in grads[0]:
+        e = rel_l2(grads[1][n], grads[0][n])
+        _say(f"  d{n}: rel-L2 {e:.2e}")
+        assert e <= 1e-5, n

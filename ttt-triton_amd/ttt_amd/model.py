@@ -5,14 +5,19 @@ inner loop, as TTTForecaster / TTTWrapper / TTTMLP / TTTLinear use it
 Per layer call, for hidden states x [B, L, D] (D = H*F):
   1. one projection GEMM x @ [Wq; Wk; Wv; Wu; w_lr]^T + [bq; bk; bv; bu; b_lr]
      (hipBLASLt through torch), the H lr-gate logits padded to an aligned row
-     width (ttt_layer.py:141-148, 151-163);
+     width (ttt_layer.py:141-148, 151-163); its weight gradient is split over
+     row blocks (_ProjectionFunction);
   2. ProducerFunction: L2 norm, RoPE, reconstruction target and lr, written
      in the inner loop's [B,H,NC,K,F] / [B,H,NC,K] layouts (ttt_layer.py:261-309);
   3. the inner loop with eta expanded on chip from lr by the layer's rule
      eta[i][j] = lr[j]/K (ttt_layer.py:309): TTTMLPFunction (+ the memory-cache
      combiner, ttt_layer.py:453-565) or TTTLinearFunction (:383-421);
   4. PostNormFunction (permute + reshape + post_norm, ttt_layer.py:349,
-     563-564) and the `wo` GEMM (:350).
+     563-564) and the `wo` GEMM (:350).  A caller that reads only the last
+     token (the forecaster's head, forecast.py:97-98) asks for it alone:
+     step 4 then runs on the last mini-batch and `wo` on its last row, which
+     gives that token's output and every gradient unchanged (the other rows'
+     outputs are never read, so their gradients are exact zeros).
 
 Parameter names and shapes are the reference's (wq ... wu, wo,
 learnable_ttt_lr_weight [H,1,D], learnable_ttt_lr_bias [H,1],
@@ -37,6 +42,41 @@ from .layer_io import POST_NORM_EPS, RECON_EPS, PostNormFunction, ProducerFuncti
 from .linear import TTTLinearFunction
 from .memo import mlp_memo_combine
 from .mlp import LN_EPS, TTTMLPFunction
+
+
+def _row_blocks(rows: int, target: int) -> int:
+    """The largest power of two S <= 16 dividing `rows` with rows / S >= target."""
+    s = 1
+    while s < 16 and rows % (2 * s) == 0 and rows // (2 * s) >= target:
+        s *= 2
+    return s
+
+
+class _ProjectionFunction(torch.autograd.Function):
+    """apply(x [R, Din], w [N, Din], b [N]) -> x w^T + b, all in one dtype.
+
+    The backward's weight gradient dy^T x contracts over all R = B*L rows into
+    an N x Din output of a few hundred 64x64 tiles, too few to fill the GPU
+    with one long contraction each; it is formed instead as S row-block
+    products (one batched GEMM) summed in fp32.  The bias gradient is the
+    column sum of dy, taken over row blocks the same way."""
+
+    @staticmethod
+    def forward(ctx, x, w, b):
+        ctx.save_for_backward(x, w)
+        return torch.addmm(b, x, w.t())
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        R, N = dy.shape
+        dy = dy.contiguous()
+        dx = dy @ w if ctx.needs_input_grad[0] else None
+        s = _row_blocks(R, 1024)
+        dw = torch.bmm(dy.view(s, R // s, N).transpose(1, 2), x.view(s, R // s, -1)).sum(0, dtype=torch.float32)
+        s = 64 if R % 64 == 0 else 1
+        db = dy.view(s, R // s, N).sum(1, dtype=torch.float32).sum(0)
+        return dx, dw.to(w.dtype), db.to(w.dtype)
 
 
 @dataclass
@@ -115,7 +155,10 @@ class TTTLayerBase(nn.Module):
         if pad:
             w.append(self.wq.weight.new_zeros(pad, D))
             b.append(self.wq.bias.new_zeros(pad))
-        return Fn.linear(x, torch.cat(w, 0), torch.cat(b, 0))
+        dt = torch.get_autocast_dtype(x.device.type) if torch.is_autocast_enabled(x.device.type) else x.dtype
+        B, L, _ = x.shape
+        y = _ProjectionFunction.apply(x.reshape(B * L, D).to(dt), torch.cat(w, 0).to(dt), torch.cat(b, 0).to(dt))
+        return y.view(B, L, -1)
 
     def process_input(self, x: torch.Tensor, rope: torch.Tensor):
         """(XQ, XK, XV, XU, lr) in the inner loop's layouts (ttt_layer.py:261-329)."""
@@ -127,11 +170,16 @@ class TTTLayerBase(nn.Module):
     def ttt(self, XQ, XK, XV, XU, lr):
         raise NotImplementedError
 
-    def forward(self, x: torch.Tensor, rope: torch.Tensor):
+    def forward(self, x: torch.Tensor, rope: torch.Tensor, last_only: bool = False):
+        """[B, L, D], or with last_only the last token's output [B, D]."""
         if x.size(1) % self.mini_batch_size:
             raise ValueError("sequence length must be a multiple of the mini-batch size")
         XQ, XK, XV, XU, lr = self.process_input(x, rope)
         out = self.ttt(XQ, XK, XV, XU, lr)                               # [B,H,NC,K,F]
+        if last_only:
+            h = PostNormFunction.apply(out[:, :, -1:].contiguous(), self.post_norm.weight, self.post_norm.bias,
+                                       POST_NORM_EPS)                    # [B, K, D]
+            return self.wo(h[:, -1])
         h = PostNormFunction.apply(out, self.post_norm.weight, self.post_norm.bias, POST_NORM_EPS)
         return self.wo(h)
 
@@ -212,8 +260,8 @@ class TTTWrapper(nn.Module):
     def init_freqs(self):
         self.rope.copy_(self._rope())
 
-    def forward(self, x: torch.Tensor, seq_metadata=None):
-        return self.ttt(x, self.rope)
+    def forward(self, x: torch.Tensor, seq_metadata=None, last_only: bool = False):
+        return self.ttt(x, self.rope, last_only)
 
 
 class TTTForecaster(nn.Module):
@@ -229,8 +277,8 @@ class TTTForecaster(nn.Module):
 
     def forward(self, seq_x: torch.Tensor) -> torch.Tensor:
         h = self.in_proj(seq_x)
-        h = self.ttt(h)
-        out = self.head(h[:, -1])
+        h = self.ttt(h, last_only=True)  # the head reads h[:, -1] only
+        out = self.head(h)
         return out.view(seq_x.size(0), self.pred_len, self.d_out)
 
 
