@@ -79,6 +79,21 @@ class _ProjectionFunction(torch.autograd.Function):
         return dx, dw.to(w.dtype), db.to(w.dtype)
 
 
+def projection(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """Fn.linear(x, weight, bias) over the last dim of x through
+    _ProjectionFunction, in the autocast dtype when autocast is on."""
+    dt = torch.get_autocast_dtype(x.device.type) if torch.is_autocast_enabled(x.device.type) else x.dtype
+    y = _ProjectionFunction.apply(x.reshape(-1, x.shape[-1]).to(dt), weight.to(dt), bias.to(dt))
+    return y.view(*x.shape[:-1], weight.shape[0])
+
+
+def _padded_width(n: int) -> int:
+    """Row width of the fused projection: a multiple of 128 where that adds
+    at most an eighth (the GEMM then tiles without a ragged edge), else of 8."""
+    n128 = -(-n // 128) * 128
+    return n128 if 8 * (n128 - n) <= n else -(-n // 8) * 8
+
+
 @dataclass
 class ModelConfig:
     """forecast.py:31-64 (the fields the layer and forecaster read)."""
@@ -147,18 +162,16 @@ class TTTLayerBase(nn.Module):
 
     def _fused_projection(self, x: torch.Tensor) -> torch.Tensor:
         """[B, L, ld]: XQ | XK | XV | XU | lr logits | zero padding (ld a
-        multiple of 8), one GEMM instead of five (ttt_layer.py:141-163)."""
+        multiple of 8, of 128 where that costs little), one GEMM instead of
+        five (ttt_layer.py:141-163)."""
         H, D = self.num_heads, self.width
-        pad = (-(4 * D + H)) % 8
+        pad = _padded_width(4 * D + H) - (4 * D + H)
         w = [self.wq.weight, self.wk.weight, self.wv.weight, self.wu.weight, self.learnable_ttt_lr_weight.view(H, D)]
         b = [self.wq.bias, self.wk.bias, self.wv.bias, self.wu.bias, self.learnable_ttt_lr_bias.view(H)]
         if pad:
             w.append(self.wq.weight.new_zeros(pad, D))
             b.append(self.wq.bias.new_zeros(pad))
-        dt = torch.get_autocast_dtype(x.device.type) if torch.is_autocast_enabled(x.device.type) else x.dtype
-        B, L, _ = x.shape
-        y = _ProjectionFunction.apply(x.reshape(B * L, D).to(dt), torch.cat(w, 0).to(dt), torch.cat(b, 0).to(dt))
-        return y.view(B, L, -1)
+        return projection(x, torch.cat(w, 0), torch.cat(b, 0))
 
     def process_input(self, x: torch.Tensor, rope: torch.Tensor):
         """(XQ, XK, XV, XU, lr) in the inner loop's layouts (ttt_layer.py:261-329)."""
@@ -276,7 +289,7 @@ class TTTForecaster(nn.Module):
         self.head = nn.Linear(config.model_dim, pred_len * d_out)
 
     def forward(self, seq_x: torch.Tensor) -> torch.Tensor:
-        h = self.in_proj(seq_x)
+        h = projection(seq_x, self.in_proj.weight, self.in_proj.bias)  # self.in_proj(seq_x)
         h = self.ttt(h, last_only=True)  # the head reads h[:, -1] only
         out = self.head(h)
         return out.view(seq_x.size(0), self.pred_len, self.d_out)
