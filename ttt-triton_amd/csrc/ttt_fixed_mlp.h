@@ -9,9 +9,14 @@
 // consecutive registers.  The hidden dimension is walked two 16-unit tiles at
 // a time:
 //
-//   Z1^T(pair) = W1^T X^T + b1      hidden x token (C layout = the A operand of
+//   Z1^T(pair) = W1^T X^T + b1      hidden x token (C layout = the B operand of
 //   X2^T       = gelu(Z1^T)          the next product, no transpose)
-//   Z2        += X2 W2(pair)
+//   Z2^T      += W2(pair)^T X2^T     feature x token
+//
+// Z2 comes out transposed, token-major: the C layout of Z2^T puts one token on
+// each lane's free index and four consecutive features in its registers, the
+// layout of X's own operand frags and of a 16-byte row store, so the callers'
+// per-token LayerNorm needs no transpose and reduces over four lanes only.
 //
 // (Issuing the next pair's Z1 products ahead of the current GELU was measured
 // no faster at B16 H12 T2048 F64 FF256 and costs 16 registers.)
@@ -25,8 +30,8 @@ template <typename T, int FT, int HTT> struct FixedMlpLds {
   using V = typename FragT<T>::type;
   V w1[HTT][FT / 2][2][64];  // [ht][kp][h]: W1 block (2kp + h, ht) = W1[16kb + 4g + j][16ht + n]
   V w2[HTT / 2][FT][2][64];  // [hp][ct][h]: W2 block (2hp + h, ct) = W2[16ht + 4g + j][16ct + n]
-  float b1[16 * HTT];
-  float b2[16 * FT];
+  alignas(16) float b1[16 * HTT];
+  alignas(16) float b2[16 * FT];
 };
 
 // Stage one (W1, b1, W2, b2) into LDS with NWAVES waves: each wave takes
@@ -91,19 +96,20 @@ __device__ __forceinline__ void stage_fixed_mlp(FixedMlpLds<T, FT, HTT>& sh, con
   if (threadIdx.x < F) sh.b2[threadIdx.x] = bias2;
 }
 
-// acc[t][c] = Z2 of token tile t, feature tile c (C layout: lane (g, n) holds
-// Z2[4g + j][16c + n]), from the operand frags xq[t][kb] of X^T (free = token,
-// contraction = feature).  b2 is added.
+// acc[t][c] = Z2 of token tile t, feature tile c, token-major (lane (g, n)
+// holds Z2[n][16c + 4g + j], the C layout of Z2^T), from the operand frags
+// xq[t][kb] of X^T (free = token, contraction = feature; lane (g, n) holds
+// X[n][16kb + 4g + j]).  b2 is added.
 template <typename T, int FT, int HTT, int NT>
 __device__ __forceinline__ void fixed_mlp_tiles(const FixedMlpLds<T, FT, HTT>& sh, const Frag<T> (&xq)[NT][FT],
                                                 Tile (&acc)[NT][FT]) {
   static_assert(FT % 2 == 0 && HTT % 2 == 0, "pairs of 16-wide tiles");
-  const int l = lane_id(), g = l >> 4, n = l & 15;
+  const int l = lane_id(), g = l >> 4;
 #pragma unroll
   for (int c = 0; c < FT; ++c) {
-    const float b2 = sh.b2[16 * c + n];
+    const f4 b2 = *reinterpret_cast<const f4*>(&sh.b2[16 * c + 4 * g]);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t][c].v = f4{b2, b2, b2, b2};
+    for (int t = 0; t < NT; ++t) acc[t][c].v = b2;
   }
   // Z1^T of hidden tiles (ht, ht + 1) for every token tile, b1 in the accumulator
   auto z1 = [&](int ht, Tile (&z)[2][NT]) {
@@ -144,7 +150,7 @@ __device__ __forceinline__ void fixed_mlp_tiles(const FixedMlpLds<T, FT, HTT>& s
       q0.v = sh.w2[ht >> 1][c][0][l];
       q1.v = sh.w2[ht >> 1][c][1][l];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) mma32(acc[t][c].v, x2[0][t], x2[1][t], q0, q1);
+      for (int t = 0; t < NT; ++t) mma32(acc[t][c].v, q0, q1, x2[0][t], x2[1][t]);
     }
   }
 }

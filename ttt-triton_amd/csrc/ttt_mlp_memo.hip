@@ -297,31 +297,34 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(XQ + (size_t)tt * K * F, F, 16 * kb);
     }
 
-    f4 oacc[NTW][FT];  // forward: acc_N; backward: dOut * ln_w (C layout, token rows)
-    f4 base[NTW];      // backward: dOut . (XQ + ln_b) of token rows 4g + j
+    // Token-major throughout (the layout of the xq frags and of the fixed MLP's
+    // Z2): lane (g, n) holds features 16c + 4g + j of token n of each tile.
+    f4 lw[FT], lb[FT];  // ln_w, ln_b of those features
+#pragma unroll
+    for (int c = 0; c < FT; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lw[c][j] = p.ln_w[h * F + 16 * c + 4 * g + j];
+        lb[c][j] = p.ln_b[h * F + 16 * c + 4 * g + j];
+      }
+    f4 oacc[NTW][FT];  // forward: acc_N; backward: dOut * ln_w
+    float base[NTW];   // backward: dOut . (XQ + ln_b) of token n
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {
-      base[t] = f4{0.f, 0.f, 0.f, 0.f};
+      base[t] = 0.f;
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         if constexpr (BWD) {
-          const size_t r0 = (size_t)(t < nv ? t0 + t : tl) * K * F + 16 * c + n;
-          const T* d = static_cast<const T*>(p.dout) + xoff + r0;
-          const float w = p.ln_w[h * F + 16 * c + n], b = p.ln_b[h * F + 16 * c + n];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float dv = (float)d[(4 * g + j) * F];
-            oacc[t][c][j] = dv * w;
-            base[t][j] += dv * ((float)XQ[r0 + (4 * g + j) * F] + b);
-          }
+          const size_t e = ((size_t)(t < nv ? t0 + t : tl) * K + n) * F + 16 * c + 4 * g;
+          const f4 dv = load4(static_cast<const T*>(p.dout) + xoff + e);
+          const f4 xb = frag_to_f4(xq[t][c]) + lb[c];
+          oacc[t][c] = dv * lw[c];
+          base[t] += (dv[0] * xb[0] + dv[1] * xb[1]) + (dv[2] * xb[2] + dv[3] * xb[3]);
         } else {
           oacc[t][c] = f4{0.f, 0.f, 0.f, 0.f};
         }
       }
-      if constexpr (BWD) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) base[t][j] = sum_row16(base[t][j]);
-      }
+      if constexpr (BWD) base[t] = sum_col4(base[t]);
     }
 
     const float invF = 1.0f / (float)F;
@@ -348,11 +351,10 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       //      the previous state; state jm + 1's copy is requested now, into the
       //      buffer the previous state used.
       if constexpr (!PK) __syncthreads();
-      f4 gjv[NTW];
+      float gjv[NTW];  // gamma_jm of token n
       if constexpr (!BWD) {
 #pragma unroll
-        for (int t = 0; t < NTW; ++t)
-          gjv[t] = *reinterpret_cast<const f4*>(gb + L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + 4 * g);
+        for (int t = 0; t < NTW; ++t) gjv[t] = gb[L.gam + (size_t)jm * NT + (t < nv ? t0 + t : tl) * K + n];
       }
       if constexpr (PK) {
         if (jm + 1 < jmax) dma_state(jm + 1, (jm + 1) & 1);
@@ -378,41 +380,36 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       Tile acc[NTW][FT];  // Z2 + b2
       fixed_mlp_tiles<T, FT, HTT, NTW>(sh, xq, acc);
 
-      // ---- N_jm = LN-normalised (Z2 + b2) per token row; fold it in
+      // ---- N_jm = LN-normalised (Z2 + b2) per token row (its features in
+      //      lanes n, n + 16, n + 32, n + 48: sum_col4); fold it in
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {
         if (seg[t] <= jm) continue;
-        f4 dg;
+        float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v[FT], s = 0.f;
+        for (int c = 0; c < FT; ++c) s += (acc[t][c].v[0] + acc[t][c].v[1]) + (acc[t][c].v[2] + acc[t][c].v[3]);
+        const float mean = sum_col4(s) * invF;
+        float q = 0.f;
 #pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            v[c] = acc[t][c].v[j];
-            s += v[c];
-          }
-          const float mean = sum_row16(s) * invF;
-          float q = 0.f;
-#pragma unroll
-          for (int c = 0; c < FT; ++c) {
-            v[c] -= mean;
-            q += v[c] * v[c];
-          }
-          const float rstd = rsqrt_f(sum_row16(q) * invF + p.eps);
-          if constexpr (BWD) {
-            float d = 0.f;
-#pragma unroll
-            for (int c = 0; c < FT; ++c) d += oacc[t][c][j] * v[c];
-            dg[j] = base[t][j] + rstd * sum_row16(d);
-          } else {
-            const float gr = gjv[t][j] * rstd;
-#pragma unroll
-            for (int c = 0; c < FT; ++c) oacc[t][c][j] += gr * v[c];
-          }
+        for (int c = 0; c < FT; ++c) {
+          acc[t][c].v -= mean;
+          const f4 v = acc[t][c].v;
+          q += (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
         }
+        const float rstd = rsqrt_f(sum_col4(q) * invF + p.eps);
         if constexpr (BWD) {
-          const int tok0 = (t0 + t) * K + 4 * g;  // token of register j: tok0 + j
-          if (n == 0) *reinterpret_cast<f4*>(gb + L.dgam + (size_t)jm * NT + tok0) = dg;
+          float d = 0.f;
+#pragma unroll
+          for (int c = 0; c < FT; ++c) {
+            const f4 v = acc[t][c].v, o = oacc[t][c];
+            d += (o[0] * v[0] + o[1] * v[1]) + (o[2] * v[2] + o[3] * v[3]);
+          }
+          const float dg = base[t] + rstd * sum_col4(d);
+          if (g == 0) gb[L.dgam + (size_t)jm * NT + (t0 + t) * K + n] = dg;
+        } else {
+          const float gr = gjv[t] * rstd;
+#pragma unroll
+          for (int c = 0; c < FT; ++c) oacc[t][c] += gr * acc[t][c].v;
         }
       }
       if constexpr (PK) {
@@ -427,25 +424,18 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
       // gamma_i = 1 and acc_N = 0, so out = XQW)
       const T* __restrict__ XQW = static_cast<const T*>(p.XQW) + xoff;
       T* __restrict__ OUT = static_cast<T*>(p.out) + xoff;
-      float lw[FT], lb[FT];
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        lw[c] = p.ln_w[h * F + 16 * c + n];
-        lb[c] = p.ln_b[h * F + 16 * c + n];
-      }
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {
         if (t >= nv) continue;
-        const int tok0 = (t0 + t) * K + 4 * g;
-        const f4 gc = *reinterpret_cast<const f4*>(gb + L.gcur + tok0);
+        const int tok = (t0 + t) * K + n;
+        const float gc = gb[L.gcur + tok];
 #pragma unroll
-        for (int c = 0; c < FT; ++c)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const size_t e = (size_t)(tok0 + j) * F + 16 * c + n;
-            const float rest = seg[t] > 0 ? (1.0f - gc[j]) * ((float)XQ[e] + lb[c]) + lw[c] * oacc[t][c][j] : 0.0f;
-            OUT[e] = (T)(gc[j] * (float)XQW[e] + rest);
-          }
+        for (int c = 0; c < FT; ++c) {
+          const size_t e = (size_t)tok * F + 16 * c + 4 * g;
+          const f4 rest = seg[t] > 0 ? (1.0f - gc) * (frag_to_f4(xq[t][c]) + lb[c]) + lw[c] * oacc[t][c]
+                                     : f4{0.f, 0.f, 0.f, 0.f};
+          store4(OUT + e, gc * load4(XQW + e) + rest);
+        }
       }
     }
   }  // half

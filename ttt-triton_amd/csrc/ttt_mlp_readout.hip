@@ -9,10 +9,15 @@
 // per lane per 16x16 block, so every operand read is one conflict-free
 // ds_read), then each wave runs up to two 16-token tiles through
 //
-//   Z1^T = W1^T XQ^T           (hidden x token: its C layout is the A operand
+//   Z1^T = W1^T XQ^T           (hidden x token: its C layout is the B operand
 //   X2^T = gelu(Z1^T + b1)      of the next product with no transpose)
-//   Z2   = X2 W2 + b2           accumulated over hidden tiles two at a time
+//   Z2^T = W2^T X2^T + b2       accumulated over hidden tiles two at a time
 //   out  = XQ + ln_w * (Z2 - mean) / sqrt(var + eps) + ln_b
+//
+// Z2 arrives token-major (lane (g, n): token n, features 16c + 4g + j), the
+// layout of the XQ operand frags and of a 16-byte row store: the LayerNorm
+// takes its row sums over four lanes (two lane swaps) and the residual and
+// the store need no transpose.
 //
 // W is read from HBM once per workgroup; blocks are mapped so that the chunks
 // of one chain run on one XCD and share its L2.  Two workgroups fit a CU's LDS
@@ -25,8 +30,8 @@ namespace ttt {
 
 template <typename T, int FT, int HTT> struct ReadoutShared {
   FixedMlpLds<T, FT, HTT> w;
-  float lnw[16 * FT];
-  float lnb[16 * FT];
+  alignas(16) float lnw[16 * FT];
+  alignas(16) float lnb[16 * FT];
 };
 
 constexpr int kReadoutWaves = 8;
@@ -50,7 +55,7 @@ __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void ml
   const int h = chain % p.H;
 
   const int wave = threadIdx.x >> 6;
-  const int l = lane_id(), g = l >> 4, n = l & 15;
+  const int g = lane_id() >> 4;
 
   const int ntiles = p.ntok >> 4;
   const int t0 = chunk * (kReadoutChunk / 16) + wave * NT;  // first token tile of this wave
@@ -89,47 +94,31 @@ __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void ml
   fixed_mlp_tiles<T, FT, HTT, NT>(sh.w, xq, acc);
 
   // ---- LayerNorm over the F features of each token row, residual, store.
-  // The residual XQ comes from the operand frags by an exact transpose (an
-  // MFMA against the identity gives XQ's C-layout tile, the layout of acc);
-  // each output tile is transposed the same way in fp32 so that a lane holds
-  // 4 consecutive features of one token and stores them with one 16-byte
-  // store.
-  float lwv[FT], lbv[FT];
-#pragma unroll
-  for (int c = 0; c < FT; ++c) {
-    lwv[c] = sh.lnw[16 * c + n];
-    lbv[c] = sh.lnb[16 * c + n];
-  }
-  const Frag<T> I = identity_frag<T>();
-  const Frag<float> I32 = identity_frag<float>();
+  // Lane (g, n) holds 4 features of token n in each feature tile; the row's
+  // other 3F/4 features are in lanes n + 16, n + 32, n + 48 (sum_col4).
   const float invF = 1.0f / (float)F;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t >= nv) break;
-    f4 mean, rstd;
+    float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float s = 0.f;
+    for (int c = 0; c < FT; ++c) s += (acc[t][c].v[0] + acc[t][c].v[1]) + (acc[t][c].v[2] + acc[t][c].v[3]);
+    const float mean = sum_col4(s) * invF;
+    float q = 0.f;
 #pragma unroll
-      for (int c = 0; c < FT; ++c) s += acc[t][c].v[j];
-      mean[j] = sum_row16(s) * invF;
-      float q = 0.f;
-#pragma unroll
-      for (int c = 0; c < FT; ++c) {
-        const float d = acc[t][c].v[j] - mean[j];
-        q += d * d;
-      }
-      rstd[j] = rsqrt_f(sum_row16(q) * invF + p.eps);
+    for (int c = 0; c < FT; ++c) {
+      acc[t][c].v -= mean;
+      const f4 d = acc[t][c].v;
+      q += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
     }
+    const float rstd = rsqrt_f(sum_col4(q) * invF + p.eps);
     float* o = OUT + (size_t)(t0 + t) * 16 * F;
 #pragma unroll
     for (int c = 0; c < FT; ++c) {
-      const f4 x = transpose16(xq[t][c], I).v;  // lane (g, n): XQ[4g + j][16c + n]
-      f4 y;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) y[j] = x[j] + lwv[c] * ((acc[t][c].v[j] - mean[j]) * rstd[j]) + lbv[c];
-      // lane (g, n): out[n][16c + 4g + j]
-      store_f4(o, F, 16 * c, transpose16(Frag<float>{y}, I32).v);
+      const f4 lw = *reinterpret_cast<const f4*>(&sh.lnw[16 * c + 4 * g]);
+      const f4 lb = *reinterpret_cast<const f4*>(&sh.lnb[16 * c + 4 * g]);
+      const f4 x = frag_to_f4(xq[t][c]);  // XQ[n][16c + 4g + j]
+      store_f4(o, F, 16 * c, x + lw * (acc[t][c].v * rstd) + lb);
     }
   }
 }
