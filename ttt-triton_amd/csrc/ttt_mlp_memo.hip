@@ -107,7 +107,9 @@ __global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams
 // broadcasts (every lane of a wave at the same segment).  Chunks of 16 keep
 // the workgroups' LDS small enough for five per CU (the gate kernel's
 // registers are held to that occupancy too): finish 84 -> 76 us, gate
-// 52 -> 46 us at B16 H12 T2048 with 16 segments.
+// 52 -> 46 us at B16 H12 T2048 with 16 segments.  The finish kernel requests
+// every load of the first chunk up front (76 -> 67 us; it then holds 116
+// registers, four workgroups per CU: capped at five it spills and is slower).
 constexpr int kTokBlk = 64;
 constexpr int kRowUnroll = kTokBlk / (kMemoThreads / 16);
 constexpr int kSegChunk = 16;
@@ -471,39 +473,57 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
   const int ilast = ((min(tb + kTokBlk, NT) - 1) / K) / M;
   const int nch = (ilast + kSegChunk - 1) / kSegChunk;  // chunks of segments below the block's last one
 
+  // Every load the first chunk of segments needs is requested before the
+  // first use of any (one memory latency for the common case NS <= 16): the
+  // token-major gates of chunk 0 kept in registers, chunk 0's summaries into
+  // LDS, the row layout's dOut, XQW, current gate and current summary.
+  constexpr int KC = kSegChunk / NSUB;  // chunk-0 segments per token-major thread
+  const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
+  const int tc = min(tb + tk, NT - 1);
+  const int i = (tc / K) / M;
+  const float gc = gb[L.gcur + tc];
+  float ga[KC], dga[KC];  // gamma_j, dgamma_j of segments j = sub + NSUB k of chunk 0 (0 past i)
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int j = sub + NSUB * k;
+    ga[k] = j < i ? gam[(size_t)j * NT + tc] : 0.f;
+    dga[k] = j < i ? dgam[(size_t)j * NT + tc] : 0.f;
+  }
+  if (nch > 0) stage_summaries<F>(sm, summ, 0, NS);
+
   // ---- row layout: dOut, the current gate, dgamma_current = dOut . XQW
   const int q = threadIdx.x & 15, row = threadIdx.x >> 4;
   const int f0 = FPL * q;
   float dout[U][FPL], gcr[U];
+  VT svc[U];  // the current summary (segment iu) of each row's token
   int iu[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int tk = u * (kMemoThreads / 16) + row;
-    const int tc = min(tb + tk, NT - 1);  // tokens past the end compute on the last one and store nothing
-    iu[u] = (tc / K) / M;
+    const int tkr = u * (kMemoThreads / 16) + row;
+    const int tcr = min(tb + tkr, NT - 1);  // tokens past the end compute on the last one and store nothing
+    iu[u] = (tcr / K) / M;
     float xqw[FPL];
-    const size_t e = ((size_t)chain * NT + tc) * F + f0;
+    const size_t e = ((size_t)chain * NT + tcr) * F + f0;
     load_n<FPL>(static_cast<const T*>(p.dout) + e, dout[u]);
     load_n<FPL>(static_cast<const T*>(p.XQW) + e, xqw);
-    gcr[u] = gb[L.gcur + tc];
+    gcr[u] = gb[L.gcur + tcr];
+    svc[u] = *reinterpret_cast<const VT*>(summ + (size_t)iu[u] * F + f0);
     float dg = 0.f;
 #pragma unroll
     for (int k = 0; k < FPL; ++k) dg += dout[u][k] * xqw[k];
     dg = sum_row16(dg);
-    if (q == 0) dgl[tk] = dg;
+    if (q == 0) dgl[tkr] = dg;
   }
 
   // ---- token-major: S
-  const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
-  const int tc = min(tb + tk, NT - 1);
-  const int i = (tc / K) / M;
   {
     float s = 0.f;
-    for (int j = sub; j < i; j += NSUB) s += gam[(size_t)j * NT + tc] * dgam[(size_t)j * NT + tc];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) s += ga[k] * dga[k];
+    for (int j = kSegChunk + sub; j < i; j += NSUB) s += gam[(size_t)j * NT + tc] * dgam[(size_t)j * NT + tc];
     sp[sub][tk] = s;
   }
   __syncthreads();
-  const float gc = gb[L.gcur + tc];
   const float dgc = dgl[tk];
   float S = gc * dgc;
 #pragma unroll
@@ -517,11 +537,17 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
 #pragma unroll
     for (int k = 0; k < FPL; ++k) dxu[u][k] = 0.f;
   for (int c = 0; c < nch; ++c) {
-    if (c > 0) __syncthreads();  // the previous chunk's LDS reads are done
-    stage_summaries<F>(sm, summ, c, NS);
-    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj < i; jj += NSUB) {
-      const int j = c * kSegChunk + jj;
-      dsl[tk][jj] = gam[(size_t)j * NT + tc] * (dgam[(size_t)j * NT + tc] - S);
+    if (c > 0) {
+      __syncthreads();  // the previous chunk's LDS reads are done
+      stage_summaries<F>(sm, summ, c, NS);
+      for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj < i; jj += NSUB) {
+        const int j = c * kSegChunk + jj;
+        dsl[tk][jj] = gam[(size_t)j * NT + tc] * (dgam[(size_t)j * NT + tc] - S);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < KC; ++k)
+        if (sub + NSUB * k < i) dsl[tk][sub + NSUB * k] = ga[k] * (dga[k] - S);
     }
     __syncthreads();
 #pragma unroll
@@ -549,9 +575,8 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
     const size_t e = ((size_t)chain * NT + tb + tkr) * F + f0;
     if (iu[u] > 0) {
       const float dsc = sp[0][tkr];
-      const VT sv = *reinterpret_cast<const VT*>(summ + (size_t)iu[u] * F + f0);
 #pragma unroll
-      for (int k = 0; k < FPL; ++k) dxu[u][k] += dsc * sv[k];
+      for (int k = 0; k < FPL; ++k) dxu[u][k] += dsc * svc[u][k];
     }
     float dq[FPL];
 #pragma unroll
