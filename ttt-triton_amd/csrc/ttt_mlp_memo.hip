@@ -109,7 +109,9 @@ __global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams
 // registers are held to that occupancy too): finish 84 -> 76 us, gate
 // 52 -> 46 us at B16 H12 T2048 with 16 segments.  The finish kernel requests
 // every load of the first chunk up front (76 -> 67 us; it then holds 116
-// registers, four workgroups per CU: capped at five it spills and is slower).
+// registers, four workgroups per CU: capped at five it spills and is slower);
+// the gate kernel keeps the first chunk's logits in registers for its second
+// pass (46 -> 37 us, the same with or without its cap).
 constexpr int kTokBlk = 64;
 constexpr int kRowUnroll = kTokBlk / (kMemoThreads / 16);
 constexpr int kSegChunk = 16;
@@ -126,8 +128,8 @@ __device__ __forceinline__ void stage_summaries(float (*sm)[F], const float* __r
 // The gates: logits s_j = XU_t . summary_j for j = 0..i and gamma =
 // softmax(s).  Each thread keeps an online (max, sum) over its segments, the
 // four partial pairs of a token are merged through LDS, and a second pass
-// recomputes each logit (the same operations, so the same value) to write the
-// normalised gate.
+// writes the normalised gates: the first chunk's logits kept in registers,
+// later chunks' recomputed (the same operations, so the same value).
 template <typename T, int F>
 __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParams p) {
   constexpr int K = 16;
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
   const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
   const int t = tb + tk;
   const int i = t < NT ? (t / K) / M : -1;
-  if (nch == 1) stage_summaries<F>(sm, summ, 0, NS);
+  stage_summaries<F>(sm, summ, 0, NS);
   __syncthreads();
   float x[F];
 #pragma unroll
@@ -176,19 +178,27 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
     }
     return s;
   };
+  constexpr int KC = kSegChunk / NSUB;  // first-chunk segments per thread
+  float lg[KC];                         // their logits
   float m = -3.0e38f, l = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    if (nch > 1) {
-      __syncthreads();
-      stage_summaries<F>(sm, summ, c, NS);
-      __syncthreads();
+  auto online = [&](float sj) {
+    const float mn = fmaxf(m, sj);
+    l = l * __expf(m - mn) + __expf(sj - mn);
+    m = mn;
+  };
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    lg[k] = 0.f;
+    if (sub + NSUB * k <= i) {
+      lg[k] = logit(sub + NSUB * k);
+      online(lg[k]);
     }
-    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj <= i; jj += NSUB) {
-      const float sj = logit(jj);
-      const float mn = fmaxf(m, sj);
-      l = l * __expf(m - mn) + __expf(sj - mn);
-      m = mn;
-    }
+  }
+  for (int c = 1; c < nch; ++c) {
+    __syncthreads();
+    stage_summaries<F>(sm, summ, c, NS);
+    __syncthreads();
+    for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj <= i; jj += NSUB) online(logit(jj));
   }
   red[0][sub][tk] = m;
   red[1][sub][tk] = l;
@@ -200,12 +210,19 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
 #pragma unroll
   for (int u = 0; u < NSUB; ++u) sum += red[1][u][tk] * __expf(red[0][u][tk] - mx);
   const float inv = i >= 0 ? 1.0f / sum : 0.f;
-  for (int c = 0; c < nch; ++c) {
-    if (nch > 1) {
-      __syncthreads();
-      stage_summaries<F>(sm, summ, c, NS);
-      __syncthreads();
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    const int j = sub + NSUB * k;
+    if (j <= i) {
+      const float gj = __expf(lg[k] - mx) * inv;
+      gam[(size_t)j * NT + t] = gj;
+      if (j == i) gb[L.gcur + t] = gj;
     }
+  }
+  for (int c = 1; c < nch; ++c) {
+    __syncthreads();
+    stage_summaries<F>(sm, summ, c, NS);
+    __syncthreads();
     for (int jj = sub; jj < kSegChunk && c * kSegChunk + jj <= i; jj += NSUB) {
       const int j = c * kSegChunk + jj;
       const float gj = __expf(logit(jj) - mx) * inv;
