@@ -181,3 +181,32 @@ def test_layer_directional_derivatives(kind, M):
             fm = f(x - h * dx, *(v - h * d for v, d in zip(vals, dirs))).item()
         num = (fp - fm) / (2 * h)
         assert abs(ana - num) <= 1e-6 * max(1.0, abs(num)), (ana, num)
+
+
+def test_row_split_projection_matches_linear():
+    """The model's projection (weight gradient as a sum of row-block
+    products, bias gradient by row blocks) against torch's linear on the CPU:
+    the same output and gradients in fp64, at row counts with 16, 4 and 1 row
+    blocks, with and without an input gradient."""
+    from ttt_amd.model import _padded_width, _ProjectionFunction, _row_blocks, projection
+    assert (_row_blocks(16384, 1024), _row_blocks(4096, 1024), _row_blocks(1000, 1024)) == (16, 4, 1)
+    assert _padded_width(1028) == 1152 and _padded_width(516) == 520 and _padded_width(3084) == 3200
+    for rows, din, dout, xgrad in ((16384, 7, 64, False), (4096, 32, 130, True), (1000, 16, 24, True)):
+        x = _rand(rows, din, seed=rows).requires_grad_(xgrad)
+        w = _rand(dout, din, seed=1).requires_grad_(True)
+        b = _rand(dout, seed=2).requires_grad_(True)
+        dy = _rand(rows, dout, seed=3)
+        y = _ProjectionFunction.apply(x, w, b)
+        y.backward(dy)
+        mine = (y.detach(), w.grad.clone(), b.grad.clone(), x.grad.clone() if xgrad else None)
+        w.grad = b.grad = x.grad = None
+        y_ref = F.linear(x, w, b)
+        y_ref.backward(dy)
+        assert torch.allclose(mine[0], y_ref.detach(), rtol=1e-12, atol=1e-12)
+        assert torch.allclose(mine[1], w.grad, rtol=1e-10, atol=1e-9)
+        assert torch.allclose(mine[2], b.grad, rtol=1e-10, atol=1e-9)
+        if xgrad:
+            assert torch.allclose(mine[3], x.grad, rtol=1e-12, atol=1e-12)
+    # projection() keeps the leading dims
+    x3 = _rand(2, 8, 5, seed=9)
+    assert projection(x3, _rand(3, 5, seed=10), _rand(3, seed=11)).shape == (2, 8, 3)

@@ -58,8 +58,9 @@ class _ProjectionFunction(torch.autograd.Function):
     The backward's weight gradient dy^T x contracts over all R = B*L rows into
     an N x Din output of a few hundred 64x64 tiles, too few to fill the GPU
     with one long contraction each; it is formed instead as S row-block
-    products (one batched GEMM) summed in fp32.  The bias gradient is the
-    column sum of dy, taken over row blocks the same way."""
+    products (one batched GEMM) summed in fp32 (in the input's own type when
+    that is wider).  The bias gradient is the column sum of dy, taken over row
+    blocks the same way."""
 
     @staticmethod
     def forward(ctx, x, w, b):
@@ -72,10 +73,11 @@ class _ProjectionFunction(torch.autograd.Function):
         R, N = dy.shape
         dy = dy.contiguous()
         dx = dy @ w if ctx.needs_input_grad[0] else None
+        acc = torch.float32 if dy.element_size() < 4 else dy.dtype  # 16-bit inputs summed in fp32
         s = _row_blocks(R, 1024)
-        dw = torch.bmm(dy.view(s, R // s, N).transpose(1, 2), x.view(s, R // s, -1)).sum(0, dtype=torch.float32)
+        dw = torch.bmm(dy.view(s, R // s, N).transpose(1, 2), x.view(s, R // s, -1)).sum(0, dtype=acc)
         s = 64 if R % 64 == 0 else 1
-        db = dy.view(s, R // s, N).sum(1, dtype=torch.float32).sum(0)
+        db = dy.view(s, R // s, N).sum(1, dtype=acc).sum(0)
         return dx, dw.to(w.dtype), db.to(w.dtype)
 
 
