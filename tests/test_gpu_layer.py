@@ -62,7 +62,9 @@ def _oracle_producer(proj, ln_w, ln_b, H, F_, base_lr, grads, dlr):
     return [o.detach() for o in outs], pj.grad, lw.grad, lb.grad
 
 
-@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 3)])
+# model widths H*F of 256 and less, 384 and 1024: the backward's per-lane
+# arrays come in one, two and four chunks of 256 features
+@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 3), (64, 6), (64, 16)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_producer_vs_oracle(F_, H, dt):
     from ttt_amd.layer_io import ProducerFunction, rope_table
@@ -96,7 +98,7 @@ def test_producer_vs_oracle(F_, H, dt):
     assert bool((pj.grad[..., 4 * D + H:] == 0).all())  # padding columns get a zero gradient
 
 
-@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 12)])
+@pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 8), (64, 12)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_post_norm_vs_oracle(F_, H, dt):
     from ttt_amd.layer_io import PostNormFunction
