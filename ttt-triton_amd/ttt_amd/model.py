@@ -151,6 +151,11 @@ class TTTLayerBase(nn.Module):
         self.ttt_norm_weight = nn.Parameter(torch.ones(H, F))
         self.ttt_norm_bias = nn.Parameter(torch.zeros(H, F))
         self.post_norm = nn.LayerNorm(D, eps=1e-6)
+        # zero rows that pad the fused projection to its row width (not
+        # parameters, not in the state dict)
+        pad = _padded_width(4 * D + H) - (4 * D + H)
+        self.register_buffer("_proj_pad_w", torch.zeros(pad, D), persistent=False)
+        self.register_buffer("_proj_pad_b", torch.zeros(pad), persistent=False)
 
     def init_weights(self):
         """ttt_layer.py:81-89"""
@@ -167,12 +172,11 @@ class TTTLayerBase(nn.Module):
         multiple of 8, of 128 where that costs little), one GEMM instead of
         five (ttt_layer.py:141-163)."""
         H, D = self.num_heads, self.width
-        pad = _padded_width(4 * D + H) - (4 * D + H)
         w = [self.wq.weight, self.wk.weight, self.wv.weight, self.wu.weight, self.learnable_ttt_lr_weight.view(H, D)]
         b = [self.wq.bias, self.wk.bias, self.wv.bias, self.wu.bias, self.learnable_ttt_lr_bias.view(H)]
-        if pad:
-            w.append(self.wq.weight.new_zeros(pad, D))
-            b.append(self.wq.bias.new_zeros(pad))
+        if self._proj_pad_w.shape[0]:
+            w.append(self._proj_pad_w.to(self.wq.weight.dtype))
+            b.append(self._proj_pad_b.to(self.wq.bias.dtype))
         return projection(x, torch.cat(w, 0), torch.cat(b, 0))
 
     def process_input(self, x: torch.Tensor, rope: torch.Tensor):
