@@ -303,3 +303,27 @@ def test_last_token_path_matches_full_output(kind):
         e = rel_l2(grads[1][n], grads[0][n])
         _say(f"  d{n}: rel-L2 {e:.2e}")
         assert e <= 1e-5, n
+
+
+@pytest.mark.parametrize("kind", ["ttt_mlp", "ttt_linear"])
+def test_inference_forward_matches_training_forward(kind):
+    """Under no_grad the inner-loop Functions skip the checkpoints, final
+    state and saved buffer their backward would read; the layer's output is
+    bitwise the training forward's."""
+    from ttt_amd.model import ModelConfig, TTTWrapper
+    B, L, H, F_ = 2, 256, 4, 64
+    _say(f"inference forward {kind} B{B} L{L} H{H} F{F_}")
+    cfg = ModelConfig(seq_len=L, model_dim=H * F_, num_heads=H, ssm_layer=kind, mini_batch_size=16,
+                      ttt_base_lr=0.05, mem_cache_segment_n_mini_batches=2 if kind == "ttt_mlp" else 0,
+                      scan_checkpoint_group_size=16)
+    torch.manual_seed(7)
+    dev = torch.device("cuda")
+    layer = TTTWrapper(cfg).to(dev)
+    x = torch.randn(B, L, H * F_, device=dev)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        with torch.no_grad():
+            y_inf = layer(x)
+        y_train = layer(x)
+    torch.cuda.synchronize()
+    assert y_train.requires_grad and not y_inf.requires_grad
+    assert torch.equal(y_inf, y_train.detach())

@@ -136,11 +136,14 @@ class TTTLinearFunction(torch.autograd.Function):
                 checkpoint_group_size, eps=LN_EPS, eta_rule="dense"):
         NC = XQ_batch.shape[2]
         G = min(max(int(checkpoint_group_size), 1), NC)
+        # what the backward reads only when a gradient is wanted
+        train = any(ctx.needs_input_grad)
         out, ck, last, saved = linear_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, XQ_batch,
-                                              XV_batch, XK_batch, eta_batch, G, eps, want_ckpt=True,
-                                              want_last=True, want_saved=True, eta_rule=eta_rule)
-        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, ck[0],
-                              last[0], saved)
+                                              XV_batch, XK_batch, eta_batch, G, eps, want_ckpt=train,
+                                              want_last=train, want_saved=train, eta_rule=eta_rule)
+        if train:
+            ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, ck[0],
+                                  last[0], saved)
         ctx.G, ctx.eps, ctx.eta_rule = G, eps, eta_rule
         ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype,
                       XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)

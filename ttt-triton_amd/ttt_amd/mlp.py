@@ -178,12 +178,16 @@ class TTTMLPFunction(torch.autograd.Function):
         NC = XQ_batch.shape[2]
         G = min(max(int(checkpoint_group_size), 1), NC)
         M = int(memo_segment_size)
+        # what the backward reads (checkpoints, final state, saved buffer) only
+        # when a gradient is wanted: an inference forward skips those stores
+        train = any(ctx.needs_input_grad)
         out, ck, memo, last, saved = mlp_forward(ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
                                                XQ_batch, XV_batch, XK_batch, eta_batch, G, M=M, eps=eps,
-                                               want_ckpt=True, want_last=True, want_saved=True,
+                                               want_ckpt=train, want_last=train, want_saved=train,
                                                ckpt_w1_only=True, eta_rule=eta_rule)
-        ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck, *last,
-                              saved)
+        if train:
+            ctx.save_for_backward(XQ_batch, XV_batch, XK_batch, eta_batch, ttt_norm_weight, ttt_norm_bias, *ck,
+                                  *last, saved)
         ctx.G, ctx.eps, ctx.eta_rule = G, eps, eta_rule
         ctx.dtypes = (ttt_norm_weight.dtype, ttt_norm_bias.dtype, W1_init.dtype, b1_init.dtype, W2_init.dtype,
                       b2_init.dtype, XQ_batch.dtype, XV_batch.dtype, XK_batch.dtype, eta_batch.dtype)
