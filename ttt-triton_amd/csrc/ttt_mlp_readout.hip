@@ -4,10 +4,11 @@
 // chain (kernels/mlp_cached_readout.py:88-109,143, indexed per chain).
 //
 // The weights are fixed, so tokens are independent: a workgroup of eight waves
-// takes one chain and a chunk of up to 256 tokens.  It stages the chain's W1
+// takes one chain and a chunk of up to 512 tokens.  It stages the chain's W1
 // and W2 once into LDS, already in MFMA operand order (one 4-element vector
 // per lane per 16x16 block, so every operand read is one conflict-free
-// ds_read), then each wave runs up to two 16-token tiles through
+// ds_read), then each wave runs two rounds of up to two 16-token tiles
+// (two rounds per staging: 61 -> 58 us at B16 H12 T2048; four: 69) through
 //
 //   Z1^T = W1^T XQ^T           (hidden x token: its C layout is the B operand
 //   X2^T = gelu(Z1^T + b1)      of the next product with no transpose)
@@ -36,7 +37,8 @@ template <typename T, int FT, int HTT> struct ReadoutShared {
 
 constexpr int kReadoutWaves = 8;
 constexpr int kReadoutTilesPerWave = 2;
-constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave;  // tokens per workgroup
+constexpr int kReadoutRounds = 2;  // rounds of tiles per wave over one staging of W
+constexpr int kReadoutChunk = 16 * kReadoutWaves * kReadoutTilesPerWave * kReadoutRounds;  // tokens per workgroup
 
 template <typename T, int FT, int HTT>
 __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void mlp_readout_kernel(MlpReadoutParams p) {
@@ -58,16 +60,16 @@ __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void ml
   const int g = lane_id() >> 4;
 
   const int ntiles = p.ntok >> 4;
-  const int t0 = chunk * (kReadoutChunk / 16) + wave * NT;  // first token tile of this wave
-  const int nv = min(NT, ntiles - t0);                      // valid tiles (may be <= 0)
   const size_t xoff = (size_t)chain * p.ntok * F;
   const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + xoff;
   float* __restrict__ OUT = p.out + xoff;
 
-  // XQ^T operand frags (free = token, contraction = feature), requested
-  // first; tiles past the valid range repeat a valid one and are not stored
+  // XQ^T operand frags of round r (free = token, contraction = feature);
+  // tiles past the valid range repeat a valid one and are not stored
   Frag<T> xq[NT][FT];
-  {
+  auto load_round = [&](int r, int& t0, int& nv) {
+    t0 = (chunk * kReadoutRounds + r) * (16 * kReadoutWaves * NT / 16) + wave * NT;  // first token tile
+    nv = min(NT, ntiles - t0);                                                    // valid tiles (may be <= 0)
     const int tl = max(nv, 1) - 1;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -75,7 +77,9 @@ __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void ml
 #pragma unroll
       for (int kb = 0; kb < FT; ++kb) xq[t][kb] = load_frag(x, F, 16 * kb);
     }
-  }
+  };
+  int t0, nv;
+  load_round(0, t0, nv);  // requested before the staging
 
   // ---- stage W1, W2, biases and LN parameters of this chain
   {
@@ -87,38 +91,43 @@ __global__ __launch_bounds__(64 * kReadoutWaves, sizeof(T) == 2 ? 2 : 1) void ml
       sh.lnb[i] = p.ln_b[h * F + i];
     }
   }
-  __syncthreads();
-  if (nv <= 0) return;  // no barrier follows
+  __syncthreads();  // the last barrier: a wave may leave after it
 
-  Tile acc[NT][FT];  // Z2 + b2
-  fixed_mlp_tiles<T, FT, HTT, NT>(sh.w, xq, acc);
-
-  // ---- LayerNorm over the F features of each token row, residual, store.
-  // Lane (g, n) holds 4 features of token n in each feature tile; the row's
-  // other 3F/4 features are in lanes n + 16, n + 32, n + 48 (sum_col4).
   const float invF = 1.0f / (float)F;
+#pragma unroll 1
+  for (int r = 0; r < kReadoutRounds; ++r) {
+    if (r > 0) load_round(r, t0, nv);
+    if (nv <= 0) break;  // later rounds lie further along
+
+    Tile acc[NT][FT];  // Z2 + b2
+    fixed_mlp_tiles<T, FT, HTT, NT>(sh.w, xq, acc);
+
+    // ---- LayerNorm over the F features of each token row, residual, store.
+    // Lane (g, n) holds 4 features of token n in each feature tile; the row's
+    // other 3F/4 features are in lanes n + 16, n + 32, n + 48 (sum_col4).
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (t >= nv) break;
-    float s = 0.f;
+    for (int t = 0; t < NT; ++t) {
+      if (t >= nv) break;
+      float s = 0.f;
 #pragma unroll
-    for (int c = 0; c < FT; ++c) s += (acc[t][c].v[0] + acc[t][c].v[1]) + (acc[t][c].v[2] + acc[t][c].v[3]);
-    const float mean = sum_col4(s) * invF;
-    float q = 0.f;
+      for (int c = 0; c < FT; ++c) s += (acc[t][c].v[0] + acc[t][c].v[1]) + (acc[t][c].v[2] + acc[t][c].v[3]);
+      const float mean = sum_col4(s) * invF;
+      float q = 0.f;
 #pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      acc[t][c].v -= mean;
-      const f4 d = acc[t][c].v;
-      q += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
-    }
-    const float rstd = rsqrt_f(sum_col4(q) * invF + p.eps);
-    float* o = OUT + (size_t)(t0 + t) * 16 * F;
+      for (int c = 0; c < FT; ++c) {
+        acc[t][c].v -= mean;
+        const f4 d = acc[t][c].v;
+        q += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+      }
+      const float rstd = rsqrt_f(sum_col4(q) * invF + p.eps);
+      float* o = OUT + (size_t)(t0 + t) * 16 * F;
 #pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      const f4 lw = *reinterpret_cast<const f4*>(&sh.lnw[16 * c + 4 * g]);
-      const f4 lb = *reinterpret_cast<const f4*>(&sh.lnb[16 * c + 4 * g]);
-      const f4 x = frag_to_f4(xq[t][c]);  // XQ[n][16c + 4g + j]
-      store_f4(o, F, 16 * c, x + lw * (acc[t][c].v * rstd) + lb);
+      for (int c = 0; c < FT; ++c) {
+        const f4 lw = *reinterpret_cast<const f4*>(&sh.lnw[16 * c + 4 * g]);
+        const f4 lb = *reinterpret_cast<const f4*>(&sh.lnb[16 * c + 4 * g]);
+        const f4 x = frag_to_f4(xq[t][c]);  // XQ[n][16c + 4g + j]
+        store_f4(o, F, 16 * c, x + lw * (acc[t][c].v * rstd) + lb);
+      }
     }
   }
 }
