@@ -63,18 +63,22 @@ size_t memo_gate_floats_per_chain(int NC, int K, int F, int M) {
 // ------------------------------------------------------------------ summaries and gates
 constexpr int kSegThreads = 256;  // threads of the per-(chain, segment) kernels
 
-// Sum over a segment's tokens t0..t1-1 of w(t) * X[t][f], for f = threadIdx.x % F,
-// kSegThreads / F token rows at a time; the block's total for column f is returned
-// to every thread of that column.
+// Sum over a segment's tokens t0..t1-1 of w(t) * X[t][f]: each thread reads
+// 4 consecutive features of a row (one 8- or 16-byte load), kSegThreads / (F/4)
+// rows at a time; the block's total for column f = threadIdx.x % F is returned
+// to every thread of that column.  `part` holds kSegPart floats.
+constexpr int kSegPart = 4 * kSegThreads;
 template <typename T, int F, typename W>
 __device__ __forceinline__ float segment_column_sum(const T* __restrict__ X, int t0, int t1, W w, float* part) {
-  constexpr int R = kSegThreads / F;
-  const int f = threadIdx.x % F, r = threadIdx.x / F;
-  float acc = 0.f;
+  constexpr int C = F / 4, R = kSegThreads / C;  // threads per row, rows per pass
+  static_assert(R * F <= kSegPart, "partials fit");
+  const int c = threadIdx.x % C, r = threadIdx.x / C;
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-  for (int t = t0 + r; t < t1; t += R) acc += w(t) * (float)X[(size_t)t * F + f];
-  part[threadIdx.x] = acc;
+  for (int t = t0 + r; t < t1; t += R) acc += w(t) * load4(X + (size_t)t * F + 4 * c);
+  *reinterpret_cast<f4*>(&part[r * F + 4 * c]) = acc;
   __syncthreads();
+  const int f = threadIdx.x % F;
   float tot = 0.f;
 #pragma unroll
   for (int q = 0; q < R; ++q) tot += part[q * F + f];
@@ -85,7 +89,7 @@ __device__ __forceinline__ float segment_column_sum(const T* __restrict__ X, int
 template <typename T, int F>
 __global__ __launch_bounds__(kSegThreads) void memo_summary_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  __shared__ float part[kSegThreads];
+  __shared__ __align__(16) float part[kSegPart];
   const int chain = blockIdx.x / p.NS, j = blockIdx.x - chain * p.NS;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
@@ -610,7 +614,7 @@ __global__ __launch_bounds__(kMemoThreads) void memo_finish_kernel(MlpMemoParams
 template <typename T, int F>
 __global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) {
   constexpr int K = 16;
-  __shared__ float part[kSegThreads];
+  __shared__ __align__(16) float part[kSegPart];
   const int chain = blockIdx.x / p.NS, j = blockIdx.x - chain * p.NS;
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
   const MemoGateLayout L(NC, K, F, NS);
@@ -619,8 +623,14 @@ __global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) 
   T* __restrict__ DXK = static_cast<T*>(p.dXK) + (size_t)chain * NT * F;
   const int t0 = j * M * K, t1 = min((j + 1) * M, NC) * K;
   const float tot = segment_column_sum<T, F>(XU, t0, t1, [ds](int t) { return ds[t]; }, part);
-  const T v = (T)(tot / (float)(t1 - t0));
-  for (int t = t0 + (int)threadIdx.x / F; t < t1; t += kSegThreads / F) DXK[(size_t)t * F + threadIdx.x % F] = v;
+  __syncthreads();  // every thread's partial sums read
+  if (threadIdx.x < F) part[threadIdx.x] = tot / (float)(t1 - t0);
+  __syncthreads();
+  // the same row for every token of the segment, 4 features per thread
+  constexpr int C = F / 4;
+  const int c = threadIdx.x % C;
+  const f4 v = *reinterpret_cast<const f4*>(&part[4 * c]);
+  for (int t = t0 + (int)threadIdx.x / C; t < t1; t += kSegThreads / C) store4(DXK + (size_t)t * F + 4 * c, v);
 }
 
 // ------------------------------------------------------------------ launchers
