@@ -698,7 +698,8 @@ ttt::MlpMemoParams memo_params(const void* XQ, const void* XQW, const float* W1,
   p.FF = FF;
   p.M = M;
   p.NS = (NC + M - 1) / M;
-  p.nchunk = (NC + ttt::mlp_memo_chunk_tiles() - 1) / ttt::mlp_memo_chunk_tiles();
+  const int ct = ttt::mlp_memo_chunk_tiles(B, H, NC);
+  p.nchunk = (NC + ct - 1) / ct;
   p.eps = eps;
   return p;
 }

@@ -107,7 +107,7 @@ struct MlpMemoParams {
 size_t memo_gate_floats_per_chain(int NC, int K, int F, int M);
 size_t mlp_memo_image_bytes(int F, int FF);
 hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStream_t stream);
-int mlp_memo_chunk_tiles();
+int mlp_memo_chunk_tiles(int B, int H, int NC);  // mini-batches per combiner workgroup chunk
 
 // What the TTT-MLP forward saves per mini-batch for the backward, one slot
 // per (chain, mini-batch) in the saved buffer [B*H][NC][slot].  Byte offsets;

@@ -15,7 +15,10 @@
 //   memo_summary_kernel   one workgroup per (chain, segment): the segment summaries;
 //   memo_gate_kernel      one workgroup per 64 tokens: the gates (written as
 //                         gamma^T [NS][tokens] plus the current-segment gate);
-//   memo_combine_kernel   one workgroup per (chain, pair of 256-token chunks):
+//   memo_combine_kernel   one workgroup per (chain, pair of 256-token chunks,
+//                         or 128-token ones where the pairs would leave CUs
+//                         idle: 128 -> 256 workgroups for the forecaster's
+//                         combines, 63-78 -> 38-48 us):
 //                         for each memo state j below a chunk's last segment, stage
 //                         W1_j/W2_j into LDS in MFMA operand order (as the cached
 //                         readout does), run the chunk's tiles of later
@@ -240,6 +243,7 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
 constexpr int kMemoWaves = 8;
 constexpr int kMemoTilesPerWave = 2;
 constexpr int kMemoChunkTiles = kMemoWaves * kMemoTilesPerWave;  // mini-batches (16 tokens each) per workgroup
+constexpr int kComputeUnits = 256;  // MI355X
 
 // Packed memo states (bf16): each state's LDS image -- the FixedMlpLds struct
 // the staging builds, operand frags and biases -- written once by
@@ -262,12 +266,12 @@ __global__ __launch_bounds__(256) void memo_pack_kernel(MlpMemoParams p) {
   for (int i = threadIdx.x; i < IMG / 16; i += 256) dst[i] = src[i];
 }
 
-template <typename T, int FT, int HTT, bool BWD, bool PK>
+template <typename T, int FT, int HTT, bool BWD, bool PK, int NTW>
 __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoParams p) {
   constexpr int F = 16 * FT;
   constexpr int FF = 16 * HTT;
   constexpr int K = 16;
-  constexpr int NTW = kMemoTilesPerWave;
+  constexpr int CT = kMemoWaves * NTW;  // mini-batches per chunk
   constexpr int IMG = kMemoImg<T, FT, HTT>;
   // unpacked: one staging area, filled between two barriers per state;
   // packed: two images, the next state's copied in while the current one is used
@@ -297,8 +301,8 @@ __global__ __launch_bounds__(64 * kMemoWaves) void memo_combine_kernel(MlpMemoPa
   for (int half = 0; half < 2; ++half) {
     const int chunk = half == 0 ? pair : p.nchunk - 1 - pair;
     if (half == 1 && chunk == pair) break;  // (uniform: the middle chunk of an odd count)
-    const int c0 = chunk * kMemoChunkTiles;                      // first mini-batch of the chunk
-    const int clast = min(c0 + kMemoChunkTiles, NC) - 1;         // last mini-batch of the chunk
+    const int c0 = chunk * CT;                                   // first mini-batch of the chunk
+    const int clast = min(c0 + CT, NC) - 1;                      // last mini-batch of the chunk
     const int jmax = clast / M;                                  // memo states 0..jmax-1 serve this chunk
     const int t0 = c0 + wave * NTW;                              // first mini-batch of this wave
     const int nv = max(0, min(NTW, NC - t0));                    // valid tiles of this wave
@@ -634,17 +638,24 @@ __global__ __launch_bounds__(kSegThreads) void memo_dxk_kernel(MlpMemoParams p) 
 }
 
 // ------------------------------------------------------------------ launchers
-template <typename T, int FT, int HTT, bool BWD>
-static hipError_t launch_combine(const MlpMemoParams& p, hipStream_t stream) {
+template <typename T, int FT, int HTT, bool BWD, int NTW>
+static hipError_t launch_combine_n(const MlpMemoParams& p, hipStream_t stream) {
   const dim3 grid(p.B * p.H * ((p.nchunk + 1) / 2)), block(64 * kMemoWaves);
   if constexpr (sizeof(T) == 2) {
     if (p.packed != nullptr) {
-      hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, true>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, true, NTW>), grid, block, 0, stream, p);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, false>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((memo_combine_kernel<T, FT, HTT, BWD, false, NTW>), grid, block, 0, stream, p);
   return hipGetLastError();
+}
+
+template <typename T, int FT, int HTT, bool BWD>
+static hipError_t launch_combine(const MlpMemoParams& p, hipStream_t stream) {
+  // p.nchunk was set from the same chunk size
+  if (mlp_memo_chunk_tiles(p.B, p.H, p.NC) == kMemoWaves) return launch_combine_n<T, FT, HTT, BWD, 1>(p, stream);
+  return launch_combine_n<T, FT, HTT, BWD, kMemoTilesPerWave>(p, stream);
 }
 
 template <typename T, int FT, int HTT>
@@ -697,7 +708,13 @@ hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStrea
   return hipErrorInvalidValue;
 }
 
-int mlp_memo_chunk_tiles() { return kMemoChunkTiles; }
+// Mini-batches per combiner chunk: two tiles per wave, or one where the
+// pairs of two-tile chunks would leave CUs idle (few chains or short
+// sequences, e.g. the forecaster's 128 chains of 32 mini-batches).
+int mlp_memo_chunk_tiles(int B, int H, int NC) {
+  const long long pairs = (long long)B * H * (((NC + kMemoChunkTiles - 1) / kMemoChunkTiles + 1) / 2);
+  return pairs < kComputeUnits ? kMemoWaves : kMemoChunkTiles;
+}
 
 size_t mlp_memo_image_bytes(int F, int FF) {
   const int FT = F / 16;
