@@ -357,8 +357,10 @@ long long ttt_get_option(int option);
 /* Status of the last ttt_mlp_bwd call that used `workspace` (same sizes):
  * waits for `stream`, then returns TTT_OK, or TTT_ERR_TIMEOUT if a fused
  * dXQ/dXK worker gave up waiting for its checkpoint group (that group's dXQ
- * and dXK rows then hold NaN).  No counterpart in the reference, whose
- * backward has no cross-workgroup waits. */
+ * and dXK rows then hold NaN).  With workspace NULL (workspace_bytes is then
+ * ignored) it reads the static scratch of ttt_mlp_bwd_noalloc on the current
+ * device instead: the status of the last no-allocation call there.  No
+ * counterpart in the reference, whose backward has no cross-workgroup waits. */
 int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int H, int NC, int K, int F,
                       int FF, int dtype, void* stream);
 

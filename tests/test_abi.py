@@ -285,6 +285,23 @@ def test_options(lib):
 def test_mlp_bwd_check_validation(lib):
     B, H, NC, K, F, FF = 2, 4, 16, 16, 64, 256
     w = lib.ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, BF16)
-    assert lib.ttt_mlp_bwd_check(None, w, B, H, NC, K, F, FF, BF16, None) == E_WS
+    # NULL names the no-allocation entry point's scratch: a problem larger than it is refused on the host
+    assert lib.ttt_mlp_bwd_check(None, 0, 16, 12, 128, K, F, FF, BF16, None) == -9
     assert lib.ttt_mlp_bwd_check(P, w - 1, B, H, NC, K, F, FF, BF16, None) == E_WS
     assert lib.ttt_mlp_bwd_check(P, w, 0, H, NC, K, F, FF, BF16, None) == E_SHAPE
+
+
+def test_model_config_rejects_shapes_the_layer_kernels_do_not_take():
+    """ModelConfig raises before any layer is built: head dims other than 32
+    and 64 (producer, post-norm, memory cache), model widths above 1024, and
+    mini-batches that are not 16..64 tokens in steps of 16."""
+    from ttt_amd.model import ModelConfig
+    ModelConfig(seq_len=512, model_dim=128, num_heads=4, mini_batch_size=64)   # main.py's shape
+    ModelConfig(seq_len=512, model_dim=1024, num_heads=16, mini_batch_size=16)
+    for kw in (dict(model_dim=192, num_heads=4),      # F = 48
+               dict(model_dim=128, num_heads=1),      # F = 128
+               dict(model_dim=2048, num_heads=32),    # F = 64, D > 1024
+               dict(model_dim=128, num_heads=4, mini_batch_size=8, seq_len=512),
+               dict(model_dim=128, num_heads=4, mini_batch_size=128, seq_len=512)):
+        with pytest.raises(ValueError):
+            ModelConfig(**{"seq_len": 512, "mini_batch_size": 64, **kw})

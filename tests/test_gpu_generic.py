@@ -1,5 +1,5 @@
-"""The general-shape inner loops (mini-batch K in {32, 64}, hidden width FF =
-F = 32 as the reference's TTTMLP builds it, F = 16/48) against the CPU oracle:
+"""The general-shape inner loops (mini-batch K in {16, 32, 48, 64}, hidden width FF =
+F = 32 as the reference's TTTMLP builds it, F from 32 to 256, FF up to 1024) against the CPU oracle:
 forward with every side output (out, final state, checkpoints, memo
 snapshots) and the backward's gradients of every input.  The reference's own
 model configuration (ModelConfig defaults, main.py: K = 64, model dim 128 over
@@ -60,6 +60,13 @@ MLP_CASES = [
     (2, 2, 5, 32, 64, 64, 2, 2, torch.bfloat16, "causal"),
     (1, 3, 7, 16, 32, 32, 3, 2, torch.float32, "causal"),   # FF = 32 at K = 16
     (1, 2, 3, 48, 48, 96, 2, 1, torch.float32, "layer"),
+    # wide shapes: 16 columns per lane in the row passes (F > 64) and products
+    # whose output is split into blocks of at most 480 rows and columns
+    (1, 2, 3, 16, 128, 128, 2, 1, torch.float32, "causal"),
+    (1, 1, 3, 32, 256, 256, 2, 2, torch.bfloat16, "causal"),
+    (1, 2, 3, 64, 64, 512, 2, 2, torch.float32, "layer"),
+    (1, 1, 2, 16, 64, 1024, 1, 1, torch.bfloat16, "causal"),
+    (1, 1, 2, 64, 256, 768, 1, 1, torch.float32, "causal"),
 ]
 
 
@@ -105,6 +112,8 @@ LIN_CASES = [
     (1, 3, 5, 32, 64, 2, torch.float32, "causal"),
     (1, 2, 4, 16, 48, 3, torch.float32, "causal"),
     (1, 2, 3, 64, 64, 1, torch.bfloat16, "causal"),
+    (1, 2, 3, 32, 128, 2, torch.float32, "causal"),
+    (1, 1, 3, 16, 256, 1, torch.bfloat16, "layer"),
 ]
 
 

@@ -21,7 +21,11 @@ pytestmark = pytest.mark.gpu
 FP32_ATOL = 1e-4
 BF16_RTOL = 2e-2
 FP32_RTOL_E2E = 1e-4
-BF16_FLOOR = 1e-2
+# bf16 bar for the XU projection's gradient, bounded against its own norm:
+# it enters only through the memory-cache gates (ttt_layer.py:519-533), is
+# 1e-4 of the largest parameter gradient at K = 64, and its bf16 error is set
+# by the rounding of the gate terms rather than by the loop
+BF16_RTOL_GATE = 1e-1
 
 
 def _say(*a):
@@ -179,20 +183,18 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
     err = abs(loss.item() - loss_ref.item()) / abs(loss_ref.item())
     _say(f"  loss {loss.item():.6f} vs {loss_ref.item():.6f}: rel {err:.3e}")
     bad = ["loss"] if err > tol else []
-    # bf16: rel-L2 per tensor, against a norm floor of BF16_FLOOR times the
-    # largest parameter gradient.  The XU projection's gradient enters only
-    # through the memory-cache gates and is 1e-4 of the rest at K = 64
-    # (1e-3 at K = 16): bf16 rounding of the gate terms sets its error there,
-    # while the fp32 runs hold it to ~1e-4 relative.
-    floor = 0.0 if dt == torch.float32 else BF16_FLOOR * max(
-        float(sd[n].grad.norm()) for n, _ in model.named_parameters() if sd[n].grad is not None)
+    # every parameter gradient by rel-L2 against its own norm; in bf16 the
+    # gate-only XU projection (BF16_RTOL_GATE) has the looser bar
     for name, prm in model.named_parameters():
         r = sd[name].grad
         if r is None:
             assert prm.grad is None or float(prm.grad.abs().max()) == 0.0, name
             continue
-        e = float((prm.grad.detach().double().cpu() - r.detach().double()).norm()) / max(float(r.norm()), floor)
-        tp = max(tol, C_FP32 * rtol32[name]) if dt == torch.float32 else tol
+        e = rel_l2(prm.grad, r)
+        if dt == torch.float32:
+            tp = max(tol, C_FP32 * rtol32[name])
+        else:
+            tp = BF16_RTOL_GATE if ".wu." in name else tol
         _say(f"  d{name}: rel-L2 {rel_l2(prm.grad, r):.3e} (|ref| {float(r.norm()):.3e}), bound ratio {e / tp:.2f}")
         if e > tp:
             bad.append(name)

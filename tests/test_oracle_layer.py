@@ -210,3 +210,54 @@ def test_row_split_projection_matches_linear():
     # projection() keeps the leading dims
     x3 = _rand(2, 8, 5, seed=9)
     assert projection(x3, _rand(3, 5, seed=10), _rand(3, seed=11)).shape == (2, 8, 3)
+
+
+def _producer_case(seed=5, B=2, L=32, H=3, Fh=32, K=16):
+    XQ, XK, XV, XU = (_rand(B, L, H, Fh, seed=seed + i) for i in range(4))
+    logits = _rand(B, L, H, seed=seed + 4)
+    freqs = LO.rope_freqs(Fh, 1, 1, L)
+    ones, zeros = torch.ones(H, Fh, dtype=torch.float64), torch.zeros(H, Fh, dtype=torch.float64)
+    out = LO.producer(XQ, XK, XV, XU, logits, freqs, ones, zeros, K, 1.0)
+    return (XQ, XK, XV, XU), out, K
+
+
+def test_producer_target_is_built_on_the_rotated_xk():
+    """ttt_layer.py:279-302 rotates XK first and builds the reconstruction
+    target from the rotated XK.  With ln_w = 1, ln_b = 0 the target minus the
+    XK the loop receives is (d - mean d) / (std d + eps), d = XV - XK_out: per
+    token and head zero mean and unbiased std sigma / (sigma + 1e-8) = 1 to
+    1e-7.  A target built on the unrotated (or unnormalised) XK adds
+    XK_l2 - rot(XK_l2) to it, which breaks both at every rotated position."""
+    _, (q, k, v, u, lr), K = _producer_case()
+    d = v - k                                        # [B, H, NC, K, F]
+    mean = d.mean(-1)
+    std = d.std(-1, unbiased=True)
+    assert float(mean.abs().max()) < 1e-12
+    assert float((std - 1).abs().max()) < 1e-7
+    # the slip this pins: the target on the L2-normalised but unrotated XK
+    (XQ, XK, XV, XU), _, _ = _producer_case()
+    B, L, H, Fh = XK.shape
+    kl2 = LO.l2_normalize(XK)
+    bad = LO.recon_target(XV, kl2, torch.ones(H, Fh, dtype=torch.float64), torch.zeros(H, Fh, dtype=torch.float64))
+    bad = bad.transpose(1, 2).reshape(B, H, L // K, K, Fh)
+    assert float((bad - k).mean(-1)[:, :, :, 1:].abs().max()) > 1e-3
+
+
+def test_producer_rotates_xu_like_xq():
+    """XU is L2-normalised and rotated with the same table as XQ
+    (ttt_layer.py:289-295): at one position both are rotated by the same
+    angles, so <XU_out, XQ_out> = <l2(XU), l2(XQ)>, while XU_out differs from
+    l2(XU) wherever the angles are not zero (every position but the first).
+    An unrotated XU fails the first identity, a missing normalisation both."""
+    (XQ, XK, XV, XU), (q, k, v, u, lr), K = _producer_case()
+    B, L, H, Fh = XQ.shape
+    to_mb = lambda t: t.transpose(1, 2).reshape(B, H, L // K, K, Fh)  # noqa: E731
+    ql2, ul2 = to_mb(LO.l2_normalize(XQ)), to_mb(LO.l2_normalize(XU))
+    # (the rotary table is fp32, as the reference's: unit modulus to ~1e-7)
+    assert torch.allclose((u * q).sum(-1), (ul2 * ql2).sum(-1), rtol=0, atol=1e-6)
+    assert torch.allclose(u.norm(dim=-1), torch.ones_like(u[..., 0]), rtol=0, atol=1e-6)
+    diff = (u - ul2).norm(dim=-1).reshape(B, H, L)
+    assert float(diff[:, :, 0].abs().max()) < 1e-15      # position 0: angle 0
+    assert float(diff[:, :, 1:].min()) > 1e-4             # every other position rotated
+    # the slip this pins: XU left unrotated gives other inner products
+    assert float(((ul2 * q).sum(-1) - (ul2 * ql2).sum(-1)).abs().max()) > 1e-3

@@ -55,6 +55,9 @@ def _case(B, H, NC, F_, FF, G, dt, seed):
     mine = _outputs(B, H, NC, F_, FF, dt, dev)
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_bwd_noalloc(*common, *(ptr(t) for t in mine), ptr(saved), saved.numel(), stream_of(dev))
+        assert st == 0, lib.ttt_error_string(st)
+        # the fused workers' timeout word of that call, read from the static scratch
+        st = lib.ttt_mlp_bwd_check(None, 0, B, H, NC, 16, F_, FF, code, stream_of(dev))
     assert st == 0, lib.ttt_error_string(st)
     torch.cuda.synchronize()
     return ref, mine

@@ -590,9 +590,16 @@ long long ttt_get_option(int option) {
 
 int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int H, int NC, int K, int F, int FF,
                       int dtype, void* stream) {
-  if (workspace == nullptr) return TTT_ERR_WORKSPACE;
   const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
   if (need == 0) return TTT_ERR_SHAPE;
+  if (workspace == nullptr) {  // the no-allocation entry point's scratch on the current device
+    if (need > TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES) return TTT_ERR_SCRATCH;
+    void* ws = nullptr;
+    const int st = scratch_of_current_device(&ws);
+    if (st != TTT_OK) return st;
+    workspace = ws;
+    workspace_bytes = TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES;
+  }
   if (workspace_bytes < need) return TTT_ERR_WORKSPACE;
   // the timeout word: control word 1 behind the B*H*NC handoff slots
   const int* ctrl = reinterpret_cast<const int*>(static_cast<const char*>(workspace) +

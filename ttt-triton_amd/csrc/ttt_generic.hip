@@ -55,6 +55,11 @@ __host__ __device__ GenLayout::GenLayout(int K_, int F_, int FF_, int NC_, bool 
 namespace {
 
 constexpr int kGenStage = 16384;  // floats of LDS staging for one product's operands (64 KB)
+// Largest output block (rows or columns) one staged product takes: a chunk
+// of 16 contraction steps of both operands, rows padded by 4 floats, must
+// fit the staging area, so that every chunk advances the contraction.
+constexpr int kGenBlock = 480;
+static_assert(kGenStage / ((kGenBlock + 4) + (kGenBlock + 4)) >= 16, "a staged chunk holds 16 contraction steps");
 
 // C[M x N] (row stride ldc) = alpha * op(A) op(B) (+ C when acc), with
 // op(A)[i][k] = ta ? A[k * lda + i] : A[i * lda + k] and likewise for B.
@@ -65,12 +70,12 @@ constexpr int kGenStage = 16384;  // floats of LDS staging for one product's ope
 // fp32 MFMA (v_mfma_f32_16x16x4_f32: exact products, fp32 sums), its operand
 // frags read from LDS (the padding puts the four lane groups of a read on
 // distinct banks).  Every thread of the workgroup calls it (it holds
-// barriers).  M, N and Kd are multiples of 16.
-__device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
-                   const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
+// barriers).  M, N and Kd are multiples of 16, M and N at most kGenBlock.
+__device__ void gg_block(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
+                         const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
   __shared__ float st[kGenStage];
   const int sa = M + 4, sb = N + 4;  // padded k-row strides: the transposing stores spread over the banks
-  const int kc = min(Kd, (kGenStage / (sa + sb)) & ~15);
+  const int kc = min(Kd, (kGenStage / (sa + sb)) & ~15);  // >= 16 (kGenBlock)
   float* As = st;
   const int wave = threadIdx.x >> 6, l = lane_id(), g = l >> 4, r = l & 15;
   const int nt = N >> 4, ntile = (M >> 4) * nt;
@@ -128,6 +133,22 @@ __device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, 
       }
     }
     __syncthreads();  // the staging area is free for the next chunk or product
+  }
+}
+
+// gg_block over output blocks of at most kGenBlock rows and columns (any M, N
+// that are multiples of 16): block (i0, j0) reads rows i0.. of op(A) and
+// columns j0.. of op(B) and writes C[i0.., j0..].
+__device__ void gg(float* __restrict__ C, int ldc, const float* __restrict__ A, int lda, bool ta,
+                   const float* __restrict__ B, int ldb, bool tb, int M, int N, int Kd, float alpha, bool acc) {
+  for (int i0 = 0; i0 < M; i0 += kGenBlock) {
+    const int mb = min(kGenBlock, M - i0);
+    const float* Ab = ta ? A + i0 : A + (size_t)i0 * lda;
+    for (int j0 = 0; j0 < N; j0 += kGenBlock) {
+      const int nb = min(kGenBlock, N - j0);
+      const float* Bb = tb ? B + (size_t)j0 * ldb : B + j0;
+      gg_block(C + (size_t)i0 * ldc + j0, ldc, Ab, lda, ta, Bb, ldb, tb, mb, nb, Kd, alpha, acc);
+    }
   }
 }
 

@@ -22,11 +22,12 @@ Per layer call, for hidden states x [B, L, D] (D = H*F):
 Parameter names and shapes are the reference's (wq ... wu, wo,
 learnable_ttt_lr_weight [H,1,D], learnable_ttt_lr_bias [H,1],
 ttt_norm_weight/bias [H,F], post_norm, W1/b1/W2/b2), so a reference state
-dict loads unchanged.  Mini-batch size K and head dim F are multiples of 16
-(K <= 64); K = 16 with F in {32, 64} (and the MLP's hidden width F, as TTTMLP
-builds it, in {64, 128, 256}) runs on the specialised kernels, any other
-shape on the general-shape ones; the memory-cache combiner needs F in
-{32, 64}."""
+dict loads unchanged.  Shapes the layer takes (ModelConfig raises ValueError
+for others): head dim F = model_dim / num_heads in {32, 64} (the producer,
+post-norm and memory-cache kernels), model_dim <= 1024, and a mini-batch
+size K that is a multiple of 16 up to 64.  The inner loop itself runs any
+shape on the general-shape kernels; K = 16 with F in {32, 64} (and the MLP's
+hidden width F, as TTTMLP builds it) runs on the specialised ones."""
 
 from __future__ import annotations
 
@@ -42,6 +43,8 @@ from .layer_io import POST_NORM_EPS, RECON_EPS, PostNormFunction, ProducerFuncti
 from .linear import TTTLinearFunction
 from .memo import mlp_memo_combine
 from .mlp import LN_EPS, TTTMLPFunction
+
+MAX_MODEL_DIM = 1024  # H * F, the widest row the producer / post-norm kernels take
 
 
 def _row_blocks(rows: int, target: int) -> int:
@@ -125,6 +128,16 @@ class ModelConfig:
             raise ValueError("seq_len must be a multiple of mini_batch_size")
         if (self.model_dim // self.num_heads) % 2:
             raise ValueError("RoPE needs an even head dim")
+        # the fused producer / post-norm kernels and the memory-cache combiner
+        # take head dims 32 and 64 and model widths up to 1024; the inner loop
+        # takes mini-batches of 16 to 64 tokens in steps of 16
+        F = self.model_dim // self.num_heads
+        if F not in (32, 64):
+            raise ValueError(f"head dim model_dim/num_heads = {F}: this build's layer kernels take 32 or 64")
+        if self.model_dim > MAX_MODEL_DIM:
+            raise ValueError(f"model_dim {self.model_dim} > {MAX_MODEL_DIM}, the widest the layer kernels take")
+        if self.mini_batch_size % 16 or not 16 <= self.mini_batch_size <= 64:
+            raise ValueError(f"mini_batch_size {self.mini_batch_size}: a multiple of 16 from 16 to 64 is needed")
 
 
 class TTTLayerBase(nn.Module):
