@@ -348,9 +348,14 @@ int ttt_mlp_bwd_noalloc(const void* XQ, const void* XK, const void* XV, const vo
  *   TTT_OPT_MLP_BWD_FUSED       1 (default): the dXQ/dXK pass runs inside the
  *                               sweep's launch when it fits; 0: always a second
  *                               launch (no waits at all)
+ *   TTT_OPT_SMALL_KERNELS       1 (default): shapes outside the specialised set
+ *                               with F = 32 (FF = 32), K <= 64 run the
+ *                               register-resident one-wave-per-chain kernels;
+ *                               0: the staged general-shape kernels (same
+ *                               interface and saved buffer)
  * ttt_set_option returns TTT_OK or TTT_ERR_ARG; ttt_get_option returns the
  * value, or -1 for an unknown option. */
-enum ttt_option { TTT_OPT_MLP_BWD_POLL_LIMIT = 1, TTT_OPT_MLP_BWD_FUSED = 2 };
+enum ttt_option { TTT_OPT_MLP_BWD_POLL_LIMIT = 1, TTT_OPT_MLP_BWD_FUSED = 2, TTT_OPT_SMALL_KERNELS = 3 };
 int ttt_set_option(int option, long long value);
 long long ttt_get_option(int option);
 

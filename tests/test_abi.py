@@ -277,9 +277,14 @@ def test_options(lib):
         assert lib.ttt_set_option(fused, 2) == E_ARG
         assert lib.ttt_set_option(99, 1) == E_ARG
         assert lib.ttt_get_option(99) == -1
+        small = _lib.OPT_SMALL_KERNELS
+        assert lib.ttt_get_option(small) == 1
+        assert lib.ttt_set_option(small, 0) == OK and lib.ttt_get_option(small) == 0
+        assert lib.ttt_set_option(small, 3) == E_ARG
     finally:
         lib.ttt_set_option(poll, old_poll)
         lib.ttt_set_option(fused, old_fused)
+        lib.ttt_set_option(_lib.OPT_SMALL_KERNELS, 1)
 
 
 def test_mlp_bwd_check_validation(lib):

@@ -60,6 +60,10 @@ MLP_CASES = [
     (2, 2, 5, 32, 64, 64, 2, 2, torch.bfloat16, "causal"),
     (1, 3, 7, 16, 32, 32, 3, 2, torch.float32, "causal"),   # FF = 32 at K = 16
     (1, 2, 3, 48, 48, 96, 2, 1, torch.float32, "layer"),
+    # the register-resident one-wave kernels' other mini-batch sizes (F = FF = 32)
+    (1, 2, 5, 48, 32, 32, 2, 2, torch.float32, "causal"),
+    (2, 2, 4, 32, 32, 32, 3, 1, torch.bfloat16, "layer"),
+    (1, 2, 3, 16, 32, 32, 1, 3, torch.bfloat16, "causal"),
     # wide shapes: 16 columns per lane in the row passes (F > 64) and products
     # whose output is split into blocks of at most 480 rows and columns
     (1, 2, 3, 16, 128, 128, 2, 1, torch.float32, "causal"),
@@ -113,6 +117,8 @@ LIN_CASES = [
     (1, 2, 4, 16, 48, 3, torch.float32, "causal"),
     (1, 2, 3, 64, 64, 1, torch.bfloat16, "causal"),
     (1, 2, 3, 32, 128, 2, torch.float32, "causal"),
+    (1, 3, 4, 48, 32, 3, torch.float32, "causal"),
+    (2, 2, 5, 32, 32, 2, torch.bfloat16, "layer"),
     (1, 1, 3, 16, 256, 1, torch.bfloat16, "layer"),
 ]
 
@@ -165,3 +171,43 @@ def test_generic_lr_rules_match_dense(kind):
             else torch.tril(torch.ones(K, K, dtype=torch.float64)) / (i + 1)[:, None])
     dlr_ref = (deta * coef).sum(-2)
     assert max_abs(res[kind][1][1][3], dlr_ref) <= 1e-4 * max(1.0, float(dlr_ref.abs().max()))
+
+
+@pytest.mark.parametrize("mlp,dt", [(True, torch.float32), (True, torch.bfloat16), (False, torch.float32)])
+def test_small_kernels_match_the_staged_kernels(mlp, dt):
+    """At the reference's model shape (K = 64, F = FF = 32) the register-
+    resident kernels and the staged general-shape kernels (TTT_OPT_SMALL_KERNELS
+    = 0) compute the same forward and gradients: fp32 to 2e-5 relative, bf16
+    within the bf16 bar (different operand roundings)."""
+    from ttt_amd import _lib
+    from ttt_amd.linear import linear_backward, linear_forward
+    from ttt_amd.mlp import mlp_backward, mlp_forward
+    B, H, NC, K, F_, G = 2, 4, 5, 64, 32, 2
+    _say(f"small vs staged {'mlp' if mlp else 'linear'} {dt}")
+    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=F_, seed=123, dtype=dt, eta_kind="causal", with_grad=True),
+                 H, F_, 11, mlp=mlp)
+    g = to_dev(d)
+    res = []
+    try:
+        for small in (1, 0):
+            _lib.set_option(_lib.OPT_SMALL_KERNELS, small)
+            if mlp:
+                out, ck, _, last, saved = mlp_forward(*(g[k] for k in MLP_KEYS), G, want_ckpt=True, want_last=True,
+                                                      want_saved=True)
+                grads = mlp_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved,
+                                     g["dOut"], G)
+                flat = [out, *last, *grads[0], *grads[1]]
+            else:
+                out, ck, last, saved = linear_forward(*(g[k] for k in LIN_KEYS), G, want_ckpt=True, want_last=True,
+                                                      want_saved=True)
+                grads = linear_backward(g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck[0], last[0],
+                                        saved, g["dOut"], G)
+                flat = [out, *last, *grads[0], *grads[1]]
+            torch.cuda.synchronize()
+            res.append([t.detach().clone() for t in flat])
+    finally:
+        _lib.set_option(_lib.OPT_SMALL_KERNELS, 1)
+    bound = 2e-5 if dt == torch.float32 else BF16_RTOL
+    worst = max(rel_l2(a, b) for a, b in zip(*res))
+    _say(f"  worst rel-L2 {worst:.3e} (bound {bound:.0e})")
+    assert worst <= bound

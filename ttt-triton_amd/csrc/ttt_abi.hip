@@ -13,6 +13,7 @@ namespace {
 // process-wide options (ttt_set_option)
 std::atomic<long long> g_mlp_bwd_poll_limit{1LL << 22};
 std::atomic<long long> g_mlp_bwd_fused{1};
+std::atomic<long long> g_small_kernels{1};
 
 bool eta_rule_ok(int r) { return r == TTT_ETA_DENSE || r == TTT_ETA_LAYER || r == TTT_ETA_CAUSAL; }
 
@@ -92,6 +93,10 @@ int check_linear(int NC, int F) {
 }
 
 }  // namespace
+
+namespace ttt {
+bool gen_force_general() { return g_small_kernels.load() == 0; }
+}  // namespace ttt
 
 extern "C" {
 
@@ -576,6 +581,10 @@ int ttt_set_option(int option, long long value) {
       if (value != 0 && value != 1) return TTT_ERR_ARG;
       g_mlp_bwd_fused.store(value);
       return TTT_OK;
+    case TTT_OPT_SMALL_KERNELS:
+      if (value != 0 && value != 1) return TTT_ERR_ARG;
+      g_small_kernels.store(value);
+      return TTT_OK;
     default: return TTT_ERR_ARG;
   }
 }
@@ -584,6 +593,7 @@ long long ttt_get_option(int option) {
   switch (option) {
     case TTT_OPT_MLP_BWD_POLL_LIMIT: return g_mlp_bwd_poll_limit.load();
     case TTT_OPT_MLP_BWD_FUSED: return g_mlp_bwd_fused.load();
+    case TTT_OPT_SMALL_KERNELS: return g_small_kernels.load();
     default: return -1;
   }
 }

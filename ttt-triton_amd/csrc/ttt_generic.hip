@@ -824,6 +824,7 @@ size_t gen_saved_bytes(int B, int H, int NC, int K, int F, int FF, bool mlp) {
 }
 
 hipError_t launch_gen_fwd(const GenFwdParams& q, int dtype, hipStream_t stream) {
+  if (small_shape_ok(q.K, q.F, q.FF, q.mlp) && !gen_force_general()) return launch_small_fwd(q, dtype, stream);
   GenArgs a{};
   a.XQ = q.XQ;
   a.XK = q.XK;
@@ -855,6 +856,7 @@ hipError_t launch_gen_fwd(const GenFwdParams& q, int dtype, hipStream_t stream) 
 }
 
 hipError_t launch_gen_bwd(const GenBwdParams& q, int dtype, hipStream_t stream) {
+  if (small_shape_ok(q.K, q.F, q.FF, q.mlp) && !gen_force_general()) return launch_small_bwd(q, dtype, stream);
   GenArgs a{};
   a.XQ = q.XQ;
   a.XK = q.XK;

@@ -245,5 +245,12 @@ bool gen_shape_ok(int K, int F, int FF, bool mlp);
 size_t gen_saved_bytes(int B, int H, int NC, int K, int F, int FF, bool mlp);
 hipError_t launch_gen_fwd(const GenFwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_gen_bwd(const GenBwdParams& p, int dtype, hipStream_t stream);
+// register-resident kernels (ttt_small.hip) for the general-shape set's small
+// heads: K = 16..64, F = 32 (and FF = 32), one wavefront per chain, same
+// interface and saved-buffer layout (only the states of GenLayout are used)
+bool small_shape_ok(int K, int F, int FF, bool mlp);
+bool gen_force_general();  // TTT_OPT_SMALL_KERNELS = 0: always the staged general-shape kernels
+hipError_t launch_small_fwd(const GenFwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_small_bwd(const GenBwdParams& p, int dtype, hipStream_t stream);
 
 }  // namespace ttt

@@ -26,6 +26,7 @@ ETA_RULES = {"dense": ETA_DENSE, "layer": ETA_LAYER, "causal": ETA_CAUSAL}
 # process-wide options (enum ttt_option)
 OPT_MLP_BWD_POLL_LIMIT = 1
 OPT_MLP_BWD_FUSED = 2
+OPT_SMALL_KERNELS = 3
 
 STATUS_TIMEOUT = -8
 STATUS_SCRATCH = -9
