@@ -566,9 +566,10 @@ def main():
             k = run_memo(torch, args.steps, args.warmup, only=args.only)
         elif args.only in ("forecaster", "forecaster_ref"):
             ref = args.only == "forecaster_ref"
-            tr, inf, _, _, _, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=32 if ref else FC_F,
-                                                 mini_batch=64 if ref else K)
-            k = {"train_step": tr, "inference": inf}
+            hd, mb = (32, 64) if ref else (FC_F, K)
+            tr, inf, _, _, _, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=hd, mini_batch=mb)
+            gtr, ginf, _ = run_forecaster_graph(torch, args.steps, args.warmup, head_dim=hd, mini_batch=mb)
+            k = {"train_step": tr, "inference": inf, "graph_train_step": gtr, "graph_inference": ginf}
         else:
             k = {"ttt_mlp_cached_readout": run_readout(torch, args.steps, args.warmup)}
         print(json.dumps({"only": args.only, "avg_us": {n: round(v * 1e6, 2) for n, v in k.items()}}), flush=True)
@@ -602,6 +603,7 @@ def main():
     fg_train, fg_inf, _ = run_forecaster_graph(torch, args.steps, args.warmup)
     print("[bench] forecaster at the reference ModelConfig shape (K=64, F=FF=32)", file=sys.stderr, flush=True)
     rc_train, rc_inf, _, _, rc_loss, _ = run_forecaster(torch, args.steps, args.warmup, head_dim=32, mini_batch=64)
+    rcg_train, rcg_inf, _ = run_forecaster_graph(torch, args.steps, args.warmup, head_dim=32, mini_batch=64)
 
     state = mlp_state_floats()
     kernels = {
@@ -681,9 +683,13 @@ def main():
             "forecaster_reference_model_shape": {
                 "train_step_ms": round(rc_train * 1e3, 3), "train_tokens_per_s": round(FC_B * FC_L / rc_train, 1),
                 "inference_ms": round(rc_inf * 1e3, 3), "inference_tokens_per_s": round(FC_B * FC_L / rc_inf, 1),
+                "graph_train_step_ms": round(rcg_train * 1e3, 3),
+                "graph_train_tokens_per_s": round(FC_B * FC_L / rcg_train, 1),
+                "graph_inference_ms": round(rcg_inf * 1e3, 3),
+                "graph_inference_tokens_per_s": round(FC_B * FC_L / rcg_inf, 1),
                 "loss": round(rc_loss, 5),
                 "shape": f"as c4 with ModelConfig's defaults of main.py: model_dim 128 over H={FC_H} heads (F=32, "
-                         f"FF=32), K=64 (the general-shape kernels), memo M={FC_M}, G={FC_G}"},
+                         f"FF=32), K=64 (the register-resident one-wave kernels), memo M={FC_M}, G={FC_G}"},
         },
         "memo_combine": {
             "value": round(B * T / (mk["ttt_mlp_memo_combine"] + mk["ttt_mlp_memo_combine_bwd"]), 1),
