@@ -14,12 +14,16 @@
  *     kernels (cached readout, memo combiner) take any K, F in {32, 64} and
  *     FF in {32, 64, 128, 256}.
  *   - Activations (XQ, XK, XV, out and their gradients) share one dtype,
- *     `dtype` (TTT_DTYPE_F32 or TTT_DTYPE_BF16).  Fast-weight state, LayerNorm
+ *     `dtype` (TTT_DTYPE_F32, TTT_DTYPE_BF16 or TTT_DTYPE_F16; both 16-bit
+ *     types are read into the matrix cores as they are and accumulate in fp32).  Fast-weight state, LayerNorm
  *     parameters, checkpoints, memo snapshots and weight gradients are fp32.
  *   - eta comes in one of two forms, chosen by `eta_rule` (enum ttt_eta_rule):
  *     TTT_ETA_DENSE: `eta` is the full [B,H,NC,K,K] tensor in the activation
  *     dtype, as ops/ttt_linear.py and ops/ttt_mlp.py take it, and the
  *     backward writes the dense [B,H,NC,K,K] gradient into `deta`;
+ *     TTT_ETA_DENSE_F32: the same dense eta and gradient in fp32 whatever
+ *     `dtype` is (the reference's kernels take eta in its own dtype; a 16-bit
+ *     deta overflows fp16 where the inputs are not normalised);
  *     TTT_ETA_LAYER / TTT_ETA_CAUSAL: `eta` is the per-token learning rate
  *     lr [B,H,NC,K] fp32 (TTTBase.get_eta, ttt_layer.py:151-163) that the
  *     kernels expand on chip (LAYER: eta[i][j] = lr[j]/K for every row i, the
@@ -46,9 +50,9 @@ extern "C" {
 
 #define TTT_AMD_ABI_VERSION 10
 
-enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1 };
+enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1, TTT_DTYPE_F16 = 2 };
 
-enum ttt_eta_rule { TTT_ETA_DENSE = 0, TTT_ETA_LAYER = 1, TTT_ETA_CAUSAL = 2 };
+enum ttt_eta_rule { TTT_ETA_DENSE = 0, TTT_ETA_LAYER = 1, TTT_ETA_CAUSAL = 2, TTT_ETA_DENSE_F32 = 3 };
 
 enum ttt_status {
   TTT_OK = 0,

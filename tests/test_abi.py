@@ -12,7 +12,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ttt_amd.h")
 
 OK, E_SHAPE, E_DTYPE, E_NULL, E_ALIGN, E_HIP, E_WS, E_ARG, E_TIMEOUT = 0, -1, -2, -3, -4, -5, -6, -7, -8
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 DENSE, LAYER, CAUSAL = 0, 1, 2
 P = 0x10000  # an aligned, never-dereferenced address
 Q = 0x10008  # misaligned
@@ -89,7 +89,8 @@ def test_linear_fwd_validation(lib):
     assert _lin_fwd(lib, G=0) == E_ARG
     assert _lin_fwd(lib, G=17) == E_ARG
     assert _lin_fwd(lib, eps=0.0) == E_ARG
-    assert _lin_fwd(lib, eta_rule=3) == E_ARG
+    assert _lin_fwd(lib, eta_rule=4) == E_ARG
+    assert _lin_fwd(lib, eta_rule=3, out=None) == E_NULL  # TTT_ETA_DENSE_F32 is a valid rule
     assert _lin_fwd(lib, eta_rule=-1) == E_ARG
     # a valid eta rule passes on to the next check (here: a missing output)
     assert _lin_fwd(lib, eta_rule=LAYER, out=None) == E_NULL
@@ -181,7 +182,7 @@ def test_mlp_saved_buffer(lib):
     args = [P] * 15 + [B, H, NC, K, F, FF, G, BF16, DENSE, 1e-8] + [P] * 10
     assert lib.ttt_mlp_bwd(*args, P, n16 - 1, P, w16, None) == E_WS
     bad = list(args)
-    bad[23] = 3  # eta_rule
+    bad[23] = 4  # eta_rule
     assert lib.ttt_mlp_bwd(*bad, P, n16, P, w16, None) == E_ARG
     assert lib.ttt_mlp_bwd(*args, None, n16, P, w16, None) == E_WS
     assert lib.ttt_mlp_bwd(*args, Q, n16, P, w16, None) == E_ALIGN
@@ -206,9 +207,22 @@ def test_readout_validation(lib):
     assert _readout(lib, NS=0) == E_SHAPE
     assert _readout(lib, S=0) == E_ARG
     assert _readout(lib, eps=-1.0) == E_ARG
-    assert _readout(lib, dtype=2) == E_DTYPE
+    assert _readout(lib, dtype=3) == E_DTYPE
     assert _readout(lib, W2=None) == E_NULL
     assert _readout(lib, out=Q) == E_ALIGN
+
+
+def test_fp16_sizes_match_bf16(lib):
+    """fp16 activations (TTT_DTYPE_F16) take the bf16 layouts: every
+    size helper returns the same byte count for both 16-bit types."""
+    for K, F, FF in ((16, 64, 256), (64, 32, 32), (32, 128, 256)):
+        assert lib.ttt_mlp_saved_bytes(2, 4, 8, K, F, FF, F16) == lib.ttt_mlp_saved_bytes(2, 4, 8, K, F, FF, BF16) > 0
+    assert lib.ttt_mlp_bwd_workspace_bytes(2, 4, 8, 16, 64, 256, F16) == \
+        lib.ttt_mlp_bwd_workspace_bytes(2, 4, 8, 16, 64, 256, BF16) > 0
+    assert lib.ttt_mlp_memo_workspace_bytes(2, 4, 8, 16, 64, 256, 2, F16) == \
+        lib.ttt_mlp_memo_workspace_bytes(2, 4, 8, 16, 64, 256, 2, BF16) > \
+        lib.ttt_mlp_memo_workspace_bytes(2, 4, 8, 16, 64, 256, 2, F32)
+    assert lib.ttt_mlp_saved_bytes(2, 4, 8, 16, 64, 256, 3) == 0
 
 
 def test_product_fails_loudly_without_a_gpu():

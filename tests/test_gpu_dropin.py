@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import fp32_bound, max_abs, rel_l2
+from tests._util import eta_own_dtype, fp32_bound, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -40,7 +40,7 @@ def _oracle(fn, d, names, dout_perm, dtype=torch.float64):
     return res
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("which", ["ops.ttt_linear", "TritonLinear", "ops.ttt_mlp", "TritonMLP"])
 def test_dropin_autograd(which, dt):
     import ops
@@ -49,7 +49,7 @@ def test_dropin_autograd(which, dt):
     _say(f"drop-in {which} {dt}")
     mlp = "mlp" in which.lower()
     B, H, NC, G = 2, 2, 5, 2
-    d = O.make_inputs(B, H, NC, 16, 64, FF=128 if mlp else 0, seed=40, dtype=dt, with_grad=True)
+    d = eta_own_dtype(O.make_inputs(B, H, NC, 16, 64, FF=128 if mlp else 0, seed=40, dtype=dt, with_grad=True), dt)
     names = MLP if mlp else LIN
     if which.startswith("ops"):
         dperm = d["dOut"].permute(0, 2, 3, 1, 4)

@@ -24,12 +24,12 @@ def _say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _inputs(B, H, NC, F_, FF, dt, rule, seed):
+def _inputs(B, H, NC, F_, FF, dt, rule, seed, K=16):
     """Inputs with lr = sigmoid(u)/F drawn as the oracle draws them, and the
     dense eta the oracle's make_eta builds from the same lr in fp32."""
-    d = O.make_inputs(B, H, NC, 16, F_, FF=FF, seed=seed, dtype=dt, with_grad=True, eta_kind=rule)
+    d = O.make_inputs(B, H, NC, K, F_, FF=FF, seed=seed, dtype=dt, with_grad=True, eta_kind=rule)
     gen = torch.Generator().manual_seed(seed + 1000)
-    u = torch.randn(B, H, NC, 16, generator=gen)
+    u = torch.randn(B, H, NC, K, generator=gen)
     d["lr"] = torch.sigmoid(u) / F_
     d["eta32"] = O.eta_from_lr(d["lr"], rule)  # fp32, from the same lr
     gen = torch.Generator().manual_seed(seed + 2000)
@@ -38,11 +38,11 @@ def _inputs(B, H, NC, F_, FF, dt, rule, seed):
     return d
 
 
-def _coef(rule):
-    i = torch.arange(16, dtype=torch.float64)
+def _coef(rule, K=16):
+    i = torch.arange(K, dtype=torch.float64)
     if rule == "layer":
-        return torch.full((16, 16), 1.0 / 16, dtype=torch.float64)
-    return torch.tril(torch.ones(16, 16, dtype=torch.float64)) / (i + 1)[:, None]
+        return torch.full((K, K), 1.0 / K, dtype=torch.float64)
+    return torch.tril(torch.ones(K, K, dtype=torch.float64)) / (i + 1)[:, None]
 
 
 def _oracle(kind, d, G, rule, dtype=torch.float64):
@@ -62,7 +62,8 @@ def _oracle(kind, d, G, rule, dtype=torch.float64):
 
 def _run(kind, d, G, rule, eta_key):
     """(out, grads) of the HIP path through the autograd Function, with eta
-    either dense (eta_key 'eta32' cast to the activation dtype) or lr."""
+    either dense (eta_key 'eta32' cast to the activation dtype, 'eta32_f32'
+    kept in fp32) or lr."""
     from ttt_amd.linear import TTTLinearFunction
     from ttt_amd.mlp import TTTMLPFunction
     g = to_dev(d)
@@ -72,6 +73,9 @@ def _run(kind, d, G, rule, eta_key):
     if eta_key == "lr":
         eta = g["lr"].clone().requires_grad_(True)
         extra = ("layer",) if rule == "layer" else ("causal",)
+    elif eta_key == "eta32_f32":
+        eta = g["eta32"].clone().requires_grad_(True)
+        extra = ("dense",)
     else:
         eta = g[eta_key].to(dt).clone().requires_grad_(True)
         extra = ("dense",)
@@ -107,9 +111,40 @@ def test_lr_fp32_bitwise_equals_dense(kind, rule):
     assert err <= 1e-6 * max(1.0, float(dlr_ref.abs().max()))
 
 
+# (kind, K, F, FF): the specialised kernels (K = 16, F = 64), the
+# register-resident ones (K = 64, F = FF = 32) and the staged general-shape
+# ones (K = 32, F = 128)
+DENSE_F32_SHAPES = [("linear", 16, 64, 0), ("mlp", 16, 64, 256), ("linear", 64, 32, 0), ("mlp", 64, 32, 32),
+                    ("linear", 32, 128, 0), ("mlp", 32, 128, 128)]
+
+
+@pytest.mark.parametrize("kind,K,F_,FF", DENSE_F32_SHAPES)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_lr_16bit_bitwise_equals_dense_fp32_eta(kind, K, F_, FF, dt):
+    """16-bit activations with a dense eta kept in fp32 (TTT_ETA_DENSE_F32):
+    the kernels read the same fp32 eta values the lr rule forms on chip, so
+    outputs and input gradients agree bit for bit with the lr path; deta
+    comes back in fp32 and its coefficient-weighted row sums are dlr."""
+    rule = "causal"
+    _say(f"{kind} K{K} F{F_} FF{FF} {dt}: lr vs dense fp32 eta")
+    B, H, NC = 2, 2, 5
+    d = _inputs(B, H, NC, F_, FF, dt, rule, seed=77, K=K)
+    out_l, g_l = _run(kind, d, 2, rule, "lr")
+    out_d, g_d = _run(kind, d, 2, rule, "eta32_f32")
+    assert out_d.dtype == dt and g_d["deta"].dtype == torch.float32
+    assert torch.equal(out_l, out_d)
+    for k in g_l:
+        if k != "deta":
+            assert torch.equal(g_l[k], g_d[k]), k
+    dlr_ref = (g_d["deta"].double().cpu() * _coef(rule, K)).sum(-2)
+    err = max_abs(g_l["deta"], dlr_ref)
+    _say(f"  dlr vs rows of dense deta: max-abs {err:.3e}")
+    assert err <= 1e-5 * max(1.0, float(dlr_ref.abs().max()))
+
+
 @pytest.mark.parametrize("kind", ["linear", "mlp"])
 @pytest.mark.parametrize("rule", ["layer", "causal"])
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 def test_lr_against_oracle(kind, rule, dt):
     """Outputs and every gradient, dlr included, against autograd of the
     oracle with lr as the leaf (eta = make_eta(lr))."""

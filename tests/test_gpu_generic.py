@@ -7,7 +7,7 @@ model configuration (ModelConfig defaults, main.py: K = 64, model dim 128 over
 
 Tolerances as for the specialised kernels: fp32 max-abs <= 1e-4, or 8 times
 the fp32 oracle's own error against fp64 where that is larger
-(tests/_util.fp32_bound); bf16 rel-L2 <= 2e-2."""
+(tests/_util.fp32_bound); bf16 and fp16 rel-L2 <= 2e-2."""
 
 import sys
 
@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import fp32_bound, max_abs, oracle_linear_grads, oracle_mlp_grads, rel_l2, to_dev
+from tests._util import eta_own_dtype, fp32_bound, max_abs, oracle_linear_grads, oracle_mlp_grads, rel_l2, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -71,6 +71,10 @@ MLP_CASES = [
     (1, 2, 3, 64, 64, 512, 2, 2, torch.float32, "layer"),
     (1, 1, 2, 16, 64, 1024, 1, 1, torch.bfloat16, "causal"),
     (1, 1, 2, 64, 256, 768, 1, 1, torch.float32, "causal"),
+    # fp16 activations: the reference's shape, a staged shape, a wide shape
+    (2, 4, 6, 64, 32, 32, 4, 2, torch.float16, "layer"),
+    (1, 2, 4, 64, 64, 256, 3, 3, torch.float16, "causal"),
+    (1, 1, 3, 32, 128, 256, 2, 1, torch.float16, "causal"),
 ]
 
 
@@ -96,8 +100,8 @@ def test_generic_mlp_forward(B, H, NC, K, F_, FF, G, M, dt, kind):
 def test_generic_mlp_backward(B, H, NC, K, F_, FF, G, M, dt, kind):
     from ttt_amd.mlp import mlp_backward, mlp_forward
     _say(f"generic mlp bwd B{B} H{H} NC{NC} K{K} F{F_} FF{FF} G{G} {dt} {kind}")
-    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=FF, seed=K + F_ + FF + 1, dtype=dt, eta_kind=kind,
-                               with_grad=True), H, F_, 8)
+    d = _perturb(eta_own_dtype(O.make_inputs(B, H, NC, K, F_, FF=FF, seed=K + F_ + FF + 1, dtype=dt, eta_kind=kind,
+                                             with_grad=True), dt), H, F_, 8)
     g = to_dev(d)
     out, ck, _, last, saved = mlp_forward(*(g[k] for k in MLP_KEYS), G, want_ckpt=True, want_last=True,
                                           want_saved=True)
@@ -120,6 +124,8 @@ LIN_CASES = [
     (1, 3, 4, 48, 32, 3, torch.float32, "causal"),
     (2, 2, 5, 32, 32, 2, torch.bfloat16, "layer"),
     (1, 1, 3, 16, 256, 1, torch.bfloat16, "layer"),
+    (2, 4, 6, 64, 32, 4, torch.float16, "layer"),
+    (1, 2, 3, 32, 128, 2, torch.float16, "causal"),
 ]
 
 
@@ -127,8 +133,8 @@ LIN_CASES = [
 def test_generic_linear_forward_backward(B, H, NC, K, F_, G, dt, kind):
     from ttt_amd.linear import linear_backward, linear_forward
     _say(f"generic linear B{B} H{H} NC{NC} K{K} F{F_} G{G} {dt} {kind}")
-    d = _perturb(O.make_inputs(B, H, NC, K, F_, seed=K + F_ + 3, dtype=dt, eta_kind=kind, with_grad=True), H, F_, 9,
-                 mlp=False)
+    d = _perturb(eta_own_dtype(O.make_inputs(B, H, NC, K, F_, seed=K + F_ + 3, dtype=dt, eta_kind=kind,
+                                             with_grad=True), dt), H, F_, 9, mlp=False)
     g = to_dev(d)
     out, ck, last, saved = linear_forward(*(g[k] for k in LIN_KEYS), G, want_ckpt=True, want_last=True,
                                           want_saved=True)
@@ -173,19 +179,20 @@ def test_generic_lr_rules_match_dense(kind):
     assert max_abs(res[kind][1][1][3], dlr_ref) <= 1e-4 * max(1.0, float(dlr_ref.abs().max()))
 
 
-@pytest.mark.parametrize("mlp,dt", [(True, torch.float32), (True, torch.bfloat16), (False, torch.float32)])
+@pytest.mark.parametrize("mlp,dt", [(True, torch.float32), (True, torch.bfloat16), (False, torch.float32),
+                                    (True, torch.float16), (False, torch.float16)])
 def test_small_kernels_match_the_staged_kernels(mlp, dt):
     """At the reference's model shape (K = 64, F = FF = 32) the register-
     resident kernels and the staged general-shape kernels (TTT_OPT_SMALL_KERNELS
     = 0) compute the same forward and gradients: fp32 to 2e-5 relative, bf16
-    within the bf16 bar (different operand roundings)."""
+    and fp16 within the 16-bit bar (different operand roundings)."""
     from ttt_amd import _lib
     from ttt_amd.linear import linear_backward, linear_forward
     from ttt_amd.mlp import mlp_backward, mlp_forward
     B, H, NC, K, F_, G = 2, 4, 5, 64, 32, 2
     _say(f"small vs staged {'mlp' if mlp else 'linear'} {dt}")
-    d = _perturb(O.make_inputs(B, H, NC, K, F_, FF=F_, seed=123, dtype=dt, eta_kind="causal", with_grad=True),
-                 H, F_, 11, mlp=mlp)
+    d = _perturb(eta_own_dtype(O.make_inputs(B, H, NC, K, F_, FF=F_, seed=123, dtype=dt, eta_kind="causal",
+                                             with_grad=True), dt), H, F_, 11, mlp=mlp)
     g = to_dev(d)
     res = []
     try:

@@ -2,10 +2,10 @@
 against the CPU oracle (oracle/ttt_layer_oracle.py, fp64).
 
 Tolerances: fp32 activations max-abs 1e-4 for the elementwise kernels (they
-compute in fp32; the observed error is ~1e-6); bf16 activations rel-L2 2e-2 (the required bar); the
+compute in fp32; the observed error is ~1e-6); bf16 and fp16 activations rel-L2 2e-2 (the required bar); the
 whole forecaster in fp32 rel-L2 per tensor within max(1e-4, C_FP32 times the
 fp32 oracle's own rel-L2 error against fp64) (a composition of four kernels,
-three GEMMs and the inner loop, each within fp32 rounding), in bf16
+three GEMMs and the inner loop, each within fp32 rounding), in bf16 and fp16
 rel-L2 2e-2 per tensor with the norm floor described at the test."""
 
 import sys
@@ -73,7 +73,7 @@ def _oracle_producer(proj, ln_w, ln_b, H, F_, base_lr, grads, dlr):
 # model widths H*F of 256 and less, 384 and 1024: the backward's per-lane
 # arrays come in one, two and four chunks of 256 features
 @pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 3), (64, 6), (64, 16)])
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 def test_producer_vs_oracle(F_, H, dt):
     from ttt_amd.layer_io import ProducerFunction, rope_table
     B, L, base_lr = 2, 64, 0.05
@@ -107,7 +107,7 @@ def test_producer_vs_oracle(F_, H, dt):
 
 
 @pytest.mark.parametrize("F_,H", [(64, 4), (32, 8), (64, 8), (64, 12)])
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 def test_post_norm_vs_oracle(F_, H, dt):
     from ttt_amd.layer_io import PostNormFunction
     B, L = 2, 48
@@ -152,7 +152,10 @@ def _forecaster(kind, B, L, H, F_, M, seed, K=16):
                                              ("ttt_linear", 0, torch.float32, 16, 64),
                                              ("ttt_mlp", 2, torch.float32, 64, 32),
                                              ("ttt_mlp", 2, torch.bfloat16, 64, 32),
-                                             ("ttt_linear", 0, torch.float32, 64, 32)])
+                                             ("ttt_linear", 0, torch.float32, 64, 32),
+                                             ("ttt_mlp", 2, torch.float16, 16, 64),
+                                             ("ttt_mlp", 2, torch.float16, 64, 32),
+                                             ("ttt_linear", 0, torch.float16, 64, 32)])
 def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
     """One training step of the end-to-end forecaster at batch 2: the loss and
     the gradient of every parameter against the oracle in fp64 on the same
@@ -160,7 +163,9 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
     512, horizon 96, 7 channels, H = 4 heads, memo segments of M = 2,
     checkpoint groups of 16); K = 64, F = 32 (model dim 128) is the
     reference's own ModelConfig / main.py shape, on the general-shape
-    kernels."""
+    kernels.  fp16 runs as mixed-precision training does: fp16 autocast and a
+    GradScaler (the loss scaled by 2^10, the gradients unscaled through
+    the scaler, which must find no overflow)."""
     B, L, H = 2, 512, 4
     _say(f"forecaster {kind} M{M} {dt} B{B} L{L} H{H} F{F_} K{K}")
     cfg, model, x, y = _forecaster(kind, B, L, H, F_, M, seed=91, K=K)
@@ -178,17 +183,25 @@ def test_forecaster_train_step_vs_oracle(kind, M, dt, K, F_):
         rtol32 = {k: rel_l2(sd32[k].grad, sd[k].grad) for k in sd if sd[k].grad is not None}
     dev = torch.device("cuda")
     model = model.to(dev)
-    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=dt == torch.bfloat16):
+    with torch.autocast("cuda", dtype=dt, enabled=dt != torch.float32):
         out = model(x.to(dev))
     loss = torch.nn.functional.mse_loss(out.float(), y.to(dev))
-    loss.backward()
+    if dt == torch.float16:
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
+        scaler.scale(loss).backward()
+        scaler.unscale_(opt)
+        found = sum(float(v) for v in scaler._found_inf_per_device(opt).values())
+        assert found == 0.0, "the scaled fp16 backward overflowed"
+    else:
+        loss.backward()
     torch.cuda.synchronize()
     tol = FP32_RTOL_E2E if dt == torch.float32 else BF16_RTOL
     err = abs(loss.item() - loss_ref.item()) / abs(loss_ref.item())
     _say(f"  loss {loss.item():.6f} vs {loss_ref.item():.6f}: rel {err:.3e}")
     bad = ["loss"] if err > tol else []
-    # every parameter gradient by rel-L2 against its own norm; in bf16 the
-    # tiny ones (TINY) have the looser bar BF16_RTOL_TINY
+    # every parameter gradient by rel-L2 against its own norm; in bf16 and
+    # fp16 the tiny ones (TINY) have the looser bar BF16_RTOL_TINY
     gmax = max(float(sd[n].grad.norm()) for n, _ in model.named_parameters() if sd[n].grad is not None)
     for name, prm in model.named_parameters():
         r = sd[name].grad

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import C_FP32, FP32_ATOL, fp32_bound, max_abs, oracle_linear_grads, rel_l2, to_dev
+from tests._util import C_FP32, FP32_ATOL, eta_own_dtype, fp32_bound, max_abs, oracle_linear_grads, rel_l2, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -120,13 +120,14 @@ def test_linear_fwd_f32_headdim32():
     assert max_abs(Wl, ref["W1_last"]) <= FP32_ATOL
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("kind", ["causal", "layer"])
-def test_linear_fwd_bf16(kind):
-    _say("linear fwd bf16", kind)
-    d = O.make_inputs(2, 3, 32, 16, 64, seed=1, dtype=torch.bfloat16, eta_kind=kind)
+def test_linear_fwd_16bit(kind, dt):
+    _say("linear fwd", dt, kind)
+    d = O.make_inputs(2, 3, 32, 16, 64, seed=1, dtype=dt, eta_kind=kind)
     out, (Wc, _), (Wl, bl) = _fwd(d, G=8)
     ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=8)
-    assert out.dtype == torch.bfloat16
+    assert out.dtype == dt
     assert rel_l2(out, ref["out"]) <= BF16_RTOL
     assert rel_l2(Wl, ref["W1_last"]) <= BF16_RTOL
     assert rel_l2(Wc, ref["W1_ckpt"]) <= BF16_RTOL
@@ -169,9 +170,10 @@ def test_linear_bwd_fp32(kind):
     assert not bad
 
 
-def test_linear_bwd_bf16():
-    _say("linear bwd bf16")
-    d = O.make_inputs(2, 3, 24, 16, 64, seed=6, dtype=torch.bfloat16, with_grad=True)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_linear_bwd_16bit(dt):
+    _say("linear bwd", dt)
+    d = eta_own_dtype(O.make_inputs(2, 3, 24, 16, 64, seed=6, dtype=dt, with_grad=True), dt)
     mine = _bwd(d, d["dOut"], G=8)
     ref = oracle_linear_grads(d, d["dOut"], G=0)
     bad = []

@@ -85,14 +85,15 @@ def test_memo_combine_fp32(B, H, NC, F_, FF, M):
     assert not bad
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("FF", [64, 256])
-def test_memo_combine_bf16(FF):
+def test_memo_combine_16bit(FF, dt):
     B, H, NC, F_, M = 2, 3, 40, 64, 2
-    _say(f"memo combine bf16 NC{NC} FF{FF} M{M}")
-    d = _inputs(B, H, NC, F_, FF, M, seed=7 + FF, dtype=torch.bfloat16)
+    _say(f"memo combine {dt} NC{NC} FF{FF} M{M}")
+    d = _inputs(B, H, NC, F_, FF, M, seed=7 + FF, dtype=dt)
     out, dxk, dxu, dxqw = _gpu(d, M)
     ref, rdxk, rdxu, rdxqw = _oracle(d, M)
-    assert out.dtype == torch.bfloat16 and dxu.dtype == torch.bfloat16 and dxk.dtype == torch.bfloat16
+    assert out.dtype == dt and dxu.dtype == dt and dxk.dtype == dt
     bad = []
     for name, a, b in (("out", out, ref), ("out - XQW", out.float().cpu() - d["XQW"].float(),
                                             ref - d["XQW"].double()),
@@ -150,9 +151,10 @@ def test_memo_combine_after_the_mlp_forward():
     assert err <= bound
 
 
-@pytest.mark.parametrize("F_,FF", [(64, 256), (32, 64)])
-def test_memo_packed_images_match_the_converting_path(monkeypatch, F_, FF):
-    """bf16: a workspace with room for the memo states' LDS images (written
+@pytest.mark.parametrize("F_,FF,dt", [(64, 256, torch.bfloat16), (32, 64, torch.bfloat16),
+                                     (64, 256, torch.float16)])
+def test_memo_packed_images_match_the_converting_path(monkeypatch, F_, FF, dt):
+    """16-bit activations: a workspace with room for the memo states' LDS images (written
     once by the forward, copied straight into LDS by both calls) gives bitwise
     the results of a gates-only workspace, where every workgroup converts each
     state it stages."""
@@ -160,8 +162,8 @@ def test_memo_packed_images_match_the_converting_path(monkeypatch, F_, FF):
     from ttt_amd.memo import memo_combine_backward, memo_combine_forward
     lib = _lib.load()
     M = 3
-    _say(f"memo packed vs converting F{F_} FF{FF}")
-    d = _inputs(2, 3, 13, F_, FF, M, seed=F_ + FF, dtype=torch.bfloat16)
+    _say(f"memo packed vs converting F{F_} FF{FF} {dt}")
+    d = _inputs(2, 3, 13, F_, FF, M, seed=F_ + FF, dtype=dt)
     g = {k: d[k].cuda() for k in KEYS}
     dout = d["dOut"].cuda()
 

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import ttt_oracle as O
-from tests._util import FP32_ATOL, fp32_bound, max_abs, oracle_mlp_grads, rel_l2, to_dev
+from tests._util import FP32_ATOL, eta_own_dtype, fp32_bound, max_abs, oracle_mlp_grads, rel_l2, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -58,10 +58,11 @@ def test_mlp_fwd_fp32(FF):
     assert not bad
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("kind", ["causal", "layer"])
-def test_mlp_fwd_bf16_ff256(kind):
-    _say("mlp fwd bf16 FF256", kind)
-    d = O.make_inputs(2, 3, 24, 16, 64, FF=256, seed=2, dtype=torch.bfloat16, eta_kind=kind)
+def test_mlp_fwd_16bit_ff256(kind, dt):
+    _say("mlp fwd FF256", dt, kind)
+    d = O.make_inputs(2, 3, 24, 16, 64, FF=256, seed=2, dtype=dt, eta_kind=kind)
     out, ck, memo, last, _ = _fwd(d, G=8, M=2)
     ref = O.mlp_forward_full(*(d[k].double() for k in KEYS), G=8, M=2)
     bad = []
@@ -83,7 +84,7 @@ def test_mlp_fwd_headdim32():
     assert max_abs(last[2], ref["W2_last"]) <= FP32_ATOL
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 def test_mlp_fwd_saved_buffer(dt):
     """Saving for the backward leaves every forward output unchanged; the saved
     bias decrements add up to the bias change over the sequence,
@@ -98,7 +99,7 @@ def test_mlp_fwd_saved_buffer(dt):
     assert torch.equal(out0, out1)
     for a, b in zip(ck0 + last0, ck1 + last1):
         assert torch.equal(a, b)
-    st = 2 if dt == torch.bfloat16 else 4
+    st = 4 if dt == torch.float32 else 2
     slot = (7 * FF + F_) * 16 * st + (FF + F_) * 4 + 3 * F_ * 64 + 4096
     assert saved.numel() == B * H * NC * slot
     u = saved.view(B * H, NC, slot)
@@ -116,7 +117,7 @@ def test_mlp_fwd_saved_buffer(dt):
         r = u[:, :, off:off + FF * 16 * st].contiguous().view(dt_).float()
         r = r.reshape(B * H, NC, FF // 64, 4, 4, 16, 4)      # [chain, s, w, o, g, n, j]
         return r.permute(0, 1, 4, 6, 2, 3, 5).reshape(B * H, NC, 16, FF)
-    dt_ = torch.bfloat16 if st == 2 else torch.float32
+    dt_ = dt
     g1e = hidden(0)
     g1 = hidden((FF + F_) * 16 * st + (FF + F_) * 4 + 2 * FF * 16 * st)
     e = g["eta"].reshape(B * H, NC, 16, 16)[:, :, 15, :].float()
@@ -150,9 +151,10 @@ def test_mlp_bwd_fp32(FF):
     assert not bad
 
 
-def test_mlp_bwd_bf16_ff256():
-    _say("mlp bwd bf16 FF256")
-    d = O.make_inputs(2, 2, 16, 16, 64, FF=256, seed=7, dtype=torch.bfloat16, with_grad=True)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_mlp_bwd_16bit_ff256(dt):
+    _say("mlp bwd FF256", dt)
+    d = eta_own_dtype(O.make_inputs(2, 2, 16, 16, 64, FF=256, seed=7, dtype=dt, with_grad=True), dt)
     mine = _bwd(d, G=8)
     ref = oracle_mlp_grads(d, d["dOut"], G=0)
     bad = []
@@ -170,11 +172,14 @@ def test_mlp_bwd_bf16_ff256():
     (6, 4, 32, 64, torch.float32),
     (1, 1, 64, 256, torch.bfloat16),
     (9, 4, 32, 128, torch.bfloat16),
+    (9, 4, 32, 128, torch.float16),
+    (5, 2, 64, 64, torch.float16),
 ])
 def test_mlp_bwd_edges(NC, G, F_, FF, dt):
     """single mini-batch, group sizes that do not divide NC, F = 32, FF = 64/128"""
     _say(f"mlp bwd NC{NC} G{G} F{F_} FF{FF} {dt}")
-    d = _perturb(O.make_inputs(1, 2, NC, 16, F_, FF=FF, seed=30 + NC, dtype=dt, with_grad=True), 2, F_, FF, 31)
+    d = _perturb(eta_own_dtype(O.make_inputs(1, 2, NC, 16, F_, FF=FF, seed=30 + NC, dtype=dt, with_grad=True), dt),
+                 2, F_, FF, 31)
     mine = _bwd(d, G=G)
     ref = oracle_mlp_grads(d, d["dOut"], G=0)
     ref32 = oracle_mlp_grads(d, d["dOut"], G=0, dtype=torch.float32) if dt == torch.float32 else None

@@ -56,10 +56,11 @@ def test_readout_fp32(B, H, NS, F_, FF):
     assert err <= bound
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("FF", [64, 256])
-def test_readout_bf16(FF):
-    _say(f"readout bf16 FF{FF}")
-    args = _inputs(2, 4, 5, 64, FF, seed=7, dtype=torch.bfloat16)
+def test_readout_16bit(FF, dt):
+    _say(f"readout {dt} FF{FF}")
+    args = _inputs(2, 4, 5, 64, FF, seed=7, dtype=dt)
     out = _gpu(args)
     ref = O.cached_readout(*(a.double() for a in args))
     x = args[0].double()

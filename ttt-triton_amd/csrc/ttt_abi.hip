@@ -10,12 +10,21 @@
 
 namespace {
 
+// activation dtypes the kernels take: fp32, bf16, fp16
+inline bool dtype_ok(int dtype) {
+  return dtype == TTT_DTYPE_F32 || dtype == TTT_DTYPE_BF16 || dtype == TTT_DTYPE_F16;
+}
+
 // process-wide options (ttt_set_option)
 std::atomic<long long> g_mlp_bwd_poll_limit{1LL << 22};
 std::atomic<long long> g_mlp_bwd_fused{1};
 std::atomic<long long> g_small_kernels{1};
 
-bool eta_rule_ok(int r) { return r == TTT_ETA_DENSE || r == TTT_ETA_LAYER || r == TTT_ETA_CAUSAL; }
+bool eta_rule_ok(int r) {
+  return r == TTT_ETA_DENSE || r == TTT_ETA_LAYER || r == TTT_ETA_CAUSAL || r == TTT_ETA_DENSE_F32;
+}
+// fp32 dense eta under fp32 activations is the plain dense form
+int eta_rule_of(int r, int dtype) { return r == TTT_ETA_DENSE_F32 && dtype == TTT_DTYPE_F32 ? TTT_ETA_DENSE : r; }
 
 // Scratch of ttt_mlp_bwd_noalloc: the backward's workspace (the reverse
 // sweep's per-mini-batch handoff and the dXQ/dXK workers' control words) in a
@@ -45,7 +54,7 @@ int scratch_of_current_device(void** out) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_common(int B, int H, int NC, int K, int F, int G, int dtype, float eps) {
-  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
+  if (!dtype_ok(dtype)) return TTT_ERR_DTYPE;
   if (B <= 0 || H <= 0 || NC <= 0) return TTT_ERR_SHAPE;
   if (K < 16 || K > 64 || K % 16 != 0) return TTT_ERR_SHAPE;
   if (F < 16 || F > 256 || F % 16 != 0) return TTT_ERR_SHAPE;
@@ -132,6 +141,7 @@ int ttt_linear_fwd(const void* XQ, const void* XK, const void* XV, const void* e
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
+  eta_rule = eta_rule_of(eta_rule, dtype);
   st = fast_linear_shape(K, F) ? check_linear(NC, F) : TTT_OK;
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
@@ -218,6 +228,7 @@ int ttt_linear_bwd(const void* XQ, const void* XK, const void* XV, const void* e
   int st = check_common(B, H, NC, K, F, G, dtype, eps);
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
+  eta_rule = eta_rule_of(eta_rule, dtype);
   st = fast_linear_shape(K, F) ? check_linear(NC, F) : TTT_OK;
   if (st != TTT_OK) return st;
   REQUIRE_PTR(XQ);
@@ -312,6 +323,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
   st = fast ? check_mlp(NC, F, FF, dtype) : TTT_OK;
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
+  eta_rule = eta_rule_of(eta_rule, dtype);
   REQUIRE_PTR(XQ);
   REQUIRE_PTR(XK);
   REQUIRE_PTR(XV);
@@ -420,7 +432,7 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
 
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
-  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
+  if (!dtype_ok(dtype)) return 0;
   if (fast_mlp_shape(K, F, FF)) return (size_t)B * H * NC * ttt::mlp_saved_slot_bytes(F, FF, dtype);
   if (ttt::gen_shape_ok(K, F, FF, true)) return ttt::gen_saved_bytes(B, H, NC, K, F, FF, true);
   return 0;
@@ -428,7 +440,7 @@ size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype
 
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype) {
   if (B <= 0 || H <= 0 || NC <= 0 || K <= 0 || F <= 0 || FF <= 0) return 0;
-  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return 0;
+  if (!dtype_ok(dtype)) return 0;
   if (fast_mlp_shape(K, F, FF))
     return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
   if (ttt::gen_shape_ok(K, F, FF, true)) return 256;  // (the general path keeps its scratch in `saved`)
@@ -449,6 +461,7 @@ static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const vo
   st = fast ? check_mlp(NC, F, FF, dtype) : TTT_OK;
   if (st != TTT_OK) return st;
   if (!eta_rule_ok(eta_rule)) return TTT_ERR_ARG;
+  eta_rule = eta_rule_of(eta_rule, dtype);
   (void)b1_ckpt;  // not read: the saved values carry the rest of the state
   (void)W2_ckpt;
   (void)b2_ckpt;
@@ -559,7 +572,7 @@ int ttt_mlp_bwd_noalloc(const void* XQ, const void* XK, const void* XV, const vo
                         float* db1, float* dW2, float* db2, float* dln_w, float* dln_b, const void* saved,
                         size_t saved_bytes, void* stream) {
   const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
-  if (need == 0) return dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16 ? TTT_ERR_DTYPE : TTT_ERR_SHAPE;
+  if (need == 0) return !dtype_ok(dtype) ? TTT_ERR_DTYPE : TTT_ERR_SHAPE;
   if (need > TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES) return TTT_ERR_SCRATCH;
   void* ws = nullptr;
   const int st = scratch_of_current_device(&ws);
@@ -665,8 +678,8 @@ size_t ttt_mlp_memo_gates_bytes(int B, int H, int NC, int K, int F, int M) {
 
 size_t ttt_mlp_memo_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int M, int dtype) {
   const size_t gb = ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M);
-  if (gb == 0 || !fixed_mlp_shape(F, FF) || (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16)) return 0;
-  if (dtype != TTT_DTYPE_BF16) return gb;
+  if (gb == 0 || !fixed_mlp_shape(F, FF) || !dtype_ok(dtype)) return 0;
+  if (dtype == TTT_DTYPE_F32) return gb;
   const size_t NS = (size_t)(NC + M - 1) / M;
   return ((gb + 255) & ~(size_t)255) + (size_t)B * H * NS * ttt::mlp_memo_image_bytes(F, FF);
 }
@@ -675,7 +688,7 @@ namespace {
 // the packed memo-state images behind the gates, when the workspace holds them
 unsigned char* memo_packed(float* gates, size_t gates_bytes, int B, int H, int NC, int K, int F, int FF, int M,
                            int dtype) {
-  if (dtype != TTT_DTYPE_BF16) return nullptr;
+  if (dtype == TTT_DTYPE_F32) return nullptr;
   const size_t need = ttt_mlp_memo_workspace_bytes(B, H, NC, K, F, FF, M, dtype);
   if (need == 0 || gates_bytes < need) return nullptr;
   return reinterpret_cast<unsigned char*>(gates) + ((ttt_mlp_memo_gates_bytes(B, H, NC, K, F, M) + 255) & ~(size_t)255);
@@ -765,7 +778,7 @@ int ttt_mlp_memo_combine_bwd(const void* XQ, const void* XU, const void* XQW, co
 
 namespace {
 int check_layer_io(int B, int L, int H, int K, int F, int dtype) {
-  if (dtype != TTT_DTYPE_F32 && dtype != TTT_DTYPE_BF16) return TTT_ERR_DTYPE;
+  if (!dtype_ok(dtype)) return TTT_ERR_DTYPE;
   if (B <= 0 || L <= 0 || H <= 0) return TTT_ERR_SHAPE;
   if (K < 16 || K > 64 || K % 16 != 0 || L % K != 0) return TTT_ERR_SHAPE;
   if (F != 32 && F != 64) return TTT_ERR_SHAPE;

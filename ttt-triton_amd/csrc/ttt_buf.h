@@ -38,6 +38,11 @@ template <> __device__ __forceinline__ Frag<__bf16> bload_frag<__bf16>(rsrc_t r,
   f.v = __builtin_bit_cast(bf4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
   return f;
 }
+template <> __device__ __forceinline__ Frag<_Float16> bload_frag<_Float16>(rsrc_t r, int voff, int soff) {
+  Frag<_Float16> f;
+  f.v = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  return f;
+}
 template <> __device__ __forceinline__ Frag<float> bload_frag<float>(rsrc_t r, int voff, int soff) {
   Frag<float> f;
   f.v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
@@ -46,6 +51,9 @@ template <> __device__ __forceinline__ Frag<float> bload_frag<float>(rsrc_t r, i
 
 template <typename T> __device__ __forceinline__ void bstore_frag(rsrc_t r, int voff, int soff, Frag<T> f);
 template <> __device__ __forceinline__ void bstore_frag<__bf16>(rsrc_t r, int voff, int soff, Frag<__bf16> f) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_frag<_Float16>(rsrc_t r, int voff, int soff, Frag<_Float16> f) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, 0);
 }
 template <> __device__ __forceinline__ void bstore_frag<float>(rsrc_t r, int voff, int soff, Frag<float> f) {
@@ -60,6 +68,9 @@ template <typename T> __device__ __forceinline__ void bstore_frag_dev(rsrc_t r, 
 template <> __device__ __forceinline__ void bstore_frag_dev<__bf16>(rsrc_t r, int voff, int soff, Frag<__bf16> f) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, kCpolDevice);
 }
+template <> __device__ __forceinline__ void bstore_frag_dev<_Float16>(rsrc_t r, int voff, int soff, Frag<_Float16> f) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, kCpolDevice);
+}
 template <> __device__ __forceinline__ void bstore_frag_dev<float>(rsrc_t r, int voff, int soff, Frag<float> f) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f.v), r, voff, soff, kCpolDevice);
 }
@@ -70,6 +81,11 @@ template <typename T> __device__ __forceinline__ Frag<T> bload_frag_dev(rsrc_t r
 template <> __device__ __forceinline__ Frag<__bf16> bload_frag_dev<__bf16>(rsrc_t r, int voff, int soff) {
   Frag<__bf16> f;
   f.v = __builtin_bit_cast(bf4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kCpolDevice));
+  return f;
+}
+template <> __device__ __forceinline__ Frag<_Float16> bload_frag_dev<_Float16>(rsrc_t r, int voff, int soff) {
+  Frag<_Float16> f;
+  f.v = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kCpolDevice));
   return f;
 }
 template <> __device__ __forceinline__ Frag<float> bload_frag_dev<float>(rsrc_t r, int voff, int soff) {
@@ -83,6 +99,10 @@ template <typename T> __device__ __forceinline__ float bload1(rsrc_t r, int voff
 template <> __device__ __forceinline__ float bload1<__bf16>(rsrc_t r, int voff, int soff) {
   const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
   return (float)__builtin_bit_cast(__bf16, u);
+}
+template <> __device__ __forceinline__ float bload1<_Float16>(rsrc_t r, int voff, int soff) {
+  const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  return (float)__builtin_bit_cast(_Float16, u);
 }
 template <> __device__ __forceinline__ float bload1<float>(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
@@ -122,6 +142,15 @@ template <> __device__ __forceinline__ Frag<__bf16> bload_ctile<__bf16>(rsrc_t r
   f.v = __builtin_bit_cast(bf4, u);
   return f;
 }
+template <> __device__ __forceinline__ Frag<_Float16> bload_ctile<_Float16>(rsrc_t r, int voff, int soff, int ld) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  us4 u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) u[j] = __builtin_amdgcn_raw_buffer_load_b16(r, voff + j * ld * 2, soff, 0);
+  Frag<_Float16> f;
+  f.v = __builtin_bit_cast(h4, u);
+  return f;
+}
 template <> __device__ __forceinline__ Frag<float> bload_ctile<float>(rsrc_t r, int voff, int soff, int ld) {
   Frag<float> f;
 #pragma unroll
@@ -130,6 +159,12 @@ template <> __device__ __forceinline__ Frag<float> bload_ctile<float>(rsrc_t r, 
 }
 template <typename T> __device__ __forceinline__ void bstore_ctile(rsrc_t r, int voff, int soff, int ld, Frag<T> f);
 template <> __device__ __forceinline__ void bstore_ctile<__bf16>(rsrc_t r, int voff, int soff, int ld, Frag<__bf16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 u = __builtin_bit_cast(us4, f.v);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(u[j], r, voff + j * ld * 2, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_ctile<_Float16>(rsrc_t r, int voff, int soff, int ld, Frag<_Float16> f) {
   typedef unsigned short us4 __attribute__((ext_vector_type(4)));
   const us4 u = __builtin_bit_cast(us4, f.v);
 #pragma unroll

@@ -322,6 +322,8 @@ __device__ void gen_step_fwd(const GenArgs& a, const GenLayout& L, float* sc, si
     const int r = i / K, c = i % K;
     if (a.eta_rule == TTT_ETA_DENSE) {
       eta[i] = ld(static_cast<const T*>(a.eta), (chain * a.NC + s) * K * K + i);
+    } else if (a.eta_rule == TTT_ETA_DENSE_F32) {
+      eta[i] = static_cast<const float*>(a.eta)[(chain * a.NC + s) * K * K + i];
     } else {
       const float lr = static_cast<const float*>(a.eta)[row0 + c];
       eta[i] = a.eta_rule == TTT_ETA_LAYER ? lr * (1.0f / (float)K) : (c <= r ? lr * (1.0f / (float)(r + 1)) : 0.0f);
@@ -784,6 +786,10 @@ __global__ __launch_bounds__(kGenThreads) __attribute__((amdgpu_waves_per_eu(1, 
       T* DE = static_cast<T*>(a.deta) + (chain * a.NC + s) * K * K;
       #pragma unroll 4
       for (int i = threadIdx.x; i < K * K; i += kGenThreads) DE[i] = (T)deta[i];
+    } else if (a.eta_rule == TTT_ETA_DENSE_F32) {
+      float* DE = static_cast<float*>(a.deta) + (chain * a.NC + s) * K * K;
+      #pragma unroll 4
+      for (int i = threadIdx.x; i < K * K; i += kGenThreads) DE[i] = deta[i];
     } else {
       float* DL = static_cast<float*>(a.deta) + row0;
       const bool layer = a.eta_rule == TTT_ETA_LAYER;
@@ -852,7 +858,9 @@ hipError_t launch_gen_fwd(const GenFwdParams& q, int dtype, hipStream_t stream) 
   a.eta_rule = q.eta_rule;
   a.mlp = q.mlp;
   a.eps = q.eps;
-  return dtype == TTT_DTYPE_BF16 ? launch_gen<__bf16>(a, false, stream) : launch_gen<float>(a, false, stream);
+  if (dtype == TTT_DTYPE_BF16) return launch_gen<__bf16>(a, false, stream);
+  if (dtype == TTT_DTYPE_F16) return launch_gen<_Float16>(a, false, stream);
+  return launch_gen<float>(a, false, stream);
 }
 
 hipError_t launch_gen_bwd(const GenBwdParams& q, int dtype, hipStream_t stream) {
@@ -887,7 +895,9 @@ hipError_t launch_gen_bwd(const GenBwdParams& q, int dtype, hipStream_t stream) 
   a.eta_rule = q.eta_rule;
   a.mlp = q.mlp;
   a.eps = q.eps;
-  return dtype == TTT_DTYPE_BF16 ? launch_gen<__bf16>(a, true, stream) : launch_gen<float>(a, true, stream);
+  if (dtype == TTT_DTYPE_BF16) return launch_gen<__bf16>(a, true, stream);
+  if (dtype == TTT_DTYPE_F16) return launch_gen<_Float16>(a, true, stream);
+  return launch_gen<float>(a, true, stream);
 }
 
 }  // namespace ttt

@@ -365,6 +365,9 @@ hipError_t launch_producer(const ProducerParams& p, int dtype, bool bwd, hipStre
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_producer_t<__bf16, 64>(p, bwd, stream);
     if (p.F == 32) return launch_producer_t<__bf16, 32>(p, bwd, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_producer_t<_Float16, 64>(p, bwd, stream);
+    if (p.F == 32) return launch_producer_t<_Float16, 32>(p, bwd, stream);
   } else {
     if (p.F == 64) return launch_producer_t<float, 64>(p, bwd, stream);
     if (p.F == 32) return launch_producer_t<float, 32>(p, bwd, stream);
@@ -392,6 +395,9 @@ hipError_t launch_post_norm(const PostNormParams& p, int dtype, bool bwd, hipStr
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_post_norm_t<__bf16, 64>(p, bwd, stream);
     if (p.F == 32) return launch_post_norm_t<__bf16, 32>(p, bwd, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_post_norm_t<_Float16, 64>(p, bwd, stream);
+    if (p.F == 32) return launch_post_norm_t<_Float16, 32>(p, bwd, stream);
   } else {
     if (p.F == 64) return launch_post_norm_t<float, 64>(p, bwd, stream);
     if (p.F == 32) return launch_post_norm_t<float, 32>(p, bwd, stream);

@@ -63,8 +63,10 @@ template <typename T, int FT> struct LinBwdShared {
 };
 
 template <typename T, int FT> struct LinBwdCtx {
-  const T *XQ, *XK, *XV, *DO, *ETA;
-  T *DXQ, *DXK, *DXV, *DETA;
+  const T *XQ, *XK, *XV, *DO;
+  T *DXQ, *DXK, *DXV;
+  const void* ETA;   // dense eta [NC][K][K] and its gradient, in the kernel's eta type
+  void* DETA;
   const float* LRP;  // lr [NC][K] when eta is given as learning rates
   float* DLR;        // dlr [NC][K] then
   int eta_rule;
@@ -73,7 +75,7 @@ template <typename T, int FT> struct LinBwdCtx {
 };
 
 // ------------------------------------------------------------------ wave P
-template <typename T, int FT, bool LR> struct WaveP {
+template <typename T, int FT, bool LR, typename ET> struct WaveP {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
   using Slot = LinSavedSlot<F>;
@@ -85,7 +87,8 @@ template <typename T, int FT, bool LR> struct WaveP {
   f4 aw[FT], ab[FT];  // readout-LN parameter gradient partials (features 16o + 4g + j, tokens of this lane)
   struct In {
     Frag<T> xq[1][FT], xk[1][FT], xv[FT], dof[FT];
-    Frag<T> etaT, e;  // raw: converted where used, so the prefetch is not waited for
+    Frag<ET> etaT, e;  // raw: converted where used, so the prefetch is not waited for
+    f4 etan;           // fp32 eta under 16-bit activations: eta[4g + j][n], read as it is
     f4 lr4;           // LR: lr[4g .. 4g+3] and lr[n], expanded where used
     float lrn;
     f4 G[FT], xhb[FT];
@@ -119,9 +122,13 @@ template <typename T, int FT, bool LR> struct WaveP {
       in.lr4 = *reinterpret_cast<const f4*>(c.LRP + (size_t)s * K + 4 * g);
       in.lrn = c.LRP[(size_t)s * K + n];
     } else {
-      const T* etas = c.ETA + (size_t)s * K * K;
+      const ET* etas = static_cast<const ET*>(c.ETA) + (size_t)s * K * K;
       in.etaT = load_frag(etas, K, 0);            // lane (g, n): eta[n][4g + j]
       in.e = load_frag(etas + (K - 1) * K, 0, 0);  // eta[K-1][4g + j]
+      if constexpr (sizeof(ET) != sizeof(T)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) in.etan[j] = etas[(4 * g + j) * K + n];
+      }
     }
     const float* sv = reinterpret_cast<const float*>(c.SV + (size_t)s * Slot::BYTES);
 #pragma unroll
@@ -174,7 +181,13 @@ template <typename T, int FT, bool LR> struct WaveP {
     gemm<1, 1, FT>(at, x.xk, x.xq);
     gemm<1, 1, FT>(a, x.xq, x.xk);
     // lane (g, n): eta[4g + j][n]
-    const f4 eta_n = LR ? eta_ctile_from_lr(c.eta_rule, x.lrn) : transpose16(x.etaT, I).v;
+    f4 eta_n;
+    if constexpr (LR)
+      eta_n = eta_ctile_from_lr(c.eta_rule, x.lrn);
+    else if constexpr (sizeof(ET) != sizeof(T))
+      eta_n = x.etan;  // (the identity product runs on T's matrix cores)
+    else
+      eta_n = transpose16(x.etaT, I).v;
     f4 m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) m[j] = eta_n[j] * a[0][0].v[j] + eta_n[j];
@@ -422,7 +435,7 @@ template <typename T, int FT> struct WaveS {
 };
 
 // ------------------------------------------------------------------ wave X
-template <typename T, int FT, bool LR> struct WaveX {
+template <typename T, int FT, bool LR, typename ET> struct WaveX {
   static constexpr int F = 16 * FT;
   static constexpr int K = 16;
   const LinearBwdParams& p;
@@ -505,12 +518,12 @@ template <typename T, int FT, bool LR> struct WaveX {
       // dlr of columns 4g..4g+3: the 16 lanes of group g store the same value
       *reinterpret_cast<f4*>(c.DLR + (size_t)s * K + 4 * g) = dlr_from_detaT(c.eta_rule, det);
     } else {
-      store_f4(c.DETA + (size_t)s * K * K, K, 0, det);
+      store_f4(static_cast<ET*>(c.DETA) + (size_t)s * K * K, K, 0, det);
     }
   }
 };
 
-template <typename T, int FT, bool LR>
+template <typename T, int FT, bool LR, typename ET = T>
 __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
@@ -527,14 +540,14 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   c.XK = static_cast<const T*>(p.XK) + xoff;
   c.XV = static_cast<const T*>(p.XV) + xoff;
   c.DO = static_cast<const T*>(p.dout) + xoff;
-  c.ETA = LR ? nullptr : static_cast<const T*>(p.eta) + eoff;
+  c.ETA = LR ? nullptr : static_cast<const ET*>(p.eta) + eoff;
   c.LRP = LR ? static_cast<const float*>(p.eta) + (size_t)c.chain * c.NC * K : nullptr;
   c.DLR = LR ? static_cast<float*>(p.deta) + (size_t)c.chain * c.NC * K : nullptr;
   c.eta_rule = p.eta_rule;
   c.DXQ = static_cast<T*>(p.dXQ) + xoff;
   c.DXK = static_cast<T*>(p.dXK) + xoff;
   c.DXV = static_cast<T*>(p.dXV) + xoff;
-  c.DETA = LR ? nullptr : static_cast<T*>(p.deta) + eoff;
+  c.DETA = LR ? nullptr : static_cast<ET*>(p.deta) + eoff;
   c.SV = static_cast<const char*>(p.saved) + (size_t)c.chain * c.NC * LinSavedSlot<F>::BYTES;
 
   // Every wave passes NC + 3 barriers: one per pipeline iteration, one before
@@ -544,7 +557,7 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int NC = c.NC;
   if (wave == 0) {
-    WaveP<T, FT, LR> w(p, c, sh);
+    WaveP<T, FT, LR, ET> w(p, c, sh);
     w.load(NC - 1);
     __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it < NC + 2; ++it) {
@@ -566,7 +579,7 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
     __syncthreads();
     w.finish(p);
   } else {
-    WaveX<T, FT, LR> w(p, c, sh);
+    WaveX<T, FT, LR, ET> w(p, c, sh);
     w.load_w(w.WT, p.W_last + (size_t)c.chain * F * F);
     __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it < NC + 2; ++it) {
@@ -582,6 +595,8 @@ template <typename T, int FT>
 static hipError_t launch_bwd(const LinearBwdParams& p, hipStream_t stream) {
   if (p.eta_rule == TTT_ETA_DENSE)
     hipLaunchKernelGGL((linear_bwd_kernel<T, FT, false>), dim3(p.B * p.H), dim3(192), 0, stream, p);
+  else if (p.eta_rule == TTT_ETA_DENSE_F32)
+    hipLaunchKernelGGL((linear_bwd_kernel<T, FT, false, float>), dim3(p.B * p.H), dim3(192), 0, stream, p);
   else
     hipLaunchKernelGGL((linear_bwd_kernel<T, FT, true>), dim3(p.B * p.H), dim3(192), 0, stream, p);
   return hipGetLastError();
@@ -591,6 +606,9 @@ hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t st
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_bwd<__bf16, 4>(p, stream);
     if (p.F == 32) return launch_bwd<__bf16, 2>(p, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_bwd<_Float16, 4>(p, stream);
+    if (p.F == 32) return launch_bwd<_Float16, 2>(p, stream);
   } else {
     if (p.F == 64) return launch_bwd<float, 4>(p, stream);
     if (p.F == 32) return launch_bwd<float, 2>(p, stream);

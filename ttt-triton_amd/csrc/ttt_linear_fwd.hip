@@ -40,7 +40,7 @@ template <typename T, int FT> struct LinFwdHandoff {
   float b[16 * FT];                         // b entering the mini-batch
 };
 
-template <typename T, int FT, bool LR>
+template <typename T, int FT, bool LR, typename ET = T>
 __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
@@ -53,11 +53,11 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
   const T* __restrict__ XQ = static_cast<const T*>(p.XQ) + (size_t)chain * NC * K * F;
   const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NC * K * F;
   const T* __restrict__ XV = static_cast<const T*>(p.XV) + (size_t)chain * NC * K * F;
-  // eta: dense [NC][K][K] blocks, or (LR) the learning rates lr [NC][K] fp32
-  // that the eta rule expands on chip; held raw until used
-  const T* __restrict__ ETA = LR ? nullptr : static_cast<const T*>(p.eta) + (size_t)chain * NC * K * K;
+  // eta: dense [NC][K][K] blocks of ET, or (LR) the learning rates lr [NC][K]
+  // fp32 that the eta rule expands on chip; held raw until used
+  const ET* __restrict__ ETA = LR ? nullptr : static_cast<const ET*>(p.eta) + (size_t)chain * NC * K * K;
   const float* __restrict__ LRP = LR ? static_cast<const float*>(p.eta) + (size_t)chain * NC * K : nullptr;
-  using ERaw = std::conditional_t<LR, f4, Frag<T>>;
+  using ERaw = std::conditional_t<LR, f4, Frag<ET>>;
   const int eta_rule = p.eta_rule;
   T* __restrict__ OUT = static_cast<T*>(p.out) + (size_t)chain * NC * K * F;
   using Slot = LinSavedSlot<F>;
@@ -369,6 +369,8 @@ template <typename T, int FT>
 static hipError_t launch_fwd(const LinearFwdParams& p, hipStream_t stream) {
   if (p.eta_rule == TTT_ETA_DENSE)
     hipLaunchKernelGGL((linear_fwd_kernel<T, FT, false>), dim3(p.B * p.H), dim3(128), 0, stream, p);
+  else if (p.eta_rule == TTT_ETA_DENSE_F32)
+    hipLaunchKernelGGL((linear_fwd_kernel<T, FT, false, float>), dim3(p.B * p.H), dim3(128), 0, stream, p);
   else
     hipLaunchKernelGGL((linear_fwd_kernel<T, FT, true>), dim3(p.B * p.H), dim3(128), 0, stream, p);
   return hipGetLastError();
@@ -378,6 +380,9 @@ hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t st
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_fwd<__bf16, 4>(p, stream);
     if (p.F == 32) return launch_fwd<__bf16, 2>(p, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_fwd<_Float16, 4>(p, stream);
+    if (p.F == 32) return launch_fwd<_Float16, 2>(p, stream);
   } else {
     if (p.F == 64) return launch_fwd<float, 4>(p, stream);
     if (p.F == 32) return launch_fwd<float, 2>(p, stream);

@@ -90,6 +90,10 @@ template <> __device__ __forceinline__ void lds_put_tfrag<__bf16>(unsigned base,
   const unsigned a = base + 2u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
   *(lds_u16*)(uintptr_t)a = __builtin_bit_cast(unsigned short, (__bf16)v);
 }
+template <> __device__ __forceinline__ void lds_put_tfrag<_Float16>(unsigned base, int c, int r, int q, float v) {
+  const unsigned a = base + 2u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
+  *(lds_u16*)(uintptr_t)a = __builtin_bit_cast(unsigned short, (_Float16)v);
+}
 template <> __device__ __forceinline__ void lds_put_tfrag<float>(unsigned base, int c, int r, int q, float v) {
   const unsigned a = base + 4u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
   *(lds_f32*)(uintptr_t)a = v;
@@ -98,12 +102,15 @@ template <typename T> __device__ __forceinline__ Frag<T> lds_get_tfrag(unsigned 
 template <> __device__ __forceinline__ Frag<__bf16> lds_get_tfrag<__bf16>(unsigned base, int c) {
   return Frag<__bf16>{*(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)(c * 64 + lane_id()))};
 }
+template <> __device__ __forceinline__ Frag<_Float16> lds_get_tfrag<_Float16>(unsigned base, int c) {
+  return Frag<_Float16>{__builtin_bit_cast(h4, *(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)(c * 64 + lane_id())))};
+}
 template <> __device__ __forceinline__ Frag<float> lds_get_tfrag<float>(unsigned base, int c) {
   return Frag<float>{*(lds_f4*)(uintptr_t)(base + 16u * (unsigned)(c * 64 + lane_id()))};
 }
 
 size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
-  const size_t t = dtype == TTT_DTYPE_BF16 ? 2 : 4;
+  const size_t t = dtype == TTT_DTYPE_F32 ? 4 : 2;
   return (size_t)2 * FF * 16 * t + (size_t)2 * F * 64;
 }
 
@@ -167,7 +174,7 @@ __device__ __forceinline__ void mlp_bwd_dx_worker(const MlpBwdParams& p) {
   }
 }
 
-template <typename T, int FT, int NW, int HT, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR, typename ET = T>
 __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   if constexpr (NW == FT) {
     if ((int)blockIdx.x >= p.B * p.H) {
@@ -180,6 +187,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   constexpr int FF = 16 * HT * NW;  // HT hidden tiles per wave
   constexpr float invF = 1.0f / F;
   constexpr int ST = (int)sizeof(T);
+  constexpr int SE = (int)sizeof(ET);  // dense eta element
   using Slot = MlpSavedSlot<F, FF, ST>;
   __shared__ MlpBwdShared<FT, NW, HT> sh;
 
@@ -193,7 +201,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
   const size_t eoff = (size_t)chain * NC * K * K;
-  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * ST);
+  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * SE);
   const rsrc_t rXQ = make_rsrc(static_cast<const T*>(p.XQ) + xoff, xbytes);
   const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
   const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
@@ -201,17 +209,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // eta and its gradient: dense [NC][K][K] blocks, or (LR) lr and dlr [NC][K] fp32
   const unsigned lbytes = (unsigned)(NC * K * 4);
   const rsrc_t rET = LR ? make_rsrc(static_cast<const float*>(p.eta) + (size_t)chain * NC * K, lbytes)
-                        : make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+                        : make_rsrc(static_cast<const ET*>(p.eta) + eoff, ebytes);
   const rsrc_t rDXV = make_rsrc(static_cast<T*>(p.dXV) + xoff, xbytes);
   const rsrc_t rDET = LR ? make_rsrc(static_cast<float*>(p.deta) + (size_t)chain * NC * K, lbytes)
-                         : make_rsrc(static_cast<T*>(p.deta) + eoff, ebytes);
+                         : make_rsrc(static_cast<ET*>(p.deta) + eoff, ebytes);
   const int eta_rule = p.eta_rule;
   const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
-  const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
-  const int en = (4 * g * K + n) * ST;        // eta[4g + j][n]: + j * K * ST
-  const int e4 = ((K - 1) * K + 4 * g) * ST;  // eta[K-1][4g .. 4g+3]
+  const int el = (n * K + 4 * g) * SE;        // frag lane offset in a [16 x 16] eta block
+  const int en = (4 * g * K + n) * SE;        // eta[4g + j][n]: + j * K * SE
+  const int e4 = ((K - 1) * K + 4 * g) * SE;  // eta[K-1][4g .. 4g+3]
   auto xs = [&](int s) { return s * K * F * ST; };
-  auto es = [&](int s) { return s * K * K * ST; };
+  auto es = [&](int s) { return s * K * K * SE; };
 
   // the forward's saved values of this chain, [NC] slots
   const rsrc_t rSV = make_rsrc(static_cast<const char*>(p.saved) + (size_t)chain * NC * Slot::BYTES,
@@ -377,15 +385,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       // wait for the load here)
       // dense: eta[n][4g+j] ([t_k x t_q]) and eta[4g+j][n] ([t_q x t_k]);
       // LR: lr[4g .. 4g+3] and lr[n]
-      Frag<T> etaT_r, etan_r;
+      Frag<ET> etaT_r, etan_r;
       f4 lr4;
       float lrn;
       if constexpr (LR) {
         lr4 = bload_frag<float>(rET, 16 * g, s * K * 4).v;
         lrn = bload_f32(rET, 4 * n, s * K * 4);
       } else {
-        etaT_r = bload_frag<T>(rET, el, es(s));
-        etan_r = bload_ctile<T>(rET, en, es(s), K);
+        etaT_r = bload_frag<ET>(rET, el, es(s));
+        etan_r = bload_ctile<ET>(rET, en, es(s), K);
       }
       // dout of this wave's feature tile for B3 (one tile per wave when NW >= FT)
       const Frag<T> dob = bload_frag<T>(rDO, xl + 16 * (wave % FT) * ST, xs(s));
@@ -476,12 +484,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         dlnw_l += aw;
         dlnb_l += ab;
         const unsigned lxb = (unsigned)(uintptr_t)(lds_f32*)sh.lx;
-        *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(lo * 64 + 16 * wave + n)) = to_frag<T>(dz).v;
+        *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(lo * 64 + 16 * wave + n)) = __builtin_bit_cast(bf4, to_frag<T>(dz).v);
         *(lds_f32*)(uintptr_t)(lxb + kRsLCol + 4u * (unsigned)(wave * 64 + n * 4 + lo)) = dz[0] + dz[1] + dz[2] + dz[3];
         __syncthreads();  // (L) the rows of dZ2b of every wave in
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          dz2bf[c].v = *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(c * 64 + l));
+          dz2bf[c].v = __builtin_bit_cast(typename FragT<T>::type, *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(c * 64 + l)));
           dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
         }
         f4 cs = f4{0.f, 0.f, 0.f, 0.f};  // column sums of features 16c + n
@@ -636,7 +644,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       //      dP = dG1 (.) gelu'(Z1) and dZ1 = dG1 (.) Pm gelu''(Z1) + dX2 (.) gelu'(Z1)
       //      (the dZ2 W2^T part of dX2 is added after the inner-loss backward)
       const f4 e = LR ? eta_lastrow_from_lr(bload_frag<float>(rET, 16 * g, s * K * 4).v)
-                      : frag_to_f4(bload_frag<T>(rET, e4, es(s)));
+                      : frag_to_f4(bload_frag<ET>(rET, e4, es(s)));
       Tile dZ1[HT];
       Frag<T> dPf[HT], dPF[HT];
       f4 dep = f4{0.f, 0.f, 0.f, 0.f};  // eta-row gradient partial (G1 . Q1 + G2 . Q2)
@@ -782,7 +790,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           const f4 dl = dlr_from_detaT(eta_rule, detT);
           bstore_frag<float>(rDET, keep_or_drop(16 * g, wave == 0 && n == 0), s * K * 4, Frag<float>{dl});
         } else {
-          bstore_frag<T>(rDET, keep_or_drop(el, wave == 0), es(s), to_frag<T>(detT));
+          bstore_frag<ET>(rDET, keep_or_drop(el, wave == 0), es(s), to_frag<ET>(detT));
         }
       }
       __syncthreads();  // (1x) exchange area free
@@ -1150,7 +1158,7 @@ static int device_cus() {
 // workers; otherwise the dXQ/dXK pass is a second launch.
 // The control words are cleared in both modes, so that the timeout word read
 // by ttt_mlp_bwd_check always belongs to this call.
-template <typename T, int FT, int NW, int HT, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR, typename ET = T>
 static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   const int chains = p.B * p.H, cus = device_cus();
   const bool fused = NW == FT && p.dx_fused != 0 && p.dx_ctrl != nullptr && cus >= chains + 16;
@@ -1160,7 +1168,7 @@ static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   if (e != hipSuccess) return e;
   if (!fused) {
     p.dx_ctrl = nullptr;
-    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR>), dim3(chains), dim3(64 * NW), 0, stream, p);
+    hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR, ET>), dim3(chains), dim3(64 * NW), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((mlp_bwd_dx_kernel<T, FT, NW, HT>), dim3(chains * p.NK), dim3(64 * FT), 0, stream, p);
@@ -1168,14 +1176,15 @@ static hipError_t launch_mlp_bwd_t(MlpBwdParams p, hipStream_t stream) {
   }
   // the sweeps, then one worker per CU: the first cus - chains run beside the
   // sweeps, the rest start on the CUs the sweeps leave
-  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
+  hipLaunchKernelGGL((mlp_bwd_kernel<T, FT, NW, HT, LR, ET>), dim3(chains + cus), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
 }
 
 template <typename T, int FT, int NW, int HT>
 static hipError_t launch_mlp_bwd_e(const MlpBwdParams& p, hipStream_t stream) {
-  return p.eta_rule == TTT_ETA_DENSE ? launch_mlp_bwd_t<T, FT, NW, HT, false>(p, stream)
-                                     : launch_mlp_bwd_t<T, FT, NW, HT, true>(p, stream);
+  if (p.eta_rule == TTT_ETA_DENSE) return launch_mlp_bwd_t<T, FT, NW, HT, false>(p, stream);
+  if (p.eta_rule == TTT_ETA_DENSE_F32) return launch_mlp_bwd_t<T, FT, NW, HT, false, float>(p, stream);
+  return launch_mlp_bwd_t<T, FT, NW, HT, true>(p, stream);
 }
 
 template <typename T, int FT>
@@ -1196,6 +1205,9 @@ hipError_t launch_mlp_bwd(const MlpBwdParams& p, int dtype, hipStream_t stream) 
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_mlp_bwd_f<__bf16, 4>(p, stream);
     if (p.F == 32) return launch_mlp_bwd_f<__bf16, 2>(p, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_mlp_bwd_f<_Float16, 4>(p, stream);
+    if (p.F == 32) return launch_mlp_bwd_f<_Float16, 2>(p, stream);
   } else {
     if (p.F == 64) return launch_mlp_bwd_f<float, 4>(p, stream);
     if (p.F == 32) return launch_mlp_bwd_f<float, 2>(p, stream);

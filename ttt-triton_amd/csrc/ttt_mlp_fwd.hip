@@ -42,7 +42,7 @@
 namespace ttt {
 
 size_t mlp_saved_slot_bytes(int F, int FF, int dtype) {
-  return mlp_saved_slot_bytes_of(F, FF, dtype == TTT_DTYPE_BF16 ? 2 : 4);
+  return mlp_saved_slot_bytes_of(F, FF, dtype == TTT_DTYPE_F32 ? 4 : 2);
 }
 
 template <int FT, int NW> struct MlpFwdShared {
@@ -62,12 +62,13 @@ template <int FT, int NW> struct MlpFwdShared {
 // the four partials of a row add up to Z2b and no wave forms all of it.
 template <int FT, int NW> constexpr bool kLnRowSplit = (NW == 4 && FT == 4);
 
-template <typename T, int FT, int NW, int HT, bool LR>
+template <typename T, int FT, int NW, int HT, bool LR, typename ET = T>
 __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
   constexpr int FF = 16 * HT * NW;  // HT hidden tiles per wave
   constexpr int ST = (int)sizeof(T);
+  constexpr int SE = (int)sizeof(ET);  // dense eta element
   using Slot = MlpSavedSlot<F, FF, ST>;
   __shared__ MlpFwdShared<FT, NW> sh;
 
@@ -81,17 +82,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   // per-chain slabs as buffer resources; lane offsets shared by all of them
   const size_t xoff = (size_t)chain * NC * K * F;
   const size_t eoff = (size_t)chain * NC * K * K;
-  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * ST);
+  const unsigned xbytes = (unsigned)((size_t)NC * K * F * ST), ebytes = (unsigned)((size_t)NC * K * K * SE);
   const rsrc_t rXQ = make_rsrc(static_cast<const T*>(p.XQ) + xoff, xbytes);
   const rsrc_t rXK = make_rsrc(static_cast<const T*>(p.XK) + xoff, xbytes);
   const rsrc_t rXV = make_rsrc(static_cast<const T*>(p.XV) + xoff, xbytes);
   const rsrc_t rET = LR ? make_rsrc(static_cast<const float*>(p.eta) + (size_t)chain * NC * K, NC * K * 4)
-                        : make_rsrc(static_cast<const T*>(p.eta) + eoff, ebytes);
+                        : make_rsrc(static_cast<const ET*>(p.eta) + eoff, ebytes);
   const int eta_rule = p.eta_rule;
   const rsrc_t rOUT = make_rsrc(static_cast<T*>(p.out) + xoff, xbytes);
   const int xl = (n * F + 4 * g) * ST;        // frag lane offset in a [16 x F] block
-  const int el = (n * K + 4 * g) * ST;        // frag lane offset in a [16 x 16] eta block
-  const int e4 = ((K - 1) * K + 4 * g) * ST;  // eta[K-1][4g .. 4g+3]
+  const int el = (n * K + 4 * g) * SE;        // frag lane offset in a [16 x 16] eta block
+  const int e4 = ((K - 1) * K + 4 * g) * SE;  // eta[K-1][4g .. 4g+3]
   const int w1l = ((4 * g) * FF + hs + n) * 4;  // [F][FF] tile lane offset, columns hs + ...
   const int w2l = ((hs + 4 * g) * F + n) * 4;   // [FF][F] tile lane offset, rows hs + ...
   const bool want_saved = p.saved != nullptr;
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt ? p.b1_ckpt + k * FF : nullptr,
                   p.W2_ckpt ? p.W2_ckpt + k * FF * F : nullptr, p.b2_ckpt ? p.b2_ckpt + k * F : nullptr);
     }
-    const int xo = s * K * F * ST, eo = s * K * K * ST;
+    const int xo = s * K * F * ST, eo = s * K * K * SE;
     const int us = s * Slot::BYTES;
     // the inner loss's target XV - XK: as frags (free = token), or, split by
     // rows, rows 4*wave+j of feature l (and XQ's for the output's residual)
@@ -195,13 +196,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       for (int q = 0; q < FT; ++q) xv[q] = bload_frag<T>(rXV, xl + 16 * q * ST, xo);
     }
     // dense: eta[n][4g+j] ([t_k x t_q]) and the last eta row; LR: lr[4g .. 4g+3]
-    Frag<T> etaTf, ef;
+    Frag<ET> etaTf, ef;
     f4 lr4;
     if constexpr (LR) {
       lr4 = bload_frag<float>(rET, 16 * g, s * K * 4).v;
     } else {
-      etaTf = bload_frag<T>(rET, el, eo);
-      ef = bload_frag<T>(rET, e4, eo);
+      etaTf = bload_frag<ET>(rET, el, eo);
+      ef = bload_frag<ET>(rET, e4, eo);
     }
 
     // ---- layer 1 on this wave's hidden units (token-major)
@@ -576,6 +577,8 @@ static hipError_t launch_mlp_fwd_t(const MlpFwdParams& p, hipStream_t stream) {
                 "saved slot layout");
   if (p.eta_rule == TTT_ETA_DENSE)
     hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, HT, false>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
+  else if (p.eta_rule == TTT_ETA_DENSE_F32)
+    hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, HT, false, float>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   else
     hipLaunchKernelGGL((mlp_fwd_kernel<T, FT, NW, HT, true>), dim3(p.B * p.H), dim3(64 * NW), 0, stream, p);
   return hipGetLastError();
@@ -599,6 +602,9 @@ hipError_t launch_mlp_fwd(const MlpFwdParams& p, int dtype, hipStream_t stream) 
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_mlp_fwd_f<__bf16, 4>(p, stream);
     if (p.F == 32) return launch_mlp_fwd_f<__bf16, 2>(p, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_mlp_fwd_f<_Float16, 4>(p, stream);
+    if (p.F == 32) return launch_mlp_fwd_f<_Float16, 2>(p, stream);
   } else {
     if (p.F == 64) return launch_mlp_fwd_f<float, 4>(p, stream);
     if (p.F == 32) return launch_mlp_fwd_f<float, 2>(p, stream);

@@ -701,6 +701,9 @@ hipError_t launch_mlp_memo(const MlpMemoParams& p, int dtype, bool bwd, hipStrea
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_memo_f<__bf16, 4>(p, bwd, stream);
     if (p.F == 32) return launch_memo_f<__bf16, 2>(p, bwd, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_memo_f<_Float16, 4>(p, bwd, stream);
+    if (p.F == 32) return launch_memo_f<_Float16, 2>(p, bwd, stream);
   } else {
     if (p.F == 64) return launch_memo_f<float, 4>(p, bwd, stream);
     if (p.F == 32) return launch_memo_f<float, 2>(p, bwd, stream);
@@ -726,5 +729,8 @@ size_t mlp_memo_image_bytes(int F, int FF) {
     default: return 0;
   }
 }
+// one image size for both 16-bit activation types
+static_assert(kMemoImg<_Float16, 4, 16> == kMemoImg<__bf16, 4, 16> && kMemoImg<_Float16, 2, 2> == kMemoImg<__bf16, 2, 2>,
+              "fp16 and bf16 memo images differ in size");
 
 }  // namespace ttt

@@ -156,6 +156,9 @@ hipError_t launch_mlp_readout(const MlpReadoutParams& p, int dtype, hipStream_t 
   if (dtype == TTT_DTYPE_BF16) {
     if (p.F == 64) return launch_readout_f<__bf16, 4>(p, stream);
     if (p.F == 32) return launch_readout_f<__bf16, 2>(p, stream);
+  } else if (dtype == TTT_DTYPE_F16) {
+    if (p.F == 64) return launch_readout_f<_Float16, 4>(p, stream);
+    if (p.F == 32) return launch_readout_f<_Float16, 2>(p, stream);
   } else {
     if (p.F == 64) return launch_readout_f<float, 4>(p, stream);
     if (p.F == 32) return launch_readout_f<float, 2>(p, stream);

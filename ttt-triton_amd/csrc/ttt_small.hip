@@ -132,6 +132,7 @@ template <typename T, int KT, int FT> struct SmallInputs {
   f4 e4[KT];                                 // last row eta[K-1][16i + 4g + jj] (row layout scale)
   float eT[KT];                              // eta[K-1][16i + n] (token layout scale)
   const T* E;                                // dense: this mini-batch's [K][K] block
+  const float* EF;                           // dense fp32 eta: the same block
   const float* lr;                           // lr form: this mini-batch's [K] rates
   int rule;
 
@@ -152,14 +153,25 @@ template <typename T, int KT, int FT> struct SmallInputs {
     rule = a.eta_rule;
     if (rule == TTT_ETA_DENSE) {
       E = static_cast<const T*>(a.eta) + row0 * K;
+      EF = nullptr;
       lr = nullptr;
 #pragma unroll
       for (int i = 0; i < KT; ++i) {
         e4[i] = load4(E + (size_t)(K - 1) * K + 16 * i + 4 * g);
         eT[i] = (float)E[(size_t)(K - 1) * K + 16 * i + n];
       }
+    } else if (rule == TTT_ETA_DENSE_F32) {
+      E = nullptr;
+      EF = static_cast<const float*>(a.eta) + row0 * K;
+      lr = nullptr;
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        e4[i] = load4(EF + (size_t)(K - 1) * K + 16 * i + 4 * g);
+        eT[i] = EF[(size_t)(K - 1) * K + 16 * i + n];
+      }
     } else {
       E = nullptr;
+      EF = nullptr;
       lr = static_cast<const float*>(a.eta) + row0;
       const float invK = 1.0f / (float)K;
 #pragma unroll
@@ -178,6 +190,11 @@ template <typename T, int KT, int FT> struct SmallInputs {
       for (int i = 0; i < KT; ++i)
 #pragma unroll
         for (int j = 0; j < KT; ++j) et[i][j] = frag_to_f4(load_frag(E + 16 * i * K, K, 16 * j));
+    } else if (rule == TTT_ETA_DENSE_F32) {
+#pragma unroll
+      for (int i = 0; i < KT; ++i)
+#pragma unroll
+        for (int j = 0; j < KT; ++j) et[i][j] = frag_to_f4(load_frag(EF + 16 * i * K, K, 16 * j));
     } else {
       const bool layer = rule == TTT_ETA_LAYER;
       const float invK = 1.0f / (float)K;
@@ -311,15 +328,20 @@ __device__ __forceinline__ void store_deta(const SmallArgs& a, size_t row0, cons
   f4 de_row[KT];  // de[16j + 4g + jj]
 #pragma unroll
   for (int j = 0; j < KT; ++j) de_row[j] = *reinterpret_cast<const f4*>(sde + 16 * j + 4 * g);
-  if (a.eta_rule == TTT_ETA_DENSE) {
+  if (a.eta_rule == TTT_ETA_DENSE || a.eta_rule == TTT_ETA_DENSE_F32) {
     T* DE = static_cast<T*>(a.deta) + row0 * K;
+    float* DEF = static_cast<float*>(a.deta) + row0 * K;
+    const bool f32 = a.eta_rule == TTT_ETA_DENSE_F32;
 #pragma unroll
     for (int i = 0; i < KT; ++i)
 #pragma unroll
       for (int j = 0; j < KT; ++j) {
         f4 v = detaT[j][i].v;
         if (i == KT - 1 && n == 15) v += de_row[j];
-        store_f4(DE + 16 * i * K, K, 16 * j, v);
+        if (f32)
+          store_f4(DEF + 16 * i * K, K, 16 * j, v);
+        else
+          store_f4(DE + 16 * i * K, K, 16 * j, v);
       }
   } else {
     float* DL = static_cast<float*>(a.deta) + row0;
@@ -1718,8 +1740,9 @@ hipError_t launch_small_fwd(const GenFwdParams& q, int dtype, hipStream_t stream
   a.eta_rule = q.eta_rule;
   a.eps = q.eps;
   const int BH = q.B * q.H;
-  return dtype == TTT_DTYPE_BF16 ? launch_t<__bf16>(a, BH, q.K, q.mlp, false, stream)
-                                 : launch_t<float>(a, BH, q.K, q.mlp, false, stream);
+  if (dtype == TTT_DTYPE_BF16) return launch_t<__bf16>(a, BH, q.K, q.mlp, false, stream);
+  if (dtype == TTT_DTYPE_F16) return launch_t<_Float16>(a, BH, q.K, q.mlp, false, stream);
+  return launch_t<float>(a, BH, q.K, q.mlp, false, stream);
 }
 
 hipError_t launch_small_bwd(const GenBwdParams& q, int dtype, hipStream_t stream) {
@@ -1746,8 +1769,9 @@ hipError_t launch_small_bwd(const GenBwdParams& q, int dtype, hipStream_t stream
   a.eta_rule = q.eta_rule;
   a.eps = q.eps;
   const int BH = q.B * q.H;
-  return dtype == TTT_DTYPE_BF16 ? launch_t<__bf16>(a, BH, q.K, q.mlp, true, stream)
-                                 : launch_t<float>(a, BH, q.K, q.mlp, true, stream);
+  if (dtype == TTT_DTYPE_BF16) return launch_t<__bf16>(a, BH, q.K, q.mlp, true, stream);
+  if (dtype == TTT_DTYPE_F16) return launch_t<_Float16>(a, BH, q.K, q.mlp, true, stream);
+  return launch_t<float>(a, BH, q.K, q.mlp, true, stream);
 }
 
 }  // namespace ttt

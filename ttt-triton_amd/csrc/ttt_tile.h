@@ -40,6 +40,9 @@ typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 struct Tile {
   f4 v;
@@ -48,6 +51,7 @@ struct Tile {
 template <typename T> struct FragT;
 template <> struct FragT<float> { typedef f4 type; };
 template <> struct FragT<__bf16> { typedef bf4 type; };
+template <> struct FragT<_Float16> { typedef h4 type; };
 
 template <typename T> struct Frag {
   typename FragT<T>::type v;
@@ -69,6 +73,22 @@ template <> __device__ __forceinline__ Frag<__bf16> to_frag<__bf16>(f4 x) {
   return f;
 }
 
+// fp32 -> fp16 with the value complete in fp32 registers first.  The empty asm
+// keeps the compiler from folding the arithmetic that produced x into the
+// conversion (v_fma_mixlo_f16 / v_fma_mixhi_f16 pairs): in the spilled
+// K = 64 Linear backward those fused forms gave wrong input gradients from the
+// second mini-batch on, while plain conversions (v_cvt_pk_f16_f32) of the same
+// values match the fp64 oracle.
+__device__ __forceinline__ h4 f16x4_of(f4 x) {
+  asm("" : "+v"(x));
+  return h4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+}
+template <> __device__ __forceinline__ Frag<_Float16> to_frag<_Float16>(f4 x) {
+  Frag<_Float16> f;
+  f.v = f16x4_of(x);
+  return f;
+}
+
 template <typename T> __device__ __forceinline__ f4 frag_to_f4(Frag<T> f) {
   return f4{(float)f.v[0], (float)f.v[1], (float)f.v[2], (float)f.v[3]};
 }
@@ -79,6 +99,13 @@ __device__ __forceinline__ Frag<__bf16> negate(Frag<__bf16> f) {
   const us4 m = {0x8000, 0x8000, 0x8000, 0x8000};
   Frag<__bf16> r;
   r.v = __builtin_bit_cast(bf4, __builtin_bit_cast(us4, f.v) ^ m);
+  return r;
+}
+__device__ __forceinline__ Frag<_Float16> negate(Frag<_Float16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 m = {0x8000, 0x8000, 0x8000, 0x8000};
+  Frag<_Float16> r;
+  r.v = __builtin_bit_cast(h4, __builtin_bit_cast(us4, f.v) ^ m);
   return r;
 }
 __device__ __forceinline__ Frag<float> negate(Frag<float> f) { return Frag<float>{-f.v}; }
@@ -98,6 +125,13 @@ __device__ __forceinline__ void mma16(f4& acc, Frag<__bf16> p, Frag<__bf16> q) {
   const bf8 b = __builtin_shufflevector(q.v, z, 0, 1, 2, 3, 4, 5, 6, 7);
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
+// fp16 the same way: only v_mfma_f32_16x16x32_f16, the upper k-half zero
+__device__ __forceinline__ void mma16(f4& acc, Frag<_Float16> p, Frag<_Float16> q) {
+  const h4 z = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+  const h8 a = __builtin_shufflevector(p.v, z, 0, 1, 2, 3, 4, 5, 6, 7);
+  const h8 b = __builtin_shufflevector(q.v, z, 0, 1, 2, 3, 4, 5, 6, 7);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+}
 __device__ __forceinline__ void mma16(f4& acc, Frag<float> p, Frag<float> q) {
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[0], q.v[0], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(p.v[1], q.v[1], acc, 0, 0, 0);
@@ -110,6 +144,12 @@ __device__ __forceinline__ void mma32(f4& acc, Frag<__bf16> p0, Frag<__bf16> p1,
   bf8 a = __builtin_shufflevector(p0.v, p1.v, 0, 1, 2, 3, 4, 5, 6, 7);
   bf8 b = __builtin_shufflevector(q0.v, q1.v, 0, 1, 2, 3, 4, 5, 6, 7);
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma32(f4& acc, Frag<_Float16> p0, Frag<_Float16> p1, Frag<_Float16> q0,
+                                      Frag<_Float16> q1) {
+  h8 a = __builtin_shufflevector(p0.v, p1.v, 0, 1, 2, 3, 4, 5, 6, 7);
+  h8 b = __builtin_shufflevector(q0.v, q1.v, 0, 1, 2, 3, 4, 5, 6, 7);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
 }
 __device__ __forceinline__ void mma32(f4& acc, Frag<float> p0, Frag<float> p1, Frag<float> q0, Frag<float> q1) {
   mma16(acc, p0, q0);
@@ -276,6 +316,13 @@ __device__ __forceinline__ Frag<__bf16> load_frag(const __bf16* __restrict__ x, 
   f.v = *reinterpret_cast<const bf4*>(x + r * ld + c0 + 4 * g);
   return f;
 }
+__device__ __forceinline__ Frag<_Float16> load_frag(const _Float16* __restrict__ x, int ld, int c0) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  Frag<_Float16> f;
+  f.v = *reinterpret_cast<const h4*>(x + r * ld + c0 + 4 * g);
+  return f;
+}
 __device__ __forceinline__ Frag<float> load_frag(const float* __restrict__ x, int ld, int c0) {
   const int l = lane_id();
   const int g = l >> 4, r = l & 15;
@@ -293,10 +340,17 @@ __device__ __forceinline__ f4 load4(const __bf16* __restrict__ p) {
   const bf4 v = *reinterpret_cast<const bf4*>(p);
   return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
+__device__ __forceinline__ f4 load4(const _Float16* __restrict__ p) {
+  const h4 v = *reinterpret_cast<const h4*>(p);
+  return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
 __device__ __forceinline__ f4 load4(const float* __restrict__ p) { return *reinterpret_cast<const f4*>(p); }
 // four consecutive values at p from fp32
 __device__ __forceinline__ void store4(__bf16* __restrict__ p, f4 v) {
   *reinterpret_cast<bf4*>(p) = to_frag<__bf16>(v).v;
+}
+__device__ __forceinline__ void store4(_Float16* __restrict__ p, f4 v) {
+  *reinterpret_cast<h4*>(p) = to_frag<_Float16>(v).v;
 }
 __device__ __forceinline__ void store4(float* __restrict__ p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
 
@@ -319,6 +373,15 @@ template <int N> __device__ __forceinline__ void load_n(const __bf16* __restrict
     for (int k = 0; k < 2; ++k) v[k] = (float)x[k];
   }
 }
+template <int N> __device__ __forceinline__ void load_n(const _Float16* __restrict__ p, float (&v)[N]) {
+  if constexpr (N == 4) {
+    const h4 x = *reinterpret_cast<const h4*>(p);
+    for (int k = 0; k < 4; ++k) v[k] = (float)x[k];
+  } else {
+    const h2 x = *reinterpret_cast<const h2*>(p);
+    for (int k = 0; k < 2; ++k) v[k] = (float)x[k];
+  }
+}
 template <int N> __device__ __forceinline__ void store_n(float* __restrict__ p, const float (&v)[N]) {
   if constexpr (N == 4) {
     *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
@@ -334,11 +397,25 @@ template <int N> __device__ __forceinline__ void store_n(__bf16* __restrict__ p,
   }
 }
 
+template <int N> __device__ __forceinline__ void store_n(_Float16* __restrict__ p, const float (&v)[N]) {
+  if constexpr (N == 4) {
+    *reinterpret_cast<h4*>(p) = f16x4_of(f4{v[0], v[1], v[2], v[3]});
+  } else {
+    const h4 h = f16x4_of(f4{v[0], v[1], 0.f, 0.f});
+    *reinterpret_cast<h2*>(p) = h2{h[0], h[1]};
+  }
+}
+
 // Store four values to X[r][c0 + 4g + j]
 __device__ __forceinline__ void store_f4(__bf16* __restrict__ x, int ld, int c0, f4 v) {
   const int l = lane_id();
   const int g = l >> 4, r = l & 15;
   *reinterpret_cast<bf4*>(x + r * ld + c0 + 4 * g) = to_frag<__bf16>(v).v;
+}
+__device__ __forceinline__ void store_f4(_Float16* __restrict__ x, int ld, int c0, f4 v) {
+  const int l = lane_id();
+  const int g = l >> 4, r = l & 15;
+  *reinterpret_cast<h4*>(x + r * ld + c0 + 4 * g) = to_frag<_Float16>(v).v;
 }
 __device__ __forceinline__ void store_f4(float* __restrict__ x, int ld, int c0, f4 v) {
   const int l = lane_id();

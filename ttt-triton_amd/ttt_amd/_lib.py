@@ -15,12 +15,14 @@ ABI_VERSION = 10
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 
 # eta forms (enum ttt_eta_rule): the dense [B,H,NC,K,K] tensor, or the per-token
 # learning rate lr [B,H,NC,K] fp32 expanded on chip by a rule
 ETA_DENSE = 0
 ETA_LAYER = 1
 ETA_CAUSAL = 2
+ETA_DENSE_F32 = 3  # dense eta kept in fp32 under 16-bit activations (chosen from eta's dtype)
 ETA_RULES = {"dense": ETA_DENSE, "layer": ETA_LAYER, "causal": ETA_CAUSAL}
 
 # process-wide options (enum ttt_option)

@@ -14,7 +14,7 @@ import math
 import torch
 
 from . import _lib
-from ._common import as_act, check_device, dtype_code, ptr, stream_of
+from ._common import as_act, check_device, dtype_code, eta_operand, ptr, stream_of
 
 LN_EPS = 1e-8  # ops/ttt_utils.py:4,21
 
@@ -58,7 +58,7 @@ def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_
     G = int(G)
     NK = math.ceil(NC / G)
     xq, xk, xv = (as_act(t, mp) for t in (XQ, XK, XV))
-    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else eta.detach().to(torch.float32).contiguous()
+    et, krule = eta_operand(eta, rule, mp)
     w1 = W1.detach().to(torch.float32).contiguous()
     bb = b1.detach().to(torch.float32).contiguous()
     lw = ln_w.detach().to(torch.float32).contiguous()
@@ -79,7 +79,7 @@ def linear_forward(ln_w, ln_b, W1, b1, XQ, XV, XK, eta, G: int, eps: float = LN_
     with torch.cuda.device(dev):
         st = lib.ttt_linear_fwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb),
-            B, H, NC, K, F, G, code, rule, float(eps), ptr(out),
+            B, H, NC, K, F, G, code, krule, float(eps), ptr(out),
             ptr(last[0]) if last else None, ptr(last[1]) if last else None,
             ptr(ck[0]) if ck else None, ptr(ck[1]) if ck else None,
             ptr(saved) if saved is not None else None, saved.numel() if saved is not None else 0,
@@ -93,7 +93,8 @@ def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, 
     """Run the backward kernel on what linear_forward(want_ckpt, want_last,
     want_saved) returned.  Returns fp32 (dln_w [H,F], dln_b [H,F],
     dW1 [B,H,F,F], db1 [B,H,1,F]) and (dXQ, dXV, dXK, deta) in XQ.dtype,
-    deta being dlr [B,H,NC,K] fp32 for an lr eta rule.  With sum_ln=False
+    deta being dlr [B,H,NC,K] fp32 for an lr eta rule, and fp32 for a dense
+    fp32 eta under 16-bit activations (read in fp32 too).  With sum_ln=False
     dln_w and dln_b are the per-chain partials [B,H,F]."""
     rule = _lib.eta_rule_code(eta_rule)
     B, H, NC, K, F = XQ.shape
@@ -101,7 +102,7 @@ def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, 
     mp = XQ.dtype
     code = dtype_code(mp)
     xq, xk, xv, do = (as_act(t, mp) for t in (XQ, XK, XV, dout))
-    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else eta.detach().to(torch.float32).contiguous()
+    et, krule = eta_operand(eta, rule, mp)
     lw = ln_w.detach().to(torch.float32).contiguous()
     lb = ln_b.detach().to(torch.float32).contiguous()
     dxq = torch.empty_like(xq)
@@ -116,7 +117,7 @@ def linear_backward(ln_w, ln_b, XQ, XV, XK, eta, W1_ckpt, W1_last, saved, dout, 
     with torch.cuda.device(dev):
         st = lib.ttt_linear_bwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(W1_ckpt), ptr(W1_last), ptr(do),
-            B, H, NC, K, F, int(G), code, rule, float(eps),
+            B, H, NC, K, F, int(G), code, krule, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW), ptr(db), ptr(dlw), ptr(dlb),
             ptr(saved), saved.numel(), stream_of(dev))
     _lib.check(st, "ttt_linear_bwd")

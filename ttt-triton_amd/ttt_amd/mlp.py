@@ -16,7 +16,7 @@ import os
 import torch
 
 from . import _lib
-from ._common import as_act, check_device, dtype_code, ptr, stream_of
+from ._common import as_act, check_device, dtype_code, eta_operand, ptr, stream_of
 
 LN_EPS = 1e-8  # ops/ttt_utils.py:4,21
 
@@ -76,7 +76,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     G = int(G)
     NK = math.ceil(NC / G)
     xq, xk, xv = (as_act(t, mp) for t in (XQ, XK, XV))
-    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else _f32(eta)
+    et, krule = eta_operand(eta, rule, mp)
     w1, bb1, w2, bb2, lw, lb = (_f32(t) for t in (W1, b1, W2, b2, ln_w, ln_b))
     out = torch.empty((B, H, NC, K, F), device=dev, dtype=mp)
 
@@ -100,7 +100,7 @@ def mlp_forward(ln_w, ln_b, W1, b1, W2, b2, XQ, XV, XK, eta, G: int, M: int = 0,
     with torch.cuda.device(dev):
         st = lib.ttt_mlp_fwd(
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb), ptr(w1), ptr(bb1), ptr(w2), ptr(bb2),
-            B, H, NC, K, F, FF, G, int(M) if M else 0, code, rule, float(eps), ptr(out),
+            B, H, NC, K, F, FF, G, int(M) if M else 0, code, krule, float(eps), ptr(out),
             *(tuple(ptr(t) for t in last) if last else none4),
             *(tuple(ptr(t) if t is not None else None for t in ck) if ck else none4),
             *(tuple(ptr(t) for t in memo) if memo else none4),
@@ -117,7 +117,8 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     call with the same G and eta form.  `workspace` (uint8, at least
     ttt_mlp_bwd_workspace_bytes) is allocated here when not given.  Returns
     fp32 (dln_w [H,F], dln_b [H,F], dW1, db1, dW2, db2) and (dXQ, dXV, dXK,
-    deta) in XQ.dtype, deta being dlr [B,H,NC,K] fp32 for an lr eta rule.
+    deta) in XQ.dtype, deta being dlr [B,H,NC,K] fp32 for an lr eta rule, and
+    fp32 for a dense fp32 eta under 16-bit activations (read in fp32 too).
     With check_timeout (default: TTT_AMD_CHECK set) the call waits for the
     launch and raises TTTError if a fused dXQ/dXK worker gave up waiting.
     With sum_ln=False dln_w and dln_b are the per-chain partials [B,H,F]."""
@@ -128,7 +129,7 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     mp = XQ.dtype
     code = dtype_code(mp)
     xq, xk, xv, do = (as_act(t, mp) for t in (XQ, XK, XV, dout))
-    et = as_act(eta, mp) if rule == _lib.ETA_DENSE else _f32(eta)
+    et, krule = eta_operand(eta, rule, mp)
     lw, lb = _f32(ln_w), _f32(ln_b)
     dxq, dxk, dxv = torch.empty_like(xq), torch.empty_like(xq), torch.empty_like(xq)
     deta = torch.empty_like(et)
@@ -144,7 +145,7 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
             ptr(xq), ptr(xk), ptr(xv), ptr(et), ptr(lw), ptr(lb),
             *(ptr(t) if t is not None else None for t in ckpt),
             *(ptr(t) for t in last), ptr(do),
-            B, H, NC, K, F, FF, int(G), code, rule, float(eps),
+            B, H, NC, K, F, FF, int(G), code, krule, float(eps),
             ptr(dxq), ptr(dxk), ptr(dxv), ptr(deta), ptr(dW1), ptr(db1), ptr(dW2), ptr(db2), ptr(dlw), ptr(dlb),
             ptr(saved), saved.numel(), ptr(ws), ws.numel(), stream_of(dev))
     _lib.check(st, "ttt_mlp_bwd")
