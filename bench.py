@@ -70,6 +70,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU time budget per config")
+    ap.add_argument("--cpu-compile", action="store_true",
+                    help="also time the headline CPU baseline (c3) with the oracle's mini-batch step under "
+                         "torch.compile, as the reference's ops path compiles its own (ops/ttt_mlp.py:9); "
+                         "compiling adds one to two minutes")
     ap.add_argument("--eta", choices=["lr", "dense"], default="dense")
     ap.add_argument("--only", choices=["mlp_fwd", "mlp_bwd", "linear_fwd", "linear_bwd", "readout", "memo_fwd",
                                        "memo_bwd", "forecaster", "forecaster_ref"])
@@ -185,7 +189,7 @@ def read_profile_line(path, key, kernel, conv=float):
 
 
 # ---------------------------------------------------------------- CPU baselines (the oracle)
-def cpu_baselines(budget_s, eta):
+def cpu_baselines(budget_s, eta, compiled=False):
     import torch
     from oracle import ttt_layer_oracle as LO
     from oracle import ttt_oracle as O
@@ -204,7 +208,7 @@ def cpu_baselines(budget_s, eta):
         med = statistics.median(times)
         return round(tokens / med, 1), len(times), med
 
-    def op_case(kind, Bn, H_, NC_, F_, FF_, G, grad):
+    def op_case(kind, Bn, H_, NC_, F_, FF_, G, grad, mini_batch=None):
         d = make_inputs(torch, Bn, H_, NC_, F_, FF_, seed=7, dtype=torch.float32, eta="dense")
         names = ["XK", "XQ", "XV", "eta", "ln_w", "ln_b", "W1", "b1"] + (["W2", "b2"] if FF_ else [])
         fn = O.ttt_mlp if FF_ else O.ttt_linear
@@ -212,11 +216,11 @@ def cpu_baselines(budget_s, eta):
         def once():
             if grad:
                 a = {n: d[n].float().requires_grad_(True) for n in names}
-                out = fn(*[a[n] for n in names], G)
+                out = fn(*[a[n] for n in names], G, mini_batch=mini_batch)
                 out.backward(d["dOut"].float().permute(0, 2, 3, 1, 4))
             else:
                 with torch.no_grad():
-                    fn(*[d[n].float() for n in names], G)
+                    fn(*[d[n].float() for n in names], G, mini_batch=mini_batch)
         return once
 
     res = {}
@@ -235,6 +239,22 @@ def cpu_baselines(budget_s, eta):
         v, n, med = timed(once, tokens)
         res[key] = {"value": v, "unit": "tokens/s", "cores": cores, "kind": "port",
                     "sample": f"oracle {sample}, median of {n} runs, {med:.3f} s each"}
+
+    if compiled:
+        # the same c3 sample with the mini-batch step compiled by inductor for
+        # the CPU; the first call (tracing and compiling forward and backward)
+        # is timed apart and excluded
+        print("[bench] CPU baseline c3 under torch.compile (compiling)", file=sys.stderr, flush=True)
+        once = op_case("mlp", 1, H, NC, F, FF, G_MLP, True, mini_batch=torch.compile(O.mlp_mini_batch))
+        t0 = time.perf_counter()
+        once()
+        compile_s = time.perf_counter() - t0
+        v, n, med = timed(once, T)
+        res["c3_compiled"] = {
+            "value": v, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"oracle ttt_mlp forward + autograd backward with its mini-batch step under torch.compile "
+                      f"(inductor, CPU), fp32, B=1 H=12 T=2048 F=64 FF=256 G=8 (1/16 of the batch), median of "
+                      f"{n} runs, {med:.3f} s each; first call with compilation {compile_s:.0f} s, excluded"}
 
     # the forecaster's training step (forward + backward) on 2 of the 32 windows
     print("[bench] CPU baseline c4", file=sys.stderr, flush=True)
@@ -623,7 +643,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baselines(args.cpu_seconds, eta)
+        cpu = cpu_baselines(args.cpu_seconds, eta, compiled=args.cpu_compile)
 
     c1_flops = mlp_fwd_flops(Bn=8)
     line = {
@@ -646,6 +666,7 @@ def main():
                    "activations": "bf16", "state": "fp32", "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": dict(cpu["c3"]) if cpu else None,
+        "cpu_baseline_compiled": dict(cpu["c3_compiled"]) if cpu and "c3_compiled" in cpu else None,
         "mfma_frac_fwd_bwd": round(3 * mlp_fwd_flops() / step_s / MFMA_PEAK_BF16, 4),
         "kernels": {n: {"avg_launch_us": r["algorithmic"]["avg_launch_us"], "bound": r["bound"],
                         "frac": r["frac"], "mfma_frac": r["algorithmic"]["mfma_frac"],

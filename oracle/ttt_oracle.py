@@ -216,24 +216,30 @@ def _permute_in(xs):
 
 
 def ttt_linear(XK, XQ, XV, eta, ttt_norm_weight, ttt_norm_bias, W1_init, b1_init,
-               checkpoint_group_size, eps: float = LN_EPS, return_state: bool = False):
-    """ops/ttt_linear.py:57-84.  Returns [B,NC,K,H,F] (and the final state if asked)."""
+               checkpoint_group_size, eps: float = LN_EPS, return_state: bool = False, mini_batch=None):
+    """ops/ttt_linear.py:57-84.  Returns [B,NC,K,H,F] (and the final state if asked).
+    `mini_batch` replaces linear_mini_batch (e.g. by its torch.compile'd form,
+    as ops/ttt_linear.py:8 compiles its own)."""
     init = {"W1_states": W1_init, "b1_states": b1_init,
             "ttt_norm_weight": ttt_norm_weight, "ttt_norm_bias": ttt_norm_bias}
     xs = _permute_in({"XK": XK, "XQ": XQ, "XV": XV, "eta": eta})
-    step = lambda p, x: linear_mini_batch(p, x, eps)  # noqa: E731
+    f = mini_batch or linear_mini_batch
+    step = lambda p, x: f(p, x, eps)  # noqa: E731
     carry, out = scan(step, init, xs, checkpoint_group_size)
     out = out.permute(1, 0, 3, 2, 4)
     return (out, carry) if return_state else out
 
 
 def ttt_mlp(XK, XQ, XV, eta, ttt_norm_weight, ttt_norm_bias, W1_init, b1_init, W2_init, b2_init,
-            checkpoint_group_size, eps: float = LN_EPS, return_state: bool = False):
-    """ops/ttt_mlp.py:70-99.  Returns [B,NC,K,H,F] (and the final state if asked)."""
+            checkpoint_group_size, eps: float = LN_EPS, return_state: bool = False, mini_batch=None):
+    """ops/ttt_mlp.py:70-99.  Returns [B,NC,K,H,F] (and the final state if asked).
+    `mini_batch` replaces mlp_mini_batch (e.g. by its torch.compile'd form, as
+    ops/ttt_mlp.py:9 compiles its own)."""
     init = {"W1_states": W1_init, "b1_states": b1_init, "W2_states": W2_init, "b2_states": b2_init,
             "ttt_norm_weight": ttt_norm_weight, "ttt_norm_bias": ttt_norm_bias}
     xs = _permute_in({"XK": XK, "XQ": XQ, "XV": XV, "eta": eta})
-    step = lambda p, x: mlp_mini_batch(p, x, eps)  # noqa: E731
+    f = mini_batch or mlp_mini_batch
+    step = lambda p, x: f(p, x, eps)  # noqa: E731
     carry, out = scan(step, init, xs, checkpoint_group_size)
     out = out.permute(1, 0, 3, 2, 4)
     return (out, carry) if return_state else out

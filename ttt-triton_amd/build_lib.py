@@ -1,9 +1,19 @@
 """Build libttt_amd.so (HIP kernels + C ABI) for gfx950 with hipcc.
 
-    python ttt-triton_amd/build_lib.py [-v]
+    python ttt-triton_amd/build_lib.py [-v] [--asan]
 
 Each .hip under csrc/ is compiled to an object in parallel, then linked into
-ttt_amd/libttt_amd.so next to the Python loader.  Always rebuilds."""
+ttt_amd/libttt_amd.so next to the Python loader.  Always rebuilds.
+
+--asan builds a checking copy instead, _build_asan/libttt_amd_asan.so, with
+AddressSanitizer on the host code only (the C ABI's validation, size helpers
+and launch set-up; device code is built as usual).  Load it with the ASan
+runtime preloaded, e.g. for the ABI tests on a machine without a GPU:
+
+    LD_PRELOAD=$(hipcc -print-file-name=libclang_rt.asan-x86_64.so) \
+    ASAN_OPTIONS=detect_leaks=0 TTT_AMD_LIB=ttt-triton_amd/_build_asan/libttt_amd_asan.so \
+    python -m pytest tests/test_abi.py -m "not gpu"
+"""
 
 from __future__ import annotations
 
@@ -39,9 +49,13 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+ASAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+ASAN_DIR = os.path.join(HERE, "_build_asan")
+
+
+def _compile(src: str, verbose: bool, asan: bool = False) -> str:
+    obj = os.path.join(ASAN_DIR if asan else BUILD_DIR, os.path.basename(src)[:-4] + ".o")
+    cmd = [HIPCC, *COMMON, *(ASAN if asan else []), "-c", src, "-o", obj]
     if verbose:
         cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,20 +68,23 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD_DIR, exist_ok=True)
+def build(verbose: bool = False, asan: bool = False) -> str:
+    out_dir = ASAN_DIR if asan else BUILD_DIR
+    lib = os.path.join(ASAN_DIR, "libttt_amd_asan.so") if asan else LIB
+    os.makedirs(out_dir, exist_ok=True)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+        objs = list(ex.map(lambda s: _compile(s, verbose, asan), srcs))
+    tmp = lib + ".tmp"
+    link = ["-Xarch_host", "-fsanitize=address", "-shared-libasan"] if asan else []
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link, "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, asan="--asan" in sys.argv)
     print(path)

@@ -10,7 +10,9 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libttt_amd.so")
+# TTT_AMD_LIB names another build of the same library (e.g. the host-ASan
+# checking build of build_lib.py --asan)
+LIB_PATH = os.environ.get("TTT_AMD_LIB") or os.path.join(_HERE, "libttt_amd.so")
 ABI_VERSION = 10
 
 DTYPE_F32 = 0
