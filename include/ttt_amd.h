@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define TTT_AMD_ABI_VERSION 10
+#define TTT_AMD_ABI_VERSION 11
 
 enum ttt_dtype { TTT_DTYPE_F32 = 0, TTT_DTYPE_BF16 = 1, TTT_DTYPE_F16 = 2 };
 

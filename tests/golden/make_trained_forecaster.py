@@ -1,5 +1,5 @@
 """Writes tests/golden/trained_forecaster_etth1.safetensors: the reference's
-trained forecaster (ttt_forecaster.pt, written by main.py:104 after 20 epochs
+trained forecaster (ttt_forecaster.pt, written by main.py:107 after 20 epochs
 on ETTh1) and eight validation windows of the series it was trained on.
 
 Run in a container that holds the reference at /root/reference:
@@ -7,7 +7,7 @@ Run in a container that holds the reference at /root/reference:
     python tests/golden/make_trained_forecaster.py
 
 The checkpoint is read with torch.load(weights_only=True) (plain tensors, no
-code).  The windows restate Dataset_ETT_hour (data_loader.py:43-95) for
+code).  The windows restate Dataset_ETT_hour (data_loader.py:43-99) for
 main.py's settings (features "S": the OT column alone; seq_len 384, label_len
 96, pred_len 96): a StandardScaler fitted on the first 12*30*24 rows (the
 training split), the validation split starting 384 rows before row 8640, and
@@ -28,8 +28,8 @@ REF = "/root/reference"
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "trained_forecaster_etth1.safetensors")
 
 SEQ_LEN, PRED_LEN = 384, 96
-TRAIN_END = 12 * 30 * 24               # data_loader.py:49 (border2s[0])
-VAL_BEGIN = TRAIN_END - SEQ_LEN        # border1s[1]
+TRAIN_END = 12 * 30 * 24               # data_loader.py:48 (border2s[0])
+VAL_BEGIN = TRAIN_END - SEQ_LEN        # border1s[1], data_loader.py:47
 VAL_END = TRAIN_END + 4 * 30 * 24      # border2s[1]
 N_WINDOWS = 8
 

@@ -13,7 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 # TTT_AMD_LIB names another build of the same library (e.g. the host-ASan
 # checking build of build_lib.py --asan)
 LIB_PATH = os.environ.get("TTT_AMD_LIB") or os.path.join(_HERE, "libttt_amd.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
