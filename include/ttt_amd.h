@@ -159,10 +159,14 @@ int ttt_mlp_fwd(const void* XQ, const void* XK, const void* XV, const void* eta,
  * mini-batch. */
 size_t ttt_mlp_saved_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
-/* Bytes of device workspace ttt_mlp_bwd needs: B*H*NC mini-batches x
+/* Bytes of device workspace ttt_mlp_bwd uses: B*H*NC mini-batches x
  * (2 * FF * K * sizeof(dtype) + 2 * F * 64), then (4 + B*H*NC) 4-byte control
- * words rounded up to 256 bytes (specialised kernels); 256 with the
- * general-shape kernels, which keep their scratch in `saved`. */
+ * words rounded up to 256 bytes (specialised kernels; all of it required);
+ * with F = FF = 32 and K <= 64 (the register-resident kernels) B*H*NC x
+ * 48 KB at K = 64 (less at smaller K), the handoff of their two-launch form,
+ * which they use when given that much and otherwise run in one launch with
+ * at least 256 bytes; 256 with the other general shapes, which keep their
+ * scratch in `saved`. */
 size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, int dtype);
 
 /* TTT-MLP backward: gradients of sum(out * dout) wrt every input (final
@@ -179,10 +183,12 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
  *   dln_w, dln_b     [B,H,F] fp32 per-chain partials; sum over B for [H,F]
  *   saved            the saved buffer written by that ttt_mlp_fwd call
  *                    (saved_bytes >= ttt_mlp_saved_bytes(...))
- *   workspace        >= ttt_mlp_bwd_workspace_bytes(...) bytes of scratch
- *                    (dZ1b, dZ1 and partial dXQ/dXK per mini-batch, handed
- *                    from the reverse sweep to the pass that forms dXQ/dXK,
- *                    and that pass's control words)
+ *   workspace        scratch of ttt_mlp_bwd_workspace_bytes(...) bytes (at
+ *                    least 256 outside the specialised kernels, above): dZ1b,
+ *                    dZ1 and partial dXQ/dXK per mini-batch, handed from the
+ *                    reverse sweep to the pass that forms dXQ/dXK, and that
+ *                    pass's control words; or the register-resident
+ *                    kernels' readout-path terms per mini-batch
  * When one chain's sweep fits per CU with CUs to spare (B*H + 16 <= CUs), the
  * dXQ/dXK pass runs in the sweep's launch on the spare CUs, each worker
  * waiting (bounded by TTT_OPT_MLP_BWD_POLL_LIMIT polls) for the checkpoint
@@ -368,7 +374,8 @@ long long ttt_get_option(int option);
  * dXQ/dXK worker gave up waiting for its checkpoint group (that group's dXQ
  * and dXK rows then hold NaN).  With workspace NULL (workspace_bytes is then
  * ignored) it reads the static scratch of ttt_mlp_bwd_noalloc on the current
- * device instead: the status of the last no-allocation call there.  No
+ * device instead: the status of the last no-allocation call there.  Shapes
+ * outside the specialised kernels have no fused workers: TTT_OK at once.  No
  * counterpart in the reference, whose backward has no cross-workgroup waits. */
 int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int H, int NC, int K, int F,
                       int FF, int dtype, void* stream);

@@ -443,9 +443,23 @@ size_t ttt_mlp_bwd_workspace_bytes(int B, int H, int NC, int K, int F, int FF, i
   if (!dtype_ok(dtype)) return 0;
   if (fast_mlp_shape(K, F, FF))
     return (size_t)B * H * NC * ttt::mlp_bwd_ws_slot_bytes(F, FF, dtype) + ttt::mlp_bwd_ctrl_bytes(B, H, NC, 1);
+  if (ttt::small_shape_ok(K, F, FF, true)) {
+    // the register-resident kernels' handoff (they also run with the minimum, in one launch)
+    const size_t hb = ttt::small_mlp_bwd_hand_bytes(B, H, NC, K);
+    return hb > 256 ? hb : 256;
+  }
   if (ttt::gen_shape_ok(K, F, FF, true)) return 256;  // (the general path keeps its scratch in `saved`)
   return 0;
 }
+
+namespace {
+// the least workspace the MLP backward runs with: the whole for the
+// specialised kernels, 256 bytes for the rest
+size_t mlp_bwd_min_workspace(int B, int H, int NC, int K, int F, int FF, int dtype) {
+  const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
+  return fast_mlp_shape(K, F, FF) || need == 0 ? need : 256;
+}
+}  // namespace
 
 static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const void* eta, const float* ln_w,
                 const float* ln_b, const float* W1_ckpt, const float* b1_ckpt, const float* W2_ckpt,
@@ -474,9 +488,11 @@ static int mlp_bwd_impl(const void* XQ, const void* XK, const void* XV, const vo
   if (saved_bytes < ttt_mlp_saved_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
   if (workspace == nullptr) return TTT_ERR_WORKSPACE;
   if (!aligned16(workspace)) return TTT_ERR_ALIGN;
-  if (workspace_bytes < ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
+  if (workspace_bytes < mlp_bwd_min_workspace(B, H, NC, K, F, FF, dtype)) return TTT_ERR_WORKSPACE;
   if (!fast) {
     ttt::GenBwdParams q{};
+    q.ws = workspace;
+    q.ws_bytes = workspace_bytes;
     q.XQ = XQ;
     q.XK = XK;
     q.XV = XV;
@@ -571,7 +587,9 @@ int ttt_mlp_bwd_noalloc(const void* XQ, const void* XK, const void* XV, const vo
                         int dtype, int eta_rule, float eps, void* dXQ, void* dXK, void* dXV, void* deta, float* dW1,
                         float* db1, float* dW2, float* db2, float* dln_w, float* dln_b, const void* saved,
                         size_t saved_bytes, void* stream) {
-  const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
+  // (the register-resident kernels take the two-launch form when their
+  // handoff fits the scratch, else the one-launch form)
+  const size_t need = mlp_bwd_min_workspace(B, H, NC, K, F, FF, dtype);
   if (need == 0) return !dtype_ok(dtype) ? TTT_ERR_DTYPE : TTT_ERR_SHAPE;
   if (need > TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES) return TTT_ERR_SCRATCH;
   void* ws = nullptr;
@@ -615,6 +633,7 @@ int ttt_mlp_bwd_check(const void* workspace, size_t workspace_bytes, int B, int 
                       int dtype, void* stream) {
   const size_t need = ttt_mlp_bwd_workspace_bytes(B, H, NC, K, F, FF, dtype);
   if (need == 0) return TTT_ERR_SHAPE;
+  if (!fast_mlp_shape(K, F, FF)) return TTT_OK;  // no fused workers, no timeout word
   if (workspace == nullptr) {  // the no-allocation entry point's scratch on the current device
     if (need > TTT_MLP_BWD_NOALLOC_SCRATCH_BYTES) return TTT_ERR_SCRATCH;
     void* ws = nullptr;

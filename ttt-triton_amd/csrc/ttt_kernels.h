@@ -237,6 +237,8 @@ struct GenBwdParams {
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   void* saved;  // written by the forward with the same shapes
+  void* ws;     // the backward's workspace (the register-resident MLP backward's handoff), may be null
+  size_t ws_bytes;
   int B, H, NC, K, F, FF, eta_rule;
   bool mlp;
   float eps;
@@ -249,6 +251,9 @@ hipError_t launch_gen_bwd(const GenBwdParams& p, int dtype, hipStream_t stream);
 // heads: K = 16..64, F = 32 (and FF = 32), one wavefront per chain, same
 // interface and saved-buffer layout (only the states of GenLayout are used)
 bool small_shape_ok(int K, int F, int FF, bool mlp);
+// workspace bytes of the register-resident MLP backward's two-launch form
+// (0 for K outside 16..64); a smaller workspace runs the one-launch form
+size_t small_mlp_bwd_hand_bytes(int B, int H, int NC, int K);
 bool gen_force_general();  // TTT_OPT_SMALL_KERNELS = 0: always the staged general-shape kernels
 hipError_t launch_small_fwd(const GenFwdParams& p, int dtype, hipStream_t stream);
 hipError_t launch_small_bwd(const GenBwdParams& p, int dtype, hipStream_t stream);

@@ -43,6 +43,7 @@ struct SmallArgs {
   void *dXQ, *dXK, *dXV, *deta;
   float *dW1, *db1, *dW2, *db2, *dln_w, *dln_b;
   float* saved;                     // per chain: GenLayout (the states entering each mini-batch first)
+  float* hand;                      // MLP backward in two launches: one MlpBwdHand slot per (chain, mini-batch)
   size_t per_chain, states, state;  // floats
   int H, NC, G, M, NK, NS, eta_rule;
   float eps;
@@ -363,6 +364,23 @@ __device__ __forceinline__ void store_deta(const SmallArgs& a, size_t row0, cons
   }
 }
 
+// deta's last row (or dlr) gains the update path's term de of column j: the
+// second launch of the two-launch MLP backward adds it to what the first
+// stored (dense: eta[K-1][j]; lr rules: dlr[j] with the last row's 1/K)
+template <typename T>
+__device__ __forceinline__ void add_deta_last_row(const SmallArgs& a, size_t row0, int K, int j, float de) {
+  if (a.eta_rule == TTT_ETA_DENSE) {
+    T* p = static_cast<T*>(a.deta) + (row0 + K - 1) * K + j;
+    float v = (float)*p + de;
+    asm("" : "+v"(v));  // (a plain conversion, as f16x4_of keeps them)
+    *p = (T)v;
+  } else if (a.eta_rule == TTT_ETA_DENSE_F32) {
+    static_cast<float*>(a.deta)[(row0 + K - 1) * K + j] += de;
+  } else {
+    static_cast<float*>(a.deta)[row0 + j] += de * (1.0f / (float)K);
+  }
+}
+
 // token-layout [FT][KT] tiles -> rows of a [K x F] activation block
 template <typename T, int KT, int FT>
 __device__ __forceinline__ void store_rows(void* base, size_t row0, const Tile (&xT)[FT][KT]) {
@@ -404,17 +422,62 @@ template <int KT, int FT, int HT, bool FULL> struct MlpPark {
   static constexpr int DETA = DXKT + (FULL ? TF : 0); // deta, tiles [t'][t]
   static constexpr int FLOATS = DETA + (FULL ? KK : 0);
 };
+// The readout-path launch of the two-launch backward parks only what its
+// phases read back (its update-path values are not formed, the normalised
+// Z2b rows stay in registers and its dG2, dX2 and dXK terms go straight to
+// the handoff): 56 KB at K = 64, so that two workgroups share a CU.
+template <int KT, int FT, int HT> struct MlpParkRO {
+  static constexpr int R = KT * HT * 256, TF = FT * KT * 256, KK = KT * KT * 256;
+  static constexpr int X2 = 0, G1 = X2 + R, G2T = G1 + R, X2BT = G2T + TF, DB1T = X2BT + R, DETA = DB1T + R;
+  static constexpr int FLOATS = DETA + KK;
+};
+
+// The MLP backward's handoff slot per (chain, mini-batch), floats, every set
+// in lane order (one 16-byte vector per lane and tile): the readout path's
+// terms of dG1 (row), dG2 (token), dX2 (row), dXK (token), of the state
+// gradients dW1, dW2 (C layout), of db1 (token sums), db2 (per lane) and of
+// the output LayerNorm parameters' gradients (per lane).
+template <int KT, int FT, int HT> struct MlpBwdHand {
+  static constexpr int R = KT * HT * 256, TF = FT * KT * 256, WW = FT * HT * 256;
+  static constexpr int DG1 = 0, DG2T = DG1 + R, DX2 = DG2T + TF, DXKT = DX2 + R, DW1 = DXKT + TF, DW2 = DW1 + WW;
+  static constexpr int DB1T = DW2 + WW, DB2C = DB1T + HT * 256, DLNW = DB2C + FT * 256, DLNB = DLNW + FT * 256;
+  static constexpr int FLOATS = DLNB + FT * 256;
+};
+template <int A, int B> __device__ __forceinline__ void hand_store(float* p, const Tile (&x)[A][B]) {
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b) *reinterpret_cast<f4*>(p + ((a * B + b) * 64 + lane_id()) * 4) = x[a][b].v;
+}
+template <int A, int B> __device__ __forceinline__ void hand_add(const float* p, Tile (&x)[A][B]) {
+#pragma unroll
+  for (int a = 0; a < A; ++a)
+#pragma unroll
+    for (int b = 0; b < B; ++b) x[a][b].v += *reinterpret_cast<const f4*>(p + ((a * B + b) * 64 + lane_id()) * 4);
+}
+template <int N> __device__ __forceinline__ void hand_store4(float* p, const f4 (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) *reinterpret_cast<f4*>(p + (i * 64 + lane_id()) * 4) = x[i];
+}
+template <int N> __device__ __forceinline__ void hand_load4(const float* p, f4 (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] = *reinterpret_cast<const f4*>(p + (i * 64 + lane_id()) * 4);
+}
 
 // One mini-batch's forward values from the state entering it; parks what
 // the caller's later phases need, returns the output rows (token layout) and
-// the two LayerNorms' 1/sigma per token tile.
-template <typename T, int KT, int FT, int HT, bool FULL>
+// the two LayerNorms' 1/sigma per token tile.  Without RO it stops after G1
+// (the inner loss's values only: no readout, rsb and outT left unset).
+// UPV parks the update path's values (gelu'(Z1), P1 gelu''(Z1), the
+// normalised Z2); XHB_OUT returns the normalised Z2b rows in outT instead of
+// the output rows and parks none.  P is the park layout.
+template <typename T, int KT, int FT, int HT, bool FULL, bool RO = true, typename P = MlpPark<KT, FT, HT, FULL>,
+          bool UPV = FULL, bool XHB_OUT = false>
 __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const Tile (&W1)[FT][HT],
                                          const Tile (&W2)[HT][FT], const float (&b1n)[HT], const f4 (&b1T)[HT],
                                          const f4 (&b2T)[FT], const f4 (&lw)[FT], const f4 (&lb)[FT], float eps,
                                          float* st, float* pk, float (&rs2)[KT], float (&rsb)[KT],
                                          Tile (&outT)[FT][KT]) {
-  using P = MlpPark<KT, FT, HT, FULL>;
   Frag<T> fW1t[HT][FT], fW2t[FT][HT], fW2[HT][FT];
   frags_t<T>(W1, fW1t);
   frags_t<T>(W2, fW2t);
@@ -440,7 +503,7 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           float y, dy, ddy;
-          if constexpr (FULL) {
+          if constexpr (UPV) {
             gelu_all(z1[i][o].v[jj], y, dy, ddy);
             z1[i][o].v[jj] = ddy;  // (z1 now holds gelu''(Z1))
           } else {
@@ -453,7 +516,7 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
     Tile x2T[HT][KT];
     tr(x2, x2T, st);
     frags_t<T>(x2T, fX2);
-    if constexpr (FULL) {
+    if constexpr (UPV) {
       park(pk + P::D1, d1);
       park(pk + P::PDD, z1);  // gelu''(Z1) for now; times P1 below
     }
@@ -485,7 +548,7 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
     }
     frags_t<T>(g2T, fG2);
     park(pk + P::G2T, g2T);
-    if constexpr (FULL) park(pk + P::XH2T, xh2T);
+    if constexpr (UPV) park(pk + P::XH2T, xh2T);
   }
   // P1 = G2 W2^T, G1 = P1 gelu'(Z1) (row layout)
   Frag<T> fG1t[HT][KT];
@@ -493,7 +556,7 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
     Tile p1[KT][HT];
     zero(p1);
     gemm<KT, HT, FT>(p1, fG2, fW2);
-    if constexpr (FULL) {
+    if constexpr (UPV) {
       Tile pdd[KT][HT];
       unpark(pk + P::PDD, pdd);
 #pragma unroll
@@ -509,6 +572,7 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
     park(pk + P::G1, p1);
     frags_t<T>(p1, fG1t);
   }
+  if constexpr (!RO) return;
   // A1 = XQ XK^T; Z1b = XQ W1 + b1 - (eta (A1 + 1)) G1 (token layout)
   f4 eta[KT][KT];
   in.eta(eta);
@@ -594,10 +658,13 @@ __device__ __forceinline__ void mlp_step(const SmallInputs<T, KT, FT>& in, const
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         xhbT[c][i].v = (z[c] - mu) * rsb[i];
-        outT[c][i].v = frag_to_f4(in.q[i][c]) + lw[c] * xhbT[c][i].v + lb[c];
+        if constexpr (XHB_OUT)
+          outT[c][i].v = xhbT[c][i].v;
+        else
+          outT[c][i].v = frag_to_f4(in.q[i][c]) + lw[c] * xhbT[c][i].v + lb[c];
       }
     }
-    if constexpr (FULL) park(pk + P::XHBT, xhbT);
+    if constexpr (FULL && !XHB_OUT) park(pk + P::XHBT, xhbT);
   }
 }
 
@@ -769,18 +836,33 @@ __global__ __launch_bounds__(64) void small_mlp_fwd_kernel(SmallArgs a) {
 // mini-batch after, in phases that each read their forward values back from
 // the park, where the gradients several phases add to also wait; see the
 // layout notes above MlpPark.
-template <typename T, int KT, int FT, int HT>
+//
+// MODE 0 runs every phase in one reverse sweep per chain.  The phases of the
+// readout path, (2)-(4), do not depend on the state gradient carried from
+// the later mini-batches, so with a handoff buffer the backward runs as two
+// launches: MODE 1, one wave per (chain, mini-batch) at once, runs (2)-(4),
+// stores dXQ and deta without the last row's update term, and leaves its
+// contributions to dG1, dG2, dX2, dXK, the state gradients and the LayerNorm
+// parameters' gradients in the handoff slot; MODE 2, the reverse sweep per
+// chain, runs (1) and (5)-(7), adds each mini-batch's slot after (1) and the
+// update term to deta's last row.
+template <typename T, int KT, int FT, int HT, int MODE = 0>
 __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
   constexpr int K = 16 * KT, F = 16 * FT, FF = 16 * HT;
-  using P = MlpPark<KT, FT, HT, true>;
+  constexpr bool RO = MODE != 2;  // the readout path's phases (2)-(4)
+  constexpr bool UP = MODE != 1;  // the update path's phases (1), (5)-(7) and the carried state gradient
+  using P = std::conditional_t<MODE == 1, MlpParkRO<KT, FT, HT>, MlpPark<KT, FT, HT, true>>;
+  using HS = MlpBwdHand<KT, FT, HT>;
   __shared__ __align__(16) float st[kStage];
   __shared__ __align__(16) float pk[P::FLOATS];
   __shared__ __align__(16) float sb1[FF];
   __shared__ __align__(16) float sdb1[FF];
   __shared__ __align__(16) float sde[K];
-  const size_t chain = blockIdx.x;
+  const size_t chain = MODE == 1 ? blockIdx.x / a.NC : blockIdx.x;
   const int h = (int)(chain % a.H), NC = a.NC;
   const int l = lane_id(), g = l >> 4, n = l & 15;
+  // MODE 1: this workgroup's one mini-batch
+  const int s_hi = MODE == 1 ? (int)(blockIdx.x % a.NC) : NC - 1, s_lo = MODE == 1 ? s_hi : 0;
   f4 lw[FT], lb[FT];
   load_ln<FT>(a, h, lw, lb);
   Tile cdW1[FT][HT], cdW2[HT][FT];
@@ -794,8 +876,9 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
   lds_order();
   const float* states = a.saved + chain * a.per_chain + a.states;
 
-  for (int s = NC - 1; s >= 0; --s) {
+  for (int s = s_hi; s >= s_lo; --s) {
     const float* S = states + (size_t)s * a.state;
+    float* hs = MODE == 0 ? nullptr : a.hand + ((size_t)chain * NC + s) * HS::FLOATS;
     Tile cW1[FT][HT], cW2[HT][FT];
     f4 b2T[FT];
     load_mlp_state<FT, HT>(S, S + F * FF, S + F * FF + FF, S + F * FF + FF + FF * F, cW1, cW2, sb1, b2T);
@@ -813,10 +896,9 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
     }
     lds_order();
     float rs2[KT], rsb[KT];
-    {
-      Tile outT[FT][KT];
-      mlp_step<T, KT, FT, HT, true>(in, cW1, cW2, b1n, b1T, b2T, lw, lb, a.eps, st, pk, rs2, rsb, outT);
-    }
+    Tile outT[FT][KT];  // (MODE 1: the normalised Z2b rows)
+    mlp_step<T, KT, FT, HT, true, RO, P, MODE != 1, MODE == 1>(in, cW1, cW2, b1n, b1T, b2T, lw, lb, a.eps, st, pk,
+                                                              rs2, rsb, outT);
     Frag<T> fW2[HT][FT], fW2t[FT][HT], fW1[FT][HT];
     frags_t<T>(cW2, fW2t);
     {
@@ -829,7 +911,7 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
     f4 db2c[FT];  // this mini-batch's db2 terms (token-layout form, per lane)
     Tile dg1[KT][HT];
     // ---- (1) through the update W' = W - X^T diag(e) G, b' = b - G^T e
-    {
+    if constexpr (UP) {
       Frag<T> fdW1t[HT][FT], fdW2t[FT][HT];
       frags_t<T>(cdW1, fdW1t);
       frags_t<T>(cdW2, fdW2t);
@@ -917,13 +999,29 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
       for (int i = 0; i < KT; ++i)
         if (g == 0) sde[16 * i + n] += deT[i];
       lds_order();
+    } else {
+      // the readout path alone: its terms start from zero
+      zero(dg1);
+      lds_order();
+      if (l < K) sde[l] = 0.f;
+      lds_order();
     }
+    f4 db1cT[HT];  // this mini-batch's db1 terms from the token layout
+    Frag<T> fXKt[FT][KT];
+    if constexpr (RO) {
     // ---- (2) output LayerNorm: out = XQ + ln_w xhb + ln_b; dXQ starts as dout
     Tile dz2bT[FT][KT], dxqT[FT][KT];
     {
       const T* DO = static_cast<const T*>(a.dout) + row0 * F;
       Tile xhbT[FT][KT];
-      unpark(pk + P::XHBT, xhbT);
+      if constexpr (MODE == 1) {
+#pragma unroll
+        for (int c = 0; c < FT; ++c)
+#pragma unroll
+          for (int i = 0; i < KT; ++i) xhbT[c][i] = outT[c][i];
+      } else {
+        unpark(pk + P::XHBT, xhbT);
+      }
 #pragma unroll
       for (int c = 0; c < FT; ++c) db2c[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1012,9 +1110,15 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
         Frag<T> fnC2t[KT][KT];
         frags_t<T>(c2R, fnC2t);
         Tile dg2T[FT][KT];
-        unpark(pk + P::DG2T, dg2T);
-        gemm<FT, KT, KT>(dg2T, fdz2bt, fnC2t);
-        park(pk + P::DG2T, dg2T);
+        if constexpr (MODE == 1) {
+          zero(dg2T);
+          gemm<FT, KT, KT>(dg2T, fdz2bt, fnC2t);
+          hand_store(hs + HS::DG2T, dg2T);
+        } else {
+          unpark(pk + P::DG2T, dg2T);
+          gemm<FT, KT, KT>(dg2T, fdz2bt, fnC2t);
+          park(pk + P::DG2T, dg2T);
+        }
       }
       // dx2b += dA2 X2 (token); dx2 += dA2^T X2b (row)
       {
@@ -1031,9 +1135,15 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
         Frag<T> fdA2t[KT][KT];
         frags_t<T>(dA2R, fdA2t);
         Tile dx2[KT][HT];
-        unpark(pk + P::DX2, dx2);
-        gemm<KT, HT, KT>(dx2, fdA2t, fX2bt);
-        park(pk + P::DX2, dx2);
+        if constexpr (MODE == 1) {
+          zero(dx2);
+          gemm<KT, HT, KT>(dx2, fdA2t, fX2bt);
+          hand_store(hs + HS::DX2, dx2);
+        } else {
+          unpark(pk + P::DX2, dx2);
+          gemm<KT, HT, KT>(dx2, fdA2t, fX2bt);
+          park(pk + P::DX2, dx2);
+        }
       }
       {
         Tile db1T[HT][KT];
@@ -1045,8 +1155,6 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
       }
     }
     // ---- (4) Z1b = XQ W1 + b1 - (eta (A1 + 1)) G1, A1 = XQ XK^T
-    f4 db1cT[HT];  // this mini-batch's db1 terms from the token layout
-    Frag<T> fXKt[FT][KT];
     {
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
@@ -1126,11 +1234,65 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
         tr(dA1, dA1R, st);
         frags_t<T>(dA1R, fdA1t);
         Tile dxkT[FT][KT];
-        unpark(pk + P::DXKT, dxkT);
-        gemm<FT, KT, KT>(dxkT, fXQt, fdA1t);
-        park(pk + P::DXKT, dxkT);
+        if constexpr (MODE == 1) {
+          zero(dxkT);
+          gemm<FT, KT, KT>(dxkT, fXQt, fdA1t);
+          hand_store(hs + HS::DXKT, dxkT);
+        } else {
+          unpark(pk + P::DXKT, dxkT);
+          gemm<FT, KT, KT>(dxkT, fXQt, fdA1t);
+          park(pk + P::DXKT, dxkT);
+        }
       }
     }
+    }  // RO
+    if constexpr (MODE == 1) {
+      // the handoff: this mini-batch's readout-path terms (dG2, dX2 and dXK
+      // went there from phases (3) and (4))
+      hand_store(hs + HS::DG1, dg1);
+      hand_store(hs + HS::DW1, cdW1);
+      hand_store(hs + HS::DW2, cdW2);
+      hand_store4(hs + HS::DB1T, db1cT);
+      hand_store4(hs + HS::DB2C, db2c);
+      hand_store4(hs + HS::DLNW, dlnw);
+      hand_store4(hs + HS::DLNB, dlnb);
+    } else if constexpr (MODE == 2) {
+      // the readout path's terms from the handoff, added after (1)
+      Tile t[FT][KT], r[KT][HT];
+      hand_add(hs + HS::DG1, dg1);
+      unpark(pk + P::DG2T, t);
+      hand_add(hs + HS::DG2T, t);
+      park(pk + P::DG2T, t);
+      unpark(pk + P::DXKT, t);
+      hand_add(hs + HS::DXKT, t);
+      park(pk + P::DXKT, t);
+      unpark(pk + P::DX2, r);
+      hand_add(hs + HS::DX2, r);
+      park(pk + P::DX2, r);
+      hand_add(hs + HS::DW1, cdW1);
+      hand_add(hs + HS::DW2, cdW2);
+      hand_load4(hs + HS::DB1T, db1cT);
+      hand_load4(hs + HS::DB2C, db2c);
+      f4 x[FT];
+      hand_load4(hs + HS::DLNW, x);
+#pragma unroll
+      for (int c = 0; c < FT; ++c) dlnw[c] += x[c];
+      hand_load4(hs + HS::DLNB, x);
+#pragma unroll
+      for (int c = 0; c < FT; ++c) dlnb[c] += x[c];
+      // XK's transposed operand frags (phase (4) forms them in MODE 0)
+      {
+        Tile xT[FT][KT], xR[KT][FT];
+        tiles_of<T>(in.k, xT);
+        tr(xT, xR, st);
+        frags_t<T>(xR, fXKt);
+      }
+      // the update term of deta's last row, which the readout launch left out
+      lds_order();
+      if (l < K) add_deta_last_row<T>(a, row0, K, l, sde[l]);
+      lds_order();
+    }
+    if constexpr (UP) {
     // ---- (5) G1 = P1 gelu'(Z1): dp = dg1 gelu'(Z1), dz1 = dg1 P1 gelu''(Z1)
     Tile dz1[KT][HT];
     {
@@ -1249,7 +1411,9 @@ __global__ __launch_bounds__(64) void small_mlp_bwd_kernel(SmallArgs a) {
     for (int o = 0; o < HT; ++o)
       if (n == 0) *reinterpret_cast<f4*>(sdb1 + 16 * o + 4 * g) += db1cT[o];
     lds_order();
+    }  // UP
   }
+  if constexpr (MODE == 1) return;
   // the initial state's gradient and the LayerNorm parameters' (per chain)
 #pragma unroll
   for (int i = 0; i < FT; ++i)
@@ -1673,8 +1837,17 @@ __global__ __launch_bounds__(64) void small_lin_bwd_kernel(SmallArgs a) {
 
 template <typename T, int KT> hipError_t launch_kt(const SmallArgs& a, int BH, bool mlp, bool bwd, hipStream_t s) {
   if (mlp) {
-    if (bwd) hipLaunchKernelGGL((small_mlp_bwd_kernel<T, KT, 2, 2>), dim3(BH), dim3(64), 0, s, a);
-    else hipLaunchKernelGGL((small_mlp_fwd_kernel<T, KT, 2, 2>), dim3(BH), dim3(64), 0, s, a);
+    if (bwd && a.hand != nullptr) {
+      // two launches: the readout path of every (chain, mini-batch) at once, then the sweeps
+      hipLaunchKernelGGL((small_mlp_bwd_kernel<T, KT, 2, 2, 1>), dim3(BH * a.NC), dim3(64), 0, s, a);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((small_mlp_bwd_kernel<T, KT, 2, 2, 2>), dim3(BH), dim3(64), 0, s, a);
+    } else if (bwd) {
+      hipLaunchKernelGGL((small_mlp_bwd_kernel<T, KT, 2, 2, 0>), dim3(BH), dim3(64), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((small_mlp_fwd_kernel<T, KT, 2, 2>), dim3(BH), dim3(64), 0, s, a);
+    }
   } else {
     if (bwd) hipLaunchKernelGGL((small_lin_bwd_kernel<T, KT, 2>), dim3(BH), dim3(64), 0, s, a);
     else hipLaunchKernelGGL((small_lin_fwd_kernel<T, KT, 2>), dim3(BH), dim3(64), 0, s, a);
@@ -1710,6 +1883,18 @@ SmallArgs small_args(int B, int H, int NC, int K, int F, int FF, bool mlp, float
 bool small_shape_ok(int K, int F, int FF, bool mlp) {
   if (K < 16 || K > 16 * kSmallMaxKT || K % 16) return false;
   return F == 32 && (!mlp || FF == 32);
+}
+
+size_t small_mlp_bwd_hand_bytes(int B, int H, int NC, int K) {
+  size_t per = 0;
+  switch (K) {
+    case 16: per = MlpBwdHand<1, 2, 2>::FLOATS; break;
+    case 32: per = MlpBwdHand<2, 2, 2>::FLOATS; break;
+    case 48: per = MlpBwdHand<3, 2, 2>::FLOATS; break;
+    case 64: per = MlpBwdHand<4, 2, 2>::FLOATS; break;
+    default: return 0;
+  }
+  return (size_t)B * H * NC * per * sizeof(float);
 }
 
 hipError_t launch_small_fwd(const GenFwdParams& q, int dtype, hipStream_t stream) {
@@ -1768,6 +1953,9 @@ hipError_t launch_small_bwd(const GenBwdParams& q, int dtype, hipStream_t stream
   a.M = 1;
   a.eta_rule = q.eta_rule;
   a.eps = q.eps;
+  // the two-launch MLP backward when the workspace holds its handoff
+  const size_t hand = q.mlp ? small_mlp_bwd_hand_bytes(q.B, q.H, q.NC, q.K) : 0;
+  a.hand = hand > 0 && q.ws != nullptr && q.ws_bytes >= hand ? static_cast<float*>(q.ws) : nullptr;
   const int BH = q.B * q.H;
   if (dtype == TTT_DTYPE_BF16) return launch_t<__bf16>(a, BH, q.K, q.mlp, true, stream);
   if (dtype == TTT_DTYPE_F16) return launch_t<_Float16>(a, BH, q.K, q.mlp, true, stream);
