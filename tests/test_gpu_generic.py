@@ -179,6 +179,37 @@ def test_generic_lr_rules_match_dense(kind):
     assert max_abs(res[kind][1][1][3], dlr_ref) <= 1e-4 * max(1.0, float(dlr_ref.abs().max()))
 
 
+@pytest.mark.parametrize("K", [64, 32])
+@pytest.mark.parametrize("dt,eta", [(torch.float32, "dense"), (torch.bfloat16, "dense"), (torch.float16, "dense"),
+                                    (torch.bfloat16, "layer"), (torch.float32, "causal")])
+def test_small_mlp_backward_one_launch_matches_two(K, dt, eta):
+    """The register-resident MLP backward with a minimal workspace (256
+    bytes: one launch, every phase in the sweep) against the two-launch form
+    (the readout path of every mini-batch first, then the sweeps), for the
+    dense eta in the activation dtype, in fp32 (fp16: DENSE_F32) and the lr
+    rules: the same gradients up to summation order (fp32 2e-5 relative,
+    16-bit within the 2e-2 bar)."""
+    from ttt_amd.mlp import mlp_backward, mlp_forward
+    B, H, NC, F_, G = 2, 3, 5, 32, 2
+    _say(f"small mlp bwd one vs two launches K{K} {dt} {eta}")
+    d = _perturb(eta_own_dtype(O.make_inputs(B, H, NC, K, F_, FF=F_, seed=K + 7, dtype=dt, eta_kind="causal",
+                                             with_grad=True), dt), H, F_, 13)
+    if eta != "dense":
+        gen = torch.Generator().manual_seed(K + 8)
+        d["eta"] = torch.sigmoid(torch.randn(B, H, NC, K, generator=gen)) / F_
+    g = to_dev(d)
+    out, ck, _, last, saved = mlp_forward(*(g[k] for k in MLP_KEYS), G, want_ckpt=True, want_last=True,
+                                          want_saved=True, eta_rule=eta)
+    args = (g["ln_w"], g["ln_b"], g["XQ"], g["XV"], g["XK"], g["eta"], ck, last, saved, g["dOut"], G)
+    two = mlp_backward(*args, eta_rule=eta)
+    one = mlp_backward(*args, eta_rule=eta, workspace=torch.empty(256, device="cuda", dtype=torch.uint8))
+    torch.cuda.synchronize()
+    bound = 2e-5 if dt == torch.float32 else BF16_RTOL
+    worst = max(rel_l2(a, b) for a, b in zip(one[0] + one[1], two[0] + two[1]))
+    _say(f"  worst rel-L2 {worst:.3e} (bound {bound:.0e})")
+    assert worst <= bound
+
+
 @pytest.mark.parametrize("mlp,dt", [(True, torch.float32), (True, torch.bfloat16), (False, torch.float32),
                                     (True, torch.float16), (False, torch.float16)])
 def test_small_kernels_match_the_staged_kernels(mlp, dt):

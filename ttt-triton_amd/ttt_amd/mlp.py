@@ -115,7 +115,9 @@ def mlp_backward(ln_w, ln_b, XQ, XV, XK, eta, ckpt, last, saved, dout, G: int, e
     """Run the backward kernel.  ckpt = (W1, b1, W2, b2) checkpoints, last =
     the final state and saved = the saved buffer, all from one mlp_forward
     call with the same G and eta form.  `workspace` (uint8, at least
-    ttt_mlp_bwd_workspace_bytes) is allocated here when not given.  Returns
+    ttt_mlp_bwd_workspace_bytes) is allocated here when not given; for the
+    register-resident shapes (F = FF = 32) one of at least 256 bytes runs
+    their one-launch backward instead of the two-launch one.  Returns
     fp32 (dln_w [H,F], dln_b [H,F], dW1, db1, dW2, db2) and (dXQ, dXV, dXK,
     deta) in XQ.dtype, deta being dlr [B,H,NC,K] fp32 for an lr eta rule, and
     fp32 for a dense fp32 eta under 16-bit activations (read in fp32 too).
