@@ -1,0 +1,180 @@
+"""LDS bank model of the MLP backward sweep's step (CPU).
+
+tests/lds_banks_dump.cpp prints the per-lane LDS address of every LDS access
+one step of one wave of mlp_bwd_kernel issues (bf16, F = 64, FF = 256, four
+waves), taking the shared matrices' and the 16-bit staging's addresses from
+csrc/ttt_lds_layout.h, the header the kernel builds them from.  The model
+(probed on gfx950 with SQ_LDS_BANK_CONFLICT, one pattern per dispatch):
+bank = dword address mod the bank count; 2- and 4-byte accesses in two
+passes (lanes 0-31, 32-63) over 32 banks, 8-byte ones in the same passes over
+64 banks, 16-byte ones in four passes of 16 lanes over 64 banks, a pass
+joining quads 0 and 3 of one 16-lane group with quads 1 and 2 of the next
+(lanes 0-3, 12-15, 20-27 are one pass); lanes of a pass that reach the same
+dword do not conflict, and a pass takes as many cycles as the most distinct
+dwords any one bank serves.  16-byte writes are served in eight passes of
+8 consecutive lanes over 32 banks.  Probed values the model reproduces: the
+replaced row-major layout's 16-byte rows and a block layout without the
+chunk permutation tau, 4 conflict cycles per read; the replaced lane-order
+dZ2 frag writes, 14 per write; 16-byte writes go in 8-lane passes over 32
+banks, so the tau layout's row writes take 8; the new layouts, 0.
+
+Checked: the layouts are bijections and the kernel's address pieces reach
+the elements they mean (the dump's --check); every pattern is conflict-free
+but the readout column-sum write (one 2-way store per step); the modelled
+conflict cycles per LDS instruction of a step are below 0.1; and the model
+gives the probed counts for the replaced layouts.
+"""
+
+import json
+import os
+import subprocess
+from collections import defaultdict
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "ttt-triton_amd", "csrc")
+SRC = os.path.join(ROOT, "tests", "lds_banks_dump.cpp")
+
+# patterns allowed to conflict, with their modelled degree
+EXPECTED_CONFLICTS = {"readout column sum write (L)": 2}
+
+
+def passes(width, store=False):
+    """Lane sets of the passes of one LDS instruction."""
+    if width == 16 and store:
+        return [list(range(8 * p, 8 * p + 8)) for p in range(8)]
+    if width == 16:
+        out = [[] for _ in range(4)]
+        for l in range(64):
+            q, grp = (l >> 2) & 3, l >> 4
+            out[2 * (l >> 5) + ((bin(q).count("1") & 1) ^ (grp & 1))].append(l)
+        return out
+    return [list(range(32)), list(range(32, 64))]
+
+
+def pass_cycles(width, addrs, store=False):
+    """Cycles of each pass of one LDS instruction under the model (an address
+    of None: the lane is inactive)."""
+    banks = 32 if width <= 4 or (width == 16 and store) else 64
+    out = []
+    for lanes in passes(width, store):
+        per_bank = defaultdict(set)
+        for l in lanes:
+            if addrs[l] is None:
+                continue
+            first = addrs[l] // 4
+            for d in range(first, first + max(1, width // 4)):
+                per_bank[d % banks].add(d)
+        out.append(max((len(v) for v in per_bank.values()), default=1))
+    return out
+
+
+def degree(width, addrs, store=False):
+    return max(pass_cycles(width, addrs, store))
+
+
+def extra_cycles(width, addrs, store=False):
+    return sum(c - 1 for c in pass_cycles(width, addrs, store))
+
+
+@pytest.fixture(scope="module")
+def dump(tmp_path_factory):
+    exe = str(tmp_path_factory.mktemp("lds") / "dump")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", CSRC, SRC, "-o", exe], check=True)
+    check = json.loads(subprocess.run([exe, "--check"], check=True, capture_output=True, text=True).stdout)
+    pats = [json.loads(ln) for ln in subprocess.run([exe], check=True, capture_output=True,
+                                                    text=True).stdout.splitlines() if ln.strip()]
+    return check, pats
+
+
+def test_layouts_are_bijections_and_accesses_reach_their_elements(dump):
+    check, _ = dump
+    assert check["failures"] == []
+
+
+def test_addresses_within_shared_arrays(dump):
+    _, pats = dump
+    # MlpBwdShared at this shape: 2 x 64 KB matrices, 28 KB exchange, LN parameters, 3 KB rows
+    total = 2 * 4 * 64 * 256 + (16 + 12) * 1024 + 2 * 4 * 64 + 3072
+    for p in pats:
+        assert min(p["addr"]) >= 0 and max(p["addr"]) + p["width"] <= total, p["name"]
+        assert all(a % p["width"] == 0 for a in p["addr"]), p["name"]
+
+
+def test_bank_conflicts_per_pattern(dump):
+    _, pats = dump
+    rows = defaultdict(lambda: [0, 0, 1, 0])  # width, count per step, degree, extra cycles per step
+    for p in pats:
+        r = rows[p["name"]]
+        r[0] = p["width"]
+        r[2] = max(r[2], degree(p["width"], p["addr"], p["store"]))
+        if p["wave"] == 0:
+            r[1] += p["count"]
+            r[3] += p["count"] * extra_cycles(p["width"], p["addr"], p["store"])
+    print("\npattern | bytes | per step | conflict degree | extra cycles per step")
+    for name, (w, cnt, deg, ext) in rows.items():
+        print(f"{name} | {w} | {cnt} | {deg} | {ext}")
+    insts = sum(r[1] for r in rows.values())
+    extra = sum(r[3] for r in rows.values())
+    print(f"total: {insts} LDS instructions, {extra} conflict cycles per step and wave "
+          f"({extra / insts:.3f} per instruction)")
+    for name, (w, cnt, deg, ext) in rows.items():
+        assert deg == EXPECTED_CONFLICTS.get(name, 1), name
+    assert extra / insts <= 0.1
+
+
+def _old_row4(cols, g, n, b):
+    # the replaced row-major layout: element (r, c) at r cols + (c ^ ((r & 7) << 2)) with
+    # column bit 4 toggled by (r >> 2) & 1 through two lane bases; lane (g, n) of a
+    # row-vector access at row n, columns 16 b + 4g..
+    return n * cols + 16 * (b ^ ((n >> 2) & 1)) + ((4 * g) ^ ((n & 3) << 2))
+
+
+def _block_no_tau(g, n):
+    # the block layout with chunk (c >> 2) ^ (r >> 2) instead of tau(c >> 2) ^ (r >> 2)
+    return 16 * (n ^ ((n >> 2) & 1)) + 4 * (g ^ (n >> 2))
+
+
+def test_model_gives_the_probed_counts():
+    # probed: 4 conflict cycles per 16-byte read for both replaced row layouts
+    for cols in (64, 256):
+        for b in (0, 1):
+            addrs = [4 * _old_row4(cols, l >> 4, l & 15, b) for l in range(64)]
+            assert degree(16, addrs) == 2 and extra_cycles(16, addrs) == 4
+    addrs = [4 * _block_no_tau(l >> 4, l & 15) for l in range(64)]
+    assert extra_cycles(16, addrs) == 4
+    # ... but none for the 16 lanes of one group alone (a pass holds 8 of them)
+    part = [addrs[l] if l < 16 else None for l in range(64)]
+    assert extra_cycles(16, part) == 0
+    # 16 lanes at dword 64 l (one bank): split 8 + 8 over two passes, 14 cycles
+    assert extra_cycles(16, [4 * 64 * l if l < 16 else None for l in range(64)]) == 14
+    # lanes 0 and k at dwords 0 and 64: one pass for k in 1, 2, 3, 12, 15, 20, 24, 27
+    for k in (1, 2, 3, 4, 5, 7, 8, 9, 11, 12, 15, 16, 17, 20, 24, 27, 30, 31, 32, 36, 48):
+        addrs = [256 if l == k else 0 if l == 0 else None for l in range(64)]
+        assert extra_cycles(16, addrs) == (1 if k in (1, 2, 3, 12, 15, 20, 24, 27) else 0), k
+    # 16-byte writes: lanes 0 and k at dwords 0 and 64 share a pass for k < 8; 16 lanes at
+    # dword 64 l, 14 cycles; the row vectors of the block layout with chunk tau(c >> 2) ^ (r >> 2),
+    # tau = (0, 3, 1, 2) (conflict-free reads), 8 cycles per write
+    for k in (1, 3, 5, 7, 8, 12, 16, 20, 32):
+        addrs = [256 if l == k else 0 if l == 0 else None for l in range(64)]
+        assert extra_cycles(16, addrs, store=True) == (1 if k < 8 else 0), k
+    assert extra_cycles(16, [4 * 64 * l if l < 16 else None for l in range(64)], store=True) == 14
+    tau = (0, 3, 1, 2)
+    addrs = [4 * (16 * (n ^ ((n >> 2) & 1)) + 4 * (tau[l >> 4] ^ (n >> 2))) for l in range(64) for n in [l & 15]]
+    assert extra_cycles(16, addrs) == 0 and extra_cycles(16, addrs, store=True) == 8
+    # replaced lane-order dZ2 frag writes, element (row 4w + j, feature n of tile lo)
+    # at 2-byte index (lo 64 + 16 (n >> 2) + 4w + j) 4 + (n & 3): 14 cycles
+    for w in range(4):
+        for j in range(4):
+            addrs = [2 * (((l >> 4) * 64 + 16 * ((l & 15) >> 2) + 4 * w + j) * 4 + (l & 3)) for l in range(64)]
+            assert degree(2, addrs) == 8 and extra_cycles(2, addrs) == 14
+
+
+def test_model_on_plain_patterns():
+    # lane-order 16-byte slots and 4-byte words: conflict-free; a stride of 64 dwords: one bank
+    assert degree(16, [16 * l for l in range(64)]) == 1
+    assert degree(4, [4 * l for l in range(64)]) == 1
+    assert degree(4, [256 * l for l in range(64)]) == 32
+    # the same dword from every lane: a broadcast
+    assert degree(4, [0] * 64) == 1

@@ -82,31 +82,30 @@ constexpr int kRsDz2 = 0, kRsDtgt = 4096, kRsDz2T = 8192;  // byte offsets in th
 
 typedef __attribute__((address_space(3))) unsigned short lds_u16;
 typedef __attribute__((address_space(3))) bf4 lds_bf4;
-// element (row r, feature 16c + q) of a [16 x F] matrix into its transposed
-// operand frags (free = row, k = feature): position q & 3 of lane 16 (q >> 2) + r
-// of tile c, tiles of 64 lanes x 4 elements
-template <typename T> __device__ __forceinline__ void lds_put_tfrag(unsigned base, int c, int r, int q, float v);
-template <> __device__ __forceinline__ void lds_put_tfrag<__bf16>(unsigned base, int c, int r, int q, float v) {
-  const unsigned a = base + 2u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
-  *(lds_u16*)(uintptr_t)a = __builtin_bit_cast(unsigned short, (__bf16)v);
+// element (row 4w + j, feature 16 lo + n) of a [16 x F] matrix into its
+// transposed operand frags (free = row, k = feature): element n & 3 of frag
+// lane 16 (n >> 2) + 4w + j of tile lo.  16-bit frags sit in the skewed 8-byte
+// slots of lds::tfrag16_slot (csrc/ttt_lds_layout.h), so that neither the
+// element writes nor the frag reads conflict; fp32 frags in tiles of 64 lanes
+// x 16 bytes in lane order.  tfrag_put_addr is the lane's address for j = 0.
+template <typename T> __device__ __forceinline__ unsigned tfrag_put_addr(unsigned base, int lo, int w, int n) {
+  if constexpr (sizeof(T) == 2)
+    return base + 8u * (unsigned)lds::tfrag16_put_slot(lo, w, n) + 2u * (unsigned)(n & 3);
+  else
+    return base + 16u * (unsigned)(lo * 64 + 16 * (n >> 2) + 4 * w) + 4u * (unsigned)(n & 3);
 }
-template <> __device__ __forceinline__ void lds_put_tfrag<_Float16>(unsigned base, int c, int r, int q, float v) {
-  const unsigned a = base + 2u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
-  *(lds_u16*)(uintptr_t)a = __builtin_bit_cast(unsigned short, (_Float16)v);
+template <typename T> __device__ __forceinline__ void lds_put_tfrag(unsigned a, int j, float v) {
+  if constexpr (sizeof(T) == 2)
+    *(lds_u16*)(uintptr_t)(a + 8u * j) = __builtin_bit_cast(unsigned short, (T)v);
+  else
+    *(lds_f32*)(uintptr_t)(a + 16u * j) = v;
 }
-template <> __device__ __forceinline__ void lds_put_tfrag<float>(unsigned base, int c, int r, int q, float v) {
-  const unsigned a = base + 4u * (unsigned)((c * 64 + 16 * (q >> 2) + r) * 4 + (q & 3));
-  *(lds_f32*)(uintptr_t)a = v;
-}
-template <typename T> __device__ __forceinline__ Frag<T> lds_get_tfrag(unsigned base, int c);
-template <> __device__ __forceinline__ Frag<__bf16> lds_get_tfrag<__bf16>(unsigned base, int c) {
-  return Frag<__bf16>{*(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)(c * 64 + lane_id()))};
-}
-template <> __device__ __forceinline__ Frag<_Float16> lds_get_tfrag<_Float16>(unsigned base, int c) {
-  return Frag<_Float16>{__builtin_bit_cast(h4, *(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)(c * 64 + lane_id())))};
-}
-template <> __device__ __forceinline__ Frag<float> lds_get_tfrag<float>(unsigned base, int c) {
-  return Frag<float>{*(lds_f4*)(uintptr_t)(base + 16u * (unsigned)(c * 64 + lane_id()))};
+template <typename T> __device__ __forceinline__ Frag<T> lds_get_tfrag(unsigned base, int c) {
+  if constexpr (sizeof(T) == 2)
+    return Frag<T>{__builtin_bit_cast(typename FragT<T>::type,
+                                      *(lds_bf4*)(uintptr_t)(base + 8u * (unsigned)lds::tfrag16_slot(c, lane_id())))};
+  else
+    return Frag<T>{*(lds_f4*)(uintptr_t)(base + 16u * (unsigned)(c * 64 + lane_id()))};
 }
 
 size_t mlp_bwd_ws_slot_bytes(int F, int FF, int dtype) {
@@ -251,6 +250,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   const int srow = (lo * 64 + 16 * wave + n) * 16;
   LdsLane xr(sh.x.mem, 768 * lo + 256 * wave);
   const unsigned dz2t_base = (unsigned)(uintptr_t)(lds_f32*)sh.x.mem + (unsigned)(Xch::PART + kRsDz2T);
+  const unsigned dz2t_put = tfrag_put_addr<T>(dz2t_base, lo, wave, n);
+  static_assert(!RS || kRsDz2T + (sizeof(T) == 2 ? lds::tfrag16_bytes(FT) : 16 * 64 * FT) <= 3 * NW * 1024,
+                "transposed dZ2 frags within the partial region");
 
   // gradient wrt the state after the current mini-batch (this wave's slice):
   // dW2[S, :] in registers, dW1[:, S] in LDS (below)
@@ -265,9 +267,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
   // LDS views (this wave's hidden columns of W2^T, its hidden rows of dW1^T)
-  // (a slice of one tile is narrower than LdsMat's 32-column swizzle groups:
-  // then W2 is kept by rows, this wave's [16 HT x F] rows, and the two access
-  // shapes swap)
+  // (with an odd number of hidden tiles per wave W2 is kept by rows, this
+  // wave's [16 HT x F] rows, and the two access shapes swap; both shapes are
+  // conflict-free in either layout)
   constexpr bool W2ROWS = (HT & 1) != 0;
   using W2Mat = std::conditional_t<W2ROWS, LdsMat<F>, LdsMat<FF>>;
   W2Mat W2t(W2ROWS ? sh.w2t + hs * F : sh.w2t, W2ROWS ? 0 : hs);
@@ -484,12 +486,14 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         dlnw_l += aw;
         dlnb_l += ab;
         const unsigned lxb = (unsigned)(uintptr_t)(lds_f32*)sh.lx;
-        *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(lo * 64 + 16 * wave + n)) = __builtin_bit_cast(bf4, to_frag<T>(dz).v);
+        *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)lds::crow16_slot(lo, 16 * wave + n)) =
+            __builtin_bit_cast(bf4, to_frag<T>(dz).v);
         *(lds_f32*)(uintptr_t)(lxb + kRsLCol + 4u * (unsigned)(wave * 64 + n * 4 + lo)) = dz[0] + dz[1] + dz[2] + dz[3];
         __syncthreads();  // (L) the rows of dZ2b of every wave in
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
-          dz2bf[c].v = __builtin_bit_cast(typename FragT<T>::type, *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)(c * 64 + l)));
+          dz2bf[c].v = __builtin_bit_cast(typename FragT<T>::type,
+                                          *(lds_bf4*)(uintptr_t)(lxb + 8u * (unsigned)lds::crow16_slot(c, l)));
           dz2bF[c] = to_frag<T>(transpose16(dz2bf[c], I).v);
         }
         f4 cs = f4{0.f, 0.f, 0.f, 0.f};  // column sums of features 16c + n
@@ -831,7 +835,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         xr.put(Xch::PART + kRsDz2, dz);
         xr.put(Xch::PART + kRsDtgt, dtg);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) lds_put_tfrag<T>(dz2t_base, lo, 4 * wave + j, n, dz[j]);
+        for (int j = 0; j < 4; ++j) lds_put_tfrag<T>(dz2t_put, j, dz[j]);
         bstore_ctile<T>(rDXV, l * ST, xs(s) + 4 * wave * F * ST, F, to_frag<T>(dtg));  // dXV rows
       } else {
         float lw_i[FT], lb_i[FT];

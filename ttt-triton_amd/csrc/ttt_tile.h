@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ttt_lds_layout.h"
+
 namespace ttt {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -439,67 +441,60 @@ __device__ __forceinline__ void store_tile(float* __restrict__ x, int ld, int r0
   for (int j = 0; j < 4; ++j) x[(r0 + 4 * g + j) * ld + c0 + n] = t.v[j];
 }
 
-// fp32 matrix [rows][COLS] in LDS with columns XOR-swizzled by 4 * (row & 7):
-// element (row, col) lives at row * COLS + (col ^ ((row & 7) << 2)).  A
-// C-layout tile (lanes of group g read rows 4g + j, 16 consecutive columns)
-// and a row-vector frag (lanes of group g read 4 consecutive columns of 16
-// rows) are both bank-conflict free with no padding.  COLS % 32 == 0.
+// fp32 matrix [rows][COLS] in LDS as 16 x 16 blocks with a swizzle inside
+// each block (lds::blk_elem, csrc/ttt_lds_layout.h): C-layout tiles (lanes of
+// group g at rows 4g + j, 16 consecutive columns; four 4-byte accesses) and
+// row-vector frags (lanes of group g at 4 consecutive columns of 16 rows; one
+// 16-byte access) are both read and written without bank conflicts and with
+// no padding.  COLS % 16 == 0; the base is 256-byte aligned.
 //
-// A view fixes a uniform column offset cw (a multiple of 32) and computes each
-// lane's share of every address once.  For row offsets r0 % 8 == 0 (% 16 for
-// row vectors) and column offsets c0 % 16 == 0 relative to cw, the swizzled
-// address splits into one of ten lane base addresses plus the constant
-// (r0 * COLS + (c0 & ~16)) * 4, which the LDS instruction's 16-bit immediate
-// offset absorbs (rows * COLS * 4 <= 64 KB).  `pin()` makes the bases opaque
-// to the optimiser; called once per loop iteration it keeps the compiler from
+// A view fixes a uniform column offset cw (a multiple of 16).  Every block
+// has the same swizzle, so a lane's share of an address does not depend on
+// the block: five lane base addresses (the four tile rows j and the row
+// vectors) plus the block's constant start r0 * COLS + 16 * c0 (r0, c0
+// multiples of 16), which the LDS instruction's 16-bit immediate offset
+// absorbs (rows * COLS * 4 <= 64 KB).  `pin()` makes the bases opaque to the
+// optimiser; called once per loop iteration it keeps the compiler from
 // hoisting every base + constant sum out of the loop into its own register.
 typedef __attribute__((address_space(3))) float lds_f32;
 typedef __attribute__((address_space(3))) f4 lds_f4;
 
 template <int COLS> struct LdsMat {
-  unsigned tb[2][4];  // tile lane base addresses by bit 4 of c0 and row j
-  unsigned rb[2];     // row-vector lane base addresses by bit 4 of c0
+  static_assert(COLS % 16 == 0, "16 x 16 blocks");
+  unsigned tb[4];  // tile lane base addresses of rows j
+  unsigned rb;     // row-vector lane base address
   __device__ __forceinline__ LdsMat(float* base, int cw) {
-    const unsigned p = (unsigned)(uintptr_t)(lds_f32*)base;
+    const unsigned p = (unsigned)(uintptr_t)(lds_f32*)base + 4u * (unsigned)lds::col_base(cw);
     const int l = lane_id(), g = l >> 4, n = l & 15;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        tb[b][j] = p + 4u * ((4 * g + j) * COLS + cw + 16 * (b ^ (g & 1)) + (n ^ (4 * j)));
-      rb[b] = p + 4u * (n * COLS + cw + 16 * (b ^ ((n >> 2) & 1)) + ((4 * g) ^ ((n & 3) << 2)));
-    }
+    for (int j = 0; j < 4; ++j) tb[j] = p + 4u * (unsigned)lds::tile_lane(g, n, j);
+    rb = p + 4u * (unsigned)lds::row_lane(g, n);
   }
   __device__ __forceinline__ void pin() {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(tb[b][j]));
-      asm volatile("" : "+v"(rb[b]));
-    }
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(tb[j]));
+    asm volatile("" : "+v"(rb));
   }
   __device__ __forceinline__ static lds_f32* at(unsigned a) { return (lds_f32*)(uintptr_t)a; }
   // C-layout tile at (r0, cw + c0): lane (g, n) holds M[r0 + 4g + j][cw + c0 + n]
   __device__ __forceinline__ Tile tile(int r0, int c0) const {
-    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
+    const int k = lds::blk_base(COLS, r0, c0);
     Tile t;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) t.v[j] = at(tb[b][j])[k];
+    for (int j = 0; j < 4; ++j) t.v[j] = at(tb[j])[k];
     return t;
   }
   __device__ __forceinline__ void put_tile(int r0, int c0, Tile t) const {
-    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
+    const int k = lds::blk_base(COLS, r0, c0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) at(tb[b][j])[k] = t.v[j];
+    for (int j = 0; j < 4; ++j) at(tb[j])[k] = t.v[j];
   }
   // row-vector frag at (r0, cw + c0): lane (g, r) holds M[r0 + r][cw + c0 + 4g + j]
   __device__ __forceinline__ f4 row4(int r0, int c0) const {
-    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
-    return *reinterpret_cast<lds_f4*>(at(rb[b]) + k);
+    return *reinterpret_cast<lds_f4*>(at(rb) + lds::blk_base(COLS, r0, c0));
   }
   __device__ __forceinline__ void put_row4(int r0, int c0, f4 v) const {
-    const int b = (c0 >> 4) & 1, k = r0 * COLS + (c0 & ~16);
-    *reinterpret_cast<lds_f4*>(at(rb[b]) + k) = v;
+    *reinterpret_cast<lds_f4*>(at(rb) + lds::blk_base(COLS, r0, c0)) = v;
   }
 };
 
