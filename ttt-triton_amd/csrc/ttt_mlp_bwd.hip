@@ -444,6 +444,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         // ---- A: rebuild W2_s (this slice) from the forward's update operands;
         //      the tiles of one feature block are read before any is written
         //      back, so the LDS reads overlap
+        //      (two register sets across feature blocks, as in the dW1 update,
+        //      measured 2% slower here)
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
           const Frag<T> ng = negate(g2e[c]);
@@ -925,15 +927,24 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
       for (int q = 0; q < FT; ++q) xqTf[q] = to_frag<T>(transpose16(xqf[q], I).v);
       prefetch(s > 0 ? s - 1 : 0);
       // the layer-1 state gradient: dW1 += XQ^T dZ1b + XK^T dZ1; biases
+      // (two register sets, so that the reads of hidden block o + 1 are in
+      // flight while block o's products and writes run)
+      {
+        Tile w[2][FT];
 #pragma unroll
-      for (int o = 0; o < HT; ++o) {
-        Tile w[FT];
+        for (int q = 0; q < FT; ++q) w[0][q] = dw1_get(q, 0);
 #pragma unroll
-        for (int q = 0; q < FT; ++q) w[q] = dw1_get(q, o);
+        for (int o = 0; o < HT; ++o) {
+          Tile(&cur)[FT] = w[o & 1];
+          if (o + 1 < HT) {
 #pragma unroll
-        for (int q = 0; q < FT; ++q) mma32(w[q].v, xqTf[q], xkTf[q], dz1bf[o], dz1f[o]);
+            for (int q = 0; q < FT; ++q) w[(o + 1) & 1][q] = dw1_get(q, o + 1);
+          }
 #pragma unroll
-        for (int q = 0; q < FT; ++q) dw1_put(q, o, w[q]);
+          for (int q = 0; q < FT; ++q) mma32(cur[q].v, xqTf[q], xkTf[q], dz1bf[o], dz1f[o]);
+#pragma unroll
+          for (int q = 0; q < FT; ++q) dw1_put(q, o, cur[q]);
+        }
       }
 #pragma unroll
       for (int o = 0; o < HT; ++o) {
