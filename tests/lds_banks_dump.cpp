@@ -6,7 +6,8 @@
 // The shared matrices and the 16-bit staging take their addresses from
 // csrc/ttt_lds_layout.h, the header the kernel itself builds them from; the
 // lane-order exchange slots (LdsLane: base + 16 lane) and the LayerNorm
-// parameter reads are restated from the kernel's expressions, cited by line.
+// parameter reads are restated from the kernel's expressions, named by
+// the kernel's variables.
 // Each pattern is printed once per wave with its width in bytes and the
 // number of times one step of one wave issues it.
 //
@@ -23,7 +24,7 @@ using namespace ttt::lds;
 namespace {
 
 constexpr int F = 64, FF = 256, NW = 4, FT = F / 16, HT = FF / (16 * NW);
-// byte offsets of the shared arrays (MlpBwdShared, csrc/ttt_mlp_bwd.hip:73-79)
+// byte offsets of the shared arrays (MlpBwdShared in csrc/ttt_mlp_bwd.hip)
 constexpr int W2T = 0, DW1T = 4 * F * FF, XCH = 8 * F * FF;
 constexpr int PART = NW * FT * 1024, XCH_BYTES = (NW * FT + 3 * NW) * 1024;
 constexpr int LNW = XCH + XCH_BYTES, LNB = LNW + 4 * F, LX = LNB + 4 * F;
@@ -131,9 +132,9 @@ int main(int argc, char** argv) {
   if (argc > 1 && std::string(argv[1]) == "--check") return check();
   for (int w = 0; w < NW; ++w) {
     const int hs = 16 * HT * w;
-    // W2^T [F][FF] by columns: the wave's view starts at column hs (csrc/ttt_mlp_bwd.hip:273)
+    // W2^T [F][FF] by columns: the wave's view W2t starts at column hs
     const long w2 = W2T + 4L * col_base(hs);
-    // dW1^T [FF][F]: the wave's rows hs.. (csrc/ttt_mlp_bwd.hip:274)
+    // dW1^T [FF][F]: the wave's view dW1s starts at row hs
     const long dw1 = DW1T + 4L * hs * F;
     // one instance per block touched: (r0, c0) as the kernel's calls pass them
     for (int c = 0; c < FT; ++c)
@@ -159,13 +160,13 @@ int main(int argc, char** argv) {
       }
     // exchange area, lane-order 16-byte slots (LdsLane, csrc/ttt_tile.h)
     const long xw = XCH + w * FT * 1024, xs16 = XCH + PART + w * 1024;
-    for (int b = 0; b < 3; ++b)  // dN1, dN1^T, eta-row partials (csrc/ttt_mlp_bwd.hip:637-709)
+    for (int b = 0; b < 3; ++b)  // dN1, dN1^T, eta-row partials (xs16.put in N and P)
       emit("exchange put xs16 (N, P)", 16, 1, w, lanes([&](int, int, int l) { return xs16 + b * NW * 1024 + 16L * l; }));
     for (int c = 0; c < FT; ++c)  // dG2 partials (P) and dXK partials (B2b)
       emit("exchange put xw (P, B2b)", 16, 2, w, lanes([&](int, int, int l) { return xw + c * 1024 + 16L * l; }));
     for (int b = 0; b < 3 * NW; ++b)  // B2a: every wave's partials
       emit("exchange get xa (B2a)", 16, 1, w, lanes([&](int, int, int l) { return XCH + PART + b * 1024 + 16L * l; }));
-    // row split: xr = 768 (l >> 4) + 256 w + 16 l (csrc/ttt_mlp_bwd.hip:252)
+    // row split: xr = 768 (l >> 4) + 256 w + 16 l (LdsLane xr)
     for (int v = 0; v < NW; ++v)
       emit("exchange get xr (B2a)", 16, 1, w,
            lanes([&](int lo, int, int l) { return XCH + 768L * lo + 256 * w + 16L * l + v * FT * 1024; }));
@@ -190,7 +191,7 @@ int main(int argc, char** argv) {
     emit("readout dZ2 row write (L)", 8, 1, w, lanes([&](int lo, int n, int) { return LX + 8L * crow16_slot(lo, 16 * w + n); }));
     for (int c = 0; c < FT; ++c)
       emit("readout dZ2 tile read (L)", 8, 1, w, lanes([&](int, int, int l) { return LX + 8L * crow16_slot(c, l); }));
-    // column-sum partials: 4 (64 w + 4 n + lo) (csrc/ttt_mlp_bwd.hip:489), read as 16 bytes at 16 (16 v + n)
+    // column-sum partials: 4 (64 w + 4 n + lo) (the readout LayerNorm backward), read as 16 bytes at 16 (16 v + n)
     emit("readout column sum write (L)", 4, 1, w, lanes([&](int lo, int n, int) { return LX + RS_LCOL + 4L * (64 * w + 4 * n + lo); }));
     for (int v = 0; v < NW; ++v)
       emit("readout column sum read (L)", 16, 1, w, lanes([&](int, int n, int) { return LX + RS_LCOL + 16L * (16 * v + n); }));

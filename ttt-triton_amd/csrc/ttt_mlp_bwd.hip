@@ -71,8 +71,8 @@ template <int FT, int NW> constexpr bool kBwdRowSplit = (NW == 4 && FT == 4);
 constexpr int kRsL = 3072, kRsLCol = 2048;
 
 template <int FT, int NW, int HT> struct MlpBwdShared {
-  float w2t[16 * FT * 16 * HT * NW];   // W2^T [F][FF] (or W2 [FF][F] by the waves' rows), swizzled
-  float dw1t[16 * FT * 16 * HT * NW];  // dW1^T [FF][F], swizzled
+  float w2t[16 * FT * 16 * HT * NW];   // W2^T [F][FF], 16 x 16 blocks (LdsMat)
+  float dw1t[16 * FT * 16 * HT * NW];  // dW1^T [FF][F], 16 x 16 blocks (LdsMat)
   MlpBwdExchange<FT, NW> x;
   float lnw[16 * FT], lnb[16 * FT];  // LayerNorm parameters of the chain's head
   alignas(16) unsigned char lx[kBwdRowSplit<FT, NW> ? kRsL : 16];  // readout LayerNorm rows (row split, bf16)
@@ -267,12 +267,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
   for (int o = 0; o < FT; ++o) db2[o] = 0.f;
   // LDS views (this wave's hidden columns of W2^T, its hidden rows of dW1^T)
-  // (with an odd number of hidden tiles per wave W2 is kept by rows, this
-  // wave's [16 HT x F] rows, and the two access shapes swap; both shapes are
-  // conflict-free in either layout)
-  constexpr bool W2ROWS = (HT & 1) != 0;
-  using W2Mat = std::conditional_t<W2ROWS, LdsMat<F>, LdsMat<FF>>;
-  W2Mat W2t(W2ROWS ? sh.w2t + hs * F : sh.w2t, W2ROWS ? 0 : hs);
+  // (W2 kept by rows instead, which swaps the two access shapes, measured
+  // 9% slower at four hidden tiles per wave and no faster at one)
+  LdsMat<FF> W2t(sh.w2t, hs);
   LdsMat<F> dW1s(sh.dw1t + hs * F, 0);
   // dW1 tile [F block q x hidden block o] (C layout), also its frag (free = hidden, k = feature)
   auto dw1_get = [&](int q, int o) {
@@ -290,25 +287,12 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
   // W2 tile [hidden block o x F block c] (C layout): frag (free = feature, k = hidden)
   auto w2_tile = [&](int o, int c) {
     Tile t;
-    if constexpr (W2ROWS)
-      t = W2t.tile(16 * o, 16 * c);
-    else
-      t.v = W2t.row4(16 * c, 16 * o);
+    t.v = W2t.row4(16 * c, 16 * o);
     return t;
   };
-  auto w2_put = [&](int o, int c, Tile t) {
-    if constexpr (W2ROWS)
-      W2t.put_tile(16 * o, 16 * c, t);
-    else
-      W2t.put_row4(16 * c, 16 * o, t.v);
-  };
+  auto w2_put = [&](int o, int c, Tile t) { W2t.put_row4(16 * c, 16 * o, t.v); };
   // W2^T frag (free = hidden block o, k = feature block c)
-  auto w2T_frag = [&](int o, int c) {
-    if constexpr (W2ROWS)
-      return to_frag<T>(W2t.row4(16 * o, 16 * c));
-    else
-      return to_frag<T>(W2t.tile(16 * c, 16 * o).v);
-  };
+  auto w2T_frag = [&](int o, int c) { return to_frag<T>(W2t.tile(16 * c, 16 * o).v); };
   // keep the gradient accumulators in the MFMA accumulator registers
   auto pin_dW = [&]() {
 #pragma unroll
