@@ -896,14 +896,27 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           bstore_frag_dev<T>(rWS, hl + o * 256 * ST, ws_ + WS::DZ1F, dz1F[o]);
           eg1F[o] = to_frag<T>(transpose16(g1ef[o], I).v);
         }
-        // dXK partial over this slice: (-e G1) dW1'^T (dW1' not yet updated)
+        // dXK partial over this slice: (-e G1) dW1'^T (dW1' not yet updated);
+        // the dW1'^T tiles of feature block f + 1 are read while block f's
+        // products run
+        {
+          Tile tl[2][HT];
 #pragma unroll
-        for (int f = 0; f < FT; ++f) {
-          f4 zk_ = f4{0.f, 0.f, 0.f, 0.f};
+          for (int c = 0; c < HT; ++c) tl[0][c] = dW1s.tile(16 * c, 0);
 #pragma unroll
-          for (int c = 0; c + 1 < HT; c += 2) mma32(zk_, eg1F[c], eg1F[c + 1], dw1T_frag(f, c), dw1T_frag(f, c + 1));
-          if constexpr (HT & 1) mma16(zk_, eg1F[HT - 1], dw1T_frag(f, HT - 1));
-          xw.put(f * 1024, zk_);
+          for (int f = 0; f < FT; ++f) {
+            if (f + 1 < FT) {
+#pragma unroll
+              for (int c = 0; c < HT; ++c) tl[(f + 1) & 1][c] = dW1s.tile(16 * c, 16 * (f + 1));
+            }
+            Tile(&cur)[HT] = tl[f & 1];
+            f4 zk_ = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c + 1 < HT; c += 2)
+              mma32(zk_, eg1F[c], eg1F[c + 1], to_frag<T>(cur[c].v), to_frag<T>(cur[c + 1].v));
+            if constexpr (HT & 1) mma16(zk_, eg1F[HT - 1], to_frag<T>(cur[HT - 1].v));
+            xw.put(f * 1024, zk_);
+          }
         }
       }
       Frag<T> xqTf[FT];
