@@ -885,11 +885,22 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           for (int o = 0; o < HT; ++o) mma16(dW2[o][c].v, x2f[o], dz2f);  // + X2^T dZ2
         }
         Frag<T> dz1F[HT], eg1F[HT];
+        // (the W2^T tiles of hidden block o + 1 are read while block o's
+        // products run)
+        Tile wt[2][FT];
+#pragma unroll
+        for (int c = 0; c < FT; ++c) wt[0][c] = W2t.tile(16 * c, 0);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
+          if (o + 1 < HT) {
+#pragma unroll
+            for (int c = 0; c < FT; ++c) wt[(o + 1) & 1][c] = W2t.tile(16 * c, 16 * (o + 1));
+          }
+          Tile(&cur)[FT] = wt[o & 1];
           f4 dx2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int c = 0; c < FT; c += 2) mma32(dx2, dz2F[c], dz2F[c + 1], w2T_frag(o, c), w2T_frag(o, c + 1));
+          for (int c = 0; c < FT; c += 2)
+            mma32(dx2, dz2F[c], dz2F[c + 1], to_frag<T>(cur[c].v), to_frag<T>(cur[c + 1].v));
           dZ1[o].v += dx2 * frag_to_f4(sp1s[o]);
           dz1f[o] = to_frag<T>(dZ1[o].v);
           dz1F[o] = to_frag<T>(transpose16(dz1f[o], I).v);
