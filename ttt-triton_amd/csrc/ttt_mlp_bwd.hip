@@ -643,12 +643,21 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) m1[j] = eta_n[j] * a[j] + eta_n[j];
         const Frag<T> mf = to_frag<T>(-m1);
+        // (the dW1' rows of hidden block o + 1 are read while block o's
+        // products run)
+        Tile dr[2][FT];
+#pragma unroll
+        for (int q = 0; q < FT; ++q) dr[0][q] = dw1_get(q, 0);
 #pragma unroll
         for (int o = 0; o < HT; ++o) {
+          if (o + 1 < HT) {
+#pragma unroll
+            for (int q = 0; q < FT; ++q) dr[(o + 1) & 1][q] = dw1_get(q, o + 1);
+          }
+          Tile(&cur)[FT] = dr[o & 1];
           f4 q1 = f4{db1[o], db1[o], db1[o], db1[o]};
 #pragma unroll
-          for (int q = 0; q < FT; q += 2)
-            mma32(q1, xk[q], xk[q + 1], to_frag<T>(dw1_get(q, o).v), to_frag<T>(dw1_get(q + 1, o).v));
+          for (int q = 0; q < FT; q += 2) mma32(q1, xk[q], xk[q + 1], to_frag<T>(cur[q].v), to_frag<T>(cur[q + 1].v));
           f4 dg1 = f4{0.f, 0.f, 0.f, 0.f};
           mma16(dg1, mf, dz1bf[o]);
           const f4 g1 = frag_to_f4(g1s[o]), sp = frag_to_f4(sp1s[o]), h1 = frag_to_f4(h1s[o]);
@@ -669,8 +678,17 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
         Frag<T> x2F[HT];
 #pragma unroll
         for (int o = 0; o < HT; ++o) x2F[o] = to_frag<T>(transpose16(x2f[o], I).v);
+        // (the W2 rows of feature block c + 1 are read while block c's products run)
+        Tile wr[2][HT];
+#pragma unroll
+        for (int o = 0; o < HT; ++o) wr[0][o] = w2_tile(o, 0);
 #pragma unroll
         for (int c = 0; c < FT; ++c) {
+          if (c + 1 < FT) {
+#pragma unroll
+            for (int o = 0; o < HT; ++o) wr[(c + 1) & 1][o] = w2_tile(o, c + 1);
+          }
+          Tile(&wc)[HT] = wr[c & 1];
           f4 q2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int o = 0; o + 1 < HT; o += 2)
@@ -689,9 +707,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_bwd_kernel(MlpBwdParams p) {
           }
           mma16(z, m2f, dz2bf[c]);
 #pragma unroll
-          for (int o = 0; o + 1 < HT; o += 2)
-            mma32(z, dPF[o], dPF[o + 1], to_frag<T>(w2_tile(o, c).v), to_frag<T>(w2_tile(o + 1, c).v));
-          if constexpr (HT & 1) mma16(z, dPF[HT - 1], to_frag<T>(w2_tile(HT - 1, c).v));
+          for (int o = 0; o + 1 < HT; o += 2) mma32(z, dPF[o], dPF[o + 1], to_frag<T>(wc[o].v), to_frag<T>(wc[o + 1].v));
+          if constexpr (HT & 1) mma16(z, dPF[HT - 1], to_frag<T>(wc[HT - 1].v));
           xw.put(c * 1024, z);
         }
 #pragma unroll
