@@ -15,14 +15,16 @@
 // on NC+1-it.
 //   P (prepare)  everything that involves neither W nor dW: the readout-LN
 //                backward (dZb), the dual-form terms (dM, dA, deta),
-//                dout + dA XK, dA^T XQ, -M^T dZb and the exact transposes the
-//                other two waves consume;
+//                -M^T dZb and the exact transposes the other two waves
+//                consume;
 //   S (state)    owns dW and db: XK dW' + db', the inner-loss LN backward,
 //                -(e G) dW'^T, the dW/db update;
 //   X (weights)  owns W^T, rebuilt backwards from the checkpoint after each
 //                group (kernels/linear_backward.py:278 walks the same groups):
 //                W_s = W_{s+1} + XK_s^T diag(e) G_s with the forward's MFMA
-//                operands; forms dXQ, dXK, dXV and deta and writes them.
+//                operands; forms dXQ, dXK, dXV and deta (with the
+//                dual-form terms dout + dA XK and dA^T XQ from P's dA) and
+//                writes them.
 // Feature-major tiles ("FM": lane (g, n) holds features 16o + 4g + j of token
 // n) are what the outputs are written from, 4 contiguous elements per lane.
 #include "ttt_eta.h"
@@ -48,8 +50,9 @@ template <typename T, int FT> struct LinBwdShared {
     Frag<T> xk_t[FT][64];   // XK token-major tiles as frags (free = feature)
     Frag<T> dzb[FT][64];    // dZb row-major frags (free = token)
     Frag<T> eg_t[FT][64];   // e G token-major tiles as frags (free = feature)
-    f4 xqp[FT][64];         // (dout + dA XK)^T, FM
-    f4 xkp[FT][64];         // (dA^T XQ)^T, FM
+    Frag<T> xq_t[FT][64];   // XQ token-major tiles as frags (free = feature)
+    Frag<T> dat[64];        // dA^T [t_k x t_q] as a frag
+    Frag<T> da[64];         // dA [t_q x t_k] as a frag
     f4 det[64];             // deta without the last-row term: lane (g, n) holds deta[n][4g + j]
   } px[3];
   // S -> X, by mini-batch parity
@@ -156,6 +159,7 @@ template <typename T, int FT, bool LR, typename ET> struct WaveP {
       ps.tgt[q][l] = transpose16(x.xv[q], I).v - xkT.v;
       ps.xk[q][l] = x.xk[0][q];
       ps.xq_t[q][l] = xqTf[q];
+      px.xq_t[q][l] = xqTf[q];
       px.xk_t[q][l] = xkTf[q];
     }
     ps.e[l] = e;
@@ -244,14 +248,10 @@ template <typename T, int FT, bool LR, typename ET> struct WaveP {
     }
     px.det[l] = det;
     const Frag<T> daTf = to_frag<T>(daT), daf = to_frag<T>(da), mf = to_frag<T>(-m);
+    px.dat[l] = daTf;  // (dout + dA XK)^T and (dA^T XQ)^T are formed by X
+    px.da[l] = daf;
 #pragma unroll
     for (int q = 0; q < FT; ++q) {
-      f4 xqp = frag_to_f4(x.dof[q]);
-      mma16(xqp, xkTf[q], daTf);  // + (dA XK)^T
-      px.xqp[q][l] = xqp;
-      f4 xkp = f4{0.f, 0.f, 0.f, 0.f};
-      mma16(xkp, xqTf[q], daf);  // (dA^T XQ)^T
-      px.xkp[q][l] = xkp;
       f4 dg = f4{0.f, 0.f, 0.f, 0.f};
       mma16(dg, mf, dZbTf[q]);  // -M^T dZb
       ps.dg0[q][l] = dg;
@@ -445,6 +445,7 @@ template <typename T, int FT, bool LR, typename ET> struct WaveX {
   Frag<T> I;
   Tile WT[FT][FT];  // WT[o][i]: lane (g, n) holds W[16i + n][16o + 4g + j]
   Tile WN[FT][FT];  // the checkpoint the next group starts from
+  Frag<T> dof_n[FT];  // dout of the next mini-batch (FM)
 
   __device__ WaveX(const LinearBwdParams& p_, const LinBwdCtx<T, FT>& c_, LinBwdShared<T, FT>& sh_)
       : p(p_), c(c_), sh(sh_) {
@@ -452,6 +453,11 @@ template <typename T, int FT, bool LR, typename ET> struct WaveX {
     g = l >> 4;
     n = l & 15;
     I = identity_frag<T>();
+  }
+
+  __device__ void load_do(int s) {
+#pragma unroll
+    for (int q = 0; q < FT; ++q) dof_n[q] = load_frag(c.DO + (size_t)s * K * F, F, 16 * q);
   }
 
   __device__ void load_w(Tile (&w)[FT][FT], const float* src) {
@@ -475,6 +481,10 @@ template <typename T, int FT, bool LR, typename ET> struct WaveX {
 
     const auto& px = sh.px[m3];
     const auto& sx = sh.sx[s & 1];
+    Frag<T> dof[FT];
+#pragma unroll
+    for (int q = 0; q < FT; ++q) dof[q] = dof_n[q];
+    load_do(s > 0 ? s - 1 : 0);  // unconditional, so that the wait for it is exact
     // W_s = W_{s+1} + XK^T diag(e) G:  W^T[o][i] += sum_t (e G)[t][o] XK[t][i]
     {
       Frag<T> xkTf[FT];
@@ -497,11 +507,15 @@ template <typename T, int FT, bool LR, typename ET> struct WaveX {
       dz1F[o] = to_frag<T>(transpose16(sx.dz1_t[o][l], I).v);
     }
     const size_t xo = (size_t)s * K * F;
+    const Frag<T> daTf = px.dat[l], daf = px.da[l];
 #pragma unroll
     for (int i = 0; i < FT; ++i) {
       const f4 dv = transpose16(sx.dtgt_t[i][l], I).v;
-      f4 q = px.xqp[i][l];
-      f4 k = px.xkp[i][l] + sx.tr[i][l] - dv;
+      f4 q = frag_to_f4(dof[i]);
+      mma16(q, px.xk_t[i][l], daTf);  // + (dA XK)^T
+      f4 xkp = f4{0.f, 0.f, 0.f, 0.f};
+      mma16(xkp, px.xq_t[i][l], daf);  // (dA^T XQ)^T
+      f4 k = xkp + sx.tr[i][l] - dv;
 #pragma unroll
       for (int o = 0; o < FT; o += 2) {
         const Frag<T> w0 = to_frag<T>(WT[o][i].v), w1 = to_frag<T>(WT[o + 1][i].v);
@@ -581,6 +595,7 @@ __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   } else {
     WaveX<T, FT, LR, ET> w(p, c, sh);
     w.load_w(w.WT, p.W_last + (size_t)c.chain * F * F);
+    w.load_do(NC - 1);
     __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it < NC + 2; ++it) {
       const int s = NC + 1 - it;
