@@ -18,13 +18,13 @@
 //                -M^T dZb and the exact transposes the other two waves
 //                consume;
 //   S (state)    owns dW and db: XK dW' + db', the inner-loss LN backward,
-//                -(e G) dW'^T, the dW/db update;
+//                the dW/db update, and hands dW' to X as operand frags;
 //   X (weights)  owns W^T, rebuilt backwards from the checkpoint after each
 //                group (kernels/linear_backward.py:278 walks the same groups):
 //                W_s = W_{s+1} + XK_s^T diag(e) G_s with the forward's MFMA
 //                operands; forms dXQ, dXK, dXV and deta (with the
-//                dual-form terms dout + dA XK and dA^T XQ from P's dA) and
-//                writes them.
+//                dual-form terms dout + dA XK and dA^T XQ from P's dA, and
+//                -(e G) dW'^T from S's dW') and writes them.
 // Feature-major tiles ("FM": lane (g, n) holds features 16o + 4g + j of token
 // n) are what the outputs are written from, 4 contiguous elements per lane.
 #include "ttt_eta.h"
@@ -32,6 +32,9 @@
 #include "ttt_ln.h"
 
 namespace ttt {
+
+// whether S hands dW' to X as operand frags (16-bit) or forms -(e G) dW'^T itself
+template <typename T> constexpr bool kLinHandDw = sizeof(T) == 2;
 
 template <typename T, int FT> struct LinBwdShared {
   // P -> S, by mini-batch parity
@@ -52,6 +55,7 @@ template <typename T, int FT> struct LinBwdShared {
     Frag<T> eg_t[FT][64];   // e G token-major tiles as frags (free = feature)
     Frag<T> xq_t[FT][64];   // XQ token-major tiles as frags (free = feature)
     Frag<T> dat[64];        // dA^T [t_k x t_q] as a frag
+    Frag<T> egn[kLinHandDw<T> ? FT : 1][64];  // -(e G) row-major frags (free = token), for X (16-bit)
     Frag<T> da[64];         // dA [t_q x t_k] as a frag
     f4 det[64];             // deta without the last-row term: lane (g, n) holds deta[n][4g + j]
   } px[3];
@@ -59,7 +63,11 @@ template <typename T, int FT> struct LinBwdShared {
   struct SX {
     Frag<T> dz1_t[FT][64];   // dZ1 token-major tiles as frags
     Frag<T> dtgt_t[FT][64];  // dtgt (= dXV) token-major tiles as frags
-    f4 tr[FT][64];           // (-(e G) dW'^T)^T, FM
+    // 16-bit: dW' (not yet updated) as operand frags, dwf[i][o] of block (i, o),
+    // for X to form (-(e G) dW'^T)^T; fp32 (twice the bytes, beyond the LDS):
+    // S forms it, FM
+    Frag<T> dwf[kLinHandDw<T> ? FT : 1][kLinHandDw<T> ? FT : 1][64];
+    f4 tr[kLinHandDw<T> ? 1 : FT][64];
     f4 de[64];               // last-row eta gradient of token 4g + j
   } sx[2];
   float red[2 * 16 * FT];    // readout-LN parameter gradients, P -> S at the end
@@ -174,7 +182,9 @@ template <typename T, int FT, bool LR, typename ET> struct WaveP {
       for (int j = 0; j < 4; ++j) v[j] = e[j] * x.G[o][j];
       const Frag<T> ge = to_frag<T>(v);
       px.eg_t[o][l] = ge;
-      ps.egn[o][l] = negate(to_frag<T>(transpose16(ge, I).v));
+      const Frag<T> egn = negate(to_frag<T>(transpose16(ge, I).v));
+      ps.egn[o][l] = egn;
+      if constexpr (kLinHandDw<T>) px.egn[o][l] = egn;
       GF[0][o] = to_frag<T>(transpose16(to_frag<T>(x.G[o]), I).v);
     }
 
@@ -357,8 +367,14 @@ template <typename T, int FT> struct WaveS {
       sx.de[l] = de;
     }
 
-    // (-(e G) dW'^T)^T from the transposed dW' blocks (FM)
-    {
+    if constexpr (kLinHandDw<T>) {
+      // dW' as operand frags for X, which forms (-(e G) dW'^T)^T
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int o = 0; o < FT; ++o) sx.dwf[i][o][l] = to_frag<T>(dW[i][o].v);
+    } else {
+      // (-(e G) dW'^T)^T from the transposed dW' blocks (FM)
       Frag<T> egn[FT];
 #pragma unroll
       for (int o = 0; o < FT; ++o) egn[o] = ps.egn[o][l];
@@ -515,7 +531,20 @@ template <typename T, int FT, bool LR, typename ET> struct WaveX {
       mma16(q, px.xk_t[i][l], daTf);  // + (dA XK)^T
       f4 xkp = f4{0.f, 0.f, 0.f, 0.f};
       mma16(xkp, px.xq_t[i][l], daf);  // (dA^T XQ)^T
-      f4 k = xkp + sx.tr[i][l] - dv;
+      // (-(e G) dW'^T)^T from the transposed dW' blocks (FM)
+      f4 tr;
+      if constexpr (kLinHandDw<T>) {
+        tr = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < FT; o += 2) {
+          const Frag<T> t0 = to_frag<T>(transpose16(sx.dwf[i][o][l], I).v);
+          const Frag<T> t1 = to_frag<T>(transpose16(sx.dwf[i][o + 1][l], I).v);
+          mma32(tr, t0, t1, px.egn[o][l], px.egn[o + 1][l]);
+        }
+      } else {
+        tr = sx.tr[i][l];
+      }
+      f4 k = xkp + tr - dv;
 #pragma unroll
       for (int o = 0; o < FT; o += 2) {
         const Frag<T> w0 = to_frag<T>(WT[o][i].v), w1 = to_frag<T>(WT[o + 1][i].v);
@@ -541,6 +570,7 @@ template <typename T, int FT, bool LR, typename ET = T>
 __global__ __launch_bounds__(192) void linear_bwd_kernel(LinearBwdParams p) {
   constexpr int F = 16 * FT;
   constexpr int K = 16;
+  static_assert(sizeof(LinBwdShared<T, FT>) <= 160 * 1024, "the handoff areas fit one CU's LDS");
   __shared__ LinBwdShared<T, FT> sh;
   LinBwdCtx<T, FT> c;
   c.chain = blockIdx.x;
