@@ -177,6 +177,16 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
   __builtin_amdgcn_s_waitcnt(0);
 
   for (int s = 0; s < NC; ++s) {
+    // the state stays in the accumulator registers (the MFMA update's own),
+    // not copied out to VGPRs and back around the phases that read it
+#pragma unroll
+    for (int i = 0; i < FT; ++i)
+#pragma unroll
+      for (int o = 0; o < HT; ++o) asm volatile("" : "+a"(W1[i][o].v));
+#pragma unroll
+    for (int i = 0; i < HT; ++i)
+#pragma unroll
+      for (int o = 0; o < FT; ++o) asm volatile("" : "+a"(W2[i][o].v));
     if (p.W1_ckpt != nullptr && (s % p.G) == 0) {
       const size_t k = (size_t)chain * p.NK + s / p.G;
       store_state(p.W1_ckpt + k * F * FF, p.b1_ckpt ? p.b1_ckpt + k * FF : nullptr,
