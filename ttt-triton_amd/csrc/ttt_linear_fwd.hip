@@ -112,6 +112,11 @@ __global__ __launch_bounds__(128) void linear_fwd_kernel(LinearFwdParams p) {
     __builtin_amdgcn_s_waitcnt(0);
 
     for (int s = 0; s < NC; ++s) {
+      // the state stays in the accumulator registers (the MFMA update's own)
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int o = 0; o < FT; ++o) asm volatile("" : "+a"(W[i][o].v));
       if (p.W_ckpt != nullptr && (s % p.G) == 0) {
         const int kk = s / p.G;
         float* wc = p.W_ckpt + ((size_t)chain * p.NK + kk) * F * F;
