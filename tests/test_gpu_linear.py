@@ -171,10 +171,13 @@ def test_linear_bwd_fp32(kind):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-def test_linear_bwd_16bit(dt):
-    _say("linear bwd", dt)
-    d = eta_own_dtype(O.make_inputs(2, 3, 24, 16, 64, seed=6, dtype=dt, with_grad=True), dt)
-    mine = _bwd(d, d["dOut"], G=8)
+@pytest.mark.parametrize("F_,NC,G", [(64, 24, 8), (32, 9, 4)], ids=["F64", "F32"])
+def test_linear_bwd_16bit(dt, F_, NC, G):
+    """16-bit activations at both widths (F = 32: two feature tiles per
+    handoff frag set; a group size that does not divide NC)"""
+    _say("linear bwd", dt, f"F{F_} NC{NC} G{G}")
+    d = eta_own_dtype(O.make_inputs(2, 3, NC, 16, F_, seed=6, dtype=dt, with_grad=True), dt)
+    mine = _bwd(d, d["dOut"], G=G)
     ref = oracle_linear_grads(d, d["dOut"], G=0)
     bad = []
     for k in mine:
