@@ -1,7 +1,11 @@
 // Per-lane LDS byte addresses of every LDS access pattern of one mini-batch
 // step of the MLP backward sweep (csrc/ttt_mlp_bwd.hip, mlp_bwd_kernel at
 // bf16, F = 64, FF = 256, four waves: HT = 4 hidden tiles per wave, LayerNorm
-// backwards split by rows), printed as JSON lines for tests/test_lds_banks.py.
+// backwards split by rows), printed as JSON lines for tests/test_lds_banks.py;
+// with --linear, those of the row-split Linear forward
+// (csrc/ttt_linear_fwd_rows.hip at F = 64), relative to each shared array's
+// start (one offset shared by all lanes of an access leaves its banks'
+// conflicts unchanged).  An inactive lane prints as null.
 //
 // The shared matrices and the 16-bit staging take their addresses from
 // csrc/ttt_lds_layout.h, the header the kernel itself builds them from; the
@@ -37,7 +41,12 @@ void emit(const char* name, int width, int count, int wave, const std::vector<lo
   const bool store = std::strstr(name, "write") != nullptr || std::strstr(name, "put") != nullptr;
   std::printf("%s{\"name\": \"%s\", \"width\": %d, \"store\": %d, \"count\": %d, \"wave\": %d, \"addr\": [",
               first ? "" : "\n", name, width, store ? 1 : 0, count, wave);
-  for (size_t i = 0; i < a.size(); ++i) std::printf("%s%ld", i ? ", " : "", a[i]);
+  for (size_t i = 0; i < a.size(); ++i) {
+    if (a[i] < 0)
+      std::printf("%snull", i ? ", " : "");
+    else
+      std::printf("%s%ld", i ? ", " : "", a[i]);
+  }
   std::printf("]}");
   first = false;
 }
@@ -120,6 +129,25 @@ int check() {
     for (int v : seen)
       if (v != 1) fail("crow16 not a permutation");
   }
+  // 16-bit tile rows read back transposed: trow_put and grow_put are
+  // permutations of a tile's 64 places, and lane l of the transposing read
+  // supplies the place of row 4 (l >> 4) + ((l & 15) >> 2), group l & 3
+  for (int o = 0; o < 4; ++o) {
+    std::vector<int> a(64, 0), b(64, 0);
+    for (int m = 0; m < 16; ++m)
+      for (int g = 0; g < 4; ++g) {
+        ++a[trow_put(m, g)];
+        ++b[grow_put(o, m, g)];
+      }
+    for (int v : a)
+      if (v != 1) fail("trow_put not a permutation");
+    for (int v : b)
+      if (v != 1) fail("grow_put not a permutation");
+    for (int l = 0; l < 64; ++l) {
+      const int m = 4 * (l >> 4) + ((l & 15) >> 2), g = l & 3;
+      if (trow_get(l) != trow_put(m, g) || grow_get(o, l) != grow_put(o, m, g)) fail("transposing read place");
+    }
+  }
   std::printf("{\"failures\": [");
   for (size_t i = 0; i < bad.size(); ++i) std::printf("%s\"%s\"", i ? ", " : "", bad[i].c_str());
   std::printf("]}\n");
@@ -128,8 +156,70 @@ int check() {
 
 }  // namespace
 
+// One mini-batch step of the row-split Linear forward at F = 64 (four feature
+// tiles, two per pair p): waves R0, R1 (the chain), S (the state), O (the
+// readout).  Arrays as LinRowsPar / LinRowsShared declare them: wf [16][64]
+// 8-byte frags, b [64] fp32, gneg and geta [4][64] 8-byte tile rows, pp
+// [2][2][64] 16-byte rows, mt [64] 8-byte frags, gx [2][4][16][20] fp32 (rows
+// padded to 20), rc [2][16] fp32, xkt [4][64] 8-byte tile rows.
+int linear_rows() {
+  constexpr int LFT = 4, PP = 2, GXT = 16 * 20;
+  auto tr = [&](int o) { return lanes([&](int, int, int l) { return 8L * (64 * o + grow_get(o, l)); }); };
+  for (int w = 0; w < 2; ++w) {
+    for (int o = 0; o < LFT; ++o) emit("G tile transposing read (R)", 8, 1, w, tr(o));
+    for (int q = 0; q < PP; ++q) {
+      emit("P partial read (R)", 16, 1, w, lanes([&](int, int, int l) { return 16L * (64 * (w * PP + q) + l); }));
+      emit("b read (R)", 16, 1, w, lanes([&](int g, int n, int) { return 4L * (16 * (2 * q + (n >> 3)) + 4 * g); }));
+    }
+    emit("M frag read (R)", 8, 1, w, lanes([&](int, int, int l) { return 8L * l; }));
+    for (int q = 0; q < PP; ++q) {
+      // -G and -(e o G): lane (g, n) holds token (n & 7) + 8w of tile 2q + (n >> 3)
+      emit("G tile row put (R)", 8, 2, w, lanes([&](int g, int n, int) {
+             const int o = 2 * q + (n >> 3), t = (n & 7) + 8 * w;
+             return 8L * (64 * o + grow_put(o, t, g));
+           }));
+      emit("G, XH fp32 row write (R)", 16, 2, w, lanes([&](int g, int n, int) {
+             const int o = 2 * q + (n >> 3), t = (n & 7) + 8 * w;
+             return 4L * (o * GXT + 20 * t + 4 * g);
+           }));
+    }
+    emit("row value write (R)", 4, 2, w,
+         lanes([&](int g, int n, int) { return g == 0 && n < 8 ? 4L * ((n & 7) + 8 * w) : -1L; }));
+  }
+  for (int o = 0; o < LFT; ++o) emit("e G tile transposing read (S)", 8, 1, 2, tr(o));
+  for (int i = 0; i < LFT; ++i)
+    emit("XK tile transposing read (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * (64 * i + trow_get(l)); }));
+  for (int k = 0; k < LFT * LFT; ++k)
+    emit("W frag write (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * (64 * k + l); }));
+  for (int o = 0; o < LFT; ++o)
+    emit("P partial write (S)", 16, 1, 2, lanes([&](int g, int n, int) {
+           return 16L * (64 * ((n >> 3) * PP + (o >> 1)) + 16 * g + (n & 7) + 8 * (o & 1));
+         }));
+  emit("M frag write (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * l; }));
+  for (int i = 0; i < LFT; ++i)
+    emit("XK tile row put (S)", 8, 1, 2, lanes([&](int g, int n, int) { return 8L * (64 * i + trow_put(n, g)); }));
+  for (int o = 0; o < LFT; ++o)
+    for (int j = 0; j < 4; ++j)
+      emit("G fp32 read (S)", 4, 1, 2, lanes([&](int g, int n, int) { return 4L * (o * GXT + 20 * (4 * g + j) + n); }));
+  for (int o = 0; o < LFT; ++o)
+    emit("b write (S)", 4, 1, 2, lanes([&](int g, int n, int) { return g == 0 ? 4L * (16 * o + n) : -1L; }));
+  for (int k = 0; k < LFT * LFT; ++k)
+    emit("W frag read (O)", 8, 1, 3, lanes([&](int, int, int l) { return 8L * (64 * k + l); }));
+  for (int o = 0; o < LFT; ++o) {
+    emit("b read (O)", 16, 1, 3, lanes([&](int g, int, int) { return 4L * (16 * o + 4 * g); }));
+    emit("G tile transposing read (O)", 8, 1, 3, tr(o));
+    for (int j = 0; j < 4; ++j)
+      emit("XH fp32 read (O)", 4, 1, 3, lanes([&](int g, int n, int) { return 4L * (4 * GXT + o * GXT + 20 * (4 * g + j) + n); }));
+  }
+  for (int a = 0; a < 2; ++a)
+    emit("row value read (O)", 16, 1, 3, lanes([&](int g, int, int) { return 4L * (16 * a + 4 * g); }));
+  std::printf("\n");
+  return 0;
+}
+
 int main(int argc, char** argv) {
   if (argc > 1 && std::string(argv[1]) == "--check") return check();
+  if (argc > 1 && std::string(argv[1]) == "--linear") return linear_rows();
   for (int w = 0; w < NW; ++w) {
     const int hs = 16 * HT * w;
     // W2^T [F][FF] by columns: the wave's view W2t starts at column hs

@@ -133,6 +133,47 @@ def test_linear_fwd_16bit(kind, dt):
     assert rel_l2(Wc, ref["W1_ckpt"]) <= BF16_RTOL
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("NC,G,F_", [(1, 1, 64), (2, 1, 64), (3, 2, 32), (5, 5, 64), (2, 2, 32), (7, 3, 64)])
+def test_linear_fwd_16bit_edges(dt, NC, G, F_):
+    """16-bit activations run the row-split kernel, whose state update enters
+    the next mini-batch as a look-ahead correction: one and two mini-batches,
+    groups that do and do not divide NC, F = 32.  Outputs and states against
+    the fp64 oracle (rel-L2 <= 2e-2); the saved slot against the relations it
+    must satisfy (fp32 rounding, 1e-4 of the magnitudes, where the kernel forms
+    the value in fp32; the state through the bf16 update operands, 2e-2)."""
+    _say("linear fwd 16-bit edges", dt, f"NC{NC} G{G} F{F_}")
+    B, H = 2, 2
+    d = O.make_inputs(B, H, NC, 16, F_, seed=30 + NC + F_, dtype=dt, eta_kind="causal")
+    gen = torch.Generator().manual_seed(31)
+    d["ln_w"] = 1 + 0.2 * torch.randn(H, F_, generator=gen)
+    d["ln_b"] = 0.2 * torch.randn(H, F_, generator=gen)
+    d["b1"] = 0.1 * torch.randn(B, H, 1, F_, generator=gen)
+    out, (Wc, bc), (Wl, bl), saved = _fwd(d, G=G, want_saved=True)
+    torch.cuda.synchronize()
+    ref = O.linear_forward_full(*(d[k].double() for k in ("ln_w", "ln_b", "W1", "b1", "XQ", "XV", "XK", "eta")), G=G)
+    for name, mine in (("out", out), ("W1_last", Wl), ("b1_last", bl), ("W1_ckpt", Wc), ("b1_ckpt", bc)):
+        err = rel_l2(mine, ref[name])
+        _say(f"  {name}: rel-L2 {err:.3e}")
+        assert err <= BF16_RTOL, name
+    sv = {k: v.cpu().double() for k, v in _unpack_saved(saved, B, H, NC, F_).items()}
+    XK, XV, XQ = d["XK"].double(), d["XV"].double(), d["XQ"].double()
+    e = d["eta"].double()[..., -1, :]
+    dW = torch.einsum("bhstf,bhst,bhsto->bhfo", XK, e, sv["G"])
+    assert rel_l2(Wl, d["W1"].double() - dW) <= BF16_RTOL
+    db = torch.einsum("bhst,bhsto->bho", e, sv["G"]).unsqueeze(2)
+    assert max_abs(bl, d["b1"].double() - db) <= 1e-4 * (1 + db.abs().max().item())
+    lw, lb = d["ln_w"].double()[None, :, None, None, :], d["ln_b"].double()[None, :, None, None, :]
+    xh = sv["XH"]
+    gx = (lw * xh + lb - (XV - XK)) * lw
+    Gr = (gx - gx.mean(-1, keepdim=True) - xh * sv["CC"][..., None]) * sv["RSTD"][..., None]
+    assert max_abs(Gr, sv["G"]) <= 1e-4 * (1 + sv["G"].abs().max().item())
+    assert max_abs(sv["CC"], (gx * xh).mean(-1)) <= 1e-4 * (1 + sv["CC"].abs().max().item())
+    assert max_abs(xh.mean(-1), torch.zeros_like(sv["RSTD"])) <= 1e-4
+    assert rel_l2(out, XQ + lw * sv["XHB"] + lb) <= 1e-2
+    assert bool((sv["RSB"] > 0).all()) and bool((sv["RSTD"] > 0).all())
+
+
 def test_linear_fwd_deterministic():
     _say("linear fwd determinism")
     d = O.make_inputs(2, 2, 8, 16, 64, seed=2, dtype=torch.bfloat16)

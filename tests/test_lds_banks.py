@@ -1,4 +1,5 @@
-"""LDS bank model of the MLP backward sweep's step (CPU).
+"""LDS bank model of the MLP backward sweep's step and the row-split Linear
+forward's step (CPU).
 
 tests/lds_banks_dump.cpp prints the per-lane LDS address of every LDS access
 one step of one wave of mlp_bwd_kernel issues (bf16, F = 64, FF = 256, four
@@ -12,17 +13,24 @@ joining quads 0 and 3 of one 16-lane group with quads 1 and 2 of the next
 (lanes 0-3, 12-15, 20-27 are one pass); lanes of a pass that reach the same
 dword do not conflict, and a pass takes as many cycles as the most distinct
 dwords any one bank serves.  16-byte writes are served in eight passes of
-8 consecutive lanes over 32 banks.  Probed values the model reproduces: the
+8 consecutive lanes over 32 banks, 8-byte writes in four passes of 16
+consecutive lanes over 32 banks.  Probed values the model reproduces: the
 replaced row-major layout's 16-byte rows and a block layout without the
 chunk permutation tau, 4 conflict cycles per read; the replaced lane-order
 dZ2 frag writes, 14 per write; 16-byte writes go in 8-lane passes over 32
-banks, so the tau layout's row writes take 8; the new layouts, 0.
+banks, so the tau layout's row writes take 8; the new layouts, 0.  8-byte
+writes: lane order 0; 16-bit tile rows at 4m + g (rows m and m + 4 in one
+16-lane pass) 4 per write, as the Linear forward's G and XK rows took before
+their swizzle.  ds_read_b64_tr_b16 reads as 8-byte reads do (lane order and
+the swizzled tiles, 0).
 
 Checked: the layouts are bijections and the kernel's address pieces reach
 the elements they mean (the dump's --check); every pattern is conflict-free
 but the readout column-sum write (one 2-way store per step); the modelled
 conflict cycles per LDS instruction of a step are below 0.1; and the model
-gives the probed counts for the replaced layouts.
+gives the probed counts for the replaced layouts.  --linear prints the
+row-split Linear forward's accesses (csrc/ttt_linear_fwd_rows.hip, F = 64,
+waves R0, R1, S, O); every one is conflict-free under the model.
 """
 
 import json
@@ -44,6 +52,8 @@ def passes(width, store=False):
     """Lane sets of the passes of one LDS instruction."""
     if width == 16 and store:
         return [list(range(8 * p, 8 * p + 8)) for p in range(8)]
+    if width == 8 and store:
+        return [list(range(16 * p, 16 * p + 16)) for p in range(4)]
     if width == 16:
         out = [[] for _ in range(4)]
         for l in range(64):
@@ -56,7 +66,7 @@ def passes(width, store=False):
 def pass_cycles(width, addrs, store=False):
     """Cycles of each pass of one LDS instruction under the model (an address
     of None: the lane is inactive)."""
-    banks = 32 if width <= 4 or (width == 16 and store) else 64
+    banks = 32 if width <= 4 or (width >= 8 and store) else 64
     out = []
     for lanes in passes(width, store):
         per_bank = defaultdict(set)
@@ -79,13 +89,21 @@ def extra_cycles(width, addrs, store=False):
 
 
 @pytest.fixture(scope="module")
-def dump(tmp_path_factory):
+def dump_exe(tmp_path_factory):
     exe = str(tmp_path_factory.mktemp("lds") / "dump")
     subprocess.run(["g++", "-std=c++17", "-O1", "-I", CSRC, SRC, "-o", exe], check=True)
-    check = json.loads(subprocess.run([exe, "--check"], check=True, capture_output=True, text=True).stdout)
-    pats = [json.loads(ln) for ln in subprocess.run([exe], check=True, capture_output=True,
+    return exe
+
+
+def _patterns(exe, *args):
+    return [json.loads(ln) for ln in subprocess.run([exe, *args], check=True, capture_output=True,
                                                     text=True).stdout.splitlines() if ln.strip()]
-    return check, pats
+
+
+@pytest.fixture(scope="module")
+def dump(dump_exe):
+    check = json.loads(subprocess.run([dump_exe, "--check"], check=True, capture_output=True, text=True).stdout)
+    return check, _patterns(dump_exe)
 
 
 def test_layouts_are_bijections_and_accesses_reach_their_elements(dump):
@@ -122,6 +140,18 @@ def test_bank_conflicts_per_pattern(dump):
     for name, (w, cnt, deg, ext) in rows.items():
         assert deg == EXPECTED_CONFLICTS.get(name, 1), name
     assert extra / insts <= 0.1
+
+
+def test_linear_rows_patterns_conflict_free(dump_exe):
+    pats = _patterns(dump_exe, "--linear")
+    waves = {p["wave"] for p in pats}
+    assert waves == {0, 1, 2, 3}
+    insts = 0
+    for p in pats:
+        assert all(a is None or a % p["width"] == 0 for a in p["addr"]), p["name"]
+        assert degree(p["width"], p["addr"], p["store"]) == 1, p["name"]
+        insts += p["count"]
+    print(f"\nrow-split Linear forward: {len(pats)} patterns, {insts} LDS instructions per step, no conflicts")
 
 
 def _old_row4(cols, g, n, b):
@@ -163,6 +193,11 @@ def test_model_gives_the_probed_counts():
     tau = (0, 3, 1, 2)
     addrs = [4 * (16 * (n ^ ((n >> 2) & 1)) + 4 * (tau[l >> 4] ^ (n >> 2))) for l in range(64) for n in [l & 15]]
     assert extra_cycles(16, addrs) == 0 and extra_cycles(16, addrs, store=True) == 8
+    # 8-byte writes: lane order none; 16-bit tile rows at 8 (4m + g), lane (g, n) at row n, and the
+    # G rows of tiles 66 8-byte places apart (lane (g, n): token n & 7, tile n >> 3): 4 per write
+    assert extra_cycles(8, [8 * l for l in range(64)], store=True) == 0
+    assert extra_cycles(8, [8 * (4 * (l & 15) + (l >> 4) + 2 * ((l & 15) >> 3)) for l in range(64)], store=True) == 4
+    assert extra_cycles(8, [8 * (66 * ((l & 15) >> 3) + 4 * (l & 7) + (l >> 4)) for l in range(64)], store=True) == 4
     # replaced lane-order dZ2 frag writes, element (row 4w + j, feature n of tile lo)
     # at 2-byte index (lo 64 + 16 (n >> 2) + 4w + j) 4 + (n & 3): 14 cycles
     for w in range(4):

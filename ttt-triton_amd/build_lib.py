@@ -45,6 +45,13 @@ COMMON = [
 ]
 
 
+# per-file additions: the row-split Linear forward keeps its MFMA accumulators
+# in VGPRs (its state wave converts W into operand frags every mini-batch)
+PER_FILE = {
+    "ttt_linear_fwd_rows.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
@@ -55,7 +62,7 @@ ASAN_DIR = os.path.join(HERE, "_build_asan")
 
 def _compile(src: str, verbose: bool, asan: bool = False) -> str:
     obj = os.path.join(ASAN_DIR if asan else BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *COMMON, *(ASAN if asan else []), "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(os.path.basename(src), []), *(ASAN if asan else []), "-c", src, "-o", obj]
     if verbose:
         cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -201,6 +201,7 @@ int layer_io_bwd_blocks(int B, int L);
 int layer_io_max_width();
 
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream);
+hipError_t launch_linear_fwd_rows(const LinearFwdParams& p, int dtype, hipStream_t stream);  // 16-bit activations
 hipError_t launch_linear_bwd(const LinearBwdParams& p, int dtype, hipStream_t stream);
 
 // ---- general-shape inner loops (ttt_generic.hip): K, F, FF multiples of 16

@@ -1,4 +1,5 @@
-// TTT-Linear mini-batch forward on gfx950.
+// TTT-Linear mini-batch forward on gfx950, fp32 activations (16-bit
+// activations run the row-split kernel of ttt_linear_fwd_rows.hip).
 //
 // One workgroup of two wavefronts per (batch, head) chain.  Per mini-batch of
 // K = 16 tokens (ops/ttt_linear.py:8-54, dual form with a full KxK eta):
@@ -382,12 +383,8 @@ static hipError_t launch_fwd(const LinearFwdParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_linear_fwd(const LinearFwdParams& p, int dtype, hipStream_t stream) {
-  if (dtype == TTT_DTYPE_BF16) {
-    if (p.F == 64) return launch_fwd<__bf16, 4>(p, stream);
-    if (p.F == 32) return launch_fwd<__bf16, 2>(p, stream);
-  } else if (dtype == TTT_DTYPE_F16) {
-    if (p.F == 64) return launch_fwd<_Float16, 4>(p, stream);
-    if (p.F == 32) return launch_fwd<_Float16, 2>(p, stream);
+  if (dtype == TTT_DTYPE_BF16 || dtype == TTT_DTYPE_F16) {
+    return launch_linear_fwd_rows(p, dtype, stream);
   } else {
     if (p.F == 64) return launch_fwd<float, 4>(p, stream);
     if (p.F == 32) return launch_fwd<float, 2>(p, stream);
