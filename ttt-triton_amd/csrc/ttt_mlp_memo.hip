@@ -142,7 +142,12 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
   constexpr int K = 16;
   constexpr int FPL = F / 16;
   constexpr int NSUB = kMemoThreads / 64;
-  __shared__ float xs[kTokBlk][F + 1];  // XU rows in fp32 (padded: conflict-free column reads)
+  // XU rows in fp32, padded (the column reads of 32 rows reach 32 banks) and
+  // column f at f ^ ((f >> 4) & 2) (the row writes of 16 threads, four
+  // columns each, reach 32 banks: columns f and f + 32 of one row would share
+  // one at F = 64)
+  __shared__ float xs[kTokBlk][F + 1];
+  auto xcol = [](int f) { return f ^ ((f >> 4) & 2); };
   __shared__ __align__(16) float sm[kSegChunk][F];
   __shared__ float red[2][NSUB][kTokBlk];
   const int NC = p.NC, M = p.M, NS = p.NS, NT = NC * K;
@@ -164,7 +169,7 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
       float x[FPL];
       load_n<FPL>(static_cast<const T*>(p.XU) + ((size_t)chain * NT + min(tb + tk, NT - 1)) * F + FPL * q, x);
 #pragma unroll
-      for (int k = 0; k < FPL; ++k) xs[tk][FPL * q + k] = x[k];
+      for (int k = 0; k < FPL; ++k) xs[tk][xcol(FPL * q + k)] = x[k];
     }
   }
   const int sub = threadIdx.x >> 6, tk = threadIdx.x & 63;
@@ -174,7 +179,7 @@ __global__ __launch_bounds__(kMemoThreads, 5) void memo_gate_kernel(MlpMemoParam
   __syncthreads();
   float x[F];
 #pragma unroll
-  for (int f = 0; f < F; ++f) x[f] = xs[tk][f];
+  for (int f = 0; f < F; ++f) x[f] = xs[tk][xcol(f)];
   auto logit = [&](int jj) {
     const f4* sj = reinterpret_cast<const f4*>(sm[jj]);
     float s = 0.f;
