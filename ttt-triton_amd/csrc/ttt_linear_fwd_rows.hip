@@ -31,7 +31,11 @@
 // G goes through LDS as 16-bit rows (-G, and -(e o G) for the update) that
 // every consumer reads back with ds_read_b64_tr_b16, which is the transpose
 // the token-major operands need, and as fp32 rows with XH for S and O (the
-// saved slot's token-major tiles, written as 16-byte rows).  One barrier per
+// saved slot's token-major tiles, written as 16-byte rows).  XK is loaded
+// from HBM by S alone, which stages it in LDS as 16-bit rows for the other
+// three waves (R's rows, O's frags, S's own transposing read): the waves
+// share the CU's memory pipeline, and the shared XK took the kernel from
+// 199.6 to 186 us.  One barrier per
 // mini-batch; every handoff double-buffered by parity.  The products keep
 // their accumulators in VGPRs (this file is compiled with
 // -amdgpu-mfma-vgpr-form, so converting W into operand frags reads no
@@ -61,7 +65,9 @@ template <typename T, int FT> struct LinRowsPar {
 };
 template <typename T, int FT> struct LinRowsShared {
   LinRowsPar<T, FT> par[2];
-  u2v xkt[FT][64];                          // XK_s as 16-bit rows (xkt_put), for the transposing read
+  u2v xkt[3][FT][64];                       // XK_s in slot s % 3 as 16-bit rows (grow_put per tile):
+                                            // S writes XK_{s+1} while mini-batch s runs; R reads XK_s's
+                                            // rows, O XK_{s-1}'s frags, S XK_{s-1} transposed
 };
 
 typedef short s4v __attribute__((ext_vector_type(4)));
@@ -87,8 +93,6 @@ template <typename T> __device__ __forceinline__ Frag<T> bits_frag(u2v v) {
 // transposing reads)
 using lds::grow_get;
 using lds::grow_put;
-__device__ __forceinline__ int xkt_put(int m, int g) { return lds::trow_put(m, g); }
-__device__ __forceinline__ int xkt_get(int l) { return lds::trow_get(l); }
 
 // lane (g, n) of R_w's packed form: own value of tile 2p + w where n >> 3 == w,
 // else tile 2p + 1 - w from lane n ^ 8 (row_ror:8 within the 16-lane row)
@@ -114,7 +118,6 @@ __device__ __forceinline__ void linear_rows_chain(const LinearFwdParams& p, LinR
   const int NC = p.NC;
   const int l = lane_id(), g = l >> 4, n = l & 15, hi = n >> 3;
   const int t = (n & 7) + 8 * W;  // this lane's token in the packed form
-  const T* __restrict__ XK = static_cast<const T*>(p.XK) + (size_t)chain * NC * K * F;
   const T* __restrict__ XV = static_cast<const T*>(p.XV) + (size_t)chain * NC * K * F;
   const ET* __restrict__ ETA = LR ? nullptr : static_cast<const ET*>(p.eta) + (size_t)chain * NC * K * K;
   const float* __restrict__ LRP = LR ? static_cast<const float*>(p.eta) + (size_t)chain * NC * K : nullptr;
@@ -131,17 +134,12 @@ __device__ __forceinline__ void linear_rows_chain(const LinearFwdParams& p, LinR
     lnb_pk[q] = *reinterpret_cast<const f4*>(p.ln_b + h * F + f0);
   }
   // XV and XK of token t (packed) and eta[K-1][t] of the next mini-batch, raw
-  VT tv_n[PP], tk_n[PP];
+  VT tv_n[PP];
   EOne et_n;
   auto load_row = [&](int s) {
-    const T* k = XK + (size_t)s * K * F + t * F;
     const T* v = XV + (size_t)s * K * F + t * F;
 #pragma unroll
-    for (int q = 0; q < PP; ++q) {
-      const int f0 = 16 * (2 * q + hi) + 4 * g;
-      tv_n[q] = *reinterpret_cast<const VT*>(v + f0);
-      tk_n[q] = *reinterpret_cast<const VT*>(k + f0);
-    }
+    for (int q = 0; q < PP; ++q) tv_n[q] = *reinterpret_cast<const VT*>(v + 16 * (2 * q + hi) + 4 * g);
     if constexpr (LR)
       et_n = LRP[(size_t)s * K + t];
     else
@@ -156,7 +154,7 @@ __device__ __forceinline__ void linear_rows_chain(const LinearFwdParams& p, LinR
 #pragma unroll
     for (int q = 0; q < PP; ++q) {
       tv[q] = tv_n[q];
-      tk[q] = tk_n[q];
+      tk[q] = __builtin_bit_cast(VT, sh.xkt[s % 3][2 * q + hi][grow_put(2 * q + hi, t, g)]);  // XK_s, token t
     }
     const EOne et = et_n;
     if (s + 1 < NC) load_row(s + 1);
@@ -323,7 +321,8 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
     for (int o = 0; o < FT; ++o) {
       pr.gneg[o][l] = z2;
       pr.geta[o][l] = z2;
-      sh.xkt[o][xkt_put(n, g)] = z2;
+      sh.xkt[2][o][grow_put(o, n, g)] = z2;
+      sh.xkt[0][o][grow_put(o, n, g)] = frag_bits(xk_cur[o]);
     }
     pr.mt[l] = z2;
     if (g == 0) {
@@ -350,7 +349,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
 #pragma unroll
       for (int o = 0; o < FT; ++o) geT[o] = lds_read_tr<T>(&prv.geta[o][grow_get(o, l)]);
 #pragma unroll
-      for (int i = 0; i < FT; ++i) xkT[i] = lds_read_tr<T>(&sh.xkt[i][xkt_get(l)]);
+      for (int i = 0; i < FT; ++i) xkT[i] = lds_read_tr<T>(&sh.xkt[(s + 2) % 3][i][grow_get(i, l)]);
 #pragma unroll
       for (int i = 0; i < FT; ++i)
 #pragma unroll
@@ -399,7 +398,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
       cur.mt[l] = frag_bits(to_frag<T>((cm[0][0].v + 1.0f) * e));
     }
 #pragma unroll
-    for (int i = 0; i < FT; ++i) sh.xkt[i][xkt_put(n, g)] = frag_bits(xk_cur[i]);
+    for (int i = 0; i < FT; ++i) sh.xkt[(s + 1) % 3][i][grow_put(i, n, g)] = frag_bits(xk_nxt[i]);  // XK_{s+1}
 #pragma unroll
     for (int c = 0; c < FT; ++c) {
       xk_cur[c] = xk_nxt[c];
@@ -417,7 +416,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
 #pragma unroll
     for (int o = 0; o < FT; ++o) geT[o] = lds_read_tr<T>(&last.geta[o][grow_get(o, l)]);
 #pragma unroll
-    for (int i = 0; i < FT; ++i) xkT[i] = lds_read_tr<T>(&sh.xkt[i][xkt_get(l)]);
+    for (int i = 0; i < FT; ++i) xkT[i] = lds_read_tr<T>(&sh.xkt[(NC - 1) % 3][i][grow_get(i, l)]);
 #pragma unroll
     for (int i = 0; i < FT; ++i)
 #pragma unroll
@@ -476,16 +475,12 @@ __global__ __launch_bounds__(256) void linear_fwd_rows_kernel(LinearFwdParams p)
       lnw_fm[o][j] = p.ln_w[h * F + 16 * o + 4 * g + j];
       lnb_fm[o][j] = p.ln_b[h * F + 16 * o + 4 * g + j];
     }
-  Frag<T> nq[1][FT], nk[1][FT];
+  Frag<T> nq[1][FT];
   ERaw n_etaT;
   auto load_step = [&](int s) {
     const T* q = XQ + (size_t)s * K * F;
-    const T* k = XK + (size_t)s * K * F;
 #pragma unroll
-    for (int c = 0; c < FT; ++c) {
-      nq[0][c] = load_frag(q, F, 16 * c);
-      nk[0][c] = load_frag(k, F, 16 * c);
-    }
+    for (int c = 0; c < FT; ++c) nq[0][c] = load_frag(q, F, 16 * c);
     if constexpr (LR)
       n_etaT = *reinterpret_cast<const f4*>(LRP + (size_t)s * K + 4 * g);  // lane (g,*): lr[4g+j]
     else
@@ -500,7 +495,7 @@ __global__ __launch_bounds__(256) void linear_fwd_rows_kernel(LinearFwdParams p)
 #pragma unroll
     for (int c = 0; c < FT; ++c) {
       xq[0][c] = nq[0][c];
-      xk[0][c] = nk[0][c];
+      xk[0][c] = bits_frag<T>(sh.xkt[s % 3][c][grow_put(c, n, g)]);  // XK_s (lane (g, n): row n)
     }
     const ERaw etaT_raw = n_etaT;
     if (s + 1 < NC) load_step(s + 1);
