@@ -161,7 +161,8 @@ int check() {
 // readout).  Arrays as LinRowsPar / LinRowsShared declare them: wf [16][64]
 // 8-byte frags, b [64] fp32, gneg and geta [4][64] 8-byte tile rows, pp
 // [2][2][64] 16-byte rows, mt [64] 8-byte frags, gx [2][4][16][20] fp32 (rows
-// padded to 20), rc [2][16] fp32, xkt [4][64] 8-byte tile rows.
+// padded to 20), rc [2][16] fp32, xkt [3][4][64] 8-byte tile rows (one slot
+// shown: the three are alike).
 int linear_rows() {
   constexpr int LFT = 4, PP = 2, GXT = 16 * 20;
   auto tr = [&](int o) { return lanes([&](int, int, int l) { return 8L * (64 * o + grow_get(o, l)); }); };
@@ -172,6 +173,11 @@ int linear_rows() {
       emit("b read (R)", 16, 1, w, lanes([&](int g, int n, int) { return 4L * (16 * (2 * q + (n >> 3)) + 4 * g); }));
     }
     emit("M frag read (R)", 8, 1, w, lanes([&](int, int, int l) { return 8L * l; }));
+    for (int q = 0; q < PP; ++q)  // XK_s of token (n & 7) + 8w from the staging ring
+      emit("XK row read (R)", 8, 1, w, lanes([&](int g, int n, int) {
+             const int o = 2 * q + (n >> 3), t = (n & 7) + 8 * w;
+             return 8L * (64 * o + grow_put(o, t, g));
+           }));
     for (int q = 0; q < PP; ++q) {
       // -G and -(e o G): lane (g, n) holds token (n & 7) + 8w of tile 2q + (n >> 3)
       emit("G tile row put (R)", 8, 2, w, lanes([&](int g, int n, int) {
@@ -188,7 +194,7 @@ int linear_rows() {
   }
   for (int o = 0; o < LFT; ++o) emit("e G tile transposing read (S)", 8, 1, 2, tr(o));
   for (int i = 0; i < LFT; ++i)
-    emit("XK tile transposing read (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * (64 * i + trow_get(l)); }));
+    emit("XK tile transposing read (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * (64 * i + grow_get(i, l)); }));
   for (int k = 0; k < LFT * LFT; ++k)
     emit("W frag write (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * (64 * k + l); }));
   for (int o = 0; o < LFT; ++o)
@@ -197,7 +203,7 @@ int linear_rows() {
          }));
   emit("M frag write (S)", 8, 1, 2, lanes([&](int, int, int l) { return 8L * l; }));
   for (int i = 0; i < LFT; ++i)
-    emit("XK tile row put (S)", 8, 1, 2, lanes([&](int g, int n, int) { return 8L * (64 * i + trow_put(n, g)); }));
+    emit("XK tile row put (S)", 8, 1, 2, lanes([&](int g, int n, int) { return 8L * (64 * i + grow_put(i, n, g)); }));
   for (int o = 0; o < LFT; ++o)
     for (int j = 0; j < 4; ++j)
       emit("G fp32 read (S)", 4, 1, 2, lanes([&](int g, int n, int) { return 4L * (o * GXT + 20 * (4 * g + j) + n); }));
@@ -205,6 +211,8 @@ int linear_rows() {
     emit("b write (S)", 4, 1, 2, lanes([&](int g, int n, int) { return g == 0 ? 4L * (16 * o + n) : -1L; }));
   for (int k = 0; k < LFT * LFT; ++k)
     emit("W frag read (O)", 8, 1, 3, lanes([&](int, int, int l) { return 8L * (64 * k + l); }));
+  for (int c = 0; c < LFT; ++c)  // XK_{s-1} operand frags (lane (g, n): row n) from the staging ring
+    emit("XK frag read (O)", 8, 1, 3, lanes([&](int g, int n, int) { return 8L * (64 * c + grow_put(c, n, g)); }));
   for (int o = 0; o < LFT; ++o) {
     emit("b read (O)", 16, 1, 3, lanes([&](int g, int, int) { return 4L * (16 * o + 4 * g); }));
     emit("G tile transposing read (O)", 8, 1, 3, tr(o));
