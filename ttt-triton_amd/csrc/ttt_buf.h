@@ -49,18 +49,15 @@ template <> __device__ __forceinline__ Frag<float> bload_frag<float>(rsrc_t r, i
   return f;
 }
 
-// Stores take a cache policy CP: 0, or kCpolStream (nt) for data that only a
-// later kernel reads back (a forward's saved activations, checkpoints and
-// outputs): such lines stream through L2 instead of displacing the lines the
-// kernel still reads.  The MLP forward at B16 H12 T2048 writes ~2 GB of them
-// per call and ran 10% faster with them streamed.
-constexpr int kCpolStream = 2;  // nt
-template <typename T, int CP = 0> __device__ __forceinline__ void bstore_frag(rsrc_t r, int voff, int soff, Frag<T> f) {
-  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "16-bit or fp32 frags");
-  if constexpr (sizeof(T) == 4)
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f.v), r, voff, soff, CP);
-  else
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, CP);
+template <typename T> __device__ __forceinline__ void bstore_frag(rsrc_t r, int voff, int soff, Frag<T> f);
+template <> __device__ __forceinline__ void bstore_frag<__bf16>(rsrc_t r, int voff, int soff, Frag<__bf16> f) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_frag<_Float16>(rsrc_t r, int voff, int soff, Frag<_Float16> f) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f.v), r, voff, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_frag<float>(rsrc_t r, int voff, int soff, Frag<float> f) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f.v), r, voff, soff, 0);
 }
 
 // Device-coherent stores (cache policy sc1): written through to memory, so a
@@ -114,8 +111,8 @@ template <> __device__ __forceinline__ float bload1<float>(rsrc_t r, int voff, i
 __device__ __forceinline__ float bload_f32(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
-template <int CP = 0> __device__ __forceinline__ void bstore_f32(rsrc_t r, int voff, int soff, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voff, soff, CP);
+__device__ __forceinline__ void bstore_f32(rsrc_t r, int voff, int soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voff, soff, 0);
 }
 
 // C-layout tile of a row-major fp32 matrix (row stride ld elements) at
@@ -127,10 +124,9 @@ __device__ __forceinline__ Tile bload_tile(rsrc_t r, int lane, int soff, int ld,
   for (int j = 0; j < 4; ++j) t.v[j] = bload_f32(r, lane, soff + ((r0 + j) * ld + c0) * 4);
   return t;
 }
-template <int CP = 0>
 __device__ __forceinline__ void bstore_tile(rsrc_t r, int lane, int soff, int ld, int r0, int c0, Tile t) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) bstore_f32<CP>(r, lane, soff + ((r0 + j) * ld + c0) * 4, t.v[j]);
+  for (int j = 0; j < 4; ++j) bstore_f32(r, lane, soff + ((r0 + j) * ld + c0) * 4, t.v[j]);
 }
 
 // C-layout tile of a row-major [16 x ld] block in the activation type: lane
@@ -161,17 +157,22 @@ template <> __device__ __forceinline__ Frag<float> bload_ctile<float>(rsrc_t r, 
   for (int j = 0; j < 4; ++j) f.v[j] = bload_f32(r, voff + j * ld * 4, soff);
   return f;
 }
-template <typename T, int CP = 0>
-__device__ __forceinline__ void bstore_ctile(rsrc_t r, int voff, int soff, int ld, Frag<T> f) {
-  if constexpr (sizeof(T) == 4) {
+template <typename T> __device__ __forceinline__ void bstore_ctile(rsrc_t r, int voff, int soff, int ld, Frag<T> f);
+template <> __device__ __forceinline__ void bstore_ctile<__bf16>(rsrc_t r, int voff, int soff, int ld, Frag<__bf16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 u = __builtin_bit_cast(us4, f.v);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bstore_f32<CP>(r, voff + j * ld * 4, soff, f.v[j]);
-  } else {
-    typedef unsigned short us4 __attribute__((ext_vector_type(4)));
-    const us4 u = __builtin_bit_cast(us4, f.v);
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(u[j], r, voff + j * ld * 2, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_ctile<_Float16>(rsrc_t r, int voff, int soff, int ld, Frag<_Float16> f) {
+  typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+  const us4 u = __builtin_bit_cast(us4, f.v);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(u[j], r, voff + j * ld * 2, soff, CP);
-  }
+  for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b16(u[j], r, voff + j * ld * 2, soff, 0);
+}
+template <> __device__ __forceinline__ void bstore_ctile<float>(rsrc_t r, int voff, int soff, int ld, Frag<float> f) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bstore_f32(r, voff + j * ld * 4, soff, f.v[j]);
 }
 
 }  // namespace ttt

@@ -35,11 +35,7 @@
 // from HBM by S alone, which stages it in LDS as 16-bit rows for the other
 // three waves (R's rows, O's frags, S's own transposing read): the waves
 // share the CU's memory pipeline, and the shared XK took the kernel from
-// 199.6 to 186 us.  Every store (the saved slot, checkpoints, the output)
-// uses the streaming cache policy (kCpolStream, or nontemporal through plain
-// pointers): no later access in this kernel reads them, and streaming them
-// took the kernel 190 -> 152 us (saved slot) -> 148 us (the rest) in A/Bs.
-// One barrier per
+// 199.6 to 186 us.  One barrier per
 // mini-batch; every handoff double-buffered by parity.  The products keep
 // their accumulators in VGPRs (this file is compiled with
 // -amdgpu-mfma-vgpr-form, so converting W into operand frags reads no
@@ -56,21 +52,6 @@
 #include "ttt_kernels.h"
 
 namespace ttt {
-
-// streamed (nontemporal) stores through plain pointers: a C-layout tile of a
-// row-major fp32 matrix, and lane (g, n)'s four values of row n at c0 + 4g
-__device__ __forceinline__ void nt_store_tile(float* __restrict__ x, int ld, int r0, int c0, Tile t) {
-  const int l = lane_id();
-  const int g = l >> 4, n = l & 15;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) __builtin_nontemporal_store(t.v[j], &x[(r0 + 4 * g + j) * ld + c0 + n]);
-}
-template <typename T> __device__ __forceinline__ void nt_store_f4(T* __restrict__ x, int ld, int c0, f4 v) {
-  const int l = lane_id();
-  const int g = l >> 4, r = l & 15;
-  const u2v u = __builtin_bit_cast(u2v, to_frag<T>(v).v);
-  __builtin_nontemporal_store(u, reinterpret_cast<u2v*>(x + r * ld + c0 + 4 * g));
-}
 
 template <typename T, int FT> struct LinRowsPar {
   typename FragT<T>::type wf[FT * FT][64];  // W_s operand frags [o * FT + i]
@@ -318,7 +299,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
       f4 gv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) gv[j] = src.gx[0][o][4 * g + j][n];
-      bstore_frag<float, kCpolStream>(SV, 16 * l + 1024 * o, sv + Slot2::G, Frag<float>{gv});
+      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot2::G, Frag<float>{gv});
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc += e[j] * gv[j];
@@ -385,7 +366,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
 #pragma unroll
       for (int i = 0; i < FT; ++i)
 #pragma unroll
-        for (int o = 0; o < FT; ++o) nt_store_tile(wc, F, 16 * i, 16 * o, W[i][o]);
+        for (int o = 0; o < FT; ++o) store_tile(wc, F, 16 * i, 16 * o, W[i][o]);
       if (g == 0) {
 #pragma unroll
         for (int o = 0; o < FT; ++o) p.b_ckpt[((size_t)chain * p.NK + kk) * F + 16 * o + n] = bn[o];
@@ -441,7 +422,7 @@ __device__ __forceinline__ void linear_rows_state(const LinearFwdParams& p, LinR
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
         mma16(W[i][o].v, xkT[i], geT[o]);
-        nt_store_tile(p.W_last + (size_t)chain * F * F, F, 16 * i, 16 * o, W[i][o]);
+        store_tile(p.W_last + (size_t)chain * F * F, F, 16 * i, 16 * o, W[i][o]);
       }
     if (g == 0) {
 #pragma unroll
@@ -526,10 +507,10 @@ __global__ __launch_bounds__(256) void linear_fwd_rows_kernel(LinearFwdParams p)
       f4 xv;
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[j] = hs.gx[1][o][4 * g + j][n];
-      bstore_frag<float, kCpolStream>(SV, 16 * l + 1024 * o, sv + Slot::XH, Frag<float>{xv});
+      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XH, Frag<float>{xv});
     }
-    bstore_frag<float, kCpolStream>(SV, 16 * g, sv + Slot::RSTD, Frag<float>{*reinterpret_cast<const f4*>(&hs.rc[0][4 * g])});
-    bstore_frag<float, kCpolStream>(SV, 16 * g, sv + Slot::CC, Frag<float>{*reinterpret_cast<const f4*>(&hs.rc[1][4 * g])});
+    bstore_frag<float>(SV, 16 * g, sv + Slot::RSTD, Frag<float>{*reinterpret_cast<const f4*>(&hs.rc[0][4 * g])});
+    bstore_frag<float>(SV, 16 * g, sv + Slot::CC, Frag<float>{*reinterpret_cast<const f4*>(&hs.rc[1][4 * g])});
 
     // Zb^T = W^T XQ^T (feature-major) - G^T (eta o A + eta)^T + b
     Frag<T> Wf[FT][FT];
@@ -584,10 +565,10 @@ __global__ __launch_bounds__(256) void linear_fwd_rows_kernel(LinearFwdParams p)
         xhb[j] = (zb[o][0].v[j] - m) * rs;
         y[j] = q[j] + lnw_fm[o][j] * xhb[j] + lnb_fm[o][j];
       }
-      nt_store_f4<T>(o_s, F, 16 * o, y);
-      bstore_frag<float, kCpolStream>(SV, 16 * l + 1024 * o, sv + Slot::XHB, Frag<float>{xhb});
+      store_f4(o_s, F, 16 * o, y);
+      bstore_frag<float>(SV, 16 * l + 1024 * o, sv + Slot::XHB, Frag<float>{xhb});
     }
-    bstore_f32<kCpolStream>(SV, 4 * n, sv + Slot::RSB, rs);  // per token: the 4 lanes of token n agree
+    bstore_f32(SV, 4 * n, sv + Slot::RSB, rs);  // per token: the 4 lanes of token n agree
   };
   for (int s = 0; s < NC; ++s) {
     if (s > 0) readout(s - 1);

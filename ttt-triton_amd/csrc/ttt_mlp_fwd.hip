@@ -30,12 +30,6 @@
 // eta is read per mini-batch either as the dense [K x K] block or, with LR,
 // as the K learning rates that the eta rule expands on chip (ttt_eta.h).
 //
-// Every store (the saved slot, ~75 KB per mini-batch at F = 64, FF = 256 in
-// bf16; checkpoints; memo snapshots; the output) uses the streaming cache
-// policy (kCpolStream): no later access in this kernel reads them, and at
-// B16 H12 T2048 the forward ran 802 -> 720 us with them streamed (the same
-// stores cost ~40 us at B8, ~140 us at B16 with the default policy).
-//
 // Slabs are read through buffer resources; the next mini-batch's XQ and XK
 // are requested right after the first barrier of the current one, before its
 // stores (gfx9 retires loads and stores in issue order), so they arrive while
@@ -153,13 +147,13 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
     for (int i = 0; i < FT; ++i)
 #pragma unroll
       for (int o = 0; o < HT; ++o)
-        bstore_frag<float, kCpolStream>(r1, w1r, (16 * i * FF + 16 * o) * 4, Frag<float>{transpose16(Frag<float>{W1[i][o].v}, I32).v});
+        bstore_frag<float>(r1, w1r, (16 * i * FF + 16 * o) * 4, Frag<float>{transpose16(Frag<float>{W1[i][o].v}, I32).v});
     if (w2d != nullptr) {
       const rsrc_t r2 = make_rsrc(w2d, FF * F * 4);
 #pragma unroll
       for (int i = 0; i < HT; ++i)
 #pragma unroll
-        for (int o = 0; o < FT; ++o) bstore_tile<kCpolStream>(r2, w2l, 0, F, 16 * i, 16 * o, W2[i][o]);
+        for (int o = 0; o < FT; ++o) bstore_tile(r2, w2l, 0, F, 16 * i, 16 * o, W2[i][o]);
     }
     if (g == 0 && b1d != nullptr) {
 #pragma unroll
@@ -242,9 +236,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           gp[o][j] = dy;
           gpp[o][j] = ddy;
         }
-        bstore_frag<T, kCpolStream>(rSV, g1l + o * 256 * ST, us + Slot::SP1, to_frag<T>(gp[o]));
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1, to_frag<T>(gp[o]));
         x2f[o] = to_frag<T>(x2);
-        bstore_frag<T, kCpolStream>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2, x2f[o]);
         x2F[0][o] = to_frag<T>(transpose16(x2f[o], I).v);
       }
     }
@@ -300,10 +294,10 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
       sh.g2[lo][16 * wave + n] = g2;
       // saved G2, XH (this wave's rows of every tile) and the row statistics
       const int sv = (lo * 64 + 16 * wave + n) * 16;
-      bstore_frag<float, kCpolStream>(rSV, sv, us + Slot::G2, Frag<float>{g2});
-      bstore_frag<float, kCpolStream>(rSV, sv, us + Slot::XH, Frag<float>{xh});
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSTD, Frag<float>{rs});
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::CC, Frag<float>{cc});
+      bstore_frag<float>(rSV, sv, us + Slot::G2, Frag<float>{g2});
+      bstore_frag<float>(rSV, sv, us + Slot::XH, Frag<float>{xh});
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSTD, Frag<float>{rs});
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::CC, Frag<float>{cc});
       __syncthreads();  // G2 rows of every wave in
 #pragma unroll
       for (int o = 0; o < FT; ++o) G2[o].v = sh.g2[o][l];
@@ -327,11 +321,11 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
 #pragma unroll
       for (int c = 0; c < FT; ++c) {
         const int v = keep_or_drop(f4l + c * 1024, c % NW == wave);
-        bstore_frag<float, kCpolStream>(rSV, v, us + Slot::G2, Frag<float>{G2[c].v});
-        bstore_frag<float, kCpolStream>(rSV, v, us + Slot::XH, Frag<float>{ln.xh[c]});
+        bstore_frag<float>(rSV, v, us + Slot::G2, Frag<float>{G2[c].v});
+        bstore_frag<float>(rSV, v, us + Slot::XH, Frag<float>{ln.xh[c]});
       }
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSTD, Frag<float>{ln.rstd});
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::CC, Frag<float>{ln.c});
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSTD, Frag<float>{ln.rstd});
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::CC, Frag<float>{ln.c});
     }
 
     // ---- G1 = (G2 W2^T) (.) gelu'(Z1); W2^T blocks by exact transposes
@@ -349,9 +343,9 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           const Frag<T> t1 = to_frag<T>(transpose16(to_frag<T>(W2[i][q + 1].v), I).v);
           mma32(G1[i].v, g2F[0][q], g2F[0][q + 1], t0, t1);
         }
-        bstore_frag<T, kCpolStream>(rSV, g1l + i * 256 * ST, us + Slot::H1, to_frag<T>(G1[i].v * gpp[i]));
+        bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::H1, to_frag<T>(G1[i].v * gpp[i]));
         G1[i].v *= gp[i];
-        bstore_frag<T, kCpolStream>(rSV, g1l + i * 256 * ST, us + Slot::G1, to_frag<T>(G1[i].v));
+        bstore_frag<T>(rSV, g1l + i * 256 * ST, us + Slot::G1, to_frag<T>(G1[i].v));
       }
     }
 
@@ -381,8 +375,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           x2b[j] = y;
           sp[j] = dy;
         }
-        bstore_frag<T, kCpolStream>(rSV, g1l + o * 256 * ST, us + Slot::X2B, to_frag<T>(x2b));
-        bstore_frag<T, kCpolStream>(rSV, g1l + o * 256 * ST, us + Slot::SP1B, to_frag<T>(sp));
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::X2B, to_frag<T>(x2b));
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::SP1B, to_frag<T>(sp));
         x2bF[0][o] = to_frag<T>(transpose16(to_frag<T>(x2b), I).v);
       }
     }
@@ -431,8 +425,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g1e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b1_tm[o] -= d;
-        bstore_frag<T, kCpolStream>(rSV, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
-        bstore_f32<kCpolStream>(rSV, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);  // the 4 lanes of column n agree
+        bstore_frag<T>(rSV, g1l + o * 256 * ST, us + Slot::G1E, g1e[o]);
+        bstore_f32(rSV, (hs + n) * 4 + 64 * o, us + Slot::B1D, d);  // the 4 lanes of column n agree
       }
 #pragma unroll
       for (int o = 0; o < FT; ++o) {
@@ -446,8 +440,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         g2e[o] = to_frag<T>(v);
         const float d = sum_col4(acc);
         b2_tm[o] -= d;
-        bstore_frag<T, kCpolStream>(rSV, keep_or_drop(g2l + o * 256 * ST, wave == 0), us + Slot::G2E, g2e[o]);
-        bstore_f32<kCpolStream>(rSV, keep_or_drop(n * 4 + 64 * o, wave == 0), us + Slot::B2D, d);
+        bstore_frag<T>(rSV, keep_or_drop(g2l + o * 256 * ST, wave == 0), us + Slot::G2E, g2e[o]);
+        bstore_f32(rSV, keep_or_drop(n * 4 + 64 * o, wave == 0), us + Slot::B2D, d);
       }
 #pragma unroll
       for (int i = 0; i < FT; ++i)
@@ -468,7 +462,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         f4 a2 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < NW; ++w) a2 += sh.a2p[w][l];
-        bstore_tile<kCpolStream>(rSV, a2l, us + Slot::A2T, 16, 0, 0, Tile{a2});
+        bstore_tile(rSV, a2l, us + Slot::A2T, 16, 0, 0, Tile{a2});
       }
       const int lo = l >> 4;
       f4 z = f4{0.f, 0.f, 0.f, 0.f};
@@ -486,15 +480,15 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         xhb[j] = d[j] * rs[j];
         y[j] = q[j] + lnw_l * xhb[j] + lnb_l;
       }
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSB, Frag<float>{rs});
-      bstore_frag<float, kCpolStream>(rSV, (lo * 64 + 16 * wave + n) * 16, us + Slot::XHB, Frag<float>{xhb});
-      bstore_ctile<T, kCpolStream>(rOUT, l * ST, xo + 4 * wave * F * ST, F, to_frag<T>(y));
+      bstore_frag<float>(rSV, keep_or_drop((16 * wave + n) * 16, lo == 0), us + Slot::RSB, Frag<float>{rs});
+      bstore_frag<float>(rSV, (lo * 64 + 16 * wave + n) * 16, us + Slot::XHB, Frag<float>{xhb});
+      bstore_ctile<T>(rOUT, l * ST, xo + 4 * wave * F * ST, F, to_frag<T>(y));
     } else {
       Tile a2[1];
       a2[0].v = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NW; ++w) a2[0].v += sh.a2p[w][l];
-      bstore_tile<kCpolStream>(rSV, keep_or_drop(a2l, wave == 0), us + Slot::A2T, 16, 0, 0, a2[0]);
+      bstore_tile(rSV, keep_or_drop(a2l, wave == 0), us + Slot::A2T, 16, 0, 0, a2[0]);
       f4 m2;
 #pragma unroll
       for (int j = 0; j < 4; ++j) m2[j] = -(etaT[j] * a2[0].v[j] + etaT[j]);
@@ -527,7 +521,7 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
         }
         rs[j] = rsqrt_f(sum_row16(acc) * invF + eps);
       }
-      bstore_frag<float, kCpolStream>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSB, Frag<float>{rs});
+      bstore_frag<float>(rSV, keep_or_drop(f4l, wave == 0), us + Slot::RSB, Frag<float>{rs});
       if constexpr (NW == FT) {
         // one tile per wave: tile o = wave, picked out of the register arrays
         // by uniform selects
@@ -548,8 +542,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
           xhb[j] = (zo[j] - mu[j]) * rs[j];
           y[j] = q[j] + lnw_own * xhb[j] + lnb_own;
         }
-        bstore_frag<float, kCpolStream>(rSV, f4l + o * 1024, us + Slot::XHB, Frag<float>{xhb});
-        bstore_frag<T, kCpolStream>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
+        bstore_frag<float>(rSV, f4l + o * 1024, us + Slot::XHB, Frag<float>{xhb});
+        bstore_frag<T>(rOUT, xl + 16 * o * ST, xo, to_frag<T>(transpose16(to_frag<T>(y), I).v));
       } else {
         // every wave forms every tile; tile o is written by wave o % NW
 #pragma unroll
@@ -562,8 +556,8 @@ __global__ __launch_bounds__(64 * NW) void mlp_fwd_kernel(MlpFwdParams p) {
             xhb[j] = (z2b[o].v[j] - mu[j]) * rs[j];
             y[j] = q[j] + lnw_tm[o] * xhb[j] + lnb_tm[o];
           }
-          bstore_frag<float, kCpolStream>(rSV, keep_or_drop(f4l + o * 1024, mine), us + Slot::XHB, Frag<float>{xhb});
-          bstore_frag<T, kCpolStream>(rOUT, keep_or_drop(xl + 16 * o * ST, mine), xo,
+          bstore_frag<float>(rSV, keep_or_drop(f4l + o * 1024, mine), us + Slot::XHB, Frag<float>{xhb});
+          bstore_frag<T>(rOUT, keep_or_drop(xl + 16 * o * ST, mine), xo,
                          to_frag<T>(transpose16(to_frag<T>(y), I).v));
         }
       }
